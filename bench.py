@@ -1,0 +1,263 @@
+"""Benchmark of cleave's tensor hot path on one MI355X.
+
+Headline: f32 GEMM C = A B, M = N = K = 4096,
+row-major, N(0,1) inputs generated on the device.  One step = one
+cleave_hip_matmul_f32 call; inputs are resident in HBM before timing starts.
+
+Prints ONE JSON line on stdout:
+  value        aggregate GFLOP/s of the timed steps (2*M*N*K per step, wall clock
+               between two stream synchronisations)
+  roofline     the GEMM kernel's achieved TFLOP/s from HIP events recorded on the
+               library stream around the timed launches, vs 157.3 TFLOP/s FP32 MFMA
+  cpu_baseline the oracle's reference-faithful i-j-k loop, one core, on a row band
+               of the same product, extrapolated to GFLOP/s
+  secondary    the other BASELINE configs (bf16 8192^3, batched bf16, f32 A B^T /
+               A^T B, MLP steps/s, escape-count map, u64 count sum, sigmoid map),
+               each with its own HIP-event roofline figure
+Progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense FP32 matrix
+PEAK_BF16_MFMA = 2516.6  # TFLOP/s, MI355X dense BF16 matrix
+PEAK_FP32_VALU_NOFMA = 39.3  # T ops/s: 256 CU x 64 lanes x 2.4 GHz, one op per lane-cycle
+PEAK_HBM = 8000.0  # GB/s
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def timed(ca, fn, steps, warmup):
+    """Run fn warmup times, then time `steps` calls: wall clock between two
+    stream syncs, and HIP events on the library stream."""
+    for _ in range(warmup):
+        fn()
+    ca.sync()
+    t = ca.Timer()
+    w0 = time.perf_counter()
+    t.start()
+    for _ in range(steps):
+        fn()
+    ev_ms = t.stop()
+    ca.sync()
+    wall = time.perf_counter() - w0
+    return wall, ev_ms / steps
+
+
+def read_traffic(name):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    p = ROOT / "profiles" / f"{name}_traffic.md"
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def cpu_info():
+    model = platform.processor() or ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model, os.cpu_count()
+
+
+def cpu_baseline_gemm(A, B, n, budget_s):
+    """Reference-faithful loop (oracle/oracle.c or_matmul_f32_rows), one core."""
+    from oracle import oracle as orc
+
+    t0 = time.perf_counter()
+    orc.matmul_rows(A, B, n, n, n, 0, 1)
+    one = time.perf_counter() - t0
+    rows = max(1, min(n, int(budget_s / max(one, 1e-6))))
+    t0 = time.perf_counter()
+    orc.matmul_rows(A, B, n, n, n, 1, 1 + rows)
+    dt = time.perf_counter() - t0
+    gflops = 2.0 * rows * n * n / dt / 1e9
+    model, ncpu = cpu_info()
+    return {
+        "value": round(gflops, 4),
+        "unit": "GFLOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"rows 1..{rows} of the 4096^3 NN product through the restated "
+                   f"k-ascending loop (gcc -O2 -ffp-contract=off), {dt:.1f} s, extrapolated "
+                   f"linearly in M; host: {model}, {ncpu} logical CPUs"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); multi-GPU runs are "
+              "out of scope for this build", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+
+    import cleave_amd as ca
+
+    if not ca.device_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+    ca.init()
+    steps, warmup = args.steps, args.warmup
+
+    # ---- headline: f32 4096^3 NN --------------------------------------------
+    n = 4096
+    a = ca.fill_normal(ca.empty((n, n)), seed=101)
+    b = ca.fill_normal(ca.empty((n, n)), seed=102)
+    c = ca.empty((n, n))
+    flop = 2.0 * n * n * n
+    log(f"gemm f32 {n}^3 NN: {warmup} warmup + {steps} timed steps")
+    wall, ev_ms = timed(ca, lambda: ca.matmul(a, b, out=c), steps, warmup)
+    value = flop * steps / wall / 1e9
+    achieved = flop / (ev_ms * 1e-3) / 1e12
+    log(f"  {value:.1f} GFLOP/s wall, kernel {ev_ms:.3f} ms = {achieved:.1f} TFLOP/s")
+    traffic = read_traffic("gemm_f32_nn_4096")
+
+    result = {
+        "metric": "GEMM GFLOP/s + % MFMA peak (f32 4096^3, bf16 8192^3); MLP train steps/s",
+        "value": round(value, 1),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(wall / steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (N(0,1) from seed, generated on the device)",
+        "config": {"workload": "gemm_f32_nn_4096 (BASELINE configs[1], A B)", "M": n, "N": n, "K": n,
+                   "layout": "row-major", "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA, 4),
+                     "traffic": traffic},
+    }
+
+    secondary = {}
+    if not args.no_secondary:
+        sec_steps = max(5, steps // 5)
+        # f32 A B^T and A^T B (reverse-mode halves of the product rule)
+        for name, ta, tb in [("gemm_f32_nt_4096", False, True), ("gemm_f32_tn_4096", True, False)]:
+            wall_s, ev = timed(ca, lambda: ca.matmul(a, b, trans_a=ta, trans_b=tb, out=c), sec_steps, 2)
+            ach = flop / (ev * 1e-3) / 1e12
+            secondary[name] = {"GFLOP/s": round(flop * sec_steps / wall_s / 1e9, 1),
+                               "kernel_ms": round(ev, 4), "frac_fp32_mfma": round(ach / PEAK_FP32_MFMA, 4)}
+            log(f"{name}: {ach:.1f} TFLOP/s")
+        del c
+        # bf16 8192^3
+        m = 8192
+        a32 = ca.fill_normal(ca.empty((m, m)), seed=201, std=0.02)
+        ab = ca.to_bf16(a32)
+        ca.fill_normal(a32, seed=202, std=0.02)
+        bb = ca.to_bf16(a32)
+        del a32
+        cb = ca.empty((m, m))
+        fl = 2.0 * m ** 3
+        wall_s, ev = timed(ca, lambda: ca.matmul(ab, bb, out=cb), sec_steps, 2)
+        ach = fl / (ev * 1e-3) / 1e12
+        secondary["gemm_bf16_8192"] = {"GFLOP/s": round(fl * sec_steps / wall_s / 1e9, 1), "kernel_ms": round(ev, 4),
+                                       "frac_bf16_mfma": round(ach / PEAK_BF16_MFMA, 4)}
+        log(f"gemm_bf16_8192: {ach:.1f} TFLOP/s")
+        del ab, bb, cb
+        # batched bf16 64 x 512^3
+        bs, k = 64, 512
+        t32 = ca.fill_normal(ca.empty((bs, k, k)), seed=301, std=0.02)
+        xb = ca.to_bf16(t32)
+        ca.fill_normal(t32, seed=302, std=0.02)
+        yb = ca.to_bf16(t32)
+        del t32
+        zb = ca.empty((bs, k, k))
+        fl = 2.0 * bs * k ** 3
+        wall_s, ev = timed(ca, lambda: ca.matmul_batched(xb, yb, out=zb), sec_steps * 4, 2)
+        ach = fl / (ev * 1e-3) / 1e12
+        secondary["gemm_bf16_batched_64x512"] = {"GFLOP/s": round(fl * sec_steps * 4 / wall_s / 1e9, 1),
+                                                 "kernel_ms": round(ev, 4),
+                                                 "frac_bf16_mfma": round(ach / PEAK_BF16_MFMA, 4)}
+        log(f"gemm_bf16_batched_64x512: {ach:.1f} TFLOP/s")
+        del xb, yb, zb
+        # MLP step (config 4)
+        B_, D_, H_ = 65536, 1024, 4096
+        x = ca.fill_normal(ca.empty((B_, D_)), seed=401)
+        yv = ca.fill_bernoulli(ca.empty(B_), seed=402)
+        lim1 = float(np.sqrt(6.0 / (D_ + H_)))
+        lim2 = float(np.sqrt(6.0 / (H_ + 1)))
+        w1 = ca.fill_uniform(ca.empty((D_, H_)), seed=403, lo=-lim1, hi=lim1)
+        w2 = ca.fill_uniform(ca.empty(H_), seed=404, lo=-lim2, hi=lim2)
+        loss = ca.empty(1)
+        mlp_steps = max(5, steps // 5)
+        wall_s, ev = timed(ca, lambda: ca.mlp_step(x, yv, w1, w2, 0.01, loss=loss), mlp_steps, 2)
+        gemm_fl = 2.0 * B_ * D_ * H_ * 2 + 4.0 * B_ * H_
+        secondary["mlp_step_65536x1024x4096"] = {
+            "steps_per_s": round(mlp_steps / wall_s, 3), "ms_per_step": round(ev, 3),
+            "gemm_TFLOP/s": round(gemm_fl / (ev * 1e-3) / 1e12, 2),
+            "loss_after": float(loss.numpy()[0])}
+        log(f"mlp step: {mlp_steps / wall_s:.2f} steps/s ({ev:.2f} ms)")
+        del x, yv, w1, w2
+        # escape-count map + u64 sum (config 3)
+        g = 16384
+        d = np.float32(3.0 / g)
+        cnt = ca.empty((g, g), "u32")
+        wall_s, ev = timed(ca, lambda: ca.escape_counts(g, g, -2.0, -1.5, d, d, 1000, out=cnt), 3, 1)
+        # sum of counts = iterations executed by escaped pixels minus one each,
+        # max_iter for pixels that never escape: a lower bound of the executed work
+        total = ca.sum_u64(cnt)
+        secondary["mandelbrot_16384_1000"] = {
+            "ms": round(ev, 3), "pixel_iter_per_s": round(total / (ev * 1e-3), 1),
+            "TFLOP/s_11_per_iter": round(11.0 * total / (ev * 1e-3) / 1e12, 2),
+            "frac_valu_nofma": round(11.0 * total / (ev * 1e-3) / 1e12 / PEAK_FP32_VALU_NOFMA, 4),
+            "sum_of_counts": int(total)}
+        log(f"mandelbrot: {ev:.2f} ms, sum {total}")
+        out_dev = ca.empty(1, "u64")
+        wall_s, ev = timed(ca, lambda: ca.reduce_sum_u64(cnt, out_dev), 20, 3)
+        gbs = g * g * 4 / (ev * 1e-3) / 1e9
+        secondary["sum_u32_u64_16384sq"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1),
+                                           "frac_hbm": round(gbs / PEAK_HBM, 4)}
+        log(f"u64 sum: {gbs:.0f} GB/s")
+        del cnt
+        # sigmoid map over an H-sized tensor (65536 x 4096 f32)
+        hn = 65536 * 4096
+        hx = ca.fill_normal(ca.empty(hn), seed=501)
+        hy = ca.empty(hn)
+        wall_s, ev = timed(ca, lambda: ca.sigmoid(hx, out=hy), 10, 2)
+        gbs = hn * 8 / (ev * 1e-3) / 1e9
+        secondary["sigmoid_map_268M"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)}
+        log(f"sigmoid map: {gbs:.0f} GB/s")
+        del hx, hy
+    if secondary:
+        result["secondary"] = secondary
+
+    if not args.no_cpu:
+        log(f"cpu baseline: ~{args.cpu_budget:.0f} s of the restated loop on one core")
+        result["cpu_baseline"] = cpu_baseline_gemm(a.numpy(), b.numpy(), n, args.cpu_budget)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,344 @@
+"""cleave_amd -- MI355X (gfx950) backend for cleave's tensor operator surface.
+
+The product is libcleave_hip.so and its C ABI (include/cleave_hip.h).  This
+module is a thin host-side mirror of the stdlib operator names a .cleave
+program calls (/root/reference/stdlib/linalg/{tensor,matrix}.cleave,
+/root/reference/stdlib/nn/nn.cleave), over device-resident tensors:
+
+    matmul(a, b)                     MatMul::matmul          matrix.cleave:27-61
+    add/sub/mul/div/neg, zero        Ring<Tensor>            tensor.cleave:66-80
+    relu/sigmoid/tanh                Activation<Tensor>      nn.cleave:82-95
+    sum/mean/max_of                  Sum/Mean/Max            nn.cleave:111-149
+    escape_counts                    escape_count over a grid, examples/mandelbrot.cleave:14-26
+    mlp_step                         SGD step, examples/xor_tensor.cleave:38-92 style
+
+Errors raise CleaveHipError (the ABI returns a negative status instead of
+aborting once the binding switches abort-on-error off).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from ._lib import CleaveHipError, call, load
+
+__all__ = [
+    "CleaveHipError", "Tensor", "device_available", "init", "sync", "empty", "from_numpy",
+    "matmul", "matmul_batched", "add", "sub", "mul", "div", "neg", "zero", "relu", "sigmoid",
+    "tanh", "sigmoid_bwd", "tanh_bwd", "relu_bwd", "div_bwd", "sgd_update", "sum", "mean",
+    "max_of", "argmax", "sum_u64", "reduce_sum", "reduce_max", "reduce_sum_u64", "escape_counts", "mlp_step", "fill_uniform", "fill_normal",
+    "fill_bernoulli", "to_bf16", "Timer", "symbol_table",
+]
+
+_DTYPES = {"f32": (np.float32, 4), "bf16": (np.uint16, 2), "u32": (np.uint32, 4),
+           "u64": (np.uint64, 8), "i64": (np.int64, 8)}
+
+
+def device_available() -> bool:
+    return bool(load().cleave_hip_device_available())
+
+
+def init() -> None:
+    call("cleave_hip_init")
+
+
+def sync() -> None:
+    call("cleave_hip_sync")
+
+
+def symbol_table() -> dict[str, int]:
+    return _lib.symbol_table()
+
+
+@dataclass
+class Tensor:
+    """A device buffer (opaque handle from cleave_hip_buf_alloc) with a shape."""
+
+    ptr: int
+    shape: tuple
+    dtype: str
+    owned: bool = True
+
+    @property
+    def size(self) -> int:
+        n = 1
+        for d in self.shape:
+            n *= int(d)
+        return n
+
+    @property
+    def nbytes(self) -> int:
+        return self.size * _DTYPES[self.dtype][1]
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=_DTYPES[self.dtype][0])
+        if out.nbytes:
+            n = call("cleave_hip_download", out.ctypes.data, self.ptr, out.nbytes)
+            if n != out.nbytes:
+                raise CleaveHipError(n, _lib.last_error()[1])
+        return out
+
+    def upload(self, arr: np.ndarray) -> "Tensor":
+        arr = np.ascontiguousarray(arr, dtype=_DTYPES[self.dtype][0])
+        if arr.size != self.size:
+            raise ValueError(f"upload of {arr.size} elements into a tensor of {self.size}")
+        if arr.nbytes:
+            n = call("cleave_hip_upload", self.ptr, arr.ctypes.data, arr.nbytes)
+            if n != arr.nbytes:
+                raise CleaveHipError(n, _lib.last_error()[1])
+        return self
+
+    def free(self) -> None:
+        if self.owned and self.ptr:
+            load().cleave_hip_buf_free(self.ptr)
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def empty(shape, dtype: str = "f32") -> Tensor:
+    shape = tuple(int(d) for d in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+    nbytes = max(1, int(np.prod(shape, dtype=np.int64)) * _DTYPES[dtype][1])
+    ptr = load().cleave_hip_buf_alloc(nbytes)
+    if not ptr:
+        code, msg = _lib.last_error()
+        raise CleaveHipError(code, msg)
+    return Tensor(ptr, shape, dtype)
+
+
+def from_numpy(arr: np.ndarray, dtype: str | None = None) -> Tensor:
+    if dtype is None:
+        dtype = {np.dtype(np.float32): "f32", np.dtype(np.uint16): "bf16",
+                 np.dtype(np.uint32): "u32"}[np.dtype(arr.dtype)]
+    t = empty(arr.shape, dtype)
+    return t.upload(arr)
+
+
+def _need(t: Tensor, dtype: str, what: str) -> None:
+    if t.dtype != dtype:
+        raise TypeError(f"{what}: expected {dtype} tensor, got {t.dtype}")
+
+
+# ---- MatMul (stdlib/linalg/matrix.cleave:22-61) ------------------------------
+
+def matmul(a: Tensor, b: Tensor, trans_a: bool = False, trans_b: bool = False,
+           out: Tensor | None = None) -> Tensor:
+    """C = op(A) op(B) with fp32 accumulation; A/B f32 or bf16 (both the same)."""
+    if len(a.shape) != 2 or len(b.shape) != 2:
+        raise ValueError("matmul: rank-2 operands required")
+    M, K = (a.shape[1], a.shape[0]) if trans_a else a.shape
+    Kb, N = (b.shape[1], b.shape[0]) if trans_b else b.shape
+    if K != Kb:
+        raise ValueError(f"matmul: inner dimensions differ ({K} vs {Kb})")
+    if a.dtype != b.dtype:
+        raise TypeError("matmul: operands must share a dtype")
+    out = out if out is not None else empty((M, N), "f32")
+    fn = "cleave_hip_matmul_f32" if a.dtype == "f32" else "cleave_hip_matmul_bf16"
+    call(fn, a.ptr, a.size, b.ptr, b.size, out.ptr, out.size, M, N, K, int(trans_a), int(trans_b))
+    return out
+
+
+def matmul_batched(a: Tensor, b: Tensor, out: Tensor | None = None, trans_a: bool = False,
+                   trans_b: bool = False) -> Tensor:
+    """batch x (M x K) . batch x (K x N); bf16 batched supports the plain layout only."""
+    batch, M, K = a.shape
+    _, Kb, N = b.shape
+    if trans_a:
+        M, K = K, M
+    if trans_b:
+        Kb, N = N, Kb
+    out = out if out is not None else empty((batch, M, N), "f32")
+    if a.dtype == "f32":
+        call("cleave_hip_matmul_batched_f32", a.ptr, a.size, b.ptr, b.size, out.ptr, out.size,
+             batch, M, N, K, int(trans_a), int(trans_b))
+    else:
+        if trans_a or trans_b:
+            raise ValueError("matmul_batched: bf16 supports the untransposed layout only")
+        call("cleave_hip_matmul_batched_bf16", a.ptr, a.size, b.ptr, b.size, out.ptr, out.size,
+             batch, M, N, K)
+    return out
+
+
+# ---- Ring<Tensor> / Activation<Tensor> ------------------------------------------
+
+def _binary(fn: str, a: Tensor, b: Tensor, out: Tensor | None) -> Tensor:
+    out = out if out is not None else empty(a.shape, "f32")
+    call(fn, a.ptr, a.size, b.ptr, b.size, out.ptr, out.size)
+    return out
+
+
+def _unary(fn: str, a: Tensor, out: Tensor | None) -> Tensor:
+    out = out if out is not None else empty(a.shape, "f32")
+    call(fn, a.ptr, a.size, out.ptr, out.size)
+    return out
+
+
+def add(a, b, out=None): return _binary("cleave_hip_add_f32", a, b, out)
+def sub(a, b, out=None): return _binary("cleave_hip_sub_f32", a, b, out)
+def mul(a, b, out=None): return _binary("cleave_hip_mul_f32", a, b, out)
+def div(a, b, out=None): return _binary("cleave_hip_div_f32", a, b, out)
+def neg(a, out=None): return _unary("cleave_hip_neg_f32", a, out)
+def relu(x, out=None): return _unary("cleave_hip_relu_f32", x, out)
+def sigmoid(x, out=None): return _unary("cleave_hip_sigmoid_f32", x, out)
+def tanh(x, out=None): return _unary("cleave_hip_tanh_f32", x, out)
+def sigmoid_bwd(s, g, out=None): return _binary("cleave_hip_sigmoid_bwd_f32", s, g, out)
+def tanh_bwd(t, g, out=None): return _binary("cleave_hip_tanh_bwd_f32", t, g, out)
+def relu_bwd(x, g, out=None): return _binary("cleave_hip_relu_bwd_f32", x, g, out)
+
+
+def zero(shape_or_tensor) -> Tensor:
+    """Ring::zero (stdlib/linalg/tensor.cleave:79)."""
+    t = shape_or_tensor if isinstance(shape_or_tensor, Tensor) else empty(shape_or_tensor, "f32")
+    call("cleave_hip_zero_f32", t.ptr, t.size)
+    return t
+
+
+def div_bwd(a: Tensor, b: Tensor, g: Tensor) -> tuple[Tensor, Tensor]:
+    da, db = empty(a.shape), empty(a.shape)
+    call("cleave_hip_div_bwd_f32", a.ptr, a.size, b.ptr, b.size, g.ptr, g.size, da.ptr, da.size,
+         db.ptr, db.size)
+    return da, db
+
+
+def sgd_update(w: Tensor, g: Tensor, lr: float) -> Tensor:
+    call("cleave_hip_sgd_update_f32", w.ptr, w.size, g.ptr, g.size, float(lr))
+    return w
+
+
+# ---- Sum / Mean / Max ----------------------------------------------------------
+
+def sum(t: Tensor) -> float:  # noqa: A001 - mirrors the stdlib name
+    _need(t, "f32", "sum")
+    return _checked_scalar("cleave_hip_sum_f32", t)
+
+
+def mean(t: Tensor) -> float:
+    _need(t, "f32", "mean")
+    return _checked_scalar("cleave_hip_mean_f32", t)
+
+
+def max_of(t: Tensor) -> float:
+    _need(t, "f32", "max_of")
+    return _checked_scalar("cleave_hip_max_of_f32", t)
+
+
+def argmax(t: Tensor) -> int:
+    _need(t, "f32", "argmax")
+    return int(_checked_scalar("cleave_hip_argmax_f32", t))
+
+
+def sum_u64(t: Tensor) -> int:
+    _need(t, "u32", "sum_u64")
+    return int(_checked_scalar("cleave_hip_sum_u32_u64", t))
+
+
+def reduce_sum(t: Tensor, out: Tensor) -> Tensor:
+    """Queued sum into a device scalar (no synchronisation)."""
+    _need(t, "f32", "reduce_sum")
+    call("cleave_hip_reduce_sum_f32", t.ptr, t.size, out.ptr)
+    return out
+
+
+def reduce_max(t: Tensor, out_max: Tensor | None, out_argmax: Tensor | None) -> None:
+    """Queued max_of / argmax into device scalars (no synchronisation)."""
+    _need(t, "f32", "reduce_max")
+    call("cleave_hip_reduce_max_f32", t.ptr, t.size, out_max.ptr if out_max else None,
+         out_argmax.ptr if out_argmax else None)
+
+
+def reduce_sum_u64(t: Tensor, out: Tensor) -> Tensor:
+    """Queued exact u64 sum of u32 values into a device scalar (no synchronisation)."""
+    _need(t, "u32", "reduce_sum_u64")
+    call("cleave_hip_reduce_sum_u32_u64", t.ptr, t.size, out.ptr)
+    return out
+
+
+def _checked_scalar(fn: str, t: Tensor):
+    # The host-returning reductions clear the error state on entry and return
+    # a NaN / sentinel on failure, so the error state tells the two apart.
+    out = getattr(load(), fn)(t.ptr, t.size)
+    code, msg = _lib.last_error()
+    if code < 0:
+        raise CleaveHipError(code, msg)
+    return out
+
+
+# ---- escape_count map ----------------------------------------------------------
+
+def escape_counts(width: int, height: int, x0: float, y0: float, dx: float, dy: float,
+                  max_iter: int, out: Tensor | None = None) -> Tensor:
+    out = out if out is not None else empty((height, width), "u32")
+    call("cleave_hip_mandelbrot_u32", out.ptr, out.size, width, height, float(x0), float(y0),
+         float(dx), float(dy), max_iter)
+    return out
+
+
+# ---- MLP step --------------------------------------------------------------------
+
+def mlp_step(x: Tensor, y: Tensor, w1: Tensor, w2: Tensor, lr: float,
+             dw1: Tensor | None = None, dw2: Tensor | None = None,
+             loss: Tensor | None = None) -> None:
+    B, D = x.shape
+    Hd = w1.shape[1]
+    call("cleave_hip_mlp_step_f32", x.ptr, x.size, y.ptr, y.size, w1.ptr, w1.size, w2.ptr,
+         w2.size, dw1.ptr if dw1 else None, dw1.size if dw1 else 0,
+         dw2.ptr if dw2 else None, dw2.size if dw2 else 0, loss.ptr if loss else None,
+         B, D, Hd, float(lr))
+
+
+# ---- synthetic inputs ------------------------------------------------------------
+
+def fill_uniform(t: Tensor, seed: int, lo: float = -1.0, hi: float = 1.0) -> Tensor:
+    call("cleave_hip_fill_uniform_f32", t.ptr, t.size, seed, lo, hi)
+    return t
+
+
+def fill_normal(t: Tensor, seed: int, mean: float = 0.0, std: float = 1.0) -> Tensor:
+    call("cleave_hip_fill_normal_f32", t.ptr, t.size, seed, mean, std)
+    return t
+
+
+def fill_bernoulli(t: Tensor, seed: int, p: float = 0.5) -> Tensor:
+    call("cleave_hip_fill_bernoulli_f32", t.ptr, t.size, seed, p)
+    return t
+
+
+def to_bf16(t: Tensor, out: Tensor | None = None) -> Tensor:
+    out = out if out is not None else empty(t.shape, "bf16")
+    call("cleave_hip_cast_f32_bf16", t.ptr, t.size, out.ptr, out.size)
+    return out
+
+
+class Timer:
+    """HIP events recorded on the library stream (the stream every kernel uses)."""
+
+    def __init__(self):
+        lib = load()
+        self.e0 = lib.cleave_hip_event_create()
+        self.e1 = lib.cleave_hip_event_create()
+        if not self.e0 or not self.e1:
+            raise CleaveHipError(*_lib.last_error())
+
+    def start(self):
+        call("cleave_hip_event_record", self.e0)
+
+    def stop(self) -> float:
+        call("cleave_hip_event_record", self.e1)
+        ms = load().cleave_hip_event_elapsed_ms(self.e0, self.e1)
+        if ms < 0:
+            raise CleaveHipError(*_lib.last_error())
+        return ms
+
+    def __del__(self):
+        try:
+            lib = load()
+            lib.cleave_hip_event_destroy(self.e0)
+            lib.cleave_hip_event_destroy(self.e1)
+        except Exception:
+            pass

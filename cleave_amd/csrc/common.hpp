@@ -1,0 +1,61 @@
+// common.hpp -- shared runtime state, error handling and launch helpers for
+// libcleave_hip.so.  Every entry point validates its arguments on the host
+// before launching anything, so a kernel never sees a shape it was not
+// written for.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+
+#include "../../include/cleave_hip.h"
+
+namespace ch {
+
+// Library stream (one per process, like the reference's single JIT thread).
+hipStream_t stream();
+// Opens device 0 and creates the stream on first use; returns status.
+int32_t ensure_init();
+
+// Records an error (code + printf-style message).  In abort mode (the
+// default, matching cleave-rt's panic) prints to stderr and aborts.
+// Returns `code` so callers can `return fail(...)`.
+int32_t fail(int32_t code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+// Checks a HIP call; on error records it and returns CLEAVE_HIP_ERR_RUNTIME.
+int32_t check_hip(hipError_t e, const char* what);
+
+// Scratch device memory owned by the library (grown on demand, never shrunk).
+// `slot` selects an independent buffer.
+void* scratch(int slot, size_t bytes);
+
+// Number of compute units (for grid sizing of persistent/strided kernels).
+int num_cus();
+
+}  // namespace ch
+
+#define CH_INIT_OR_RETURN()                       \
+    do {                                          \
+        int32_t _st = ch::ensure_init();          \
+        if (_st != CLEAVE_HIP_OK) return _st;     \
+    } while (0)
+
+#define CH_HIP(expr)                                                   \
+    do {                                                               \
+        int32_t _st = ch::check_hip((expr), #expr);                    \
+        if (_st != CLEAVE_HIP_OK) return _st;                          \
+    } while (0)
+
+#define CH_LAUNCHED(name)                                               \
+    do {                                                                \
+        int32_t _st = ch::check_hip(hipGetLastError(), name);           \
+        if (_st != CLEAVE_HIP_OK) return _st;                           \
+    } while (0)
+
+// Argument checks used by every entry point.
+#define CH_REQUIRE(cond, ...)                                     \
+    do {                                                          \
+        if (!(cond)) return ch::fail(CLEAVE_HIP_ERR_ARG, __VA_ARGS__); \
+    } while (0)

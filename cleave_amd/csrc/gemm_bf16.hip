@@ -1,0 +1,237 @@
+// gemm_bf16.hip -- bf16-input / fp32-accumulate matmul on CDNA4 matrix cores
+// (v_mfma_f32_32x32x16_bf16), plus its batched form.
+//
+// Same operator as gemm_f32.hip (linalg.matmul of stdlib/linalg/matrix.cleave:
+// 27-61) with bf16 operands; the reference is f32/f64 only, so this is an
+// extension checked against the f32 loop run on the upcast values.
+//
+// LDS layout: both operands are staged [row][k] with k contiguous and a row
+// pitch of BK+8 elements (80 bytes), so the 16-byte MFMA operand reads of 16
+// consecutive lanes land in 16 distinct bank quads.  An operand that is
+// k-contiguous in global memory is copied in 16-byte chunks; one that is
+// contiguous along m/n is read as 8(k) x 2(m/n) blocks of 4-byte words and
+// transposed in registers before a pair of 16-byte LDS stores.
+#include "common.hpp"
+#include "gemm_common.hpp"
+
+namespace {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+constexpr int BM = 128, BN = 128, BK = 32, NT = 256;
+constexpr int PITCH = BK + 8;  // elements
+
+// Registers holding one thread's share of a 128 x BK operand tile.
+template <bool KCONTIG>
+struct Stage;
+template <>
+struct Stage<true> {  // 128 rows x 32 k = 512 chunks of 8 -> 2 per thread
+    uint4 v[2];
+};
+template <>
+struct Stage<false> {  // 64 row-pairs x 4 k-groups of 8 -> 1 block per thread
+    uint32_t w[8];
+};
+
+// X is the operand, `ld` its leading dimension.  KCONTIG: element (r, k) at
+// X[r*ld + k]; otherwise at X[k*ld + r].  rows/ks bound the valid region
+// (EDGE only).
+template <bool KCONTIG, bool EDGE>
+__device__ __forceinline__ void load_tile(Stage<KCONTIG>& s, const uint16_t* __restrict__ X,
+                                          int64_t ld, int r0, int k0, int rows, int ks, int tid) {
+    if constexpr (KCONTIG) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            int idx = tid + NT * q;
+            int r = idx >> 2, kc = (idx & 3) * 8;
+            int gr = r0 + r, gk = k0 + kc;
+            if (!EDGE) {
+                s.v[q] = *reinterpret_cast<const uint4*>(X + (int64_t)gr * ld + gk);
+            } else {
+                uint16_t e[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                    e[t] = (gr < rows && gk + t < ks) ? X[(int64_t)gr * ld + gk + t] : (uint16_t)0;
+                s.v[q] = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16),
+                                    e[6] | (e[7] << 16));
+            }
+        }
+    } else {
+        int rp = (tid & 63) * 2, kg = (tid >> 6) * 8;
+        int gr = r0 + rp;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            int gk = k0 + kg + t;
+            if (!EDGE) {
+                s.w[t] = *reinterpret_cast<const uint32_t*>(X + (int64_t)gk * ld + gr);
+            } else {
+                uint32_t lo = (gk < ks && gr < rows) ? X[(int64_t)gk * ld + gr] : 0u;
+                uint32_t hi = (gk < ks && gr + 1 < rows) ? X[(int64_t)gk * ld + gr + 1] : 0u;
+                s.w[t] = lo | (hi << 16);
+            }
+        }
+    }
+}
+
+template <bool KCONTIG>
+__device__ __forceinline__ void store_tile(const Stage<KCONTIG>& s, uint16_t (*L)[PITCH], int tid) {
+    if constexpr (KCONTIG) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            int idx = tid + NT * q;
+            int r = idx >> 2, kc = (idx & 3) * 8;
+            *reinterpret_cast<uint4*>(&L[r][kc]) = s.v[q];
+        }
+    } else {
+        int rp = (tid & 63) * 2, kg = (tid >> 6) * 8;
+        uint4 lo, hi;  // rows rp and rp+1, k = kg..kg+7
+        lo.x = (s.w[0] & 0xFFFFu) | (s.w[1] << 16);
+        lo.y = (s.w[2] & 0xFFFFu) | (s.w[3] << 16);
+        lo.z = (s.w[4] & 0xFFFFu) | (s.w[5] << 16);
+        lo.w = (s.w[6] & 0xFFFFu) | (s.w[7] << 16);
+        hi.x = (s.w[0] >> 16) | (s.w[1] & 0xFFFF0000u);
+        hi.y = (s.w[2] >> 16) | (s.w[3] & 0xFFFF0000u);
+        hi.z = (s.w[4] >> 16) | (s.w[5] & 0xFFFF0000u);
+        hi.w = (s.w[6] >> 16) | (s.w[7] & 0xFFFF0000u);
+        *reinterpret_cast<uint4*>(&L[rp][kg]) = lo;
+        *reinterpret_cast<uint4*>(&L[rp + 1][kg]) = hi;
+    }
+}
+
+template <bool TA, bool TB, bool EDGE>
+__global__ __launch_bounds__(NT) void gemm_bf16_kernel(const uint16_t* __restrict__ A,
+                                                       const uint16_t* __restrict__ B,
+                                                       float* __restrict__ C, int M, int N, int K,
+                                                       int64_t strideA, int64_t strideB,
+                                                       int64_t strideC, int tiles_m, int tiles_n) {
+    constexpr bool AK = !TA;  // A k-contiguous when stored M x K
+    constexpr bool BKC = TB;  // B k-contiguous when stored N x K
+    __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][PITCH];
+    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN][PITCH];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    int tm, tn;
+    ch::tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    A += (int64_t)blockIdx.y * strideA;
+    B += (int64_t)blockIdx.y * strideB;
+    C += (int64_t)blockIdx.y * strideC;
+    const int64_t lda = TA ? M : K, ldb = TB ? K : N;
+
+    Stage<AK> sa;
+    Stage<BKC> sb;
+    v16f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+
+    const int nk = (K + BK - 1) / BK;
+    load_tile<AK, EDGE>(sa, A, lda, m0, 0, M, K, tid);
+    load_tile<BKC, EDGE>(sb, B, ldb, n0, 0, N, K, tid);
+    store_tile<AK>(sa, As[0], tid);
+    store_tile<BKC>(sb, Bs[0], tid);
+    __syncthreads();
+
+    const int half = lane >> 5, r32 = lane & 31;
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) {
+            load_tile<AK, EDGE>(sa, A, lda, m0, (kt + 1) * BK, M, K, tid);
+            load_tile<BKC, EDGE>(sb, B, ldb, n0, (kt + 1) * BK, N, K, tid);
+        }
+#pragma unroll
+        for (int ks = 0; ks < BK; ks += 16) {
+            v8bf a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                a[i] = *reinterpret_cast<const v8bf*>(&As[cur][wm * 64 + i * 32 + r32][ks + 8 * half]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                b[j] = *reinterpret_cast<const v8bf*>(&Bs[cur][wn * 64 + j * 32 + r32][ks + 8 * half]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            store_tile<AK>(sa, As[cur ^ 1], tid);
+            store_tile<BKC>(sb, Bs[cur ^ 1], tid);
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                int r = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+                int c = n0 + wn * 64 + j * 32 + r32;
+                if (!EDGE || (r < M && c < N)) C[(int64_t)r * N + c] = acc[i][j][v];
+            }
+}
+
+template <bool TA, bool TB>
+int32_t launch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch) {
+    const int64_t sA = (int64_t)M * K, sB = (int64_t)K * N, sC = (int64_t)M * N;
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)batch);
+    // 4-byte (transposed) or 16-byte (k-contiguous) global reads need the
+    // matching alignment of every row start.
+    const bool fast = (M % BM == 0) && (N % BN == 0) && (K % BK == 0);
+    if (fast)
+        gemm_bf16_kernel<TA, TB, false><<<grid, NT, 0, ch::stream()>>>(a, b, c, M, N, K, sA, sB, sC,
+                                                                       tiles_m, tiles_n);
+    else
+        gemm_bf16_kernel<TA, TB, true><<<grid, NT, 0, ch::stream()>>>(a, b, c, M, N, K, sA, sB, sC,
+                                                                      tiles_m, tiles_n);
+    CH_LAUNCHED("gemm_bf16_kernel");
+    return CLEAVE_HIP_OK;
+}
+
+int32_t dispatch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
+                 int ta, int tb) {
+    if (!ta && !tb) return launch<false, false>(a, b, c, M, N, K, batch);
+    if (!ta && tb) return launch<false, true>(a, b, c, M, N, K, batch);
+    if (ta && !tb) return launch<true, false>(a, b, c, M, N, K, batch);
+    return launch<true, true>(a, b, c, M, N, K, batch);
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t cleave_hip_matmul_bf16(const uint16_t* a, int64_t alen, const uint16_t* b, int64_t blen,
+                               float* c, int64_t clen, int32_t M, int32_t N, int32_t K,
+                               int32_t trans_a, int32_t trans_b) {
+    CH_REQUIRE(M > 0 && N > 0 && K > 0, "cleave_hip_matmul_bf16: dims must be positive (M=%d N=%d K=%d)", M, N, K);
+    CH_REQUIRE((trans_a == 0 || trans_a == 1) && (trans_b == 0 || trans_b == 1),
+               "cleave_hip_matmul_bf16: trans flags must be 0 or 1");
+    CH_REQUIRE(alen == (int64_t)M * K, "cleave_hip_matmul_bf16: alen %lld != M*K %lld", (long long)alen, (long long)M * K);
+    CH_REQUIRE(blen == (int64_t)K * N, "cleave_hip_matmul_bf16: blen %lld != K*N %lld", (long long)blen, (long long)K * N);
+    CH_REQUIRE(clen == (int64_t)M * N, "cleave_hip_matmul_bf16: clen %lld != M*N %lld", (long long)clen, (long long)M * N);
+    CH_REQUIRE(a && b && c, "cleave_hip_matmul_bf16: null buffer");
+    CH_INIT_OR_RETURN();
+    return dispatch(a, b, c, M, N, K, 1, trans_a, trans_b);
+}
+
+int32_t cleave_hip_matmul_batched_bf16(const uint16_t* a, int64_t alen, const uint16_t* b,
+                                       int64_t blen, float* c, int64_t clen, int32_t batch,
+                                       int32_t M, int32_t N, int32_t K) {
+    CH_REQUIRE(batch > 0 && batch <= 65535 && M > 0 && N > 0 && K > 0,
+               "cleave_hip_matmul_batched_bf16: bad dims (batch=%d M=%d N=%d K=%d)", batch, M, N, K);
+    CH_REQUIRE(alen == (int64_t)batch * M * K && blen == (int64_t)batch * K * N &&
+                   clen == (int64_t)batch * M * N,
+               "cleave_hip_matmul_batched_bf16: lengths do not match batch*M*K, batch*K*N, batch*M*N");
+    CH_REQUIRE(a && b && c, "cleave_hip_matmul_batched_bf16: null buffer");
+    CH_INIT_OR_RETURN();
+    return dispatch(a, b, c, M, N, K, batch, 0, 0);
+}
+
+}  // extern "C"

@@ -1,0 +1,30 @@
+// gemm_common.hpp -- tile scheduling shared by the matrix-core kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace ch {
+
+// MI355X dispatches consecutive workgroups round-robin over its 8 XCDs, each
+// with a private L2.  Map the hardware order so XCD x receives the contiguous
+// range [x*T/8, (x+1)*T/8) of logical tiles, then walk logical tiles in
+// groups of GROUP_M tile-rows (column-major inside a group) so the tiles that
+// run together share A row-panels and B column-panels.
+constexpr int kXcds = 8;
+constexpr int kGroupM = 8;
+
+__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& tm,
+                                            int& tn) {
+    const int total = tiles_m * tiles_n;
+    int t = bid;
+    if (total % kXcds == 0) t = (bid % kXcds) * (total / kXcds) + bid / kXcds;
+    const int per_group = kGroupM * tiles_n;
+    const int group = t / per_group;
+    const int first_m = group * kGroupM;
+    const int gsize = min(tiles_m - first_m, kGroupM);
+    const int in_group = t - group * per_group;
+    tm = first_m + in_group % gsize;
+    tn = in_group / gsize;
+}
+
+}  // namespace ch

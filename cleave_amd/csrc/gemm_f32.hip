@@ -1,0 +1,279 @@
+// gemm_f32.hip -- fp32 matmul on CDNA4 matrix cores (v_mfma_f32_32x32x2f32).
+//
+// Replaces linalg.matmul as cleave lowers it (stdlib/linalg/matrix.cleave:27-61,
+// region cleave/src/mlir_lower.rs:2089-2120): C = 0; C[i,j] += A[i,k]*B[k,j].
+// The A^T B and A B^T forms are the reverse-mode halves of the MatMul product
+// rule (stdlib/linalg/matrix.cleave:24).
+//
+// Design (one workgroup = one BM x BN tile of C):
+//   * 256 threads = 4 waves in a 2 x 2 grid; each wave owns a (BM/2) x (BN/2)
+//     block made of 32 x 32 MFMA tiles, accumulators kept in registers.
+//   * K is walked in BK slices.  Both operands are staged in LDS k-major
+//     ([k][m] and [k][n]) so every MFMA operand read is 32 consecutive floats
+//     per half-wave (conflict-free ds_read_b32).  A slice that is contiguous
+//     along m/n in global memory is copied with 16-byte stores; one that is
+//     contiguous along k is transposed on the way in.
+//   * Two LDS buffers: the next slice's global loads are issued before the
+//     current slice's MFMAs, and written to the other buffer afterwards, so a
+//     single barrier per slice suffices.
+//   * Workgroups are dispatched round-robin over the 8 XCDs; the tile index is
+//     remapped so each XCD works on a contiguous, grouped band of tiles and its
+//     private L2 sees the A rows / B columns its neighbours also read.
+//   * EDGE instantiations guard every global access (any M, N, K); the fast
+//     path needs M % BM == N % BN == K % BK == 0.
+#include "common.hpp"
+#include "gemm_common.hpp"
+
+namespace {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+template <int BM, int BN, int BK, bool TA, bool TB, bool EDGE>
+__global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ A,
+                                                       const float* __restrict__ B,
+                                                       float* __restrict__ C, int M, int N,
+                                                       int K, int64_t lda, int64_t ldb,
+                                                       int64_t ldc, int64_t strideA,
+                                                       int64_t strideB, int64_t strideC,
+                                                       int tiles_m, int tiles_n) {
+    constexpr int NT = 256;
+    constexpr int WTM = BM / 2, WTN = BN / 2;  // wave tile
+    constexpr int FM = WTM / 32, FN = WTN / 32;
+    constexpr int PA = BM + 4, PB = BN + 4;  // LDS row pitch (floats)
+    __shared__ float As[2][BK][PA];
+    __shared__ float Bs[2][BK][PB];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    int tm, tn;
+    ch::tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    A += (int64_t)blockIdx.y * strideA;
+    B += (int64_t)blockIdx.y * strideB;
+    C += (int64_t)blockIdx.y * strideC;
+
+    // ---- global -> register staging -------------------------------------
+    constexpr int A_VEC = BM * BK / 4 / NT;  // float4 per thread
+    constexpr int B_VEC = BN * BK / 4 / NT;
+    static_assert(A_VEC * NT * 4 == BM * BK && B_VEC * NT * 4 == BN * BK, "tile/threads");
+    float4 ra[A_VEC], rb[B_VEC];
+
+    auto load_a = [&](int k0) {
+#pragma unroll
+        for (int q = 0; q < A_VEC; ++q) {
+            int idx = tid + NT * q;
+            int r, c;  // element (m, k) of the first of 4
+            if (!TA) { r = idx / (BK / 4); c = (idx % (BK / 4)) * 4; }  // along k
+            else     { c = idx / (BM / 4); r = (idx % (BM / 4)) * 4; }  // along m
+            int gm = m0 + r, gk = k0 + c;
+            if (!EDGE) {
+                const float* p = !TA ? A + (int64_t)gm * lda + gk : A + (int64_t)gk * lda + gm;
+                ra[q] = *reinterpret_cast<const float4*>(p);
+            } else {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    int mm = !TA ? gm : gm + e, kk = !TA ? gk + e : gk;
+                    v[e] = (mm < M && kk < K) ? (!TA ? A[(int64_t)mm * lda + kk] : A[(int64_t)kk * lda + mm]) : 0.0f;
+                }
+                ra[q] = make_float4(v[0], v[1], v[2], v[3]);
+            }
+        }
+    };
+    auto load_b = [&](int k0) {
+#pragma unroll
+        for (int q = 0; q < B_VEC; ++q) {
+            int idx = tid + NT * q;
+            int r, c;  // element (k, n) of the first of 4
+            if (!TB) { r = idx / (BN / 4); c = (idx % (BN / 4)) * 4; }  // along n
+            else     { c = idx / (BK / 4); r = (idx % (BK / 4)) * 4; }  // along k
+            int gk = k0 + r, gn = n0 + c;
+            if (!EDGE) {
+                const float* p = !TB ? B + (int64_t)gk * ldb + gn : B + (int64_t)gn * ldb + gk;
+                rb[q] = *reinterpret_cast<const float4*>(p);
+            } else {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    int kk = !TB ? gk : gk + e, nn = !TB ? gn + e : gn;
+                    v[e] = (kk < K && nn < N) ? (!TB ? B[(int64_t)kk * ldb + nn] : B[(int64_t)nn * ldb + kk]) : 0.0f;
+                }
+                rb[q] = make_float4(v[0], v[1], v[2], v[3]);
+            }
+        }
+    };
+    auto store_a = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < A_VEC; ++q) {
+            int idx = tid + NT * q;
+            if (!TA) {
+                int m = idx / (BK / 4), k = (idx % (BK / 4)) * 4;
+                As[buf][k + 0][m] = ra[q].x;
+                As[buf][k + 1][m] = ra[q].y;
+                As[buf][k + 2][m] = ra[q].z;
+                As[buf][k + 3][m] = ra[q].w;
+            } else {
+                int k = idx / (BM / 4), m = (idx % (BM / 4)) * 4;
+                *reinterpret_cast<float4*>(&As[buf][k][m]) = ra[q];
+            }
+        }
+    };
+    auto store_b = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < B_VEC; ++q) {
+            int idx = tid + NT * q;
+            if (!TB) {
+                int k = idx / (BN / 4), n = (idx % (BN / 4)) * 4;
+                *reinterpret_cast<float4*>(&Bs[buf][k][n]) = rb[q];
+            } else {
+                int n = idx / (BK / 4), k = (idx % (BK / 4)) * 4;
+                Bs[buf][k + 0][n] = rb[q].x;
+                Bs[buf][k + 1][n] = rb[q].y;
+                Bs[buf][k + 2][n] = rb[q].z;
+                Bs[buf][k + 3][n] = rb[q].w;
+            }
+        }
+    };
+
+    v16f acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = v16f{};
+
+    const int nk = (K + BK - 1) / BK;
+    load_a(0);
+    load_b(0);
+    store_a(0);
+    store_b(0);
+    __syncthreads();
+
+    const int half = lane >> 5, col = lane & 31;
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = (kt + 1) < nk;
+        if (more) {
+            load_a((kt + 1) * BK);
+            load_b((kt + 1) * BK);
+        }
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 2) {
+            float a[FM], b[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) a[i] = As[cur][kk + half][wm * WTM + i * 32 + col];
+#pragma unroll
+            for (int j = 0; j < FN; ++j) b[j] = Bs[cur][kk + half][wn * WTN + j * 32 + col];
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            store_a(cur ^ 1);
+            store_b(cur ^ 1);
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue: 32x32 accumulator layout, lane holds column lane%32 and
+    // rows 8*(v/4) + 4*(lane/32) + v%4 for v = 0..15.
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                int r = m0 + wm * WTM + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+                int c = n0 + wn * WTN + j * 32 + col;
+                if (!EDGE || (r < M && c < N)) C[(int64_t)r * ldc + c] = acc[i][j][v];
+            }
+}
+
+constexpr int BM = 128, BN = 128, BK = 16;
+
+template <bool TA, bool TB>
+int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
+               int64_t ldb, int64_t ldc, int batch, int64_t sA, int64_t sB, int64_t sC) {
+    // The 16-byte loads of the fast path also need every row start aligned.
+    const bool fast = (M % BM == 0) && (N % BN == 0) && (K % BK == 0) && (lda % 4 == 0) &&
+                      (ldb % 4 == 0) && (sA % 4 == 0) && (sB % 4 == 0);
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)batch);
+    if (fast)
+        gemm_f32_kernel<BM, BN, BK, TA, TB, false><<<grid, 256, 0, ch::stream()>>>(
+            a, b, c, M, N, K, lda, ldb, ldc, sA, sB, sC, tiles_m, tiles_n);
+    else
+        gemm_f32_kernel<BM, BN, BK, TA, TB, true><<<grid, 256, 0, ch::stream()>>>(
+            a, b, c, M, N, K, lda, ldb, ldc, sA, sB, sC, tiles_m, tiles_n);
+    CH_LAUNCHED("gemm_f32_kernel");
+    return CLEAVE_HIP_OK;
+}
+
+// batch >= 1 independent products packed back to back, or (splits > 1, batch
+// must be 1) one product whose K range is cut into `splits` equal slices,
+// slice s writing its partial sum to c + s*M*N.
+int32_t dispatch(const float* a, const float* b, float* c, int M, int N, int K, int batch,
+                 int ta, int tb, int splits) {
+    const int64_t lda = ta ? M : K, ldb = tb ? K : N, ldc = N;
+    int64_t sA = (int64_t)M * K, sB = (int64_t)K * N, sC = (int64_t)M * N;
+    int kk = K;
+    if (splits > 1) {
+        kk = K / splits;
+        sA = ta ? (int64_t)kk * lda : kk;
+        sB = tb ? kk : (int64_t)kk * ldb;
+        batch = splits;
+    }
+    if (!ta && !tb) return launch<false, false>(a, b, c, M, N, kk, lda, ldb, ldc, batch, sA, sB, sC);
+    if (!ta && tb) return launch<false, true>(a, b, c, M, N, kk, lda, ldb, ldc, batch, sA, sB, sC);
+    if (ta && !tb) return launch<true, false>(a, b, c, M, N, kk, lda, ldb, ldc, batch, sA, sB, sC);
+    return launch<true, true>(a, b, c, M, N, kk, lda, ldb, ldc, batch, sA, sB, sC);
+}
+
+}  // namespace
+
+namespace ch {
+// Internal entry used by the MLP step (same kernels, no argument checks).
+// splits > 1 requires K % splits == 0 and c sized splits*M*N.
+int32_t gemm_f32_device(const float* a, const float* b, float* c, int M, int N, int K, int ta,
+                        int tb, int splits) {
+    return dispatch(a, b, c, M, N, K, 1, ta, tb, splits);
+}
+}  // namespace ch
+
+extern "C" {
+
+int32_t cleave_hip_matmul_f32(const float* a, int64_t alen, const float* b, int64_t blen,
+                              float* c, int64_t clen, int32_t M, int32_t N, int32_t K,
+                              int32_t trans_a, int32_t trans_b) {
+    CH_REQUIRE(M > 0 && N > 0 && K > 0, "cleave_hip_matmul_f32: dims must be positive (M=%d N=%d K=%d)", M, N, K);
+    CH_REQUIRE((trans_a == 0 || trans_a == 1) && (trans_b == 0 || trans_b == 1),
+               "cleave_hip_matmul_f32: trans flags must be 0 or 1");
+    CH_REQUIRE(alen == (int64_t)M * K, "cleave_hip_matmul_f32: alen %lld != M*K %lld", (long long)alen, (long long)M * K);
+    CH_REQUIRE(blen == (int64_t)K * N, "cleave_hip_matmul_f32: blen %lld != K*N %lld", (long long)blen, (long long)K * N);
+    CH_REQUIRE(clen == (int64_t)M * N, "cleave_hip_matmul_f32: clen %lld != M*N %lld", (long long)clen, (long long)M * N);
+    CH_REQUIRE(a && b && c, "cleave_hip_matmul_f32: null buffer");
+    CH_INIT_OR_RETURN();
+    return dispatch(a, b, c, M, N, K, 1, trans_a, trans_b, 1);
+}
+
+int32_t cleave_hip_matmul_batched_f32(const float* a, int64_t alen, const float* b,
+                                      int64_t blen, float* c, int64_t clen, int32_t batch,
+                                      int32_t M, int32_t N, int32_t K, int32_t trans_a,
+                                      int32_t trans_b) {
+    CH_REQUIRE(batch > 0 && batch <= 65535 && M > 0 && N > 0 && K > 0,
+               "cleave_hip_matmul_batched_f32: bad dims (batch=%d M=%d N=%d K=%d)", batch, M, N, K);
+    CH_REQUIRE((trans_a == 0 || trans_a == 1) && (trans_b == 0 || trans_b == 1),
+               "cleave_hip_matmul_batched_f32: trans flags must be 0 or 1");
+    CH_REQUIRE(alen == (int64_t)batch * M * K && blen == (int64_t)batch * K * N &&
+                   clen == (int64_t)batch * M * N,
+               "cleave_hip_matmul_batched_f32: lengths do not match batch*M*K, batch*K*N, batch*M*N");
+    CH_REQUIRE(a && b && c, "cleave_hip_matmul_batched_f32: null buffer");
+    CH_INIT_OR_RETURN();
+    return dispatch(a, b, c, M, N, K, batch, trans_a, trans_b, 1);
+}
+
+}  // extern "C"

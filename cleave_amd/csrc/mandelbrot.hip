@@ -1,0 +1,63 @@
+// mandelbrot.hip -- escape-time map of examples/mandelbrot.cleave:14-26 in f32.
+//
+// escape_count(c): z = 0; for n in 0..max_iter { z = z*z + c;
+// if |z|^2 > 4 { return n } }; return max_iter.  Complex mul/add and
+// magnitude_sq follow stdlib/complex/complex.cleave:25-32 and :54:
+//   re = zr*zr - zi*zi;  im = zr*zi + zi*zr;  z = (re + cr, im + ci);
+//   |z|^2 = zr*zr + zi*zi.
+// The reference latches the first escape and keeps iterating; stopping at the
+// first escape returns the same n.
+//
+// Bit-exactness: the library is compiled with -ffp-contract=off, so no mul+add
+// is fused.  Two rewrites are exact and save work: the zr*zr and zi*zi of the
+// |z|^2 test are the same rounded products the next step's re needs, and
+// zr*zi + zi*zr == 2*(zr*zi) exactly (same rounded product added to itself).
+//
+// Mapping: one wave per 8 x 8 pixel block (neighbouring pixels have similar
+// iteration counts, so waves diverge less than with 64 x 1 strips); a
+// 256-thread workgroup covers 16 x 16 pixels.
+#include "common.hpp"
+
+namespace {
+
+__global__ __launch_bounds__(256) void mandelbrot_kernel(uint32_t* __restrict__ out, int width,
+                                                         int height, float x0, float y0, float dx,
+                                                         float dy, int max_iter) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = blockIdx.x * 16 + (wave & 1) * 8 + (lane & 7);
+    const int row = blockIdx.y * 16 + (wave >> 1) * 8 + (lane >> 3);
+    if (col >= width || row >= height) return;
+    const float cr = x0 + (float)col * dx;
+    const float ci = y0 + (float)row * dy;
+    float zr = 0.0f, zi = 0.0f, zr2 = 0.0f, zi2 = 0.0f;
+    int n = 0;
+    for (; n < max_iter; ++n) {
+        float p = zr * zi;
+        float re = zr2 - zi2;
+        float im = p + p;
+        zr = re + cr;
+        zi = im + ci;
+        zr2 = zr * zr;
+        zi2 = zi * zi;
+        if (zr2 + zi2 > 4.0f) break;
+    }
+    out[(int64_t)row * width + col] = (uint32_t)n;
+}
+
+}  // namespace
+
+extern "C" int32_t cleave_hip_mandelbrot_u32(uint32_t* out, int64_t outlen, int32_t width,
+                                             int32_t height, float x0, float y0, float dx,
+                                             float dy, int32_t max_iter) {
+    CH_REQUIRE(width > 0 && height > 0, "cleave_hip_mandelbrot_u32: width/height must be positive");
+    CH_REQUIRE(max_iter >= 0, "cleave_hip_mandelbrot_u32: max_iter must be >= 0");
+    CH_REQUIRE(outlen == (int64_t)width * height, "cleave_hip_mandelbrot_u32: outlen %lld != width*height %lld",
+               (long long)outlen, (long long)width * height);
+    CH_REQUIRE(out != nullptr, "cleave_hip_mandelbrot_u32: null buffer");
+    CH_INIT_OR_RETURN();
+    dim3 grid((unsigned)((width + 15) / 16), (unsigned)((height + 15) / 16));
+    CH_REQUIRE(grid.y <= 65535u, "cleave_hip_mandelbrot_u32: height %d too large", height);
+    mandelbrot_kernel<<<grid, 256, 0, ch::stream()>>>(out, width, height, x0, y0, dx, dy, max_iter);
+    CH_LAUNCHED("mandelbrot_kernel");
+    return CLEAVE_HIP_OK;
+}

@@ -1,0 +1,200 @@
+// mlp.hip -- one SGD step of a 2-layer sigmoid MLP with MSE loss, in the style
+// of examples/xor_tensor.cleave:38-92 (config: batch mean, no biases).
+//
+// Forward ops are the stdlib bodies (matmul stdlib/linalg/matrix.cleave:27-61,
+// sigmoid stdlib/nn/nn.cleave:87-93, mean stdlib/nn/nn.cleave:135-138); the
+// backward applies the reference's derivative rules in reverse mode:
+//   MatMul product rule (stdlib/linalg/matrix.cleave:24) -> dA = dC B^T, dB = A^T dC
+//   d(e*e) = de*e + e*de (stdlib/num/num.cleave:125)      -> dL/dyhat = (e+e)/B
+//   sigmoid via quotient + exp rules (num.cleave:132-134, :222) -> s(1-s)
+//
+// Kernel sequence on the library stream (device-resident, no host sync):
+//   1. H = X W1                         gemm_f32 NN   (M=B, N=Hd, K=D)
+//   2. H = sigmoid(H)                   map, in place
+//   3. row pass: z2 = H W2, yhat, e, sq = e*e, d2 = (e+e)/B * yhat(1-yhat)
+//   4. loss = sum(sq) / B               2-stage reduction
+//   5. column pass over H: dW2 partials += h*d2[m]; H <- d1 = (d2[m] W2[n]) h(1-h)
+//   6. dW2 = sum of partials; W2 -= lr dW2
+//   7. dW1 partials = X^T d1            gemm_f32 TN, split-K slices
+//   8. dW1 = sum of slices; W1 -= lr dW1
+#include "common.hpp"
+
+namespace ch {
+int32_t gemm_f32_device(const float* a, const float* b, float* c, int M, int N, int K, int ta,
+                        int tb, int splits);
+}
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float sigmoidf_ref(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__global__ __launch_bounds__(kThreads) void sigmoid_inplace_kernel(float* __restrict__ h, int64_t n) {
+    const int64_t nv = n / 4;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < nv; i += (int64_t)gridDim.x * kThreads) {
+        float4 v = reinterpret_cast<float4*>(h)[i];
+        v.x = sigmoidf_ref(v.x);
+        v.y = sigmoidf_ref(v.y);
+        v.z = sigmoidf_ref(v.z);
+        v.w = sigmoidf_ref(v.w);
+        reinterpret_cast<float4*>(h)[i] = v;
+    }
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3)) h[nv * 4 + threadIdx.x] = sigmoidf_ref(h[nv * 4 + threadIdx.x]);
+}
+
+// One wave per row: z2 = H[m,:] . W2, then the per-row loss pieces.
+__global__ __launch_bounds__(kThreads) void row_pass_kernel(const float* __restrict__ H,
+                                                            const float* __restrict__ W2,
+                                                            const float* __restrict__ y, int B,
+                                                            int Hd, float* __restrict__ sq,
+                                                            float* __restrict__ d2) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (row >= B) return;
+    const float* h = H + (int64_t)row * Hd;
+    float acc = 0.0f;
+    if ((Hd & 3) == 0) {
+        for (int c = lane * 4; c < Hd; c += 256) {
+            float4 a = *reinterpret_cast<const float4*>(h + c);
+            float4 w = *reinterpret_cast<const float4*>(W2 + c);
+            acc += a.x * w.x + a.y * w.y + a.z * w.z + a.w * w.w;
+        }
+    } else {
+        for (int c = lane; c < Hd; c += 64) acc += h[c] * W2[c];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+    if (lane == 0) {
+        float yh = sigmoidf_ref(acc);
+        float e = yh - y[row];
+        sq[row] = e * e;
+        float gy = (e + e) / (float)B;
+        d2[row] = gy * yh * (1.0f - yh);
+    }
+}
+
+// Column pass: each thread owns 4 consecutive columns of a band of rows.
+// Writes d1 over H and one dW2 partial per (row band, column).
+constexpr int kRowsPerBand = 256;
+__global__ __launch_bounds__(kThreads) void col_pass_kernel(float* __restrict__ H,
+                                                            const float* __restrict__ W2,
+                                                            const float* __restrict__ d2, int B,
+                                                            int Hd, float* __restrict__ part) {
+    const int c = (blockIdx.x * kThreads + threadIdx.x) * 4;
+    if (c >= Hd) return;
+    const int r0 = blockIdx.y * kRowsPerBand;
+    const int r1 = min(B, r0 + kRowsPerBand);
+    const int nc = min(4, Hd - c);
+    float w[4], s[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; ++j) w[j] = j < nc ? W2[c + j] : 0.0f;
+    for (int r = r0; r < r1; ++r) {
+        float* h = H + (int64_t)r * Hd + c;
+        const float dm = d2[r];
+        for (int j = 0; j < nc; ++j) {
+            float hv = h[j];
+            s[j] += hv * dm;
+            float g = dm * w[j];
+            h[j] = g * hv * (1.0f - hv);
+        }
+    }
+    for (int j = 0; j < nc; ++j) part[(int64_t)blockIdx.y * Hd + c + j] = s[j];
+}
+
+// out[i] = sum_s part[s*n + i] (fixed order); optional copy to dW; W -= lr * out.
+__global__ __launch_bounds__(kThreads) void sum_slices_sgd_kernel(const float* __restrict__ part,
+                                                                  int slices, int64_t n,
+                                                                  float* __restrict__ dw,
+                                                                  float* __restrict__ w, float lr) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+        float g = part[i];
+        for (int s = 1; s < slices; ++s) g += part[(int64_t)s * n + i];
+        if (dw) dw[i] = g;
+        if (lr != 0.0f) w[i] = w[i] - lr * g;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void loss_kernel(const float* __restrict__ sq, int B,
+                                                        float* __restrict__ loss) {
+    __shared__ float part[kThreads / 64];
+    float acc = 0.0f;
+    for (int i = threadIdx.x; i < B; i += kThreads) acc += sq[i];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float r = 0.0f;
+        for (int w = 0; w < kThreads / 64; ++w) r += part[w];
+        *loss = r / (float)B;
+    }
+}
+
+unsigned capped_grid(int64_t n) {
+    int64_t want = (n + kThreads - 1) / kThreads;
+    int64_t cap = (int64_t)ch::num_cus() * 8;
+    if (want > cap) want = cap;
+    return (unsigned)(want < 1 ? 1 : want);
+}
+
+// Split count for X^T d1: enough workgroups to fill the chip, K divisible.
+int choose_splits(int D, int Hd, int B) {
+    const int tiles = ((D + 127) / 128) * ((Hd + 127) / 128);
+    int splits = 1;
+    while (splits < 16 && tiles * splits < 4 * ch::num_cus() && B % (splits * 2 * 16) == 0) splits *= 2;
+    return splits;
+}
+
+}  // namespace
+
+extern "C" int32_t cleave_hip_mlp_step_f32(const float* x, int64_t xlen, const float* y,
+                                           int64_t ylen, float* w1, int64_t w1len, float* w2,
+                                           int64_t w2len, float* dw1, int64_t dw1len, float* dw2,
+                                           int64_t dw2len, float* loss_dev, int32_t B, int32_t D,
+                                           int32_t Hd, float lr) {
+    CH_REQUIRE(B > 0 && D > 0 && Hd > 0, "cleave_hip_mlp_step_f32: dims must be positive (B=%d D=%d Hd=%d)", B, D, Hd);
+    CH_REQUIRE(xlen == (int64_t)B * D, "cleave_hip_mlp_step_f32: xlen %lld != B*D", (long long)xlen);
+    CH_REQUIRE(ylen == B, "cleave_hip_mlp_step_f32: ylen %lld != B", (long long)ylen);
+    CH_REQUIRE(w1len == (int64_t)D * Hd, "cleave_hip_mlp_step_f32: w1len %lld != D*Hd", (long long)w1len);
+    CH_REQUIRE(w2len == Hd, "cleave_hip_mlp_step_f32: w2len %lld != Hd", (long long)w2len);
+    CH_REQUIRE(!dw1 || dw1len == (int64_t)D * Hd, "cleave_hip_mlp_step_f32: dw1len %lld != D*Hd", (long long)dw1len);
+    CH_REQUIRE(!dw2 || dw2len == Hd, "cleave_hip_mlp_step_f32: dw2len %lld != Hd", (long long)dw2len);
+    CH_REQUIRE(x && y && w1 && w2, "cleave_hip_mlp_step_f32: null buffer");
+    CH_REQUIRE(((uintptr_t)w2 & 15) == 0, "cleave_hip_mlp_step_f32: w2 must be 16-byte aligned");
+    CH_INIT_OR_RETURN();
+
+    const int splits = choose_splits(D, Hd, B);
+    const int bands = (B + kRowsPerBand - 1) / kRowsPerBand;
+    // Scratch slot 4: H/d1 | sq | d2 | dW2 partials | dW1 slices | loss.
+    const size_t nH = (size_t)B * Hd, nPart = (size_t)bands * Hd, nSl = (size_t)splits * D * Hd;
+    auto up = [](size_t n) { return (n + 63) & ~(size_t)63; };
+    const size_t total = up(nH) + up(B) + up(B) + up(nPart) + up(nSl) + 64;
+    float* base = (float*)ch::scratch(4, total * sizeof(float));
+    if (!base) return CLEAVE_HIP_ERR_OOM;
+    float* H = base;
+    float* sq = H + up(nH);
+    float* d2 = sq + up(B);
+    float* part = d2 + up(B);
+    float* slices = part + up(nPart);
+    float* loss_tmp = slices + up(nSl);
+    hipStream_t st = ch::stream();
+
+    int32_t rc = ch::gemm_f32_device(x, w1, H, B, Hd, D, 0, 0, 1);
+    if (rc != CLEAVE_HIP_OK) return rc;
+    sigmoid_inplace_kernel<<<capped_grid(nH / 4 + 1), kThreads, 0, st>>>(H, (int64_t)nH);
+    CH_LAUNCHED("sigmoid_inplace_kernel");
+    row_pass_kernel<<<(B + 3) / 4, kThreads, 0, st>>>(H, w2, y, B, Hd, sq, d2);
+    CH_LAUNCHED("row_pass_kernel");
+    loss_kernel<<<1, kThreads, 0, st>>>(sq, B, loss_dev ? loss_dev : loss_tmp);
+    CH_LAUNCHED("loss_kernel");
+    dim3 cgrid((unsigned)((Hd + 4 * kThreads - 1) / (4 * kThreads)), (unsigned)bands);
+    col_pass_kernel<<<cgrid, kThreads, 0, st>>>(H, w2, d2, B, Hd, part);
+    CH_LAUNCHED("col_pass_kernel");
+    sum_slices_sgd_kernel<<<capped_grid(Hd), kThreads, 0, st>>>(part, bands, Hd, dw2, w2, lr);
+    CH_LAUNCHED("sum_slices_sgd_kernel(dW2)");
+    rc = ch::gemm_f32_device(x, H, slices, D, Hd, B, 1, 0, splits);
+    if (rc != CLEAVE_HIP_OK) return rc;
+    sum_slices_sgd_kernel<<<capped_grid((int64_t)D * Hd), kThreads, 0, st>>>(slices, splits, (int64_t)D * Hd, dw1, w1, lr);
+    CH_LAUNCHED("sum_slices_sgd_kernel(dW1)");
+    return CLEAVE_HIP_OK;
+}

@@ -1,0 +1,341 @@
+// reduce.hip -- Sum / Mean / Max (stdlib/nn/nn.cleave:111-149) and the exact
+// u64 sum of u32 escape counts.
+//
+// Two stages, both deterministic for a given length: stage 1 runs a fixed
+// grid (a function of the length and the CU count only); each thread folds
+// 16-byte vectors in registers, the wave combines lanes with cross-lane
+// shuffles, LDS carries the 4 wave results to one block result.  Stage 2 is
+// one block over the block results.
+//
+// Max semantics: the reference folds acc = v[0]; if v[i] > acc then acc = v[i]
+// (cmpf ogt, stdlib/num/num.cleave:303).  A NaN at i > 0 never wins; a NaN at
+// v[0] is the answer.  With v[0] not NaN the fold returns the first index of
+// the largest non-NaN value, which is associative as (value desc, index asc)
+// -- that is what the tree combines (-0 and +0 compare equal, so the earlier
+// one is kept, as in the fold).
+#include <cfloat>
+
+#include "common.hpp"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+
+unsigned stage1_blocks(int64_t nvec) {
+    int64_t want = (nvec + (int64_t)kThreads * kUnroll - 1) / ((int64_t)kThreads * kUnroll);
+    int64_t cap = (int64_t)ch::num_cus() * 4;
+    if (want > cap) want = cap;
+    return (unsigned)(want < 1 ? 1 : want);
+}
+
+// ---- sum f32 --------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ float block_sum(float v) {
+    __shared__ float part[kThreads / 64];
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = 0.0f;
+    if (threadIdx.x == 0)
+        for (int w = 0; w < kThreads / 64; ++w) r += part[w];
+    return r;  // valid in thread 0
+}
+
+__global__ __launch_bounds__(kThreads) void sum_f32_stage1(const float* __restrict__ x,
+                                                           int64_t n, float* __restrict__ partial,
+                                                           int aligned) {
+    float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+    if (aligned) {
+        const int64_t nv = n / 4;
+        const int64_t step = (int64_t)gridDim.x * kThreads * kUnroll;
+        for (int64_t base = (int64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x; base < nv; base += step) {
+            float4 v[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                int64_t i = base + (int64_t)u * kThreads;
+                v[u] = i < nv ? reinterpret_cast<const float4*>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                acc0 += v[u].x;
+                acc1 += v[u].y;
+                acc2 += v[u].z;
+                acc3 += v[u].w;
+            }
+        }
+        if (blockIdx.x == 0 && threadIdx.x < (n & 3)) acc0 += x[nv * 4 + threadIdx.x];
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+            acc0 += x[i];
+    }
+    float r = block_sum((acc0 + acc1) + (acc2 + acc3));
+    if (threadIdx.x == 0) partial[blockIdx.x] = r;
+}
+
+__global__ __launch_bounds__(kThreads) void sum_f32_stage2(const float* __restrict__ partial,
+                                                           int nparts, float* __restrict__ out) {
+    float acc = 0.f;
+    for (int i = threadIdx.x; i < nparts; i += kThreads) acc += partial[i];
+    float r = block_sum(acc);
+    if (threadIdx.x == 0) *out = r;
+}
+
+// ---- max / argmax f32 -------------------------------------------------------
+struct Best {
+    float v;
+    int64_t i;
+};
+__device__ __forceinline__ void take_better(Best& a, float v, int64_t i) {
+    // Comparisons involving NaN are false, so a NaN candidate never wins.
+    if (v > a.v || (v == a.v && i < a.i)) {
+        a.v = v;
+        a.i = i;
+    }
+}
+__device__ __forceinline__ Best wave_best(Best b) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float v = __shfl_xor(b.v, o);
+        int64_t i = __shfl_xor(b.i, o);
+        take_better(b, v, i);
+    }
+    return b;
+}
+__device__ Best block_best(Best b) {
+    __shared__ float pv[kThreads / 64];
+    __shared__ int64_t pi[kThreads / 64];
+    b = wave_best(b);
+    if ((threadIdx.x & 63) == 0) {
+        pv[threadIdx.x >> 6] = b.v;
+        pi[threadIdx.x >> 6] = b.i;
+    }
+    __syncthreads();
+    Best r{-INFINITY, INT64_MAX};
+    if (threadIdx.x == 0)
+        for (int w = 0; w < kThreads / 64; ++w) take_better(r, pv[w], pi[w]);
+    return r;
+}
+
+__global__ __launch_bounds__(kThreads) void max_f32_stage1(const float* __restrict__ x, int64_t n,
+                                                           float* __restrict__ pv,
+                                                           int64_t* __restrict__ pi, int aligned) {
+    Best b{-INFINITY, INT64_MAX};
+    if (aligned) {
+        const int64_t nv = n / 4;
+        const int64_t step = (int64_t)gridDim.x * kThreads * kUnroll;
+        for (int64_t base = (int64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x; base < nv; base += step) {
+            float4 v[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                int64_t i = base + (int64_t)u * kThreads;
+                if (i < nv) v[u] = reinterpret_cast<const float4*>(x)[i];
+            }
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                int64_t i = base + (int64_t)u * kThreads;
+                if (i < nv) {
+                    take_better(b, v[u].x, 4 * i + 0);
+                    take_better(b, v[u].y, 4 * i + 1);
+                    take_better(b, v[u].z, 4 * i + 2);
+                    take_better(b, v[u].w, 4 * i + 3);
+                }
+            }
+        }
+        if (blockIdx.x == 0 && threadIdx.x < (n & 3)) take_better(b, x[nv * 4 + threadIdx.x], nv * 4 + threadIdx.x);
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+            take_better(b, x[i], i);
+    }
+    Best r = block_best(b);
+    if (threadIdx.x == 0) {
+        pv[blockIdx.x] = r.v;
+        pi[blockIdx.x] = r.i;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void max_f32_stage2(const float* __restrict__ x,
+                                                           const float* __restrict__ pv,
+                                                           const int64_t* __restrict__ pi,
+                                                           int nparts, float* __restrict__ out_v,
+                                                           int64_t* __restrict__ out_i) {
+    Best b{-INFINITY, INT64_MAX};
+    for (int i = threadIdx.x; i < nparts; i += kThreads) take_better(b, pv[i], pi[i]);
+    Best r = block_best(b);
+    if (threadIdx.x == 0) {
+        float x0 = x[0];
+        if (x0 != x0) {  // nothing compares > NaN, so the fold keeps a NaN v[0]
+            r.v = x0;
+            r.i = 0;
+        } else if (r.i == INT64_MAX) {  // every other element is NaN
+            r.v = x0;
+            r.i = 0;
+        }
+        if (out_v) *out_v = r.v;
+        if (out_i) *out_i = r.i;
+    }
+}
+
+// ---- u64 sum of u32 -----------------------------------------------------------
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ uint64_t block_sum_u64(uint64_t v) {
+    __shared__ uint64_t part[kThreads / 64];
+    v = wave_sum_u64(v);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    uint64_t r = 0;
+    if (threadIdx.x == 0)
+        for (int w = 0; w < kThreads / 64; ++w) r += part[w];
+    return r;
+}
+
+__global__ __launch_bounds__(kThreads) void sum_u32_stage1(const uint32_t* __restrict__ x, int64_t n,
+                                                           uint64_t* __restrict__ partial,
+                                                           int aligned) {
+    uint64_t acc = 0;
+    if (aligned) {
+        const int64_t nv = n / 4;
+        const int64_t step = (int64_t)gridDim.x * kThreads * kUnroll;
+        for (int64_t base = (int64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x; base < nv; base += step) {
+            uint4 v[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                int64_t i = base + (int64_t)u * kThreads;
+                v[u] = i < nv ? reinterpret_cast<const uint4*>(x)[i] : make_uint4(0, 0, 0, 0);
+            }
+            // Four u32 fit in u64 without overflow; add pairs in 64 bits.
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u)
+                acc += ((uint64_t)v[u].x + v[u].y) + ((uint64_t)v[u].z + v[u].w);
+        }
+        if (blockIdx.x == 0 && threadIdx.x < (n & 3)) acc += x[nv * 4 + threadIdx.x];
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+            acc += x[i];
+    }
+    uint64_t r = block_sum_u64(acc);
+    if (threadIdx.x == 0) partial[blockIdx.x] = r;
+}
+
+__global__ __launch_bounds__(kThreads) void sum_u64_stage2(const uint64_t* __restrict__ partial,
+                                                           int nparts, uint64_t* __restrict__ out) {
+    uint64_t acc = 0;
+    for (int i = threadIdx.x; i < nparts; i += kThreads) acc += partial[i];
+    uint64_t r = block_sum_u64(acc);
+    if (threadIdx.x == 0) *out = r;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int32_t cleave_hip_reduce_sum_f32(const float* x, int64_t len, float* out_dev) {
+    CH_REQUIRE(len >= 1, "cleave_hip_reduce_sum_f32: length must be >= 1 (sum reads v[0])");
+    CH_REQUIRE(x && out_dev, "cleave_hip_reduce_sum_f32: null buffer");
+    CH_INIT_OR_RETURN();
+    const int aligned = aligned16(x);
+    unsigned blocks = stage1_blocks(aligned ? len / 4 + 1 : len / kUnroll + 1);
+    float* part = (float*)ch::scratch(0, sizeof(float) * blocks);
+    if (!part) return CLEAVE_HIP_ERR_OOM;
+    sum_f32_stage1<<<blocks, kThreads, 0, ch::stream()>>>(x, len, part, aligned);
+    CH_LAUNCHED("sum_f32_stage1");
+    sum_f32_stage2<<<1, kThreads, 0, ch::stream()>>>(part, (int)blocks, out_dev);
+    CH_LAUNCHED("sum_f32_stage2");
+    return CLEAVE_HIP_OK;
+}
+
+int32_t cleave_hip_reduce_max_f32(const float* x, int64_t len, float* max_dev, int64_t* argmax_dev) {
+    CH_REQUIRE(len >= 1, "cleave_hip_reduce_max_f32: length must be >= 1 (max_of reads v[0])");
+    CH_REQUIRE(x && (max_dev || argmax_dev), "cleave_hip_reduce_max_f32: null buffer");
+    CH_INIT_OR_RETURN();
+    const int aligned = aligned16(x);
+    unsigned blocks = stage1_blocks(aligned ? len / 4 + 1 : len / kUnroll + 1);
+    char* base = (char*)ch::scratch(1, (sizeof(float) + sizeof(int64_t)) * blocks + 64);
+    if (!base) return CLEAVE_HIP_ERR_OOM;
+    int64_t* pi = (int64_t*)base;
+    float* pv = (float*)(base + sizeof(int64_t) * blocks);
+    max_f32_stage1<<<blocks, kThreads, 0, ch::stream()>>>(x, len, pv, pi, aligned);
+    CH_LAUNCHED("max_f32_stage1");
+    max_f32_stage2<<<1, kThreads, 0, ch::stream()>>>(x, pv, pi, (int)blocks, max_dev, argmax_dev);
+    CH_LAUNCHED("max_f32_stage2");
+    return CLEAVE_HIP_OK;
+}
+
+int32_t cleave_hip_reduce_sum_u32_u64(const uint32_t* x, int64_t len, uint64_t* out_dev) {
+    CH_REQUIRE(len >= 0, "cleave_hip_reduce_sum_u32_u64: negative length");
+    CH_REQUIRE(x && out_dev, "cleave_hip_reduce_sum_u32_u64: null buffer");
+    CH_INIT_OR_RETURN();
+    const int aligned = aligned16(x);
+    unsigned blocks = stage1_blocks(aligned ? len / 4 + 1 : len / kUnroll + 1);
+    uint64_t* part = (uint64_t*)ch::scratch(2, sizeof(uint64_t) * blocks);
+    if (!part) return CLEAVE_HIP_ERR_OOM;
+    sum_u32_stage1<<<blocks, kThreads, 0, ch::stream()>>>(x, len, part, aligned);
+    CH_LAUNCHED("sum_u32_stage1");
+    sum_u64_stage2<<<1, kThreads, 0, ch::stream()>>>(part, (int)blocks, out_dev);
+    CH_LAUNCHED("sum_u64_stage2");
+    return CLEAVE_HIP_OK;
+}
+
+// Host-returning forms: queue the reduction into a library-owned device word,
+// then copy it back (synchronising the stream).
+float cleave_hip_sum_f32(const float* x, int64_t len) {
+    ch::clear_error();
+    if (ch::ensure_init() != CLEAVE_HIP_OK) return NAN;
+    float* d = (float*)ch::scratch(3, 64);
+    if (!d) return NAN;
+    if (cleave_hip_reduce_sum_f32(x, len, d) != CLEAVE_HIP_OK) return NAN;
+    float r = NAN;
+    if (cleave_hip_download(&r, d, sizeof(float)) != (int64_t)sizeof(float)) return NAN;
+    return r;
+}
+
+float cleave_hip_mean_f32(const float* x, int64_t len) {
+    float s = cleave_hip_sum_f32(x, len);
+    return s / (float)len;  // sum(v) / sitofp(N), stdlib/nn/nn.cleave:135-138
+}
+
+float cleave_hip_max_of_f32(const float* x, int64_t len) {
+    ch::clear_error();
+    if (ch::ensure_init() != CLEAVE_HIP_OK) return NAN;
+    float* d = (float*)ch::scratch(3, 64);
+    if (!d) return NAN;
+    if (cleave_hip_reduce_max_f32(x, len, d, nullptr) != CLEAVE_HIP_OK) return NAN;
+    float r = NAN;
+    if (cleave_hip_download(&r, d, sizeof(float)) != (int64_t)sizeof(float)) return NAN;
+    return r;
+}
+
+int64_t cleave_hip_argmax_f32(const float* x, int64_t len) {
+    ch::clear_error();
+    if (ch::ensure_init() != CLEAVE_HIP_OK) return -1;
+    int64_t* d = (int64_t*)ch::scratch(3, 64);
+    if (!d) return -1;
+    if (cleave_hip_reduce_max_f32(x, len, nullptr, d) != CLEAVE_HIP_OK) return -1;
+    int64_t r = -1;
+    if (cleave_hip_download(&r, d, sizeof(int64_t)) != (int64_t)sizeof(int64_t)) return -1;
+    return r;
+}
+
+uint64_t cleave_hip_sum_u32_u64(const uint32_t* x, int64_t len) {
+    ch::clear_error();
+    if (ch::ensure_init() != CLEAVE_HIP_OK) return 0;
+    uint64_t* d = (uint64_t*)ch::scratch(3, 64);
+    if (!d) return 0;
+    if (cleave_hip_reduce_sum_u32_u64(x, len, d) != CLEAVE_HIP_OK) return 0;
+    uint64_t r = 0;
+    if (cleave_hip_download(&r, d, sizeof(uint64_t)) != (int64_t)sizeof(uint64_t)) return 0;
+    return r;
+}
+
+}  // extern "C"

@@ -1,0 +1,233 @@
+/*
+ * cleave_hip.h -- C ABI of libcleave_hip.so, the MI355X (gfx950) backend for
+ * cleave's tensor operator surface.
+ *
+ * Conventions follow cleave-rt, the reference's only native boundary
+ * (/root/reference/cleave-rt/src/lib.rs:13-213):
+ *   - plain `extern "C"` symbols, no C++ mangling (lib.rs:13-21);
+ *   - scalars by value: int32_t dims, int64_t lengths, float scalars
+ *     (cleave/src/rust_bindings.rs:21-35);
+ *   - every array operand is a pair (pointer, int64_t element count), the
+ *     form mlir_lower.rs emits for an array crossing an extern call
+ *     (cleave/src/mlir_lower.rs:1096-1114, :1720-1751; sum_bytes,
+ *     cleave-rt/src/lib.rs:86-90);
+ *   - arrays are never returned: outputs are caller-allocated (ptr, len)
+ *     pairs (cleave/src/mlir_lower.rs:1062-1075);
+ *   - device buffers are opaque handles, like stdlib's RawBuf
+ *     (stdlib/dynarray/dynarray.cleave:29), allocated by cleave_hip_buf_alloc;
+ *   - errors: cleave-rt panics (lib.rs:69, :120, :148).  Here every call
+ *     validates its arguments on the host before any launch; by default an
+ *     error prints a message to stderr and aborts (same observable
+ *     behaviour); cleave_hip_set_abort_on_error(0) switches to returning a
+ *     negative status with the message kept for cleave_hip_last_error_message().
+ *
+ * Threading/sync: one thread, one HIP stream owned by the library
+ * (cleave/src/main.rs:607 runs JIT code on the calling thread).  Calls that
+ * return host-visible data (downloads, scalar-returning reductions)
+ * synchronise the stream before returning; calls that only write device
+ * buffers are queued on the stream and return immediately.  Pointers passed
+ * as tensor operands are device pointers from cleave_hip_buf_alloc; host
+ * pointers appear only in upload/download.
+ */
+#ifndef CLEAVE_HIP_H
+#define CLEAVE_HIP_H
+
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define CLEAVE_HIP_API __attribute__((visibility("default")))
+#else
+#define CLEAVE_HIP_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define CLEAVE_HIP_OK 0
+#define CLEAVE_HIP_ERR_RUNTIME (-1) /* HIP runtime error or no device */
+#define CLEAVE_HIP_ERR_ARG (-2)     /* length/shape/flag validation failed */
+#define CLEAVE_HIP_ERR_OOM (-3)     /* device allocation failed */
+
+/* ---------------------------------------------------------------------- */
+/* runtime (replaces cleave-rt's allocation and registration surface)     */
+/* ---------------------------------------------------------------------- */
+
+/* Selects device 0 and creates the library stream.  Idempotent.  Every other
+ * entry point calls it implicitly.  (No reference counterpart: the reference
+ * runs on the CPU with no device to open.) */
+CLEAVE_HIP_API int32_t cleave_hip_init(void);
+/* 1 when a device is usable, 0 otherwise (never aborts). */
+CLEAVE_HIP_API int32_t cleave_hip_device_available(void);
+
+/* Device allocation, 256-byte aligned.  Mirrors cleave_alloc
+ * (cleave-rt/src/lib.rs:56-71; that one is 16-byte aligned and never freed);
+ * here the library owns the memory and cleave_hip_buf_free releases it. */
+CLEAVE_HIP_API void* cleave_hip_buf_alloc(int64_t bytes);
+CLEAVE_HIP_API void cleave_hip_buf_free(void* buf);
+/* Host <-> device copies on the library stream; both return the byte count
+ * (like print_bytes' "returns len", cleave-rt/src/lib.rs:114-122) after the
+ * stream has drained, so the host buffer may be reused at once. */
+CLEAVE_HIP_API int64_t cleave_hip_upload(void* dst_dev, const void* src_host, int64_t bytes);
+CLEAVE_HIP_API int64_t cleave_hip_download(void* dst_host, const void* src_dev, int64_t bytes);
+/* Waits for all queued work. */
+CLEAVE_HIP_API int32_t cleave_hip_sync(void);
+
+/* Error channel. */
+CLEAVE_HIP_API void cleave_hip_set_abort_on_error(int32_t on);
+CLEAVE_HIP_API int32_t cleave_hip_last_error(void);
+CLEAVE_HIP_API const char* cleave_hip_last_error_message(void);
+
+/* Events on the library stream (timing of queued work). */
+CLEAVE_HIP_API void* cleave_hip_event_create(void);
+CLEAVE_HIP_API int32_t cleave_hip_event_record(void* ev);
+CLEAVE_HIP_API float cleave_hip_event_elapsed_ms(void* start, void* stop); /* syncs on stop */
+CLEAVE_HIP_API void cleave_hip_event_destroy(void* ev);
+
+/* Symbol table for a JIT host: name -> function pointer, the same shape as
+ * register_cleave_rt_symbols (cleave/src/pipeline.rs:159-198).  Returns the
+ * table and writes its length to *count. */
+typedef struct cleave_hip_symbol {
+    const char* name;
+    void* fn;
+} cleave_hip_symbol;
+CLEAVE_HIP_API const cleave_hip_symbol* cleave_hip_symbols(int64_t* count);
+
+/* ---------------------------------------------------------------------- */
+/* synthetic inputs (the reference has no RNG; generator is build-defined) */
+/* ---------------------------------------------------------------------- */
+
+/* out[i] = lo + (hi-lo) * u_i, u_i = (splitmix64_i(seed) >> 40) * 2^-24. */
+CLEAVE_HIP_API int32_t cleave_hip_fill_uniform_f32(float* out, int64_t len, uint64_t seed, float lo, float hi);
+/* Box-Muller on draws 2i and 2i+1 (cos branch), mean + std * z. */
+CLEAVE_HIP_API int32_t cleave_hip_fill_normal_f32(float* out, int64_t len, uint64_t seed, float mean, float std);
+/* out[i] = (u_i < p) ? 1 : 0. */
+CLEAVE_HIP_API int32_t cleave_hip_fill_bernoulli_f32(float* out, int64_t len, uint64_t seed, float p);
+/* f32 -> bf16 round-to-nearest-even; bf16 stored as uint16_t. */
+CLEAVE_HIP_API int32_t cleave_hip_cast_f32_bf16(const float* in, int64_t inlen, uint16_t* out, int64_t outlen);
+
+/* ---------------------------------------------------------------------- */
+/* MatMul (stdlib/linalg/matrix.cleave:22-61)                               */
+/* ---------------------------------------------------------------------- */
+
+/* C[M x N] = op(A) * op(B), fp32 accumulate, C overwritten (the reference
+ * zero-fills its accumulator, stdlib/linalg/matrix.cleave:59).
+ * trans_a = 0: A stored M x K row-major; 1: A stored K x M (C = A^T B).
+ * trans_b = 0: B stored K x N row-major; 1: B stored N x K (C = A B^T).
+ * The A^T B / A B^T forms are the reverse-mode halves of the product rule
+ * add(matmul(d(a),b), matmul(a,d(b))) (stdlib/linalg/matrix.cleave:24).
+ * Requires alen == M*K, blen == K*N, clen == M*N. */
+CLEAVE_HIP_API int32_t cleave_hip_matmul_f32(const float* a, int64_t alen, const float* b, int64_t blen,
+                              float* c, int64_t clen, int32_t M, int32_t N, int32_t K,
+                              int32_t trans_a, int32_t trans_b);
+/* batch independent f32 matmuls, operands packed back to back. */
+CLEAVE_HIP_API int32_t cleave_hip_matmul_batched_f32(const float* a, int64_t alen, const float* b,
+                                      int64_t blen, float* c, int64_t clen, int32_t batch,
+                                      int32_t M, int32_t N, int32_t K, int32_t trans_a,
+                                      int32_t trans_b);
+/* bf16 inputs (uint16_t storage), fp32 accumulate and fp32 output.
+ * Extension of the same operator (the reference is f32/f64 only). */
+CLEAVE_HIP_API int32_t cleave_hip_matmul_bf16(const uint16_t* a, int64_t alen, const uint16_t* b,
+                               int64_t blen, float* c, int64_t clen, int32_t M, int32_t N,
+                               int32_t K, int32_t trans_a, int32_t trans_b);
+CLEAVE_HIP_API int32_t cleave_hip_matmul_batched_bf16(const uint16_t* a, int64_t alen, const uint16_t* b,
+                                       int64_t blen, float* c, int64_t clen, int32_t batch,
+                                       int32_t M, int32_t N, int32_t K);
+
+/* ---------------------------------------------------------------------- */
+/* Ring<Tensor> elementwise (stdlib/linalg/tensor.cleave:66-80)             */
+/* Same-shape operands, no broadcasting (as in the reference).              */
+/* ---------------------------------------------------------------------- */
+
+CLEAVE_HIP_API int32_t cleave_hip_add_f32(const float* a, int64_t alen, const float* b, int64_t blen,
+                           float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_sub_f32(const float* a, int64_t alen, const float* b, int64_t blen,
+                           float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_mul_f32(const float* a, int64_t alen, const float* b, int64_t blen,
+                           float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_div_f32(const float* a, int64_t alen, const float* b, int64_t blen,
+                           float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_neg_f32(const float* a, int64_t alen, float* out, int64_t outlen);
+/* Ring::zero (stdlib/linalg/tensor.cleave:79). */
+CLEAVE_HIP_API int32_t cleave_hip_zero_f32(float* out, int64_t outlen);
+
+/* ---------------------------------------------------------------------- */
+/* Activation<Tensor> (stdlib/nn/nn.cleave:82-95)                           */
+/* ---------------------------------------------------------------------- */
+
+/* arith.maximumf(x, 0): NaN propagates, max(-0,+0) = +0 (nn.cleave:83-85). */
+CLEAVE_HIP_API int32_t cleave_hip_relu_f32(const float* x, int64_t xlen, float* out, int64_t outlen);
+/* 1 / (1 + exp(-x)) (nn.cleave:87-93). */
+CLEAVE_HIP_API int32_t cleave_hip_sigmoid_f32(const float* x, int64_t xlen, float* out, int64_t outlen);
+/* math.tanh (nn.cleave:94). */
+CLEAVE_HIP_API int32_t cleave_hip_tanh_f32(const float* x, int64_t xlen, float* out, int64_t outlen);
+
+/* ---------------------------------------------------------------------- */
+/* backward ops: reverse-mode forms of the reference's derivative rules     */
+/* (stdlib/num/num.cleave:123-136, :222-223; stdlib/linalg/tensor.cleave:126)*/
+/* ---------------------------------------------------------------------- */
+
+/* out = g * s * (1 - s), s = sigmoid(x) from the forward pass. */
+CLEAVE_HIP_API int32_t cleave_hip_sigmoid_bwd_f32(const float* s, int64_t slen, const float* g, int64_t glen,
+                                   float* out, int64_t outlen);
+/* out = g * (1 - t*t), t = tanh(x) (num.cleave:223). */
+CLEAVE_HIP_API int32_t cleave_hip_tanh_bwd_f32(const float* t, int64_t tlen, const float* g, int64_t glen,
+                                float* out, int64_t outlen);
+/* out = x > 0 ? g : 0. */
+CLEAVE_HIP_API int32_t cleave_hip_relu_bwd_f32(const float* x, int64_t xlen, const float* g, int64_t glen,
+                                float* out, int64_t outlen);
+/* quotient rule (num.cleave:132-134): da = g / b, db = -(g*a) / (b*b). */
+CLEAVE_HIP_API int32_t cleave_hip_div_bwd_f32(const float* a, int64_t alen, const float* b, int64_t blen,
+                               const float* g, int64_t glen, float* da, int64_t dalen,
+                               float* db, int64_t dblen);
+/* SGD update in place: w = w - lr * g (examples/xor_tensor.cleave:86-90). */
+CLEAVE_HIP_API int32_t cleave_hip_sgd_update_f32(float* w, int64_t wlen, const float* g, int64_t glen,
+                                  float lr);
+
+/* ---------------------------------------------------------------------- */
+/* Sum / Mean / Max (stdlib/nn/nn.cleave:111-149)                           */
+/* ---------------------------------------------------------------------- */
+
+/* Device-result forms (queued; result written to a device scalar). */
+CLEAVE_HIP_API int32_t cleave_hip_reduce_sum_f32(const float* x, int64_t len, float* out_dev);
+CLEAVE_HIP_API int32_t cleave_hip_reduce_max_f32(const float* x, int64_t len, float* max_dev,
+                                  int64_t* argmax_dev);
+CLEAVE_HIP_API int32_t cleave_hip_reduce_sum_u32_u64(const uint32_t* x, int64_t len, uint64_t* out_dev);
+/* Host-returning forms, like the stdlib functions (synchronise). */
+CLEAVE_HIP_API float cleave_hip_sum_f32(const float* x, int64_t len);
+CLEAVE_HIP_API float cleave_hip_mean_f32(const float* x, int64_t len);
+CLEAVE_HIP_API float cleave_hip_max_of_f32(const float* x, int64_t len);
+/* First index of the value max_of returns (extension; the reference has no argmax). */
+CLEAVE_HIP_API int64_t cleave_hip_argmax_f32(const float* x, int64_t len);
+CLEAVE_HIP_API uint64_t cleave_hip_sum_u32_u64(const uint32_t* x, int64_t len);
+
+/* ---------------------------------------------------------------------- */
+/* escape_count map (examples/mandelbrot.cleave:14-26) in f32                */
+/* ---------------------------------------------------------------------- */
+
+/* out[row*width + col] = escape count of c = (x0 + col*dx, y0 + row*dy),
+ * max_iter if it never escapes.  Requires outlen == width*height. */
+CLEAVE_HIP_API int32_t cleave_hip_mandelbrot_u32(uint32_t* out, int64_t outlen, int32_t width, int32_t height,
+                                  float x0, float y0, float dx, float dy, int32_t max_iter);
+
+/* ---------------------------------------------------------------------- */
+/* 2-layer MLP step (style of examples/xor_tensor.cleave:38-92)             */
+/* ---------------------------------------------------------------------- */
+
+/* H = sigmoid(X W1), yhat = sigmoid(H W2), loss = mean((yhat - y)^2),
+ * reverse-mode gradients, then W -= lr * dW in place (lr = 0 skips the
+ * update).  X [B x D], y [B], W1 [D x Hd], W2 [Hd].  dW1/dW2 receive the
+ * gradients when non-null (lengths D*Hd and Hd).  loss_dev receives the
+ * loss (device scalar) when non-null.  Scratch (B*Hd + 2*B floats) is
+ * allocated by the library on first use and kept. */
+CLEAVE_HIP_API int32_t cleave_hip_mlp_step_f32(const float* x, int64_t xlen, const float* y, int64_t ylen,
+                                float* w1, int64_t w1len, float* w2, int64_t w2len,
+                                float* dw1, int64_t dw1len, float* dw2, int64_t dw2len,
+                                float* loss_dev, int32_t B, int32_t D, int32_t Hd, float lr);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CLEAVE_HIP_H */

@@ -1,0 +1,475 @@
+/*
+ * oracle.c -- CPU restatement of cleave's tensor hot path (TEST INFRASTRUCTURE).
+ *
+ * Checker only: loaded by tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg, never by the product library.  Build: oracle/Makefile
+ * (gcc -O2 -ffp-contract=off -fopenmp).  Each function cites the reference
+ * source whose lowered semantics it restates.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* generators                                                               */
+/* ------------------------------------------------------------------------ */
+
+static uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+/* splitmix64 (Steele, Lea, Flood 2014): state += golden; out = mix(state).
+ * The i-th output of a stream seeded with s is mix(s + (i+1)*golden). */
+uint64_t or_splitmix64_at(uint64_t seed, uint64_t i) {
+    return mix64(seed + (i + 1) * 0x9E3779B97F4A7C15ULL);
+}
+
+static float unit24(uint64_t x) { /* [0,1) with 2^-24 spacing, exact in f32 */
+    return (float)(x >> 40) * 5.9604644775390625e-08f;
+}
+
+void or_fill_uniform_f32(float* out, int64_t n, uint64_t seed, float lo, float hi) {
+    const float w = hi - lo;
+    for (int64_t i = 0; i < n; ++i) out[i] = lo + w * unit24(or_splitmix64_at(seed, (uint64_t)i));
+}
+
+void or_fill_normal_f32(float* out, int64_t n, uint64_t seed, float mean, float std) {
+    for (int64_t i = 0; i < n; ++i) {
+        uint64_t a = or_splitmix64_at(seed, 2 * (uint64_t)i);
+        uint64_t b = or_splitmix64_at(seed, 2 * (uint64_t)i + 1);
+        double u1 = ((double)(a >> 11) + 1.0) * 0x1.0p-53; /* (0,1] */
+        double u2 = (double)(b >> 11) * 0x1.0p-53;         /* [0,1) */
+        double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+        out[i] = (float)((double)mean + (double)std * z);
+    }
+}
+
+uint16_t or_f32_to_bf16(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+float or_bf16_to_f32(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+void or_f32_to_bf16_array(const float* in, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = or_f32_to_bf16(in[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* MatMul: linalg.matmul lowered by convert-linalg-to-loops.                */
+/* stdlib/linalg/matrix.cleave:59-60 zero-fills C (Ring::zero) and the      */
+/* region at cleave/src/mlir_lower.rs:2089-2120 is mulf(in0,in1) then       */
+/* addf(out, .), with k the innermost ascending loop.                       */
+/* ------------------------------------------------------------------------ */
+
+static inline float a_at(const float* A, int32_t M, int32_t K, int32_t ta, int32_t i, int32_t k) {
+    return ta ? A[(int64_t)k * M + i] : A[(int64_t)i * K + k];
+}
+static inline float b_at(const float* B, int32_t N, int32_t K, int32_t tb, int32_t k, int32_t j) {
+    return tb ? B[(int64_t)j * K + k] : B[(int64_t)k * N + j];
+}
+
+void or_matmul_f32_rows(const float* A, const float* B, float* C, int32_t M, int32_t N,
+                        int32_t K, int32_t trans_a, int32_t trans_b, int32_t row0,
+                        int32_t row1) {
+    for (int32_t i = row0; i < row1; ++i) {
+        for (int32_t j = 0; j < N; ++j) {
+            float* c = &C[(int64_t)i * N + j];
+            *c = 0.0f;
+            for (int32_t k = 0; k < K; ++k) {
+                float p = a_at(A, M, K, trans_a, i, k) * b_at(B, N, K, trans_b, k, j);
+                *c = *c + p;
+            }
+        }
+    }
+}
+
+void or_matmul_f32(const float* A, const float* B, float* C, int32_t M, int32_t N,
+                   int32_t K, int32_t trans_a, int32_t trans_b) {
+    or_matmul_f32_rows(A, B, C, M, N, K, trans_a, trans_b, 0, M);
+}
+
+void or_matmul_f32_mt(const float* A, const float* B, float* C, int32_t M, int32_t N,
+                      int32_t K, int32_t trans_a, int32_t trans_b, int32_t threads) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)
+#endif
+    for (int32_t i = 0; i < M; ++i)
+        or_matmul_f32_rows(A, B, C, M, N, K, trans_a, trans_b, i, i + 1);
+    (void)threads;
+}
+
+void or_matmul_f32_entries(const float* A, const float* B, int32_t M, int32_t N, int32_t K,
+                           int32_t trans_a, int32_t trans_b, const int32_t* ii,
+                           const int32_t* jj, int64_t n, float* out, float* absout) {
+    for (int64_t e = 0; e < n; ++e) {
+        float c = 0.0f;
+        double s = 0.0;
+        for (int32_t k = 0; k < K; ++k) {
+            float a = a_at(A, M, K, trans_a, ii[e], k);
+            float b = b_at(B, N, K, trans_b, k, jj[e]);
+            c = c + a * b;
+            s += fabs((double)a) * fabs((double)b);
+        }
+        out[e] = c;
+        if (absout) absout[e] = (float)s;
+    }
+}
+
+static inline float bf_at(const uint16_t* X, int64_t idx) { return or_bf16_to_f32(X[idx]); }
+
+void or_matmul_bf16_entries(const uint16_t* A, const uint16_t* B, int32_t M, int32_t N,
+                            int32_t K, int32_t trans_a, int32_t trans_b, const int32_t* ii,
+                            const int32_t* jj, int64_t n, float* out, float* absout) {
+    for (int64_t e = 0; e < n; ++e) {
+        float c = 0.0f;
+        double s = 0.0;
+        for (int32_t k = 0; k < K; ++k) {
+            int32_t i = ii[e], j = jj[e];
+            float a = trans_a ? bf_at(A, (int64_t)k * M + i) : bf_at(A, (int64_t)i * K + k);
+            float b = trans_b ? bf_at(B, (int64_t)j * K + k) : bf_at(B, (int64_t)k * N + j);
+            c = c + a * b;
+            s += fabs((double)a) * fabs((double)b);
+        }
+        out[e] = c;
+        if (absout) absout[e] = (float)s;
+    }
+}
+
+void or_matmul_bf16_rows(const uint16_t* A, const uint16_t* B, float* C, int32_t M,
+                         int32_t N, int32_t K, int32_t row0, int32_t row1) {
+    (void)M;
+    for (int32_t i = row0; i < row1; ++i)
+        for (int32_t j = 0; j < N; ++j) {
+            float* c = &C[(int64_t)i * N + j];
+            *c = 0.0f;
+            for (int32_t k = 0; k < K; ++k)
+                *c = *c + bf_at(A, (int64_t)i * K + k) * bf_at(B, (int64_t)k * N + j);
+        }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Ring<Tensor> (stdlib/linalg/tensor.cleave:66-71): arith.{add,sub,mul,div,neg}f */
+/* applied elementwise after elementwise-to-linalg + linalg-to-loops.       */
+/* ------------------------------------------------------------------------ */
+
+void or_add_f32(const float* a, const float* b, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = a[i] + b[i];
+}
+void or_sub_f32(const float* a, const float* b, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = a[i] - b[i];
+}
+void or_mul_f32(const float* a, const float* b, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = a[i] * b[i];
+}
+void or_div_f32(const float* a, const float* b, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = a[i] / b[i];
+}
+void or_neg_f32(const float* a, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = -a[i];
+}
+
+/* arith.maximumf (stdlib/nn/nn.cleave:83-85): IEEE 754-2019 maximum. */
+static inline float ieee_maximum(float x, float y) {
+    if (isnan(x) || isnan(y)) return x + y; /* propagates a quiet NaN */
+    if (x == y) return signbit(x) ? y : x;  /* max(-0,+0) = +0 */
+    return x > y ? x : y;
+}
+void or_relu_f32(const float* a, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = ieee_maximum(a[i], 0.0f);
+}
+
+/* stdlib/nn/nn.cleave:87-93: negf, math.exp, addf(one, e), divf(one, denom). */
+float or_sigmoid_scalar(float x) {
+    float negx = -x;
+    float e = expf(negx);
+    float denom = 1.0f + e;
+    return 1.0f / denom;
+}
+void or_sigmoid_f32(const float* a, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = or_sigmoid_scalar(a[i]);
+}
+/* stdlib/nn/nn.cleave:94: math.tanh -> libm tanhf. */
+void or_tanh_f32(const float* a, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = tanhf(a[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* backward ops: the reference's derivative rules, in reverse mode.         */
+/* sigmoid: d(1/(1+e^-x)) via quotient + exp rules (stdlib/num/num.cleave   */
+/* :132-134, :222) = e^-x/(1+e^-x)^2 = s(1-s).                               */
+/* tanh: stdlib/num/num.cleave:223, 1 - t^2.                                 */
+/* ------------------------------------------------------------------------ */
+
+void or_sigmoid_bwd_f32(const float* s, const float* g, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = g[i] * s[i] * (1.0f - s[i]);
+}
+void or_tanh_bwd_f32(const float* t, const float* g, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = g[i] * (1.0f - t[i] * t[i]);
+}
+void or_relu_bwd_f32(const float* x, const float* g, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = x[i] > 0.0f ? g[i] : 0.0f;
+}
+/* quotient rule, stdlib/num/num.cleave:132-134: d(a/b) = (da*b - a*db)/(b*b). */
+void or_div_bwd_f32(const float* a, const float* b, const float* g, float* da, float* db,
+                    int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        da[i] = g[i] / b[i];
+        db[i] = -(g[i] * a[i]) / (b[i] * b[i]);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Sum / Mean / Max (stdlib/nn/nn.cleave:111-149).                          */
+/* ------------------------------------------------------------------------ */
+
+float or_sum_f32(const float* v, int64_t n) {
+    float acc = v[0];
+    for (int64_t i = 1; i < n; ++i) acc = acc + v[i];
+    return acc;
+}
+float or_mean_f32(const float* v, int64_t n) { return or_sum_f32(v, n) / (float)n; }
+float or_max_of_f32(const float* v, int64_t n) {
+    float acc = v[0];
+    for (int64_t i = 1; i < n; ++i)
+        if (v[i] > acc) acc = v[i]; /* cmpf ogt: false when either side is NaN */
+    return acc;
+}
+int64_t or_argmax_f32(const float* v, int64_t n) {
+    float acc = v[0];
+    int64_t idx = 0;
+    for (int64_t i = 1; i < n; ++i)
+        if (v[i] > acc) {
+            acc = v[i];
+            idx = i;
+        }
+    return idx;
+}
+uint64_t or_sum_u32_u64(const uint32_t* v, int64_t n) {
+    uint64_t s = 0;
+    for (int64_t i = 0; i < n; ++i) s += v[i];
+    return s;
+}
+
+/* ------------------------------------------------------------------------ */
+/* escape_count (examples/mandelbrot.cleave:14-26) with Complex mul/add     */
+/* (stdlib/complex/complex.cleave:25-32) and magnitude_sq (:54), in f32.    */
+/* ------------------------------------------------------------------------ */
+
+uint32_t or_escape_count_f32(float cr, float ci, int32_t max_iter) {
+    float zr = 0.0f, zi = 0.0f;
+    for (int32_t n = 0; n < max_iter; ++n) {
+        float re = zr * zr - zi * zi; /* x.real*y.real - x.imag*y.imag */
+        float im = zr * zi + zi * zr; /* x.real*y.imag + x.imag*y.real */
+        zr = re + cr;
+        zi = im + ci;
+        if (zr * zr + zi * zi > 4.0f) return (uint32_t)n;
+    }
+    return (uint32_t)max_iter;
+}
+
+uint32_t or_escape_count_latch_f32(float cr, float ci, int32_t max_iter) {
+    float zr = 0.0f, zi = 0.0f;
+    int32_t count = max_iter, escaped = 0;
+    for (int32_t n = 0; n < max_iter; ++n) {
+        float re = zr * zr - zi * zi;
+        float im = zr * zi + zi * zr;
+        zr = re + cr;
+        zi = im + ci;
+        if (!escaped && (zr * zr + zi * zi > 4.0f)) {
+            escaped = 1;
+            count = n;
+        }
+    }
+    return (uint32_t)count;
+}
+
+void or_mandelbrot_rows(uint32_t* out, int32_t width, int32_t height, float x0, float y0,
+                        float dx, float dy, int32_t max_iter, int32_t row0, int32_t row1) {
+    (void)height;
+    for (int32_t r = row0; r < row1; ++r) {
+        float ci = y0 + (float)r * dy;
+        for (int32_t c = 0; c < width; ++c) {
+            float cr = x0 + (float)c * dx;
+            out[(int64_t)r * width + c] = or_escape_count_f32(cr, ci, max_iter);
+        }
+    }
+}
+
+void or_mandelbrot_mt(uint32_t* out, int32_t width, int32_t height, float x0, float y0,
+                      float dx, float dy, int32_t max_iter, int32_t threads) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)
+#endif
+    for (int32_t r = 0; r < height; ++r)
+        or_mandelbrot_rows(out, width, height, x0, y0, dx, dy, max_iter, r, r + 1);
+    (void)threads;
+}
+
+/* ------------------------------------------------------------------------ */
+/* 2-layer MLP step in the style of examples/xor_tensor.cleave:38-92 with   */
+/* the config's batch mean and no biases.  Forward ops follow the stdlib    */
+/* bodies above; the backward applies the reference's derivative rules     */
+/* (matmul product rule stdlib/linalg/matrix.cleave:24 in reverse mode,     */
+/* d(e*e) = de*e + e*de, sigmoid' = s(1-s), d(sum/N) = d(sum)/N).           */
+/* ------------------------------------------------------------------------ */
+
+float or_mlp_step_f32(const float* X, const float* y, float* W1, float* W2, int32_t B,
+                      int32_t D, int32_t Hd, float lr, float* dW1, float* dW2,
+                      int32_t threads) {
+    if (threads < 1) threads = 1;
+    float* H = (float*)malloc(sizeof(float) * (size_t)B * (size_t)Hd);
+    float* d2 = (float*)malloc(sizeof(float) * (size_t)B);
+    /* H = sigmoid(X W1) */
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(threads)
+#endif
+    for (int32_t m = 0; m < B; ++m) {
+        float* h = &H[(int64_t)m * Hd];
+        for (int32_t n = 0; n < Hd; ++n) h[n] = 0.0f;
+        for (int32_t k = 0; k < D; ++k) {
+            float x = X[(int64_t)m * D + k];
+            const float* w = &W1[(int64_t)k * Hd];
+            for (int32_t n = 0; n < Hd; ++n) h[n] = h[n] + x * w[n]; /* k ascending per (m,n) */
+        }
+        for (int32_t n = 0; n < Hd; ++n) h[n] = or_sigmoid_scalar(h[n]);
+    }
+    /* yhat = sigmoid(H W2); e = yhat - y; loss = mean(e*e) */
+    float acc = 0.0f;
+    for (int32_t m = 0; m < B; ++m) {
+        const float* h = &H[(int64_t)m * Hd];
+        float z = 0.0f;
+        for (int32_t n = 0; n < Hd; ++n) z = z + h[n] * W2[n];
+        float yh = or_sigmoid_scalar(z);
+        float e = yh - y[m];
+        float sq = e * e;
+        acc = (m == 0) ? sq : acc + sq;
+        float gy = (e + e) / (float)B;     /* d(e*e)/dyhat = e + e; mean divides by N */
+        d2[m] = gy * yh * (1.0f - yh);     /* sigmoid' = s(1-s) */
+    }
+    float loss = acc / (float)B;
+    /* dW2 = H^T d2 (m ascending) */
+    for (int32_t n = 0; n < Hd; ++n) dW2[n] = 0.0f;
+    for (int32_t m = 0; m < B; ++m) {
+        const float* h = &H[(int64_t)m * Hd];
+        for (int32_t n = 0; n < Hd; ++n) dW2[n] = dW2[n] + h[n] * d2[m];
+    }
+    /* d1 = (d2 W2^T) * H(1-H), written over H; dW1 = X^T d1 (m ascending) */
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(threads)
+#endif
+    for (int32_t m = 0; m < B; ++m) {
+        float* h = &H[(int64_t)m * Hd];
+        for (int32_t n = 0; n < Hd; ++n) {
+            float g = d2[m] * W2[n];
+            h[n] = g * h[n] * (1.0f - h[n]);
+        }
+    }
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(threads)
+#endif
+    for (int32_t k = 0; k < D; ++k) {
+        float* dw = &dW1[(int64_t)k * Hd];
+        for (int32_t n = 0; n < Hd; ++n) dw[n] = 0.0f;
+        for (int32_t m = 0; m < B; ++m) {
+            float x = X[(int64_t)m * D + k];
+            const float* d1 = &H[(int64_t)m * Hd];
+            for (int32_t n = 0; n < Hd; ++n) dw[n] = dw[n] + x * d1[n];
+        }
+    }
+    if (lr != 0.0f) {
+        for (int64_t i = 0; i < (int64_t)D * Hd; ++i) W1[i] = W1[i] - lr * dW1[i];
+        for (int32_t n = 0; n < Hd; ++n) W2[n] = W2[n] - lr * dW2[n];
+    }
+    free(H);
+    free(d2);
+    return loss;
+}
+
+double or_mlp_loss_f64(const float* X, const float* y, const float* W1, const float* W2,
+                       int32_t B, int32_t D, int32_t Hd) {
+    double loss = 0.0;
+    for (int32_t m = 0; m < B; ++m) {
+        double z2 = 0.0;
+        for (int32_t n = 0; n < Hd; ++n) {
+            double z = 0.0;
+            for (int32_t k = 0; k < D; ++k) z += (double)X[(int64_t)m * D + k] * W1[(int64_t)k * Hd + n];
+            double h = 1.0 / (1.0 + exp(-z));
+            z2 += h * W2[n];
+        }
+        double yh = 1.0 / (1.0 + exp(-z2));
+        double e = yh - y[m];
+        loss += e * e;
+    }
+    return loss / B;
+}
+
+/* ------------------------------------------------------------------------ */
+/* examples/xor_tensor.cleave:38-92 (forward :47-56, loss :58-62, loop :81-92) */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+    float w[4], b1[2], w2[2], b2;
+} xor_params;
+
+static float xor_forward(const xor_params* p, float x1, float x2, float* h0, float* h1) {
+    /* z = matmul(x, w) + b1: k-ascending matmul, then the Ring add */
+    float z0 = 0.0f, z1 = 0.0f;
+    z0 = z0 + x1 * p->w[0];
+    z0 = z0 + x2 * p->w[2];
+    z1 = z1 + x1 * p->w[1];
+    z1 = z1 + x2 * p->w[3];
+    z0 = z0 + p->b1[0];
+    z1 = z1 + p->b1[1];
+    *h0 = or_sigmoid_scalar(z0);
+    *h1 = or_sigmoid_scalar(z1);
+    float o = 0.0f;
+    o = o + *h0 * p->w2[0];
+    o = o + *h1 * p->w2[1];
+    o = o + p->b2;
+    return or_sigmoid_scalar(o);
+}
+
+void or_xor_tensor_train(int32_t steps, float lr, float* preds4) {
+    xor_params p = {{0.5f, 0.5f, 0.5f, -0.5f}, {-0.2f, -0.2f}, {1.0f, -1.0f}, 0.0f};
+    const float xs1[4] = {0.0f, 0.0f, 1.0f, 1.0f}, xs2[4] = {0.0f, 1.0f, 0.0f, 1.0f};
+    const float ys[4] = {0.0f, 1.0f, 1.0f, 0.0f};
+    for (int32_t step = 0; step < steps; ++step) {
+        int i = step % 4;
+        float h0, h1;
+        float pred = xor_forward(&p, xs1[i], xs2[i], &h0, &h1);
+        float e = pred - ys[i];
+        float dpred = e + e;                          /* d(e*e) = de*e + e*de */
+        float dout = dpred * pred * (1.0f - pred);    /* sigmoid' = s(1-s) */
+        float dh0 = dout * p.w2[0], dh1 = dout * p.w2[1];
+        float dz0 = dh0 * h0 * (1.0f - h0), dz1 = dh1 * h1 * (1.0f - h1);
+        float g_w[4] = {dz0 * xs1[i], dz1 * xs1[i], dz0 * xs2[i], dz1 * xs2[i]};
+        float g_w2[2] = {dout * h0, dout * h1};
+        for (int k = 0; k < 4; ++k) p.w[k] = p.w[k] - lr * g_w[k];
+        p.b1[0] = p.b1[0] - lr * dz0;
+        p.b1[1] = p.b1[1] - lr * dz1;
+        p.w2[0] = p.w2[0] - lr * g_w2[0];
+        p.w2[1] = p.w2[1] - lr * g_w2[1];
+        p.b2 = p.b2 - lr * dout;
+    }
+    for (int r = 0; r < 4; ++r) {
+        float h0, h1;
+        preds4[r] = xor_forward(&p, xs1[r], xs2[r], &h0, &h1);
+    }
+}

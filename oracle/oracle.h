@@ -1,0 +1,144 @@
+/*
+ * oracle.h -- CPU restatement of cleave's tensor hot path (TEST INFRASTRUCTURE).
+ *
+ * This library is the checker, never the product.  Only tests/, the smoke()
+ * check in __graft_entry__.py and the cpu_baseline leg of bench.py may load
+ * it.  The product path (libcleave_hip.so) never links or calls it.
+ *
+ * Every function restates what the reference's CPU pipeline computes for one
+ * stdlib tensor operation after MLIR lowers it to scalar loops
+ * (convert-linalg-to-loops -> LLVM O2, no fast-math, no FP contraction;
+ * /root/reference/cleave/src/main.rs:544-607).  It is compiled with
+ * -O2 -ffp-contract=off so gcc keeps the same IEEE f32 operation order.
+ *
+ * Parity status per function (how each one is pinned) is listed next to the
+ * declaration; the checks themselves live in tests/test_oracle.py.
+ */
+#ifndef CLEAVE_ORACLE_H
+#define CLEAVE_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- synthetic-input generators (build-defined; the reference has no RNG) ---- */
+
+/* i-th output (0-based) of a splitmix64 stream seeded with `seed`.
+ * Pinned: known-answer vector of splitmix64 seeded with 0. */
+uint64_t or_splitmix64_at(uint64_t seed, uint64_t i);
+/* U[lo,hi) in f32: u = (x>>40) * 2^-24 in [0,1), exact; out = lo + (hi-lo)*u.
+ * For lo=-1, hi=1 the result is exact (2u - 1). */
+void or_fill_uniform_f32(float* out, int64_t n, uint64_t seed, float lo, float hi);
+/* N(mean, std) via Box-Muller (cos branch) on draws 2i, 2i+1, computed in
+ * double and rounded to f32.  Pinned: sample mean/variance/normality. */
+void or_fill_normal_f32(float* out, int64_t n, uint64_t seed, float mean, float std);
+/* f32 -> bf16 round-to-nearest-even (NaN kept quiet). Pinned: hand-made vectors. */
+uint16_t or_f32_to_bf16(float x);
+float or_bf16_to_f32(uint16_t h);
+void or_f32_to_bf16_array(const float* in, uint16_t* out, int64_t n);
+
+/* ---- MatMul (stdlib/linalg/matrix.cleave:27-61; region mlir_lower.rs:2089-2120) ----
+ * C = 0; for i, j, k ascending: C[i,j] = C[i,j] + a(i,k) * b(k,j).
+ * trans_a: A is stored K x M (C = A^T B); trans_b: B is stored N x K (C = A B^T).
+ * rows [row0,row1) only, so a row band can be timed or checked.
+ * Pinned: reference golden vectors (2x3*3x2, 2x2*2x2, A*0 = 0), f64 brute force. */
+void or_matmul_f32_rows(const float* A, const float* B, float* C, int32_t M, int32_t N,
+                        int32_t K, int32_t trans_a, int32_t trans_b, int32_t row0,
+                        int32_t row1);
+void or_matmul_f32(const float* A, const float* B, float* C, int32_t M, int32_t N,
+                   int32_t K, int32_t trans_a, int32_t trans_b);
+/* Same loop, rows split across `threads` OpenMP threads (each C[i,j] is an
+ * independent sequential k-sum, so the bits are identical). */
+void or_matmul_f32_mt(const float* A, const float* B, float* C, int32_t M, int32_t N,
+                      int32_t K, int32_t trans_a, int32_t trans_b, int32_t threads);
+/* Selected entries only: out[e] = C[ii[e], jj[e]], and absout[e] = sum_k |a||b|
+ * (the denominator of the GEMM tolerance). */
+void or_matmul_f32_entries(const float* A, const float* B, int32_t M, int32_t N, int32_t K,
+                           int32_t trans_a, int32_t trans_b, const int32_t* ii,
+                           const int32_t* jj, int64_t n, float* out, float* absout);
+/* bf16 inputs upcast exactly to f32, then the same f32 loop. */
+void or_matmul_bf16_entries(const uint16_t* A, const uint16_t* B, int32_t M, int32_t N,
+                            int32_t K, int32_t trans_a, int32_t trans_b, const int32_t* ii,
+                            const int32_t* jj, int64_t n, float* out, float* absout);
+void or_matmul_bf16_rows(const uint16_t* A, const uint16_t* B, float* C, int32_t M,
+                         int32_t N, int32_t K, int32_t row0, int32_t row1);
+
+/* ---- Ring<Tensor> elementwise (stdlib/linalg/tensor.cleave:66-71) and
+ *      Activation<Tensor> (stdlib/nn/nn.cleave:82-95) ---- */
+void or_add_f32(const float* a, const float* b, float* out, int64_t n);
+void or_sub_f32(const float* a, const float* b, float* out, int64_t n);
+void or_mul_f32(const float* a, const float* b, float* out, int64_t n);
+void or_div_f32(const float* a, const float* b, float* out, int64_t n);
+void or_neg_f32(const float* a, float* out, int64_t n);
+/* arith.maximumf(x, 0): IEEE-754-2019 maximum -- NaN propagates, max(-0,+0)=+0. */
+void or_relu_f32(const float* a, float* out, int64_t n);
+/* negf, math.exp (libm expf), addf(1,.), divf(1,.) in that order. */
+void or_sigmoid_f32(const float* a, float* out, int64_t n);
+void or_tanh_f32(const float* a, float* out, int64_t n);
+float or_sigmoid_scalar(float x);
+
+/* ---- derivative rules used by backward ops (stdlib/num/num.cleave:123-136, :222-223;
+ *      stdlib/nn/nn.cleave:87-93 via the quotient + exp rules) ---- */
+/* out = g * s * (1 - s), s = sigmoid(x) already computed. */
+void or_sigmoid_bwd_f32(const float* s, const float* g, float* out, int64_t n);
+/* out = g * (1 - t*t), t = tanh(x). */
+void or_tanh_bwd_f32(const float* t, const float* g, float* out, int64_t n);
+/* out = x > 0 ? g : 0 (maximumf subgradient, 0 at x == 0). */
+void or_relu_bwd_f32(const float* x, const float* g, float* out, int64_t n);
+/* div: da = g / b, db = -(g * a) / (b * b). */
+void or_div_bwd_f32(const float* a, const float* b, const float* g, float* da, float* db,
+                    int64_t n);
+
+/* ---- Sum / Mean / Max (stdlib/nn/nn.cleave:111-149) ---- */
+/* acc = v[0]; for i in 1..N: acc = acc + v[i]. */
+float or_sum_f32(const float* v, int64_t n);
+/* sum(v) / sitofp(N) (computed as f32 division). */
+float or_mean_f32(const float* v, int64_t n);
+/* acc = v[0]; for i in 1..N: if v[i] > acc (cmpf ogt) then acc = v[i]. */
+float or_max_of_f32(const float* v, int64_t n);
+/* index of the element the max_of fold returns (first occurrence; extension). */
+int64_t or_argmax_f32(const float* v, int64_t n);
+/* exact u64 sum of u32 counts. */
+uint64_t or_sum_u32_u64(const uint32_t* v, int64_t n);
+
+/* ---- escape_count (examples/mandelbrot.cleave:14-26 over
+ *      stdlib/complex/complex.cleave:24-32, :54), f32 ---- */
+/* z = 0; for n in 0..max_iter: z = z*z + c; first n with |z|^2 > 4, else max_iter.
+ * Early exit after the first escape (the reference latches and keeps
+ * iterating; the result is identical). */
+uint32_t or_escape_count_f32(float cr, float ci, int32_t max_iter);
+/* Literal latch form (no early exit) for small-grid equivalence checks. */
+uint32_t or_escape_count_latch_f32(float cr, float ci, int32_t max_iter);
+/* Grid: c = (x0 + col*dx, y0 + row*dy), rows [row0,row1), out row-major width wide. */
+void or_mandelbrot_rows(uint32_t* out, int32_t width, int32_t height, float x0, float y0,
+                        float dx, float dy, int32_t max_iter, int32_t row0, int32_t row1);
+void or_mandelbrot_mt(uint32_t* out, int32_t width, int32_t height, float x0, float y0,
+                      float dx, float dy, int32_t max_iter, int32_t threads);
+
+/* ---- 2-layer MLP step (style of examples/xor_tensor.cleave:38-92) ----
+ * H = sigmoid(X W1); yhat = sigmoid(H W2); L = mean((yhat - y)^2);
+ * backward by the reference's derivative rules; SGD W -= lr dW.
+ * Row-major X [B x D], W1 [D x Hd], W2 [Hd], y [B].
+ * Outputs loss, dW1 [D x Hd], dW2 [Hd]; when lr != 0, W1/W2 are updated in place.
+ * Scratch: H [B x Hd] and delta [B] are allocated internally. */
+float or_mlp_step_f32(const float* X, const float* y, float* W1, float* W2, int32_t B,
+                      int32_t D, int32_t Hd, float lr, float* dW1, float* dW2,
+                      int32_t threads);
+/* Loss only, in double (for finite-difference gradient checks). */
+double or_mlp_loss_f64(const float* X, const float* y, const float* W1, const float* W2,
+                       int32_t B, int32_t D, int32_t Hd);
+
+/* ---- examples/xor_tensor.cleave:38-92 restated: 2-2-1 sigmoid network with
+ * biases, per-example loss (pred - y)^2, SGD over the 4 XOR rows in order
+ * (i = step mod 4), init examples/xor_tensor.cleave:69-74.  Gradients by the
+ * reverse-mode form of the same derivative rules.  Writes the 4 trained
+ * predictions (forward of rows 00, 01, 10, 11).  Pinned: doc/backlog.md:142. */
+void or_xor_tensor_train(int32_t steps, float lr, float* preds4);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CLEAVE_ORACLE_H */

@@ -1,0 +1,271 @@
+"""ctypes wrapper of liboracle.so -- the CPU restatement (TEST INFRASTRUCTURE).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this module.  It is the checker: the product (cleave_amd / libcleave_hip.so)
+never imports or calls it.  Function-level citations of the reference live in
+oracle/oracle.c.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+_f = C.c_float
+_i32 = C.c_int32
+_i64 = C.c_int64
+_u64 = C.c_uint64
+_p = C.c_void_p
+
+_SIGS = {
+    "or_splitmix64_at": (_u64, [_u64, _u64]),
+    "or_fill_uniform_f32": (None, [_p, _i64, _u64, _f, _f]),
+    "or_fill_normal_f32": (None, [_p, _i64, _u64, _f, _f]),
+    "or_f32_to_bf16": (C.c_uint16, [_f]),
+    "or_bf16_to_f32": (_f, [C.c_uint16]),
+    "or_f32_to_bf16_array": (None, [_p, _p, _i64]),
+    "or_matmul_f32_rows": (None, [_p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "or_matmul_f32": (None, [_p, _p, _p, _i32, _i32, _i32, _i32, _i32]),
+    "or_matmul_f32_mt": (None, [_p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "or_matmul_f32_entries": (None, [_p, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _i64, _p, _p]),
+    "or_matmul_bf16_entries": (None, [_p, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _i64, _p, _p]),
+    "or_matmul_bf16_rows": (None, [_p, _p, _p, _i32, _i32, _i32, _i32, _i32]),
+    "or_add_f32": (None, [_p, _p, _p, _i64]),
+    "or_sub_f32": (None, [_p, _p, _p, _i64]),
+    "or_mul_f32": (None, [_p, _p, _p, _i64]),
+    "or_div_f32": (None, [_p, _p, _p, _i64]),
+    "or_neg_f32": (None, [_p, _p, _i64]),
+    "or_relu_f32": (None, [_p, _p, _i64]),
+    "or_sigmoid_f32": (None, [_p, _p, _i64]),
+    "or_tanh_f32": (None, [_p, _p, _i64]),
+    "or_sigmoid_scalar": (_f, [_f]),
+    "or_sigmoid_bwd_f32": (None, [_p, _p, _p, _i64]),
+    "or_tanh_bwd_f32": (None, [_p, _p, _p, _i64]),
+    "or_relu_bwd_f32": (None, [_p, _p, _p, _i64]),
+    "or_div_bwd_f32": (None, [_p, _p, _p, _p, _p, _i64]),
+    "or_sum_f32": (_f, [_p, _i64]),
+    "or_mean_f32": (_f, [_p, _i64]),
+    "or_max_of_f32": (_f, [_p, _i64]),
+    "or_argmax_f32": (_i64, [_p, _i64]),
+    "or_sum_u32_u64": (_u64, [_p, _i64]),
+    "or_escape_count_f32": (C.c_uint32, [_f, _f, _i32]),
+    "or_escape_count_latch_f32": (C.c_uint32, [_f, _f, _i32]),
+    "or_mandelbrot_rows": (None, [_p, _i32, _i32, _f, _f, _f, _f, _i32, _i32, _i32]),
+    "or_mandelbrot_mt": (None, [_p, _i32, _i32, _f, _f, _f, _f, _i32, _i32]),
+    "or_mlp_step_f32": (_f, [_p, _p, _p, _p, _i32, _i32, _i32, _f, _p, _p, _i32]),
+    "or_mlp_loss_f64": (C.c_double, [_p, _p, _p, _p, _i32, _i32, _i32]),
+    "or_xor_tensor_train": (None, [_i32, _f, _p]),
+}
+
+_lib = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---- generators --------------------------------------------------------------
+
+def splitmix64_at(seed: int, i: int) -> int:
+    return int(lib().or_splitmix64_at(seed, i))
+
+
+def uniform(n: int, seed: int, lo: float = -1.0, hi: float = 1.0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().or_fill_uniform_f32(_ptr(out), n, seed, lo, hi)
+    return out
+
+
+def normal(n: int, seed: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().or_fill_normal_f32(_ptr(out), n, seed, mean, std)
+    return out
+
+
+def to_bf16(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty(x.shape, np.uint16)
+    lib().or_f32_to_bf16_array(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+# ---- matmul -------------------------------------------------------------------
+
+def matmul(A, B, trans_a=False, trans_b=False, threads: int = 0) -> np.ndarray:
+    A, B = _f32(A), _f32(B)
+    M, K = (A.shape[1], A.shape[0]) if trans_a else A.shape
+    N = B.shape[0] if trans_b else B.shape[1]
+    C_ = np.empty((M, N), np.float32)
+    if threads > 0:
+        lib().or_matmul_f32_mt(_ptr(A), _ptr(B), _ptr(C_), M, N, K, int(trans_a), int(trans_b), threads)
+    else:
+        lib().or_matmul_f32(_ptr(A), _ptr(B), _ptr(C_), M, N, K, int(trans_a), int(trans_b))
+    return C_
+
+
+def matmul_rows(A, B, M, N, K, row0, row1, trans_a=False, trans_b=False) -> np.ndarray:
+    """Rows [row0,row1) of C; the rest of the returned buffer is unspecified."""
+    A, B = _f32(A), _f32(B)
+    C_ = np.empty((M, N), np.float32)
+    lib().or_matmul_f32_rows(_ptr(A), _ptr(B), _ptr(C_), M, N, K, int(trans_a), int(trans_b), row0, row1)
+    return C_[row0:row1]
+
+
+def matmul_entries(A, B, M, N, K, ii, jj, trans_a=False, trans_b=False, bf16=False):
+    """C[ii[e], jj[e]] and sum_k |a||b| for each entry."""
+    ii = np.ascontiguousarray(ii, np.int32)
+    jj = np.ascontiguousarray(jj, np.int32)
+    out = np.empty(ii.size, np.float32)
+    absout = np.empty(ii.size, np.float32)
+    if bf16:
+        A = np.ascontiguousarray(A, np.uint16)
+        B = np.ascontiguousarray(B, np.uint16)
+        fn = lib().or_matmul_bf16_entries
+    else:
+        A, B = _f32(A), _f32(B)
+        fn = lib().or_matmul_f32_entries
+    fn(_ptr(A), _ptr(B), M, N, K, int(trans_a), int(trans_b), _ptr(ii), _ptr(jj), ii.size,
+       _ptr(out), _ptr(absout))
+    return out, absout
+
+
+# ---- maps -----------------------------------------------------------------------
+
+def _map1(name, a):
+    a = _f32(a)
+    out = np.empty_like(a)
+    getattr(lib(), name)(_ptr(a), _ptr(out), a.size)
+    return out
+
+
+def _map2(name, a, b):
+    a, b = _f32(a), _f32(b)
+    out = np.empty_like(a)
+    getattr(lib(), name)(_ptr(a), _ptr(b), _ptr(out), a.size)
+    return out
+
+
+def add(a, b): return _map2("or_add_f32", a, b)
+def sub(a, b): return _map2("or_sub_f32", a, b)
+def mul(a, b): return _map2("or_mul_f32", a, b)
+def div(a, b): return _map2("or_div_f32", a, b)
+def neg(a): return _map1("or_neg_f32", a)
+def relu(a): return _map1("or_relu_f32", a)
+def sigmoid(a): return _map1("or_sigmoid_f32", a)
+def tanh(a): return _map1("or_tanh_f32", a)
+def sigmoid_bwd(s, g): return _map2("or_sigmoid_bwd_f32", s, g)
+def tanh_bwd(t, g): return _map2("or_tanh_bwd_f32", t, g)
+def relu_bwd(x, g): return _map2("or_relu_bwd_f32", x, g)
+
+
+def div_bwd(a, b, g):
+    a, b, g = _f32(a), _f32(b), _f32(g)
+    da, db = np.empty_like(a), np.empty_like(a)
+    lib().or_div_bwd_f32(_ptr(a), _ptr(b), _ptr(g), _ptr(da), _ptr(db), a.size)
+    return da, db
+
+
+# ---- reductions ---------------------------------------------------------------------
+
+def sum_f32(v) -> float:
+    v = _f32(v)
+    return float(lib().or_sum_f32(_ptr(v), v.size))
+
+
+def mean_f32(v) -> float:
+    v = _f32(v)
+    return float(lib().or_mean_f32(_ptr(v), v.size))
+
+
+def max_of(v) -> float:
+    v = _f32(v)
+    return float(lib().or_max_of_f32(_ptr(v), v.size))
+
+
+def argmax(v) -> int:
+    v = _f32(v)
+    return int(lib().or_argmax_f32(_ptr(v), v.size))
+
+
+def sum_u64(v) -> int:
+    v = np.ascontiguousarray(v, np.uint32)
+    return int(lib().or_sum_u32_u64(_ptr(v), v.size))
+
+
+# ---- escape counts ---------------------------------------------------------------
+
+def escape_count(cr: float, ci: float, max_iter: int, latch: bool = False) -> int:
+    fn = lib().or_escape_count_latch_f32 if latch else lib().or_escape_count_f32
+    return int(fn(cr, ci, max_iter))
+
+
+def mandelbrot(width, height, x0, y0, dx, dy, max_iter, threads: int = 0, rows=None):
+    out = np.zeros((height, width), np.uint32)
+    if rows is not None:
+        lib().or_mandelbrot_rows(_ptr(out), width, height, x0, y0, dx, dy, max_iter, rows[0], rows[1])
+    elif threads > 0:
+        lib().or_mandelbrot_mt(_ptr(out), width, height, x0, y0, dx, dy, max_iter, threads)
+    else:
+        lib().or_mandelbrot_rows(_ptr(out), width, height, x0, y0, dx, dy, max_iter, 0, height)
+    return out
+
+
+# ---- MLP ---------------------------------------------------------------------------
+
+def mlp_step(X, y, W1, W2, lr: float, threads: int = 1):
+    """Returns (loss, dW1, dW2, W1_new, W2_new); inputs are not modified."""
+    X, y = _f32(X), _f32(y)
+    W1n, W2n = _f32(W1).copy(), _f32(W2).copy()
+    B, D = X.shape
+    Hd = W1n.shape[1]
+    dW1 = np.empty((D, Hd), np.float32)
+    dW2 = np.empty(Hd, np.float32)
+    loss = lib().or_mlp_step_f32(_ptr(X), _ptr(y), _ptr(W1n), _ptr(W2n), B, D, Hd, lr, _ptr(dW1),
+                                 _ptr(dW2), threads)
+    return float(loss), dW1, dW2, W1n, W2n
+
+
+def mlp_loss_f64(X, y, W1, W2) -> float:
+    X, y, W1, W2 = _f32(X), _f32(y), _f32(W1), _f32(W2)
+    B, D = X.shape
+    return float(lib().or_mlp_loss_f64(_ptr(X), _ptr(y), _ptr(W1), _ptr(W2), B, D, W1.shape[1]))
+
+
+def xor_tensor_train(steps: int = 4000, lr: float = 1.0) -> np.ndarray:
+    out = np.empty(4, np.float32)
+    lib().or_xor_tensor_train(steps, lr, _ptr(out))
+    return out

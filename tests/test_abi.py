@@ -1,0 +1,136 @@
+"""The drop-in boundary: libcleave_hip.so loads, exports exactly the C ABI of
+include/cleave_hip.h, registers it in its symbol table (the shape of
+register_cleave_rt_symbols, /root/reference/cleave/src/pipeline.rs:159-198),
+and validates arguments on the host before touching a device.  No GPU needed.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import re
+import subprocess
+import sys
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "cleave_hip.h"
+
+
+def header_functions() -> list[str]:
+    text = HEADER.read_text()
+    return list(dict.fromkeys(re.findall(r"^CLEAVE_HIP_API [^(]*?\b(cleave_hip_[a-z0-9_]+)\(", text, re.M)))
+
+
+def test_header_declares_the_expected_surface():
+    names = header_functions()
+    assert len(names) >= 40
+    for must in ["cleave_hip_matmul_f32", "cleave_hip_matmul_bf16", "cleave_hip_matmul_batched_bf16",
+                 "cleave_hip_sigmoid_f32", "cleave_hip_sum_f32", "cleave_hip_mandelbrot_u32",
+                 "cleave_hip_mlp_step_f32", "cleave_hip_symbols", "cleave_hip_buf_alloc"]:
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol_and_nothing_else():
+    from cleave_amd import _lib
+
+    lib = _lib.load()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    assert exported == set(header_functions())
+
+
+def test_symbol_table_matches_header_and_addresses():
+    from cleave_amd import _lib
+
+    lib = _lib.load()
+    table = _lib.symbol_table()
+    assert set(table) == set(header_functions())
+    for name, addr in table.items():
+        assert addr == C.cast(getattr(lib, name), C.c_void_p).value, name
+
+
+def test_python_signatures_cover_the_header():
+    from cleave_amd import _lib
+
+    assert set(_lib.SIGNATURES) == set(header_functions())
+
+
+def _lib_noabort():
+    from cleave_amd import _lib
+
+    lib = _lib.load()
+    lib.cleave_hip_set_abort_on_error(0)
+    return lib, _lib
+
+
+@pytest.mark.parametrize("fn,args,needle", [
+    ("cleave_hip_matmul_f32", (None, 5, None, 4, None, 4, 2, 2, 2, 0, 0), "alen"),
+    ("cleave_hip_matmul_f32", (None, 4, None, 4, None, 4, 2, 2, 2, 2, 0), "trans"),
+    ("cleave_hip_matmul_f32", (None, 0, None, 0, None, 0, 0, 2, 2, 0, 0), "positive"),
+    ("cleave_hip_matmul_bf16", (None, 4, None, 6, None, 4, 2, 2, 2, 0, 0), "blen"),
+    ("cleave_hip_matmul_batched_bf16", (None, 8, None, 8, None, 7, 2, 2, 2, 2), "lengths"),
+    ("cleave_hip_matmul_batched_f32", (None, 8, None, 8, None, 8, 0, 2, 2, 2, 0, 0), "batch"),
+    ("cleave_hip_add_f32", (None, 3, None, 4, None, 3), "broadcast"),
+    ("cleave_hip_sigmoid_f32", (None, 3, None, 2, ), "length"),
+    ("cleave_hip_sgd_update_f32", (None, 3, None, 2, 0.1), "glen"),
+    ("cleave_hip_reduce_sum_f32", (None, 0, None), ">= 1"),
+    ("cleave_hip_reduce_max_f32", (None, 0, None, None), ">= 1"),
+    ("cleave_hip_mandelbrot_u32", (None, 10, 4, 4, -2.0, -1.5, 0.1, 0.1, 10), "outlen"),
+    ("cleave_hip_mandelbrot_u32", (None, 16, 4, 4, -2.0, -1.5, 0.1, 0.1, -1), "max_iter"),
+    ("cleave_hip_mlp_step_f32", (None, 9, None, 2, None, 15, None, 3, None, 0, None, 0, None,
+                                 2, 5, 3, 0.01), "xlen"),
+    ("cleave_hip_cast_f32_bf16", (None, 4, None, 3), "null"),
+])
+def test_argument_validation_happens_before_any_device_work(fn, args, needle):
+    lib, _lib = _lib_noabort()
+    status = getattr(lib, fn)(*args)
+    code, msg = _lib.last_error()
+    assert status == _lib.ERR_ARG and code == _lib.ERR_ARG
+    assert fn in msg and needle in msg, msg
+
+
+def test_zero_length_maps_are_no_ops_without_a_device():
+    lib, _lib = _lib_noabort()
+    assert lib.cleave_hip_add_f32(None, 0, None, 0, None, 0) == 0
+    assert lib.cleave_hip_neg_f32(None, 0, None, 0) == 0
+    assert lib.cleave_hip_zero_f32(None, 0) == 0
+
+
+def test_missing_device_is_a_runtime_error_not_a_fallback():
+    lib, _lib = _lib_noabort()
+    if lib.cleave_hip_device_available():
+        pytest.skip("a device is present; this checks the no-device path")
+    assert lib.cleave_hip_init() == _lib.ERR_RUNTIME
+    assert lib.cleave_hip_matmul_f32(1, 4, 1, 4, 1, 4, 2, 2, 2, 0, 0) == _lib.ERR_RUNTIME
+    assert lib.cleave_hip_buf_alloc(64) is None
+    assert "device" in _lib.last_error()[1]
+
+
+def test_default_error_mode_aborts_like_cleave_rt():
+    # cleave-rt panics on bad input (cleave-rt/src/lib.rs:69, :120); by default
+    # the library prints the message and aborts.
+    code = (
+        "import ctypes, sys; L = ctypes.CDLL(sys.argv[1]);"
+        "L.cleave_hip_add_f32.argtypes = [ctypes.c_void_p, ctypes.c_int64] * 3;"
+        "L.cleave_hip_add_f32(None, 3, None, 4, None, 3)"
+    )
+    from cleave_amd import _lib
+
+    r = subprocess.run([sys.executable, "-c", code, str(_lib.LIB_PATH)], capture_output=True, text=True)
+    assert r.returncode != 0
+    assert "cleave_hip: error -2: cleave_hip_add_f32" in r.stderr
+
+
+def test_product_package_does_not_reach_the_oracle():
+    # The product path must never import, link or load the checker.
+    for path in (ROOT / "cleave_amd").rglob("*"):
+        if path.suffix in {".py", ".hip", ".cpp", ".hpp", ".h"}:
+            text = path.read_text()
+            assert "liboracle" not in text and "from oracle" not in text and "import oracle" not in text, path
+    out = subprocess.run(["ldd", str(ROOT / "cleave_amd" / "libcleave_hip.so")], capture_output=True,
+                         text=True).stdout
+    assert "oracle" not in out

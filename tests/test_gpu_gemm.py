@@ -1,0 +1,175 @@
+"""GEMM parity on the GPU, through the C ABI (cleave_hip_matmul_*).
+
+Oracle: oracle/oracle.c's restated linalg.matmul loop (C = 0; C[i,j] += A[i,k]*B[k,j]).
+Full-matrix comparison where the oracle finishes in seconds; at the BASELINE
+sizes, sampled entries (each one an exact run of the reference loop) plus a
+size-independent linearity property on every row: C 1 = A (B 1).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import assert_gemm_close, sample_entries
+
+pytestmark = pytest.mark.gpu
+
+
+def _full_check(hip, oracle, A, B, ta, tb, what):
+    a, b = hip.from_numpy(A), hip.from_numpy(B)
+    c = hip.matmul(a, b, trans_a=ta, trans_b=tb)
+    got = c.numpy()
+    ref = oracle.matmul(A, B, trans_a=ta, trans_b=tb, threads=16)
+    Af = np.abs(A.T if ta else A).astype(np.float64)
+    Bf = np.abs(B.T if tb else B).astype(np.float64)
+    K = Af.shape[1]
+    return assert_gemm_close(got, ref, Af @ Bf, K, what)
+
+
+def test_golden_vectors_exact(hip, golden):
+    for case in golden["matmul"]:
+        A = np.array(case["a"], np.float32)
+        B = np.array(case["b"], np.float32)
+        got = hip.matmul(hip.from_numpy(A), hip.from_numpy(B)).numpy()
+        assert np.array_equal(got, np.array(case["c"], np.float32)), case["source"]
+
+
+def test_matmul_against_ring_zero_is_exactly_zero(hip):
+    # cleave/tests/mlir_lower.rs:2846-2858: the accumulator starts from a real zero.
+    rng = np.random.default_rng(0)
+    A = rng.standard_normal((256, 256)).astype(np.float32)
+    c = hip.from_numpy(np.full((256, 256), np.nan, np.float32))  # garbage in the output buffer
+    z = hip.zero((256, 256))
+    hip.matmul(hip.from_numpy(A), z, out=c)
+    assert np.array_equal(c.numpy(), np.zeros((256, 256), np.float32))
+
+
+def test_config1_256_cube_uniform_seed0(hip, oracle):
+    n = 256
+    a = hip.fill_uniform(hip.empty((n, n)), seed=0)
+    b = hip.fill_uniform(hip.empty((n, n)), seed=1)
+    A, B = a.numpy(), b.numpy()
+    # the device generator is the oracle's generator, bit for bit
+    assert np.array_equal(A.ravel(), oracle.uniform(n * n, seed=0))
+    got = hip.matmul(a, b).numpy()
+    ref = oracle.matmul(A, B, threads=16)
+    assert_gemm_close(got, ref, np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64), n, "256^3")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (2, 3, 2), (127, 129, 33), (300, 200, 17),
+                                   (130, 257, 1000), (128, 128, 16), (256, 384, 48)])
+def test_shapes_and_layouts(hip, oracle, M, N, K, ta, tb):
+    rng = np.random.default_rng(M * 7 + N * 3 + K)
+    A = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    _full_check(hip, oracle, A, B, bool(ta), bool(tb), f"{M}x{N}x{K} ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+def test_config2_4096_cube_sampled_and_linearity(hip, oracle, ta, tb):
+    n = 4096
+    a = hip.fill_normal(hip.empty((n, n)), seed=11)
+    b = hip.fill_normal(hip.empty((n, n)), seed=12)
+    c = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb))
+    A, B, C = a.numpy(), b.numpy(), c.numpy()
+    ii, jj = sample_entries(n, n, 512, seed=ta * 2 + tb)
+    ref, absden = oracle.matmul_entries(A, B, n, n, n, ii, jj, trans_a=bool(ta), trans_b=bool(tb))
+    assert_gemm_close(C[ii, jj], ref, absden, n, f"4096^3 ta={ta} tb={tb}")
+    # every row: C 1 = A (B 1), in float64, within the same normalised bound
+    Ad = (A.T if ta else A).astype(np.float64)
+    Bd = (B.T if tb else B).astype(np.float64)
+    rows = Ad @ Bd.sum(axis=1)
+    den = np.abs(Ad) @ np.abs(Bd).sum(axis=1)
+    assert np.max(np.abs(C.astype(np.float64).sum(axis=1) - rows) / den) <= 1e-5 * np.sqrt(n)
+
+
+def test_deterministic(hip):
+    n = 1024
+    a = hip.fill_normal(hip.empty((n, n)), seed=3)
+    b = hip.fill_normal(hip.empty((n, n)), seed=4)
+    c1 = hip.matmul(a, b).numpy()
+    c2 = hip.matmul(a, b).numpy()
+    assert np.array_equal(c1, c2)
+
+
+def test_batched_f32(hip, oracle):
+    rng = np.random.default_rng(5)
+    bsz, M, N, K = 5, 96, 130, 70
+    A = rng.standard_normal((bsz, M, K)).astype(np.float32)
+    B = rng.standard_normal((bsz, K, N)).astype(np.float32)
+    got = hip.matmul_batched(hip.from_numpy(A), hip.from_numpy(B)).numpy()
+    for i in range(bsz):
+        ref = oracle.matmul(A[i], B[i])
+        assert_gemm_close(got[i], ref, np.abs(A[i]).astype(np.float64) @ np.abs(B[i]).astype(np.float64), K,
+                          f"batch {i}")
+
+
+# ---- bf16 in, f32 accumulate -------------------------------------------------------
+
+def test_bf16_golden_vectors_exact(hip, golden, oracle):
+    for case in golden["matmul"]:
+        A = oracle.to_bf16(np.array(case["a"], np.float32))
+        B = oracle.to_bf16(np.array(case["b"], np.float32))
+        got = hip.matmul(hip.from_numpy(A, "bf16"), hip.from_numpy(B, "bf16")).numpy()
+        assert np.array_equal(got, np.array(case["c"], np.float32)), case["source"]
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (3, 5, 7), (129, 131, 40), (256, 128, 64), (200, 300, 100)])
+def test_bf16_shapes_and_layouts(hip, oracle, M, N, K, ta, tb):
+    rng = np.random.default_rng(M + N + K)
+    A32 = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B32 = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    A, B = oracle.to_bf16(A32), oracle.to_bf16(B32)
+    got = hip.matmul(hip.from_numpy(A, "bf16"), hip.from_numpy(B, "bf16"), trans_a=bool(ta),
+                     trans_b=bool(tb)).numpy()
+    Au = oracle.bf16_to_f32(A).reshape(A.shape)
+    Bu = oracle.bf16_to_f32(B).reshape(B.shape)
+    ref = oracle.matmul(Au, Bu, trans_a=bool(ta), trans_b=bool(tb))
+    Ad = np.abs(Au.T if ta else Au).astype(np.float64)
+    Bd = np.abs(Bu.T if tb else Bu).astype(np.float64)
+    assert_gemm_close(got, ref, Ad @ Bd, K, f"bf16 {M}x{N}x{K}")
+
+
+def test_config5_bf16_8192_cube(hip, oracle):
+    n = 8192
+    a32 = hip.fill_normal(hip.empty((n, n)), seed=21, std=0.02)
+    b32 = hip.fill_normal(hip.empty((n, n)), seed=22, std=0.02)
+    a, b = hip.to_bf16(a32), hip.to_bf16(b32)
+    # the device cast is RNE, bit for bit with the oracle's
+    A32 = a32.numpy()
+    A = a.numpy()
+    assert np.array_equal(A[:64], oracle.to_bf16(A32[:64]))
+    del a32, b32
+    c = hip.matmul(a, b)
+    B = b.numpy()
+    C = c.numpy()
+    ii, jj = sample_entries(n, n, 384, seed=5)
+    ref, absden = oracle.matmul_entries(A, B, n, n, n, ii, jj, bf16=True)
+    assert_gemm_close(C[ii, jj], ref, absden, n, "bf16 8192^3")
+    # the stated bf16 tolerance: rel <= 1e-2 against the f32 loop on upcast values
+    assert np.all(np.abs(C[ii, jj] - ref) <= 1e-2 * np.abs(ref) + 1e-2 * absden / np.sqrt(n))
+    Ad = oracle.bf16_to_f32(A).reshape(n, n).astype(np.float64)
+    Bd = oracle.bf16_to_f32(B).reshape(n, n).astype(np.float64)
+    rows = Ad @ Bd.sum(axis=1)
+    den = np.abs(Ad) @ np.abs(Bd).sum(axis=1)
+    assert np.max(np.abs(C.astype(np.float64).sum(axis=1) - rows) / den) <= 1e-5 * np.sqrt(n)
+
+
+def test_config5_batched_bf16_64x512(hip, oracle):
+    bsz, n = 64, 512
+    a32 = hip.fill_normal(hip.empty((bsz, n, n)), seed=31, std=0.02)
+    b32 = hip.fill_normal(hip.empty((bsz, n, n)), seed=32, std=0.02)
+    a, b = hip.to_bf16(a32), hip.to_bf16(b32)
+    c = hip.matmul_batched(a, b)
+    A, B, C = a.numpy(), b.numpy(), c.numpy()
+    for i in [0, 1, 17, 63]:
+        ii, jj = sample_entries(n, n, 128, seed=i)
+        ref, absden = oracle.matmul_entries(A[i], B[i], n, n, n, ii, jj, bf16=True)
+        assert_gemm_close(C[i][ii, jj], ref, absden, n, f"batched bf16 #{i}")
+    # full check of one batch entry
+    Au = oracle.bf16_to_f32(A[5]).reshape(n, n)
+    Bu = oracle.bf16_to_f32(B[5]).reshape(n, n)
+    ref = oracle.matmul(Au, Bu, threads=16)
+    assert_gemm_close(C[5], ref, np.abs(Au).astype(np.float64) @ np.abs(Bu).astype(np.float64), n, "batch 5 full")
