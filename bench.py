@@ -103,6 +103,22 @@ def cpu_baseline_gemm(A, B, n, budget_s):
     }
 
 
+COPY_ELEMS = 1 << 26  # 256 MiB of f32 read, 256 MiB written per launch
+
+
+def calibrate_copy(ca, steps):
+    """A plain streaming copy of known size (neg map: 4 bytes read and 4 bytes
+    written per element).  Its FETCH_SIZE / WRITE_SIZE per dispatch, divided by
+    the 268435456 bytes it must move each way, is the scale factor applied to
+    the same counters read for the GEMM."""
+    x = ca.fill_normal(ca.empty(COPY_ELEMS), seed=7)
+    y = ca.empty(COPY_ELEMS)
+    wall, ev = timed(ca, lambda: ca.neg(x, out=y), steps, 1)
+    gbs = 2 * 4 * COPY_ELEMS / (ev * 1e-3) / 1e9
+    print(json.dumps({"calibration": "copy", "bytes_each_way": 4 * COPY_ELEMS,
+                      "kernel_ms": round(ev, 4), "GB/s": round(gbs, 1)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -111,6 +127,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run the copy kernel used to scale rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); multi-GPU runs are "
@@ -126,6 +144,9 @@ def main():
         sys.exit(1)
     ca.init()
     steps, warmup = args.steps, args.warmup
+    if args.calibrate_copy:
+        calibrate_copy(ca, steps)
+        return
 
     # ---- headline: f32 4096^3 NN --------------------------------------------
     n = 4096

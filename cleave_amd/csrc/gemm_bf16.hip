@@ -18,6 +18,8 @@ namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+// Native clang vector (HIP's uint4 struct defeats register promotion).
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128, BN = 128, BK = 32, NT = 256;
 constexpr int PITCH = BK + 8;  // elements
@@ -27,7 +29,7 @@ template <bool KCONTIG>
 struct Stage;
 template <>
 struct Stage<true> {  // 128 rows x 32 k = 512 chunks of 8 -> 2 per thread
-    uint4 v[2];
+    u4 v[2];
 };
 template <>
 struct Stage<false> {  // 64 row-pairs x 4 k-groups of 8 -> 1 block per thread
@@ -47,14 +49,14 @@ __device__ __forceinline__ void load_tile(Stage<KCONTIG>& s, const uint16_t* __r
             int r = idx >> 2, kc = (idx & 3) * 8;
             int gr = r0 + r, gk = k0 + kc;
             if (!EDGE) {
-                s.v[q] = *reinterpret_cast<const uint4*>(X + (int64_t)gr * ld + gk);
+                s.v[q] = *reinterpret_cast<const u4*>(X + (int64_t)gr * ld + gk);
             } else {
                 uint16_t e[8];
 #pragma unroll
                 for (int t = 0; t < 8; ++t)
                     e[t] = (gr < rows && gk + t < ks) ? X[(int64_t)gr * ld + gk + t] : (uint16_t)0;
-                s.v[q] = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16),
-                                    e[6] | (e[7] << 16));
+                s.v[q] = u4{e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16),
+                           e[4] | ((uint32_t)e[5] << 16), e[6] | ((uint32_t)e[7] << 16)};
             }
         }
     } else {
@@ -81,11 +83,11 @@ __device__ __forceinline__ void store_tile(const Stage<KCONTIG>& s, uint16_t (*L
         for (int q = 0; q < 2; ++q) {
             int idx = tid + NT * q;
             int r = idx >> 2, kc = (idx & 3) * 8;
-            *reinterpret_cast<uint4*>(&L[r][kc]) = s.v[q];
+            *reinterpret_cast<u4*>(&L[r][kc]) = s.v[q];
         }
     } else {
         int rp = (tid & 63) * 2, kg = (tid >> 6) * 8;
-        uint4 lo, hi;  // rows rp and rp+1, k = kg..kg+7
+        u4 lo, hi;  // rows rp and rp+1, k = kg..kg+7
         lo.x = (s.w[0] & 0xFFFFu) | (s.w[1] << 16);
         lo.y = (s.w[2] & 0xFFFFu) | (s.w[3] << 16);
         lo.z = (s.w[4] & 0xFFFFu) | (s.w[5] << 16);
@@ -94,8 +96,8 @@ __device__ __forceinline__ void store_tile(const Stage<KCONTIG>& s, uint16_t (*L
         hi.y = (s.w[2] >> 16) | (s.w[3] & 0xFFFF0000u);
         hi.z = (s.w[4] >> 16) | (s.w[5] & 0xFFFF0000u);
         hi.w = (s.w[6] >> 16) | (s.w[7] & 0xFFFF0000u);
-        *reinterpret_cast<uint4*>(&L[rp][kg]) = lo;
-        *reinterpret_cast<uint4*>(&L[rp + 1][kg]) = hi;
+        *reinterpret_cast<u4*>(&L[rp][kg]) = lo;
+        *reinterpret_cast<u4*>(&L[rp + 1][kg]) = hi;
     }
 }
 

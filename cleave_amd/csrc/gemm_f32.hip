@@ -27,6 +27,9 @@
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+// Native clang vectors: HIP's float4 struct defeats register promotion of the
+// staging arrays (they land in scratch memory).
+typedef float f4 __attribute__((ext_vector_type(4)));
 
 template <int BM, int BN, int BK, bool TA, bool TB, bool EDGE>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ A,
@@ -59,7 +62,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
     constexpr int A_VEC = BM * BK / 4 / NT;  // float4 per thread
     constexpr int B_VEC = BN * BK / 4 / NT;
     static_assert(A_VEC * NT * 4 == BM * BK && B_VEC * NT * 4 == BN * BK, "tile/threads");
-    float4 ra[A_VEC], rb[B_VEC];
+    f4 ra[A_VEC], rb[B_VEC];
 
     auto load_a = [&](int k0) {
 #pragma unroll
@@ -71,7 +74,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
             int gm = m0 + r, gk = k0 + c;
             if (!EDGE) {
                 const float* p = !TA ? A + (int64_t)gm * lda + gk : A + (int64_t)gk * lda + gm;
-                ra[q] = *reinterpret_cast<const float4*>(p);
+                ra[q] = *reinterpret_cast<const f4*>(p);
             } else {
                 float v[4];
 #pragma unroll
@@ -79,7 +82,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
                     int mm = !TA ? gm : gm + e, kk = !TA ? gk + e : gk;
                     v[e] = (mm < M && kk < K) ? (!TA ? A[(int64_t)mm * lda + kk] : A[(int64_t)kk * lda + mm]) : 0.0f;
                 }
-                ra[q] = make_float4(v[0], v[1], v[2], v[3]);
+                ra[q] = f4{v[0], v[1], v[2], v[3]};
             }
         }
     };
@@ -93,7 +96,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
             int gk = k0 + r, gn = n0 + c;
             if (!EDGE) {
                 const float* p = !TB ? B + (int64_t)gk * ldb + gn : B + (int64_t)gn * ldb + gk;
-                rb[q] = *reinterpret_cast<const float4*>(p);
+                rb[q] = *reinterpret_cast<const f4*>(p);
             } else {
                 float v[4];
 #pragma unroll
@@ -101,7 +104,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
                     int kk = !TB ? gk : gk + e, nn = !TB ? gn + e : gn;
                     v[e] = (kk < K && nn < N) ? (!TB ? B[(int64_t)kk * ldb + nn] : B[(int64_t)nn * ldb + kk]) : 0.0f;
                 }
-                rb[q] = make_float4(v[0], v[1], v[2], v[3]);
+                rb[q] = f4{v[0], v[1], v[2], v[3]};
             }
         }
     };
@@ -117,7 +120,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
                 As[buf][k + 3][m] = ra[q].w;
             } else {
                 int k = idx / (BM / 4), m = (idx % (BM / 4)) * 4;
-                *reinterpret_cast<float4*>(&As[buf][k][m]) = ra[q];
+                *reinterpret_cast<f4*>(&As[buf][k][m]) = ra[q];
             }
         }
     };
@@ -127,7 +130,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
             int idx = tid + NT * q;
             if (!TB) {
                 int k = idx / (BN / 4), n = (idx % (BN / 4)) * 4;
-                *reinterpret_cast<float4*>(&Bs[buf][k][n]) = rb[q];
+                *reinterpret_cast<f4*>(&Bs[buf][k][n]) = rb[q];
             } else {
                 int n = idx / (BK / 4), k = (idx % (BK / 4)) * 4;
                 Bs[buf][k + 0][n] = rb[q].x;
