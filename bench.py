@@ -39,12 +39,19 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def timed(ca, fn, steps, warmup):
-    """Run fn warmup times, then time `steps` calls: wall clock between two
-    stream syncs, and HIP events on the library stream."""
+def timed(ca, fn, steps, warmup, warm_s=0.0):
+    """Run fn `warmup` times (and further until `warm_s` seconds have passed),
+    then time `steps` calls: wall clock between two stream syncs, and HIP
+    events on the library stream.  MI355X clocks settle only after ~0.1-0.3 s
+    of sustained matrix-core load, so short warm-ups under-report."""
     for _ in range(warmup):
         fn()
     ca.sync()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < warm_s:
+        for _ in range(4):
+            fn()
+        ca.sync()
     t = ca.Timer()
     w0 = time.perf_counter()
     t.start()
@@ -123,7 +130,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -183,10 +190,10 @@ def main():
 
     secondary = {}
     if not args.no_secondary:
-        sec_steps = max(5, steps // 5)
+        sec_steps = max(20, steps // 2)
         # f32 A B^T and A^T B (reverse-mode halves of the product rule)
         for name, ta, tb in [("gemm_f32_nt_4096", False, True), ("gemm_f32_tn_4096", True, False)]:
-            wall_s, ev = timed(ca, lambda: ca.matmul(a, b, trans_a=ta, trans_b=tb, out=c), sec_steps, 2)
+            wall_s, ev = timed(ca, lambda: ca.matmul(a, b, trans_a=ta, trans_b=tb, out=c), sec_steps, 2, 0.3)
             ach = flop / (ev * 1e-3) / 1e12
             secondary[name] = {"GFLOP/s": round(flop * sec_steps / wall_s / 1e9, 1),
                                "kernel_ms": round(ev, 4), "frac_fp32_mfma": round(ach / PEAK_FP32_MFMA, 4)}
@@ -201,7 +208,7 @@ def main():
         del a32
         cb = ca.empty((m, m))
         fl = 2.0 * m ** 3
-        wall_s, ev = timed(ca, lambda: ca.matmul(ab, bb, out=cb), sec_steps, 2)
+        wall_s, ev = timed(ca, lambda: ca.matmul(ab, bb, out=cb), sec_steps, 2, 0.4)
         ach = fl / (ev * 1e-3) / 1e12
         secondary["gemm_bf16_8192"] = {"GFLOP/s": round(fl * sec_steps / wall_s / 1e9, 1), "kernel_ms": round(ev, 4),
                                        "frac_bf16_mfma": round(ach / PEAK_BF16_MFMA, 4)}
@@ -216,7 +223,7 @@ def main():
         del t32
         zb = ca.empty((bs, k, k))
         fl = 2.0 * bs * k ** 3
-        wall_s, ev = timed(ca, lambda: ca.matmul_batched(xb, yb, out=zb), sec_steps * 4, 2)
+        wall_s, ev = timed(ca, lambda: ca.matmul_batched(xb, yb, out=zb), sec_steps * 4, 2, 0.3)
         ach = fl / (ev * 1e-3) / 1e12
         secondary["gemm_bf16_batched_64x512"] = {"GFLOP/s": round(fl * sec_steps * 4 / wall_s / 1e9, 1),
                                                  "kernel_ms": round(ev, 4),
@@ -233,7 +240,7 @@ def main():
         w2 = ca.fill_uniform(ca.empty(H_), seed=404, lo=-lim2, hi=lim2)
         loss = ca.empty(1)
         mlp_steps = max(5, steps // 5)
-        wall_s, ev = timed(ca, lambda: ca.mlp_step(x, yv, w1, w2, 0.01, loss=loss), mlp_steps, 2)
+        wall_s, ev = timed(ca, lambda: ca.mlp_step(x, yv, w1, w2, 0.01, loss=loss), mlp_steps, 2, 0.3)
         gemm_fl = 2.0 * B_ * D_ * H_ * 2 + 4.0 * B_ * H_
         secondary["mlp_step_65536x1024x4096"] = {
             "steps_per_s": round(mlp_steps / wall_s, 3), "ms_per_step": round(ev, 3),

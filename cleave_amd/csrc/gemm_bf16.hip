@@ -1,17 +1,23 @@
 // gemm_bf16.hip -- bf16-input / fp32-accumulate matmul on CDNA4 matrix cores
 // (v_mfma_f32_32x32x16_bf16), plus its batched form.
 //
+// Shapes that divide a 256 x 256 x 64 (or 128 x 128 x 64) tile run the
+// large-tile kernel of gemm_bf16_tiled.hpp (LDS filled by global_load_lds,
+// transposing LDS reads for m/n-contiguous operands).  Everything else runs
+// the general kernel below, which guards every access.
+//
 // Same operator as gemm_f32.hip (linalg.matmul of stdlib/linalg/matrix.cleave:
 // 27-61) with bf16 operands; the reference is f32/f64 only, so this is an
 // extension checked against the f32 loop run on the upcast values.
 //
-// LDS layout: both operands are staged [row][k] with k contiguous and a row
+// General kernel.  LDS layout: both operands are staged [row][k] with k contiguous and a row
 // pitch of BK+8 elements (80 bytes), so the 16-byte MFMA operand reads of 16
 // consecutive lanes land in 16 distinct bank quads.  An operand that is
 // k-contiguous in global memory is copied in 16-byte chunks; one that is
 // contiguous along m/n is read as 8(k) x 2(m/n) blocks of 4-byte words and
 // transposed in registers before a pair of 16-byte LDS stores.
 #include "common.hpp"
+#include "gemm_bf16_tiled.hpp"
 #include "gemm_common.hpp"
 
 namespace {
@@ -197,12 +203,37 @@ int32_t launch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int
     return CLEAVE_HIP_OK;
 }
 
+// Large-tile kernel (gemm_bf16_tiled.hpp) for shapes that divide its tile.
+// Returns false when the shape or alignment does not fit.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool TA, bool TB>
+bool launch_tiled(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
+                  int32_t* status) {
+    using P = ch::Bf16Tiled<BM, BN, BK, WM, WN, STAGES, !TA, TB>;
+    if (!P::fits(M, N, K) || ((uintptr_t)a & 15) || ((uintptr_t)b & 15)) return false;
+    const int tiles_m = M / BM, tiles_n = N / BN;
+    dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)batch);
+    ch::gemm_bf16_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
+        a, b, c, M, N, K, (int64_t)M * K, (int64_t)K * N, (int64_t)M * N, tiles_m, tiles_n);
+    *status = ch::check_hip(hipGetLastError(), "gemm_bf16_tiled_kernel");
+    return true;
+}
+
+template <bool TA, bool TB>
+int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch) {
+    int32_t st = CLEAVE_HIP_OK;
+    // 256 x 256 x 64 tile, 8 waves of 128 x 64, two LDS stages (128 KiB)
+    if (launch_tiled<256, 256, 64, 2, 4, 2, TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
+    // 128 x 128 x 64 tile, 4 waves of 64 x 64, three LDS stages (96 KiB)
+    if (launch_tiled<128, 128, 64, 2, 2, 3, TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
+    return launch<TA, TB>(a, b, c, M, N, K, batch);
+}
+
 int32_t dispatch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
                  int ta, int tb) {
-    if (!ta && !tb) return launch<false, false>(a, b, c, M, N, K, batch);
-    if (!ta && tb) return launch<false, true>(a, b, c, M, N, K, batch);
-    if (ta && !tb) return launch<true, false>(a, b, c, M, N, K, batch);
-    return launch<true, true>(a, b, c, M, N, K, batch);
+    if (!ta && !tb) return launch_any<false, false>(a, b, c, M, N, K, batch);
+    if (!ta && tb) return launch_any<false, true>(a, b, c, M, N, K, batch);
+    if (ta && !tb) return launch_any<true, false>(a, b, c, M, N, K, batch);
+    return launch_any<true, true>(a, b, c, M, N, K, batch);
 }
 
 }  // namespace

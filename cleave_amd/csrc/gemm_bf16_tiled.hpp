@@ -1,0 +1,175 @@
+// gemm_bf16_tiled.hpp -- the large-tile bf16-in / f32-accumulate GEMM kernel
+// for gfx950 (shapes that divide the block tile).
+//
+// One workgroup computes a BM x BN block of C with WM x WN waves; each wave
+// owns a (BM/WM) x (BN/WN) block of 32 x 32 accumulators (v16f per MFMA tile).
+// K is walked in BK-deep tiles through a STAGES-deep ring of LDS buffers that
+// are filled by global_load_lds (see gemm_tiles.hpp for the layouts):
+//
+//   prologue: issue tiles 0 .. STAGES-2, wait for tile 0, s_barrier,
+//             issue tile STAGES-1, read the fragments of k-step 0
+//   for kt, for each of the BK/16 k-steps:
+//             read the next k-step's fragments (double-buffered registers)
+//             FM x FN MFMAs on this k-step's fragments
+//   where the last k-step of tile kt first waits for tile kt+1's copies and
+//   for its own LDS reads, passes an s_barrier, issues tile kt+STAGES into
+//   tile kt's buffer and reads tile kt+1's first fragments -- so the
+//   fragment pipeline never drains at a tile boundary.
+//
+// The waits are s_waitcnt vmcnt(copies issued after the awaited tile) and the
+// barrier is a bare s_barrier, so copies of later tiles stay in flight across
+// it.  Both are inline asm with a memory clobber, which keeps the compiler
+// from moving LDS reads across them.
+#pragma once
+
+#include "gemm_common.hpp"
+#include "gemm_tiles.hpp"
+
+namespace ch {
+
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC>
+struct Bf16Tiled {
+    static constexpr int NW = WM * WN, THREADS = 64 * NW;
+    static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+    static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
+    static constexpr int STAGE_BYTES = A_BYTES + B_BYTES, LDS_BYTES = STAGES * STAGE_BYTES;
+    // global_load_lds instructions per wave per k-tile
+    static constexpr int LPW = STAGE_BYTES / 1024 / NW;
+    static_assert(TM % 32 == 0 && TN % 32 == 0 && BK % 16 == 0, "tile shape");
+    static_assert(STAGES >= 2 && LPW * (STAGES - 2) < 64, "pipeline depth");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS per workgroup");
+
+    // Shapes this kernel takes without bounds checks.  The copies address an
+    // operand with 32-bit byte offsets from a per-k-tile scalar base, so a
+    // k-contiguous operand must stay under 4 GiB (an m/n-contiguous one only
+    // needs its BK-row band to).
+    static bool fits(int M, int N, int K) {
+        const bool dims = M % BM == 0 && N % BN == 0 && K % BK == 0;
+        const uint64_t a_span = AKC ? (uint64_t)M * K * 2 : (uint64_t)BK * M * 2;
+        const uint64_t b_span = BKC ? (uint64_t)N * K * 2 : (uint64_t)BK * N * 2;
+        return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
+    }
+};
+
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, float* __restrict__ C, int M,
+    int N, int K, int64_t strideA, int64_t strideB, int64_t strideC, int tiles_m, int tiles_n) {
+    using namespace ch::tiles;
+    using P = Bf16Tiled<BM, BN, BK, WM, WN, STAGES, AKC, BKC>;
+    constexpr int FM = P::FM, FN = P::FN, NW = P::NW;
+    __shared__ __attribute__((aligned(1024))) char smem[P::LDS_BYTES];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: keeps LDS/DMA bases scalar
+    const int wm = wave / WN, wn = wave % WN;
+    int tm, tn;
+    ch::tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    A += (int64_t)blockIdx.y * strideA;
+    B += (int64_t)blockIdx.y * strideB;
+    C += (int64_t)blockIdx.y * strideC;
+    const int64_t lda = AKC ? K : M, ldb = BKC ? K : N;
+
+    TileCopy<AKC, BM, BK, NW> copy_a;
+    TileCopy<BKC, BN, BK, NW> copy_b;
+    copy_a.init(lda, m0, wave, lane);
+    copy_b.init(ldb, n0, wave, lane);
+    const int64_t step_a = copy_a.kstep(lda), step_b = copy_b.kstep(ldb);
+    const uint32_t lds0 = lds_addr(smem);
+    auto issue = [&](int kt, int stage) {
+        const uint32_t dst = lds0 + (uint32_t)(stage * P::STAGE_BYTES);
+        copy_a.issue(reinterpret_cast<const char*>(A) + kt * step_a, dst, wave);
+        copy_b.issue(reinterpret_cast<const char*>(B) + kt * step_b, dst + P::A_BYTES, wave);
+    };
+
+    v16f acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = v16f{};
+
+    // Operand fragments of two consecutive k-steps: step s+1 is read while
+    // step s's MFMAs run, also across the k-tile boundary.
+    v8bf fa[2][FM], fb[2][FN];
+    auto read_step = [&](int buf, const char* tile, int kk) {
+        const char* ta = tile;
+        const char* tb = tile + P::A_BYTES;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) fa[buf][i] = read_frag<AKC, BM, BK>(ta, wm * P::TM + i * 32, kk, lane);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) fb[buf][j] = read_frag<BKC, BN, BK>(tb, wn * P::TN + j * 32, kk, lane);
+    };
+
+    constexpr int KS = BK / 16;  // k-steps per k-tile
+    static_assert(KS % 2 == 0, "fragment double-buffer parity assumes an even k-step count");
+    const int nk = K / BK;
+    // Prologue: tiles 0 .. STAGES-2 in flight; wait for tile 0; then tile
+    // STAGES-1 goes into the last free buffer.
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < nk) issue(s, s);
+    if (nk >= STAGES - 1) {
+        constexpr int n = P::LPW * (STAGES - 2);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
+    } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    asm volatile("s_barrier" ::: "memory");
+    if (STAGES - 1 < nk) issue(STAGES - 1, STAGES - 1);
+    read_step(0, smem, 0);
+
+    // ds_read instructions per k-step (a transposed fragment takes two).
+    constexpr int NR = FM * (AKC ? 1 : 2) + FN * (BKC ? 1 : 2);
+    auto mfma_step = [&](int cur) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
+    };
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const char* tile = smem + (kt % STAGES) * P::STAGE_BYTES;
+        // k-steps 0 .. KS-2: next step's reads spread between this step's MFMAs
+#pragma unroll
+        for (int kk = 0; kk + 1 < KS; ++kk) {
+            read_step((kk & 1) ^ 1, tile, kk + 1);
+            mfma_step(kk & 1);
+        }
+#pragma unroll
+        for (int g = 0; g < (KS - 1) * FM * FN; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            if (g % (FM * FN) < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one ds_read
+        }
+        // Last k-step.  Tile kt+1 must have landed (tiles kt+2 .. kt+STAGES-1
+        // may stay in flight) and every wave must be done reading tile kt
+        // before its buffer takes tile kt+STAGES.
+        if (kt + 1 < nk) {
+            if (kt + STAGES - 1 < nk) {
+                constexpr int n = P::LPW * (STAGES - 2);
+                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(n) : "memory");
+            } else {
+                asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+            }
+            asm volatile("s_barrier" ::: "memory");
+            read_step(0, smem + ((kt + 1) % STAGES) * P::STAGE_BYTES, 0);
+            if (kt + STAGES < nk) issue(kt + STAGES, kt % STAGES);
+        }
+        mfma_step((KS - 1) & 1);
+    }
+
+    const int half = lane >> 5, col = lane & 31;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int r = m0 + wm * P::TM + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+                const int c = n0 + wn * P::TN + j * 32 + col;
+                C[(int64_t)r * N + c] = acc[i][j][v];
+            }
+}
+
+}  // namespace ch

@@ -1,0 +1,146 @@
+// gemm_tiles.hpp -- LDS tile layouts and copy/read helpers for the bf16
+// matrix-core GEMM on gfx950.
+//
+// Operands move global -> LDS with global_load_lds_dwordx4 (no VGPR staging):
+// one instruction moves 16 bytes per lane, and lane l's bytes land at
+// lds_base + 16*l, so a wave writes 1 KiB of LDS contiguously.  The LDS layout
+// is therefore chosen by picking, per lane, WHICH 16-byte global chunk it
+// fetches.  Two layouts, named by which index is contiguous in global memory:
+//
+//   KC ("k-contiguous", A stored M x K or B stored N x K):
+//     LDS tile [R rows][BK], row pitch 2*BK bytes, CPR = BK/8 chunks per row.
+//     Chunk c of row r is stored in slot c ^ kc_swizzle(r).  The MFMA operand
+//     read (ds_read_b128) has 16 lanes read rows r0..r0+15 at one logical
+//     chunk; the swizzle spreads them over all banks whether the LDS serves
+//     8 or 16 lanes of a 16-byte read per cycle.
+//
+//   MN ("m/n-contiguous", A stored K x M or B stored K x N):
+//     LDS tile [BK][R], row pitch 2*R bytes, 16-byte chunk c of k-row kr in
+//     slot c ^ (2*(kr & 3)) (pairs of chunks move together).  The operand is
+//     read with ds_read_b64_tr_b16: within each 16-lane group, result lane i,
+//     element j = the element (i % 4) of source lane 4*j + i/4.  Source lane
+//     (4*j + q) points at k-row kb + j, columns c0 + 4q .. c0 + 4q + 3, so
+//     result lane i receives column c0 + i at k-rows kb .. kb + 3 -- exactly
+//     the k-contiguous register layout the MFMA wants, with no register
+//     shuffles.  A 16-lane group touches 4 k-rows x 32 bytes in 4 distinct
+//     32-byte bank groups.
+//
+// v_mfma_f32_32x32x16_bf16 operand layout: lane l holds 8 bf16 of row
+// (l % 32) at k = 8*(l / 32) .. +7 (both A and B, B indexed by column);
+// the accumulator holds column (l % 32), rows 8*(v/4) + 4*(l/32) + v%4.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace ch {
+namespace tiles {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Slot of logical chunk c in KC row r (CPR chunks per row).
+template <int CPR>
+__device__ __forceinline__ int kc_slot(int r, int c) {
+    static_assert(CPR == 4 || CPR == 8, "KC rows hold 4 or 8 chunks");
+    if constexpr (CPR == 8) return c ^ ((r & 7) ^ ((r >> 3) & 1));
+    else return c ^ (((r >> 1) & 3) ^ ((r >> 3) & 1));
+}
+// Slot of chunk c in MN k-row kr.
+__device__ __forceinline__ int mn_slot(int kr, int c) { return c ^ ((kr & 3) << 1); }
+
+// Byte address (within the LDS window) of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const lds_void*)p;
+}
+
+// One global -> LDS copy instruction: 16 bytes per lane from sbase + voff
+// (SGPR base, 32-bit per-lane byte offset) into LDS at lds_dst + 16*lane.
+// Written as inline asm so the compiler does not see an outstanding LDS write:
+// it would otherwise wait for every copy in flight before each ds_read, which
+// serialises the copy of tile k+1 behind the math of tile k.  The caller
+// orders copies and reads with s_waitcnt vmcnt + s_barrier.
+// The LDS address goes in through an {m0} operand, so the compiler itself
+// writes M0 and knows it did.
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds_dst) {
+    asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds_dst) : "memory");
+}
+
+// Per-lane byte offsets (relative to the operand base of k-tile 0) of this
+// wave's NI/NW copy instructions for one operand tile, and the byte step that
+// moves them to the next k-tile (added to the scalar base).
+//   KC: tile [R rows][BK]; instruction q covers rows q*RPI .. +RPI-1.
+//   MN: tile [BK][R];      instruction q covers k-rows q*KPI .. +KPI-1.
+// Instruction q's LDS destination is tile_base + 1024*q.
+template <bool KC, int R, int BK, int NW>
+struct TileCopy {
+    static constexpr int NI = R * BK * 2 / 1024, PER_WAVE = NI / NW;
+    static_assert(NI % NW == 0, "tile copy must split evenly over the waves");
+    uint32_t voff[PER_WAVE];
+
+    __device__ __forceinline__ void init(int64_t ld, int r0, int wave, int lane) {
+        if constexpr (KC) {
+            constexpr int CPR = BK / 8, RPI = 64 / CPR;
+#pragma unroll
+            for (int j = 0; j < PER_WAVE; ++j) {
+                const int q = wave + NW * j;
+                const int r = q * RPI + lane / CPR;
+                const int c = kc_slot<CPR>(r, lane % CPR);  // slot lane%CPR holds chunk c
+                voff[j] = (uint32_t)(((int64_t)(r0 + r) * ld + 8 * c) * 2);
+            }
+        } else {
+            constexpr int CPR = R / 8, KPI = 64 / CPR;
+            static_assert(CPR >= 8 && 64 % CPR == 0, "MN rows must hold 8..64 chunks");
+#pragma unroll
+            for (int j = 0; j < PER_WAVE; ++j) {
+                const int q = wave + NW * j;
+                const int kr = q * KPI + lane / CPR;
+                const int c = mn_slot(kr, lane % CPR);
+                voff[j] = (uint32_t)(((int64_t)kr * ld + r0 + 8 * c) * 2);
+            }
+        }
+    }
+    // Byte step of the scalar base per k-tile.
+    static __device__ __forceinline__ int64_t kstep(int64_t ld) { return KC ? (int64_t)BK * 2 : (int64_t)BK * ld * 2; }
+
+    __device__ __forceinline__ void issue(const char* sbase, uint32_t lds_tile, int wave) const {
+#pragma unroll
+        for (int j = 0; j < PER_WAVE; ++j) dma16(sbase, voff[j], lds_tile + 1024u * (uint32_t)(wave + NW * j));
+    }
+};
+
+// MFMA operand fragment (32 rows x 16 k) starting at tile row `row0`, k-step kk.
+template <bool KC, int R, int BK>
+__device__ __forceinline__ v8bf read_frag(const char* tile, int row0, int kk, int lane) {
+    if constexpr (KC) {
+        constexpr int CPR = BK / 8;
+        const int r = row0 + (lane & 31);
+        const int c = 2 * kk + (lane >> 5);
+        return *reinterpret_cast<const v8bf*>(tile + r * (BK * 2) + kc_slot<CPR>(r, c) * 16);
+    } else {
+        const int j = (lane & 15) >> 2, q = lane & 3;
+        const int col = row0 + 16 * ((lane >> 4) & 1) + 4 * q;
+        const int kb = kk * 16 + 8 * (lane >> 5) + j;
+        v4s lo, hi;
+        {
+            const int kr = kb;
+            const char* p = tile + kr * (R * 2) + mn_slot(kr, col >> 3) * 16 + (col & 7) * 2;
+            lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(const lds_void*)p);
+        }
+        {
+            const int kr = kb + 4;
+            const char* p = tile + kr * (R * 2) + mn_slot(kr, col >> 3) * 16 + (col & 7) * 2;
+            hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(const lds_void*)p);
+        }
+        typedef short v8s __attribute__((ext_vector_type(8)));
+        v8s w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        return __builtin_bit_cast(v8bf, w);
+    }
+}
+
+}  // namespace tiles
+}  // namespace ch

@@ -116,7 +116,11 @@ def test_bf16_golden_vectors_exact(hip, golden, oracle):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (3, 5, 7), (129, 131, 40), (256, 128, 64), (200, 300, 100)])
+@pytest.mark.parametrize("M,N,K", [
+    (1, 1, 1), (3, 5, 7), (129, 131, 40), (200, 300, 100),  # general kernel (ragged)
+    (256, 128, 64), (384, 128, 192),                         # 128 x 128 x 64 tiled kernel
+    (256, 256, 64), (512, 768, 384), (768, 512, 640),        # 256 x 256 x 64 tiled kernel
+])
 def test_bf16_shapes_and_layouts(hip, oracle, M, N, K, ta, tb):
     rng = np.random.default_rng(M + N + K)
     A32 = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
@@ -130,6 +134,34 @@ def test_bf16_shapes_and_layouts(hip, oracle, M, N, K, ta, tb):
     Ad = np.abs(Au.T if ta else Au).astype(np.float64)
     Bd = np.abs(Bu.T if tb else Bu).astype(np.float64)
     assert_gemm_close(got, ref, Ad @ Bd, K, f"bf16 {M}x{N}x{K}")
+
+
+def test_bf16_batched_tiled_every_entry(hip, oracle):
+    # batch entries back to back through the 256 x 256 x 64 kernel: each one
+    # checked in full against the sequential loop on the upcast values
+    rng = np.random.default_rng(9)
+    bsz, M, N, K = 3, 256, 512, 128
+    A = oracle.to_bf16(rng.standard_normal((bsz, M, K)).astype(np.float32))
+    B = oracle.to_bf16(rng.standard_normal((bsz, K, N)).astype(np.float32))
+    got = hip.matmul_batched(hip.from_numpy(A, "bf16"), hip.from_numpy(B, "bf16")).numpy()
+    for i in range(bsz):
+        Au = oracle.bf16_to_f32(A[i]).reshape(M, K)
+        Bu = oracle.bf16_to_f32(B[i]).reshape(K, N)
+        ref = oracle.matmul(Au, Bu, threads=8)
+        den = np.abs(Au).astype(np.float64) @ np.abs(Bu).astype(np.float64)
+        assert_gemm_close(got[i], ref, den, K, f"batched bf16 entry {i}")
+
+
+def test_bf16_tiled_output_is_overwritten_and_deterministic(hip):
+    # C is written, not accumulated into (the reference zero-fills its
+    # accumulator), and two runs agree bit for bit
+    n = 512
+    a = hip.to_bf16(hip.fill_normal(hip.empty((n, n)), seed=5, std=0.02))
+    b = hip.to_bf16(hip.fill_normal(hip.empty((n, n)), seed=6, std=0.02))
+    c = hip.fill_normal(hip.empty((n, n)), seed=7)
+    first = hip.matmul(a, b, out=c).numpy()
+    second = hip.matmul(a, b, out=c).numpy()
+    assert np.array_equal(first, second)
 
 
 def test_config5_bf16_8192_cube(hip, oracle):
