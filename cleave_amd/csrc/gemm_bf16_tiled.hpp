@@ -43,18 +43,21 @@ struct Bf16Tiled {
     // operand with 32-bit byte offsets from a per-k-tile scalar base, so a
     // k-contiguous operand must stay under 4 GiB (an m/n-contiguous one only
     // needs its BK-row band to).
-    static bool fits(int M, int N, int K) {
-        const bool dims = M % BM == 0 && N % BN == 0 && K % BK == 0;
-        const uint64_t a_span = AKC ? (uint64_t)M * K * 2 : (uint64_t)BK * M * 2;
-        const uint64_t b_span = BKC ? (uint64_t)N * K * 2 : (uint64_t)BK * N * 2;
+    // Shapes this kernel takes without bounds checks.  The copies address an
+    // operand with 32-bit byte offsets from a per-k-tile scalar base, so the
+    // addressed span of each operand must stay under 4 GiB.
+    static bool fits(int M, int N, int K, int64_t lda, int64_t ldb) {
+        const bool dims = M % BM == 0 && N % BN == 0 && K % BK == 0 && lda % 8 == 0 && ldb % 8 == 0;
+        const uint64_t a_span = (AKC ? (uint64_t)M : (uint64_t)BK + 1) * (uint64_t)lda * 2;
+        const uint64_t b_span = (BKC ? (uint64_t)N : (uint64_t)BK + 1) * (uint64_t)ldb * 2;
         return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
-    }
-};
+    }};
 
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, float* __restrict__ C, int M,
-    int N, int K, int64_t strideA, int64_t strideB, int64_t strideC, int tiles_m, int tiles_n) {
+    int N, int K, int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC,
+    int tiles_m, int tiles_n) {
     using namespace ch::tiles;
     using P = Bf16Tiled<BM, BN, BK, WM, WN, STAGES, AKC, BKC>;
     constexpr int FM = P::FM, FN = P::FN, NW = P::NW;
@@ -69,7 +72,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
     A += (int64_t)blockIdx.y * strideA;
     B += (int64_t)blockIdx.y * strideB;
     C += (int64_t)blockIdx.y * strideC;
-    const int64_t lda = AKC ? K : M, ldb = BKC ? K : N;
 
     TileCopy<AKC, BM, BK, NW> copy_a;
     TileCopy<BKC, BN, BK, NW> copy_b;

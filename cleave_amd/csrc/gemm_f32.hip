@@ -1,11 +1,16 @@
 // gemm_f32.hip -- fp32 matmul on CDNA4 matrix cores (v_mfma_f32_32x32x2f32).
 //
+// Shapes that divide a 256 x 256 x 16 or 128 x 128 x 16 tile run the
+// large-tile kernel of gemm_f32_tiled.hpp (LDS filled by global_load_lds,
+// four MFMA k-steps per 16-byte operand read).  Everything else runs the
+// general kernel below.
+//
 // Replaces linalg.matmul as cleave lowers it (stdlib/linalg/matrix.cleave:27-61,
 // region cleave/src/mlir_lower.rs:2089-2120): C = 0; C[i,j] += A[i,k]*B[k,j].
 // The A^T B and A B^T forms are the reverse-mode halves of the MatMul product
 // rule (stdlib/linalg/matrix.cleave:24).
 //
-// Design (one workgroup = one BM x BN tile of C):
+// General kernel (one workgroup = one BM x BN tile of C):
 //   * 256 threads = 4 waves in a 2 x 2 grid; each wave owns a (BM/2) x (BN/2)
 //     block made of 32 x 32 MFMA tiles, accumulators kept in registers.
 //   * K is walked in BK slices.  Both operands are staged in LDS k-major
@@ -23,6 +28,7 @@
 //     path needs M % BM == N % BN == K % BK == 0.
 #include "common.hpp"
 #include "gemm_common.hpp"
+#include "gemm_f32_tiled.hpp"
 
 namespace {
 
@@ -199,7 +205,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
 constexpr int BM = 128, BN = 128, BK = 16;
 
 template <bool TA, bool TB>
-int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
+int32_t launch_general(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
                int64_t ldb, int64_t ldc, int batch, int64_t sA, int64_t sB, int64_t sC) {
     // The 16-byte loads of the fast path also need every row start aligned.
     const bool fast = (M % BM == 0) && (N % BN == 0) && (K % BK == 0) && (lda % 4 == 0) &&
@@ -214,6 +220,40 @@ int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, in
             a, b, c, M, N, K, lda, ldb, ldc, sA, sB, sC, tiles_m, tiles_n);
     CH_LAUNCHED("gemm_f32_kernel");
     return CLEAVE_HIP_OK;
+}
+
+// Large-tile kernel (gemm_f32_tiled.hpp) when the shape divides its tile;
+// false when it does not.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool TA, bool TB>
+bool launch_tiled(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
+                  int64_t ldb, int batch, int64_t sA, int64_t sB, int64_t sC, int32_t* status) {
+    using P = ch::F32Tiled<BM, BN, BK, WM, WN, STAGES, !TA, TB>;
+    if (!P::fits(M, N, K, lda, ldb) || ((uintptr_t)a & 15) || ((uintptr_t)b & 15) || (sA % 4) ||
+        (sB % 4))
+        return false;
+    const int tiles_m = M / BM, tiles_n = N / BN;
+    dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)batch);
+    ch::gemm_f32_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
+        a, b, c, M, N, K, lda, ldb, sA, sB, sC, tiles_m, tiles_n);
+    *status = ch::check_hip(hipGetLastError(), "gemm_f32_tiled_kernel");
+    return true;
+}
+
+template <bool TA, bool TB>
+int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
+               int64_t ldb, int64_t ldc, int batch, int64_t sA, int64_t sB, int64_t sC) {
+    int32_t st = CLEAVE_HIP_OK;
+    if (ldc == N) {
+        // 256 x 256 x 16 tile (8 waves of 128 x 64) when it still yields a tile
+        // per CU, else 128 x 128 x 16 (4 waves of 64 x 64).
+        const int64_t big_tiles = (int64_t)(M / 256) * (N / 256) * batch;
+        if (big_tiles >= ch::num_cus() &&
+            launch_tiled<256, 256, 16, 2, 4, 2, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
+            return st;
+        if (launch_tiled<128, 128, 16, 2, 2, 2, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
+            return st;
+    }
+    return launch_general<TA, TB>(a, b, c, M, N, K, lda, ldb, ldc, batch, sA, sB, sC);
 }
 
 // batch >= 1 independent products packed back to back, or (splits > 1, batch

@@ -50,8 +50,18 @@ __device__ __forceinline__ int kc_slot(int r, int c) {
     if constexpr (CPR == 8) return c ^ ((r & 7) ^ ((r >> 3) & 1));
     else return c ^ (((r >> 1) & 3) ^ ((r >> 3) & 1));
 }
-// Slot of chunk c in MN k-row kr.
-__device__ __forceinline__ int mn_slot(int kr, int c) { return c ^ ((kr & 3) << 1); }
+// Slot of chunk c in MN k-row kr, for the two MN read instructions:
+//   bf16, ds_read_b64_tr_b16: 16-lane groups read 4 consecutive k-rows x 32 B;
+//     XOR-ing chunk pairs with kr & 3 spreads the 4 rows over 4 bank groups.
+//   f32, ds_read_b32: the two half-waves read k-rows kr and kr + 4 at the same
+//     128 B of columns; flipping 128 B on (kr >> 2) & 1 puts them in opposite
+//     bank halves.
+template <int ESZ>
+__device__ __forceinline__ int mn_slot(int kr, int c) {
+    static_assert(ESZ == 2 || ESZ == 4, "bf16 or f32 operands");
+    if constexpr (ESZ == 2) return c ^ ((kr & 3) << 1);
+    else return c ^ (((kr >> 2) & 1) << 3);
+}
 
 // Byte address (within the LDS window) of a __shared__ object.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -76,36 +86,39 @@ __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t
 //   KC: tile [R rows][BK]; instruction q covers rows q*RPI .. +RPI-1.
 //   MN: tile [BK][R];      instruction q covers k-rows q*KPI .. +KPI-1.
 // Instruction q's LDS destination is tile_base + 1024*q.
-template <bool KC, int R, int BK, int NW>
+template <bool KC, int R, int BK, int NW, int ESZ = 2>
 struct TileCopy {
-    static constexpr int NI = R * BK * 2 / 1024, PER_WAVE = NI / NW;
+    static constexpr int EPC = 16 / ESZ;  // elements per 16-byte chunk
+    static constexpr int NI = R * BK * ESZ / 1024, PER_WAVE = NI / NW;
     static_assert(NI % NW == 0, "tile copy must split evenly over the waves");
     uint32_t voff[PER_WAVE];
 
     __device__ __forceinline__ void init(int64_t ld, int r0, int wave, int lane) {
         if constexpr (KC) {
-            constexpr int CPR = BK / 8, RPI = 64 / CPR;
+            constexpr int CPR = BK / EPC, RPI = 64 / CPR;
 #pragma unroll
             for (int j = 0; j < PER_WAVE; ++j) {
                 const int q = wave + NW * j;
                 const int r = q * RPI + lane / CPR;
                 const int c = kc_slot<CPR>(r, lane % CPR);  // slot lane%CPR holds chunk c
-                voff[j] = (uint32_t)(((int64_t)(r0 + r) * ld + 8 * c) * 2);
+                voff[j] = (uint32_t)(((int64_t)(r0 + r) * ld + EPC * c) * ESZ);
             }
         } else {
-            constexpr int CPR = R / 8, KPI = 64 / CPR;
-            static_assert(CPR >= 8 && 64 % CPR == 0, "MN rows must hold 8..64 chunks");
+            constexpr int CPR = R / EPC, KPI = 64 / CPR;
+            static_assert(CPR >= (ESZ == 2 ? 8 : 16) && 64 % CPR == 0, "MN row too narrow for its swizzle");
 #pragma unroll
             for (int j = 0; j < PER_WAVE; ++j) {
                 const int q = wave + NW * j;
                 const int kr = q * KPI + lane / CPR;
-                const int c = mn_slot(kr, lane % CPR);
-                voff[j] = (uint32_t)(((int64_t)kr * ld + r0 + 8 * c) * 2);
+                const int c = mn_slot<ESZ>(kr, lane % CPR);
+                voff[j] = (uint32_t)(((int64_t)kr * ld + r0 + EPC * c) * ESZ);
             }
         }
     }
     // Byte step of the scalar base per k-tile.
-    static __device__ __forceinline__ int64_t kstep(int64_t ld) { return KC ? (int64_t)BK * 2 : (int64_t)BK * ld * 2; }
+    static __device__ __forceinline__ int64_t kstep(int64_t ld) {
+        return KC ? (int64_t)BK * ESZ : (int64_t)BK * ld * ESZ;
+    }
 
     __device__ __forceinline__ void issue(const char* sbase, uint32_t lds_tile, int wave) const {
 #pragma unroll
@@ -128,17 +141,41 @@ __device__ __forceinline__ v8bf read_frag(const char* tile, int row0, int kk, in
         v4s lo, hi;
         {
             const int kr = kb;
-            const char* p = tile + kr * (R * 2) + mn_slot(kr, col >> 3) * 16 + (col & 7) * 2;
+            const char* p = tile + kr * (R * 2) + mn_slot<2>(kr, col >> 3) * 16 + (col & 7) * 2;
             lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(const lds_void*)p);
         }
         {
             const int kr = kb + 4;
-            const char* p = tile + kr * (R * 2) + mn_slot(kr, col >> 3) * 16 + (col & 7) * 2;
+            const char* p = tile + kr * (R * 2) + mn_slot<2>(kr, col >> 3) * 16 + (col & 7) * 2;
             hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(const lds_void*)p);
         }
         typedef short v8s __attribute__((ext_vector_type(8)));
         v8s w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         return __builtin_bit_cast(v8bf, w);
+    }
+}
+
+// f32 operand for four consecutive v_mfma_f32_32x32x2f32 steps over the
+// 8-deep k-block kb (32 rows starting at tile row row0).  Lane-half h holds
+// k = 8*kb + 4*h + s at step s (A and B agree, so the k-sum is complete).
+typedef float v4f __attribute__((ext_vector_type(4)));
+template <bool KC, int R, int BK>
+__device__ __forceinline__ v4f read_frag_f32(const char* tile, int row0, int kb, int lane) {
+    if constexpr (KC) {
+        constexpr int CPR = BK / 4;
+        const int r = row0 + (lane & 31);
+        const int c = 2 * kb + (lane >> 5);
+        return *reinterpret_cast<const v4f*>(tile + r * (BK * 4) + kc_slot<CPR>(r, c) * 16);
+    } else {
+        const int col = row0 + (lane & 31);
+        const int k0 = 8 * kb + 4 * (lane >> 5);
+        v4f v;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int kr = k0 + s;
+            v[s] = *reinterpret_cast<const float*>(tile + kr * (R * 4) + mn_slot<4>(kr, col >> 2) * 16 + (col & 3) * 4);
+        }
+        return v;
     }
 }
 
