@@ -2,7 +2,8 @@
 // (v_mfma_f32_32x32x16_bf16), plus its batched form.
 //
 // Shapes that divide a 256 x 256 x 64 (or 128 x 128 x 64) tile run the
-// large-tile kernel of gemm_bf16_tiled.hpp (LDS filled by global_load_lds,
+// large-tile kernel of gemm_bf16_tiled.hpp (v_mfma_f32_16x16x32_bf16 for the
+// big tile) (LDS filled by global_load_lds,
 // transposing LDS reads for m/n-contiguous operands).  Everything else runs
 // the general kernel below, which guards every access.
 //
@@ -205,15 +206,15 @@ int32_t launch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int
 
 // Large-tile kernel (gemm_bf16_tiled.hpp) for shapes that divide its tile.
 // Returns false when the shape or alignment does not fit.
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool TA, bool TB>
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int MI, bool TA, bool TB>
 bool launch_tiled(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
                   int32_t* status) {
-    using P = ch::Bf16Tiled<BM, BN, BK, WM, WN, STAGES, !TA, TB>;
+    using P = ch::Bf16Tiled<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI>;
     const int64_t lda = TA ? M : K, ldb = TB ? K : N;
     if (!P::fits(M, N, K, lda, ldb) || ((uintptr_t)a & 15) || ((uintptr_t)b & 15)) return false;
     const int tiles_m = M / BM, tiles_n = N / BN;
     dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)batch);
-    ch::gemm_bf16_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
+    ch::gemm_bf16_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI><<<grid, P::THREADS, 0, ch::stream()>>>(
         a, b, c, M, N, K, lda, ldb, (int64_t)M * K, (int64_t)K * N, (int64_t)M * N, tiles_m, tiles_n);
     *status = ch::check_hip(hipGetLastError(), "gemm_bf16_tiled_kernel");
     return true;
@@ -222,10 +223,12 @@ bool launch_tiled(const uint16_t* a, const uint16_t* b, float* c, int M, int N, 
 template <bool TA, bool TB>
 int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch) {
     int32_t st = CLEAVE_HIP_OK;
-    // 256 x 256 x 64 tile, 8 waves of 128 x 64, two LDS stages (128 KiB)
-    if (launch_tiled<256, 256, 64, 2, 4, 2, TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
-    // 128 x 128 x 64 tile, 4 waves of 64 x 64, three LDS stages (96 KiB)
-    if (launch_tiled<128, 128, 64, 2, 2, 3, TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
+    // 256 x 256 x 64 tile, 8 waves of 128 x 64 in 16 x 16 x 32 MFMAs, two LDS
+    // stages (128 KiB)
+    if (launch_tiled<256, 256, 64, 2, 4, 2, 16, TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
+    // 128 x 128 x 64 tile, 4 waves of 64 x 64 in 32 x 32 x 16 MFMAs, three
+    // LDS stages (96 KiB)
+    if (launch_tiled<128, 128, 64, 2, 2, 3, 32, TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
     return launch<TA, TB>(a, b, c, M, N, K, batch);
 }
 

@@ -155,6 +155,39 @@ __device__ __forceinline__ v8bf read_frag(const char* tile, int row0, int kk, in
     }
 }
 
+// MFMA operand fragment for v_mfma_f32_16x16x32_bf16: 16 rows starting at
+// tile row `row0`, k-step kk of 32.  Lane l holds row (l % 16) at
+// k = 32*kk + 8*(l / 16) .. +7 (A by row, B by column).
+template <bool KC, int R, int BK>
+__device__ __forceinline__ v8bf read_frag16(const char* tile, int row0, int kk, int lane) {
+    if constexpr (KC) {
+        constexpr int CPR = BK / 8;
+        const int r = row0 + (lane & 15);
+        const int c = 4 * kk + (lane >> 4);
+        return *reinterpret_cast<const v8bf*>(tile + r * (BK * 2) + kc_slot<CPR>(r, c) * 16);
+    } else {
+        // 16-lane group g reads k-rows 32*kk + 8*g + 4*h + (0..3) for h = 0, 1;
+        // source lane 4*j + q points at k-row +j, columns row0 + 4*q .. +3.
+        const int j = (lane & 15) >> 2, q = lane & 3;
+        const int col = row0 + 4 * q;
+        const int kb = kk * 32 + 8 * (lane >> 4) + j;
+        v4s lo, hi;
+        {
+            const int kr = kb;
+            const char* p = tile + kr * (R * 2) + mn_slot<2>(kr, col >> 3) * 16 + (col & 7) * 2;
+            lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(const lds_void*)p);
+        }
+        {
+            const int kr = kb + 4;
+            const char* p = tile + kr * (R * 2) + mn_slot<2>(kr, col >> 3) * 16 + (col & 7) * 2;
+            hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(const lds_void*)p);
+        }
+        typedef short v8s __attribute__((ext_vector_type(8)));
+        v8s w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        return __builtin_bit_cast(v8bf, w);
+    }
+}
+
 // f32 operand for four consecutive v_mfma_f32_32x32x2f32 steps over the
 // 8-deep k-block kb (32 rows starting at tile row row0).  Lane-half h holds
 // k = 8*kb + 4*h + s at step s (A and B agree, so the k-sum is complete).
