@@ -277,6 +277,24 @@ def main():
         gbs = hn * 8 / (ev * 1e-3) / 1e9
         secondary["sigmoid_map_268M"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)}
         log(f"sigmoid map: {gbs:.0f} GB/s")
+        # binary Ring map (two reads, one write per element)
+        hz = ca.fill_normal(ca.empty(hn), seed=502)
+        wall_s, ev = timed(ca, lambda: ca.add(hx, hz, out=hy), 10, 2)
+        gbs = hn * 12 / (ev * 1e-3) / 1e9
+        secondary["add_map_268M"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)}
+        log(f"add map: {gbs:.0f} GB/s")
+        del hz
+        # f32 Sum and Max/argmax reductions (one read per element)
+        sdev = ca.empty(1)
+        wall_s, ev = timed(ca, lambda: ca.reduce_sum(hx, sdev), 10, 2)
+        gbs = hn * 4 / (ev * 1e-3) / 1e9
+        secondary["sum_f32_268M"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)}
+        log(f"sum f32: {gbs:.0f} GB/s")
+        mdev, idev = ca.empty(1), ca.empty(1, "i64")
+        wall_s, ev = timed(ca, lambda: ca.reduce_max(hx, mdev, idev), 10, 2)
+        gbs = hn * 4 / (ev * 1e-3) / 1e9
+        secondary["max_argmax_f32_268M"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)}
+        log(f"max/argmax f32: {gbs:.0f} GB/s")
         del hx, hy
     if secondary:
         result["secondary"] = secondary

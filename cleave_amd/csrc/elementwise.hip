@@ -2,8 +2,8 @@
 // Activation<Tensor> (stdlib/nn/nn.cleave:82-95) and the backward forms of the
 // reference's derivative rules (stdlib/num/num.cleave:123-136, :222-223).
 //
-// HBM-bound: each thread moves 16-byte vectors, UNROLL of them in flight
-// before the first store, over a grid-stride loop sized to the CU count.
+// HBM-bound: each thread moves one 16-byte vector per operand with
+// non-temporal loads/stores, over a grid that covers the array.
 // The library is compiled with -ffp-contract=off, so every op below rounds
 // exactly where the reference's scalar loop does (add/sub/mul/div/neg/relu
 // are bit-exact; exp/tanh come from the device math library).
@@ -36,36 +36,31 @@ struct ReluBwdOp {  // x > 0 ? g : 0
 };
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
 
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// One 16-byte vector per thread over a grid that covers the whole array (a
+// grid-stride loop only past 2^31 blocks), with non-temporal loads and stores:
+// streamed data is not kept in L2, which lifts a read+write stream from ~5.5
+// to ~6.4 TB/s on MI355X.
 unsigned grid_for(int64_t nvec) {
-    int64_t want = (nvec + (int64_t)kThreads * kUnroll - 1) / ((int64_t)kThreads * kUnroll);
-    int64_t cap = (int64_t)ch::num_cus() * 8;
-    if (want > cap) want = cap;
+    int64_t want = (nvec + kThreads - 1) / kThreads;
+    if (want > 0x7FFFFFFF) want = 0x7FFFFFFF;
     return (unsigned)(want < 1 ? 1 : want);
 }
 
-__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
-__device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+__device__ __forceinline__ f4 ld4(const float* p) { return __builtin_nontemporal_load(reinterpret_cast<const f4*>(p)); }
+__device__ __forceinline__ void st4(float* p, f4 v) { __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p)); }
 
 template <class Op>
 __global__ __launch_bounds__(kThreads) void map1_kernel(const float* __restrict__ a,
                                                         float* __restrict__ out, int64_t n) {
     Op op;
     const int64_t nv = n / 4;
-    const int64_t step = (int64_t)gridDim.x * kThreads * kUnroll;
-    for (int64_t base = (int64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x; base < nv; base += step) {
-        float4 x[kUnroll];
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            int64_t i = base + (int64_t)u * kThreads;
-            if (i < nv) x[u] = ld4(a + 4 * i);
-        }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            int64_t i = base + (int64_t)u * kThreads;
-            if (i < nv) st4(out + 4 * i, make_float4(op(x[u].x), op(x[u].y), op(x[u].z), op(x[u].w)));
-        }
+    const int64_t step = (int64_t)gridDim.x * kThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < nv; i += step) {
+        const f4 x = ld4(a + 4 * i);
+        st4(out + 4 * i, f4{op(x[0]), op(x[1]), op(x[2]), op(x[3])});
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
         int64_t i = nv * 4 + threadIdx.x;
@@ -79,24 +74,10 @@ __global__ __launch_bounds__(kThreads) void map2_kernel(const float* __restrict_
                                                         float* __restrict__ out, int64_t n) {
     Op op;
     const int64_t nv = n / 4;
-    const int64_t step = (int64_t)gridDim.x * kThreads * kUnroll;
-    for (int64_t base = (int64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x; base < nv; base += step) {
-        float4 x[kUnroll], y[kUnroll];
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            int64_t i = base + (int64_t)u * kThreads;
-            if (i < nv) {
-                x[u] = ld4(a + 4 * i);
-                y[u] = ld4(b + 4 * i);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            int64_t i = base + (int64_t)u * kThreads;
-            if (i < nv)
-                st4(out + 4 * i, make_float4(op(x[u].x, y[u].x), op(x[u].y, y[u].y),
-                                             op(x[u].z, y[u].z), op(x[u].w, y[u].w)));
-        }
+    const int64_t step = (int64_t)gridDim.x * kThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < nv; i += step) {
+        const f4 x = ld4(a + 4 * i), y = ld4(b + 4 * i);
+        st4(out + 4 * i, f4{op(x[0], y[0]), op(x[1], y[1]), op(x[2], y[2]), op(x[3], y[3])});
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
         int64_t i = nv * 4 + threadIdx.x;
@@ -128,7 +109,7 @@ int32_t run1(const char* name, const float* a, int64_t alen, float* out, int64_t
     CH_REQUIRE(a && out, "%s: null buffer", name);
     CH_INIT_OR_RETURN();
     if (aligned16(a) && aligned16(out))
-        map1_kernel<Op><<<grid_for(alen / 4 + 1), kThreads, 0, ch::stream()>>>(a, out, alen);
+        map1_kernel<Op><<<grid_for(alen / 4), kThreads, 0, ch::stream()>>>(a, out, alen);
     else
         map1_scalar_kernel<Op><<<grid_for(alen / 4 + 1), kThreads, 0, ch::stream()>>>(a, out, alen);
     CH_LAUNCHED(name);
@@ -145,7 +126,7 @@ int32_t run2(const char* name, const float* a, int64_t alen, const float* b, int
     CH_REQUIRE(a && b && out, "%s: null buffer", name);
     CH_INIT_OR_RETURN();
     if (aligned16(a) && aligned16(b) && aligned16(out))
-        map2_kernel<Op><<<grid_for(alen / 4 + 1), kThreads, 0, ch::stream()>>>(a, b, out, alen);
+        map2_kernel<Op><<<grid_for(alen / 4), kThreads, 0, ch::stream()>>>(a, b, out, alen);
     else
         map2_scalar_kernel<Op><<<grid_for(alen / 4 + 1), kThreads, 0, ch::stream()>>>(a, b, out, alen);
     CH_LAUNCHED(name);

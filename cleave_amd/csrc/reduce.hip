@@ -22,9 +22,16 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kUnroll = 4;
 
+// Native clang vectors (register-promoted; HIP's float4/uint4 structs are not
+// always) loaded with non-temporal hints: the data is streamed once.
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+// Stage-1 grid: enough blocks for 16 per CU (a function of the length and the
+// CU count only, so results are reproducible on a given device).
 unsigned stage1_blocks(int64_t nvec) {
     int64_t want = (nvec + (int64_t)kThreads * kUnroll - 1) / ((int64_t)kThreads * kUnroll);
-    int64_t cap = (int64_t)ch::num_cus() * 4;
+    int64_t cap = (int64_t)ch::num_cus() * 16;
     if (want > cap) want = cap;
     return (unsigned)(want < 1 ? 1 : want);
 }
@@ -55,18 +62,18 @@ __global__ __launch_bounds__(kThreads) void sum_f32_stage1(const float* __restri
         const int64_t nv = n / 4;
         const int64_t step = (int64_t)gridDim.x * kThreads * kUnroll;
         for (int64_t base = (int64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x; base < nv; base += step) {
-            float4 v[kUnroll];
+            f4 v[kUnroll];
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) {
                 int64_t i = base + (int64_t)u * kThreads;
-                v[u] = i < nv ? reinterpret_cast<const float4*>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                v[u] = i < nv ? __builtin_nontemporal_load(reinterpret_cast<const f4*>(x) + i) : f4{0.f, 0.f, 0.f, 0.f};
             }
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) {
-                acc0 += v[u].x;
-                acc1 += v[u].y;
-                acc2 += v[u].z;
-                acc3 += v[u].w;
+                acc0 += v[u][0];
+                acc1 += v[u][1];
+                acc2 += v[u][2];
+                acc3 += v[u][3];
             }
         }
         if (blockIdx.x == 0 && threadIdx.x < (n & 3)) acc0 += x[nv * 4 + threadIdx.x];
@@ -130,20 +137,20 @@ __global__ __launch_bounds__(kThreads) void max_f32_stage1(const float* __restri
         const int64_t nv = n / 4;
         const int64_t step = (int64_t)gridDim.x * kThreads * kUnroll;
         for (int64_t base = (int64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x; base < nv; base += step) {
-            float4 v[kUnroll];
+            f4 v[kUnroll];
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) {
                 int64_t i = base + (int64_t)u * kThreads;
-                if (i < nv) v[u] = reinterpret_cast<const float4*>(x)[i];
+                if (i < nv) v[u] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(x) + i);
             }
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) {
                 int64_t i = base + (int64_t)u * kThreads;
                 if (i < nv) {
-                    take_better(b, v[u].x, 4 * i + 0);
-                    take_better(b, v[u].y, 4 * i + 1);
-                    take_better(b, v[u].z, 4 * i + 2);
-                    take_better(b, v[u].w, 4 * i + 3);
+                    take_better(b, v[u][0], 4 * i + 0);
+                    take_better(b, v[u][1], 4 * i + 1);
+                    take_better(b, v[u][2], 4 * i + 2);
+                    take_better(b, v[u][3], 4 * i + 3);
                 }
             }
         }
@@ -206,16 +213,16 @@ __global__ __launch_bounds__(kThreads) void sum_u32_stage1(const uint32_t* __res
         const int64_t nv = n / 4;
         const int64_t step = (int64_t)gridDim.x * kThreads * kUnroll;
         for (int64_t base = (int64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x; base < nv; base += step) {
-            uint4 v[kUnroll];
+            u4 v[kUnroll];
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) {
                 int64_t i = base + (int64_t)u * kThreads;
-                v[u] = i < nv ? reinterpret_cast<const uint4*>(x)[i] : make_uint4(0, 0, 0, 0);
+                v[u] = i < nv ? __builtin_nontemporal_load(reinterpret_cast<const u4*>(x) + i) : u4{0, 0, 0, 0};
             }
             // Four u32 fit in u64 without overflow; add pairs in 64 bits.
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u)
-                acc += ((uint64_t)v[u].x + v[u].y) + ((uint64_t)v[u].z + v[u].w);
+                acc += ((uint64_t)v[u][0] + v[u][1]) + ((uint64_t)v[u][2] + v[u][3]);
         }
         if (blockIdx.x == 0 && threadIdx.x < (n & 3)) acc += x[nv * 4 + threadIdx.x];
     } else {
