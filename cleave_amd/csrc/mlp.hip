@@ -18,6 +18,7 @@
 //   7. dW1 partials = X^T d1            gemm_f32 TN, split-K slices
 //   8. dW1 = sum of slices; W1 -= lr dW1
 #include "common.hpp"
+#include "gemm_f32_tiled.hpp"
 
 namespace ch {
 int32_t gemm_f32_device(const float* a, const float* b, float* c, int M, int N, int K, int ta,
@@ -72,6 +73,23 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(const float* __restr
         float gy = (e + e) / (float)B;
         d2[row] = gy * yh * (1.0f - yh);
     }
+}
+
+// Fused path, after the MODE-1 GEMM: z2[row] = sum of the P partials of
+// H[row] . W2, then the same per-row loss pieces as row_pass_kernel.
+__global__ __launch_bounds__(kThreads) void row_finish_kernel(const float* __restrict__ zpart, int P,
+                                                              const float* __restrict__ y, int B,
+                                                              float* __restrict__ sq,
+                                                              float* __restrict__ d2) {
+    const int row = blockIdx.x * kThreads + threadIdx.x;
+    if (row >= B) return;
+    float z = zpart[row];
+    for (int p = 1; p < P; ++p) z += zpart[(int64_t)p * B + row];
+    const float yh = sigmoidf_ref(z);
+    const float e = yh - y[row];
+    sq[row] = e * e;
+    const float gy = (e + e) / (float)B;
+    d2[row] = gy * yh * (1.0f - yh);
 }
 
 // Column pass: each thread owns 4 consecutive columns of a band of rows.
@@ -145,6 +163,76 @@ int choose_splits(int D, int Hd, int B) {
     return splits;
 }
 
+// ---- fused path (shapes that divide the 256 x 256 x 16 f32 tile) -----------
+//   1. H = sigmoid(X W1) and partials of H W2      f32 tiled GEMM, MODE 1
+//   2. z2, yhat, e, sq, d2 per row; loss           row_finish, loss kernels
+//   3. dW1 slices = X^T d1 with d1 = (d2 W2) H(1-H) formed as the MFMA reads H,
+//      and dW2 partials                            f32 tiled GEMM, MODE 2
+//   4. dW1 = sum of slices, W1 -= lr dW1; dW2 likewise (W2 is updated last:
+//      step 3 reads it)
+using FusedTile1 = ch::F32Tiled<256, 256, 16, 2, 4, 2, true, false, 1>;
+using FusedTile2 = ch::F32Tiled<256, 256, 16, 2, 4, 2, false, false, 2>;
+
+int fused_splits(int B, int D, int Hd) {
+    const int tiles = (D / 256) * (Hd / 256);
+    int splits = 1;
+    while (tiles * splits < ch::num_cus() && splits < 64 && B % (splits * 2 * 16) == 0) splits *= 2;
+    return splits;
+}
+
+bool fused_fits(int B, int D, int Hd) {
+    if (B % 256 || D % 256 || Hd % 256) return false;
+    const int splits = fused_splits(B, D, Hd);
+    return FusedTile1::fits(B, Hd, D, D, Hd) && FusedTile2::fits(D, Hd, B / splits, D, Hd);
+}
+
+int32_t fused_step(const float* x, const float* y, float* w1, float* w2, float* dw1, float* dw2,
+                   float* loss_dev, int B, int D, int Hd, float lr, hipStream_t st) {
+    const int splits = fused_splits(B, D, Hd);
+    const int P = (Hd / 256) * 4;  // H W2 partials per row (tiles_n x waves along N)
+    // Scratch slot 4: H | zpart | sq | d2 | dW2 partials | dW1 slices | loss.
+    const size_t nH = (size_t)B * Hd, nZ = (size_t)P * B, nPart = (size_t)splits * Hd,
+                 nSl = (size_t)splits * D * Hd;
+    auto up = [](size_t n) { return (n + 63) & ~(size_t)63; };
+    const size_t total = up(nH) + up(nZ) + up(B) + up(B) + up(nPart) + up(nSl) + 64;
+    float* base = (float*)ch::scratch(4, total * sizeof(float));
+    if (!base) return CLEAVE_HIP_ERR_OOM;
+    float* H = base;
+    float* zpart = H + up(nH);
+    float* sq = zpart + up(nZ);
+    float* d2 = sq + up(B);
+    float* part = d2 + up(B);
+    float* slices = part + up(nPart);
+    float* loss_tmp = slices + up(nSl);
+
+    ch::MlpFuse f1;
+    f1.w2 = w2;
+    f1.zpart = zpart;
+    ch::gemm_f32_tiled_kernel<256, 256, 16, 2, 4, 2, true, false, 1>
+        <<<dim3((unsigned)((B / 256) * (Hd / 256)), 1), FusedTile1::THREADS, 0, st>>>(
+            x, w1, H, B, Hd, D, D, Hd, 0, 0, 0, B / 256, Hd / 256, f1);
+    CH_LAUNCHED("gemm_f32_tiled_kernel(MODE 1)");
+    row_finish_kernel<<<(B + kThreads - 1) / kThreads, kThreads, 0, st>>>(zpart, P, y, B, sq, d2);
+    CH_LAUNCHED("row_finish_kernel");
+    loss_kernel<<<1, kThreads, 0, st>>>(sq, B, loss_dev ? loss_dev : loss_tmp);
+    CH_LAUNCHED("loss_kernel");
+    const int kk = B / splits;
+    ch::MlpFuse f2;
+    f2.w2 = w2;
+    f2.d2 = d2;
+    f2.dw2part = part;
+    ch::gemm_f32_tiled_kernel<256, 256, 16, 2, 4, 2, false, false, 2>
+        <<<dim3((unsigned)((D / 256) * (Hd / 256)), (unsigned)splits), FusedTile2::THREADS, 0, st>>>(
+            x, H, slices, D, Hd, kk, D, Hd, (int64_t)kk * D, (int64_t)kk * Hd, (int64_t)D * Hd, D / 256,
+            Hd / 256, f2);
+    CH_LAUNCHED("gemm_f32_tiled_kernel(MODE 2)");
+    sum_slices_sgd_kernel<<<capped_grid((int64_t)D * Hd), kThreads, 0, st>>>(slices, splits, (int64_t)D * Hd, dw1, w1, lr);
+    CH_LAUNCHED("sum_slices_sgd_kernel(dW1)");
+    sum_slices_sgd_kernel<<<capped_grid(Hd), kThreads, 0, st>>>(part, splits, Hd, dw2, w2, lr);
+    CH_LAUNCHED("sum_slices_sgd_kernel(dW2)");
+    return CLEAVE_HIP_OK;
+}
+
 }  // namespace
 
 extern "C" int32_t cleave_hip_mlp_step_f32(const float* x, int64_t xlen, const float* y,
@@ -163,6 +251,9 @@ extern "C" int32_t cleave_hip_mlp_step_f32(const float* x, int64_t xlen, const f
     CH_REQUIRE(((uintptr_t)w2 & 15) == 0, "cleave_hip_mlp_step_f32: w2 must be 16-byte aligned");
     CH_INIT_OR_RETURN();
 
+    hipStream_t st = ch::stream();
+    if (fused_fits(B, D, Hd)) return fused_step(x, y, w1, w2, dw1, dw2, loss_dev, B, D, Hd, lr, st);
+
     const int splits = choose_splits(D, Hd, B);
     const int bands = (B + kRowsPerBand - 1) / kRowsPerBand;
     // Scratch slot 4: H/d1 | sq | d2 | dW2 partials | dW1 slices | loss.
@@ -177,7 +268,6 @@ extern "C" int32_t cleave_hip_mlp_step_f32(const float* x, int64_t xlen, const f
     float* part = d2 + up(B);
     float* slices = part + up(nPart);
     float* loss_tmp = slices + up(nSl);
-    hipStream_t st = ch::stream();
 
     int32_t rc = ch::gemm_f32_device(x, w1, H, B, Hd, D, 0, 0, 1);
     if (rc != CLEAVE_HIP_OK) return rc;

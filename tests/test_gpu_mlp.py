@@ -20,7 +20,10 @@ def _xavier(rng, fan_in, fan_out, shape):
     return rng.uniform(-lim, lim, shape).astype(np.float32)
 
 
-@pytest.mark.parametrize("B,D,Hd", [(64, 32, 48), (256, 64, 128), (100, 33, 70), (512, 128, 256)])
+@pytest.mark.parametrize("B,D,Hd", [
+    (64, 32, 48), (256, 64, 128), (100, 33, 70), (512, 128, 256),  # unfused kernel sequence
+    (512, 256, 512), (1024, 256, 768), (2048, 512, 256),           # fused GEMM path (256-tile shapes)
+])
 def test_small_step_against_oracle(hip, oracle, B, D, Hd):
     rng = np.random.default_rng(B + D + Hd)
     X = rng.standard_normal((B, D)).astype(np.float32)
@@ -40,6 +43,24 @@ def test_small_step_against_oracle(hip, oracle, B, D, Hd):
     assert np.max(np.abs(g2 - dW2_r)) <= 1e-4 * s2
     assert np.max(np.abs(w1.numpy() - W1_r)) <= 1e-6 * max(1.0, np.abs(W1_r).max())
     assert np.max(np.abs(w2.numpy() - W2_r)) <= 1e-6 * max(1.0, np.abs(W2_r).max())
+
+
+def test_fused_step_zero_lr_keeps_weights_and_reports_gradients(hip, oracle):
+    # the fused path reads W2 while forming d1, so W2 may only change after
+    # the dW1 product; with lr = 0 both weights stay bit-identical
+    rng = np.random.default_rng(11)
+    B, D, Hd = 512, 256, 512
+    X = rng.standard_normal((B, D)).astype(np.float32)
+    y = (rng.random(B) < 0.5).astype(np.float32)
+    W1 = _xavier(rng, D, Hd, (D, Hd))
+    W2 = _xavier(rng, Hd, 1, Hd)
+    x, yd, w1, w2 = (hip.from_numpy(v) for v in (X, y, W1, W2))
+    dw1, dw2 = hip.empty((D, Hd)), hip.empty(Hd)
+    hip.mlp_step(x, yd, w1, w2, 0.0, dw1=dw1, dw2=dw2)
+    assert np.array_equal(w1.numpy(), W1) and np.array_equal(w2.numpy(), W2)
+    _, dW1_r, dW2_r, _, _ = oracle.mlp_step(X, y, W1, W2, lr=0.0, threads=16)
+    assert np.max(np.abs(dw1.numpy() - dW1_r)) <= 1e-4 * np.abs(dW1_r).max()
+    assert np.max(np.abs(dw2.numpy() - dW2_r)) <= 1e-4 * np.abs(dW2_r).max()
 
 
 def test_step_without_gradient_outputs_and_zero_lr(hip, oracle):
