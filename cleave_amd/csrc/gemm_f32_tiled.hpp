@@ -122,17 +122,21 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
         for (int j = 0; j < FN; ++j)
             fb[buf][j] = read_frag_f32<BKC, BN, BK>(tile + P::A_BYTES, wn * P::TN + j * 32, kb, lane);
     };
-    auto mfma_block = [&](int cur) {
+    // MODE 2: d1 = (d2[k] w2[n]) h (1 - h), the order of the reference step.
+    // Applied to a k-block's fragments right after the previous block's MFMAs
+    // are issued, so this VALU work overlaps the matrix core.
+    auto transform = [&](int buf) {
         if constexpr (MODE == 2) {
-            // d1 = (d2[k] w2[n]) h (1 - h), the order of the reference step
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
-                const v4f h = fb[cur][j];
-                if (do_dw2) dw2acc[j] += h * d2v[cur];
+                const v4f h = fb[buf][j];
+                if (do_dw2) dw2acc[j] += h * d2v[buf];
 #pragma unroll
-                for (int s = 0; s < 4; ++s) fb[cur][j][s] = (d2v[cur][s] * w2c[j]) * h[s] * (1.0f - h[s]);
+                for (int s = 0; s < 4; ++s) fb[buf][j][s] = (d2v[buf][s] * w2c[j]) * h[s] * (1.0f - h[s]);
             }
         }
+    };
+    auto mfma_block = [&](int cur) {
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -160,6 +164,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
     asm volatile("s_barrier" ::: "memory");
     if (STAGES - 1 < nk) issue(STAGES - 1, STAGES - 1);
     read_block(0, smem, 0);
+    transform(0);
 
     for (int kt = 0; kt < nk; ++kt) {
         const char* tile = smem + (kt % STAGES) * P::STAGE_BYTES;
@@ -167,6 +172,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
         for (int kb = 0; kb + 1 < KB; ++kb) {
             read_block((kb & 1) ^ 1, tile, kb + 1);
             mfma_block(kb & 1);
+            transform((kb & 1) ^ 1);
         }
 #pragma unroll
         for (int g = 0; g < (KB - 1) * NM; ++g) {
@@ -185,13 +191,16 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
             if (kt + STAGES < nk) issue(kt + STAGES, kt % STAGES);
         }
         mfma_block((KB - 1) & 1);
+        if (kt + 1 < nk) transform(0);
     }
 
     const int half = lane >> 5, col = lane & 31;
     if constexpr (MODE == 1) {
-        // H = sigmoid(acc) (negf, exp, addf, divf as the reference's sigmoid),
-        // and per row the sum of H * w2 over this wave's columns: lanes of a
-        // half-wave hold the 32 columns of the same rows.
+        // H = sigmoid(acc) = 1 / (1 + exp(-acc)) with the hardware exp2 and
+        // reciprocal (about 1 ulp each; the IEEE expf + division would cost
+        // ~30 VALU ops per element with the matrix core idle), and per row the
+        // sum of H * w2 over this wave's columns: lanes of a half-wave hold
+        // the 32 columns of the same rows.
         float w2j[FN];
 #pragma unroll
         for (int j = 0; j < FN; ++j) w2j[j] = fuse.w2[n0 + wn * P::TN + j * 32 + col];
@@ -204,7 +213,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
             for (int j = 0; j < FN; ++j)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    const float h = 1.0f / (1.0f + expf(-acc[i][j][v]));
+                    const float e = __builtin_amdgcn_exp2f(-acc[i][j][v] * 1.4426950408889634f);
+                    const float h = __builtin_amdgcn_rcpf(1.0f + e);
                     acc[i][j][v] = h;
                     zs[v] += h * w2j[j];
                 }
