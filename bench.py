@@ -225,9 +225,13 @@ def main():
         fl = 2.0 * bs * k ** 3
         wall_s, ev = timed(ca, lambda: ca.matmul_batched(xb, yb, out=zb), sec_steps * 4, 2, 0.3)
         ach = fl / (ev * 1e-3) / 1e12
+        # compulsory HBM bytes: bf16 A and B read once, f32 C written once
+        hbm = bs * k * k * (2 + 2 + 4)
         secondary["gemm_bf16_batched_64x512"] = {"GFLOP/s": round(fl * sec_steps * 4 / wall_s / 1e9, 1),
                                                  "kernel_ms": round(ev, 4),
-                                                 "frac_bf16_mfma": round(ach / PEAK_BF16_MFMA, 4)}
+                                                 "frac_bf16_mfma": round(ach / PEAK_BF16_MFMA, 4),
+                                                 "hbm_GB/s": round(hbm / (ev * 1e-3) / 1e9, 1),
+                                                 "frac_hbm": round(hbm / (ev * 1e-3) / 1e9 / PEAK_HBM, 4)}
         log(f"gemm_bf16_batched_64x512: {ach:.1f} TFLOP/s")
         del xb, yb, zb
         # MLP step (config 4)

@@ -213,9 +213,10 @@ bool launch_tiled(const uint16_t* a, const uint16_t* b, float* c, int M, int N, 
     const int64_t lda = TA ? M : K, ldb = TB ? K : N;
     if (!P::fits(M, N, K, lda, ldb) || ((uintptr_t)a & 15) || ((uintptr_t)b & 15)) return false;
     const int tiles_m = M / BM, tiles_n = N / BN;
-    dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)batch);
+    if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
+    dim3 grid((unsigned)(tiles_m * tiles_n * batch));
     ch::gemm_bf16_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI><<<grid, P::THREADS, 0, ch::stream()>>>(
-        a, b, c, M, N, K, lda, ldb, (int64_t)M * K, (int64_t)K * N, (int64_t)M * N, tiles_m, tiles_n);
+        a, b, c, M, N, K, lda, ldb, (int64_t)M * K, (int64_t)K * N, (int64_t)M * N, tiles_m, tiles_n, batch);
     *status = ch::check_hip(hipGetLastError(), "gemm_bf16_tiled_kernel");
     return true;
 }

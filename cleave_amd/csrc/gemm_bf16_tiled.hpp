@@ -63,7 +63,7 @@ template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC
 __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC,
-    int tiles_m, int tiles_n) {
+    int tiles_m, int tiles_n, int batch) {
     using namespace ch::tiles;
     using P = Bf16Tiled<BM, BN, BK, WM, WN, STAGES, AKC, BKC, MI>;
     typedef float vacc __attribute__((ext_vector_type(MI == 32 ? 16 : 4)));
@@ -73,12 +73,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: keeps LDS/DMA bases scalar
     const int wm = wave / WN, wn = wave % WN;
-    int tm, tn;
-    ch::tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    int bt, tm, tn;  // product (batch entry or K-slice) and tile of this workgroup
+    ch::block_coords(blockIdx.x, tiles_m, tiles_n, batch, bt, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    A += (int64_t)blockIdx.y * strideA;
-    B += (int64_t)blockIdx.y * strideB;
-    C += (int64_t)blockIdx.y * strideC;
+    A += (int64_t)bt * strideA;
+    B += (int64_t)bt * strideB;
+    C += (int64_t)bt * strideC;
 
     TileCopy<AKC, BM, BK, NW> copy_a;
     TileCopy<BKC, BN, BK, NW> copy_b;

@@ -27,4 +27,27 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
     tn = in_group / gsize;
 }
 
+// Several products in one launch (a batch, or the K-slices of a split-K
+// product): a 1-D grid of T*batch workgroups, T = tiles_m*tiles_n.  When the
+// count divides by 8, XCD x takes the contiguous logical range
+// [x*W/8, (x+1)*W/8) of (product, tile) pairs, so a product's operands are
+// fetched into one or two L2s rather than all eight; inside a product the
+// tiles are walked as in tile_coords.
+__device__ __forceinline__ void block_coords(int bid, int tiles_m, int tiles_n, int batch, int& b,
+                                             int& tm, int& tn) {
+    const int T = tiles_m * tiles_n;
+    const int W = T * batch;
+    int g = bid;
+    if (W % kXcds == 0) g = (bid % kXcds) * (W / kXcds) + bid / kXcds;
+    b = g / T;
+    const int t = g - b * T;
+    const int per_group = kGroupM * tiles_n;
+    const int group = t / per_group;
+    const int first_m = group * kGroupM;
+    const int gsize = min(tiles_m - first_m, kGroupM);
+    const int in_group = t - group * per_group;
+    tm = first_m + in_group % gsize;
+    tn = in_group / gsize;
+}
+
 }  // namespace ch

@@ -232,9 +232,10 @@ bool launch_tiled(const float* a, const float* b, float* c, int M, int N, int K,
         (sB % 4))
         return false;
     const int tiles_m = M / BM, tiles_n = N / BN;
-    dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)batch);
+    if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
+    dim3 grid((unsigned)(tiles_m * tiles_n * batch));
     ch::gemm_f32_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
-        a, b, c, M, N, K, lda, ldb, sA, sB, sC, tiles_m, tiles_n, ch::MlpFuse{});
+        a, b, c, M, N, K, lda, ldb, sA, sB, sC, tiles_m, tiles_n, batch, ch::MlpFuse{});
     *status = ch::check_hip(hipGetLastError(), "gemm_f32_tiled_kernel");
     return true;
 }

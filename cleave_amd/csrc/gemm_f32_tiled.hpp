@@ -59,7 +59,7 @@ template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N,
     int K, int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC, int tiles_m,
-    int tiles_n, MlpFuse fuse) {
+    int tiles_n, int batch, MlpFuse fuse) {
     using namespace ch::tiles;
     using P = F32Tiled<BM, BN, BK, WM, WN, STAGES, AKC, BKC, MODE>;
     constexpr int FM = P::FM, FN = P::FN, NW = P::NW;
@@ -68,12 +68,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WN, wn = wave % WN;
-    int tm, tn;
-    ch::tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    int bt, tm, tn;  // product (batch entry or K-slice) and tile of this workgroup
+    ch::block_coords(blockIdx.x, tiles_m, tiles_n, batch, bt, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    A += (int64_t)blockIdx.y * strideA;
-    B += (int64_t)blockIdx.y * strideB;
-    C += (int64_t)blockIdx.y * strideC;
+    A += (int64_t)bt * strideA;
+    B += (int64_t)bt * strideB;
+    C += (int64_t)bt * strideC;
 
     TileCopy<AKC, BM, BK, NW, 4> copy_a;
     TileCopy<BKC, BN, BK, NW, 4> copy_b;
@@ -81,8 +81,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
     copy_b.init(ldb, n0, wave, lane);
     const int64_t step_a = copy_a.kstep(lda), step_b = copy_b.kstep(ldb);
     const uint32_t lds0 = lds_addr(smem);
-    // MODE 2: this split's d2 slice starts at batch row blockIdx.y * K.
-    const float* d2 = MODE == 2 ? fuse.d2 + (int64_t)blockIdx.y * K : nullptr;
+    // MODE 2: this split's d2 slice starts at batch row bt * K.
+    const float* d2 = MODE == 2 ? fuse.d2 + (int64_t)bt * K : nullptr;
     auto issue = [&](int kt, int stage) {
         const uint32_t dst = lds0 + (uint32_t)(stage * P::STAGE_BYTES);
         copy_a.issue(reinterpret_cast<const char*>(A) + kt * step_a, dst, wave);
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
             for (int j = 0; j < FN; ++j) {
                 float v = (dw2acc[j][0] + dw2acc[j][1]) + (dw2acc[j][2] + dw2acc[j][3]);
                 v += __shfl_xor(v, 32);
-                if (half == 0) fuse.dw2part[(int64_t)blockIdx.y * N + n0 + wn * P::TN + j * 32 + col] = v;
+                if (half == 0) fuse.dw2part[(int64_t)bt * N + n0 + wn * P::TN + j * 32 + col] = v;
             }
         }
     }

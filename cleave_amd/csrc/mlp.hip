@@ -209,8 +209,8 @@ int32_t fused_step(const float* x, const float* y, float* w1, float* w2, float* 
     f1.w2 = w2;
     f1.zpart = zpart;
     ch::gemm_f32_tiled_kernel<256, 256, 16, 2, 4, 2, true, false, 1>
-        <<<dim3((unsigned)((B / 256) * (Hd / 256)), 1), FusedTile1::THREADS, 0, st>>>(
-            x, w1, H, B, Hd, D, D, Hd, 0, 0, 0, B / 256, Hd / 256, f1);
+        <<<dim3((unsigned)((B / 256) * (Hd / 256))), FusedTile1::THREADS, 0, st>>>(
+            x, w1, H, B, Hd, D, D, Hd, 0, 0, 0, B / 256, Hd / 256, 1, f1);
     CH_LAUNCHED("gemm_f32_tiled_kernel(MODE 1)");
     row_finish_kernel<<<(B + kThreads - 1) / kThreads, kThreads, 0, st>>>(zpart, P, y, B, sq, d2);
     CH_LAUNCHED("row_finish_kernel");
@@ -222,9 +222,9 @@ int32_t fused_step(const float* x, const float* y, float* w1, float* w2, float* 
     f2.d2 = d2;
     f2.dw2part = part;
     ch::gemm_f32_tiled_kernel<256, 256, 16, 2, 4, 2, false, false, 2>
-        <<<dim3((unsigned)((D / 256) * (Hd / 256)), (unsigned)splits), FusedTile2::THREADS, 0, st>>>(
+        <<<dim3((unsigned)((D / 256) * (Hd / 256) * splits)), FusedTile2::THREADS, 0, st>>>(
             x, H, slices, D, Hd, kk, D, Hd, (int64_t)kk * D, (int64_t)kk * Hd, (int64_t)D * Hd, D / 256,
-            Hd / 256, f2);
+            Hd / 256, splits, f2);
     CH_LAUNCHED("gemm_f32_tiled_kernel(MODE 2)");
     sum_slices_sgd_kernel<<<capped_grid((int64_t)D * Hd), kThreads, 0, st>>>(slices, splits, (int64_t)D * Hd, dw1, w1, lr);
     CH_LAUNCHED("sum_slices_sgd_kernel(dW1)");
