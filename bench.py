@@ -31,7 +31,7 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense FP32 matrix
 PEAK_BF16_MFMA = 2516.6  # TFLOP/s, MI355X dense BF16 matrix
-PEAK_FP32_VALU_NOFMA = 39.3  # T ops/s: 256 CU x 64 lanes x 2.4 GHz, one op per lane-cycle
+PEAK_FP32_VALU_NOFMA = 78.6  # T op/s: MI355X FP32 vector peak 157.3 TFLOP/s counts an FMA as 2; one non-FMA op per lane-cycle is half
 PEAK_HBM = 8000.0  # GB/s
 
 
