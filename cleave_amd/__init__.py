@@ -9,6 +9,7 @@ program calls (/root/reference/stdlib/linalg/{tensor,matrix}.cleave,
     add/sub/mul/div/neg, zero        Ring<Tensor>            tensor.cleave:66-80
     relu/sigmoid/tanh                Activation<Tensor>      nn.cleave:82-95
     sum/mean/max_of                  Sum/Mean/Max            nn.cleave:111-149
+    index, index_bwd                 Index + its derivative  tensor.cleave:113-133
     escape_counts                    escape_count over a grid, examples/mandelbrot.cleave:14-26
     mlp_step                         SGD step, examples/xor_tensor.cleave:38-92 style
 
@@ -28,7 +29,7 @@ __all__ = [
     "CleaveHipError", "Tensor", "device_available", "init", "sync", "empty", "from_numpy",
     "matmul", "matmul_batched", "add", "sub", "mul", "div", "neg", "zero", "relu", "sigmoid",
     "tanh", "sigmoid_bwd", "tanh_bwd", "relu_bwd", "div_bwd", "sgd_update", "sum", "mean",
-    "max_of", "argmax", "sum_u64", "reduce_sum", "reduce_max", "reduce_sum_u64", "escape_counts", "mlp_step", "fill_uniform", "fill_normal",
+    "max_of", "argmax", "sum_u64", "index", "index_bwd", "reduce_sum", "reduce_max", "reduce_sum_u64", "escape_counts", "mlp_step", "fill_uniform", "fill_normal",
     "fill_bernoulli", "to_bf16", "Timer", "symbol_table",
 ]
 
@@ -267,6 +268,34 @@ def _checked_scalar(fn: str, t: Tensor):
     if code < 0:
         raise CleaveHipError(code, msg)
     return out
+
+
+# ---- Index<Tensor> (stdlib/linalg/tensor.cleave:113-133) -------------------------
+
+def _dims_idx(t: Tensor, idx):
+    dims = np.ascontiguousarray(t.shape, dtype=np.int32)
+    ix = np.ascontiguousarray(np.atleast_1d(np.asarray(idx)), dtype=np.int32)
+    return dims, ix
+
+
+def index(t: Tensor, idx) -> float:
+    """t[idx]: one index per dimension of t, row-major (Index::index)."""
+    _need(t, "f32", "index")
+    dims, ix = _dims_idx(t, idx)
+    v = load().cleave_hip_index_f32(t.ptr, t.size, dims.ctypes.data, dims.size, ix.ctypes.data, ix.size)
+    code, msg = _lib.last_error()
+    if code < 0:
+        raise CleaveHipError(code, msg)
+    return float(v)
+
+
+def index_bwd(g: float, dt: Tensor, idx) -> Tensor:
+    """Reverse mode of `derivative index(c, idx): index(d(c), idx)`: dt[idx] += g."""
+    _need(dt, "f32", "index_bwd")
+    dims, ix = _dims_idx(dt, idx)
+    call("cleave_hip_index_bwd_f32", float(g), dt.ptr, dt.size, dims.ctypes.data, dims.size,
+         ix.ctypes.data, ix.size)
+    return dt
 
 
 # ---- escape_count map ----------------------------------------------------------

@@ -84,6 +84,8 @@ SIGNATURES: dict[str, tuple] = {
     "cleave_hip_max_of_f32": (f32, [vp, i64]),
     "cleave_hip_argmax_f32": (i64, [vp, i64]),
     "cleave_hip_sum_u32_u64": (u64, [vp, i64]),
+    "cleave_hip_index_f32": (f32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_index_bwd_f32": (i32, [f32, vp, i64, vp, i64, vp, i64]),
     "cleave_hip_mandelbrot_u32": (i32, [vp, i64, i32, i32, f32, f32, f32, f32, i32]),
     "cleave_hip_mlp_step_f32": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64,
                                       vp, i32, i32, i32, f32]),

@@ -54,6 +54,8 @@ const cleave_hip_symbol kSymbols[] = {
     CH_SYM(cleave_hip_max_of_f32),
     CH_SYM(cleave_hip_argmax_f32),
     CH_SYM(cleave_hip_sum_u32_u64),
+    CH_SYM(cleave_hip_index_f32),
+    CH_SYM(cleave_hip_index_bwd_f32),
     CH_SYM(cleave_hip_mandelbrot_u32),
     CH_SYM(cleave_hip_mlp_step_f32),
 };

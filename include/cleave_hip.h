@@ -203,6 +203,21 @@ CLEAVE_HIP_API int64_t cleave_hip_argmax_f32(const float* x, int64_t len);
 CLEAVE_HIP_API uint64_t cleave_hip_sum_u32_u64(const uint32_t* x, int64_t len);
 
 /* ---------------------------------------------------------------------- */
+/* Index<Tensor> (stdlib/linalg/tensor.cleave:113-133)                      */
+/* ---------------------------------------------------------------------- */
+
+/* t[idx] of a row-major tensor with extents dims (tensor.extract).  dims and
+ * idx are host int32 arrays of equal length (an [i32; K] across an extern
+ * call); every index is checked against its extent and prod(dims) against
+ * len.  Returns the element (synchronises); NaN after an error. */
+CLEAVE_HIP_API float cleave_hip_index_f32(const float* t, int64_t len, const int32_t* dims, int64_t ndims,
+                                          const int32_t* idx, int64_t nidx);
+/* Reverse-mode form of `derivative index(c, idx): index(d(c), idx)`
+ * (tensor.cleave:126): dt[idx] += g on the library stream. */
+CLEAVE_HIP_API int32_t cleave_hip_index_bwd_f32(float g, float* dt, int64_t len, const int32_t* dims,
+                                                int64_t ndims, const int32_t* idx, int64_t nidx);
+
+/* ---------------------------------------------------------------------- */
 /* escape_count map (examples/mandelbrot.cleave:14-26) in f32                */
 /* ---------------------------------------------------------------------- */
 

@@ -134,3 +134,30 @@ def test_product_package_does_not_reach_the_oracle():
     out = subprocess.run(["ldd", str(ROOT / "cleave_amd" / "libcleave_hip.so")], capture_output=True,
                          text=True).stdout
     assert "oracle" not in out
+
+
+def test_index_bounds_and_rank_are_checked_on_the_host():
+    # Index<Tensor>::index (stdlib/linalg/tensor.cleave:113-133): a bad index
+    # is an argument error before any device work, so a placeholder (never
+    # dereferenced) device pointer is enough here.
+    import numpy as np
+
+    from cleave_amd import _lib
+
+    lib = _lib.load()
+    fake = 4096
+    dims = np.array([2, 3], np.int32)
+    cases = [
+        (np.array([1, 3], np.int32), 6, "out of range"),
+        (np.array([-1, 0], np.int32), 6, "out of range"),
+        (np.array([1], np.int32), 6, "indices for a rank-2"),
+        (np.array([1, 1], np.int32), 7, "dims describe 6 elements"),
+    ]
+    for idx, length, needle in cases:
+        st = lib.cleave_hip_index_bwd_f32(1.0, fake, length, dims.ctypes.data, dims.size,
+                                          idx.ctypes.data, idx.size)
+        code, msg = _lib.last_error()
+        assert st == _lib.ERR_ARG and needle in msg, (idx, msg)
+        v = lib.cleave_hip_index_f32(fake, length, dims.ctypes.data, dims.size, idx.ctypes.data, idx.size)
+        code, msg = _lib.last_error()
+        assert v != v and code == _lib.ERR_ARG and needle in msg, (idx, msg)

@@ -116,3 +116,27 @@ def test_hbm_sized_map(hip, oracle):
     assert rel_close(Y[-5:], oracle.sigmoid(X[-5:]), 1e-5)
     z = hip.add(x, y).numpy()
     assert np.array_equal(z[idx], X[idx] + Y[idx]) and np.array_equal(z[-5:], X[-5:] + Y[-5:])
+
+
+def test_index_reads_row_major_elements(hip):
+    # Index::index over a rank-3 tensor (tensor.extract, row-major flattening)
+    rng = np.random.default_rng(21)
+    T = rng.standard_normal((3, 4, 5)).astype(np.float32)
+    t = hip.from_numpy(T)
+    for idx in [(0, 0, 0), (2, 3, 4), (1, 2, 3), (0, 3, 1), (2, 0, 4)]:
+        assert hip.index(t, idx) == T[idx]
+    with pytest.raises(hip.CleaveHipError):
+        hip.index(t, (3, 0, 0))
+
+
+def test_index_bwd_is_the_reverse_of_the_index_rule(hip):
+    # derivative index(c, idx): index(d(c), idx) -> dL/dc = g at idx, 0 elsewhere;
+    # repeated reads of one element accumulate
+    dt = hip.zero((4, 6))
+    hip.index_bwd(2.5, dt, (1, 2))
+    hip.index_bwd(0.5, dt, (1, 2))
+    hip.index_bwd(-1.0, dt, (3, 5))
+    want = np.zeros((4, 6), np.float32)
+    want[1, 2] = 3.0
+    want[3, 5] = -1.0
+    assert np.array_equal(dt.numpy(), want)
