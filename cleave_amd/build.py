@@ -11,10 +11,15 @@ Flags:
   -target-feature -packed-fp32-ops
                                  keep the compiler from emitting packed FP32 ops
   -fvisibility=hidden            only the extern "C" ABI (marked default) is exported
+
+Every compile also asks for the kernel resource report; a kernel that uses
+scratch memory (private arrays or register spills, a silent 10x slowdown for
+the GEMMs) fails the build.
 """
 from __future__ import annotations
 
 import os
+import re
 import subprocess
 import sys
 from concurrent.futures import ThreadPoolExecutor
@@ -42,14 +47,37 @@ SOURCES = ["runtime.hip", "gemm_f32.hip", "gemm_bf16.hip", "elementwise.hip", "r
            "mandelbrot.hip", "mlp.hip", "index.hip", "symbols.cpp"]
 
 
+REPORT = "-Rpass-analysis=kernel-resource-usage"
+
+
+def scratch_users(text: str) -> list[str]:
+    """Kernels with a non-zero ScratchSize in a kernel-resource-usage report."""
+    bad, name = [], None
+    for line in text.splitlines():
+        m = re.search(r"remark:\s+Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+        m = re.search(r"remark:\s+ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and int(m.group(1)) > 0:
+            bad.append(f"{name}: {m.group(1)} bytes/lane")
+    return bad
+
+
 def _run(cmd: list[str]) -> None:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(" ".join(cmd) + "\n" + r.stdout + r.stderr)
         raise RuntimeError(f"build step failed: {cmd[-1]}")
-    # The host pass does not know the packed-fp32 target feature; drop that noise.
-    noise = "'-packed-fp32-ops' is not a recognized feature"
-    msgs = [l for l in (r.stdout + r.stderr).splitlines() if noise not in l and l.strip()]
+    out = r.stdout + r.stderr
+    bad = scratch_users(out)
+    if bad:
+        raise RuntimeError("kernels use scratch memory (spills or private arrays):\n  " + "\n  ".join(bad))
+    # The host pass does not know the packed-fp32 target feature; drop that
+    # noise and the resource report itself.
+    noise = ("'-packed-fp32-ops' is not a recognized feature", "remark:", "kernel-resource-usage",
+             "In file included from", "|", "^")
+    msgs = [l for l in out.splitlines() if l.strip() and not any(n in l for n in noise)
+            and not l.strip()[:1].isdigit()]
     if msgs:
         sys.stderr.write("\n".join(msgs) + "\n")
 
@@ -60,7 +88,8 @@ def build_library(jobs: int = 8) -> Path:
     def compile_one(src: str) -> Path:
         obj = BUILD / (src.rsplit(".", 1)[0] + ".o")
         lang = ["-x", "hip"] if src.endswith(".hip") else []
-        _run([HIPCC, *HIP_FLAGS, *lang, "-c", str(CSRC / src), "-o", str(obj)])
+        report = [REPORT] if src.endswith(".hip") else []
+        _run([HIPCC, *HIP_FLAGS, *report, *lang, "-c", str(CSRC / src), "-o", str(obj)])
         return obj
 
     with ThreadPoolExecutor(max_workers=jobs) as ex:
