@@ -225,8 +225,11 @@ template <bool TA, bool TB>
 int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch) {
     int32_t st = CLEAVE_HIP_OK;
     // 256 x 256 x 64 tile, 8 waves of 128 x 64 in 16 x 16 x 32 MFMAs, two LDS
-    // stages (128 KiB)
-    if (launch_tiled<256, 256, 64, 2, 4, 2, 16, TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
+    // stages (128 KiB), when that still gives every CU a tile
+    const int64_t big_tiles = (int64_t)(M / 256) * (N / 256) * batch;
+    if (big_tiles >= ch::num_cus() &&
+        launch_tiled<256, 256, 64, 2, 4, 2, 16, TA, TB>(a, b, c, M, N, K, batch, &st))
+        return st;
     // 128 x 128 x 64 tile, 4 waves of 64 x 64 in 32 x 32 x 16 MFMAs, three
     // LDS stages (96 KiB)
     if (launch_tiled<128, 128, 64, 2, 2, 3, 32, TA, TB>(a, b, c, M, N, K, batch, &st)) return st;

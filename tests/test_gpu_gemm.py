@@ -205,3 +205,24 @@ def test_config5_batched_bf16_64x512(hip, oracle):
     Bu = oracle.bf16_to_f32(B[5]).reshape(n, n)
     ref = oracle.matmul(Au, Bu, threads=16)
     assert_gemm_close(C[5], ref, np.abs(Au).astype(np.float64) @ np.abs(Bu).astype(np.float64), n, "batch 5 full")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_big_tile_path_every_layout(hip, oracle, dtype, ta, tb):
+    # 4096 x 4096 outputs give the 256 x 256 tiled kernels a tile per CU, so
+    # every layout of that path runs here; a short K keeps the oracle cheap
+    M = N = 4096
+    K = 128
+    a32 = hip.fill_normal(hip.empty((K, M) if ta else (M, K)), seed=61 + 2 * ta + tb)
+    b32 = hip.fill_normal(hip.empty((N, K) if tb else (K, N)), seed=71 + 2 * ta + tb)
+    if dtype == "bf16":
+        a, b = hip.to_bf16(a32), hip.to_bf16(b32)
+    else:
+        a, b = a32, b32
+    c = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    A, B = a.numpy(), b.numpy()
+    ii, jj = sample_entries(M, N, 1024, seed=5 + ta + 2 * tb)
+    ref, absden = oracle.matmul_entries(A, B, M, N, K, ii, jj, trans_a=bool(ta), trans_b=bool(tb),
+                                        bf16=(dtype == "bf16"))
+    assert_gemm_close(c[ii, jj], ref, absden, K, f"{dtype} big tile ta={ta} tb={tb}")
