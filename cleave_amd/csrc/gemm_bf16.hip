@@ -1,9 +1,9 @@
 // gemm_bf16.hip -- bf16-input / fp32-accumulate matmul on CDNA4 matrix cores
 // (v_mfma_f32_32x32x16_bf16), plus its batched form.
 //
-// Shapes that divide a 256 x 256 x 64 (or 128 x 128 x 64) tile run the
-// large-tile kernel of gemm_bf16_tiled.hpp (v_mfma_f32_16x16x32_bf16 for the
-// big tile) (LDS filled by global_load_lds,
+// Shapes that divide a 256 x 256 x 32 tile run the ping-pong kernel of
+// gemm_bf16_pingpong.hpp; 128 x 128 x 64 tiles run the large-tile kernel of
+// gemm_bf16_tiled.hpp (LDS filled by global_load_lds,
 // transposing LDS reads for m/n-contiguous operands).  Everything else runs
 // the general kernel below, which guards every access.
 //
@@ -18,6 +18,7 @@
 // contiguous along m/n is read as 8(k) x 2(m/n) blocks of 4-byte words and
 // transposed in registers before a pair of 16-byte LDS stores.
 #include "common.hpp"
+#include "gemm_bf16_pingpong.hpp"
 #include "gemm_bf16_tiled.hpp"
 #include "gemm_common.hpp"
 
@@ -221,15 +222,32 @@ bool launch_tiled(const uint16_t* a, const uint16_t* b, float* c, int M, int N, 
     return true;
 }
 
+// Ping-pong kernel (gemm_bf16_pingpong.hpp): 256 x 256 x 32 tiles.
+template <bool TA, bool TB>
+bool launch_pingpong(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
+                     int32_t* status) {
+    using P = ch::Bf16PingPong<!TA, TB>;
+    const int64_t lda = TA ? M : K, ldb = TB ? K : N;
+    if (!P::fits(M, N, K, lda, ldb) || ((uintptr_t)a & 15) || ((uintptr_t)b & 15)) return false;
+    const int tiles_m = M / P::BM, tiles_n = N / P::BN;
+    if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
+    dim3 grid((unsigned)(tiles_m * tiles_n * batch));
+    ch::gemm_bf16_pingpong_kernel<!TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
+        a, b, c, M, N, K, lda, ldb, (int64_t)M * K, (int64_t)K * N, (int64_t)M * N, tiles_m, tiles_n, batch);
+    *status = ch::check_hip(hipGetLastError(), "gemm_bf16_pingpong_kernel");
+    return true;
+}
+
 template <bool TA, bool TB>
 int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch) {
     int32_t st = CLEAVE_HIP_OK;
-    // 256 x 256 x 64 tile, 8 waves of 128 x 64 in 16 x 16 x 32 MFMAs, two LDS
-    // stages (128 KiB), when that still gives every CU a tile
+    // 256 x 256 tiles, when that still gives every CU a tile: the ping-pong
+    // kernel (k-tiles of 32), else the tiled kernel (k-tiles of 64)
     const int64_t big_tiles = (int64_t)(M / 256) * (N / 256) * batch;
-    if (big_tiles >= ch::num_cus() &&
-        launch_tiled<256, 256, 64, 2, 4, 2, 16, TA, TB>(a, b, c, M, N, K, batch, &st))
-        return st;
+    if (big_tiles >= ch::num_cus()) {
+        if (launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
+        if (launch_tiled<256, 256, 64, 2, 4, 2, 16, TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
+    }
     // 128 x 128 x 64 tile, 4 waves of 64 x 64 in 32 x 32 x 16 MFMAs, three
     // LDS stages (96 KiB)
     if (launch_tiled<128, 128, 64, 2, 2, 3, 32, TA, TB>(a, b, c, M, N, K, batch, &st)) return st;

@@ -1,0 +1,160 @@
+// gemm_bf16_pingpong.hpp -- bf16 GEMM with a ping-pong schedule of its two
+// wave groups (gfx950, v_mfma_f32_16x16x32_bf16, 256 x 256 x 32 tiles).
+//
+// Eight waves; each owns a 128 x 64 block of C (8 x 4 tiles of 16 x 16).
+// Waves 0-3 (group 0, rows 0-127 of the tile) and 4-7 (group 1, rows
+// 128-255) sit one per SIMD, and the two groups alternate between
+//   C phase: the k-step's 32 MFMAs back to back, operands already in
+//            registers, at raised wave priority;
+//   M phase: read the next k-step's fragments from LDS, issue this wave's
+//            share of the global -> LDS copy three k-tiles ahead, wait for
+//            its own copy of the next k-tile and for the fragment reads.
+// A workgroup barrier closes every phase, and group 1 runs one phase behind
+// group 0, so on every SIMD one wave feeds the matrix core while the other
+// moves data.  k-tiles are 32 deep (one MFMA k-step) in a ring of 4 LDS
+// buffers (128 KiB); the copy of tile u+3 goes into the buffer of tile u-1,
+// which both groups finished reading a phase earlier.
+//
+// Group 0: M(0) in the prologue, then per k-step s: C(s) | M(s+1).
+// Group 1: per k-step s: M(s) | C(s).  A barrier ends every phase.
+#pragma once
+
+#include "gemm_common.hpp"
+#include "gemm_tiles.hpp"
+
+namespace ch {
+
+template <bool AKC, bool BKC>
+struct Bf16PingPong {
+    static constexpr int BM = 256, BN = 256, BK = 32, NW = 8, WN = 4, THREADS = 64 * NW;
+    static constexpr int TM = 128, TN = 64, FM = TM / 16, FN = TN / 16, STAGES = 4;
+    static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
+    static constexpr int STAGE_BYTES = A_BYTES + B_BYTES, LDS_BYTES = STAGES * STAGE_BYTES;
+    static constexpr int LPW = STAGE_BYTES / 1024 / NW;  // copy instructions per wave per k-tile
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS per workgroup");
+
+    static bool fits(int M, int N, int K, int64_t lda, int64_t ldb) {
+        const bool dims = M % BM == 0 && N % BN == 0 && K % BK == 0 && lda % 8 == 0 && ldb % 8 == 0;
+        const uint64_t a_span = (AKC ? (uint64_t)M : (uint64_t)BK + 1) * (uint64_t)lda * 2;
+        const uint64_t b_span = (BKC ? (uint64_t)N : (uint64_t)BK + 1) * (uint64_t)ldb * 2;
+        return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
+    }
+};
+
+template <bool AKC, bool BKC, bool PRIO = true>
+__global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, float* __restrict__ C, int M,
+    int N, int K, int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC,
+    int tiles_m, int tiles_n, int batch) {
+    using namespace ch::tiles;
+    using P = Bf16PingPong<AKC, BKC>;
+    constexpr int FM = P::FM, FN = P::FN, NW = P::NW, BK = P::BK, LPW = P::LPW;
+    __shared__ __attribute__((aligned(1024))) char smem[P::LDS_BYTES];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = wave / P::WN, wn = wave % P::WN;  // grp is also the wave's row block
+    int bt, tm, tn;
+    ch::block_coords(blockIdx.x, tiles_m, tiles_n, batch, bt, tm, tn);
+    const int m0 = tm * P::BM, n0 = tn * P::BN;
+    A += (int64_t)bt * strideA;
+    B += (int64_t)bt * strideB;
+    C += (int64_t)bt * strideC;
+
+    TileCopy<AKC, P::BM, BK, NW> copy_a;
+    TileCopy<BKC, P::BN, BK, NW> copy_b;
+    copy_a.init(lda, m0, wave, lane);
+    copy_b.init(ldb, n0, wave, lane);
+    const int64_t step_a = copy_a.kstep(lda), step_b = copy_b.kstep(ldb);
+    const uint32_t lds0 = lds_addr(smem);
+    const int nk = K / BK;
+    auto issue = [&](int kt) {
+        const uint32_t dst = lds0 + (uint32_t)((kt % P::STAGES) * P::STAGE_BYTES);
+        copy_a.issue(reinterpret_cast<const char*>(A) + kt * step_a, dst, wave);
+        copy_b.issue(reinterpret_cast<const char*>(B) + kt * step_b, dst + P::A_BYTES, wave);
+    };
+
+    v4f acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = v4f{};
+    v8bf fa[FM], fb[FN];
+
+    // M phase for k-step u: fragments of tile u; copy of tile u+3; then wait
+    // for this wave's copy of tile u+1 (tiles u+2, u+3 may stay in flight)
+    // and for the fragment reads.
+    auto m_phase = [&](int u) {
+        const char* tile = smem + (u % P::STAGES) * P::STAGE_BYTES;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) fa[i] = read_frag16<AKC, P::BM, BK>(tile, grp * P::TM + i * 16, 0, lane);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+            fb[j] = read_frag16<BKC, P::BN, BK>(tile + P::A_BYTES, wn * P::TN + j * 16, 0, lane);
+        if (u + 3 < nk) {
+            issue(u + 3);
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * LPW) : "memory");
+        } else if (u + 2 < nk) {
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(LPW) : "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        }
+    };
+    auto c_phase = [&]() {
+        if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
+    };
+
+    // Prologue: tiles 0..2 in flight; tile 0 landed everywhere; group 0 reads
+    // k-step 0 (and issues tile 3) so it can compute in phase 0.
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+        if (t < nk) issue(t);
+    if (nk >= 3) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LPW) : "memory");
+    } else if (nk == 2) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory");
+    } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    asm volatile("s_barrier" ::: "memory");
+    if (grp == 0) m_phase(0);
+    asm volatile("s_barrier" ::: "memory");
+
+    // Each group runs a loop of fixed shape (no phase-dependent branches, so
+    // the fragment registers stay put); both execute 2*nk barriers.
+    if (grp == 0) {
+        for (int s = 0; s < nk; ++s) {
+            c_phase();
+            asm volatile("s_barrier" ::: "memory");
+            if (s + 1 < nk) m_phase(s + 1);
+            asm volatile("s_barrier" ::: "memory");
+        }
+    } else {
+        for (int s = 0; s < nk; ++s) {
+            m_phase(s);
+            asm volatile("s_barrier" ::: "memory");
+            c_phase();
+            asm volatile("s_barrier" ::: "memory");
+        }
+    }
+
+    // 16 x 16 accumulator layout: lane holds column l%16, rows 4*(l/16) + v.
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int r = m0 + grp * P::TM + i * 16 + 4 * (lane >> 4) + v;
+                const int c = n0 + wn * P::TN + j * 16 + (lane & 15);
+                C[(int64_t)r * N + c] = acc[i][j][v];
+            }
+}
+
+}  // namespace ch
