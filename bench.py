@@ -22,6 +22,7 @@ import argparse
 import json
 import os
 import platform
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -61,6 +62,63 @@ def timed(ca, fn, steps, warmup, warm_s=0.0):
     ca.sync()
     wall = time.perf_counter() - w0
     return wall, ev_ms / steps
+
+
+def vendor_yardstick(steps):
+    """torch.matmul / torch.bmm (hipBLASLt or rocBLAS underneath) on the bench's
+    GEMM shapes and data distributions, timed the same way on the same device.
+    bf16 matrix-core throughput is power-limited and differs from chip to chip,
+    so a vendor figure from the same box is the fair reference point.  The
+    vendor bf16 products write bf16 C (half the bytes of this library's f32 C).
+    Runs in a process of its own: torch brings its own HIP runtime, which sees
+    no device once this library's runtime holds it in the same process."""
+    import torch
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    out = {}
+
+    def run(name, fn, flop, warm_s):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < warm_s:
+            for _ in range(4):
+                fn()
+            torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        out[name] = {"kernel_ms": round(ms, 4), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1)}
+        log(f"vendor {name}: {out[name]['TFLOP/s']} TFLOP/s")
+
+    n = 4096
+    a = torch.randn(n, n, device=dev, generator=g)
+    b = torch.randn(n, n, device=dev, generator=g)
+    c = torch.empty(n, n, device=dev)
+    run("gemm_f32_nn_4096", lambda: torch.matmul(a, b, out=c), 2.0 * n ** 3, 0.3)
+    del a, b, c
+    m = 8192
+    ab = (torch.randn(m, m, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    bb = (torch.randn(m, m, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    cb = torch.empty(m, m, device=dev, dtype=torch.bfloat16)
+    run("gemm_bf16_8192", lambda: torch.matmul(ab, bb, out=cb), 2.0 * m ** 3, 0.4)
+    del ab, bb, cb
+    bs, k = 64, 512
+    x = (torch.randn(bs, k, k, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    y = (torch.randn(bs, k, k, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    z = torch.empty(bs, k, k, device=dev, dtype=torch.bfloat16)
+    run("gemm_bf16_batched_64x512", lambda: torch.bmm(x, y, out=z), 2.0 * bs * k ** 3, 0.3)
+    del x, y, z
+    torch.cuda.synchronize()
+    return out
 
 
 def read_traffic(name):
@@ -134,6 +192,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--vendor", action="store_true",
+                    help="also time torch.matmul (hipBLASLt) on the GEMM shapes, same device")
+    ap.add_argument("--vendor-only", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run the copy kernel used to scale rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
@@ -141,6 +202,9 @@ def main():
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); multi-GPU runs are "
               "out of scope for this build", file=sys.stderr)
         sys.exit(2)
+    if args.vendor_only:
+        print(json.dumps(vendor_yardstick(max(20, args.steps // 2))), flush=True)
+        return
 
     import numpy as np
 
@@ -302,6 +366,13 @@ def main():
         del hx, hy
     if secondary:
         result["secondary"] = secondary
+    if args.vendor:
+        # a child process (not an exec): see vendor_yardstick
+        proc = subprocess.run([sys.executable, os.path.abspath(__file__), "--vendor-only", "--steps", str(steps)],
+                              stdout=subprocess.PIPE, timeout=600)
+        if proc.returncode != 0:
+            raise RuntimeError(f"vendor yardstick child failed with status {proc.returncode}")
+        result["vendor_same_device"] = json.loads(proc.stdout.decode().strip().splitlines()[-1])
 
     if not args.no_cpu:
         log(f"cpu baseline: ~{args.cpu_budget:.0f} s of the restated loop on one core")

@@ -11,9 +11,9 @@
 //            its own copy of the next k-tile and for the fragment reads.
 // A workgroup barrier closes every phase, and group 1 runs one phase behind
 // group 0, so on every SIMD one wave feeds the matrix core while the other
-// moves data.  k-tiles are 32 deep (one MFMA k-step) in a ring of 4 LDS
-// buffers (128 KiB); the copy of tile u+3 goes into the buffer of tile u-1,
-// which both groups finished reading a phase earlier.
+// moves data.  k-tiles are 32 deep (one MFMA k-step) in a ring of S = 4 or
+// 5 LDS buffers (32 KiB each); the copy of tile u+S-1 goes into the buffer of
+// tile u-1, which both groups finished reading a phase earlier.
 //
 // Group 0: M(0) in the prologue, then per k-step s: C(s) | M(s+1).
 // Group 1: per k-step s: M(s) | C(s).  A barrier ends every phase.
@@ -24,10 +24,11 @@
 
 namespace ch {
 
-template <bool AKC, bool BKC>
+template <bool AKC, bool BKC, int STAGES_ = 4>
 struct Bf16PingPong {
     static constexpr int BM = 256, BN = 256, BK = 32, NW = 8, WN = 4, THREADS = 64 * NW;
-    static constexpr int TM = 128, TN = 64, FM = TM / 16, FN = TN / 16, STAGES = 4;
+    static constexpr int TM = 128, TN = 64, FM = TM / 16, FN = TN / 16, STAGES = STAGES_;
+    static_assert(STAGES == 4 || STAGES == 5, "ring depth");
     static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
     static constexpr int STAGE_BYTES = A_BYTES + B_BYTES, LDS_BYTES = STAGES * STAGE_BYTES;
     static constexpr int LPW = STAGE_BYTES / 1024 / NW;  // copy instructions per wave per k-tile
@@ -41,14 +42,23 @@ struct Bf16PingPong {
     }
 };
 
-template <bool AKC, bool BKC, bool PRIO = true>
+// s_waitcnt vmcnt(n * LPW) lgkmcnt(0) for a runtime tile count n in 0..3.
+template <int LPW>
+__device__ __forceinline__ void wait_tiles(int n) {
+    if (n >= 3) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(3 * LPW) : "memory");
+    else if (n == 2) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * LPW) : "memory");
+    else if (n == 1) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(LPW) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+}
+
+template <bool AKC, bool BKC, bool PRIO = true, int STAGES_ = 4>
 __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC,
     int tiles_m, int tiles_n, int batch) {
     using namespace ch::tiles;
-    using P = Bf16PingPong<AKC, BKC>;
-    constexpr int FM = P::FM, FN = P::FN, NW = P::NW, BK = P::BK, LPW = P::LPW;
+    using P = Bf16PingPong<AKC, BKC, STAGES_>;
+    constexpr int FM = P::FM, FN = P::FN, NW = P::NW, BK = P::BK, LPW = P::LPW, S = P::STAGES;
     __shared__ __attribute__((aligned(1024))) char smem[P::LDS_BYTES];
 
     const int lane = threadIdx.x & 63;
@@ -69,7 +79,7 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
     const uint32_t lds0 = lds_addr(smem);
     const int nk = K / BK;
     auto issue = [&](int kt) {
-        const uint32_t dst = lds0 + (uint32_t)((kt % P::STAGES) * P::STAGE_BYTES);
+        const uint32_t dst = lds0 + (uint32_t)((kt % S) * P::STAGE_BYTES);
         copy_a.issue(reinterpret_cast<const char*>(A) + kt * step_a, dst, wave);
         copy_b.issue(reinterpret_cast<const char*>(B) + kt * step_b, dst + P::A_BYTES, wave);
     };
@@ -81,24 +91,20 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
         for (int j = 0; j < FN; ++j) acc[i][j] = v4f{};
     v8bf fa[FM], fb[FN];
 
-    // M phase for k-step u: fragments of tile u; copy of tile u+3; then wait
-    // for this wave's copy of tile u+1 (tiles u+2, u+3 may stay in flight)
-    // and for the fragment reads.
+    // M phase for k-step u: fragments of tile u; copy of tile u+S-1 (into
+    // the buffer of tile u-1); then wait for this wave's copy of tile u+1
+    // (the later tiles issued so far may stay in flight) and for the reads.
     auto m_phase = [&](int u) {
-        const char* tile = smem + (u % P::STAGES) * P::STAGE_BYTES;
+        const char* tile = smem + (u % S) * P::STAGE_BYTES;
 #pragma unroll
         for (int i = 0; i < FM; ++i) fa[i] = read_frag16<AKC, P::BM, BK>(tile, grp * P::TM + i * 16, 0, lane);
 #pragma unroll
         for (int j = 0; j < FN; ++j)
             fb[j] = read_frag16<BKC, P::BN, BK>(tile + P::A_BYTES, wn * P::TN + j * 16, 0, lane);
-        if (u + 3 < nk) {
-            issue(u + 3);
-            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * LPW) : "memory");
-        } else if (u + 2 < nk) {
-            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(LPW) : "memory");
-        } else {
-            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-        }
+        if (u + S - 1 < nk) issue(u + S - 1);
+        // tiles issued after u+1: u+2 .. min(u+S-1, nk-1)
+        const int later = min(u + S - 1, nk - 1) - (u + 1);
+        wait_tiles<LPW>(later < 0 ? 0 : later);
     };
     auto c_phase = [&]() {
         if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
@@ -110,17 +116,14 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
         if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     };
 
-    // Prologue: tiles 0..2 in flight; tile 0 landed everywhere; group 0 reads
-    // k-step 0 (and issues tile 3) so it can compute in phase 0.
+    // Prologue: tiles 0..S-2 in flight; tile 0 landed everywhere; group 0
+    // reads k-step 0 (and issues tile S-1) so it can compute in phase 0.
 #pragma unroll
-    for (int t = 0; t < 3; ++t)
+    for (int t = 0; t < S - 1; ++t)
         if (t < nk) issue(t);
-    if (nk >= 3) {
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LPW) : "memory");
-    } else if (nk == 2) {
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory");
-    } else {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    {
+        const int later = min(S - 2, nk - 1);  // tiles issued after tile 0
+        wait_tiles<LPW>(later);
     }
     asm volatile("s_barrier" ::: "memory");
     if (grp == 0) m_phase(0);

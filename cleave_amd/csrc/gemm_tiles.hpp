@@ -9,21 +9,25 @@
 //
 //   KC ("k-contiguous", A stored M x K or B stored N x K):
 //     LDS tile [R rows][BK], row pitch 2*BK bytes, CPR = BK/8 chunks per row.
-//     Chunk c of row r is stored in slot c ^ kc_swizzle(r).  The MFMA operand
-//     read (ds_read_b128) has 16 lanes read rows r0..r0+15 at one logical
-//     chunk; the swizzle spreads them over all banks whether the LDS serves
-//     8 or 16 lanes of a 16-byte read per cycle.
+//     Chunk c of row r is stored in slot kc_slot(r, c).  The MFMA operand
+//     read (ds_read_b128) has 16 or 32 lanes read consecutive rows at one
+//     logical chunk; the swizzle spreads the rows that share LDS banks.
 //
 //   MN ("m/n-contiguous", A stored K x M or B stored K x N):
 //     LDS tile [BK][R], row pitch 2*R bytes, 16-byte chunk c of k-row kr in
-//     slot c ^ (2*(kr & 3)) (pairs of chunks move together).  The operand is
-//     read with ds_read_b64_tr_b16: within each 16-lane group, result lane i,
-//     element j = the element (i % 4) of source lane 4*j + i/4.  Source lane
-//     (4*j + q) points at k-row kb + j, columns c0 + 4q .. c0 + 4q + 3, so
-//     result lane i receives column c0 + i at k-rows kb .. kb + 3 -- exactly
-//     the k-contiguous register layout the MFMA wants, with no register
-//     shuffles.  A 16-lane group touches 4 k-rows x 32 bytes in 4 distinct
-//     32-byte bank groups.
+//     slot mn_slot(kr, c).  The operand is read with ds_read_b64_tr_b16:
+//     within each 16-lane group, result lane i, element j = the element
+//     (i % 4) of source lane 4*j + i/4.  Source lane (4*j + q) points at
+//     k-row kb + j, columns c0 + 4q .. c0 + 4q + 3, so result lane i receives
+//     column c0 + i at k-rows kb .. kb + 3 -- exactly the k-contiguous
+//     register layout the MFMA wants, with no register shuffles.
+//
+// LDS banks (gfx950, measured with the SQ_LDS_BANK_CONFLICT counter):
+// ds_read_b64 and ds_read_b64_tr_b16 serve 32 lanes per cycle from 64 banks
+// of 4 bytes, so the 32 lanes of a half-wave must cover 256 distinct bytes
+// modulo 256.  ds_read_b128 takes 4 cycles per wave when conflict-free; a
+// half-wave reading 16 B from rows 512 B apart pays a second pass.  Every
+// swizzle below was checked pattern by pattern against that counter.
 //
 // v_mfma_f32_32x32x16_bf16 operand layout: lane l holds 8 bf16 of row
 // (l % 32) at k = 8*(l / 32) .. +7 (both A and B, B indexed by column);
@@ -43,23 +47,31 @@ typedef short v4s __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4s lds_v4s;
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Slot of logical chunk c in KC row r (CPR chunks per row).
-template <int CPR>
+// Slot of logical chunk c in KC row r (CPR chunks per row, ESZ-byte elements).
+//   bf16, 4 chunks (BK = 32): the 16 x 16 x 32 read has a half-wave read rows
+//     r0..r0+15 at chunks c, c+1; rows r and r+8 share banks, so bit 3 of the
+//     row moves them two chunks apart (bit 4 does the same for the 32-row read).
+//   bf16, 8 chunks (BK = 64) and f32: the 32-row read of the 32 x 32 MFMAs.
+template <int CPR, int ESZ>
 __device__ __forceinline__ int kc_slot(int r, int c) {
     static_assert(CPR == 4 || CPR == 8, "KC rows hold 4 or 8 chunks");
     if constexpr (CPR == 8) return c ^ ((r & 7) ^ ((r >> 3) & 1));
+    else if constexpr (ESZ == 2) return c ^ (((r >> 3) & 1) << 1) ^ ((r >> 4) & 1);
     else return c ^ (((r >> 1) & 3) ^ ((r >> 3) & 1));
 }
 // Slot of chunk c in MN k-row kr, for the two MN read instructions:
-//   bf16, ds_read_b64_tr_b16: 16-lane groups read 4 consecutive k-rows x 32 B;
-//     XOR-ing chunk pairs with kr & 3 spreads the 4 rows over 4 bank groups.
+//   bf16, ds_read_b64_tr_b16: a half-wave reads either 4 k-rows x 64 B
+//     (32 x 32 x 16 operand) or k-rows kb..kb+3 and kb+8..kb+11 x 32 B
+//     (16 x 16 x 32 operand).  XOR-ing 64 B blocks with kr & 3 separates the
+//     4 rows of the first; flipping 32 B on bit 3 of kr separates the two row
+//     quads of the second.  Needs 16 chunks (256 B) per k-row.
 //   f32, ds_read_b32: the two half-waves read k-rows kr and kr + 4 at the same
 //     128 B of columns; flipping 128 B on (kr >> 2) & 1 puts them in opposite
 //     bank halves.
 template <int ESZ>
 __device__ __forceinline__ int mn_slot(int kr, int c) {
     static_assert(ESZ == 2 || ESZ == 4, "bf16 or f32 operands");
-    if constexpr (ESZ == 2) return c ^ ((kr & 3) << 1);
+    if constexpr (ESZ == 2) return c ^ ((kr & 3) << 2) ^ (((kr >> 3) & 1) << 1);
     else return c ^ (((kr >> 2) & 1) << 3);
 }
 
@@ -100,12 +112,12 @@ struct TileCopy {
             for (int j = 0; j < PER_WAVE; ++j) {
                 const int q = wave + NW * j;
                 const int r = q * RPI + lane / CPR;
-                const int c = kc_slot<CPR>(r, lane % CPR);  // slot lane%CPR holds chunk c
+                const int c = kc_slot<CPR, ESZ>(r, lane % CPR);  // slot lane%CPR holds chunk c
                 voff[j] = (uint32_t)(((int64_t)(r0 + r) * ld + EPC * c) * ESZ);
             }
         } else {
             constexpr int CPR = R / EPC, KPI = 64 / CPR;
-            static_assert(CPR >= (ESZ == 2 ? 8 : 16) && 64 % CPR == 0, "MN row too narrow for its swizzle");
+            static_assert(CPR >= 16 && 64 % CPR == 0, "MN row too narrow for its swizzle");
 #pragma unroll
             for (int j = 0; j < PER_WAVE; ++j) {
                 const int q = wave + NW * j;
@@ -133,7 +145,7 @@ __device__ __forceinline__ v8bf read_frag(const char* tile, int row0, int kk, in
         constexpr int CPR = BK / 8;
         const int r = row0 + (lane & 31);
         const int c = 2 * kk + (lane >> 5);
-        return *reinterpret_cast<const v8bf*>(tile + r * (BK * 2) + kc_slot<CPR>(r, c) * 16);
+        return *reinterpret_cast<const v8bf*>(tile + r * (BK * 2) + kc_slot<CPR, 2>(r, c) * 16);
     } else {
         const int j = (lane & 15) >> 2, q = lane & 3;
         const int col = row0 + 16 * ((lane >> 4) & 1) + 4 * q;
@@ -164,7 +176,7 @@ __device__ __forceinline__ v8bf read_frag16(const char* tile, int row0, int kk, 
         constexpr int CPR = BK / 8;
         const int r = row0 + (lane & 15);
         const int c = 4 * kk + (lane >> 4);
-        return *reinterpret_cast<const v8bf*>(tile + r * (BK * 2) + kc_slot<CPR>(r, c) * 16);
+        return *reinterpret_cast<const v8bf*>(tile + r * (BK * 2) + kc_slot<CPR, 2>(r, c) * 16);
     } else {
         // 16-lane group g reads k-rows 32*kk + 8*g + 4*h + (0..3) for h = 0, 1;
         // source lane 4*j + q points at k-row +j, columns row0 + 4*q .. +3.
@@ -198,7 +210,7 @@ __device__ __forceinline__ v4f read_frag_f32(const char* tile, int row0, int kb,
         constexpr int CPR = BK / 4;
         const int r = row0 + (lane & 31);
         const int c = 2 * kb + (lane >> 5);
-        return *reinterpret_cast<const v4f*>(tile + r * (BK * 4) + kc_slot<CPR>(r, c) * 16);
+        return *reinterpret_cast<const v4f*>(tile + r * (BK * 4) + kc_slot<CPR, 4>(r, c) * 16);
     } else {
         const int col = row0 + (lane & 31);
         const int k0 = 8 * kb + 4 * (lane >> 5);
