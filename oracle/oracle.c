@@ -236,6 +236,36 @@ void or_div_bwd_f32(const float* a, const float* b, const float* g, float* da, f
 }
 
 /* ------------------------------------------------------------------------ */
+/* Index (stdlib/linalg/tensor.cleave:113-133): tensor.extract over the     */
+/* row-major buffer (cleave/src/mlir_lower.rs:1968-2002).                   */
+/* ------------------------------------------------------------------------ */
+
+static int64_t or_flat_offset(const int32_t* dims, int32_t ndims, const int32_t* idx) {
+    int64_t off = 0;
+    for (int32_t d = 0; d < ndims; ++d) {
+        if (dims[d] <= 0 || idx[d] < 0 || idx[d] >= dims[d]) return -1;
+        off = off * dims[d] + idx[d];
+    }
+    return off;
+}
+int32_t or_index_f32(const float* t, const int32_t* dims, int32_t ndims, const int32_t* idx,
+                     float* out) {
+    const int64_t off = or_flat_offset(dims, ndims, idx);
+    if (off < 0) return -1;
+    *out = t[off];
+    return 0;
+}
+/* `derivative index(c, idx): index(d(c), idx)` in reverse form: the cotangent
+ * of c gains g at idx; repeated reads of one element accumulate. */
+int32_t or_index_bwd_f32(float g, float* dt, const int32_t* dims, int32_t ndims,
+                         const int32_t* idx) {
+    const int64_t off = or_flat_offset(dims, ndims, idx);
+    if (off < 0) return -1;
+    dt[off] = dt[off] + g;
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* Sum / Mean / Max (stdlib/nn/nn.cleave:111-149).                          */
 /* ------------------------------------------------------------------------ */
 

@@ -91,6 +91,20 @@ void or_relu_bwd_f32(const float* x, const float* g, float* out, int64_t n);
 void or_div_bwd_f32(const float* a, const float* b, const float* g, float* da, float* db,
                     int64_t n);
 
+/* ---- Index (stdlib/linalg/tensor.cleave:113-133) ---- */
+
+/* tensor.extract over the row-major buffer (cleave/src/mlir_lower.rs:1968-2002):
+ * element at offset sum_d idx[d] * prod_{e>d} dims[e].  Returns 0 with the
+ * element in *out, or -1 for an index outside dims (undefined in the reference).
+ * Pinned: numpy C-order indexing on random shapes of rank 1-4, and the
+ * reference's constructed-tensor gradient (cleave/tests/mlir_lower.rs:2738-2757). */
+int32_t or_index_f32(const float* t, const int32_t* dims, int32_t ndims, const int32_t* idx,
+                     float* out);
+/* Reverse form of `derivative index(c, idx): index(d(c), idx)`: dt[idx] += g.
+ * Returns -1 for an index outside dims.  Pinned as above. */
+int32_t or_index_bwd_f32(float g, float* dt, const int32_t* dims, int32_t ndims,
+                         const int32_t* idx);
+
 /* ---- Sum / Mean / Max (stdlib/nn/nn.cleave:111-149) ---- */
 /* acc = v[0]; for i in 1..N: acc = acc + v[i]. */
 float or_sum_f32(const float* v, int64_t n);

@@ -52,6 +52,8 @@ _SIGS = {
     "or_mean_f32": (_f, [_p, _i64]),
     "or_max_of_f32": (_f, [_p, _i64]),
     "or_argmax_f32": (_i64, [_p, _i64]),
+    "or_index_f32": (_i32, [_p, _p, _i32, _p, _p]),
+    "or_index_bwd_f32": (_i32, [_f, _p, _p, _i32, _p]),
     "or_sum_u32_u64": (_u64, [_p, _i64]),
     "or_escape_count_f32": (C.c_uint32, [_f, _f, _i32]),
     "or_escape_count_latch_f32": (C.c_uint32, [_f, _f, _i32]),
@@ -197,6 +199,34 @@ def div_bwd(a, b, g):
     da, db = np.empty_like(a), np.empty_like(a)
     lib().or_div_bwd_f32(_ptr(a), _ptr(b), _ptr(g), _ptr(da), _ptr(db), a.size)
     return da, db
+
+
+# ---- Index ---------------------------------------------------------------------------
+
+def _dims_idx(shape, idx):
+    dims = np.ascontiguousarray(shape, np.int32)
+    ix = np.ascontiguousarray(idx, np.int32)
+    if dims.size != ix.size:
+        raise ValueError("index rank differs from the tensor's")
+    return dims, ix
+
+
+def index(t, idx) -> float:
+    """Element of t at idx (row-major); IndexError outside the shape."""
+    t = _f32(t)
+    dims, ix = _dims_idx(t.shape, idx)
+    out = np.zeros(1, np.float32)
+    if lib().or_index_f32(_ptr(t), _ptr(dims), dims.size, _ptr(ix), _ptr(out)) != 0:
+        raise IndexError(f"index {tuple(idx)} outside shape {t.shape}")
+    return float(out[0])
+
+
+def index_bwd(g: float, dt: np.ndarray, idx) -> None:
+    """dt[idx] += g in place (dt float32, C-contiguous); IndexError outside."""
+    assert dt.dtype == np.float32 and dt.flags["C_CONTIGUOUS"]
+    dims, ix = _dims_idx(dt.shape, idx)
+    if lib().or_index_bwd_f32(g, _ptr(dt), _ptr(dims), dims.size, _ptr(ix)) != 0:
+        raise IndexError(f"index {tuple(idx)} outside shape {dt.shape}")
 
 
 # ---- reductions ---------------------------------------------------------------------

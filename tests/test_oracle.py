@@ -222,7 +222,49 @@ def test_reference_derivative_known_answers(oracle, golden):
     I2 = np.eye(2, dtype=np.float32)
     dA = oracle.matmul(I2, I2, trans_b=True)
     assert list(dA.ravel()) == golden["derivatives"][7]["grad"]
-    assert d  # all sources parsed
+    # sum_i w * data[i]: the mul rule gives data[i] per term, the sum adds them
+    loop = d["2540-2558"]
+    terms = oracle.mul(np.ones(3, np.float32), np.array(loop["data"], np.float32))
+    assert oracle.sum_f32(terms) == loop["grad"][0]
+    # w[0] + w[1]*w[1] with w built from (w1, w2): Index's rule scatters each
+    # read's cotangent back; the product rule gives w[1] + w[1] for the square
+    built = d["2738-2757"]
+    w = np.array(built["at"], np.float32)
+    dw = np.zeros(2, np.float32)
+    oracle.index_bwd(1.0, dw, (0,))
+    w1 = oracle.index(w, (1,))
+    oracle.index_bwd(float(np.float32(w1) + np.float32(w1)), dw, (1,))
+    assert list(dw) == built["grad"]
+    assert len(d) == len(golden["derivatives"])  # every source is distinct
+
+
+# ---- Index ----------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape", [(7,), (3, 5), (2, 3, 4), (2, 1, 3, 5)])
+def test_index_is_row_major_extract(oracle, shape):
+    # tensor.extract over the row-major buffer: numpy's C-order indexing is the
+    # same closed form, offset = sum_d idx[d] * prod_{e>d} shape[e]
+    rng = np.random.default_rng(len(shape))
+    T = rng.standard_normal(shape).astype(np.float32)
+    for flat in range(T.size):
+        idx = np.unravel_index(flat, shape)
+        assert oracle.index(T, idx) == T[idx] == T.ravel()[flat]
+    for bad in [tuple(s for s in shape), tuple([-1] + [0] * (len(shape) - 1))]:
+        with pytest.raises(IndexError):
+            oracle.index(T, bad)
+
+
+def test_index_bwd_scatters_and_accumulates(oracle):
+    dt = np.zeros((3, 4), np.float32)
+    oracle.index_bwd(2.5, dt, (1, 2))
+    oracle.index_bwd(0.5, dt, (1, 2))
+    oracle.index_bwd(-1.0, dt, (2, 3))
+    want = np.zeros((3, 4), np.float32)
+    want[1, 2], want[2, 3] = 3.0, -1.0
+    assert np.array_equal(dt, want)
+    with pytest.raises(IndexError):
+        oracle.index_bwd(1.0, dt, (3, 0))
+    assert np.array_equal(dt, want)  # a rejected call leaves dt alone
 
 
 # ---- reductions -----------------------------------------------------------------
