@@ -168,6 +168,96 @@ def cpu_baseline_gemm(A, B, n, budget_s):
     }
 
 
+def _cpu_entry(value, unit, sample):
+    model, ncpu = cpu_info()
+    return {"value": value, "unit": unit, "cores": 1, "kind": "port",
+            "sample": f"{sample}; host: {model}, {ncpu} logical CPUs"}
+
+
+def _timed_cpu(fn):
+    t0 = time.perf_counter()
+    r = fn()
+    return time.perf_counter() - t0, r
+
+
+def cpu_rows(run_rows, total_rows, budget_s):
+    """Time a 1-row probe, then as many further rows as fit in budget_s; returns
+    (rows timed, seconds).  run_rows(r0, r1) computes rows [r0, r1)."""
+    one, _ = _timed_cpu(lambda: run_rows(0, 1))
+    rows = max(1, min(total_rows - 1, int(budget_s / max(one, 1e-6))))
+    dt, _ = _timed_cpu(lambda: run_rows(1, 1 + rows))
+    return rows, dt
+
+
+def cpu_secondary(orc, name, budget_s, **kw):
+    """Single-core restated loop (oracle/) on a bounded sample of a secondary
+    workload, extrapolated to the full workload's unit."""
+    import numpy as np
+    if name in ("gemm_f32_nt_4096", "gemm_f32_tn_4096"):
+        A, B, n, ta, tb = kw["A"], kw["B"], kw["n"], kw["ta"], kw["tb"]
+        rows, dt = cpu_rows(lambda r0, r1: orc.matmul_rows(A, B, n, n, n, r0, r1, ta, tb), n, budget_s)
+        return _cpu_entry(round(2.0 * rows * n * n / dt / 1e9, 4), "GFLOP/s",
+                          f"rows 1..{rows} of the {n}^3 product, restated k-ascending loop, {dt:.1f} s")
+    if name == "gemm_bf16_8192":
+        A, B, m = kw["A"], kw["B"], kw["m"]
+        rows, dt = cpu_rows(lambda r0, r1: orc.matmul_bf16_rows(A, B, m, m, m, r0, r1), m, budget_s)
+        return _cpu_entry(round(2.0 * rows * m * m / dt / 1e9, 4), "GFLOP/s",
+                          f"rows 1..{rows} of the {m}^3 product on upcast bf16, restated f32 loop, {dt:.1f} s")
+    if name == "gemm_bf16_batched_64x512":
+        A, B, bs, k = kw["A"], kw["B"], kw["bs"], kw["k"]
+        rows, dt = cpu_rows(lambda r0, r1: orc.matmul_bf16_rows(A, B, k, k, k, r0, r1), k, budget_s)
+        return _cpu_entry(round(2.0 * rows * k * k / dt / 1e9, 4), "GFLOP/s",
+                          f"rows 1..{rows} of product 0 of {bs}, restated f32 loop on upcast bf16, {dt:.1f} s")
+    if name == "mlp_step_65536x1024x4096":
+        X, y, W1, W2, B_ = kw["X"], kw["y"], kw["W1"], kw["W2"], kw["B"]
+        # a step costs f (the SGD update, batch-independent) + rows * r; two
+        # batch sizes give both, and the full step is f + B * r
+        t2, _ = _timed_cpu(lambda: orc.mlp_step(X[:2], y[:2], W1, W2, 0.01))
+        bs = int(max(4, min(X.shape[0], 1024, 2 * budget_s / max(t2, 1e-6))))
+        dt, _ = _timed_cpu(lambda: orc.mlp_step(X[:bs], y[:bs], W1, W2, 0.01))
+        r = max((dt - t2) / (bs - 2), 1e-12)
+        f = max(t2 - 2 * r, 0.0)
+        full = f + B_ * r
+        return _cpu_entry(round(1.0 / full, 6), "steps/s",
+                          f"steps on batch rows 0..1 ({t2:.2f} s) and 0..{bs - 1} ({dt:.1f} s) of {B_} "
+                          f"(forward, backward, SGD), fitted as fixed + per-row cost: {full:.0f} s per full step")
+    if name == "mandelbrot_16384_1000":
+        g, d, total = kw["g"], kw["d"], kw["total"]
+        mid, band = g // 2, 2
+        while True:  # widen a centred band of rows until it costs at least budget_s / 4
+            dt, out = _timed_cpu(lambda: orc.mandelbrot(g, g, -2.0, -1.5, d, d, 1000, rows=(mid - band, mid + band)))
+            if dt > budget_s / 4 or 2 * band >= g // 4:
+                break
+            band *= 2
+        it = float(out[mid - band:mid + band].astype(np.uint64).sum())
+        rate = it / dt
+        return _cpu_entry(round(rate, 1), "pixel-iter/s",
+                          f"rows {mid - band}..{mid + band - 1} (the set's widest band), {dt:.1f} s; "
+                          f"the full grid's {total} counted iterations would take {total / rate:.0f} s")
+    arr_n = kw.get("n", 1 << 24)
+    rng = np.random.default_rng(7)
+    if name == "sum_u32_u64_16384sq":
+        v = rng.integers(0, 1000, arr_n, dtype=np.uint32)
+        dt, _ = _timed_cpu(lambda: orc.sum_u64(v))
+        return _cpu_entry(round(arr_n * 4 / dt / 1e9, 3), "GB/s", f"{arr_n} u32 counts summed into u64, {dt * 1e3:.0f} ms")
+    v = rng.standard_normal(arr_n).astype(np.float32)
+    if name == "sigmoid_map_268M":
+        dt, _ = _timed_cpu(lambda: orc.sigmoid(v))
+        return _cpu_entry(round(arr_n * 8 / dt / 1e9, 3), "GB/s", f"{arr_n} f32, 1/(1+expf(-x)), {dt * 1e3:.0f} ms")
+    if name == "add_map_268M":
+        w = rng.standard_normal(arr_n).astype(np.float32)
+        dt, _ = _timed_cpu(lambda: orc.add(v, w))
+        return _cpu_entry(round(arr_n * 12 / dt / 1e9, 3), "GB/s", f"{arr_n} f32 pairs, {dt * 1e3:.0f} ms")
+    if name == "sum_f32_268M":
+        dt, _ = _timed_cpu(lambda: orc.sum_f32(v))
+        return _cpu_entry(round(arr_n * 4 / dt / 1e9, 3), "GB/s", f"{arr_n} f32, left fold, {dt * 1e3:.0f} ms")
+    if name == "max_argmax_f32_268M":
+        dt, _ = _timed_cpu(lambda: (orc.max_of(v), orc.argmax(v)))
+        return _cpu_entry(round(arr_n * 4 / dt / 1e9, 3), "GB/s",
+                          f"{arr_n} f32, max_of then argmax (two passes, as two reference calls), {dt * 1e3:.0f} ms")
+    raise KeyError(name)
+
+
 COPY_ELEMS = 1 << 26  # 256 MiB of f32 read, 256 MiB written per launch
 
 
@@ -189,7 +279,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work (headline)")
+    ap.add_argument("--cpu-budget-secondary", type=float, default=2.0,
+                    help="seconds of CPU baseline work per secondary workload")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--vendor", action="store_true",
@@ -253,6 +345,11 @@ def main():
     }
 
     secondary = {}
+    want_cpu = not args.no_cpu
+    if want_cpu:
+        from oracle import oracle as orc
+        A_host, B_host = a.numpy(), b.numpy()
+    cb = args.cpu_budget_secondary
     if not args.no_secondary:
         sec_steps = max(20, steps // 2)
         # f32 A B^T and A^T B (reverse-mode halves of the product rule)
@@ -262,6 +359,8 @@ def main():
             secondary[name] = {"GFLOP/s": round(flop * sec_steps / wall_s / 1e9, 1),
                                "kernel_ms": round(ev, 4), "frac_fp32_mfma": round(ach / PEAK_FP32_MFMA, 4)}
             log(f"{name}: {ach:.1f} TFLOP/s")
+            if want_cpu:
+                secondary[name]["cpu_baseline"] = cpu_secondary(orc, name, cb, A=A_host, B=B_host, n=n, ta=ta, tb=tb)
         del c
         # bf16 8192^3
         m = 8192
@@ -270,14 +369,17 @@ def main():
         ca.fill_normal(a32, seed=202, std=0.02)
         bb = ca.to_bf16(a32)
         del a32
-        cb = ca.empty((m, m))
+        cmat = ca.empty((m, m))
         fl = 2.0 * m ** 3
-        wall_s, ev = timed(ca, lambda: ca.matmul(ab, bb, out=cb), sec_steps, 2, 0.4)
+        wall_s, ev = timed(ca, lambda: ca.matmul(ab, bb, out=cmat), sec_steps, 2, 0.4)
         ach = fl / (ev * 1e-3) / 1e12
         secondary["gemm_bf16_8192"] = {"GFLOP/s": round(fl * sec_steps / wall_s / 1e9, 1), "kernel_ms": round(ev, 4),
                                        "frac_bf16_mfma": round(ach / PEAK_BF16_MFMA, 4)}
         log(f"gemm_bf16_8192: {ach:.1f} TFLOP/s")
-        del ab, bb, cb
+        if want_cpu:
+            secondary["gemm_bf16_8192"]["cpu_baseline"] = cpu_secondary(
+                orc, "gemm_bf16_8192", cb, A=ab.numpy(), B=bb.numpy(), m=m)
+        del ab, bb, cmat
         # batched bf16 64 x 512^3
         bs, k = 64, 512
         t32 = ca.fill_normal(ca.empty((bs, k, k)), seed=301, std=0.02)
@@ -297,6 +399,9 @@ def main():
                                                  "hbm_GB/s": round(hbm / (ev * 1e-3) / 1e9, 1),
                                                  "frac_hbm": round(hbm / (ev * 1e-3) / 1e9 / PEAK_HBM, 4)}
         log(f"gemm_bf16_batched_64x512: {ach:.1f} TFLOP/s")
+        if want_cpu:
+            secondary["gemm_bf16_batched_64x512"]["cpu_baseline"] = cpu_secondary(
+                orc, "gemm_bf16_batched_64x512", cb, A=xb.numpy()[0], B=yb.numpy()[0], bs=bs, k=k)
         del xb, yb, zb
         # MLP step (config 4)
         B_, D_, H_ = 65536, 1024, 4096
@@ -315,6 +420,9 @@ def main():
             "gemm_TFLOP/s": round(gemm_fl / (ev * 1e-3) / 1e12, 2),
             "loss_after": float(loss.numpy()[0])}
         log(f"mlp step: {mlp_steps / wall_s:.2f} steps/s ({ev:.2f} ms)")
+        if want_cpu:
+            secondary["mlp_step_65536x1024x4096"]["cpu_baseline"] = cpu_secondary(
+                orc, "mlp_step_65536x1024x4096", cb, X=x.numpy(), y=yv.numpy(), W1=w1.numpy(), W2=w2.numpy(), B=B_)
         del x, yv, w1, w2
         # escape-count map + u64 sum (config 3)
         g = 16384
@@ -330,12 +438,17 @@ def main():
             "frac_valu_nofma": round(11.0 * total / (ev * 1e-3) / 1e12 / PEAK_FP32_VALU_NOFMA, 4),
             "sum_of_counts": int(total)}
         log(f"mandelbrot: {ev:.2f} ms, sum {total}")
+        if want_cpu:
+            secondary["mandelbrot_16384_1000"]["cpu_baseline"] = cpu_secondary(
+                orc, "mandelbrot_16384_1000", cb, g=g, d=d, total=int(total))
         out_dev = ca.empty(1, "u64")
         wall_s, ev = timed(ca, lambda: ca.reduce_sum_u64(cnt, out_dev), 20, 3)
         gbs = g * g * 4 / (ev * 1e-3) / 1e9
         secondary["sum_u32_u64_16384sq"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1),
                                            "frac_hbm": round(gbs / PEAK_HBM, 4)}
         log(f"u64 sum: {gbs:.0f} GB/s")
+        if want_cpu:
+            secondary["sum_u32_u64_16384sq"]["cpu_baseline"] = cpu_secondary(orc, "sum_u32_u64_16384sq", cb)
         del cnt
         # sigmoid map over an H-sized tensor (65536 x 4096 f32)
         hn = 65536 * 4096
@@ -345,12 +458,16 @@ def main():
         gbs = hn * 8 / (ev * 1e-3) / 1e9
         secondary["sigmoid_map_268M"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)}
         log(f"sigmoid map: {gbs:.0f} GB/s")
+        if want_cpu:
+            secondary["sigmoid_map_268M"]["cpu_baseline"] = cpu_secondary(orc, "sigmoid_map_268M", cb)
         # binary Ring map (two reads, one write per element)
         hz = ca.fill_normal(ca.empty(hn), seed=502)
         wall_s, ev = timed(ca, lambda: ca.add(hx, hz, out=hy), 10, 2)
         gbs = hn * 12 / (ev * 1e-3) / 1e9
         secondary["add_map_268M"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)}
         log(f"add map: {gbs:.0f} GB/s")
+        if want_cpu:
+            secondary["add_map_268M"]["cpu_baseline"] = cpu_secondary(orc, "add_map_268M", cb)
         del hz
         # f32 Sum and Max/argmax reductions (one read per element)
         sdev = ca.empty(1)
@@ -358,11 +475,15 @@ def main():
         gbs = hn * 4 / (ev * 1e-3) / 1e9
         secondary["sum_f32_268M"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)}
         log(f"sum f32: {gbs:.0f} GB/s")
+        if want_cpu:
+            secondary["sum_f32_268M"]["cpu_baseline"] = cpu_secondary(orc, "sum_f32_268M", cb)
         mdev, idev = ca.empty(1), ca.empty(1, "i64")
         wall_s, ev = timed(ca, lambda: ca.reduce_max(hx, mdev, idev), 10, 2)
         gbs = hn * 4 / (ev * 1e-3) / 1e9
         secondary["max_argmax_f32_268M"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)}
         log(f"max/argmax f32: {gbs:.0f} GB/s")
+        if want_cpu:
+            secondary["max_argmax_f32_268M"]["cpu_baseline"] = cpu_secondary(orc, "max_argmax_f32_268M", cb)
         del hx, hy
     if secondary:
         result["secondary"] = secondary
@@ -376,7 +497,7 @@ def main():
 
     if not args.no_cpu:
         log(f"cpu baseline: ~{args.cpu_budget:.0f} s of the restated loop on one core")
-        result["cpu_baseline"] = cpu_baseline_gemm(a.numpy(), b.numpy(), n, args.cpu_budget)
+        result["cpu_baseline"] = cpu_baseline_gemm(A_host, B_host, n, args.cpu_budget)
     print(json.dumps(result), flush=True)
 
 

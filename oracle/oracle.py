@@ -147,6 +147,15 @@ def matmul_rows(A, B, M, N, K, row0, row1, trans_a=False, trans_b=False) -> np.n
     return C_[row0:row1]
 
 
+def matmul_bf16_rows(A, B, M, N, K, row0, row1) -> np.ndarray:
+    """Rows [row0,row1) of the A*B product of bf16 bit arrays (NN), upcast to f32."""
+    A = np.ascontiguousarray(A, np.uint16)
+    B = np.ascontiguousarray(B, np.uint16)
+    C_ = np.empty((M, N), np.float32)
+    lib().or_matmul_bf16_rows(_ptr(A), _ptr(B), _ptr(C_), M, N, K, row0, row1)
+    return C_[row0:row1]
+
+
 def matmul_entries(A, B, M, N, K, ii, jj, trans_a=False, trans_b=False, bf16=False):
     """C[ii[e], jj[e]] and sum_k |a||b| for each entry."""
     ii = np.ascontiguousarray(ii, np.int32)
