@@ -1,8 +1,11 @@
-"""Build recipe for libcleave_hip.so (gfx950).
+"""Build recipe for libcleave_hip.so and libcleave_hip.a (gfx950).
 
 Each HIP source compiles to an object under cleave_amd/_build/ in parallel,
 then one `hipcc -shared` link produces cleave_amd/libcleave_hip.so (in-tree,
-so it travels with the source tree to the GPU box).
+so it travels with the source tree to the GPU box), and `ar` packs the same
+objects into cleave_amd/libcleave_hip.a for hosts that link statically (the
+counterpart of cleave-rt's staticlib crate type, cleave-rt/Cargo.toml:15-16;
+the final link needs hipcc or -lamdhip64).
 
 Flags:
   --offload-arch=gfx950          MI355X only, no other targets
@@ -30,6 +33,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libcleave_hip.so"
+ARCHIVE = PKG / "libcleave_hip.a"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
@@ -97,6 +101,11 @@ def build_library(jobs: int = 8) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, LIB)
+    atmp = ARCHIVE.with_suffix(".a.tmp")
+    if atmp.exists():
+        atmp.unlink()
+    _run(["ar", "rcs", str(atmp), *map(str, objs)])
+    os.replace(atmp, ARCHIVE)
     return LIB
 
 

@@ -8,6 +8,7 @@ from __future__ import annotations
 import ctypes as C
 import re
 import subprocess
+from pathlib import Path
 import sys
 
 import pytest
@@ -41,6 +42,44 @@ def test_library_exports_every_declared_symbol_and_nothing_else():
                          text=True, check=True).stdout
     exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
     assert exported == set(header_functions())
+
+
+def test_static_archive_defines_every_declared_symbol():
+    from cleave_amd import build
+
+    assert build.ARCHIVE.exists(), "libcleave_hip.a is built beside the shared library"
+    out = subprocess.run(["nm", "--defined-only", str(build.ARCHIVE)], capture_output=True,
+                         text=True, check=True).stdout
+    defined = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    assert set(header_functions()) <= defined
+
+
+def test_static_archive_links_into_a_host_program(tmp_path):
+    # the AOT path: a C host links libcleave_hip.a (plus the HIP runtime) and
+    # walks the symbol table, with or without a visible device
+    from cleave_amd import build
+
+    hipcc = Path(build.HIPCC)
+    if not hipcc.exists():
+        pytest.skip("hipcc not installed")
+    src = tmp_path / "host.c"
+    src.write_text(
+        "#include <stdio.h>\n#include <string.h>\n#include \"cleave_hip.h\"\n"
+        "int main(void) {\n"
+        "  int64_t n = 0;\n"
+        "  const cleave_hip_symbol* t = cleave_hip_symbols(&n);\n"
+        "  int found = 0;\n"
+        "  for (int64_t i = 0; i < n; ++i)\n"
+        "    if (!strcmp(t[i].name, \"cleave_hip_matmul_f32\") && t[i].fn == (void*)cleave_hip_matmul_f32) found = 1;\n"
+        "  printf(\"%lld %d %d\\n\", (long long)n, found, (int)cleave_hip_device_available());\n"
+        "  return 0;\n"
+        "}\n")
+    obj, exe = tmp_path / "host.o", tmp_path / "host"
+    subprocess.run(["gcc", "-c", "-I", str(ROOT / "include"), str(src), "-o", str(obj)], check=True)
+    subprocess.run([str(hipcc), "--offload-arch=gfx950", str(obj), str(build.ARCHIVE), "-o", str(exe)],
+                   check=True, capture_output=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True, timeout=60).stdout.split()
+    assert int(out[0]) == len(header_functions()) and out[1] == "1" and out[2] in ("0", "1")
 
 
 def test_symbol_table_matches_header_and_addresses():
