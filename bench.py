@@ -442,7 +442,7 @@ def main():
             secondary["mandelbrot_16384_1000"]["cpu_baseline"] = cpu_secondary(
                 orc, "mandelbrot_16384_1000", cb, g=g, d=d, total=int(total))
         out_dev = ca.empty(1, "u64")
-        wall_s, ev = timed(ca, lambda: ca.reduce_sum_u64(cnt, out_dev), 20, 3)
+        wall_s, ev = timed(ca, lambda: ca.reduce_sum_u64(cnt, out_dev), 40, 5, 0.2)
         gbs = g * g * 4 / (ev * 1e-3) / 1e9
         secondary["sum_u32_u64_16384sq"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1),
                                            "frac_hbm": round(gbs / PEAK_HBM, 4)}
@@ -454,7 +454,7 @@ def main():
         hn = 65536 * 4096
         hx = ca.fill_normal(ca.empty(hn), seed=501)
         hy = ca.empty(hn)
-        wall_s, ev = timed(ca, lambda: ca.sigmoid(hx, out=hy), 10, 2)
+        wall_s, ev = timed(ca, lambda: ca.sigmoid(hx, out=hy), 30, 5, 0.2)
         gbs = hn * 8 / (ev * 1e-3) / 1e9
         secondary["sigmoid_map_268M"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)}
         log(f"sigmoid map: {gbs:.0f} GB/s")
@@ -462,7 +462,7 @@ def main():
             secondary["sigmoid_map_268M"]["cpu_baseline"] = cpu_secondary(orc, "sigmoid_map_268M", cb)
         # binary Ring map (two reads, one write per element)
         hz = ca.fill_normal(ca.empty(hn), seed=502)
-        wall_s, ev = timed(ca, lambda: ca.add(hx, hz, out=hy), 10, 2)
+        wall_s, ev = timed(ca, lambda: ca.add(hx, hz, out=hy), 30, 5, 0.2)
         gbs = hn * 12 / (ev * 1e-3) / 1e9
         secondary["add_map_268M"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)}
         log(f"add map: {gbs:.0f} GB/s")
@@ -471,14 +471,14 @@ def main():
         del hz
         # f32 Sum and Max/argmax reductions (one read per element)
         sdev = ca.empty(1)
-        wall_s, ev = timed(ca, lambda: ca.reduce_sum(hx, sdev), 10, 2)
+        wall_s, ev = timed(ca, lambda: ca.reduce_sum(hx, sdev), 30, 5, 0.2)
         gbs = hn * 4 / (ev * 1e-3) / 1e9
         secondary["sum_f32_268M"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)}
         log(f"sum f32: {gbs:.0f} GB/s")
         if want_cpu:
             secondary["sum_f32_268M"]["cpu_baseline"] = cpu_secondary(orc, "sum_f32_268M", cb)
         mdev, idev = ca.empty(1), ca.empty(1, "i64")
-        wall_s, ev = timed(ca, lambda: ca.reduce_max(hx, mdev, idev), 10, 2)
+        wall_s, ev = timed(ca, lambda: ca.reduce_max(hx, mdev, idev), 30, 5, 0.2)
         gbs = hn * 4 / (ev * 1e-3) / 1e9
         secondary["max_argmax_f32_268M"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)}
         log(f"max/argmax f32: {gbs:.0f} GB/s")
