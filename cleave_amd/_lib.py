@@ -1,4 +1,5 @@
-"""ctypes binding of libcleave_hip.so (the C ABI declared in include/cleave_hip.h).
+"""ctypes binding of libcleave_hip.so (the C ABI declared in include/cleave_hip.h
+and, for the memref-descriptor forms, include/cleave_hip_memref.h).
 
 This is the reference-side binding a host would add (the Python equivalent of
 the `extern(symbol) fn ...` declarations of /root/reference/stdlib/io/io.cleave:16-21):
@@ -89,6 +90,33 @@ SIGNATURES: dict[str, tuple] = {
     "cleave_hip_mandelbrot_u32": (i32, [vp, i64, i32, i32, f32, f32, f32, f32, i32]),
     "cleave_hip_mlp_step_f32": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64,
                                       vp, i32, i32, i32, f32]),
+    # memref-descriptor forms: every tensor argument is a pointer to an
+    # unranked descriptor {int64 rank; void* ranked descriptor}
+    "_mlir_ciface_cleave_hip_matmul_f32": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_matmul_bf16": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_add_f32": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_sub_f32": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_mul_f32": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_div_f32": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_neg_f32": (i32, [vp, vp]),
+    "_mlir_ciface_cleave_hip_zero_f32": (i32, [vp]),
+    "_mlir_ciface_cleave_hip_relu_f32": (i32, [vp, vp]),
+    "_mlir_ciface_cleave_hip_sigmoid_f32": (i32, [vp, vp]),
+    "_mlir_ciface_cleave_hip_tanh_f32": (i32, [vp, vp]),
+    "_mlir_ciface_cleave_hip_sigmoid_bwd_f32": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_tanh_bwd_f32": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_relu_bwd_f32": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_div_bwd_f32": (i32, [vp, vp, vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_sgd_update_f32": (i32, [vp, vp, f32]),
+    "_mlir_ciface_cleave_hip_sum_f32": (f32, [vp]),
+    "_mlir_ciface_cleave_hip_mean_f32": (f32, [vp]),
+    "_mlir_ciface_cleave_hip_max_of_f32": (f32, [vp]),
+    "_mlir_ciface_cleave_hip_argmax_f32": (i64, [vp]),
+    "_mlir_ciface_cleave_hip_sum_u32_u64": (u64, [vp]),
+    "_mlir_ciface_cleave_hip_index_f32": (f32, [vp, vp]),
+    "_mlir_ciface_cleave_hip_index_bwd_f32": (i32, [f32, vp, vp]),
+    "_mlir_ciface_cleave_hip_mandelbrot_u32": (i32, [vp, f32, f32, f32, f32, i32]),
+    "_mlir_ciface_cleave_hip_mlp_step_f32": (i32, [vp, vp, vp, vp, vp, vp, vp, f32]),
 }
 
 # Functions whose int32 return is a status code.

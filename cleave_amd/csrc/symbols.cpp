@@ -2,8 +2,9 @@
 // register_cleave_rt_symbols (/root/reference/cleave/src/pipeline.rs:159-198),
 // which registers every cleave-rt function by pointer.  A host that JITs
 // `extern(cleave_hip_...)` calls walks this table once instead of keeping its
-// own list.  Every function declared in include/cleave_hip.h appears here.
-#include "../../include/cleave_hip.h"
+// own list.  Every function declared in include/cleave_hip.h and
+// include/cleave_hip_memref.h appears here.
+#include "../../include/cleave_hip_memref.h"
 
 #define CH_SYM(f) {#f, reinterpret_cast<void*>(&f)}
 
@@ -58,6 +59,31 @@ const cleave_hip_symbol kSymbols[] = {
     CH_SYM(cleave_hip_index_bwd_f32),
     CH_SYM(cleave_hip_mandelbrot_u32),
     CH_SYM(cleave_hip_mlp_step_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_matmul_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_matmul_bf16),
+    CH_SYM(_mlir_ciface_cleave_hip_add_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_sub_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_mul_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_div_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_neg_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_zero_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_relu_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_sigmoid_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_tanh_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_sigmoid_bwd_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_tanh_bwd_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_relu_bwd_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_div_bwd_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_sgd_update_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_sum_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_mean_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_max_of_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_argmax_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_sum_u32_u64),
+    CH_SYM(_mlir_ciface_cleave_hip_index_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_index_bwd_f32),
+    CH_SYM(_mlir_ciface_cleave_hip_mandelbrot_u32),
+    CH_SYM(_mlir_ciface_cleave_hip_mlp_step_f32),
 };
 }  // namespace
 

@@ -16,11 +16,14 @@ import pytest
 from conftest import ROOT
 
 HEADER = ROOT / "include" / "cleave_hip.h"
+HEADERS = [HEADER, ROOT / "include" / "cleave_hip_memref.h"]
 
 
 def header_functions() -> list[str]:
-    text = HEADER.read_text()
-    return list(dict.fromkeys(re.findall(r"^CLEAVE_HIP_API [^(]*?\b(cleave_hip_[a-z0-9_]+)\(", text, re.M)))
+    names = []
+    for h in HEADERS:
+        names += re.findall(r"^CLEAVE_HIP_API [^(]*?\b((?:_mlir_ciface_)?cleave_hip_[a-z0-9_]+)\(", h.read_text(), re.M)
+    return list(dict.fromkeys(names))
 
 
 def test_header_declares_the_expected_surface():
