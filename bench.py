@@ -251,6 +251,15 @@ def cpu_secondary(orc, name, budget_s, **kw):
     if name == "sum_f32_268M":
         dt, _ = _timed_cpu(lambda: orc.sum_f32(v))
         return _cpu_entry(round(arr_n * 4 / dt / 1e9, 3), "GB/s", f"{arr_n} f32, left fold, {dt * 1e3:.0f} ms")
+    if name in ("add_row_bias_65536x4096", "sum_rows_65536x4096"):
+        cols = 4096
+        m = v.reshape(-1, cols)
+        if name == "add_row_bias_65536x4096":
+            bias = rng.standard_normal(cols).astype(np.float32)
+            dt, _ = _timed_cpu(lambda: orc.add_row_bias(m, bias))
+            return _cpu_entry(round(arr_n * 8 / dt / 1e9, 3), "GB/s", f"{m.shape[0]} x {cols} f32 plus a row bias, {dt * 1e3:.0f} ms")
+        dt, _ = _timed_cpu(lambda: orc.sum_rows(m))
+        return _cpu_entry(round(arr_n * 4 / dt / 1e9, 3), "GB/s", f"{m.shape[0]} x {cols} f32 summed down the columns, {dt * 1e3:.0f} ms")
     if name == "max_argmax_f32_268M":
         dt, _ = _timed_cpu(lambda: (orc.max_of(v), orc.argmax(v)))
         return _cpu_entry(round(arr_n * 4 / dt / 1e9, 3), "GB/s",
@@ -469,6 +478,24 @@ def main():
         if want_cpu:
             secondary["add_map_268M"]["cpu_baseline"] = cpu_secondary(orc, "add_map_268M", cb)
         del hz
+        # bias shared by every row of the hidden layer, and its reverse rule
+        hb = ca.fill_normal(ca.empty(4096), seed=503)
+        hx2, hy2 = hx.view((65536, 4096)), hy.view((65536, 4096))
+        wall_s, ev = timed(ca, lambda: ca.add_row_bias(hx2, hb, out=hy2), 30, 5, 0.2)
+        gbs = hn * 8 / (ev * 1e-3) / 1e9
+        secondary["add_row_bias_65536x4096"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1),
+                                                "frac_hbm": round(gbs / PEAK_HBM, 4)}
+        log(f"add row bias: {gbs:.0f} GB/s")
+        if want_cpu:
+            secondary["add_row_bias_65536x4096"]["cpu_baseline"] = cpu_secondary(orc, "add_row_bias_65536x4096", cb)
+        sr = ca.empty(4096)
+        wall_s, ev = timed(ca, lambda: ca.sum_rows(hx2, out=sr), 30, 5, 0.2)
+        gbs = hn * 4 / (ev * 1e-3) / 1e9
+        secondary["sum_rows_65536x4096"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1),
+                                            "frac_hbm": round(gbs / PEAK_HBM, 4)}
+        log(f"sum rows: {gbs:.0f} GB/s")
+        if want_cpu:
+            secondary["sum_rows_65536x4096"]["cpu_baseline"] = cpu_secondary(orc, "sum_rows_65536x4096", cb)
         # f32 Sum and Max/argmax reductions (one read per element)
         sdev = ca.empty(1)
         wall_s, ev = timed(ca, lambda: ca.reduce_sum(hx, sdev), 30, 5, 0.2)

@@ -18,7 +18,7 @@ aborting once the binding switches abort-on-error off).
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import numpy as np
 
@@ -61,6 +61,7 @@ class Tensor:
     shape: tuple
     dtype: str
     owned: bool = True
+    base: "Tensor | None" = field(default=None, repr=False, compare=False)  # keeps a view's buffer alive
 
     @property
     def size(self) -> int:
@@ -90,6 +91,14 @@ class Tensor:
             if n != arr.nbytes:
                 raise CleaveHipError(n, _lib.last_error()[1])
         return self
+
+    def view(self, shape) -> "Tensor":
+        """The same buffer under another shape with the same element count (no copy)."""
+        shape = tuple(int(d) for d in shape)
+        t = Tensor(self.ptr, shape, self.dtype, owned=False, base=self)
+        if t.size != self.size:
+            raise ValueError(f"view {shape} does not cover {self.size} elements")
+        return t
 
     def free(self) -> None:
         if self.owned and self.ptr:
@@ -191,6 +200,22 @@ def tanh(x, out=None): return _unary("cleave_hip_tanh_f32", x, out)
 def sigmoid_bwd(s, g, out=None): return _binary("cleave_hip_sigmoid_bwd_f32", s, g, out)
 def tanh_bwd(t, g, out=None): return _binary("cleave_hip_tanh_bwd_f32", t, g, out)
 def relu_bwd(x, g, out=None): return _binary("cleave_hip_relu_bwd_f32", x, g, out)
+
+
+def add_row_bias(a: Tensor, bias: Tensor, out: Tensor | None = None) -> Tensor:
+    """out[i, j] = a[i, j] + bias[j]: a bias shared by every row of a batch."""
+    rows, cols = a.shape
+    out = out if out is not None else empty(a.shape, "f32")
+    call("cleave_hip_add_row_bias_f32", a.ptr, a.size, bias.ptr, bias.size, out.ptr, out.size, rows, cols)
+    return out
+
+
+def sum_rows(g: Tensor, out: Tensor | None = None) -> Tensor:
+    """out[j] = sum_i g[i, j]: the reverse rule of add_row_bias."""
+    rows, cols = g.shape
+    out = out if out is not None else empty((cols,), "f32")
+    call("cleave_hip_sum_rows_f32", g.ptr, g.size, out.ptr, out.size, rows, cols)
+    return out
 
 
 def zero(shape_or_tensor) -> Tensor:

@@ -77,6 +77,8 @@ SIGNATURES: dict[str, tuple] = {
     "cleave_hip_relu_bwd_f32": (i32, [vp, i64, vp, i64, vp, i64]),
     "cleave_hip_div_bwd_f32": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64]),
     "cleave_hip_sgd_update_f32": (i32, [vp, i64, vp, i64, f32]),
+    "cleave_hip_add_row_bias_f32": (i32, [vp, i64, vp, i64, vp, i64, i32, i32]),
+    "cleave_hip_sum_rows_f32": (i32, [vp, i64, vp, i64, i32, i32]),
     "cleave_hip_reduce_sum_f32": (i32, [vp, i64, vp]),
     "cleave_hip_reduce_max_f32": (i32, [vp, i64, vp, vp]),
     "cleave_hip_reduce_sum_u32_u64": (i32, [vp, i64, vp]),
@@ -108,6 +110,8 @@ SIGNATURES: dict[str, tuple] = {
     "_mlir_ciface_cleave_hip_relu_bwd_f32": (i32, [vp, vp, vp]),
     "_mlir_ciface_cleave_hip_div_bwd_f32": (i32, [vp, vp, vp, vp, vp]),
     "_mlir_ciface_cleave_hip_sgd_update_f32": (i32, [vp, vp, f32]),
+    "_mlir_ciface_cleave_hip_add_row_bias_f32": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_sum_rows_f32": (i32, [vp, vp]),
     "_mlir_ciface_cleave_hip_sum_f32": (f32, [vp]),
     "_mlir_ciface_cleave_hip_mean_f32": (f32, [vp]),
     "_mlir_ciface_cleave_hip_max_of_f32": (f32, [vp]),

@@ -48,7 +48,8 @@ HIP_FLAGS = [
     "-fvisibility=hidden",
 ]
 SOURCES = ["runtime.hip", "gemm_f32.hip", "gemm_bf16.hip", "elementwise.hip", "reduce.hip",
-           "mandelbrot.hip", "mlp.hip", "index.hip", "memref.cpp", "symbols.cpp"]
+           "mandelbrot.hip", "mlp.hip", "index.hip", "broadcast.hip", "memref.cpp",
+           "symbols.cpp"]
 
 
 REPORT = "-Rpass-analysis=kernel-resource-usage"

@@ -1,0 +1,190 @@
+// broadcast.hip -- a bias shared by every row of a batch, and its reverse rule.
+//
+// The reference adds a bias of the operand's own shape (examples/xor_tensor.cleave:44-49,
+// one example at a time: matmul(x, w) + b1 with both 1 x n), because Ring<Tensor>::add
+// needs equal shapes (stdlib/linalg/tensor.cleave:66-71).  A batch of rows needs the
+// broadcast form out[i][j] = a[i][j] + b[j]; its reverse rule is db[j] = sum_i g[i][j],
+// the cotangent summed over the broadcast dimension.
+//
+// Both are HBM-bound.  Threads own one 16-byte column chunk and walk a group of rows,
+// so every wave reads and writes whole 1 KiB row segments; the bias chunk (or the
+// column accumulator) stays in registers.  The column sums add each row group in
+// ascending row order, then the group partials in ascending group order: a fixed
+// order, so results are deterministic for a given shape.
+#include "common.hpp"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowUnroll = 4;
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f4 ld4nt(const float* p) { return __builtin_nontemporal_load(reinterpret_cast<const f4*>(p)); }
+__device__ __forceinline__ void st4nt(float* p, f4 v) { __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p)); }
+
+// Launch shape of both kernels: blockIdx.x = group * nseg + seg, where seg
+// picks kThreads column chunks and group a run of rows_per_group rows.
+struct Tiling {
+    int64_t cv = 0;          // 16-byte column chunks per row (cols / 4)
+    int64_t nseg = 0;        // column segments of kThreads chunks
+    int64_t groups = 0;      // row groups
+    int64_t rows_per_group = 0;
+};
+
+Tiling tiling_rows(int64_t rows, int64_t cols, int64_t rows_per_group) {
+    Tiling t;
+    t.cv = cols / 4;
+    t.nseg = (t.cv + kThreads - 1) / kThreads;
+    t.rows_per_group = rows_per_group < rows ? rows_per_group : rows;
+    t.groups = (rows + t.rows_per_group - 1) / t.rows_per_group;
+    return t;
+}
+// The bias add moves every element once, so short row groups (many blocks, as a
+// one-shot map) keep the most bytes in flight: 8 rows per block measured
+// 6.6 TB/s at 65536 x 4096 against 4.8 TB/s for 128.
+Tiling tiling_bias(int64_t rows, int64_t cols) { return tiling_rows(rows, cols, 8); }
+// The column sums write one partial row per group, which the second stage
+// reads back; about four blocks per CU in the first stage measured best
+// (6.75 TB/s at 65536 x 4096, 256 groups).
+Tiling tiling_sum(int64_t rows, int64_t cols) {
+    const int64_t nseg = (cols / 4 + kThreads - 1) / kThreads;
+    int64_t groups = 4LL * ch::num_cus() / nseg;
+    if (groups < 1) groups = 1;
+    if (groups > rows) groups = rows;
+    return tiling_rows(rows, cols, (rows + groups - 1) / groups);
+}
+
+__global__ __launch_bounds__(kThreads) void add_row_bias_kernel(const float* __restrict__ a,
+                                                                const float* __restrict__ bias,
+                                                                float* __restrict__ out, int64_t rows,
+                                                                int64_t cols, int64_t nseg, int64_t rpg) {
+    const int64_t seg = blockIdx.x % nseg, group = blockIdx.x / nseg;
+    const int64_t c = (seg * kThreads + threadIdx.x) * 4;
+    if (c >= cols) return;
+    const f4 b = *reinterpret_cast<const f4*>(bias + c);
+    const int64_t r0 = group * rpg;
+    const int64_t r1 = r0 + rpg < rows ? r0 + rpg : rows;
+    int64_t r = r0;
+    for (; r + kRowUnroll <= r1; r += kRowUnroll) {
+        f4 v[kRowUnroll];
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) v[u] = ld4nt(a + (r + u) * cols + c);
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) st4nt(out + (r + u) * cols + c, v[u] + b);
+    }
+    for (; r < r1; ++r) st4nt(out + r * cols + c, ld4nt(a + r * cols + c) + b);
+}
+
+__global__ __launch_bounds__(kThreads) void sum_rows_stage1(const float* __restrict__ g, float* __restrict__ part,
+                                                            int64_t rows, int64_t cols, int64_t nseg, int64_t rpg) {
+    const int64_t seg = blockIdx.x % nseg, group = blockIdx.x / nseg;
+    const int64_t c = (seg * kThreads + threadIdx.x) * 4;
+    if (c >= cols) return;
+    const int64_t r0 = group * rpg;
+    const int64_t r1 = r0 + rpg < rows ? r0 + rpg : rows;
+    f4 acc = ld4nt(g + r0 * cols + c);
+    int64_t r = r0 + 1;
+    for (; r + kRowUnroll <= r1; r += kRowUnroll) {
+        f4 v[kRowUnroll];
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) v[u] = ld4nt(g + (r + u) * cols + c);
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) acc = acc + v[u];
+    }
+    for (; r < r1; ++r) acc = acc + ld4nt(g + r * cols + c);
+    *reinterpret_cast<f4*>(part + group * cols + c) = acc;
+}
+
+// out[j] = part[0][j] + part[1][j] + ... (groups ascending).  The loads of
+// eight groups are issued together; the adds keep the ascending order.
+constexpr int kGroupUnroll = 8;
+__global__ __launch_bounds__(kThreads) void sum_rows_stage2(const float* __restrict__ part, float* __restrict__ out,
+                                                            int64_t groups, int64_t cols) {
+    const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (j >= cols) return;
+    float acc = part[j];
+    int64_t q = 1;
+    for (; q + kGroupUnroll <= groups; q += kGroupUnroll) {
+        float v[kGroupUnroll];
+#pragma unroll
+        for (int u = 0; u < kGroupUnroll; ++u) v[u] = part[(q + u) * cols + j];
+#pragma unroll
+        for (int u = 0; u < kGroupUnroll; ++u) acc = acc + v[u];
+    }
+    for (; q < groups; ++q) acc = acc + part[q * cols + j];
+    out[j] = acc;
+}
+
+// Scalar forms for widths that are not a multiple of 4 or unaligned pointers.
+__global__ void add_row_bias_scalar(const float* a, const float* bias, float* out, int64_t rows, int64_t cols) {
+    const int64_t n = rows * cols;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = a[i] + bias[i % cols];
+}
+__global__ void sum_rows_scalar(const float* g, float* out, int64_t rows, int64_t cols) {
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < cols; j += (int64_t)gridDim.x * blockDim.x) {
+        float acc = g[j];
+        for (int64_t r = 1; r < rows; ++r) acc = acc + g[r * cols + j];
+        out[j] = acc;
+    }
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+unsigned blocks_for(int64_t n) {
+    int64_t b = (n + kThreads - 1) / kThreads;
+    if (b > 65536) b = 65536;
+    return (unsigned)(b < 1 ? 1 : b);
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t cleave_hip_add_row_bias_f32(const float* a, int64_t alen, const float* bias, int64_t blen, float* out,
+                                    int64_t outlen, int32_t rows, int32_t cols) {
+    const char* fn = "cleave_hip_add_row_bias_f32";
+    CH_REQUIRE(rows >= 0 && cols >= 0, "%s: negative shape (%d x %d)", fn, rows, cols);
+    CH_REQUIRE(alen == (int64_t)rows * cols && outlen == alen, "%s: a/out lengths (%lld, %lld) != rows*cols %lld",
+               fn, (long long)alen, (long long)outlen, (long long)rows * cols);
+    CH_REQUIRE(blen == cols, "%s: bias length %lld != cols %d", fn, (long long)blen, cols);
+    if (alen == 0) return CLEAVE_HIP_OK;
+    CH_REQUIRE(a && bias && out, "%s: null buffer", fn);
+    CH_INIT_OR_RETURN();
+    if (cols % 4 == 0 && aligned16(a) && aligned16(bias) && aligned16(out)) {
+        const Tiling t = tiling_bias(rows, cols);
+        add_row_bias_kernel<<<(unsigned)(t.nseg * t.groups), kThreads, 0, ch::stream()>>>(
+            a, bias, out, rows, cols, t.nseg, t.rows_per_group);
+    } else {
+        add_row_bias_scalar<<<blocks_for(alen), kThreads, 0, ch::stream()>>>(a, bias, out, rows, cols);
+    }
+    CH_LAUNCHED(fn);
+    return CLEAVE_HIP_OK;
+}
+
+int32_t cleave_hip_sum_rows_f32(const float* g, int64_t glen, float* out, int64_t outlen, int32_t rows,
+                                int32_t cols) {
+    const char* fn = "cleave_hip_sum_rows_f32";
+    CH_REQUIRE(rows >= 1 && cols >= 0, "%s: need at least one row (%d x %d)", fn, rows, cols);
+    CH_REQUIRE(glen == (int64_t)rows * cols, "%s: g length %lld != rows*cols %lld", fn, (long long)glen,
+               (long long)rows * cols);
+    CH_REQUIRE(outlen == cols, "%s: out length %lld != cols %d", fn, (long long)outlen, cols);
+    if (cols == 0) return CLEAVE_HIP_OK;
+    CH_REQUIRE(g && out, "%s: null buffer", fn);
+    CH_INIT_OR_RETURN();
+    if (cols % 4 == 0 && aligned16(g)) {
+        const Tiling t = tiling_sum(rows, cols);
+        float* part = (float*)ch::scratch(5, sizeof(float) * (size_t)(t.groups * cols));
+        if (!part) return ch::fail(CLEAVE_HIP_ERR_OOM, "%s: scratch of %lld floats", fn, (long long)(t.groups * cols));
+        sum_rows_stage1<<<(unsigned)(t.nseg * t.groups), kThreads, 0, ch::stream()>>>(g, part, rows, cols, t.nseg,
+                                                                                       t.rows_per_group);
+        CH_LAUNCHED(fn);
+        sum_rows_stage2<<<blocks_for(cols), kThreads, 0, ch::stream()>>>(part, out, t.groups, cols);
+    } else {
+        sum_rows_scalar<<<blocks_for(cols), kThreads, 0, ch::stream()>>>(g, out, rows, cols);
+    }
+    CH_LAUNCHED(fn);
+    return CLEAVE_HIP_OK;
+}
+
+}  // extern "C"

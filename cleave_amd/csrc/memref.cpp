@@ -245,6 +245,37 @@ int32_t _mlir_ciface_cleave_hip_sgd_update_f32(cleave_hip_mr w, cleave_hip_mr g,
                                      reinterpret_cast<const float*>(G.data), G.count, lr);
 }
 
+int32_t _mlir_ciface_cleave_hip_add_row_bias_f32(cleave_hip_mr a, cleave_hip_mr bias, cleave_hip_mr out) {
+    const char* fn = "_mlir_ciface_cleave_hip_add_row_bias_f32";
+    View A, Bv, O;
+    CH_TRY(flat_view(a, 4, fn, "a", nullptr, &A));
+    CH_REQUIRE(A.rank == 2, "%s: a must be [rows x cols]", fn);
+    CH_TRY(flat_view(bias, 4, fn, "bias", nullptr, &Bv));
+    CH_REQUIRE(Bv.count == A.sizes[1] && (Bv.rank == 1 || (Bv.rank == 2 && Bv.sizes[0] == 1)),
+               "%s: bias must be [cols] or [1 x cols]", fn);
+    CH_TRY(flat_view(out, 4, fn, "out", &A, &O));
+    int32_t rows, cols;
+    CH_TRY(narrow(A.sizes[0], fn, "rows", &rows));
+    CH_TRY(narrow(A.sizes[1], fn, "cols", &cols));
+    return cleave_hip_add_row_bias_f32(reinterpret_cast<const float*>(A.data), A.count,
+                                       reinterpret_cast<const float*>(Bv.data), Bv.count,
+                                       reinterpret_cast<float*>(O.data), O.count, rows, cols);
+}
+
+int32_t _mlir_ciface_cleave_hip_sum_rows_f32(cleave_hip_mr g, cleave_hip_mr out) {
+    const char* fn = "_mlir_ciface_cleave_hip_sum_rows_f32";
+    View G, O;
+    CH_TRY(flat_view(g, 4, fn, "g", nullptr, &G));
+    CH_REQUIRE(G.rank == 2, "%s: g must be [rows x cols]", fn);
+    CH_TRY(flat_view(out, 4, fn, "out", nullptr, &O));
+    CH_REQUIRE(O.count == G.sizes[1], "%s: out must hold cols = %lld elements", fn, (long long)G.sizes[1]);
+    int32_t rows, cols;
+    CH_TRY(narrow(G.sizes[0], fn, "rows", &rows));
+    CH_TRY(narrow(G.sizes[1], fn, "cols", &cols));
+    return cleave_hip_sum_rows_f32(reinterpret_cast<const float*>(G.data), G.count,
+                                   reinterpret_cast<float*>(O.data), O.count, rows, cols);
+}
+
 float _mlir_ciface_cleave_hip_sum_f32(cleave_hip_mr x) {
     View X;
     if (flat_view(x, 4, "_mlir_ciface_cleave_hip_sum_f32", "x", nullptr, &X) != CLEAVE_HIP_OK) return NAN;

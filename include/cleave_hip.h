@@ -186,6 +186,22 @@ CLEAVE_HIP_API int32_t cleave_hip_sgd_update_f32(float* w, int64_t wlen, const f
                                   float lr);
 
 /* ---------------------------------------------------------------------- */
+/* A bias shared by every row of a batch (extension: the reference's add    */
+/* needs equal shapes, stdlib/linalg/tensor.cleave:66-71, and adds a         */
+/* same-shape bias one example at a time, examples/xor_tensor.cleave:44-49) */
+/* ---------------------------------------------------------------------- */
+
+/* out[i*cols + j] = a[i*cols + j] + bias[j] for a row-major [rows x cols] a.
+ * Requires alen == outlen == rows*cols and blen == cols. */
+CLEAVE_HIP_API int32_t cleave_hip_add_row_bias_f32(const float* a, int64_t alen, const float* bias, int64_t blen,
+                                                   float* out, int64_t outlen, int32_t rows, int32_t cols);
+/* Reverse rule of that broadcast: out[j] = sum over i of g[i*cols + j]
+ * (device order: ascending rows within fixed row groups, then the groups in
+ * order).  Requires rows >= 1, glen == rows*cols, outlen == cols. */
+CLEAVE_HIP_API int32_t cleave_hip_sum_rows_f32(const float* g, int64_t glen, float* out, int64_t outlen,
+                                               int32_t rows, int32_t cols);
+
+/* ---------------------------------------------------------------------- */
 /* Sum / Mean / Max (stdlib/nn/nn.cleave:111-149)                           */
 /* ---------------------------------------------------------------------- */
 

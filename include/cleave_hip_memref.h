@@ -89,6 +89,11 @@ CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_div_bwd_f32(cleave_hip_mr a, clea
                                                           cleave_hip_mr da, cleave_hip_mr db);
 CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_sgd_update_f32(cleave_hip_mr w, cleave_hip_mr g, float lr);
 
+/* Row-broadcast bias: a, out [rows x cols], bias [cols] (or [1 x cols]);
+ * its reverse rule sums g [rows x cols] over the rows into out [cols]. */
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_add_row_bias_f32(cleave_hip_mr a, cleave_hip_mr bias, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_sum_rows_f32(cleave_hip_mr g, cleave_hip_mr out);
+
 /* Sum / Mean / Max (stdlib/nn/nn.cleave:111-149), host-returning. */
 CLEAVE_HIP_API float _mlir_ciface_cleave_hip_sum_f32(cleave_hip_mr x);
 CLEAVE_HIP_API float _mlir_ciface_cleave_hip_mean_f32(cleave_hip_mr x);

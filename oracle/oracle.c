@@ -236,6 +236,25 @@ void or_div_bwd_f32(const float* a, const float* b, const float* g, float* da, f
 }
 
 /* ------------------------------------------------------------------------ */
+/* A bias shared by every row: the batched form of the reference's          */
+/* same-shape `matmul(x, w) + b1` (examples/xor_tensor.cleave:44-49), and    */
+/* its reverse rule (the cotangent summed over the broadcast rows).         */
+/* ------------------------------------------------------------------------ */
+
+void or_add_row_bias_f32(const float* a, const float* bias, float* out, int32_t rows, int32_t cols) {
+    for (int64_t i = 0; i < rows; ++i)
+        for (int64_t j = 0; j < cols; ++j) out[i * cols + j] = a[i * cols + j] + bias[j];
+}
+/* Left fold down each column from row 0, like Sum (stdlib/nn/nn.cleave:111-117). */
+void or_sum_rows_f32(const float* g, float* out, int32_t rows, int32_t cols) {
+    for (int64_t j = 0; j < cols; ++j) {
+        float acc = g[j];
+        for (int64_t i = 1; i < rows; ++i) acc = acc + g[i * cols + j];
+        out[j] = acc;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* Index (stdlib/linalg/tensor.cleave:113-133): tensor.extract over the     */
 /* row-major buffer (cleave/src/mlir_lower.rs:1968-2002).                   */
 /* ------------------------------------------------------------------------ */

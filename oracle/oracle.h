@@ -91,6 +91,15 @@ void or_relu_bwd_f32(const float* x, const float* g, float* out, int64_t n);
 void or_div_bwd_f32(const float* a, const float* b, const float* g, float* da, float* db,
                     int64_t n);
 
+/* ---- a bias shared by every row (batched form of examples/xor_tensor.cleave:44-49) ---- */
+
+/* out[i][j] = a[i][j] + bias[j].  Pinned: numpy broadcasting bit for bit; one
+ * row is the reference's same-shape Ring add (or_add_f32). */
+void or_add_row_bias_f32(const float* a, const float* bias, float* out, int32_t rows, int32_t cols);
+/* out[j] = left fold of g[i][j] over i from row 0.  Pinned: exact integer
+ * sums, a fold-order case that cancels differently, float64 bound. */
+void or_sum_rows_f32(const float* g, float* out, int32_t rows, int32_t cols);
+
 /* ---- Index (stdlib/linalg/tensor.cleave:113-133) ---- */
 
 /* tensor.extract over the row-major buffer (cleave/src/mlir_lower.rs:1968-2002):

@@ -53,6 +53,8 @@ _SIGS = {
     "or_max_of_f32": (_f, [_p, _i64]),
     "or_argmax_f32": (_i64, [_p, _i64]),
     "or_index_f32": (_i32, [_p, _p, _i32, _p, _p]),
+    "or_add_row_bias_f32": (None, [_p, _p, _p, _i32, _i32]),
+    "or_sum_rows_f32": (None, [_p, _p, _i32, _i32]),
     "or_index_bwd_f32": (_i32, [_f, _p, _p, _i32, _p]),
     "or_sum_u32_u64": (_u64, [_p, _i64]),
     "or_escape_count_f32": (C.c_uint32, [_f, _f, _i32]),
@@ -208,6 +210,25 @@ def div_bwd(a, b, g):
     da, db = np.empty_like(a), np.empty_like(a)
     lib().or_div_bwd_f32(_ptr(a), _ptr(b), _ptr(g), _ptr(da), _ptr(db), a.size)
     return da, db
+
+
+# ---- row-broadcast bias ----------------------------------------------------------------
+
+def add_row_bias(a, bias) -> np.ndarray:
+    a, bias = _f32(a), _f32(bias)
+    rows, cols = a.shape
+    assert bias.shape == (cols,)
+    out = np.empty_like(a)
+    lib().or_add_row_bias_f32(_ptr(a), _ptr(bias), _ptr(out), rows, cols)
+    return out
+
+
+def sum_rows(g) -> np.ndarray:
+    g = _f32(g)
+    rows, cols = g.shape
+    out = np.empty(cols, np.float32)
+    lib().or_sum_rows_f32(_ptr(g), _ptr(out), rows, cols)
+    return out
 
 
 # ---- Index ---------------------------------------------------------------------------

@@ -138,3 +138,38 @@ def test_index_bwd_is_the_reverse_of_the_index_rule(hip, oracle):
         hip.index_bwd(g, dt, idx)
         oracle.index_bwd(g, want, idx)
     assert np.array_equal(dt.numpy(), want)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 8), (37, 64), (1000, 1028), (513, 100), (64, 4096), (7, 13), (300, 3)])
+def test_add_row_bias_matches_the_oracle_bitwise(hip, oracle, rows, cols):
+    # vector path (cols % 4 == 0) and the scalar path (cols = 13, 3)
+    rng = np.random.default_rng(rows * 131 + cols)
+    A = rng.standard_normal((rows, cols)).astype(np.float32)
+    b = rng.standard_normal(cols).astype(np.float32)
+    out = hip.add_row_bias(hip.from_numpy(A), hip.from_numpy(b)).numpy()
+    assert np.array_equal(out, oracle.add_row_bias(A, b))
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 8), (37, 64), (1000, 1028), (4097, 96), (7, 13), (300, 3)])
+def test_sum_rows_against_the_left_fold(hip, oracle, rows, cols):
+    rng = np.random.default_rng(rows * 7 + cols)
+    # integer-valued cotangents: every summation order is exact, so bit-equal
+    G = rng.integers(-512, 512, (rows, cols)).astype(np.float32)
+    assert np.array_equal(hip.sum_rows(hip.from_numpy(G)).numpy(), oracle.sum_rows(G))
+    # general values: within the sum tolerance, relative to sum |g| per column
+    G = rng.standard_normal((rows, cols)).astype(np.float32)
+    got = hip.sum_rows(hip.from_numpy(G)).numpy().astype(np.float64)
+    want = oracle.sum_rows(G).astype(np.float64)
+    scale = np.abs(G).astype(np.float64).sum(axis=0)
+    assert np.all(np.abs(got - want) <= 1e-5 * scale + 1e-30)
+
+
+def test_sum_rows_is_deterministic_and_at_full_size(hip):
+    # the H-sized cotangent of config 4's hidden layer: sums of a constant are exact
+    g = hip.empty((65536, 4096))
+    hip.fill_uniform(g, seed=5, lo=0.25, hi=0.25)
+    s1 = hip.sum_rows(g).numpy()
+    assert np.all(s1 == np.float32(0.25 * 65536))
+    x = hip.fill_normal(hip.empty((8192, 1024)), seed=6)
+    a, b = hip.sum_rows(x).numpy(), hip.sum_rows(x).numpy()
+    assert np.array_equal(a, b)

@@ -81,6 +81,17 @@ def test_div_bwd_zero_and_sgd(hip, mr):
     assert not w.numpy().any()
 
 
+def test_row_bias_and_its_reverse_rule(hip, mr):
+    a, b = _rand(hip, (40, 24), 16), _rand(hip, (24,), 17)
+    want = hip.add_row_bias(a, b).numpy()
+    out = hip.empty((40, 24))
+    mr.call("cleave_hip_add_row_bias_f32", mr.of(a), mr.of(b, (1, 24)), mr.of(out))
+    assert np.array_equal(out.numpy(), want)
+    s = hip.empty((24,))
+    mr.call("cleave_hip_sum_rows_f32", mr.of(a), mr.of(s))
+    assert np.array_equal(s.numpy(), hip.sum_rows(a).numpy())
+
+
 def test_reductions_match_pointer_forms(hip, mr):
     x = _rand(hip, (64, 129), 13)
     assert mr.call("cleave_hip_sum_f32", mr.of(x)) == hip.sum(x)

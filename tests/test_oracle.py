@@ -238,6 +238,33 @@ def test_reference_derivative_known_answers(oracle, golden):
     assert len(d) == len(golden["derivatives"])  # every source is distinct
 
 
+# ---- row-broadcast bias ---------------------------------------------------------
+
+def test_add_row_bias_is_broadcast_add(oracle):
+    rng = np.random.default_rng(31)
+    a = rng.standard_normal((37, 19)).astype(np.float32)
+    b = rng.standard_normal(19).astype(np.float32)
+    assert np.array_equal(oracle.add_row_bias(a, b), a + b[None, :])
+    # one row is the reference's own same-shape bias add (xor_tensor, batch of 1)
+    assert np.array_equal(oracle.add_row_bias(a[:1], b)[0], oracle.add(a[0], b))
+
+
+def test_sum_rows_is_a_left_fold_down_each_column(oracle):
+    rng = np.random.default_rng(32)
+    ints = rng.integers(-1000, 1000, (300, 7)).astype(np.float32)
+    assert np.array_equal(oracle.sum_rows(ints), ints.sum(axis=0, dtype=np.float64).astype(np.float32))
+    # the fold order decides what cancels: ((1e8 + 1) - 1e8) = 0 in f32, 1 in exact arithmetic
+    g = np.array([[1e8, 1.0], [1.0, 1e8], [-1e8, -1e8]], np.float32)
+    assert list(oracle.sum_rows(g)) == [0.0, 0.0]
+    g2 = np.array([[1.0, 1.0], [1e8, 1e8], [-1e8, -1e8]], np.float32)
+    assert list(oracle.sum_rows(g2)) == [0.0, 0.0]
+    h = np.array([[1e8, 1e8], [-1e8, -1e8], [1.0, 1.0]], np.float32)
+    assert list(oracle.sum_rows(h)) == [1.0, 1.0]
+    x = rng.standard_normal((500, 9)).astype(np.float32)
+    exact = x.astype(np.float64).sum(axis=0)
+    assert np.all(np.abs(oracle.sum_rows(x) - exact) <= 500 * 2**-24 * np.abs(x).astype(np.float64).sum(axis=0))
+
+
 # ---- Index ----------------------------------------------------------------------
 
 @pytest.mark.parametrize("shape", [(7,), (3, 5), (2, 3, 4), (2, 1, 3, 5)])
