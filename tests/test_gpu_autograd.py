@@ -1,0 +1,122 @@
+"""Reverse-mode tape over the library's operators (cleave_amd/autograd.py), on the GPU.
+
+Pinned three ways: every operator's rule against central differences of a float64
+restatement of the same program; the tape's MLP gradients against the fused
+cleave_hip_mlp_step_f32; and the reference's own xor_tensor training record
+(doc/backlog.md:142), now reached by differentiating the forward pass instead of
+hand-written backward code."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ad(hip):
+    from cleave_amd import autograd
+    return autograd
+
+
+def _sig(x):
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+def test_every_rule_against_float64_finite_differences(hip, ad):
+    rng = np.random.default_rng(40)
+    X = rng.standard_normal((8, 5)).astype(np.float32)
+    Y = rng.uniform(0.1, 0.9, (8, 3)).astype(np.float32)
+    D = rng.uniform(1.0, 2.0, (8, 3)).astype(np.float32)
+    P = {"W1": rng.standard_normal((5, 6)).astype(np.float32) * 0.5,
+         "b1": rng.standard_normal(6).astype(np.float32) * 0.1,
+         "W2": rng.standard_normal((6, 3)).astype(np.float32) * 0.5}
+
+    def f64(p):
+        h = np.tanh(X.astype(np.float64) @ p["W1"] + p["b1"])
+        r = np.maximum(h + 2.0, 0.0)                # relu on a strictly positive input
+        z = _sig(r @ p["W2"])
+        e = z - Y
+        q = (e * e) / D - (-e) * 0.5 * e            # div, neg and mul rules
+        return q.mean() + q.sum() * 0.01 + (h + 2.0)[1, 2]
+
+    v = {k: ad.param(a) for k, a in P.items()}
+    x, y, d = ad.const(X), ad.const(Y), ad.const(D)
+    half = ad.const(np.full((8, 3), 0.5, np.float32))
+    two = ad.const(np.full((8, 6), 2.0, np.float32))
+    cent = ad.const(np.full((1,), 0.01, np.float32))
+    h = ad.tanh(ad.add_row_bias(x @ v["W1"], v["b1"]))
+    hp = h + two
+    r = ad.relu(hp)
+    z = ad.sigmoid(r @ v["W2"])
+    e = z - y
+    q = (e * e) / d - (-e) * half * e
+    loss = ad.mean(q) + ad.sum(q) * cent + ad.index(hp, (1, 2))
+    ad.backward(loss)
+    assert abs(float(loss.numpy()[0]) - f64({k: a.astype(np.float64) for k, a in P.items()})) < 1e-4
+    eps = 1e-3
+    for k, a in P.items():
+        base = {n: b.astype(np.float64) for n, b in P.items()}
+        num = np.zeros(a.shape)
+        for i in np.ndindex(a.shape):
+            up, dn = {n: b.copy() for n, b in base.items()}, {n: b.copy() for n, b in base.items()}
+            up[k][i] += eps
+            dn[k][i] -= eps
+            num[i] = (f64(up) - f64(dn)) / (2 * eps)
+        got = v[k].grad.numpy().reshape(a.shape)
+        assert np.allclose(got, num, rtol=2e-3, atol=2e-4), (k, np.abs(got - num).max())
+
+
+def test_tape_gradients_match_the_fused_mlp_step(hip, ad):
+    B, D, Hd = 512, 256, 512
+    rng = np.random.default_rng(41)
+    X = rng.standard_normal((B, D)).astype(np.float32)
+    Y = (rng.random(B) < 0.5).astype(np.float32)
+    W1 = rng.uniform(-0.05, 0.05, (D, Hd)).astype(np.float32)
+    W2 = rng.uniform(-0.05, 0.05, Hd).astype(np.float32)
+    dw1, dw2 = hip.empty((D, Hd)), hip.empty(Hd)
+    hip.mlp_step(hip.from_numpy(X), hip.from_numpy(Y), hip.from_numpy(W1), hip.from_numpy(W2), 0.0,
+                 dw1=dw1, dw2=dw2)
+    w1, w2 = ad.param(W1), ad.param(W2.reshape(Hd, 1))
+    yhat = ad.sigmoid(ad.sigmoid(ad.const(X) @ w1) @ w2)
+    e = yhat - ad.const(Y.reshape(B, 1))
+    ad.backward(ad.mean(e * e))
+    for got, want in [(w1.grad.numpy(), dw1.numpy()), (w2.grad.numpy().ravel(), dw2.numpy())]:
+        assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max() + 1e-9
+
+
+def test_xor_tensor_record_through_the_tape(hip, ad, golden):
+    """examples/xor_tensor.cleave:38-92: forward as the reference writes it,
+    `grad = derive(loss)` as a backward pass over the tape, SGD with lr 1.0."""
+    g = golden["xor_tensor"]
+    xs = np.array([[0, 0], [0, 1], [1, 0], [1, 1]], np.float32)
+    ys = np.array([0, 1, 1, 0], np.float32)
+    W = ad.param(np.array([[0.5, 0.5], [0.5, -0.5]], np.float32))
+    b1 = ad.param(np.array([[-0.2, -0.2]], np.float32))
+    W2 = ad.param(np.array([[1.0], [-1.0]], np.float32))
+    b2 = ad.param(np.array([[0.0]], np.float32))
+    X = [ad.const(xs[i:i + 1].copy()) for i in range(4)]
+    Y = [ad.const(ys[i:i + 1].copy()) for i in range(4)]
+
+    def forward(i):
+        h = ad.sigmoid(X[i] @ W + b1)
+        return ad.sigmoid(ad.index(h @ W2 + b2, (0, 0)))
+
+    for step in range(g["steps"]):
+        i = step % 4
+        err = forward(i) - Y[i]
+        for p in (W, b1, W2, b2):
+            p.grad = None
+        ad.backward(err * err)
+        for p in (W, b1, W2, b2):
+            hip.sgd_update(p.tensor, p.grad, g["lr"])
+    preds = [float(forward(i).numpy()[0]) for i in range(4)]
+    assert np.allclose(preds, g["predictions"], atol=2e-6, rtol=0), preds
+
+
+def test_shape_errors_are_raised_before_any_kernel(hip, ad):
+    a, b = ad.param(np.zeros((2, 3), np.float32)), ad.param(np.zeros((3, 2), np.float32))
+    with pytest.raises(ValueError, match="no broadcasting"):
+        ad.add(a, b)
+    with pytest.raises(ValueError, match="one element"):
+        ad.backward(a)
