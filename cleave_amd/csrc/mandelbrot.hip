@@ -26,9 +26,22 @@ namespace {
 // radius, so a lane whose first escape is iteration n counts exactly n and one
 // that never escapes counts max_iter (the reference's `escaped`/`count` latch,
 // examples/mandelbrot.cleave:14-26).  The wave leaves once no lane is alive.
-// Per iteration: 8 arithmetic ops, a compare, a mask update and an add -- no
-// branch.
+// Per iteration: 8 arithmetic ops, a compare, a mask update (scalar) and an
+// add -- no branch.
 constexpr int kBlockIters = 8;
+
+// count + 1 in the lanes set in `lanes` (a wave lane mask), as one
+// v_addc_co_u32 whose carry-in is that mask: one VALU op per iteration where
+// `count += alive ? 1 : 0` takes a select and half of a three-way add.
+// The carry-out goes to a scratch SGPR pair of its own, so consecutive
+// iterations do not serialise on VCC (which the compares write).
+__device__ __forceinline__ uint32_t count_lanes(uint32_t count, uint64_t lanes) {
+    uint32_t r;
+    uint64_t carry_out;
+    asm("v_addc_co_u32_e64 %0, %1, 0, %2, %3" : "=v"(r), "=s"(carry_out) : "v"(count), "s"(lanes));
+    (void)carry_out;
+    return r;
+}
 
 __global__ __launch_bounds__(256) void mandelbrot_kernel(uint32_t* __restrict__ out, int width,
                                                          int height, float x0, float y0, float dx,
@@ -41,7 +54,9 @@ __global__ __launch_bounds__(256) void mandelbrot_kernel(uint32_t* __restrict__ 
     const float ci = y0 + (float)row * dy;
     float zr = 0.0f, zi = 0.0f, zr2 = 0.0f, zi2 = 0.0f;
     uint32_t count = 0;
-    bool alive = inside;
+    // The lanes still inside the radius, as a wave mask: the escape compare
+    // writes a mask, a scalar AND narrows it, and the count add reads it.
+    uint64_t alive = __builtin_amdgcn_ballot_w64(inside);
     int n = 0;
     // Whole blocks: lanes past their escape keep iterating (z may overflow to
     // inf/NaN, which no longer matters: the count is latched).
@@ -55,14 +70,13 @@ __global__ __launch_bounds__(256) void mandelbrot_kernel(uint32_t* __restrict__ 
             zi = im + ci;
             zr2 = zr * zr;
             zi2 = zi * zi;
-            alive = alive && !(zr2 + zi2 > 4.0f);
-            count += alive ? 1u : 0u;
+            alive &= __builtin_amdgcn_ballot_w64(!(zr2 + zi2 > 4.0f));
+            count = count_lanes(count, alive);
         }
-        if (!__any(alive)) break;
+        if (alive == 0) break;
     }
     // Remaining max_iter % kBlockIters iterations (only when some lane survived).
-    for (int m = n; m < max_iter && __any(alive); ++m) {
-        (void)m;
+    for (int m = n; m < max_iter && alive != 0; ++m) {
         const float p = zr * zi;
         const float re = zr2 - zi2;
         const float im = p + p;
@@ -70,8 +84,8 @@ __global__ __launch_bounds__(256) void mandelbrot_kernel(uint32_t* __restrict__ 
         zi = im + ci;
         zr2 = zr * zr;
         zi2 = zi * zi;
-        alive = alive && !(zr2 + zi2 > 4.0f);
-        count += alive ? 1u : 0u;
+        alive &= __builtin_amdgcn_ballot_w64(!(zr2 + zi2 > 4.0f));
+        count = count_lanes(count, alive);
     }
     if (inside) out[(int64_t)row * width + col] = count;
 }
