@@ -22,8 +22,13 @@ namespace ch {
 //     columns of H[row][col] * w2[col] (a partial of z2 = H W2).
 //   MODE 2 (dW1 = X^T d1, split-K over the batch): B is H, and each operand
 //     value h of column n at batch row k becomes d1 = (d2[k] w2[n]) h (1 - h)
-//     as the MFMA consumes it; the waves of the first M-tile also accumulate
-//     dw2part[split][n] = sum_k h d2[k].  d2 reaches LDS with the k-tile.
+//     as the MFMA consumes it.  The same values give dW2[n] = sum_k h d2[k]:
+//     each k-block's contribution is taken by exactly one wave -- M-tile tm
+//     takes the k-tiles with kt % tiles_m == tm and, within them, row-half wm
+//     the k-block kb == wm -- so every workgroup carries an equal share, and
+//     each wave writes its partial to
+//     dw2part[((split * tiles_m + tm) * WM + wm) * N + n].  d2 reaches LDS
+//     with the k-tile.
 struct MlpFuse {
     const float* w2 = nullptr;
     const float* d2 = nullptr;
@@ -105,7 +110,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
     v4f d2v[2];               // MODE 2: d2 at this lane's 4 k of the k-block
     float w2c[FN];            // MODE 2: w2 at this lane's column of fragment j
     v4f dw2acc[FN];           // MODE 2: partial dW2 of that column
-    const bool do_dw2 = MODE == 2 && tm == 0 && wm == 0;
+    static_assert(MODE != 2 || (BK / 8) % WM == 0, "each row-half wave takes whole k-blocks of a k-tile");
+    // MODE 2: does this wave accumulate dW2 for k-block kb of k-tile kt?
+    auto dw2_mine = [&](int kt, int kb) { return (kt % tiles_m) == tm && (kb % WM) == wm; };
     if constexpr (MODE == 2) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
@@ -125,12 +132,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
     // MODE 2: d1 = (d2[k] w2[n]) h (1 - h), the order of the reference step.
     // Applied to a k-block's fragments right after the previous block's MFMAs
     // are issued, so this VALU work overlaps the matrix core.
-    auto transform = [&](int buf) {
+    auto transform = [&](int buf, bool mine) {
         if constexpr (MODE == 2) {
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
                 const v4f h = fb[buf][j];
-                if (do_dw2) dw2acc[j] += h * d2v[buf];
+                if (mine) dw2acc[j] += h * d2v[buf];
 #pragma unroll
                 for (int s = 0; s < 4; ++s) fb[buf][j][s] = (d2v[buf][s] * w2c[j]) * h[s] * (1.0f - h[s]);
             }
@@ -164,7 +171,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
     asm volatile("s_barrier" ::: "memory");
     if (STAGES - 1 < nk) issue(STAGES - 1, STAGES - 1);
     read_block(0, smem, 0);
-    transform(0);
+    transform(0, dw2_mine(0, 0));
 
     for (int kt = 0; kt < nk; ++kt) {
         const char* tile = smem + (kt % STAGES) * P::STAGE_BYTES;
@@ -172,7 +179,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
         for (int kb = 0; kb + 1 < KB; ++kb) {
             read_block((kb & 1) ^ 1, tile, kb + 1);
             mfma_block(kb & 1);
-            transform((kb & 1) ^ 1);
+            transform((kb & 1) ^ 1, dw2_mine(kt, kb + 1));
         }
 #pragma unroll
         for (int g = 0; g < (KB - 1) * NM; ++g) {
@@ -191,7 +198,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
             if (kt + STAGES < nk) issue(kt + STAGES, kt % STAGES);
         }
         mfma_block((KB - 1) & 1);
-        if (kt + 1 < nk) transform(0);
+        if (kt + 1 < nk) transform(0, dw2_mine(kt + 1, 0));
     }
 
     const int half = lane >> 5, col = lane & 31;
@@ -231,13 +238,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
         }
     }
     if constexpr (MODE == 2) {
-        if (do_dw2) {
+        // every wave writes its partial (zero when it took no k-block)
+        float* dst = fuse.dw2part + ((int64_t)(bt * tiles_m + tm) * WM + wm) * N + n0 + wn * P::TN + col;
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                float v = (dw2acc[j][0] + dw2acc[j][1]) + (dw2acc[j][2] + dw2acc[j][3]);
-                v += __shfl_xor(v, 32);
-                if (half == 0) fuse.dw2part[(int64_t)bt * N + n0 + wn * P::TN + j * 32 + col] = v;
-            }
+        for (int j = 0; j < FN; ++j) {
+            float v = (dw2acc[j][0] + dw2acc[j][1]) + (dw2acc[j][2] + dw2acc[j][3]);
+            v += __shfl_xor(v, 32);
+            if (half == 0) dst[j * 32] = v;
         }
     }
 #pragma unroll

@@ -76,20 +76,44 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(const float* __restr
 }
 
 // Fused path, after the MODE-1 GEMM: z2[row] = sum of the P partials of
-// H[row] . W2, then the same per-row loss pieces as row_pass_kernel.
+// H[row] . W2 (in order; loads eight at a time), then the same per-row loss
+// pieces as row_pass_kernel.  Each block also reduces its rows' squared
+// errors into sqpart[block] (wave shuffles, then the 4 wave sums in order),
+// which loss_kernel adds up.
+constexpr int kPartUnroll = 8;
 __global__ __launch_bounds__(kThreads) void row_finish_kernel(const float* __restrict__ zpart, int P,
                                                               const float* __restrict__ y, int B,
-                                                              float* __restrict__ sq,
+                                                              float* __restrict__ sqpart,
                                                               float* __restrict__ d2) {
+    __shared__ float wsum[kThreads / 64];
     const int row = blockIdx.x * kThreads + threadIdx.x;
-    if (row >= B) return;
-    float z = zpart[row];
-    for (int p = 1; p < P; ++p) z += zpart[(int64_t)p * B + row];
-    const float yh = sigmoidf_ref(z);
-    const float e = yh - y[row];
-    sq[row] = e * e;
-    const float gy = (e + e) / (float)B;
-    d2[row] = gy * yh * (1.0f - yh);
+    float sq = 0.0f;
+    if (row < B) {
+        float z = zpart[row];
+        int p = 1;
+        for (; p + kPartUnroll <= P; p += kPartUnroll) {
+            float v[kPartUnroll];
+#pragma unroll
+            for (int u = 0; u < kPartUnroll; ++u) v[u] = zpart[(int64_t)(p + u) * B + row];
+#pragma unroll
+            for (int u = 0; u < kPartUnroll; ++u) z += v[u];
+        }
+        for (; p < P; ++p) z += zpart[(int64_t)p * B + row];
+        const float yh = sigmoidf_ref(z);
+        const float e = yh - y[row];
+        sq = e * e;
+        const float gy = (e + e) / (float)B;
+        d2[row] = gy * yh * (1.0f - yh);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = sq;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float r = wsum[0];
+        for (int w = 1; w < kThreads / 64; ++w) r += wsum[w];
+        sqpart[blockIdx.x] = r;
+    }
 }
 
 // Column pass: each thread owns 4 consecutive columns of a band of rows.
@@ -132,11 +156,13 @@ __global__ __launch_bounds__(kThreads) void sum_slices_sgd_kernel(const float* _
     }
 }
 
-__global__ __launch_bounds__(kThreads) void loss_kernel(const float* __restrict__ sq, int B,
+// loss = (sum of the n values v) / count: per-row squared errors (unfused
+// path, n = B) or per-block sums of them (fused path).
+__global__ __launch_bounds__(kThreads) void loss_kernel(const float* __restrict__ v, int n, float count,
                                                         float* __restrict__ loss) {
     __shared__ float part[kThreads / 64];
     float acc = 0.0f;
-    for (int i = threadIdx.x; i < B; i += kThreads) acc += sq[i];
+    for (int i = threadIdx.x; i < n; i += kThreads) acc += v[i];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
@@ -144,7 +170,7 @@ __global__ __launch_bounds__(kThreads) void loss_kernel(const float* __restrict_
     if (threadIdx.x == 0) {
         float r = 0.0f;
         for (int w = 0; w < kThreads / 64; ++w) r += part[w];
-        *loss = r / (float)B;
+        *loss = r / count;
     }
 }
 
@@ -190,8 +216,11 @@ int32_t fused_step(const float* x, const float* y, float* w1, float* w2, float* 
                    float* loss_dev, int B, int D, int Hd, float lr, hipStream_t st) {
     const int splits = fused_splits(B, D, Hd);
     const int P = (Hd / 256) * 4;  // H W2 partials per row (tiles_n x waves along N)
+    const int row_blocks = (B + kThreads - 1) / kThreads;
+    // dW2 partials: one per (split, M-tile, row-half wave), see MlpFuse
+    const int dw2_slices = splits * (D / 256) * 2;
     // Scratch slot 4: H | zpart | sq | d2 | dW2 partials | dW1 slices | loss.
-    const size_t nH = (size_t)B * Hd, nZ = (size_t)P * B, nPart = (size_t)splits * Hd,
+    const size_t nH = (size_t)B * Hd, nZ = (size_t)P * B, nPart = (size_t)dw2_slices * Hd,
                  nSl = (size_t)splits * D * Hd;
     auto up = [](size_t n) { return (n + 63) & ~(size_t)63; };
     const size_t total = up(nH) + up(nZ) + up(B) + up(B) + up(nPart) + up(nSl) + 64;
@@ -212,9 +241,10 @@ int32_t fused_step(const float* x, const float* y, float* w1, float* w2, float* 
         <<<dim3((unsigned)((B / 256) * (Hd / 256))), FusedTile1::THREADS, 0, st>>>(
             x, w1, H, B, Hd, D, D, Hd, 0, 0, 0, B / 256, Hd / 256, 1, f1);
     CH_LAUNCHED("gemm_f32_tiled_kernel(MODE 1)");
-    row_finish_kernel<<<(B + kThreads - 1) / kThreads, kThreads, 0, st>>>(zpart, P, y, B, sq, d2);
+    row_finish_kernel<<<row_blocks, kThreads, 0, st>>>(zpart, P, y, B, sq, d2);
     CH_LAUNCHED("row_finish_kernel");
-    loss_kernel<<<1, kThreads, 0, st>>>(sq, B, loss_dev ? loss_dev : loss_tmp);
+    // mean of the squared errors: the row blocks' sums, added in order, over B
+    loss_kernel<<<1, kThreads, 0, st>>>(sq, row_blocks, (float)B, loss_dev ? loss_dev : loss_tmp);
     CH_LAUNCHED("loss_kernel");
     const int kk = B / splits;
     ch::MlpFuse f2;
@@ -228,7 +258,7 @@ int32_t fused_step(const float* x, const float* y, float* w1, float* w2, float* 
     CH_LAUNCHED("gemm_f32_tiled_kernel(MODE 2)");
     sum_slices_sgd_kernel<<<capped_grid((int64_t)D * Hd), kThreads, 0, st>>>(slices, splits, (int64_t)D * Hd, dw1, w1, lr);
     CH_LAUNCHED("sum_slices_sgd_kernel(dW1)");
-    sum_slices_sgd_kernel<<<capped_grid(Hd), kThreads, 0, st>>>(part, splits, Hd, dw2, w2, lr);
+    sum_slices_sgd_kernel<<<capped_grid(Hd), kThreads, 0, st>>>(part, dw2_slices, Hd, dw2, w2, lr);
     CH_LAUNCHED("sum_slices_sgd_kernel(dW2)");
     return CLEAVE_HIP_OK;
 }
@@ -275,7 +305,7 @@ extern "C" int32_t cleave_hip_mlp_step_f32(const float* x, int64_t xlen, const f
     CH_LAUNCHED("sigmoid_inplace_kernel");
     row_pass_kernel<<<(B + 3) / 4, kThreads, 0, st>>>(H, w2, y, B, Hd, sq, d2);
     CH_LAUNCHED("row_pass_kernel");
-    loss_kernel<<<1, kThreads, 0, st>>>(sq, B, loss_dev ? loss_dev : loss_tmp);
+    loss_kernel<<<1, kThreads, 0, st>>>(sq, B, (float)B, loss_dev ? loss_dev : loss_tmp);
     CH_LAUNCHED("loss_kernel");
     dim3 cgrid((unsigned)((Hd + 4 * kThreads - 1) / (4 * kThreads)), (unsigned)bands);
     col_pass_kernel<<<cgrid, kThreads, 0, st>>>(H, w2, d2, B, Hd, part);
