@@ -20,6 +20,7 @@
 #pragma once
 
 #include "gemm_common.hpp"
+#include "gemm_pingpong.hpp"  // wait_tiles
 #include "gemm_tiles.hpp"
 
 namespace ch {
@@ -41,15 +42,6 @@ struct Bf16PingPong {
         return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
     }
 };
-
-// s_waitcnt vmcnt(n * LPW) lgkmcnt(0) for a runtime tile count n in 0..3.
-template <int LPW>
-__device__ __forceinline__ void wait_tiles(int n) {
-    if (n >= 3) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(3 * LPW) : "memory");
-    else if (n == 2) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * LPW) : "memory");
-    else if (n == 1) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(LPW) : "memory");
-    else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-}
 
 template <bool AKC, bool BKC, bool PRIO = true, int STAGES_ = 4>
 __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(

@@ -1,9 +1,10 @@
 // gemm_f32.hip -- fp32 matmul on CDNA4 matrix cores (v_mfma_f32_32x32x2f32).
 //
-// Shapes that divide a 256 x 256 x 16 or 128 x 128 x 16 tile run the
-// large-tile kernel of gemm_f32_tiled.hpp (LDS filled by global_load_lds,
-// four MFMA k-steps per 16-byte operand read).  Everything else runs the
-// general kernel below.
+// Shapes that divide a 256 x 256 x 16 tile, with a tile per CU, run the
+// ping-pong kernel of gemm_f32_pingpong.hpp; shapes that divide a
+// 128 x 128 x 16 tile run the large-tile kernel of gemm_f32_tiled.hpp (LDS
+// filled by global_load_lds, four MFMA k-steps per 16-byte operand read).
+// Everything else runs the general kernel below.
 //
 // Replaces linalg.matmul as cleave lowers it (stdlib/linalg/matrix.cleave:27-61,
 // region cleave/src/mlir_lower.rs:2089-2120): C = 0; C[i,j] += A[i,k]*B[k,j].
@@ -28,6 +29,7 @@
 //     path needs M % BM == N % BN == K % BK == 0.
 #include "common.hpp"
 #include "gemm_common.hpp"
+#include "gemm_f32_pingpong.hpp"
 #include "gemm_f32_tiled.hpp"
 
 namespace {
@@ -240,16 +242,33 @@ bool launch_tiled(const float* a, const float* b, float* c, int M, int N, int K,
     return true;
 }
 
+// Ping-pong kernel (gemm_f32_pingpong.hpp) when the shape divides its
+// 256 x 256 x 16 tile; false when it does not.
+template <bool TA, bool TB>
+bool launch_pingpong(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
+                     int64_t ldb, int batch, int64_t sA, int64_t sB, int64_t sC, int32_t* status) {
+    using P = ch::F32PingPong<!TA, TB>;
+    if (!P::fits(M, N, K, lda, ldb) || ((uintptr_t)a & 15) || ((uintptr_t)b & 15) || (sA % 4) || (sB % 4))
+        return false;
+    const int tiles_m = M / P::BM, tiles_n = N / P::BN;
+    if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
+    dim3 grid((unsigned)(tiles_m * tiles_n * batch));
+    ch::gemm_f32_pingpong_kernel<!TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
+        a, b, c, M, N, K, lda, ldb, sA, sB, sC, tiles_m, tiles_n, batch);
+    *status = ch::check_hip(hipGetLastError(), "gemm_f32_pingpong_kernel");
+    return true;
+}
+
 template <bool TA, bool TB>
 int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
                int64_t ldb, int64_t ldc, int batch, int64_t sA, int64_t sB, int64_t sC) {
     int32_t st = CLEAVE_HIP_OK;
     if (ldc == N) {
-        // 256 x 256 x 16 tile (8 waves of 128 x 64) when it still yields a tile
-        // per CU, else 128 x 128 x 16 (4 waves of 64 x 64).
+        // 256 x 256 x 16 tile (ping-pong, 8 waves of 128 x 64) when it still
+        // yields a tile per CU, else 128 x 128 x 16 (4 waves of 64 x 64).
         const int64_t big_tiles = (int64_t)(M / 256) * (N / 256) * batch;
         if (big_tiles >= ch::num_cus() &&
-            launch_tiled<256, 256, 16, 2, 4, 2, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
+            launch_pingpong<TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
             return st;
         if (launch_tiled<128, 128, 16, 2, 2, 2, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
             return st;

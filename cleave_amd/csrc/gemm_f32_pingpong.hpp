@@ -1,0 +1,337 @@
+// gemm_f32_pingpong.hpp -- f32 GEMM on the ping-pong schedule of
+// gemm_pingpong.hpp (gfx950, v_mfma_f32_32x32x2f32, 256 x 256 x 16 tiles).
+//
+// Eight waves; each owns a 128 x 64 block of C (4 x 2 tiles of 32 x 32).
+// Waves 0-3 (group 0, rows 0-127) and 4-7 (group 1, rows 128-255) sit one
+// per SIMD.  A C phase is the k-tile's 64 MFMAs (two 8-deep k-blocks of four
+// k=2 steps), 4096 matrix-core cycles, so the two barriers per k-tile cost
+// little next to it; the single-barrier schedule of gemm_f32_tiled.hpp
+// stops both waves of a SIMD at every k-tile.
+//
+// Both operands sit in LDS k-major, whatever their layout in global memory,
+// and every fragment is read with ds_read2st64_b32 (two k-rows, one float
+// per lane).  Measured at 4096^3 with the k-contiguous operand kept
+// k-contiguous in LDS and read with ds_read_b128, the M phase cost 0.911 of
+// peak against 0.962 for the k-major form; LDS writes in the M phase cost
+// nothing measurable.  So the operands move in two ways:
+//   m/n-contiguous in global memory (A^T stored K x M, B stored K x N):
+//     global_load_lds straight into the k-major tile;
+//   k-contiguous (A stored M x K, B^T stored N x K): 16 bytes per lane
+//     (4 k of one row) into registers one k-tile ahead, then written to the
+//     k-major tile with ds_write2st64_b32 ("staged").
+// LDS holds each operand as [16 k-rows][4 stages][256 floats] (64 KiB; A at
+// 0, B at 64 KiB): one k-row of one stage is the 1 KiB a copy instruction
+// writes, and every fragment, k-row and stage of an operand is one
+// loop-invariant register plus an immediate offset below 64 KiB.  So the M
+// phase issues no VALU instruction; the accumulators live in AGPRs.
+// Within a 1 KiB row, 16-byte chunk c of k-row kr sits in slot
+// mn_slot<4>(kr, c) (gemm_tiles.hpp), which keeps the two half-waves of a
+// fragment read, at k-rows kr and kr + 4, in opposite bank halves.
+#pragma once
+
+#include "gemm_common.hpp"
+#include "gemm_pingpong.hpp"
+#include "gemm_tiles.hpp"
+
+namespace ch {
+
+template <bool AKC, bool BKC>
+struct F32PingPong {
+    static constexpr int BM = 256, BN = 256, BK = 16, NW = 8, WN = 4, THREADS = 64 * NW;
+    static constexpr int TM = 128, TN = 64, FM = TM / 32, FN = TN / 32, KB = BK / 8, STAGES = kPingPongStages;
+    static constexpr int A_BYTES = BM * BK * 4, B_BYTES = BN * BK * 4;  // one stage of one operand
+    static constexpr int ROW = BM * 4;                                    // one k-row of one stage
+    static constexpr int KROW = STAGES * ROW;                             // k-row pitch
+    static constexpr int OP_BYTES = BK * KROW, LDS_BYTES = 2 * OP_BYTES;  // A at 0, B at OP_BYTES
+    // Per wave and k-tile: global_load_lds instructions of the m/n-contiguous
+    // operands, and 16-byte staged loads of the k-contiguous ones.
+    static constexpr int OP_LOADS = A_BYTES / 1024 / NW;  // per operand
+    static constexpr int LDMA = OP_LOADS * ((AKC ? 0 : 1) + (BKC ? 0 : 1));
+    static constexpr int LSTAGED = OP_LOADS * ((AKC ? 1 : 0) + (BKC ? 1 : 0));
+    static_assert(A_BYTES == B_BYTES && OP_LOADS == 2 && OP_BYTES == 65536, "operand tiles of 16 KiB");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS per workgroup");
+
+    static bool fits(int M, int N, int K, int64_t lda, int64_t ldb) {
+        const bool dims = M % BM == 0 && N % BN == 0 && K % BK == 0 && lda % 4 == 0 && ldb % 4 == 0;
+        const uint64_t a_span = (AKC ? (uint64_t)M : (uint64_t)BK + 1) * (uint64_t)lda * 4;
+        const uint64_t b_span = (BKC ? (uint64_t)N : (uint64_t)BK + 1) * (uint64_t)ldb * 4;
+        return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
+    }
+};
+
+namespace f32pp {
+
+typedef __attribute__((address_space(3))) float lds_float;
+__device__ __forceinline__ const lds_float* lds_ptr(uint32_t a) { return (const lds_float*)(uintptr_t)a; }
+__device__ __forceinline__ lds_float* lds_ptr_w(uint32_t a) { return (lds_float*)(uintptr_t)a; }
+
+// Hide a value from the optimiser so it stays one register (the compiler
+// would otherwise re-derive addresses from the lane id inside the loop).
+template <class T>
+__device__ __forceinline__ void opaque(T& v) { asm volatile("" : "+v"(v)); }
+
+// One staged load: 16 bytes per lane at byte offset voff + soff of the
+// operand behind rsrc.  A buffer load: the per-lane offset is one VGPR and
+// the k-tile's offset one SGPR, so no VALU address arithmetic; and an
+// ordinary (not inline-asm) load, so the compiler knows the registers are in
+// flight and waits (vmcnt) before their first use -- including any register
+// copy it makes.  The compiler does not count the global_load_lds copies
+// (inline asm), so its waits can only be longer than needed, never shorter.
+__device__ __forceinline__ tiles::v4f load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, soff, 0);
+}
+// Raw buffer resource over [p, p + 4 GiB): gfx9-family word 3 (32-bit
+// untyped elements); offsets past the end would read as zero, not fault.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)0xFFFFFFFF, 0x00020000);
+}
+
+// Staged copy of a k-contiguous operand tile [256 rows][16 k] into its
+// k-major LDS region.  Load q (q = wave + 8 j) covers rows 16q .. 16q+15,
+// lane l taking row 16q + l/4, k-chunk l%4 (64 bytes of each row per load);
+// its four floats go to k-rows 4*(l%4) + s, column row.  One register set
+// (data) in the loop: the M phase writes tile u+1 to LDS before loading tile
+// u+2 into it.
+template <int NW, int KROW, int ROW>
+struct Staged {
+    static constexpr int R = 256, BK = 16, PER_WAVE = R * BK * 4 / 1024 / NW;
+    static_assert(PER_WAVE == 2, "two loads per wave");
+    uint32_t voff[PER_WAVE];
+    uint32_t waddr[PER_WAVE];  // LDS address of (k-row 4*kc, stage 0, column row)
+    tiles::v4f data[PER_WAVE];
+
+    __device__ __forceinline__ void init(int64_t ld, int r0, int wave, int lane, uint32_t region) {
+#pragma unroll
+        for (int j = 0; j < PER_WAVE; ++j) {
+            const int q = wave + NW * j;
+            const int row = 16 * q + (lane >> 2), kc = lane & 3;
+            voff[j] = (uint32_t)(((int64_t)(r0 + row) * ld + 4 * kc) * 4);
+            // mn_slot<4>(4*kc + s, row/4) does not depend on s
+            waddr[j] = region + (uint32_t)(4 * kc * KROW + tiles::mn_slot<4>(4 * kc, row >> 2) * 16 + (row & 3) * 4);
+            opaque(voff[j]);
+            opaque(waddr[j]);
+        }
+    }
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rsrc, uint32_t kt_off, tiles::v4f (&d)[PER_WAVE]) const {
+#pragma unroll
+        for (int j = 0; j < PER_WAVE; ++j) d[j] = load16(rsrc, voff[j], kt_off);
+    }
+    // Write registers d into LDS stage ST.
+    template <int ST>
+    __device__ __forceinline__ void store(const tiles::v4f (&d)[PER_WAVE]) const {
+#pragma unroll
+        for (int j = 0; j < PER_WAVE; ++j)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) lds_ptr_w(waddr[j] + ST * ROW + s * KROW)[0] = d[j][s];
+    }
+};
+
+// global_load_lds copy of an m/n-contiguous operand tile [16 k][256 rows]:
+// instruction q (q = wave + 8 j) moves k-row q, lane l fetching the 16-byte
+// chunk that belongs in slot l of the row.
+template <int NW, int KROW>
+struct Direct {
+    static constexpr int R = 256, BK = 16, PER_WAVE = BK / NW;
+    static_assert(PER_WAVE == 2, "two k-rows per wave");
+    uint32_t voff[PER_WAVE];
+    uint32_t dst[PER_WAVE];  // LDS address of k-row q, stage 0 (SGPR-uniform)
+
+    __device__ __forceinline__ void init(int64_t ld, int r0, int wave, int lane, uint32_t region) {
+#pragma unroll
+        for (int j = 0; j < PER_WAVE; ++j) {
+            const int kr = wave + NW * j;
+            const int c = tiles::mn_slot<4>(kr, lane);  // slot lane holds chunk c (the XOR is its own inverse)
+            voff[j] = (uint32_t)(((int64_t)kr * ld + r0 + 4 * c) * 4);
+            dst[j] = region + (uint32_t)(kr * KROW);
+        }
+    }
+    __device__ __forceinline__ void issue(const char* sbase_kt, uint32_t stage_off) const {
+#pragma unroll
+        for (int j = 0; j < PER_WAVE; ++j) tiles::dma16(sbase_kt, voff[j], dst[j] + stage_off);
+    }
+};
+
+}  // namespace f32pp
+
+template <bool AKC, bool BKC>
+__global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
+    int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC, int tiles_m, int tiles_n,
+    int batch) {
+    using namespace ch::tiles;
+    using namespace ch::f32pp;
+    using P = F32PingPong<AKC, BKC>;
+    constexpr int FM = P::FM, FN = P::FN, NW = P::NW, BK = P::BK, KB = P::KB, S = P::STAGES;
+    constexpr int ROW = P::ROW, KROW = P::KROW;
+    constexpr bool STAGED = AKC || BKC;
+    __shared__ __attribute__((aligned(1024))) char smem[P::LDS_BYTES];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = wave / P::WN, wn = wave % P::WN;  // grp is also the wave's row block
+    int bt, tm, tn;
+    ch::block_coords(blockIdx.x, tiles_m, tiles_n, batch, bt, tm, tn);
+    const int m0 = tm * P::BM, n0 = tn * P::BN;
+    A += (int64_t)bt * strideA;
+    B += (int64_t)bt * strideB;
+    C += (int64_t)bt * strideC;
+    const uint32_t lds0 = lds_addr(smem);
+    const int nk = K / BK;
+
+    const uint32_t region_a = lds0, region_b = lds0 + P::OP_BYTES;
+    // m/n-contiguous operands: global_load_lds into the k-major tile.
+    Direct<NW, KROW> dma_a, dma_b;
+    // k-contiguous operands: staged through registers.
+    Staged<NW, KROW, ROW> st_a, st_b;
+    if constexpr (!AKC) dma_a.init(lda, m0, wave, lane, region_a);
+    else st_a.init(lda, m0, wave, lane, region_a);
+    if constexpr (!BKC) dma_b.init(ldb, n0, wave, lane, region_b);
+    else st_b.init(ldb, n0, wave, lane, region_b);
+    // byte step of an operand's base per k-tile
+    const int64_t step_a = AKC ? (int64_t)BK * 4 : (int64_t)BK * lda * 4;
+    const int64_t step_b = BKC ? (int64_t)BK * 4 : (int64_t)BK * ldb * 4;
+    const char* a_base = reinterpret_cast<const char*>(A);
+    const char* b_base = reinterpret_cast<const char*>(B);
+
+    // Copies of k-tile kt into stage kt % S.  With STAGED the M phase copies
+    // unconditionally: past the last k-tile the source is clamped to it (in
+    // bounds) and the bytes land in a stage no later M phase reads.
+    auto issue_dma = [&](int kt) {
+        const uint32_t stage_off = (uint32_t)((kt % S) * ROW);
+        const int src = min(kt, nk - 1);
+        if constexpr (!AKC) dma_a.issue(a_base + src * step_a, stage_off);
+        if constexpr (!BKC) dma_b.issue(b_base + src * step_b, stage_off);
+    };
+    const __amdgpu_buffer_rsrc_t rsrc_a = raw_rsrc(A), rsrc_b = raw_rsrc(B);
+    auto load_staged = [&](int kt) {
+        const uint32_t src = (uint32_t)min(kt, nk - 1);
+        if constexpr (AKC) st_a.load(rsrc_a, src * (uint32_t)step_a, st_a.data);
+        if constexpr (BKC) st_b.load(rsrc_b, src * (uint32_t)step_b, st_b.data);
+    };
+    auto store_staged = [&](auto stage) {
+        constexpr int ST = decltype(stage)::value;
+        if constexpr (AKC) st_a.template store<ST>(st_a.data);
+        if constexpr (BKC) st_b.template store<ST>(st_b.data);
+    };
+
+    // Fragment read addresses: fragment f (A: f < FM, B: f >= FM) of k-block
+    // kb, step s, stage ST sits at rd[f] + (8kb + s)*KROW + ST*ROW.  Half-wave
+    // h reads k-rows 8kb + 4h + s; mn_slot<4> depends on kr only through
+    // (kr >> 2) & 1 = h.
+    uint32_t rd[FM + FN];
+    {
+        const int h = lane >> 5;
+#pragma unroll
+        for (int f = 0; f < FM + FN; ++f) {
+            const int col = f < FM ? grp * P::TM + f * 32 + (lane & 31) : wn * P::TN + (f - FM) * 32 + (lane & 31);
+            rd[f] = (f < FM ? region_a : region_b) +
+                    (uint32_t)(4 * h * KROW + mn_slot<4>(4 * h, col >> 2) * 16 + (col & 3) * 4);
+            opaque(rd[f]);
+        }
+    }
+
+    v16f acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = v16f{};
+    v4f fa[KB][FM], fb[KB][FN];
+
+    // M phase for k-tile u in stage ST: fragments of tile u; then the staged
+    // operand of tile u+1 (loaded in the previous M phase; for u = 0 the
+    // prologue wrote it) into its stage;
+    // then the staged loads of tile u+2 (into the same registers) and the
+    // global_load_lds of tile u+3; then wait for the LDS reads and writes.
+    // Before the staged store the compiler waits for its loads with vmcnt(0)
+    // (it counts no load issued after them), which also covers the copy of
+    // tile u+1, issued a phase before them.  The wave issued nothing in the
+    // other group's phase, so that wait finds loads a k-tile old.  Stage
+    // (u+1)%4 last held tile u-3 and stage (u+3)%4 tile u-1, both read by
+    // both groups before this phase.
+    auto m_phase = [&](auto stage, int u) {
+        constexpr int ST = decltype(stage)::value;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const uint32_t off = (8 * kb + s) * KROW + ST * ROW;
+#pragma unroll
+                for (int i = 0; i < FM; ++i) fa[kb][i][s] = *lds_ptr(rd[i] + off);
+#pragma unroll
+                for (int j = 0; j < FN; ++j) fb[kb][j][s] = *lds_ptr(rd[FM + j] + off);
+            }
+        if constexpr (STAGED) {
+            if (u > 0) store_staged(PingPongStage<(ST + 1) % S>{});  // the prologue wrote tile 1
+            load_staged(u + 2);
+            issue_dma(u + S - 1);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        } else {
+            pingpong_copy<P::LDMA>(u, nk, issue_dma);
+        }
+    };
+    // Half-wave h holds k = 8*kb + 4*h + s at step s for both operands, so the
+    // four steps of a k-block complete its 8-deep k-sum.
+    auto c_phase = [&]() {
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[kb][i][s], fb[kb][j][s], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) asm volatile("" : "+a"(acc[i][j]));  // accumulators stay in AGPRs
+    };
+
+    if constexpr (STAGED) {
+        // Prologue: tiles 0 and 1 in stages 0 and 1 (staged parts written,
+        // copied parts landed), the copy of tile 2 in flight.  Tile 1's staged
+        // registers are temporaries: no staged register is live when the
+        // groups' loops begin.
+        {
+            v4f t1a[2], t1b[2];
+            load_staged(0);
+            if constexpr (AKC) st_a.load(rsrc_a, (uint32_t)min(1, nk - 1) * (uint32_t)step_a, t1a);
+            if constexpr (BKC) st_b.load(rsrc_b, (uint32_t)min(1, nk - 1) * (uint32_t)step_b, t1b);
+            issue_dma(0);
+            issue_dma(1);
+            issue_dma(2);
+            store_staged(PingPongStage<0>{});
+            if constexpr (AKC) st_a.template store<1>(t1a);
+            if constexpr (BKC) st_b.template store<1>(t1b);
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        }
+        pingpong_schedule<P::LDMA>(nk, grp, [](int) {}, m_phase, c_phase, /*prologue_copies=*/false);
+        // the clamped copies past the last k-tile must land before the
+        // workgroup's LDS is released
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+        pingpong_schedule<P::LDMA>(nk, grp, issue_dma, m_phase, c_phase, /*prologue_copies=*/true);
+    }
+
+    // 32 x 32 accumulator layout: lane holds column l%32, rows 8*(v/4) + 4*(l/32) + v%4.
+    // One tile at a time out of the AGPRs (the asm keeps the compiler from
+    // reading all 128 first, which would need 128 more VGPRs).
+    const int half = lane >> 5, col = lane & 31;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            v16f t = acc[i][j];
+            asm volatile("" : "+v"(t)::"memory");
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int r = m0 + grp * P::TM + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+                const int c = n0 + wn * P::TN + j * 32 + col;
+                C[(int64_t)r * N + c] = t[v];
+            }
+        }
+}
+
+}  // namespace ch

@@ -226,3 +226,39 @@ def test_big_tile_path_every_layout(hip, oracle, dtype, ta, tb):
     ref, absden = oracle.matmul_entries(A, B, M, N, K, ii, jj, trans_a=bool(ta), trans_b=bool(tb),
                                         bf16=(dtype == "bf16"))
     assert_gemm_close(c[ii, jj], ref, absden, K, f"{dtype} big tile ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("K", [16, 48, 80])
+def test_f32_pingpong_short_k(hip, oracle, K, ta, tb):
+    # 1, 3 and 5 k-tiles of 16: the ring of four LDS stages is never filled,
+    # or wraps once, so the copies past the last k-tile (clamped to it) and
+    # the prologue's two tiles are all exercised
+    M = N = 4096
+    a = hip.fill_normal(hip.empty((K, M) if ta else (M, K)), seed=81 + K + 2 * ta + tb)
+    b = hip.fill_normal(hip.empty((N, K) if tb else (K, N)), seed=91 + K + 2 * ta + tb)
+    c = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    A, B = a.numpy(), b.numpy()
+    ii, jj = sample_entries(M, N, 1024, seed=K + ta + 2 * tb)
+    ref, absden = oracle.matmul_entries(A, B, M, N, K, ii, jj, trans_a=bool(ta), trans_b=bool(tb))
+    assert_gemm_close(c[ii, jj], ref, absden, K, f"f32 short K={K} ta={ta} tb={tb}")
+    # every row sum, in float64
+    Ad = (A.T if ta else A).astype(np.float64)
+    Bd = (B.T if tb else B).astype(np.float64)
+    rows = Ad @ Bd.sum(axis=1)
+    den = np.abs(Ad) @ np.abs(Bd).sum(axis=1)
+    assert np.max(np.abs(c.astype(np.float64).sum(axis=1) - rows) / den) <= 1e-5 * np.sqrt(K)
+
+
+def test_f32_batched_through_pingpong(hip, oracle):
+    # 16 products of 1024 x 1024 (16 tiles of 256 x 256 each, 256 in all):
+    # the batch strides go through the ping-pong kernel
+    bsz, M, N, K = 16, 1024, 1024, 64
+    rng = np.random.default_rng(17)
+    A = rng.standard_normal((bsz, M, K)).astype(np.float32)
+    B = rng.standard_normal((bsz, K, N)).astype(np.float32)
+    got = hip.matmul_batched(hip.from_numpy(A), hip.from_numpy(B)).numpy()
+    for i in (0, 7, 15):
+        ii, jj = sample_entries(M, N, 256, seed=i)
+        ref, absden = oracle.matmul_entries(A[i], B[i], M, N, K, ii, jj)
+        assert_gemm_close(got[i][ii, jj], ref, absden, K, f"batched f32 entry {i}")
