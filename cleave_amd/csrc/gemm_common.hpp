@@ -50,4 +50,14 @@ __device__ __forceinline__ void block_coords(int bid, int tiles_m, int tiles_n, 
     tn = in_group / gsize;
 }
 
+// Operands of the fused epilogues and operand transforms of the two GEMMs
+// of the MLP step (mlp.hip); a plain GEMM passes {}.  The f32 kernels
+// document what each MODE does with them.
+struct MlpFuse {
+    const float* w2 = nullptr;
+    const float* d2 = nullptr;
+    float* zpart = nullptr;
+    float* dw2part = nullptr;
+};
+
 }  // namespace ch

@@ -254,7 +254,7 @@ bool launch_pingpong(const float* a, const float* b, float* c, int M, int N, int
     if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
     dim3 grid((unsigned)(tiles_m * tiles_n * batch));
     ch::gemm_f32_pingpong_kernel<!TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
-        a, b, c, M, N, K, lda, ldb, sA, sB, sC, tiles_m, tiles_n, batch);
+        a, b, c, M, N, K, lda, ldb, sA, sB, sC, tiles_m, tiles_n, batch, ch::MlpFuse{});
     *status = ch::check_hip(hipGetLastError(), "gemm_f32_pingpong_kernel");
     return true;
 }

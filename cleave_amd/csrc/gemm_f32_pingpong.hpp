@@ -27,6 +27,19 @@
 // Within a 1 KiB row, 16-byte chunk c of k-row kr sits in slot
 // mn_slot<4>(kr, c) (gemm_tiles.hpp), which keeps the two half-waves of a
 // fragment read, at k-rows kr and kr + 4, in opposite bank halves.
+//
+// MODE carries the fusions of the MLP step (mlp.hip), as in
+// gemm_f32_tiled.hpp with the row-half wave wm = group and WN = 4:
+//   MODE 1 (H = sigmoid(X W1), A staged, B copied): sigmoid in the epilogue,
+//     and zpart[(tn*4 + wn)*M + row] = sum over the wave's 64 columns of
+//     H[row][col] * w2[col];
+//   MODE 2 (dW1 slice = X^T d1, both operands copied): B is H; each B value
+//     h of column n at batch row k becomes d1 = (d2[k] w2[n]) h (1 - h) in the
+//     C phase before its MFMAs, and the wave owning the k-block (k-tile kt of
+//     M-tile kt % tiles_m, k-block kb of group kb % 2) adds h d2[k] to its
+//     dW2 partial, written to dw2part[((split*tiles_m + tm)*2 + grp)*N + n].
+//     d2 reaches LDS with the k-tile (every wave copies the same 64 bytes, so
+//     each wave's count of copies stays uniform).
 #pragma once
 
 #include "gemm_common.hpp"
@@ -35,21 +48,25 @@
 
 namespace ch {
 
-template <bool AKC, bool BKC>
+template <bool AKC, bool BKC, int MODE = 0>
 struct F32PingPong {
     static constexpr int BM = 256, BN = 256, BK = 16, NW = 8, WN = 4, THREADS = 64 * NW;
     static constexpr int TM = 128, TN = 64, FM = TM / 32, FN = TN / 32, KB = BK / 8, STAGES = kPingPongStages;
     static constexpr int A_BYTES = BM * BK * 4, B_BYTES = BN * BK * 4;  // one stage of one operand
     static constexpr int ROW = BM * 4;                                    // one k-row of one stage
     static constexpr int KROW = STAGES * ROW;                             // k-row pitch
-    static constexpr int OP_BYTES = BK * KROW, LDS_BYTES = 2 * OP_BYTES;  // A at 0, B at OP_BYTES
+    static constexpr int OP_BYTES = BK * KROW;                           // A at 0, B at OP_BYTES
+    static constexpr int D2_BYTES = MODE == 2 ? STAGES * BK * 4 : 0;        // MODE 2: d2 per stage
+    static constexpr int LDS_BYTES = 2 * OP_BYTES + D2_BYTES;
     // Per wave and k-tile: global_load_lds instructions of the m/n-contiguous
-    // operands, and 16-byte staged loads of the k-contiguous ones.
+    // operands (and of d2), and 16-byte staged loads of the k-contiguous ones.
     static constexpr int OP_LOADS = A_BYTES / 1024 / NW;  // per operand
-    static constexpr int LDMA = OP_LOADS * ((AKC ? 0 : 1) + (BKC ? 0 : 1));
+    static constexpr int LDMA = OP_LOADS * ((AKC ? 0 : 1) + (BKC ? 0 : 1)) + (MODE == 2 ? 1 : 0);
     static constexpr int LSTAGED = OP_LOADS * ((AKC ? 1 : 0) + (BKC ? 1 : 0));
     static_assert(A_BYTES == B_BYTES && OP_LOADS == 2 && OP_BYTES == 65536, "operand tiles of 16 KiB");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS per workgroup");
+    static_assert(MODE == 0 || (MODE == 1 && AKC && !BKC) || (MODE == 2 && !AKC && !BKC),
+                  "MODE 1 is the NN form, MODE 2 the TN form");
 
     static bool fits(int M, int N, int K, int64_t lda, int64_t ldb) {
         const bool dims = M % BM == 0 && N % BN == 0 && K % BK == 0 && lda % 4 == 0 && ldb % 4 == 0;
@@ -153,14 +170,14 @@ struct Direct {
 
 }  // namespace f32pp
 
-template <bool AKC, bool BKC>
+template <bool AKC, bool BKC, int MODE = 0>
 __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
     int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC, int tiles_m, int tiles_n,
-    int batch) {
+    int batch, MlpFuse fuse) {
     using namespace ch::tiles;
     using namespace ch::f32pp;
-    using P = F32PingPong<AKC, BKC>;
+    using P = F32PingPong<AKC, BKC, MODE>;
     constexpr int FM = P::FM, FN = P::FN, NW = P::NW, BK = P::BK, KB = P::KB, S = P::STAGES;
     constexpr int ROW = P::ROW, KROW = P::KROW;
     constexpr bool STAGED = AKC || BKC;
@@ -196,11 +213,18 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
     // Copies of k-tile kt into stage kt % S.  With STAGED the M phase copies
     // unconditionally: past the last k-tile the source is clamped to it (in
     // bounds) and the bytes land in a stage no later M phase reads.
+    // MODE 2: this split's d2 slice starts at batch row bt * K.
+    const float* d2 = MODE == 2 ? fuse.d2 + (int64_t)bt * K : nullptr;
+    const uint32_t region_d2 = lds0 + 2u * P::OP_BYTES;
     auto issue_dma = [&](int kt) {
         const uint32_t stage_off = (uint32_t)((kt % S) * ROW);
         const int src = min(kt, nk - 1);
         if constexpr (!AKC) dma_a.issue(a_base + src * step_a, stage_off);
         if constexpr (!BKC) dma_b.issue(b_base + src * step_b, stage_off);
+        if constexpr (MODE == 2) {
+            if (lane < BK / 4)
+                dma16(d2 + (int64_t)src * BK, (uint32_t)(lane * 16), region_d2 + (uint32_t)((kt % S) * BK * 4));
+        }
     };
     const __amdgpu_buffer_rsrc_t rsrc_a = raw_rsrc(A), rsrc_b = raw_rsrc(B);
     auto load_staged = [&](int kt) {
@@ -237,6 +261,22 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
         for (int j = 0; j < FN; ++j) acc[i][j] = v16f{};
     v4f fa[KB][FM], fb[KB][FN];
 
+    // MODE 2: d2 at this lane's k-rows of each k-block, w2 at its columns,
+    // and the dW2 partial of those columns.
+    v4f d2v[KB];
+    float w2c[FN];
+    v4f dw2acc[FN];
+    uint32_t rd_d2 = 0;
+    if constexpr (MODE == 2) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            w2c[j] = fuse.w2[n0 + wn * P::TN + j * 32 + (lane & 31)];
+            dw2acc[j] = v4f{};
+        }
+        rd_d2 = region_d2 + (uint32_t)(16 * (lane >> 5));  // k = 8kb + 4h + s
+        opaque(rd_d2);
+    }
+
     // M phase for k-tile u in stage ST: fragments of tile u; then the staged
     // operand of tile u+1 (loaded in the previous M phase; for u = 0 the
     // prologue wrote it) into its stage;
@@ -260,6 +300,12 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
 #pragma unroll
                 for (int j = 0; j < FN; ++j) fb[kb][j][s] = *lds_ptr(rd[FM + j] + off);
             }
+        if constexpr (MODE == 2) {
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+                d2v[kb] = *reinterpret_cast<const __attribute__((address_space(3))) v4f*>(
+                    (uintptr_t)(rd_d2 + ST * BK * 4 + kb * 32));
+        }
         if constexpr (STAGED) {
             if (u > 0) store_staged(PingPongStage<(ST + 1) % S>{});  // the prologue wrote tile 1
             load_staged(u + 2);
@@ -271,10 +317,21 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
     };
     // Half-wave h holds k = 8*kb + 4*h + s at step s for both operands, so the
     // four steps of a k-block complete its 8-deep k-sum.
-    auto c_phase = [&]() {
+    auto c_phase = [&](int u) {
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
+        for (int kb = 0; kb < KB; ++kb) {
+            if constexpr (MODE == 2) {
+                // d1 = (d2[k] w2[n]) h (1 - h), the order of the reference step
+                const bool mine = (u % tiles_m) == tm && kb % 2 == grp;
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const v4f h = fb[kb][j];
+                    if (mine) dw2acc[j] += h * d2v[kb];
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) fb[kb][j][s] = (d2v[kb][s] * w2c[j]) * h[s] * (1.0f - h[s]);
+                }
+            }
 #pragma unroll
             for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -282,6 +339,7 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
 #pragma unroll
                     for (int j = 0; j < FN; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[kb][i][s], fb[kb][j][s], acc[i][j], 0, 0, 0);
+        }
         __builtin_amdgcn_s_setprio(0);
 #pragma unroll
         for (int i = 0; i < FM; ++i)
@@ -316,15 +374,44 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
     }
 
     // 32 x 32 accumulator layout: lane holds column l%32, rows 8*(v/4) + 4*(l/32) + v%4.
-    // One tile at a time out of the AGPRs (the asm keeps the compiler from
-    // reading all 128 first, which would need 128 more VGPRs).
+    // One row of tiles at a time out of the AGPRs (the asm keeps the compiler
+    // from reading all 128 first, which would need 128 more VGPRs).
     const int half = lane >> 5, col = lane & 31;
+    if constexpr (MODE == 2) {
+        // every wave writes its partial (zero when it took no k-block)
+        float* dst = fuse.dw2part + ((int64_t)(bt * tiles_m + tm) * 2 + grp) * N + n0 + wn * P::TN + col;
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+        for (int j = 0; j < FN; ++j) {
+            float v = (dw2acc[j][0] + dw2acc[j][1]) + (dw2acc[j][2] + dw2acc[j][3]);
+            v += __shfl_xor(v, 32);
+            if (half == 0) dst[j * 32] = v;
+        }
+    }
+    float w2j[FN];
+    if constexpr (MODE == 1) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) w2j[j] = fuse.w2[n0 + wn * P::TN + j * 32 + col];
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        float zs[16];  // MODE 1: per row, the sum of H * w2 over the wave's columns
+#pragma unroll
+        for (int v = 0; v < 16; ++v) zs[v] = 0.0f;
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             v16f t = acc[i][j];
             asm volatile("" : "+v"(t)::"memory");
+            if constexpr (MODE == 1) {
+                // H = sigmoid(acc) = 1 / (1 + exp(-acc)) with the hardware exp2
+                // and reciprocal (about 1 ulp each)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const float e = __builtin_amdgcn_exp2f(-t[v] * 1.4426950408889634f);
+                    const float h = __builtin_amdgcn_rcpf(1.0f + e);
+                    t[v] = h;
+                    zs[v] += h * w2j[j];
+                }
+            }
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int r = m0 + grp * P::TM + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
@@ -332,6 +419,19 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
                 C[(int64_t)r * N + c] = t[v];
             }
         }
+        if constexpr (MODE == 1) {
+            // lanes of a half-wave hold the 32 columns of the same rows
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+#pragma unroll
+                for (int o = 16; o > 0; o >>= 1) zs[v] += __shfl_xor(zs[v], o);
+            if (col == 0) {
+                float* zp = fuse.zpart + (int64_t)(tn * P::WN + wn) * M;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) zp[m0 + grp * P::TM + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3)] = zs[v];
+            }
+        }
+    }
 }
 
 }  // namespace ch

@@ -16,7 +16,8 @@
 
 namespace ch {
 
-// Fusions for the two GEMMs of the MLP step (mlp.hip); plain GEMMs pass {}.
+// Fusions for the two GEMMs of the MLP step (mlp.hip, MlpFuse in
+// gemm_common.hpp); plain GEMMs pass {}.
 //   MODE 1 (H = sigmoid(X W1)): the epilogue applies the sigmoid before
 //     storing and writes zpart[(tn*WN + wn)*M + row] = sum over this wave's
 //     columns of H[row][col] * w2[col] (a partial of z2 = H W2).
@@ -29,13 +30,6 @@ namespace ch {
 //     each wave writes its partial to
 //     dw2part[((split * tiles_m + tm) * WM + wm) * N + n].  d2 reaches LDS
 //     with the k-tile.
-struct MlpFuse {
-    const float* w2 = nullptr;
-    const float* d2 = nullptr;
-    float* zpart = nullptr;
-    float* dw2part = nullptr;
-};
-
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC, int MODE = 0>
 struct F32Tiled {
     static constexpr int NW = WM * WN, THREADS = 64 * NW;

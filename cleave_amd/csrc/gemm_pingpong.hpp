@@ -57,8 +57,8 @@ __device__ __forceinline__ void pingpong_copy(int u, int nk, Issue&& issue) {
 
 // Runs the whole schedule over nk k-tiles.  issue(kt) copies this wave's
 // share of k-tile kt into stage kt % 4; m_phase(PingPongStage<ST>{}, u) is the
-// M phase of k-tile u (stage ST = u % 4), ending in pingpong_copy; c_phase()
-// is the C phase on the fragments the wave's last M phase read.  With
+// M phase of k-tile u (stage ST = u % 4), ending in pingpong_copy; c_phase(u)
+// is the C phase of k-tile u, on the fragments the wave's last M phase read.  With
 // prologue_copies false the caller has already put tile 0 in stage 0 and
 // started the copies of the next tiles, and issue is not called.
 template <int LPW, class Issue, class MPhase, class CPhase>
@@ -82,7 +82,7 @@ __device__ __forceinline__ void pingpong_schedule(int nk, int grp, Issue&& issue
     // a group's loop reads before writing.  (The branch is uniform per wave,
     // and s_barrier counts waves, not program counters.)
     auto step0 = [&](auto next_stage, int s) {
-        c_phase();
+        c_phase(s);
         asm volatile("s_barrier" ::: "memory");
         if (s + 1 < nk) m_phase(next_stage, s + 1);
         asm volatile("s_barrier" ::: "memory");
@@ -90,7 +90,7 @@ __device__ __forceinline__ void pingpong_schedule(int nk, int grp, Issue&& issue
     auto step1 = [&](auto stage, int s) {
         m_phase(stage, s);
         asm volatile("s_barrier" ::: "memory");
-        c_phase();
+        c_phase(s);
         asm volatile("s_barrier" ::: "memory");
     };
     if (grp == 0) {

@@ -18,7 +18,7 @@
 //   7. dW1 partials = X^T d1            gemm_f32 TN, split-K slices
 //   8. dW1 = sum of slices; W1 -= lr dW1
 #include "common.hpp"
-#include "gemm_f32_tiled.hpp"
+#include "gemm_f32_pingpong.hpp"
 
 namespace ch {
 int32_t gemm_f32_device(const float* a, const float* b, float* c, int M, int N, int K, int ta,
@@ -190,14 +190,14 @@ int choose_splits(int D, int Hd, int B) {
 }
 
 // ---- fused path (shapes that divide the 256 x 256 x 16 f32 tile) -----------
-//   1. H = sigmoid(X W1) and partials of H W2      f32 tiled GEMM, MODE 1
+//   1. H = sigmoid(X W1) and partials of H W2      f32 ping-pong GEMM, MODE 1
 //   2. z2, yhat, e, sq, d2 per row; loss           row_finish, loss kernels
 //   3. dW1 slices = X^T d1 with d1 = (d2 W2) H(1-H) formed as the MFMA reads H,
-//      and dW2 partials                            f32 tiled GEMM, MODE 2
+//      and dW2 partials                            f32 ping-pong GEMM, MODE 2
 //   4. dW1 = sum of slices, W1 -= lr dW1; dW2 likewise (W2 is updated last:
 //      step 3 reads it)
-using FusedTile1 = ch::F32Tiled<256, 256, 16, 2, 4, 2, true, false, 1>;
-using FusedTile2 = ch::F32Tiled<256, 256, 16, 2, 4, 2, false, false, 2>;
+using FusedTile1 = ch::F32PingPong<true, false, 1>;
+using FusedTile2 = ch::F32PingPong<false, false, 2>;
 
 int fused_splits(int B, int D, int Hd) {
     const int tiles = (D / 256) * (Hd / 256);
@@ -206,8 +206,9 @@ int fused_splits(int B, int D, int Hd) {
     return splits;
 }
 
-bool fused_fits(int B, int D, int Hd) {
+bool fused_fits(const float* x, const float* w1, int B, int D, int Hd) {
     if (B % 256 || D % 256 || Hd % 256) return false;
+    if (((uintptr_t)x & 15) || ((uintptr_t)w1 & 15)) return false;  // 16-byte operand loads
     const int splits = fused_splits(B, D, Hd);
     return FusedTile1::fits(B, Hd, D, D, Hd) && FusedTile2::fits(D, Hd, B / splits, D, Hd);
 }
@@ -237,10 +238,10 @@ int32_t fused_step(const float* x, const float* y, float* w1, float* w2, float* 
     ch::MlpFuse f1;
     f1.w2 = w2;
     f1.zpart = zpart;
-    ch::gemm_f32_tiled_kernel<256, 256, 16, 2, 4, 2, true, false, 1>
+    ch::gemm_f32_pingpong_kernel<true, false, 1>
         <<<dim3((unsigned)((B / 256) * (Hd / 256))), FusedTile1::THREADS, 0, st>>>(
             x, w1, H, B, Hd, D, D, Hd, 0, 0, 0, B / 256, Hd / 256, 1, f1);
-    CH_LAUNCHED("gemm_f32_tiled_kernel(MODE 1)");
+    CH_LAUNCHED("gemm_f32_pingpong_kernel(MODE 1)");
     row_finish_kernel<<<row_blocks, kThreads, 0, st>>>(zpart, P, y, B, sq, d2);
     CH_LAUNCHED("row_finish_kernel");
     // mean of the squared errors: the row blocks' sums, added in order, over B
@@ -251,11 +252,11 @@ int32_t fused_step(const float* x, const float* y, float* w1, float* w2, float* 
     f2.w2 = w2;
     f2.d2 = d2;
     f2.dw2part = part;
-    ch::gemm_f32_tiled_kernel<256, 256, 16, 2, 4, 2, false, false, 2>
+    ch::gemm_f32_pingpong_kernel<false, false, 2>
         <<<dim3((unsigned)((D / 256) * (Hd / 256) * splits)), FusedTile2::THREADS, 0, st>>>(
             x, H, slices, D, Hd, kk, D, Hd, (int64_t)kk * D, (int64_t)kk * Hd, (int64_t)D * Hd, D / 256,
             Hd / 256, splits, f2);
-    CH_LAUNCHED("gemm_f32_tiled_kernel(MODE 2)");
+    CH_LAUNCHED("gemm_f32_pingpong_kernel(MODE 2)");
     sum_slices_sgd_kernel<<<capped_grid((int64_t)D * Hd), kThreads, 0, st>>>(slices, splits, (int64_t)D * Hd, dw1, w1, lr);
     CH_LAUNCHED("sum_slices_sgd_kernel(dW1)");
     sum_slices_sgd_kernel<<<capped_grid(Hd), kThreads, 0, st>>>(part, dw2_slices, Hd, dw2, w2, lr);
@@ -282,7 +283,7 @@ extern "C" int32_t cleave_hip_mlp_step_f32(const float* x, int64_t xlen, const f
     CH_INIT_OR_RETURN();
 
     hipStream_t st = ch::stream();
-    if (fused_fits(B, D, Hd)) return fused_step(x, y, w1, w2, dw1, dw2, loss_dev, B, D, Hd, lr, st);
+    if (fused_fits(x, w1, B, D, Hd)) return fused_step(x, y, w1, w2, dw1, dw2, loss_dev, B, D, Hd, lr, st);
 
     const int splits = choose_splits(D, Hd, B);
     const int bands = (B + kRowsPerBand - 1) / kRowsPerBand;
