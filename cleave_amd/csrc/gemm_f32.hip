@@ -237,7 +237,7 @@ bool launch_tiled(const float* a, const float* b, float* c, int M, int N, int K,
     if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
     dim3 grid((unsigned)(tiles_m * tiles_n * batch));
     ch::gemm_f32_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
-        a, b, c, M, N, K, lda, ldb, sA, sB, sC, tiles_m, tiles_n, batch, ch::MlpFuse{});
+        a, b, c, M, N, K, lda, ldb, sA, sB, sC, tiles_m, tiles_n, batch);
     *status = ch::check_hip(hipGetLastError(), "gemm_f32_tiled_kernel");
     return true;
 }

@@ -33,9 +33,11 @@
 //   MODE 1 (H = sigmoid(X W1), A staged, B copied): sigmoid in the epilogue,
 //     and zpart[(tn*4 + wn)*M + row] = sum over the wave's 64 columns of
 //     H[row][col] * w2[col];
-//   MODE 2 (dW1 slice = X^T d1, both operands copied): B is H; each B value
-//     h of column n at batch row k becomes d1 = (d2[k] w2[n]) h (1 - h) in the
-//     C phase before its MFMAs, and the wave owning the k-block (k-tile kt of
+//   MODE 2 (slice of X^T d1 / w2, both operands copied): B is H; each B
+//     value h at batch row k becomes d2[k] h (1 - h) in the C phase before its
+//     MFMAs.  d1 = (d2[k] w2[n]) h (1 - h) also has the column factor w2[n],
+//     which the caller applies to the summed slices: two VALU instructions per
+//     value here instead of four.  The wave owning the k-block (k-tile kt of
 //     M-tile kt % tiles_m, k-block kb of group kb % 2) adds h d2[k] to its
 //     dW2 partial, written to dw2part[((split*tiles_m + tm)*2 + grp)*N + n].
 //     d2 reaches LDS with the k-tile (every wave copies the same 64 bytes, so
@@ -261,18 +263,14 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
         for (int j = 0; j < FN; ++j) acc[i][j] = v16f{};
     v4f fa[KB][FM], fb[KB][FN];
 
-    // MODE 2: d2 at this lane's k-rows of each k-block, w2 at its columns,
-    // and the dW2 partial of those columns.
+    // MODE 2: d2 at this lane's k-rows of each k-block, and the dW2 partial
+    // of its columns.
     v4f d2v[KB];
-    float w2c[FN];
     v4f dw2acc[FN];
     uint32_t rd_d2 = 0;
     if constexpr (MODE == 2) {
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            w2c[j] = fuse.w2[n0 + wn * P::TN + j * 32 + (lane & 31)];
-            dw2acc[j] = v4f{};
-        }
+        for (int j = 0; j < FN; ++j) dw2acc[j] = v4f{};
         rd_d2 = region_d2 + (uint32_t)(16 * (lane >> 5));  // k = 8kb + 4h + s
         opaque(rd_d2);
     }
@@ -322,15 +320,18 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
             if constexpr (MODE == 2) {
-                // d1 = (d2[k] w2[n]) h (1 - h), the order of the reference step
-                const bool mine = (u % tiles_m) == tm && kb % 2 == grp;
+                if ((u % tiles_m) == tm && kb % 2 == grp) {
+                    asm volatile("");  // a branch, not a select in every wave
 #pragma unroll
-                for (int j = 0; j < FN; ++j) {
-                    const v4f h = fb[kb][j];
-                    if (mine) dw2acc[j] += h * d2v[kb];
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) fb[kb][j][s] = (d2v[kb][s] * w2c[j]) * h[s] * (1.0f - h[s]);
+                    for (int j = 0; j < FN; ++j) dw2acc[j] += fb[kb][j] * d2v[kb];
                 }
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        const float h = fb[kb][j][s];
+                        fb[kb][j][s] = d2v[kb][s] * __builtin_fmaf(-h, h, h);  // d2[k] h (1 - h)
+                    }
             }
 #pragma unroll
             for (int s = 0; s < 4; ++s)

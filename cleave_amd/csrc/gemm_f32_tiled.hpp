@@ -16,31 +16,14 @@
 
 namespace ch {
 
-// Fusions for the two GEMMs of the MLP step (mlp.hip, MlpFuse in
-// gemm_common.hpp); plain GEMMs pass {}.
-//   MODE 1 (H = sigmoid(X W1)): the epilogue applies the sigmoid before
-//     storing and writes zpart[(tn*WN + wn)*M + row] = sum over this wave's
-//     columns of H[row][col] * w2[col] (a partial of z2 = H W2).
-//   MODE 2 (dW1 = X^T d1, split-K over the batch): B is H, and each operand
-//     value h of column n at batch row k becomes d1 = (d2[k] w2[n]) h (1 - h)
-//     as the MFMA consumes it.  The same values give dW2[n] = sum_k h d2[k]:
-//     each k-block's contribution is taken by exactly one wave -- M-tile tm
-//     takes the k-tiles with kt % tiles_m == tm and, within them, row-half wm
-//     the k-block kb == wm -- so every workgroup carries an equal share, and
-//     each wave writes its partial to
-//     dw2part[((split * tiles_m + tm) * WM + wm) * N + n].  d2 reaches LDS
-//     with the k-tile.
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC, int MODE = 0>
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC>
 struct F32Tiled {
     static constexpr int NW = WM * WN, THREADS = 64 * NW;
     static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
     static constexpr int A_BYTES = BM * BK * 4, B_BYTES = BN * BK * 4;
-    static constexpr int AUX_BYTES = MODE == 2 ? 1024 : 0;  // d2 slice of the k-tile
-    static constexpr int STAGE_BYTES = A_BYTES + B_BYTES + AUX_BYTES, LDS_BYTES = STAGES * STAGE_BYTES;
-    // copy instructions per wave per k-tile (MODE 2 adds the d2 slice)
-    static constexpr int LPW = (A_BYTES + B_BYTES) / 1024 / NW + (MODE == 2 ? 1 : 0);
+    static constexpr int STAGE_BYTES = A_BYTES + B_BYTES, LDS_BYTES = STAGES * STAGE_BYTES;
+    static constexpr int LPW = (A_BYTES + B_BYTES) / 1024 / NW;  // copy instructions per wave per k-tile
     static_assert(TM % 32 == 0 && TN % 32 == 0 && BK % 16 == 0, "tile shape");
-    static_assert(MODE != 2 || (!BKC && BK <= 64), "MODE 2 transforms an m/n-contiguous B");
     static_assert(STAGES >= 2 && LPW * (STAGES - 2) < 64, "pipeline depth");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS per workgroup");
 
@@ -54,13 +37,13 @@ struct F32Tiled {
         return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
     }};
 
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC, int MODE = 0>
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N,
     int K, int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC, int tiles_m,
-    int tiles_n, int batch, MlpFuse fuse) {
+    int tiles_n, int batch) {
     using namespace ch::tiles;
-    using P = F32Tiled<BM, BN, BK, WM, WN, STAGES, AKC, BKC, MODE>;
+    using P = F32Tiled<BM, BN, BK, WM, WN, STAGES, AKC, BKC>;
     constexpr int FM = P::FM, FN = P::FN, NW = P::NW;
     __shared__ __attribute__((aligned(1024))) char smem[P::LDS_BYTES];
 
@@ -80,18 +63,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
     copy_b.init(ldb, n0, wave, lane);
     const int64_t step_a = copy_a.kstep(lda), step_b = copy_b.kstep(ldb);
     const uint32_t lds0 = lds_addr(smem);
-    // MODE 2: this split's d2 slice starts at batch row bt * K.
-    const float* d2 = MODE == 2 ? fuse.d2 + (int64_t)bt * K : nullptr;
     auto issue = [&](int kt, int stage) {
         const uint32_t dst = lds0 + (uint32_t)(stage * P::STAGE_BYTES);
         copy_a.issue(reinterpret_cast<const char*>(A) + kt * step_a, dst, wave);
         copy_b.issue(reinterpret_cast<const char*>(B) + kt * step_b, dst + P::A_BYTES, wave);
-        if constexpr (MODE == 2) {
-            // every wave copies the BK d2 values (BK/4 lanes x 16 bytes), so
-            // each wave's vmcnt accounting stays uniform
-            if (lane < BK / 4)
-                dma16(d2 + (int64_t)kt * BK, (uint32_t)(lane * 16), dst + P::A_BYTES + P::B_BYTES);
-        }
     };
 
     v16f acc[FM][FN];
@@ -101,41 +76,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
         for (int j = 0; j < FN; ++j) acc[i][j] = v16f{};
 
     v4f fa[2][FM], fb[2][FN];
-    v4f d2v[2];               // MODE 2: d2 at this lane's 4 k of the k-block
-    float w2c[FN];            // MODE 2: w2 at this lane's column of fragment j
-    v4f dw2acc[FN];           // MODE 2: partial dW2 of that column
-    static_assert(MODE != 2 || (BK / 8) % WM == 0, "each row-half wave takes whole k-blocks of a k-tile");
-    // MODE 2: does this wave accumulate dW2 for k-block kb of k-tile kt?
-    auto dw2_mine = [&](int kt, int kb) { return (kt % tiles_m) == tm && (kb % WM) == wm; };
-    if constexpr (MODE == 2) {
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            w2c[j] = fuse.w2[n0 + wn * P::TN + j * 32 + (lane & 31)];
-            dw2acc[j] = v4f{};
-        }
-    }
     auto read_block = [&](int buf, const char* tile, int kb) {
-        if constexpr (MODE == 2)
-            d2v[buf] = *reinterpret_cast<const v4f*>(tile + P::A_BYTES + P::B_BYTES + (8 * kb + 4 * (lane >> 5)) * 4);
 #pragma unroll
         for (int i = 0; i < FM; ++i) fa[buf][i] = read_frag_f32<AKC, BM, BK>(tile, wm * P::TM + i * 32, kb, lane);
 #pragma unroll
         for (int j = 0; j < FN; ++j)
             fb[buf][j] = read_frag_f32<BKC, BN, BK>(tile + P::A_BYTES, wn * P::TN + j * 32, kb, lane);
-    };
-    // MODE 2: d1 = (d2[k] w2[n]) h (1 - h), the order of the reference step.
-    // Applied to a k-block's fragments right after the previous block's MFMAs
-    // are issued, so this VALU work overlaps the matrix core.
-    auto transform = [&](int buf, bool mine) {
-        if constexpr (MODE == 2) {
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const v4f h = fb[buf][j];
-                if (mine) dw2acc[j] += h * d2v[buf];
-#pragma unroll
-                for (int s = 0; s < 4; ++s) fb[buf][j][s] = (d2v[buf][s] * w2c[j]) * h[s] * (1.0f - h[s]);
-            }
-        }
     };
     auto mfma_block = [&](int cur) {
 #pragma unroll
@@ -165,7 +111,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
     asm volatile("s_barrier" ::: "memory");
     if (STAGES - 1 < nk) issue(STAGES - 1, STAGES - 1);
     read_block(0, smem, 0);
-    transform(0, dw2_mine(0, 0));
 
     for (int kt = 0; kt < nk; ++kt) {
         const char* tile = smem + (kt % STAGES) * P::STAGE_BYTES;
@@ -173,7 +118,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
         for (int kb = 0; kb + 1 < KB; ++kb) {
             read_block((kb & 1) ^ 1, tile, kb + 1);
             mfma_block(kb & 1);
-            transform((kb & 1) ^ 1, dw2_mine(kt, kb + 1));
         }
 #pragma unroll
         for (int g = 0; g < (KB - 1) * NM; ++g) {
@@ -192,55 +136,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
             if (kt + STAGES < nk) issue(kt + STAGES, kt % STAGES);
         }
         mfma_block((KB - 1) & 1);
-        if (kt + 1 < nk) transform(0, dw2_mine(kt + 1, 0));
     }
 
     const int half = lane >> 5, col = lane & 31;
-    if constexpr (MODE == 1) {
-        // H = sigmoid(acc) = 1 / (1 + exp(-acc)) with the hardware exp2 and
-        // reciprocal (about 1 ulp each; the IEEE expf + division would cost
-        // ~30 VALU ops per element with the matrix core idle), and per row the
-        // sum of H * w2 over this wave's columns: lanes of a half-wave hold
-        // the 32 columns of the same rows.
-        float w2j[FN];
-#pragma unroll
-        for (int j = 0; j < FN; ++j) w2j[j] = fuse.w2[n0 + wn * P::TN + j * 32 + col];
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            float zs[16];
-#pragma unroll
-            for (int v = 0; v < 16; ++v) zs[v] = 0.0f;
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const float e = __builtin_amdgcn_exp2f(-acc[i][j][v] * 1.4426950408889634f);
-                    const float h = __builtin_amdgcn_rcpf(1.0f + e);
-                    acc[i][j][v] = h;
-                    zs[v] += h * w2j[j];
-                }
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-#pragma unroll
-                for (int o = 16; o > 0; o >>= 1) zs[v] += __shfl_xor(zs[v], o);
-            if (col == 0) {
-                float* zp = fuse.zpart + (int64_t)(tn * WN + wn) * M;
-#pragma unroll
-                for (int v = 0; v < 16; ++v)
-                    zp[m0 + wm * P::TM + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3)] = zs[v];
-            }
-        }
-    }
-    if constexpr (MODE == 2) {
-        // every wave writes its partial (zero when it took no k-block)
-        float* dst = fuse.dw2part + ((int64_t)(bt * tiles_m + tm) * WM + wm) * N + n0 + wn * P::TN + col;
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            float v = (dw2acc[j][0] + dw2acc[j][1]) + (dw2acc[j][2] + dw2acc[j][3]);
-            v += __shfl_xor(v, 32);
-            if (half == 0) dst[j * 32] = v;
-        }
-    }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll

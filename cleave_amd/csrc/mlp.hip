@@ -156,6 +156,28 @@ __global__ __launch_bounds__(kThreads) void sum_slices_sgd_kernel(const float* _
     }
 }
 
+// Fused path: dW1[m][n] = w2[n] * sum_s part[s][m][n] (fixed order) -- the
+// column factor of d1 = (d2 w2) h(1-h), left out of the GEMM's operand
+// transform -- with an optional copy to dW, then W -= lr * dW1.  Blocks cover
+// 256 columns and stride over rows.
+__global__ __launch_bounds__(kThreads) void dw1_finish_kernel(const float* __restrict__ part, int slices,
+                                                              int rows, int cols, const float* __restrict__ w2,
+                                                              float* __restrict__ dw, float* __restrict__ w,
+                                                              float lr) {
+    const int c = blockIdx.x * kThreads + threadIdx.x;
+    if (c >= cols) return;
+    const float f = w2[c];
+    const int64_t n = (int64_t)rows * cols;
+    for (int r = blockIdx.y; r < rows; r += gridDim.y) {
+        const int64_t i = (int64_t)r * cols + c;
+        float g = part[i];
+        for (int s = 1; s < slices; ++s) g += part[(int64_t)s * n + i];
+        g = f * g;
+        if (dw) dw[i] = g;
+        if (lr != 0.0f) w[i] = w[i] - lr * g;
+    }
+}
+
 // loss = (sum of the n values v) / count: per-row squared errors (unfused
 // path, n = B) or per-block sums of them (fused path).
 __global__ __launch_bounds__(kThreads) void loss_kernel(const float* __restrict__ v, int n, float count,
@@ -192,10 +214,10 @@ int choose_splits(int D, int Hd, int B) {
 // ---- fused path (shapes that divide the 256 x 256 x 16 f32 tile) -----------
 //   1. H = sigmoid(X W1) and partials of H W2      f32 ping-pong GEMM, MODE 1
 //   2. z2, yhat, e, sq, d2 per row; loss           row_finish, loss kernels
-//   3. dW1 slices = X^T d1 with d1 = (d2 W2) H(1-H) formed as the MFMA reads H,
-//      and dW2 partials                            f32 ping-pong GEMM, MODE 2
-//   4. dW1 = sum of slices, W1 -= lr dW1; dW2 likewise (W2 is updated last:
-//      step 3 reads it)
+//   3. slices of X^T (d1 / W2) with d1 / W2 = d2 H(1-H) formed as the MFMA
+//      reads H, and dW2 partials                   f32 ping-pong GEMM, MODE 2
+//   4. dW1 = W2 (column factor) * sum of slices, W1 -= lr dW1; dW2 likewise
+//      (W2 is updated last: steps 3 and 4 read it)
 using FusedTile1 = ch::F32PingPong<true, false, 1>;
 using FusedTile2 = ch::F32PingPong<false, false, 2>;
 
@@ -249,7 +271,6 @@ int32_t fused_step(const float* x, const float* y, float* w1, float* w2, float* 
     CH_LAUNCHED("loss_kernel");
     const int kk = B / splits;
     ch::MlpFuse f2;
-    f2.w2 = w2;
     f2.d2 = d2;
     f2.dw2part = part;
     ch::gemm_f32_pingpong_kernel<false, false, 2>
@@ -257,8 +278,9 @@ int32_t fused_step(const float* x, const float* y, float* w1, float* w2, float* 
             x, H, slices, D, Hd, kk, D, Hd, (int64_t)kk * D, (int64_t)kk * Hd, (int64_t)D * Hd, D / 256,
             Hd / 256, splits, f2);
     CH_LAUNCHED("gemm_f32_pingpong_kernel(MODE 2)");
-    sum_slices_sgd_kernel<<<capped_grid((int64_t)D * Hd), kThreads, 0, st>>>(slices, splits, (int64_t)D * Hd, dw1, w1, lr);
-    CH_LAUNCHED("sum_slices_sgd_kernel(dW1)");
+    dw1_finish_kernel<<<dim3((unsigned)((Hd + kThreads - 1) / kThreads), (unsigned)(D < 1024 ? D : 1024)),
+                        kThreads, 0, st>>>(slices, splits, D, Hd, w2, dw1, w1, lr);
+    CH_LAUNCHED("dw1_finish_kernel");
     sum_slices_sgd_kernel<<<capped_grid(Hd), kThreads, 0, st>>>(part, dw2_slices, Hd, dw2, w2, lr);
     CH_LAUNCHED("sum_slices_sgd_kernel(dW2)");
     return CLEAVE_HIP_OK;
