@@ -24,9 +24,16 @@
 // writes, and every fragment, k-row and stage of an operand is one
 // loop-invariant register plus an immediate offset below 64 KiB.  So the M
 // phase issues no VALU instruction; the accumulators live in AGPRs.
-// Within a 1 KiB row, 16-byte chunk c of k-row kr sits in slot
-// mn_slot<4>(kr, c) (gemm_tiles.hpp), which keeps the two half-waves of a
-// fragment read, at k-rows kr and kr + 4, in opposite bank halves.
+// Within a 1 KiB row, 16-byte chunk c of k-row kr sits in slot pp_slot(kr, c)
+// = c ^ 8*bit2(kr) ^ 4*bit3(kr).  Bit 2 puts the two half-waves of a fragment
+// read (k-rows kr and kr + 4, the same 32 columns) in opposite bank halves;
+// bit 3 moves the k-rows 4c + s that one staged write covers apart.  With bit
+// 2 alone the staged writes took 1.7 (NN) and 3.0 (NT) bank-conflict cycles
+// per LDS instruction, with both bits 0.57 and 1.0; the reads have none.
+// Writing the values one ds_write_b32 at a time (instead of the pairs of
+// ds_write2st64_b32, whose two values always share a bank) moved the same
+// conflict cycles to more instructions.  None of it is on the matrix core's
+// path: NN, NT and TT run as fast as TN.
 //
 // MODE carries the fusions of the MLP step (mlp.hip), as in
 // gemm_f32_tiled.hpp with the row-half wave wm = group and WN = 4:
@@ -80,6 +87,9 @@ struct F32PingPong {
 
 namespace f32pp {
 
+// Slot of 16-byte chunk c (of 64) in k-major LDS row kr.
+__device__ __forceinline__ int pp_slot(int kr, int c) { return c ^ (((kr >> 2) & 1) << 3) ^ (((kr >> 3) & 1) << 2); }
+
 typedef __attribute__((address_space(3))) float lds_float;
 __device__ __forceinline__ const lds_float* lds_ptr(uint32_t a) { return (const lds_float*)(uintptr_t)a; }
 __device__ __forceinline__ lds_float* lds_ptr_w(uint32_t a) { return (lds_float*)(uintptr_t)a; }
@@ -125,8 +135,8 @@ struct Staged {
             const int q = wave + NW * j;
             const int row = 16 * q + (lane >> 2), kc = lane & 3;
             voff[j] = (uint32_t)(((int64_t)(r0 + row) * ld + 4 * kc) * 4);
-            // mn_slot<4>(4*kc + s, row/4) does not depend on s
-            waddr[j] = region + (uint32_t)(4 * kc * KROW + tiles::mn_slot<4>(4 * kc, row >> 2) * 16 + (row & 3) * 4);
+            // pp_slot(4*kc + s, row/4) does not depend on s
+            waddr[j] = region + (uint32_t)(4 * kc * KROW + pp_slot(4 * kc, row >> 2) * 16 + (row & 3) * 4);
             opaque(voff[j]);
             opaque(waddr[j]);
         }
@@ -159,7 +169,7 @@ struct Direct {
 #pragma unroll
         for (int j = 0; j < PER_WAVE; ++j) {
             const int kr = wave + NW * j;
-            const int c = tiles::mn_slot<4>(kr, lane);  // slot lane holds chunk c (the XOR is its own inverse)
+            const int c = pp_slot(kr, lane);  // slot lane holds chunk c (the XOR is its own inverse)
             voff[j] = (uint32_t)(((int64_t)kr * ld + r0 + 4 * c) * 4);
             dst[j] = region + (uint32_t)(kr * KROW);
         }
@@ -241,19 +251,23 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
     };
 
     // Fragment read addresses: fragment f (A: f < FM, B: f >= FM) of k-block
-    // kb, step s, stage ST sits at rd[f] + (8kb + s)*KROW + ST*ROW.  Half-wave
-    // h reads k-rows 8kb + 4h + s; mn_slot<4> depends on kr only through
-    // (kr >> 2) & 1 = h.
-    uint32_t rd[FM + FN];
+    // kb, step s, stage ST sits at rd[kb][f] + (8kb + s)*KROW + ST*ROW.
+    // Half-wave h reads k-rows kr = 8kb + 4h + s, whose slot depends on kr
+    // through bit 2 (= h) and bit 3 (= kb).
+    uint32_t rd[KB][FM + FN];
     {
         const int h = lane >> 5;
 #pragma unroll
-        for (int f = 0; f < FM + FN; ++f) {
-            const int col = f < FM ? grp * P::TM + f * 32 + (lane & 31) : wn * P::TN + (f - FM) * 32 + (lane & 31);
-            rd[f] = (f < FM ? region_a : region_b) +
-                    (uint32_t)(4 * h * KROW + mn_slot<4>(4 * h, col >> 2) * 16 + (col & 3) * 4);
-            opaque(rd[f]);
-        }
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int f = 0; f < FM + FN; ++f) {
+                const int col =
+                    f < FM ? grp * P::TM + f * 32 + (lane & 31) : wn * P::TN + (f - FM) * 32 + (lane & 31);
+                const int kr = 8 * kb + 4 * h;
+                rd[kb][f] = (f < FM ? region_a : region_b) +
+                            (uint32_t)(4 * h * KROW + pp_slot(kr, col >> 2) * 16 + (col & 3) * 4);
+                opaque(rd[kb][f]);
+            }
     }
 
     v16f acc[FM][FN];
@@ -294,9 +308,9 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
             for (int s = 0; s < 4; ++s) {
                 const uint32_t off = (8 * kb + s) * KROW + ST * ROW;
 #pragma unroll
-                for (int i = 0; i < FM; ++i) fa[kb][i][s] = *lds_ptr(rd[i] + off);
+                for (int i = 0; i < FM; ++i) fa[kb][i][s] = *lds_ptr(rd[kb][i] + off);
 #pragma unroll
-                for (int j = 0; j < FN; ++j) fb[kb][j][s] = *lds_ptr(rd[FM + j] + off);
+                for (int j = 0; j < FN; ++j) fb[kb][j][s] = *lds_ptr(rd[kb][FM + j] + off);
             }
         if constexpr (MODE == 2) {
 #pragma unroll
