@@ -246,11 +246,16 @@ template <bool TA, bool TB>
 int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch) {
     int32_t st = CLEAVE_HIP_OK;
     // 256 x 256 tiles, when that still gives every CU a tile: the ping-pong
-    // kernel (k-tiles of 32), else the tiled kernel (k-tiles of 64)
+    // kernel (k-tiles of 32), or the tiled kernel (k-tiles of 64).  With one
+    // round of tiles and K up to 2048 the tiled kernel measured equal or 3-10%
+    // faster (64 x 512^3: 24.3 against 25.1-27.3 us); with K from 4096, or
+    // several rounds, the ping-pong kernel (8192^3: 802 against 830 us).
     const int64_t big_tiles = (int64_t)(M / 256) * (N / 256) * batch;
     if (big_tiles >= ch::num_cus()) {
-        if (launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
+        const bool short_single_round = big_tiles <= ch::num_cus() && K <= 2048;
+        if (!short_single_round && launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
         if (launch_tiled<256, 256, 64, 2, 4, 2, 16, TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
+        if (launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
     }
     // 128 x 128 x 64 tile, 4 waves of 64 x 64 in 32 x 32 x 16 MFMAs, three
     // LDS stages (96 KiB)

@@ -229,6 +229,21 @@ def test_big_tile_path_every_layout(hip, oracle, dtype, ta, tb):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_bf16_pingpong_every_layout(hip, oracle, ta, tb):
+    # 8192 x 8192 outputs are four rounds of 256 x 256 tiles, which take the
+    # bf16 ping-pong kernel at any K; K = 96 is three of its k-tiles
+    M = N = 8192
+    K = 96
+    a = hip.to_bf16(hip.fill_normal(hip.empty((K, M) if ta else (M, K)), seed=31 + 2 * ta + tb, std=0.02))
+    b = hip.to_bf16(hip.fill_normal(hip.empty((N, K) if tb else (K, N)), seed=41 + 2 * ta + tb, std=0.02))
+    c = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    A, B = a.numpy(), b.numpy()
+    ii, jj = sample_entries(M, N, 1024, seed=7 + ta + 2 * tb)
+    ref, absden = oracle.matmul_entries(A, B, M, N, K, ii, jj, trans_a=bool(ta), trans_b=bool(tb), bf16=True)
+    assert_gemm_close(c[ii, jj], ref, absden, K, f"bf16 ping-pong ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("K", [16, 48, 80])
 def test_f32_pingpong_short_k(hip, oracle, K, ta, tb):
     # 1, 3 and 5 k-tiles of 16: the ring of four LDS stages is never filled,
