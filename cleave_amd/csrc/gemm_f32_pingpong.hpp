@@ -35,8 +35,9 @@
 // conflict cycles to more instructions.  None of it is on the matrix core's
 // path: NN, NT and TT run as fast as TN.
 //
-// MODE carries the fusions of the MLP step (mlp.hip), as in
-// gemm_f32_tiled.hpp with the row-half wave wm = group and WN = 4:
+// MODE carries the fusions of the MLP step (mlp.hip); MlpFuse (gemm_common.hpp)
+// holds their operands.  A group is a row half, and there are WN = 4 waves
+// along N:
 //   MODE 1 (H = sigmoid(X W1), A staged, B copied): sigmoid in the epilogue,
 //     and zpart[(tn*4 + wn)*M + row] = sum over the wave's 64 columns of
 //     H[row][col] * w2[col];
@@ -68,10 +69,9 @@ struct F32PingPong {
     static constexpr int D2_BYTES = MODE == 2 ? STAGES * BK * 4 : 0;        // MODE 2: d2 per stage
     static constexpr int LDS_BYTES = 2 * OP_BYTES + D2_BYTES;
     // Per wave and k-tile: global_load_lds instructions of the m/n-contiguous
-    // operands (and of d2), and 16-byte staged loads of the k-contiguous ones.
+    // operands (and of d2).
     static constexpr int OP_LOADS = A_BYTES / 1024 / NW;  // per operand
     static constexpr int LDMA = OP_LOADS * ((AKC ? 0 : 1) + (BKC ? 0 : 1)) + (MODE == 2 ? 1 : 0);
-    static constexpr int LSTAGED = OP_LOADS * ((AKC ? 1 : 0) + (BKC ? 1 : 0));
     static_assert(A_BYTES == B_BYTES && OP_LOADS == 2 && OP_BYTES == 65536, "operand tiles of 16 KiB");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS per workgroup");
     static_assert(MODE == 0 || (MODE == 1 && AKC && !BKC) || (MODE == 2 && !AKC && !BKC),
