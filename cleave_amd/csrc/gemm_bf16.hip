@@ -223,20 +223,17 @@ bool launch_tiled(const uint16_t* a, const uint16_t* b, float* c, int M, int N, 
 }
 
 // Ping-pong kernel (gemm_bf16_pingpong.hpp): 256 x 256 x 32 tiles in a ring
-// of four k-tiles (128 KiB of LDS).  A fifth stage (all 160 KiB) measured 7%
-// slower at 8192^3 with no LDS bank conflicts in either.
-constexpr int kPingPongStages = 4;
-
+// of five k-tiles (all 160 KiB of LDS).
 template <bool TA, bool TB>
 bool launch_pingpong(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
                      int32_t* status) {
-    using P = ch::Bf16PingPong<!TA, TB, kPingPongStages>;
+    using P = ch::Bf16PingPong<!TA, TB>;
     const int64_t lda = TA ? M : K, ldb = TB ? K : N;
     if (!P::fits(M, N, K, lda, ldb) || ((uintptr_t)a & 15) || ((uintptr_t)b & 15)) return false;
     const int tiles_m = M / P::BM, tiles_n = N / P::BN;
     if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
     dim3 grid((unsigned)(tiles_m * tiles_n * batch));
-    ch::gemm_bf16_pingpong_kernel<!TA, TB, true, kPingPongStages><<<grid, P::THREADS, 0, ch::stream()>>>(
+    ch::gemm_bf16_pingpong_kernel<!TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
         a, b, c, M, N, K, lda, ldb, (int64_t)M * K, (int64_t)K * N, (int64_t)M * N, tiles_m, tiles_n, batch);
     *status = ch::check_hip(hipGetLastError(), "gemm_bf16_pingpong_kernel");
     return true;

@@ -6,17 +6,18 @@
 //   C phase: one k-tile's MFMAs back to back, operands already in registers;
 //   M phase: read the next k-tile's operand fragments from LDS, issue this
 //            wave's share of the global -> LDS copy S-1 k-tiles ahead, wait
-//            for its own copy of the k-tile after that and for the reads.
+//            for its own copy of the k-tile after the one just read, and for
+//            the reads.
 // A workgroup barrier closes every phase and group 1 runs one phase behind
 // group 0, so on every SIMD one wave feeds the matrix core while the other
-// moves data.  The k-tiles sit in a ring of S = 4 LDS stages; the copy of
-// tile u+3 goes into the stage of tile u-1, which both groups finished
+// moves data.  The k-tiles sit in a ring of S LDS stages (4 or 5); the copy
+// of tile u+S-1 goes into the stage of tile u-1, which both groups finished
 // reading a phase earlier.
 //
 // Group 0: M(0) in the prologue, then per k-tile s: C(s) | M(s+1).
 // Group 1: per k-tile s: M(s) | C(s).
 //
-// The loops are unrolled over the four stages, so the M phase is handed its
+// The loops are unrolled over the S stages, so the M phase is handed its
 // stage as a compile-time constant and can address every fragment as a
 // loop-invariant register plus an immediate offset.  That keeps the M phase
 // free of VALU instructions, which matters: a VALU instruction of the M wave
@@ -27,6 +28,7 @@
 #pragma once
 
 #include <type_traits>
+#include <utility>
 
 namespace ch {
 
@@ -43,28 +45,34 @@ __device__ __forceinline__ void wait_tiles(int n) {
     else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
 }
 
-// The copy half of an M phase for k-tile u: issue tile u+3 (if any), then
+// The copy half of an M phase for k-tile u: issue tile u+S-1 (if any), then
 // wait for this wave's copy of tile u+1 -- the tiles issued after it may
 // stay in flight -- and for the LDS reads already issued.  LPW is the number
 // of copy instructions a wave issues per k-tile.
-template <int LPW, class Issue>
+template <int LPW, int S = kPingPongStages, class Issue>
 __device__ __forceinline__ void pingpong_copy(int u, int nk, Issue&& issue) {
-    constexpr int S = kPingPongStages;
+    static_assert(S >= 2 && S - 2 <= 3, "wait_tiles covers up to three later tiles");
     if (u + S - 1 < nk) issue(u + S - 1);
     const int later = min(u + S - 1, nk - 1) - (u + 1);  // tiles issued after u+1
     wait_tiles<LPW>(later < 0 ? 0 : later);
 }
 
+// step(PingPongStage<(OFF + i) % S>{}, s + i) for i = 0, 1, ... while s + i < nk.
+template <int S, int OFF, class Step, int... I>
+__device__ __forceinline__ void pingpong_unrolled(int s, int nk, Step& step,
+                                                  std::integer_sequence<int, I...>) {
+    (void)((s + I < nk ? (step(PingPongStage<(OFF + I) % S>{}, s + I), true) : false) && ...);
+}
+
 // Runs the whole schedule over nk k-tiles.  issue(kt) copies this wave's
-// share of k-tile kt into stage kt % 4; m_phase(PingPongStage<ST>{}, u) is the
-// M phase of k-tile u (stage ST = u % 4), ending in pingpong_copy; c_phase(u)
-// is the C phase of k-tile u, on the fragments the wave's last M phase read.  With
-// prologue_copies false the caller has already put tile 0 in stage 0 and
-// started the copies of the next tiles, and issue is not called.
-template <int LPW, class Issue, class MPhase, class CPhase>
+// share of k-tile kt into stage kt % S; m_phase(PingPongStage<ST>{}, u) is the
+// M phase of k-tile u (stage ST = u % S), ending in pingpong_copy<LPW, S>;
+// c_phase(u) is the C phase of k-tile u, on the fragments the wave's last M
+// phase read.  With prologue_copies false the caller has already put tile 0 in
+// stage 0 and started the copies of the next tiles, and issue is not called.
+template <int LPW, int S = kPingPongStages, class Issue, class MPhase, class CPhase>
 __device__ __forceinline__ void pingpong_schedule(int nk, int grp, Issue&& issue, MPhase&& m_phase,
                                                   CPhase&& c_phase, bool prologue_copies = true) {
-    constexpr int S = kPingPongStages;
     // Prologue: tiles 0..S-2 in flight; tile 0 landed everywhere; group 0
     // reads k-tile 0 (and issues tile S-1) so it can compute in phase 0.
     if (prologue_copies) {
@@ -96,20 +104,12 @@ __device__ __forceinline__ void pingpong_schedule(int nk, int grp, Issue&& issue
     if (grp == 0) {
         m_phase(PingPongStage<0>{}, 0);
         asm volatile("s_barrier" ::: "memory");
-        for (int s = 0; s < nk; s += S) {
-            step0(PingPongStage<1>{}, s);
-            if (s + 1 < nk) step0(PingPongStage<2>{}, s + 1);
-            if (s + 2 < nk) step0(PingPongStage<3>{}, s + 2);
-            if (s + 3 < nk) step0(PingPongStage<0>{}, s + 3);
-        }
+        for (int s = 0; s < nk; s += S)
+            pingpong_unrolled<S, 1>(s, nk, step0, std::make_integer_sequence<int, S>{});
     } else {
         asm volatile("s_barrier" ::: "memory");
-        for (int s = 0; s < nk; s += S) {
-            step1(PingPongStage<0>{}, s);
-            if (s + 1 < nk) step1(PingPongStage<1>{}, s + 1);
-            if (s + 2 < nk) step1(PingPongStage<2>{}, s + 2);
-            if (s + 3 < nk) step1(PingPongStage<3>{}, s + 3);
-        }
+        for (int s = 0; s < nk; s += S)
+            pingpong_unrolled<S, 0>(s, nk, step1, std::make_integer_sequence<int, S>{});
     }
 }
 
