@@ -79,22 +79,49 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
         for (int j = 0; j < FN; ++j) acc[i][j] = v4f{};
     v8bf fa[FM], fb[FN];
 
-    // Stage ST starts ST * 32 KiB into the ring.  A DS instruction's
-    // immediate offset reaches 64 KiB, so the stages are addressed from three
-    // bases 64 KiB apart: stage ST from base ST / 2.
-    const char* window[3] = {smem, smem + 2 * P::STAGE_BYTES, smem + 4 * P::STAGE_BYTES};
+    // Per-lane LDS addresses of this wave's fragment reads, one set per
+    // 64 KiB window of the ring (a DS immediate offset reaches 64 KiB), kept
+    // opaque so that each stays one register: the M phase then reads every
+    // fragment as register + immediate, with no VALU instruction (left to
+    // itself the compiler re-added lane offsets to window bases there, which
+    // cost 1-3% at 8192^3).  A KC operand's swizzle repeats every 32 rows, so
+    // its fragments two apart share a register; an MN operand's swizzle mixes
+    // the fragment's column bits, so each MN fragment has its own.
+    constexpr int NWIN = (S + 1) / 2;
+    constexpr int NA = AKC ? 2 : FM, NB = BKC ? 2 : FN;
+    uint32_t ra[NWIN][NA], rb[NWIN][NB];
+#pragma unroll
+    for (int w = 0; w < NWIN; ++w) {
+        const uint32_t win = lds0 + (uint32_t)(2 * w * P::STAGE_BYTES);
+#pragma unroll
+        for (int x = 0; x < NA; ++x) {
+            ra[w][x] = win + frag16_offset<AKC, P::BM, BK>(grp * P::TM + x * 16, lane);
+            opaque(ra[w][x]);
+        }
+#pragma unroll
+        for (int x = 0; x < NB; ++x) {
+            rb[w][x] = win + (uint32_t)P::A_BYTES + frag16_offset<BKC, P::BN, BK>(wn * P::TN + x * 16, lane);
+            opaque(rb[w][x]);
+        }
+    }
 
-    // M phase for k-step u (stage ST = u % S): fragments of tile u; copy of
-    // tile u+S-1 into the stage of tile u-1; wait for this wave's copy of
-    // tile u+1 and for the reads.
+    // M phase for k-step u (stage ST = u % S, at ST * 32 KiB): fragments of
+    // tile u; copy of tile u+S-1 into the stage of tile u-1; wait for this
+    // wave's copy of tile u+1 and for the reads.
     auto m_phase = [&](auto stage, int u) {
-        constexpr int ST = decltype(stage)::value;
-        const char* tile = window[ST / 2] + (ST % 2) * P::STAGE_BYTES;
+        constexpr int ST = decltype(stage)::value, W = ST / 2;
+        constexpr uint32_t SO = (ST % 2) * P::STAGE_BYTES;  // stage offset within window W
+        constexpr uint32_t PAIR = 2 * 16 * BK * 2;            // two 16-row KC fragments
 #pragma unroll
-        for (int i = 0; i < FM; ++i) fa[i] = read_frag16<AKC, P::BM, BK>(tile, grp * P::TM + i * 16, 0, lane);
+        for (int i = 0; i < FM; ++i) {
+            if constexpr (AKC) fa[i] = read16_kc_at(ra[W][i & 1] + SO + (uint32_t)(i / 2) * PAIR);
+            else fa[i] = read16_mn_at<P::BM>(ra[W][i] + SO);
+        }
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-            fb[j] = read_frag16<BKC, P::BN, BK>(tile + P::A_BYTES, wn * P::TN + j * 16, 0, lane);
+        for (int j = 0; j < FN; ++j) {
+            if constexpr (BKC) fb[j] = read16_kc_at(rb[W][j & 1] + SO + (uint32_t)(j / 2) * PAIR);
+            else fb[j] = read16_mn_at<P::BN>(rb[W][j] + SO);
+        }
         pingpong_copy<LPW, S>(u, nk, issue);
     };
     auto c_phase = [&](int) {

@@ -94,10 +94,7 @@ typedef __attribute__((address_space(3))) float lds_float;
 __device__ __forceinline__ const lds_float* lds_ptr(uint32_t a) { return (const lds_float*)(uintptr_t)a; }
 __device__ __forceinline__ lds_float* lds_ptr_w(uint32_t a) { return (lds_float*)(uintptr_t)a; }
 
-// Hide a value from the optimiser so it stays one register (the compiler
-// would otherwise re-derive addresses from the lane id inside the loop).
-template <class T>
-__device__ __forceinline__ void opaque(T& v) { asm volatile("" : "+v"(v)); }
+using tiles::opaque;
 
 // One staged load: 16 bytes per lane at byte offset voff + soff of the
 // operand behind rsrc.  A buffer load: the per-lane offset is one VGPR and

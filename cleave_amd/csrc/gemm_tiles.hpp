@@ -200,6 +200,41 @@ __device__ __forceinline__ v8bf read_frag16(const char* tile, int row0, int kk, 
     }
 }
 
+// The same 16 x 16 x 32 fragments, read at an address computed once.
+// frag16_offset is the byte offset within a tile of the fragment
+// read_frag16(tile, row0, 0, lane) reads (for an MN operand, its first k-row
+// quad; the second quad is 4 k-rows on, with the same swizzle, since the
+// quad's k-rows kb..kb+3 have kb % 8 <= 3).
+template <bool KC, int R, int BK>
+__device__ __forceinline__ uint32_t frag16_offset(int row0, int lane) {
+    if constexpr (KC) {
+        constexpr int CPR = BK / 8;
+        const int r = row0 + (lane & 15), c = lane >> 4;
+        return (uint32_t)(r * (BK * 2) + kc_slot<CPR, 2>(r, c) * 16);
+    } else {
+        const int j = (lane & 15) >> 2, q = lane & 3;
+        const int col = row0 + 4 * q, kr = 8 * (lane >> 4) + j;
+        return (uint32_t)(kr * (R * 2) + mn_slot<2>(kr, col >> 3) * 16 + (col & 7) * 2);
+    }
+}
+typedef __attribute__((address_space(3))) v8bf lds_v8bf;
+// KC fragment at LDS byte address a.
+__device__ __forceinline__ v8bf read16_kc_at(uint32_t a) { return *(const lds_v8bf*)(uintptr_t)a; }
+// MN fragment whose first k-row quad is at LDS byte address a (tile rows of R).
+template <int R>
+__device__ __forceinline__ v8bf read16_mn_at(uint32_t a) {
+    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)a);
+    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)(a + 4 * R * 2));
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    const v8s w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(v8bf, w);
+}
+
+// Hide a value from the optimiser so it stays one register (the compiler
+// would otherwise re-derive addresses from the lane id inside a loop).
+template <class T>
+__device__ __forceinline__ void opaque(T& v) { asm volatile("" : "+v"(v)); }
+
 // f32 operand for four consecutive v_mfma_f32_32x32x2f32 steps over the
 // 8-deep k-block kb (32 rows starting at tile row row0).  Lane-half h holds
 // k = 8*kb + 4*h + s at step s (A and B agree, so the k-sum is complete).
