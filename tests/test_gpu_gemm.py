@@ -277,3 +277,28 @@ def test_f32_batched_through_pingpong(hip, oracle):
         ii, jj = sample_entries(M, N, 256, seed=i)
         ref, absden = oracle.matmul_entries(A[i], B[i], M, N, K, ii, jj)
         assert_gemm_close(got[i][ii, jj], ref, absden, K, f"batched f32 entry {i}")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("K", [32, 128, 160, 192, 352])
+def test_bf16_pingpong_ring_depths(hip, oracle, K, ta, tb):
+    # 1, 4, 5, 6 and 11 k-tiles of 32 through the ring of five LDS stages:
+    # never filled, one short of full, exactly full, wrapping once, wrapping
+    # twice.  4096 x 8192 outputs are two rounds of 256 x 256 tiles, which the
+    # dispatch always gives to the ping-pong kernel.
+    M, N = 4096, 8192
+    a = hip.to_bf16(hip.fill_normal(hip.empty((K, M) if ta else (M, K)), seed=101 + K + 2 * ta + tb, std=0.02))
+    b = hip.to_bf16(hip.fill_normal(hip.empty((N, K) if tb else (K, N)), seed=111 + K + 2 * ta + tb, std=0.02))
+    c = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    A, B = a.numpy(), b.numpy()
+    ii, jj = sample_entries(M, N, 1024, seed=3 * K + ta + 2 * tb)
+    ref, absden = oracle.matmul_entries(A, B, M, N, K, ii, jj, trans_a=bool(ta), trans_b=bool(tb), bf16=True)
+    assert_gemm_close(c[ii, jj], ref, absden, K, f"bf16 ring K={K} ta={ta} tb={tb}")
+    # every row sum, in float64 on the upcast operands
+    Ad = oracle.bf16_to_f32(A).reshape(A.shape).astype(np.float64)
+    Bd = oracle.bf16_to_f32(B).reshape(B.shape).astype(np.float64)
+    Ad = Ad.T if ta else Ad
+    Bd = Bd.T if tb else Bd
+    rows = Ad @ Bd.sum(axis=1)
+    den = np.abs(Ad) @ np.abs(Bd).sum(axis=1)
+    assert np.max(np.abs(c.astype(np.float64).sum(axis=1) - rows) / den) <= 1e-5 * np.sqrt(K)
