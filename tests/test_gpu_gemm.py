@@ -302,3 +302,49 @@ def test_bf16_pingpong_ring_depths(hip, oracle, K, ta, tb):
     rows = Ad @ Bd.sum(axis=1)
     den = np.abs(Ad) @ np.abs(Bd).sum(axis=1)
     assert np.max(np.abs(c.astype(np.float64).sum(axis=1) - rows) / den) <= 1e-5 * np.sqrt(K)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_infinities_and_nans_propagate_like_the_loop(hip, oracle, dtype):
+    # The reference loop is IEEE arithmetic without reassociation, so an Inf
+    # or NaN in an operand reaches exactly the entries whose k-sum touches it:
+    # NaN stays NaN, an Inf with finite partners stays an Inf of the product's
+    # sign, and Inf meeting -Inf in one sum (or Inf times 0) is NaN.  The
+    # sum's order does not change any of that, so float64 products pin it.
+    # 4096 x 4096 outputs take the 256 x 256 kernels (f32 ping-pong, bf16 tiled).
+    M = N = 4096
+    K = 64
+    rng = np.random.default_rng(23)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    A[3, 5] = np.inf
+    A[7, 9] = np.nan
+    A[11, 2] = -np.inf
+    A[11, 3] = np.inf           # row 11: -Inf and +Inf, NaN or an Inf by the signs of their partners
+    B[10, 20] = -np.inf
+    B[5, 600] = 0.0             # A[3,5] = Inf times 0 -> NaN at (3, 600)
+    B[33, 4000] = np.nan
+    if dtype == "bf16":
+        a = hip.from_numpy(oracle.to_bf16(A))
+        b = hip.from_numpy(oracle.to_bf16(B))
+        Au, Bu = oracle.bf16_to_f32(a.numpy()), oracle.bf16_to_f32(b.numpy())
+    else:
+        a, b = hip.from_numpy(A), hip.from_numpy(B)
+        Au, Bu = A, B
+    got = hip.matmul(a, b).numpy()
+    rows = [3, 7, 11, 100]
+    cols = [20, 600, 4000, 17]
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref_rows = Au[rows].astype(np.float64) @ Bu.astype(np.float64)
+        ref_cols = Au.astype(np.float64) @ Bu[:, cols].astype(np.float64)
+    for g, r in ((got[rows], ref_rows), (got[:, cols], ref_cols)):
+        assert np.array_equal(np.isnan(g), np.isnan(r))
+        assert np.array_equal(np.isposinf(g), np.isposinf(r))
+        assert np.array_equal(np.isneginf(g), np.isneginf(r))
+    # the special entries are where they should be, and nowhere else
+    assert np.isnan(got[7]).all() and np.isnan(got[:, 4000]).all()
+    assert np.isnan(got[3, 600])
+    clean = np.ones((M, N), bool)
+    clean[[3, 7, 11]] = False
+    clean[:, [20, 4000]] = False
+    assert np.isfinite(got[clean]).all()
