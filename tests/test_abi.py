@@ -101,6 +101,24 @@ def test_python_signatures_cover_the_header():
     assert set(_lib.SIGNATURES) == set(header_functions())
 
 
+def test_integration_rust_binding_declares_every_c_function_with_its_arity():
+    # The FFI stub a cleave maintainer would copy must stay in step with the header.
+    text = (ROOT / "INTEGRATION.md").read_text()
+    block = text[text.index("unsafe extern \"C\" {"):]
+    block = block[:block.index("\n}\n")]
+    rust = {m.group(1): m.group(2) for m in re.finditer(r"pub fn (cleave_hip_\w+)\(([^)]*)\)", block, re.S)}
+    src = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    c = {m.group(1): m.group(2) for m in re.finditer(r"^CLEAVE_HIP_API [^(]*?\b(cleave_hip_\w+)\(([^)]*)\);", src, re.M | re.S)}
+    assert set(rust) == set(c)
+
+    def arity(params: str) -> int:
+        params = " ".join(params.split())
+        return 0 if params in ("", "void") else params.count(",") + 1
+
+    for name in c:
+        assert arity(rust[name]) == arity(c[name]), name
+
+
 def _lib_noabort():
     from cleave_amd import _lib
 
