@@ -244,12 +244,14 @@ int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N,
     int32_t st = CLEAVE_HIP_OK;
     // 256 x 256 tiles, when that still gives every CU a tile: the ping-pong
     // kernel (k-tiles of 32), or the tiled kernel (k-tiles of 64).  With one
-    // round of tiles and K up to 2048 the tiled kernel measured equal or 3-10%
-    // faster (64 x 512^3: 24.3 against 25.1-27.3 us); with K from 4096, or
-    // several rounds, the ping-pong kernel (8192^3: 802 against 830 us).
+    // round of tiles and K up to 512 the two measured equal (64 x 512^3:
+    // 25.0-29.3 against 25.5-26.9 us over two runs; 4096^2 x 512: 26.1-26.7
+    // against 26.3 us) and the tiled kernel is kept; from K = 1024 the
+    // ping-pong kernel is 2-5% faster (4096^2 x 2048: 58.7 against 60.5-61.7
+    // us), and with several rounds more so.
     const int64_t big_tiles = (int64_t)(M / 256) * (N / 256) * batch;
     if (big_tiles >= ch::num_cus()) {
-        const bool short_single_round = big_tiles <= ch::num_cus() && K <= 2048;
+        const bool short_single_round = big_tiles <= ch::num_cus() && K <= 512;
         if (!short_single_round && launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
         if (launch_tiled<256, 256, 64, 2, 4, 2, 16, TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
         if (launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
