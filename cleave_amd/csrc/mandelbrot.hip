@@ -22,24 +22,34 @@
 namespace {
 
 // Iterations per block of the unrolled loop.  Inside a block every lane
-// iterates; a lane counts the iterations after which it is still inside the
-// radius, so a lane whose first escape is iteration n counts exactly n and one
-// that never escapes counts max_iter (the reference's `escaped`/`count` latch,
-// examples/mandelbrot.cleave:14-26).  The wave leaves once no lane is alive.
-// Per iteration: 8 arithmetic ops, a compare, a mask update (scalar) and an
-// add -- no branch.
+// iterates, and the lanes still inside the radius after each iteration are
+// kept as a wave mask (the escape compare writes a mask, a scalar AND narrows
+// it).  A lane whose first escape is iteration n gets count n, and one that
+// never escapes gets max_iter (the reference's `escaped`/`count` latch,
+// examples/mandelbrot.cleave:14-26).  Per iteration: 8 arithmetic ops and a
+// compare on the VALU, one scalar AND -- no branch, no count update.  Only in
+// a block where some lane escapes are the escaping lanes' counts formed, from
+// the block's masks: n = the block's first iteration + the number of the
+// block's masks that still hold the lane.  The wave leaves once no lane is
+// alive.  At 16384^2 x 1000 blocks of 8 measured 6.10 ms, blocks of 16
+// 6.28 ms, and a count added every iteration 6.69 ms.
 constexpr int kBlockIters = 8;
 
 // count + 1 in the lanes set in `lanes` (a wave lane mask), as one
-// v_addc_co_u32 whose carry-in is that mask: one VALU op per iteration where
-// `count += alive ? 1 : 0` takes a select and half of a three-way add.
-// The carry-out goes to a scratch SGPR pair of its own, so consecutive
-// iterations do not serialise on VCC (which the compares write).
+// v_addc_co_u32 whose carry-in is that mask.  The carry-out goes to a scratch
+// SGPR pair of its own, so consecutive adds do not serialise on VCC.
 __device__ __forceinline__ uint32_t count_lanes(uint32_t count, uint64_t lanes) {
     uint32_t r;
     uint64_t carry_out;
     asm("v_addc_co_u32_e64 %0, %1, 0, %2, %3" : "=v"(r), "=s"(carry_out) : "v"(count), "s"(lanes));
     (void)carry_out;
+    return r;
+}
+
+// if_set in the lanes set in `lanes`, if_clear in the others.
+__device__ __forceinline__ uint32_t select_lanes(uint64_t lanes, uint32_t if_set, uint32_t if_clear) {
+    uint32_t r;
+    asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(if_clear), "v"(if_set), "s"(lanes));
     return r;
 }
 
@@ -53,14 +63,14 @@ __global__ __launch_bounds__(256) void mandelbrot_kernel(uint32_t* __restrict__ 
     const float cr = x0 + (float)col * dx;
     const float ci = y0 + (float)row * dy;
     float zr = 0.0f, zi = 0.0f, zr2 = 0.0f, zi2 = 0.0f;
-    uint32_t count = 0;
-    // The lanes still inside the radius, as a wave mask: the escape compare
-    // writes a mask, a scalar AND narrows it, and the count add reads it.
+    uint32_t count = 0;  // final in the lanes that have escaped
     uint64_t alive = __builtin_amdgcn_ballot_w64(inside);
     int n = 0;
     // Whole blocks: lanes past their escape keep iterating (z may overflow to
     // inf/NaN, which no longer matters: the count is latched).
     for (; n + kBlockIters <= max_iter; n += kBlockIters) {
+        const uint64_t before = alive;
+        uint64_t after[kBlockIters];  // alive after each iteration of the block
 #pragma unroll
         for (int u = 0; u < kBlockIters; ++u) {
             const float p = zr * zi;
@@ -71,12 +81,20 @@ __global__ __launch_bounds__(256) void mandelbrot_kernel(uint32_t* __restrict__ 
             zr2 = zr * zr;
             zi2 = zi * zi;
             alive &= __builtin_amdgcn_ballot_w64(!(zr2 + zi2 > 4.0f));
-            count = count_lanes(count, alive);
+            after[u] = alive;
+        }
+        const uint64_t escaped = before & ~alive;
+        if (escaped != 0) {  // wave-uniform
+            uint32_t c = (uint32_t)n;
+#pragma unroll
+            for (int u = 0; u < kBlockIters; ++u) c = count_lanes(c, after[u]);
+            count = select_lanes(escaped, c, count);
         }
         if (alive == 0) break;
     }
     // Remaining max_iter % kBlockIters iterations (only when some lane survived).
     for (int m = n; m < max_iter && alive != 0; ++m) {
+        const uint64_t before = alive;
         const float p = zr * zi;
         const float re = zr2 - zi2;
         const float im = p + p;
@@ -85,8 +103,9 @@ __global__ __launch_bounds__(256) void mandelbrot_kernel(uint32_t* __restrict__ 
         zr2 = zr * zr;
         zi2 = zi * zi;
         alive &= __builtin_amdgcn_ballot_w64(!(zr2 + zi2 > 4.0f));
-        count = count_lanes(count, alive);
+        count = select_lanes(before & ~alive, (uint32_t)m, count);
     }
+    count = select_lanes(alive, (uint32_t)max_iter, count);  // never escaped
     if (inside) out[(int64_t)row * width + col] = count;
 }
 
