@@ -150,7 +150,8 @@ def test_add_row_bias_matches_the_oracle_bitwise(hip, oracle, rows, cols):
     assert np.array_equal(out, oracle.add_row_bias(A, b))
 
 
-@pytest.mark.parametrize("rows,cols", [(1, 8), (37, 64), (1000, 1028), (4097, 96), (7, 13), (300, 3)])
+@pytest.mark.parametrize("rows,cols", [(1, 8), (3, 64), (5, 256), (9, 4096), (37, 64), (1000, 1028), (4097, 96),
+                                       (7, 13), (300, 3)])
 def test_sum_rows_against_the_left_fold(hip, oracle, rows, cols):
     rng = np.random.default_rng(rows * 7 + cols)
     # integer-valued cotangents: every summation order is exact, so bit-equal
