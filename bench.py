@@ -443,7 +443,7 @@ def main():
         g = 16384
         d = np.float32(3.0 / g)
         cnt = ca.empty((g, g), "u32")
-        wall_s, ev = timed(ca, lambda: ca.escape_counts(g, g, -2.0, -1.5, d, d, 1000, out=cnt), 3, 1)
+        wall_s, ev = timed(ca, lambda: ca.escape_counts(g, g, -2.0, -1.5, d, d, 1000, out=cnt), 10, 2, 0.2)
         # sum of counts = iterations executed by escaped pixels minus one each,
         # max_iter for pixels that never escape: a lower bound of the executed work
         total = ca.sum_u64(cnt)
