@@ -66,10 +66,11 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
     const int64_t step_a = copy_a.kstep(lda), step_b = copy_b.kstep(ldb);
     const uint32_t lds0 = lds_addr(smem);
     const int nk = K / BK;
-    auto issue = [&](int kt) {
+    auto issue = [&](int kt) {  // k-tile min(kt, nk-1) into stage kt % S
+        const int src = min(kt, nk - 1);
         const uint32_t dst = lds0 + (uint32_t)((kt % S) * P::STAGE_BYTES);
-        copy_a.issue(reinterpret_cast<const char*>(A) + kt * step_a, dst, wave);
-        copy_b.issue(reinterpret_cast<const char*>(B) + kt * step_b, dst + P::A_BYTES, wave);
+        copy_a.issue(reinterpret_cast<const char*>(A) + src * step_a, dst, wave);
+        copy_b.issue(reinterpret_cast<const char*>(B) + src * step_b, dst + P::A_BYTES, wave);
     };
 
     v4f acc[FM][FN];
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
             if constexpr (BKC) fb[j] = read16_kc_at(rb[W][j & 1] + SO + (uint32_t)(j / 2) * PAIR);
             else fb[j] = read16_mn_at<P::BN>(rb[W][j] + SO);
         }
-        pingpong_copy<LPW, S>(u, nk, issue);
+        pingpong_copy<LPW, S>(u, issue);
     };
     auto c_phase = [&](int) {
         __builtin_amdgcn_s_setprio(1);

@@ -321,7 +321,7 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
             issue_dma(u + S - 1);
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         } else {
-            pingpong_copy<P::LDMA>(u, nk, issue_dma);
+            pingpong_copy<P::LDMA>(u, issue_dma);
         }
     };
     // Half-wave h holds k = 8*kb + 4*h + s at step s for both operands, so the
@@ -378,9 +378,6 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
             asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
         }
         pingpong_schedule<P::LDMA>(nk, grp, [](int) {}, m_phase, c_phase, /*prologue_copies=*/false);
-        // the clamped copies past the last k-tile must land before the
-        // workgroup's LDS is released
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     } else {
         pingpong_schedule<P::LDMA>(nk, grp, issue_dma, m_phase, c_phase, /*prologue_copies=*/true);
     }

@@ -36,25 +36,20 @@ constexpr int kPingPongStages = 4;
 template <int ST>
 using PingPongStage = std::integral_constant<int, ST>;
 
-// s_waitcnt vmcnt(n * LPW) lgkmcnt(0) for a runtime tile count n in 0..3.
-template <int LPW>
-__device__ __forceinline__ void wait_tiles(int n) {
-    if (n >= 3) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(3 * LPW) : "memory");
-    else if (n == 2) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * LPW) : "memory");
-    else if (n == 1) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(LPW) : "memory");
-    else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-}
-
-// The copy half of an M phase for k-tile u: issue tile u+S-1 (if any), then
-// wait for this wave's copy of tile u+1 -- the tiles issued after it may
-// stay in flight -- and for the LDS reads already issued.  LPW is the number
-// of copy instructions a wave issues per k-tile.
+// The copy half of an M phase for k-tile u: issue tile u+S-1, then wait for
+// this wave's copy of tile u+1 -- the S-2 tiles issued after it may stay in
+// flight -- and for the LDS reads already issued.  LPW is the number of copy
+// instructions a wave issues per k-tile.  The copy is unconditional: issue()
+// clamps its source to the last k-tile, so past the end it refills the stage
+// of a tile both groups have finished with, which no later M phase reads.
+// That keeps the M phase free of branches and its wait a constant (measured
+// 0.5-3% faster for the bf16 kernel than issuing only real tiles and picking
+// the wait count at run time).
 template <int LPW, int S = kPingPongStages, class Issue>
-__device__ __forceinline__ void pingpong_copy(int u, int nk, Issue&& issue) {
-    static_assert(S >= 2 && S - 2 <= 3, "wait_tiles covers up to three later tiles");
-    if (u + S - 1 < nk) issue(u + S - 1);
-    const int later = min(u + S - 1, nk - 1) - (u + 1);  // tiles issued after u+1
-    wait_tiles<LPW>(later < 0 ? 0 : later);
+__device__ __forceinline__ void pingpong_copy(int u, Issue&& issue) {
+    static_assert(S >= 3 && (S - 2) * LPW < 64, "vmcnt counts up to 63");
+    issue(u + S - 1);
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((S - 2) * LPW) : "memory");
 }
 
 // step(PingPongStage<(OFF + i) % S>{}, s + i) for i = 0, 1, ... while s + i < nk.
@@ -65,7 +60,7 @@ __device__ __forceinline__ void pingpong_unrolled(int s, int nk, Step& step,
 }
 
 // Runs the whole schedule over nk k-tiles.  issue(kt) copies this wave's
-// share of k-tile kt into stage kt % S; m_phase(PingPongStage<ST>{}, u) is the
+// share of k-tile min(kt, nk-1) into stage kt % S; m_phase(PingPongStage<ST>{}, u) is the
 // M phase of k-tile u (stage ST = u % S), ending in pingpong_copy<LPW, S>;
 // c_phase(u) is the C phase of k-tile u, on the fragments the wave's last M
 // phase read.  With prologue_copies false the caller has already put tile 0 in
@@ -77,9 +72,8 @@ __device__ __forceinline__ void pingpong_schedule(int nk, int grp, Issue&& issue
     // reads k-tile 0 (and issues tile S-1) so it can compute in phase 0.
     if (prologue_copies) {
 #pragma unroll
-        for (int t = 0; t < S - 1; ++t)
-            if (t < nk) issue(t);
-        wait_tiles<LPW>(min(S - 2, nk - 1));  // tiles issued after tile 0
+        for (int t = 0; t < S - 1; ++t) issue(t);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((S - 2) * LPW) : "memory");  // tile 0 landed
     }
     asm volatile("s_barrier" ::: "memory");
 
@@ -111,6 +105,9 @@ __device__ __forceinline__ void pingpong_schedule(int nk, int grp, Issue&& issue
         for (int s = 0; s < nk; s += S)
             pingpong_unrolled<S, 0>(s, nk, step1, std::make_integer_sequence<int, S>{});
     }
+    // the copies past the last k-tile must land before the workgroup's LDS
+    // is released
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 }  // namespace ch
