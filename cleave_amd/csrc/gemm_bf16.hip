@@ -233,8 +233,17 @@ bool launch_pingpong(const uint16_t* a, const uint16_t* b, float* c, int M, int 
     const int tiles_m = M / P::BM, tiles_n = N / P::BN;
     if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
     dim3 grid((unsigned)(tiles_m * tiles_n * batch));
-    ch::gemm_bf16_pingpong_kernel<!TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
-        a, b, c, M, N, K, lda, ldb, (int64_t)M * K, (int64_t)K * N, (int64_t)M * N, tiles_m, tiles_n, batch);
+    // byte offset of the last k-tile from an operand's base: k-contiguous
+    // operands step 64 bytes per k-tile, m/n-contiguous ones 32 rows
+    const uint64_t last_a = (uint64_t)K * (TA ? (uint64_t)lda * 2 : 2);
+    const uint64_t last_b = (uint64_t)K * (TB ? 2 : (uint64_t)ldb * 2);
+    const int64_t sa = (int64_t)M * K, sb = (int64_t)K * N, sc = (int64_t)M * N;
+    if (last_a < (1ull << 32) && last_b < (1ull << 32))
+        ch::gemm_bf16_pingpong_kernel<!TA, TB, true><<<grid, P::THREADS, 0, ch::stream()>>>(
+            a, b, c, M, N, K, lda, ldb, sa, sb, sc, tiles_m, tiles_n, batch);
+    else
+        ch::gemm_bf16_pingpong_kernel<!TA, TB, false><<<grid, P::THREADS, 0, ch::stream()>>>(
+            a, b, c, M, N, K, lda, ldb, sa, sb, sc, tiles_m, tiles_n, batch);
     *status = ch::check_hip(hipGetLastError(), "gemm_bf16_pingpong_kernel");
     return true;
 }

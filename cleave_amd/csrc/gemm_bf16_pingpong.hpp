@@ -39,7 +39,10 @@ struct Bf16PingPong {
     }
 };
 
-template <bool AKC, bool BKC, int STAGES_ = 5>
+// OFF32: every k-tile's offset from an operand's base fits 32 bits (K times
+// the operand's k-step under 4 GiB), so the M phase forms the copy sources
+// with one 32-bit scalar multiply instead of a 64-bit one (0.5-1% at 8192^3).
+template <bool AKC, bool BKC, bool OFF32 = false, int STAGES_ = 5>
 __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC,
@@ -66,11 +69,17 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
     const int64_t step_a = copy_a.kstep(lda), step_b = copy_b.kstep(ldb);
     const uint32_t lds0 = lds_addr(smem);
     const int nk = K / BK;
+    const uint32_t step_a32 = (uint32_t)step_a, step_b32 = (uint32_t)step_b;
     auto issue = [&](int kt) {  // k-tile min(kt, nk-1) into stage kt % S
         const int src = min(kt, nk - 1);
         const uint32_t dst = lds0 + (uint32_t)((kt % S) * P::STAGE_BYTES);
-        copy_a.issue(reinterpret_cast<const char*>(A) + src * step_a, dst, wave);
-        copy_b.issue(reinterpret_cast<const char*>(B) + src * step_b, dst + P::A_BYTES, wave);
+        if constexpr (OFF32) {
+            copy_a.issue(reinterpret_cast<const char*>(A) + (uint32_t)src * step_a32, dst, wave);
+            copy_b.issue(reinterpret_cast<const char*>(B) + (uint32_t)src * step_b32, dst + P::A_BYTES, wave);
+        } else {
+            copy_a.issue(reinterpret_cast<const char*>(A) + src * step_a, dst, wave);
+            copy_b.issue(reinterpret_cast<const char*>(B) + src * step_b, dst + P::A_BYTES, wave);
+        }
     };
 
     v4f acc[FM][FN];
