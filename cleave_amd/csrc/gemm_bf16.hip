@@ -248,6 +248,27 @@ bool launch_pingpong(const uint16_t* a, const uint16_t* b, float* c, int M, int 
     return true;
 }
 
+// Layouts with one k-contiguous operand (A·B, Aᵀ·Bᵀ): the ping-pong kernel
+// that copies that operand two k-tiles at a time (gemm_bf16_pingpong.hpp).
+template <bool TA, bool TB>
+bool launch_pairs(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
+                  int32_t* status) {
+    if constexpr (TA != TB) {
+        return false;
+    } else {
+        using P = ch::Bf16PingPongPairs<!TA, TB>;
+        const int64_t lda = TA ? M : K, ldb = TB ? K : N;
+        if (!P::fits(M, N, K, lda, ldb) || ((uintptr_t)a & 15) || ((uintptr_t)b & 15)) return false;
+        const int tiles_m = M / P::BM, tiles_n = N / P::BN;
+        if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
+        dim3 grid((unsigned)(tiles_m * tiles_n * batch));
+        ch::gemm_bf16_pingpong_pairs_kernel<!TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
+            a, b, c, M, N, K, lda, ldb, (int64_t)M * K, (int64_t)K * N, (int64_t)M * N, tiles_m, tiles_n, batch);
+        *status = ch::check_hip(hipGetLastError(), "gemm_bf16_pingpong_pairs_kernel");
+        return true;
+    }
+}
+
 template <bool TA, bool TB>
 int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch) {
     int32_t st = CLEAVE_HIP_OK;
@@ -261,6 +282,7 @@ int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N,
     const int64_t big_tiles = (int64_t)(M / 256) * (N / 256) * batch;
     if (big_tiles >= ch::num_cus()) {
         const bool short_single_round = big_tiles <= ch::num_cus() && K <= 512;
+        if (!short_single_round && launch_pairs<TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
         if (!short_single_round && launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
         if (launch_tiled<256, 256, 64, 2, 4, 2, 16, TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
         if (launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, &st)) return st;

@@ -159,3 +159,188 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
 }
 
 }  // namespace ch
+
+namespace ch {
+
+// The same ping-pong for the layouts with exactly one k-contiguous operand
+// (A·B: A; Aᵀ·Bᵀ: B).  A k-contiguous k-tile is a 64-byte segment of each
+// row, and copying it as such cost 3-5% against the layout with none.  Here
+// that operand ("paired") is copied two k-tiles at a time, whole 128-byte
+// rows, into a ring of 3 pair-stages (96 KiB); the m/n-contiguous operand
+// ("single") keeps a ring of 4 single k-tile stages (64 KiB).  8192^3 A·B:
+// 0.736-0.740 ms against 0.777-0.790 for the single-stage kernel, bit-identical.
+//
+// Pair-stage layout: [256 rows][8 chunks of 16 bytes], chunk c of row r in
+// slot c ^ ((r >> 1) & 7).  A fragment read has each 16-lane quarter read one
+// chunk of 16 consecutive rows; rows r and r+1 sit 128 bytes apart and the
+// XOR spreads the 8 row pairs over the 8 slots, so the quarter covers all
+// 256 bytes of the banks once.
+//
+// Copy schedule, per M phase u: the pair u/2 + 2 (at even u, 4 instructions
+// per wave) and then the single k-tile u + 3 (2 per wave), both clamped to
+// the last one.  This wave's copies of k-tile u + 1 were issued at M(u - 2)
+// or earlier, and exactly 8 instructions follow them: M(u - 1) and M(u)
+// issue 2 single instructions each and one of them, being even, a pair.  So
+// every M phase ends in s_waitcnt vmcnt(8).
+template <bool AKC, bool BKC>
+struct Bf16PingPongPairs {
+    static_assert(AKC != BKC, "exactly one k-contiguous operand");
+    static constexpr int BM = 256, BN = 256, BK = 32, NW = 8, WN = 4, THREADS = 64 * NW;
+    static constexpr int TM = 128, TN = 64, FM = TM / 16, FN = TN / 16;
+    static constexpr int PAIR_BYTES = 256 * 2 * BK * 2, SINGLE_BYTES = 256 * BK * 2;
+    static constexpr int PAIRS = 3, SINGLES = 4, PERIOD = 12;  // PERIOD = lcm(2 * PAIRS, SINGLES)
+    static constexpr int SINGLE_REGION = PAIRS * PAIR_BYTES;
+    static constexpr int LDS_BYTES = SINGLE_REGION + SINGLES * SINGLE_BYTES;
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS per workgroup");
+
+    // Also requires every byte offset a copy forms (the whole k-contiguous
+    // operand, K rows of the m/n-contiguous one) under 4 GiB.
+    static bool fits(int M, int N, int K, int64_t lda, int64_t ldb) {
+        const bool dims = M % BM == 0 && N % BN == 0 && K % (2 * BK) == 0 && lda % 8 == 0 && ldb % 8 == 0;
+        const uint64_t a_span = (uint64_t)(AKC ? M : K + 1) * (uint64_t)lda * 2;
+        const uint64_t b_span = (uint64_t)(BKC ? N : K + 1) * (uint64_t)ldb * 2;
+        return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
+    }
+};
+
+template <bool AKC, bool BKC>
+__global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, float* __restrict__ C, int M,
+    int N, int K, int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC,
+    int tiles_m, int tiles_n, int batch) {
+    using namespace ch::tiles;
+    using P = Bf16PingPongPairs<AKC, BKC>;
+    constexpr int FM = P::FM, FN = P::FN, NW = P::NW, BK = P::BK;
+    constexpr int PAIRS = P::PAIRS, SINGLES = P::SINGLES;
+    __shared__ __attribute__((aligned(1024))) char smem[P::LDS_BYTES];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = wave / P::WN, wn = wave % P::WN;
+    int bt, tm, tn;
+    ch::block_coords(blockIdx.x, tiles_m, tiles_n, batch, bt, tm, tn);
+    const int m0 = tm * P::BM, n0 = tn * P::BN;
+    A += (int64_t)bt * strideA;
+    B += (int64_t)bt * strideB;
+    C += (int64_t)bt * strideC;
+    const uint32_t lds0 = lds_addr(smem);
+    const int nk = K / BK, np = nk / 2;
+
+    // the paired (k-contiguous) operand and the single (m/n-contiguous) one
+    const char* pbase = reinterpret_cast<const char*>(AKC ? A : B);
+    const char* sbase = reinterpret_cast<const char*>(AKC ? B : A);
+    const int64_t pld = AKC ? lda : ldb, sld = AKC ? ldb : lda;
+    const int pr0 = AKC ? m0 : n0, sr0 = AKC ? n0 : m0;
+
+    // pair copy: instruction q = wave + 8 j moves rows 8q .. 8q+7; lane l takes
+    // row 8q + l/8 and slot l%8, which holds chunk (l%8) ^ ((row >> 1) & 7)
+    uint32_t pvoff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int q = wave + NW * j;
+        const int r = 8 * q + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        pvoff[j] = (uint32_t)(((int64_t)(pr0 + r) * pld + 8 * c) * 2);
+    }
+    TileCopy<false, 256, BK, NW> scopy;
+    scopy.init(sld, sr0, wave, lane);
+    const uint32_t sstep = (uint32_t)scopy.kstep(sld);
+    auto issue_pair = [&](auto stage, int p) {
+        constexpr int PS = decltype(stage)::value;
+        const char* src = pbase + (uint32_t)min(p, np - 1) * (uint32_t)(2 * BK * 2);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            dma16(src, pvoff[j], lds0 + (uint32_t)(PS * P::PAIR_BYTES + 1024 * (wave + NW * j)));
+    };
+    auto issue_single = [&](auto stage, int kt) {
+        constexpr int SS = decltype(stage)::value;
+        scopy.issue(sbase + (uint32_t)min(kt, nk - 1) * sstep,
+                    lds0 + (uint32_t)(P::SINGLE_REGION + SS * P::SINGLE_BYTES), wave);
+    };
+
+    // Fragment addresses.  Paired operand: per 64 KiB window (pair-stages 0-1,
+    // pair-stage 2) and per half h of the pair; its fragments 16 rows apart
+    // differ by an immediate.  Single operand: one window over its 4 stages,
+    // one register per fragment (its swizzle mixes the fragment's columns).
+    constexpr int NPF = AKC ? FM : FN, NSF = AKC ? FN : FM;  // paired / single fragments
+    const int prow0 = AKC ? grp * P::TM : wn * P::TN;
+    const int srow0 = AKC ? wn * P::TN : grp * P::TM;
+    uint32_t rp[2][2], rs[NSF];
+    {
+        const int x = (lane & 15) >> 1, qd = lane >> 4;
+        const int r = prow0 + (lane & 15);
+#pragma unroll
+        for (int w = 0; w < 2; ++w)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                rp[w][h] = lds0 + (uint32_t)(w * 2 * P::PAIR_BYTES) + (uint32_t)(r * 128 + (((h << 2) | qd) ^ x) * 16);
+                opaque(rp[w][h]);
+            }
+#pragma unroll
+        for (int f = 0; f < NSF; ++f) {
+            rs[f] = lds0 + (uint32_t)P::SINGLE_REGION + frag16_offset<false, 256, BK>(srow0 + f * 16, lane);
+            opaque(rs[f]);
+        }
+    }
+
+    v4f acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = v4f{};
+    v8bf fa[FM], fb[FN];
+
+    // M phase of k-tile u (ST = u % 12): fragments, then the copies, then the wait.
+    auto m_phase = [&](auto phase, int u) {
+        constexpr int ST = decltype(phase)::value;
+        constexpr int H = ST % 2, PS = (ST / 2) % PAIRS, SS = ST % SINGLES, W = PS / 2;
+        constexpr uint32_t PO = (uint32_t)((PS - 2 * W) * P::PAIR_BYTES);
+#pragma unroll
+        for (int f = 0; f < NPF; ++f) {
+            const v8bf v = read16_kc_at(rp[W][H] + PO + (uint32_t)(f * 16 * 128));
+            if constexpr (AKC) fa[f] = v;
+            else fb[f] = v;
+        }
+#pragma unroll
+        for (int f = 0; f < NSF; ++f) {
+            const v8bf v = read16_mn_at<256>(rs[f] + (uint32_t)(SS * P::SINGLE_BYTES));
+            if constexpr (AKC) fb[f] = v;
+            else fa[f] = v;
+        }
+        if constexpr (H == 0) issue_pair(std::integral_constant<int, (ST / 2 + 2) % PAIRS>{}, u / 2 + 2);
+        issue_single(std::integral_constant<int, (ST + 3) % SINGLES>{}, u + 3);
+        asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+    };
+    auto c_phase = [&](int) {
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_s_setprio(0);
+    };
+    // Prologue in the steady state's order (pair 0, single 0, pair 1, single
+    // 1, single 2): k-tile 0 has landed once 8 later instructions remain.
+    issue_pair(std::integral_constant<int, 0>{}, 0);
+    issue_single(std::integral_constant<int, 0>{}, 0);
+    issue_pair(std::integral_constant<int, 1>{}, 1);
+    issue_single(std::integral_constant<int, 1>{}, 1);
+    issue_single(std::integral_constant<int, 2>{}, 2);
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    pingpong_schedule<1, P::PERIOD>(nk, grp, [](int) {}, m_phase, c_phase, /*prologue_copies=*/false);
+
+    // 16 x 16 accumulator layout: lane holds column l%16, rows 4*(l/16) + v.
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int r = m0 + grp * P::TM + i * 16 + 4 * (lane >> 4) + v;
+                const int c = n0 + wn * P::TN + j * 16 + (lane & 15);
+                C[(int64_t)r * N + c] = acc[i][j][v];
+            }
+}
+
+}  // namespace ch

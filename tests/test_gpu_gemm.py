@@ -280,12 +280,15 @@ def test_f32_batched_through_pingpong(hip, oracle):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-@pytest.mark.parametrize("K", [32, 128, 160, 192, 352])
+@pytest.mark.parametrize("K", [32, 64, 128, 160, 192, 352, 384, 832])
 def test_bf16_pingpong_ring_depths(hip, oracle, K, ta, tb):
-    # 1, 4, 5, 6 and 11 k-tiles of 32 through the ring of five LDS stages:
-    # never filled, one short of full, exactly full, wrapping once, wrapping
-    # twice.  4096 x 8192 outputs are two rounds of 256 x 256 tiles, which the
-    # dispatch always gives to the ping-pong kernel.
+    # 4096 x 8192 outputs are two rounds of 256 x 256 tiles, which the
+    # dispatch gives to a ping-pong kernel.  With K a multiple of 64, A·B and
+    # Aᵀ·Bᵀ take the kernel that copies the k-contiguous operand in pairs of
+    # k-tiles (a ring of 3 pairs beside a ring of 4 single k-tiles): K = 64,
+    # 128, 192, 384, 832 are 1, 2, 3, 6 and 13 pairs (never filled, filled,
+    # wrapping).  The other K, and the other layouts, take the kernel with a
+    # ring of five single k-tiles: 1, 5 and 11 k-tiles for K = 32, 160, 352.
     M, N = 4096, 8192
     a = hip.to_bf16(hip.fill_normal(hip.empty((K, M) if ta else (M, K)), seed=101 + K + 2 * ta + tb, std=0.02))
     b = hip.to_bf16(hip.fill_normal(hip.empty((N, K) if tb else (K, N)), seed=111 + K + 2 * ta + tb, std=0.02))
