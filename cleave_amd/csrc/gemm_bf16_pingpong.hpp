@@ -145,17 +145,7 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
     };
     pingpong_schedule<LPW, S>(nk, grp, issue, m_phase, c_phase);
 
-    // 16 x 16 accumulator layout: lane holds column l%16, rows 4*(l/16) + v.
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int r = m0 + grp * P::TM + i * 16 + 4 * (lane >> 4) + v;
-                const int c = n0 + wn * P::TN + j * 16 + (lane & 15);
-                C[(int64_t)r * N + c] = acc[i][j][v];
-            }
+    store_acc16_lines(C, N, m0 + grp * P::TM, n0 + wn * P::TN, acc, lane);
 }
 
 }  // namespace ch
@@ -330,17 +320,7 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
     asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
     pingpong_schedule<1, P::PERIOD>(nk, grp, [](int) {}, m_phase, c_phase, /*prologue_copies=*/false);
 
-    // 16 x 16 accumulator layout: lane holds column l%16, rows 4*(l/16) + v.
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int r = m0 + grp * P::TM + i * 16 + 4 * (lane >> 4) + v;
-                const int c = n0 + wn * P::TN + j * 16 + (lane & 15);
-                C[(int64_t)r * N + c] = acc[i][j][v];
-            }
+    store_acc16_lines(C, N, m0 + grp * P::TM, n0 + wn * P::TN, acc, lane);
 }
 
 }  // namespace ch

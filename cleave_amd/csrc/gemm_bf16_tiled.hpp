@@ -178,24 +178,22 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
         mfma_step((KS - 1) & 1);
     }
 
-    // Accumulator layouts: 32 x 32 -> lane holds column l%32, rows
-    // 8*(v/4) + 4*(l/32) + v%4; 16 x 16 -> column l%16, rows 4*(l/16) + v.
+    // 32 x 32 accumulator layout: lane holds column l%32, rows
+    // 8*(v/4) + 4*(l/32) + v%4, so a store already covers whole 128-byte rows.
+    if constexpr (MI == 16) {
+        store_acc16_lines(C, N, m0 + wm * P::TM, n0 + wn * P::TN, acc, lane);
+    } else {
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
+            for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int v = 0; v < (MI == 32 ? 16 : 4); ++v) {
-                int r, c;
-                if constexpr (MI == 32) {
-                    r = m0 + wm * P::TM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                    c = n0 + wn * P::TN + j * 32 + (lane & 31);
-                } else {
-                    r = m0 + wm * P::TM + i * 16 + 4 * (lane >> 4) + v;
-                    c = n0 + wn * P::TN + j * 16 + (lane & 15);
+                for (int v = 0; v < 16; ++v) {
+                    const int r = m0 + wm * P::TM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                    const int c = n0 + wn * P::TN + j * 32 + (lane & 31);
+                    C[(int64_t)r * N + c] = acc[i][j][v];
                 }
-                C[(int64_t)r * N + c] = acc[i][j][v];
-            }
+    }
 }
 
 }  // namespace ch
