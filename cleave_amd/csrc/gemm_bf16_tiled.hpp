@@ -46,10 +46,6 @@ struct Bf16Tiled {
     static_assert(LDS_BYTES <= 160 * 1024, "LDS per workgroup");
 
     // Shapes this kernel takes without bounds checks.  The copies address an
-    // operand with 32-bit byte offsets from a per-k-tile scalar base, so a
-    // k-contiguous operand must stay under 4 GiB (an m/n-contiguous one only
-    // needs its BK-row band to).
-    // Shapes this kernel takes without bounds checks.  The copies address an
     // operand with 32-bit byte offsets from a per-k-tile scalar base, so the
     // addressed span of each operand must stay under 4 GiB.
     static bool fits(int M, int N, int K, int64_t lda, int64_t ldb) {
