@@ -278,7 +278,9 @@ int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N,
     // 25.0-29.3 against 25.5-26.9 us over two runs; 4096^2 x 512: 26.1-26.7
     // against 26.3 us) and the tiled kernel is kept; from K = 1024 the
     // ping-pong kernel is 2-5% faster (4096^2 x 2048: 58.7 against 60.5-61.7
-    // us), and with several rounds more so.
+    // us), and with several rounds more so.  With whole-line C stores in all
+    // three, 64 x 512^3 measured 24.3-24.5 us tiled, 24.8-24.9 paired-copy
+    // ping-pong, 25.0-25.7 single-stage ping-pong (same box).
     const int64_t big_tiles = (int64_t)(M / 256) * (N / 256) * batch;
     if (big_tiles >= ch::num_cus()) {
         const bool short_single_round = big_tiles <= ch::num_cus() && K <= 512;
