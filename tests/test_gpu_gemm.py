@@ -280,6 +280,27 @@ def test_f32_batched_through_pingpong(hip, oracle):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_bf16_pingpong_every_entry(hip, oracle, ta, tb):
+    # Two rounds of 256 x 256 tiles go to a ping-pong kernel (the paired-copy
+    # one for A·B and Aᵀ·Bᵀ).  Its epilogue swaps 16-lane rows between
+    # accumulator blocks to store whole 128-byte rows; every entry of C is
+    # checked, since a value stored in the wrong column of its row would keep
+    # the row sums the sampled tests also check.
+    M, N, K = 4096, 8192, 128
+    rng = np.random.default_rng(40 + 2 * ta + tb)
+    A = oracle.to_bf16(rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32))
+    B = oracle.to_bf16(rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32))
+    got = hip.matmul(hip.from_numpy(A, "bf16"), hip.from_numpy(B, "bf16"), trans_a=bool(ta),
+                     trans_b=bool(tb)).numpy()
+    Au = oracle.bf16_to_f32(A).reshape(A.shape)
+    Bu = oracle.bf16_to_f32(B).reshape(B.shape)
+    ref = oracle.matmul(Au, Bu, trans_a=bool(ta), trans_b=bool(tb), threads=16)
+    Ad = np.abs(Au.T if ta else Au).astype(np.float64)
+    Bd = np.abs(Bu.T if tb else Bu).astype(np.float64)
+    assert_gemm_close(got, ref, Ad @ Bd, K, f"bf16 ping-pong every entry ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("K", [32, 64, 128, 160, 192, 352, 384, 832])
 def test_bf16_pingpong_ring_depths(hip, oracle, K, ta, tb):
     # 4096 x 8192 outputs are two rounds of 256 x 256 tiles, which the
