@@ -100,6 +100,16 @@ class Tensor:
             raise ValueError(f"view {shape} does not cover {self.size} elements")
         return t
 
+    def sub(self, offset: int, shape) -> "Tensor":
+        """The elements [offset, offset + prod(shape)) of the buffer, as a tensor of
+        that shape (no copy)."""
+        shape = tuple(int(d) for d in shape)
+        t = Tensor(self.ptr + int(offset) * _DTYPES[self.dtype][1], shape, self.dtype, owned=False,
+                   base=self)
+        if offset < 0 or offset + t.size > self.size:
+            raise ValueError(f"sub-tensor [{offset}, {offset + t.size}) outside {self.size} elements")
+        return t
+
     def free(self) -> None:
         if self.owned and self.ptr:
             load().cleave_hip_buf_free(self.ptr)
@@ -156,7 +166,7 @@ def matmul(a: Tensor, b: Tensor, trans_a: bool = False, trans_b: bool = False,
 
 def matmul_batched(a: Tensor, b: Tensor, out: Tensor | None = None, trans_a: bool = False,
                    trans_b: bool = False) -> Tensor:
-    """batch x (M x K) . batch x (K x N); bf16 batched supports the plain layout only."""
+    """batch x op(M x K) . batch x op(K x N), with the single product's trans flags."""
     batch, M, K = a.shape
     _, Kb, N = b.shape
     if trans_a:
@@ -168,10 +178,8 @@ def matmul_batched(a: Tensor, b: Tensor, out: Tensor | None = None, trans_a: boo
         call("cleave_hip_matmul_batched_f32", a.ptr, a.size, b.ptr, b.size, out.ptr, out.size,
              batch, M, N, K, int(trans_a), int(trans_b))
     else:
-        if trans_a or trans_b:
-            raise ValueError("matmul_batched: bf16 supports the untransposed layout only")
         call("cleave_hip_matmul_batched_bf16", a.ptr, a.size, b.ptr, b.size, out.ptr, out.size,
-             batch, M, N, K)
+             batch, M, N, K, int(trans_a), int(trans_b))
     return out
 
 

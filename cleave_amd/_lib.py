@@ -62,7 +62,7 @@ SIGNATURES: dict[str, tuple] = {
     "cleave_hip_matmul_f32": (i32, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, i32]),
     "cleave_hip_matmul_batched_f32": (i32, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, i32, i32]),
     "cleave_hip_matmul_bf16": (i32, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, i32]),
-    "cleave_hip_matmul_batched_bf16": (i32, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32]),
+    "cleave_hip_matmul_batched_bf16": (i32, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, i32, i32]),
     "cleave_hip_add_f32": (i32, [vp, i64, vp, i64, vp, i64]),
     "cleave_hip_sub_f32": (i32, [vp, i64, vp, i64, vp, i64]),
     "cleave_hip_mul_f32": (i32, [vp, i64, vp, i64, vp, i64]),
@@ -92,6 +92,37 @@ SIGNATURES: dict[str, tuple] = {
     "cleave_hip_mandelbrot_u32": (i32, [vp, i64, i32, i32, f32, f32, f32, f32, i32]),
     "cleave_hip_mlp_step_f32": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64,
                                       vp, i32, i32, i32, f32]),
+    # host-array forms: the device form's signature, every tensor operand a host array
+    "cleave_hip_matmul_f32_host": (i32, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, i32]),
+    "cleave_hip_matmul_batched_f32_host": (i32, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, i32, i32]),
+    "cleave_hip_matmul_bf16_host": (i32, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, i32]),
+    "cleave_hip_matmul_batched_bf16_host": (i32, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, i32, i32]),
+    "cleave_hip_add_f32_host": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_sub_f32_host": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_mul_f32_host": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_div_f32_host": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_neg_f32_host": (i32, [vp, i64, vp, i64]),
+    "cleave_hip_zero_f32_host": (i32, [vp, i64]),
+    "cleave_hip_relu_f32_host": (i32, [vp, i64, vp, i64]),
+    "cleave_hip_sigmoid_f32_host": (i32, [vp, i64, vp, i64]),
+    "cleave_hip_tanh_f32_host": (i32, [vp, i64, vp, i64]),
+    "cleave_hip_sigmoid_bwd_f32_host": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_tanh_bwd_f32_host": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_relu_bwd_f32_host": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_div_bwd_f32_host": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_sgd_update_f32_host": (i32, [vp, i64, vp, i64, f32]),
+    "cleave_hip_add_row_bias_f32_host": (i32, [vp, i64, vp, i64, vp, i64, i32, i32]),
+    "cleave_hip_sum_rows_f32_host": (i32, [vp, i64, vp, i64, i32, i32]),
+    "cleave_hip_sum_f32_host": (f32, [vp, i64]),
+    "cleave_hip_mean_f32_host": (f32, [vp, i64]),
+    "cleave_hip_max_of_f32_host": (f32, [vp, i64]),
+    "cleave_hip_argmax_f32_host": (i64, [vp, i64]),
+    "cleave_hip_sum_u32_u64_host": (u64, [vp, i64]),
+    "cleave_hip_index_f32_host": (f32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_index_bwd_f32_host": (i32, [f32, vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_mandelbrot_u32_host": (i32, [vp, i64, i32, i32, f32, f32, f32, f32, i32]),
+    "cleave_hip_mlp_step_f32_host": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64,
+                                           vp, i32, i32, i32, f32]),
     # memref-descriptor forms: every tensor argument is a pointer to an
     # unranked descriptor {int64 rank; void* ranked descriptor}
     "_mlir_ciface_cleave_hip_matmul_f32": (i32, [vp, vp, vp]),

@@ -49,7 +49,7 @@ HIP_FLAGS = [
 ]
 SOURCES = ["runtime.hip", "gemm_f32.hip", "gemm_bf16.hip", "elementwise.hip", "reduce.hip",
            "mandelbrot.hip", "mlp.hip", "index.hip", "broadcast.hip", "memref.cpp",
-           "symbols.cpp"]
+           "host.cpp", "symbols.cpp"]
 
 
 REPORT = "-Rpass-analysis=kernel-resource-usage"

@@ -173,6 +173,9 @@ int32_t cleave_hip_add_row_bias_f32(const float* a, int64_t alen, const float* b
     if (alen == 0) return CLEAVE_HIP_OK;
     CH_REQUIRE(a && bias && out, "%s: null buffer", fn);
     CH_INIT_OR_RETURN();
+    CH_DEVICE(fn, a, alen * 4);
+    CH_DEVICE(fn, bias, blen * 4);
+    CH_DEVICE(fn, out, outlen * 4);
     if (cols % 4 == 0 && aligned16(a) && aligned16(bias) && aligned16(out)) {
         const Tiling t = tiling_bias(rows, cols);
         add_row_bias_kernel<<<(unsigned)(t.nseg * t.groups), kThreads, 0, ch::stream()>>>(
@@ -194,6 +197,8 @@ int32_t cleave_hip_sum_rows_f32(const float* g, int64_t glen, float* out, int64_
     if (cols == 0) return CLEAVE_HIP_OK;
     CH_REQUIRE(g && out, "%s: null buffer", fn);
     CH_INIT_OR_RETURN();
+    CH_DEVICE(fn, g, glen * 4);
+    CH_DEVICE(fn, out, outlen * 4);
     if (cols % 4 == 0 && aligned16(g)) {
         const Tiling t = tiling_sum(rows, cols);
         float* part = (float*)ch::scratch(5, sizeof(float) * (size_t)(t.groups * cols));

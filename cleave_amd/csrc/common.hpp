@@ -34,6 +34,13 @@ void* scratch(int slot, size_t bytes);
 // Number of compute units (for grid sizing of persistent/strided kernels).
 int num_cus();
 
+// Tensor operands of the device entry points must be device memory: a host
+// address handed to a kernel faults the GPU.  Fails with CLEAVE_HIP_ERR_ARG
+// when `p` is not device (or managed) memory of this process, or when its
+// allocation ends fewer than `bytes` bytes after `p`.  The `_host` entry
+// points take host arrays instead.
+int32_t require_device(const char* fn, const char* what, const void* p, uint64_t bytes);
+
 }  // namespace ch
 
 #define CH_INIT_OR_RETURN()                       \
@@ -52,6 +59,13 @@ int num_cus();
     do {                                                                \
         int32_t _st = ch::check_hip(hipGetLastError(), name);           \
         if (_st != CLEAVE_HIP_OK) return _st;                           \
+    } while (0)
+
+// Device-operand check: `CH_DEVICE(fn, ptr, bytes)` returns on failure.
+#define CH_DEVICE(fn, p, bytes)                                                       \
+    do {                                                                              \
+        int32_t _st = ch::require_device((fn), #p, (const void*)(p), (uint64_t)(bytes)); \
+        if (_st != CLEAVE_HIP_OK) return _st;                                         \
     } while (0)
 
 // Argument checks used by every entry point.

@@ -108,6 +108,8 @@ int32_t run1(const char* name, const float* a, int64_t alen, float* out, int64_t
     if (alen == 0) return CLEAVE_HIP_OK;
     CH_REQUIRE(a && out, "%s: null buffer", name);
     CH_INIT_OR_RETURN();
+    CH_DEVICE(name, a, alen * 4);
+    CH_DEVICE(name, out, outlen * 4);
     if (aligned16(a) && aligned16(out))
         map1_kernel<Op><<<grid_for(alen / 4), kThreads, 0, ch::stream()>>>(a, out, alen);
     else
@@ -125,6 +127,9 @@ int32_t run2(const char* name, const float* a, int64_t alen, const float* b, int
     if (alen == 0) return CLEAVE_HIP_OK;
     CH_REQUIRE(a && b && out, "%s: null buffer", name);
     CH_INIT_OR_RETURN();
+    CH_DEVICE(name, a, alen * 4);
+    CH_DEVICE(name, b, blen * 4);
+    CH_DEVICE(name, out, outlen * 4);
     if (aligned16(a) && aligned16(b) && aligned16(out))
         map2_kernel<Op><<<grid_for(alen / 4), kThreads, 0, ch::stream()>>>(a, b, out, alen);
     else
@@ -195,6 +200,7 @@ int32_t cleave_hip_zero_f32(float* out, int64_t outlen) {
     if (outlen == 0) return CLEAVE_HIP_OK;
     CH_REQUIRE(out != nullptr, "cleave_hip_zero_f32: null buffer");
     CH_INIT_OR_RETURN();
+    CH_DEVICE("cleave_hip_zero_f32", out, outlen * 4);
     // A fill kernel rather than hipMemsetAsync, so the call can be captured in a graph.
     zero_kernel<<<grid_for(outlen / 4 + 1), kThreads, 0, ch::stream()>>>(out, outlen);
     CH_LAUNCHED("zero_kernel");
@@ -209,6 +215,12 @@ int32_t cleave_hip_div_bwd_f32(const float* a, int64_t alen, const float* b, int
     if (alen == 0) return CLEAVE_HIP_OK;
     CH_REQUIRE(a && b && g && da && db, "cleave_hip_div_bwd_f32: null buffer");
     CH_INIT_OR_RETURN();
+    const char* fn = "cleave_hip_div_bwd_f32";
+    CH_DEVICE(fn, a, alen * 4);
+    CH_DEVICE(fn, b, blen * 4);
+    CH_DEVICE(fn, g, glen * 4);
+    CH_DEVICE(fn, da, dalen * 4);
+    CH_DEVICE(fn, db, dblen * 4);
     div_bwd_kernel<<<grid_for(alen / 4 + 1), kThreads, 0, ch::stream()>>>(a, b, g, da, db, alen);
     CH_LAUNCHED("div_bwd_kernel");
     return CLEAVE_HIP_OK;
@@ -220,6 +232,8 @@ int32_t cleave_hip_sgd_update_f32(float* w, int64_t wlen, const float* g, int64_
     if (wlen == 0) return CLEAVE_HIP_OK;
     CH_REQUIRE(w && g, "cleave_hip_sgd_update_f32: null buffer");
     CH_INIT_OR_RETURN();
+    CH_DEVICE("cleave_hip_sgd_update_f32", w, wlen * 4);
+    CH_DEVICE("cleave_hip_sgd_update_f32", g, glen * 4);
     sgd_kernel<<<grid_for(wlen / 4 + 1), kThreads, 0, ch::stream()>>>(w, g, lr, wlen);
     CH_LAUNCHED("sgd_kernel");
     return CLEAVE_HIP_OK;

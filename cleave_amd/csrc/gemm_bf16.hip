@@ -194,7 +194,8 @@ int32_t launch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int
     dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)batch);
     // 4-byte (transposed) or 16-byte (k-contiguous) global reads need the
     // matching alignment of every row start.
-    const bool fast = (M % BM == 0) && (N % BN == 0) && (K % BK == 0);
+    const bool fast = (M % BM == 0) && (N % BN == 0) && (K % BK == 0) &&
+                      ((uintptr_t)a & 15) == 0 && ((uintptr_t)b & 15) == 0;
     if (fast)
         gemm_bf16_kernel<TA, TB, false><<<grid, NT, 0, ch::stream()>>>(a, b, c, M, N, K, sA, sB, sC,
                                                                        tiles_m, tiles_n);
@@ -318,20 +319,29 @@ int32_t cleave_hip_matmul_bf16(const uint16_t* a, int64_t alen, const uint16_t* 
     CH_REQUIRE(clen == (int64_t)M * N, "cleave_hip_matmul_bf16: clen %lld != M*N %lld", (long long)clen, (long long)M * N);
     CH_REQUIRE(a && b && c, "cleave_hip_matmul_bf16: null buffer");
     CH_INIT_OR_RETURN();
+    CH_DEVICE("cleave_hip_matmul_bf16", a, alen * 2);
+    CH_DEVICE("cleave_hip_matmul_bf16", b, blen * 2);
+    CH_DEVICE("cleave_hip_matmul_bf16", c, clen * 4);
     return dispatch(a, b, c, M, N, K, 1, trans_a, trans_b);
 }
 
 int32_t cleave_hip_matmul_batched_bf16(const uint16_t* a, int64_t alen, const uint16_t* b,
                                        int64_t blen, float* c, int64_t clen, int32_t batch,
-                                       int32_t M, int32_t N, int32_t K) {
+                                       int32_t M, int32_t N, int32_t K, int32_t trans_a,
+                                       int32_t trans_b) {
     CH_REQUIRE(batch > 0 && batch <= 65535 && M > 0 && N > 0 && K > 0,
                "cleave_hip_matmul_batched_bf16: bad dims (batch=%d M=%d N=%d K=%d)", batch, M, N, K);
+    CH_REQUIRE((trans_a == 0 || trans_a == 1) && (trans_b == 0 || trans_b == 1),
+               "cleave_hip_matmul_batched_bf16: trans flags must be 0 or 1");
     CH_REQUIRE(alen == (int64_t)batch * M * K && blen == (int64_t)batch * K * N &&
                    clen == (int64_t)batch * M * N,
                "cleave_hip_matmul_batched_bf16: lengths do not match batch*M*K, batch*K*N, batch*M*N");
     CH_REQUIRE(a && b && c, "cleave_hip_matmul_batched_bf16: null buffer");
     CH_INIT_OR_RETURN();
-    return dispatch(a, b, c, M, N, K, batch, 0, 0);
+    CH_DEVICE("cleave_hip_matmul_batched_bf16", a, alen * 2);
+    CH_DEVICE("cleave_hip_matmul_batched_bf16", b, blen * 2);
+    CH_DEVICE("cleave_hip_matmul_batched_bf16", c, clen * 4);
+    return dispatch(a, b, c, M, N, K, batch, trans_a, trans_b);
 }
 
 }  // extern "C"

@@ -211,7 +211,8 @@ int32_t launch_general(const float* a, const float* b, float* c, int M, int N, i
                int64_t ldb, int64_t ldc, int batch, int64_t sA, int64_t sB, int64_t sC) {
     // The 16-byte loads of the fast path also need every row start aligned.
     const bool fast = (M % BM == 0) && (N % BN == 0) && (K % BK == 0) && (lda % 4 == 0) &&
-                      (ldb % 4 == 0) && (sA % 4 == 0) && (sB % 4 == 0);
+                      (ldb % 4 == 0) && (sA % 4 == 0) && (sB % 4 == 0) &&
+                      ((uintptr_t)a & 15) == 0 && ((uintptr_t)b & 15) == 0;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)batch);
     if (fast)
@@ -320,6 +321,9 @@ int32_t cleave_hip_matmul_f32(const float* a, int64_t alen, const float* b, int6
     CH_REQUIRE(clen == (int64_t)M * N, "cleave_hip_matmul_f32: clen %lld != M*N %lld", (long long)clen, (long long)M * N);
     CH_REQUIRE(a && b && c, "cleave_hip_matmul_f32: null buffer");
     CH_INIT_OR_RETURN();
+    CH_DEVICE("cleave_hip_matmul_f32", a, alen * 4);
+    CH_DEVICE("cleave_hip_matmul_f32", b, blen * 4);
+    CH_DEVICE("cleave_hip_matmul_f32", c, clen * 4);
     return dispatch(a, b, c, M, N, K, 1, trans_a, trans_b, 1);
 }
 
@@ -336,6 +340,9 @@ int32_t cleave_hip_matmul_batched_f32(const float* a, int64_t alen, const float*
                "cleave_hip_matmul_batched_f32: lengths do not match batch*M*K, batch*K*N, batch*M*N");
     CH_REQUIRE(a && b && c, "cleave_hip_matmul_batched_f32: null buffer");
     CH_INIT_OR_RETURN();
+    CH_DEVICE("cleave_hip_matmul_batched_f32", a, alen * 4);
+    CH_DEVICE("cleave_hip_matmul_batched_f32", b, blen * 4);
+    CH_DEVICE("cleave_hip_matmul_batched_f32", c, clen * 4);
     return dispatch(a, b, c, M, N, K, batch, trans_a, trans_b, 1);
 }
 

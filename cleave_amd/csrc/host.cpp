@@ -1,0 +1,351 @@
+// host.cpp -- host-array forms (`<entry>_host`) of the compute entry points.
+//
+// cleave's extern lowering passes an array argument as the aligned pointer of
+// a host memref plus its element count (cleave/src/mlir_lower.rs:1720-1751),
+// and cleave-rt reads that memory on the host (sum_bytes,
+// cleave-rt/src/lib.rs:86-90).  These entry points accept exactly that: every
+// tensor operand is a borrowed, possibly pageable host array, valid only for
+// the call.  Each one
+//   1. copies its input arrays into a staging arena in HBM (hipMemcpyAsync on
+//      the library stream; the arena is library scratch, grown on demand and
+//      kept),
+//   2. runs the device entry point on the staged copies (same kernels, same
+//      argument checks, same error contract),
+//   3. copies its output arrays back and waits for the stream,
+// so on return every output array holds its result and every array may be
+// reused.  A failed call leaves the output arrays unwritten.
+#include <cmath>
+
+#include "common.hpp"
+
+namespace {
+
+// Scratch slot of the staging arena (slots 0-5 belong to the reductions, the
+// MLP step and the column sums).
+constexpr int kArenaSlot = 6;
+constexpr int kMaxArgs = 8;
+
+// The host arrays of one call, staged through the arena.
+class Staged {
+  public:
+    explicit Staged(const char* fn) : fn_(fn) {}
+
+    // Declares host array i: `len` elements of `esz` bytes, copied to the
+    // device before the call when `in`, and back after it when `out`.
+    int add(const void* host, int64_t len, int esz, bool in, bool out) {
+        const int i = n_++;
+        if (i < kMaxArgs) args_[i] = Arg{host, len, esz, in, out, 0};
+        return i;
+    }
+    int in(const void* host, int64_t len, int esz) { return add(host, len, esz, true, false); }
+    int out(void* host, int64_t len, int esz) { return add(host, len, esz, false, true); }
+    int inout(void* host, int64_t len, int esz) { return add(host, len, esz, true, true); }
+
+    // Sizes the arena and queues the copies in.  Returns a status.
+    int32_t stage() {
+        if (n_ > kMaxArgs) return ch::fail(CLEAVE_HIP_ERR_ARG, "%s: too many operands", fn_);
+        size_t total = 0;
+        for (int i = 0; i < n_; ++i) {
+            const Arg& a = args_[i];
+            CH_REQUIRE(a.len >= 0, "%s: operand %d has negative length %lld", fn_, i, (long long)a.len);
+            CH_REQUIRE(a.len == 0 || a.host != nullptr, "%s: operand %d is a null array of %lld elements",
+                       fn_, i, (long long)a.len);
+            CH_REQUIRE((uint64_t)a.len <= (UINT64_MAX >> 4) / (uint64_t)a.esz,
+                       "%s: operand %d length %lld is too large", fn_, i, (long long)a.len);
+            args_[i].off = total;
+            total += ((size_t)a.len * a.esz + 255) & ~(size_t)255;  // 256-byte aligned sub-buffers
+        }
+        CH_INIT_OR_RETURN();
+        base_ = (char*)ch::scratch(kArenaSlot, total ? total : 256);
+        if (!base_) return CLEAVE_HIP_ERR_OOM;
+        for (int i = 0; i < n_; ++i) {
+            const Arg& a = args_[i];
+            if (a.in && a.len > 0) {
+                const int32_t st = ch::check_hip(hipMemcpyAsync(base_ + a.off, a.host, (size_t)a.len * a.esz,
+                                                                hipMemcpyHostToDevice, ch::stream()),
+                                                 "hipMemcpyAsync (host array to staging)");
+                if (st != CLEAVE_HIP_OK) return drain(st);
+            }
+        }
+        staged_ = true;
+        return CLEAVE_HIP_OK;
+    }
+
+    // Device address of staged array i (valid after stage()).
+    template <class T>
+    T* dev(int i) const {
+        return reinterpret_cast<T*>(base_ + args_[i].off);
+    }
+
+    // After the device entry point returned `st`: when it succeeded, queues
+    // the copies out; always waits for the stream.  Returns the first error.
+    int32_t finish(int32_t st) {
+        if (st == CLEAVE_HIP_OK && staged_) {
+            for (int i = 0; i < n_; ++i) {
+                const Arg& a = args_[i];
+                if (a.out && a.len > 0) {
+                    st = ch::check_hip(hipMemcpyAsync(const_cast<void*>(a.host), base_ + a.off,
+                                                      (size_t)a.len * a.esz, hipMemcpyDeviceToHost, ch::stream()),
+                                       "hipMemcpyAsync (staging to host array)");
+                    if (st != CLEAVE_HIP_OK) break;
+                }
+            }
+        }
+        return drain(st);
+    }
+
+  private:
+    struct Arg {
+        const void* host;
+        int64_t len;
+        int esz;
+        bool in, out;
+        size_t off;
+    };
+
+    // Waits for every queued copy, so no host array is touched after return.
+    int32_t drain(int32_t st) {
+        if (ch::stream() == nullptr) return st;
+        const hipError_t e = hipStreamSynchronize(ch::stream());
+        if (st != CLEAVE_HIP_OK) return st;
+        return ch::check_hip(e, "hipStreamSynchronize");
+    }
+
+    const char* fn_;
+    Arg args_[kMaxArgs] = {};
+    int n_ = 0;
+    char* base_ = nullptr;
+    bool staged_ = false;
+};
+
+using Map1 = int32_t (*)(const float*, int64_t, float*, int64_t);
+using Map2 = int32_t (*)(const float*, int64_t, const float*, int64_t, float*, int64_t);
+
+int32_t map1_host(const char* fn, Map1 f, const float* a, int64_t alen, float* out, int64_t outlen) {
+    Staged s(fn);
+    const int ia = s.in(a, alen, 4), io = s.out(out, outlen, 4);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(f(s.dev<float>(ia), alen, s.dev<float>(io), outlen));
+}
+
+int32_t map2_host(const char* fn, Map2 f, const float* a, int64_t alen, const float* b, int64_t blen, float* out,
+                  int64_t outlen) {
+    Staged s(fn);
+    const int ia = s.in(a, alen, 4), ib = s.in(b, blen, 4), io = s.out(out, outlen, 4);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(f(s.dev<float>(ia), alen, s.dev<float>(ib), blen, s.dev<float>(io), outlen));
+}
+
+// Scalar-returning reductions: stage x, then call the device form (which
+// clears the error state, synchronises and returns the value).
+template <class R, class T>
+R reduce_host(const char* fn, R (*f)(const T*, int64_t), const T* x, int64_t len, R on_error) {
+    ch::clear_error();
+    Staged s(fn);
+    const int ix = s.in(x, len, (int)sizeof(T));
+    if (s.stage() != CLEAVE_HIP_OK) return on_error;
+    const R r = f(s.dev<T>(ix), len);
+    const int32_t err = cleave_hip_last_error();
+    if (s.finish(CLEAVE_HIP_OK) != CLEAVE_HIP_OK || err != CLEAVE_HIP_OK) return on_error;
+    return r;
+}
+
+}  // namespace
+
+extern "C" {
+
+// ---- MatMul -----------------------------------------------------------------
+
+int32_t cleave_hip_matmul_f32_host(const float* a, int64_t alen, const float* b, int64_t blen, float* c,
+                                   int64_t clen, int32_t M, int32_t N, int32_t K, int32_t trans_a,
+                                   int32_t trans_b) {
+    Staged s("cleave_hip_matmul_f32_host");
+    const int ia = s.in(a, alen, 4), ib = s.in(b, blen, 4), ic = s.out(c, clen, 4);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_matmul_f32(s.dev<float>(ia), alen, s.dev<float>(ib), blen, s.dev<float>(ic), clen,
+                                          M, N, K, trans_a, trans_b));
+}
+
+int32_t cleave_hip_matmul_batched_f32_host(const float* a, int64_t alen, const float* b, int64_t blen, float* c,
+                                           int64_t clen, int32_t batch, int32_t M, int32_t N, int32_t K,
+                                           int32_t trans_a, int32_t trans_b) {
+    Staged s("cleave_hip_matmul_batched_f32_host");
+    const int ia = s.in(a, alen, 4), ib = s.in(b, blen, 4), ic = s.out(c, clen, 4);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_matmul_batched_f32(s.dev<float>(ia), alen, s.dev<float>(ib), blen,
+                                                  s.dev<float>(ic), clen, batch, M, N, K, trans_a, trans_b));
+}
+
+int32_t cleave_hip_matmul_bf16_host(const uint16_t* a, int64_t alen, const uint16_t* b, int64_t blen, float* c,
+                                    int64_t clen, int32_t M, int32_t N, int32_t K, int32_t trans_a,
+                                    int32_t trans_b) {
+    Staged s("cleave_hip_matmul_bf16_host");
+    const int ia = s.in(a, alen, 2), ib = s.in(b, blen, 2), ic = s.out(c, clen, 4);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_matmul_bf16(s.dev<uint16_t>(ia), alen, s.dev<uint16_t>(ib), blen,
+                                           s.dev<float>(ic), clen, M, N, K, trans_a, trans_b));
+}
+
+int32_t cleave_hip_matmul_batched_bf16_host(const uint16_t* a, int64_t alen, const uint16_t* b, int64_t blen,
+                                            float* c, int64_t clen, int32_t batch, int32_t M, int32_t N,
+                                            int32_t K, int32_t trans_a, int32_t trans_b) {
+    Staged s("cleave_hip_matmul_batched_bf16_host");
+    const int ia = s.in(a, alen, 2), ib = s.in(b, blen, 2), ic = s.out(c, clen, 4);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_matmul_batched_bf16(s.dev<uint16_t>(ia), alen, s.dev<uint16_t>(ib), blen,
+                                                   s.dev<float>(ic), clen, batch, M, N, K, trans_a, trans_b));
+}
+
+// ---- Ring<Tensor>, Activation<Tensor>, backward maps ------------------------------
+
+#define CH_MAP2_HOST(name)                                                                                   \
+    int32_t name##_host(const float* a, int64_t alen, const float* b, int64_t blen, float* out,          \
+                        int64_t outlen) {                                                                 \
+        return map2_host(#name "_host", &name, a, alen, b, blen, out, outlen);                            \
+    }
+#define CH_MAP1_HOST(name)                                                                                   \
+    int32_t name##_host(const float* a, int64_t alen, float* out, int64_t outlen) {                       \
+        return map1_host(#name "_host", &name, a, alen, out, outlen);                                     \
+    }
+
+CH_MAP2_HOST(cleave_hip_add_f32)
+CH_MAP2_HOST(cleave_hip_sub_f32)
+CH_MAP2_HOST(cleave_hip_mul_f32)
+CH_MAP2_HOST(cleave_hip_div_f32)
+CH_MAP1_HOST(cleave_hip_neg_f32)
+CH_MAP1_HOST(cleave_hip_relu_f32)
+CH_MAP1_HOST(cleave_hip_sigmoid_f32)
+CH_MAP1_HOST(cleave_hip_tanh_f32)
+CH_MAP2_HOST(cleave_hip_sigmoid_bwd_f32)
+CH_MAP2_HOST(cleave_hip_tanh_bwd_f32)
+CH_MAP2_HOST(cleave_hip_relu_bwd_f32)
+
+int32_t cleave_hip_zero_f32_host(float* out, int64_t outlen) {
+    Staged s("cleave_hip_zero_f32_host");
+    const int io = s.out(out, outlen, 4);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_zero_f32(s.dev<float>(io), outlen));
+}
+
+int32_t cleave_hip_div_bwd_f32_host(const float* a, int64_t alen, const float* b, int64_t blen, const float* g,
+                                    int64_t glen, float* da, int64_t dalen, float* db, int64_t dblen) {
+    Staged s("cleave_hip_div_bwd_f32_host");
+    const int ia = s.in(a, alen, 4), ib = s.in(b, blen, 4), ig = s.in(g, glen, 4);
+    const int ida = s.out(da, dalen, 4), idb = s.out(db, dblen, 4);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_div_bwd_f32(s.dev<float>(ia), alen, s.dev<float>(ib), blen, s.dev<float>(ig), glen,
+                                           s.dev<float>(ida), dalen, s.dev<float>(idb), dblen));
+}
+
+int32_t cleave_hip_sgd_update_f32_host(float* w, int64_t wlen, const float* g, int64_t glen, float lr) {
+    Staged s("cleave_hip_sgd_update_f32_host");
+    const int iw = s.inout(w, wlen, 4), ig = s.in(g, glen, 4);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_sgd_update_f32(s.dev<float>(iw), wlen, s.dev<float>(ig), glen, lr));
+}
+
+int32_t cleave_hip_add_row_bias_f32_host(const float* a, int64_t alen, const float* bias, int64_t blen,
+                                         float* out, int64_t outlen, int32_t rows, int32_t cols) {
+    Staged s("cleave_hip_add_row_bias_f32_host");
+    const int ia = s.in(a, alen, 4), ib = s.in(bias, blen, 4), io = s.out(out, outlen, 4);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_add_row_bias_f32(s.dev<float>(ia), alen, s.dev<float>(ib), blen, s.dev<float>(io),
+                                                outlen, rows, cols));
+}
+
+int32_t cleave_hip_sum_rows_f32_host(const float* g, int64_t glen, float* out, int64_t outlen, int32_t rows,
+                                     int32_t cols) {
+    Staged s("cleave_hip_sum_rows_f32_host");
+    const int ig = s.in(g, glen, 4), io = s.out(out, outlen, 4);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_sum_rows_f32(s.dev<float>(ig), glen, s.dev<float>(io), outlen, rows, cols));
+}
+
+// ---- Sum / Mean / Max ----------------------------------------------------------
+
+float cleave_hip_sum_f32_host(const float* x, int64_t len) {
+    return reduce_host<float, float>("cleave_hip_sum_f32_host", &cleave_hip_sum_f32, x, len, NAN);
+}
+
+float cleave_hip_mean_f32_host(const float* x, int64_t len) {
+    return reduce_host<float, float>("cleave_hip_mean_f32_host", &cleave_hip_mean_f32, x, len, NAN);
+}
+
+float cleave_hip_max_of_f32_host(const float* x, int64_t len) {
+    return reduce_host<float, float>("cleave_hip_max_of_f32_host", &cleave_hip_max_of_f32, x, len, NAN);
+}
+
+int64_t cleave_hip_argmax_f32_host(const float* x, int64_t len) {
+    return reduce_host<int64_t, float>("cleave_hip_argmax_f32_host", &cleave_hip_argmax_f32, x, len, -1);
+}
+
+uint64_t cleave_hip_sum_u32_u64_host(const uint32_t* x, int64_t len) {
+    return reduce_host<uint64_t, uint32_t>("cleave_hip_sum_u32_u64_host", &cleave_hip_sum_u32_u64, x, len, 0);
+}
+
+// ---- Index<Tensor> ---------------------------------------------------------------
+
+float cleave_hip_index_f32_host(const float* t, int64_t len, const int32_t* dims, int64_t ndims,
+                                const int32_t* idx, int64_t nidx) {
+    ch::clear_error();
+    Staged s("cleave_hip_index_f32_host");
+    const int it = s.in(t, len, 4);
+    if (s.stage() != CLEAVE_HIP_OK) return NAN;
+    const float v = cleave_hip_index_f32(s.dev<float>(it), len, dims, ndims, idx, nidx);
+    const int32_t err = cleave_hip_last_error();
+    if (s.finish(CLEAVE_HIP_OK) != CLEAVE_HIP_OK || err != CLEAVE_HIP_OK) return NAN;
+    return v;
+}
+
+int32_t cleave_hip_index_bwd_f32_host(float g, float* dt, int64_t len, const int32_t* dims, int64_t ndims,
+                                      const int32_t* idx, int64_t nidx) {
+    Staged s("cleave_hip_index_bwd_f32_host");
+    const int it = s.inout(dt, len, 4);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_index_bwd_f32(g, s.dev<float>(it), len, dims, ndims, idx, nidx));
+}
+
+// ---- escape_count map ---------------------------------------------------------------
+
+int32_t cleave_hip_mandelbrot_u32_host(uint32_t* out, int64_t outlen, int32_t width, int32_t height, float x0,
+                                       float y0, float dx, float dy, int32_t max_iter) {
+    Staged s("cleave_hip_mandelbrot_u32_host");
+    const int io = s.out(out, outlen, 4);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_mandelbrot_u32(s.dev<uint32_t>(io), outlen, width, height, x0, y0, dx, dy, max_iter));
+}
+
+// ---- MLP step -----------------------------------------------------------------------
+
+int32_t cleave_hip_mlp_step_f32_host(const float* x, int64_t xlen, const float* y, int64_t ylen, float* w1,
+                                     int64_t w1len, float* w2, int64_t w2len, float* dw1, int64_t dw1len,
+                                     float* dw2, int64_t dw2len, float* loss, int32_t B, int32_t D, int32_t Hd,
+                                     float lr) {
+    Staged s("cleave_hip_mlp_step_f32_host");
+    const int ix = s.in(x, xlen, 4), iy = s.in(y, ylen, 4);
+    const int iw1 = s.inout(w1, w1len, 4), iw2 = s.inout(w2, w2len, 4);
+    const int idw1 = dw1 ? s.out(dw1, dw1len, 4) : -1;
+    const int idw2 = dw2 ? s.out(dw2, dw2len, 4) : -1;
+    const int il = loss ? s.out(loss, 1, 4) : -1;
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_mlp_step_f32(
+        s.dev<float>(ix), xlen, s.dev<float>(iy), ylen, s.dev<float>(iw1), w1len, s.dev<float>(iw2), w2len,
+        idw1 >= 0 ? s.dev<float>(idw1) : nullptr, dw1len, idw2 >= 0 ? s.dev<float>(idw2) : nullptr, dw2len,
+        il >= 0 ? s.dev<float>(il) : nullptr, B, D, Hd, lr));
+}
+
+}  // extern "C"

@@ -46,6 +46,8 @@ float cleave_hip_index_f32(const float* t, int64_t len, const int32_t* dims, int
         return NAN;
     }
     if (flat_offset("cleave_hip_index_f32", len, dims, ndims, idx, nidx, &off) != CLEAVE_HIP_OK) return NAN;
+    if (ch::ensure_init() != CLEAVE_HIP_OK) return NAN;
+    if (ch::require_device("cleave_hip_index_f32", "t", t, (uint64_t)len * 4) != CLEAVE_HIP_OK) return NAN;
     float v = NAN;
     if (cleave_hip_download(&v, t + off, sizeof(float)) != (int64_t)sizeof(float)) return NAN;
     return v;
@@ -58,6 +60,7 @@ int32_t cleave_hip_index_bwd_f32(float g, float* dt, int64_t len, const int32_t*
     const int32_t st = flat_offset("cleave_hip_index_bwd_f32", len, dims, ndims, idx, nidx, &off);
     if (st != CLEAVE_HIP_OK) return st;
     CH_INIT_OR_RETURN();
+    CH_DEVICE("cleave_hip_index_bwd_f32", dt, len * 4);
     scatter_add_kernel<<<1, 1, 0, ch::stream()>>>(dt, off, g);
     CH_LAUNCHED("scatter_add_kernel");
     return CLEAVE_HIP_OK;

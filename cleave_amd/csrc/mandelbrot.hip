@@ -120,6 +120,7 @@ extern "C" int32_t cleave_hip_mandelbrot_u32(uint32_t* out, int64_t outlen, int3
                (long long)outlen, (long long)width * height);
     CH_REQUIRE(out != nullptr, "cleave_hip_mandelbrot_u32: null buffer");
     CH_INIT_OR_RETURN();
+    CH_DEVICE("cleave_hip_mandelbrot_u32", out, outlen * 4);
     dim3 grid((unsigned)((width + 15) / 16), (unsigned)((height + 15) / 16));
     CH_REQUIRE(grid.y <= 65535u, "cleave_hip_mandelbrot_u32: height %d too large", height);
     mandelbrot_kernel<<<grid, 256, 0, ch::stream()>>>(out, width, height, x0, y0, dx, dy, max_iter);

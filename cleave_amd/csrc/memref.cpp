@@ -140,10 +140,10 @@ int32_t matmul_mr(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr c, const char*
     int32_t batch;
     CH_TRY(narrow(A.sizes[0], fn, "batch", &batch));
     if (BF16) {
-        CH_REQUIRE(ta == 0 && tb == 0, "%s: the batched bf16 product takes row-major operands only", fn);
         return cleave_hip_matmul_batched_bf16(reinterpret_cast<const uint16_t*>(A.data), A.count,
                                               reinterpret_cast<const uint16_t*>(B.data), B.count,
-                                              reinterpret_cast<float*>(C.data), C.count, batch, m32, n32, k32);
+                                              reinterpret_cast<float*>(C.data), C.count, batch, m32, n32, k32,
+                                              ta, tb);
     }
     return cleave_hip_matmul_batched_f32(reinterpret_cast<const float*>(A.data), A.count,
                                          reinterpret_cast<const float*>(B.data), B.count,

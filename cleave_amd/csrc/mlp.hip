@@ -303,6 +303,14 @@ extern "C" int32_t cleave_hip_mlp_step_f32(const float* x, int64_t xlen, const f
     CH_REQUIRE(x && y && w1 && w2, "cleave_hip_mlp_step_f32: null buffer");
     CH_REQUIRE(((uintptr_t)w2 & 15) == 0, "cleave_hip_mlp_step_f32: w2 must be 16-byte aligned");
     CH_INIT_OR_RETURN();
+    const char* fn = "cleave_hip_mlp_step_f32";
+    CH_DEVICE(fn, x, xlen * 4);
+    CH_DEVICE(fn, y, ylen * 4);
+    CH_DEVICE(fn, w1, w1len * 4);
+    CH_DEVICE(fn, w2, w2len * 4);
+    if (dw1) CH_DEVICE(fn, dw1, dw1len * 4);
+    if (dw2) CH_DEVICE(fn, dw2, dw2len * 4);
+    if (loss_dev) CH_DEVICE(fn, loss_dev, 4);
 
     hipStream_t st = ch::stream();
     if (fused_fits(x, w1, B, D, Hd)) return fused_step(x, y, w1, w2, dw1, dw2, loss_dev, B, D, Hd, lr, st);

@@ -251,6 +251,8 @@ int32_t cleave_hip_reduce_sum_f32(const float* x, int64_t len, float* out_dev) {
     CH_REQUIRE(len >= 1, "cleave_hip_reduce_sum_f32: length must be >= 1 (sum reads v[0])");
     CH_REQUIRE(x && out_dev, "cleave_hip_reduce_sum_f32: null buffer");
     CH_INIT_OR_RETURN();
+    CH_DEVICE("cleave_hip_reduce_sum_f32", x, len * 4);
+    CH_DEVICE("cleave_hip_reduce_sum_f32", out_dev, 4);
     const int aligned = aligned16(x);
     unsigned blocks = stage1_blocks(aligned ? len / 4 + 1 : len / kUnroll + 1);
     float* part = (float*)ch::scratch(0, sizeof(float) * blocks);
@@ -266,6 +268,9 @@ int32_t cleave_hip_reduce_max_f32(const float* x, int64_t len, float* max_dev, i
     CH_REQUIRE(len >= 1, "cleave_hip_reduce_max_f32: length must be >= 1 (max_of reads v[0])");
     CH_REQUIRE(x && (max_dev || argmax_dev), "cleave_hip_reduce_max_f32: null buffer");
     CH_INIT_OR_RETURN();
+    CH_DEVICE("cleave_hip_reduce_max_f32", x, len * 4);
+    if (max_dev) CH_DEVICE("cleave_hip_reduce_max_f32", max_dev, 4);
+    if (argmax_dev) CH_DEVICE("cleave_hip_reduce_max_f32", argmax_dev, 8);
     const int aligned = aligned16(x);
     unsigned blocks = stage1_blocks(aligned ? len / 4 + 1 : len / kUnroll + 1);
     char* base = (char*)ch::scratch(1, (sizeof(float) + sizeof(int64_t)) * blocks + 64);
@@ -283,6 +288,8 @@ int32_t cleave_hip_reduce_sum_u32_u64(const uint32_t* x, int64_t len, uint64_t* 
     CH_REQUIRE(len >= 0, "cleave_hip_reduce_sum_u32_u64: negative length");
     CH_REQUIRE(x && out_dev, "cleave_hip_reduce_sum_u32_u64: null buffer");
     CH_INIT_OR_RETURN();
+    CH_DEVICE("cleave_hip_reduce_sum_u32_u64", x, len * 4);
+    CH_DEVICE("cleave_hip_reduce_sum_u32_u64", out_dev, 8);
     const int aligned = aligned16(x);
     unsigned blocks = stage1_blocks(aligned ? len / 4 + 1 : len / kUnroll + 1);
     uint64_t* part = (uint64_t*)ch::scratch(2, sizeof(uint64_t) * blocks);

@@ -97,6 +97,36 @@ void* scratch(int slot, size_t bytes) {
     return p;
 }
 
+int32_t require_device(const char* fn, const char* what, const void* p, uint64_t bytes) {
+    hipPointerAttribute_t at{};
+    if (hipPointerGetAttributes(&at, p) != hipSuccess) {
+        // A pointer the runtime does not know at all.
+        (void)hipGetLastError();
+        return fail(CLEAVE_HIP_ERR_ARG,
+                    "%s: %s (%p) is not device memory; pass a buffer from cleave_hip_buf_alloc "
+                    "(the _host entry points take host arrays)", fn, what, p);
+    }
+    // Unregistered (type 0, what ROCm 7 reports for pageable memory) or pinned
+    // host memory: a kernel must not be handed either.
+    if (at.type != hipMemoryTypeDevice && at.type != hipMemoryTypeManaged)
+        return fail(CLEAVE_HIP_ERR_ARG,
+                    "%s: %s (%p) is not device memory (memory type %d); pass a buffer from "
+                    "cleave_hip_buf_alloc (the _host entry points take host arrays)", fn, what, p, (int)at.type);
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p) == hipSuccess) {
+        const uintptr_t lo = (uintptr_t)base, q = (uintptr_t)p;
+        if (q < lo || bytes > (uint64_t)(lo + size - q))
+            return fail(CLEAVE_HIP_ERR_ARG,
+                        "%s: %s needs %llu bytes from %p, but its allocation holds %llu bytes from there",
+                        fn, what, (unsigned long long)bytes, p,
+                        (unsigned long long)(q >= lo && q - lo <= size ? lo + size - q : 0));
+    } else {
+        (void)hipGetLastError();
+    }
+    return CLEAVE_HIP_OK;
+}
+
 }  // namespace ch
 
 // ---------------------------------------------------------------------------
@@ -209,6 +239,7 @@ int64_t cleave_hip_upload(void* dst_dev, const void* src_host, int64_t bytes) {
                "cleave_hip_upload: null pointer or negative size");
     CH_INIT_OR_RETURN();
     if (bytes == 0) return 0;
+    CH_DEVICE("cleave_hip_upload", dst_dev, bytes);
     CH_HIP(hipMemcpyAsync(dst_dev, src_host, (size_t)bytes, hipMemcpyHostToDevice, ch::stream()));
     CH_HIP(hipStreamSynchronize(ch::stream()));
     return bytes;
@@ -219,6 +250,7 @@ int64_t cleave_hip_download(void* dst_host, const void* src_dev, int64_t bytes) 
                "cleave_hip_download: null pointer or negative size");
     CH_INIT_OR_RETURN();
     if (bytes == 0) return 0;
+    CH_DEVICE("cleave_hip_download", src_dev, bytes);
     CH_HIP(hipMemcpyAsync(dst_host, src_dev, (size_t)bytes, hipMemcpyDeviceToHost, ch::stream()));
     CH_HIP(hipStreamSynchronize(ch::stream()));
     return bytes;
@@ -270,6 +302,7 @@ void cleave_hip_event_destroy(void* ev) {
 int32_t cleave_hip_fill_uniform_f32(float* out, int64_t len, uint64_t seed, float lo, float hi) {
     CH_REQUIRE(out && len > 0, "cleave_hip_fill_uniform_f32: null buffer or empty length");
     CH_INIT_OR_RETURN();
+    CH_DEVICE("cleave_hip_fill_uniform_f32", out, len * 4);
     fill_uniform_kernel<<<grid_for(len, 256), 256, 0, ch::stream()>>>(out, len, seed, lo, hi - lo);
     CH_LAUNCHED("fill_uniform_kernel");
     return CLEAVE_HIP_OK;
@@ -278,6 +311,7 @@ int32_t cleave_hip_fill_uniform_f32(float* out, int64_t len, uint64_t seed, floa
 int32_t cleave_hip_fill_normal_f32(float* out, int64_t len, uint64_t seed, float mean, float std) {
     CH_REQUIRE(out && len > 0, "cleave_hip_fill_normal_f32: null buffer or empty length");
     CH_INIT_OR_RETURN();
+    CH_DEVICE("cleave_hip_fill_normal_f32", out, len * 4);
     fill_normal_kernel<<<grid_for(len, 256), 256, 0, ch::stream()>>>(out, len, seed, mean, std);
     CH_LAUNCHED("fill_normal_kernel");
     return CLEAVE_HIP_OK;
@@ -286,6 +320,7 @@ int32_t cleave_hip_fill_normal_f32(float* out, int64_t len, uint64_t seed, float
 int32_t cleave_hip_fill_bernoulli_f32(float* out, int64_t len, uint64_t seed, float p) {
     CH_REQUIRE(out && len > 0, "cleave_hip_fill_bernoulli_f32: null buffer or empty length");
     CH_INIT_OR_RETURN();
+    CH_DEVICE("cleave_hip_fill_bernoulli_f32", out, len * 4);
     fill_bernoulli_kernel<<<grid_for(len, 256), 256, 0, ch::stream()>>>(out, len, seed, p);
     CH_LAUNCHED("fill_bernoulli_kernel");
     return CLEAVE_HIP_OK;
@@ -296,6 +331,8 @@ int32_t cleave_hip_cast_f32_bf16(const float* in, int64_t inlen, uint16_t* out, 
     CH_REQUIRE(inlen == outlen, "cleave_hip_cast_f32_bf16: inlen %lld != outlen %lld",
                (long long)inlen, (long long)outlen);
     CH_INIT_OR_RETURN();
+    CH_DEVICE("cleave_hip_cast_f32_bf16", in, inlen * 4);
+    CH_DEVICE("cleave_hip_cast_f32_bf16", out, outlen * 2);
     cast_f32_bf16_kernel<<<grid_for(inlen, 256), 256, 0, ch::stream()>>>(in, out, inlen);
     CH_LAUNCHED("cast_f32_bf16_kernel");
     return CLEAVE_HIP_OK;

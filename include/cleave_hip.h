@@ -25,9 +25,16 @@
  * (cleave/src/main.rs:607 runs JIT code on the calling thread).  Calls that
  * return host-visible data (downloads, scalar-returning reductions)
  * synchronise the stream before returning; calls that only write device
- * buffers are queued on the stream and return immediately.  Pointers passed
- * as tensor operands are device pointers from cleave_hip_buf_alloc; host
- * pointers appear only in upload/download.
+ * buffers are queued on the stream and return immediately.
+ *
+ * Two pointer kinds, two sets of entry points:
+ *   - the device entry points (cleave_hip_matmul_f32, ...) take device
+ *     buffers (cleave_hip_buf_alloc, or any hipMalloc'd memory) and check on
+ *     the host that every tensor operand is device memory whose allocation
+ *     covers its length; anything else is CLEAVE_HIP_ERR_ARG, never a launch;
+ *   - the host entry points (cleave_hip_matmul_f32_host, ...; end of this
+ *     file) take host arrays, as cleave's extern lowering passes them, stage
+ *     them through library memory in HBM and synchronise before returning.
  */
 #ifndef CLEAVE_HIP_H
 #define CLEAVE_HIP_H
@@ -131,9 +138,13 @@ CLEAVE_HIP_API int32_t cleave_hip_matmul_batched_f32(const float* a, int64_t ale
 CLEAVE_HIP_API int32_t cleave_hip_matmul_bf16(const uint16_t* a, int64_t alen, const uint16_t* b,
                                int64_t blen, float* c, int64_t clen, int32_t M, int32_t N,
                                int32_t K, int32_t trans_a, int32_t trans_b);
+/* batch independent bf16 matmuls, operands packed back to back, with the
+ * same trans flags as the single product (each batch entry stored K x M for
+ * trans_a, N x K for trans_b): the batched halves of the product rule. */
 CLEAVE_HIP_API int32_t cleave_hip_matmul_batched_bf16(const uint16_t* a, int64_t alen, const uint16_t* b,
                                        int64_t blen, float* c, int64_t clen, int32_t batch,
-                                       int32_t M, int32_t N, int32_t K);
+                                       int32_t M, int32_t N, int32_t K, int32_t trans_a,
+                                       int32_t trans_b);
 
 /* ---------------------------------------------------------------------- */
 /* Ring<Tensor> elementwise (stdlib/linalg/tensor.cleave:66-80)             */
@@ -256,6 +267,98 @@ CLEAVE_HIP_API int32_t cleave_hip_mlp_step_f32(const float* x, int64_t xlen, con
                                 float* w1, int64_t w1len, float* w2, int64_t w2len,
                                 float* dw1, int64_t dw1len, float* dw2, int64_t dw2len,
                                 float* loss_dev, int32_t B, int32_t D, int32_t Hd, float lr);
+
+/* ---------------------------------------------------------------------- */
+/* Host-array forms                                                         */
+/* ---------------------------------------------------------------------- */
+/* cleave's extern lowering passes an [T; N] argument as the aligned pointer
+ * of a HOST memref and its element count (cleave/src/mlir_lower.rs:1720-1751),
+ * and cleave-rt's natives read that memory on the host (sum_bytes,
+ * cleave-rt/src/lib.rs:86-90).  Each `_host` entry point below has the
+ * signature and argument meaning of the device entry point of the same name
+ * without the suffix, but every tensor operand is a borrowed host array
+ * (pageable or pinned, valid only during the call).  The call copies the
+ * inputs into library staging memory in HBM, runs the same kernels, copies
+ * the outputs back and synchronises the library stream before it returns;
+ * on error no output array is written.  In-out arrays (w of the SGD update,
+ * w1/w2 of the MLP step, dt of index_bwd) are copied both ways.
+ * Binding these is the drop-in for an `extern(...)` declaration. */
+
+/* MatMul (stdlib/linalg/matrix.cleave:22-61, product rule :24). */
+CLEAVE_HIP_API int32_t cleave_hip_matmul_f32_host(const float* a, int64_t alen, const float* b, int64_t blen,
+                                                  float* c, int64_t clen, int32_t M, int32_t N, int32_t K,
+                                                  int32_t trans_a, int32_t trans_b);
+CLEAVE_HIP_API int32_t cleave_hip_matmul_batched_f32_host(const float* a, int64_t alen, const float* b,
+                                                          int64_t blen, float* c, int64_t clen, int32_t batch,
+                                                          int32_t M, int32_t N, int32_t K, int32_t trans_a,
+                                                          int32_t trans_b);
+CLEAVE_HIP_API int32_t cleave_hip_matmul_bf16_host(const uint16_t* a, int64_t alen, const uint16_t* b,
+                                                   int64_t blen, float* c, int64_t clen, int32_t M, int32_t N,
+                                                   int32_t K, int32_t trans_a, int32_t trans_b);
+CLEAVE_HIP_API int32_t cleave_hip_matmul_batched_bf16_host(const uint16_t* a, int64_t alen, const uint16_t* b,
+                                                           int64_t blen, float* c, int64_t clen, int32_t batch,
+                                                           int32_t M, int32_t N, int32_t K, int32_t trans_a,
+                                                           int32_t trans_b);
+
+/* Ring<Tensor> and Activation<Tensor> (stdlib/linalg/tensor.cleave:66-80,
+ * stdlib/nn/nn.cleave:82-95). */
+CLEAVE_HIP_API int32_t cleave_hip_add_f32_host(const float* a, int64_t alen, const float* b, int64_t blen,
+                                               float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_sub_f32_host(const float* a, int64_t alen, const float* b, int64_t blen,
+                                               float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_mul_f32_host(const float* a, int64_t alen, const float* b, int64_t blen,
+                                               float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_div_f32_host(const float* a, int64_t alen, const float* b, int64_t blen,
+                                               float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_neg_f32_host(const float* a, int64_t alen, float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_zero_f32_host(float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_relu_f32_host(const float* x, int64_t xlen, float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_sigmoid_f32_host(const float* x, int64_t xlen, float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_tanh_f32_host(const float* x, int64_t xlen, float* out, int64_t outlen);
+
+/* Backward maps (stdlib/num/num.cleave:123-136, :222-223). */
+CLEAVE_HIP_API int32_t cleave_hip_sigmoid_bwd_f32_host(const float* s, int64_t slen, const float* g, int64_t glen,
+                                                       float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_tanh_bwd_f32_host(const float* t, int64_t tlen, const float* g, int64_t glen,
+                                                    float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_relu_bwd_f32_host(const float* x, int64_t xlen, const float* g, int64_t glen,
+                                                    float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_div_bwd_f32_host(const float* a, int64_t alen, const float* b, int64_t blen,
+                                                   const float* g, int64_t glen, float* da, int64_t dalen,
+                                                   float* db, int64_t dblen);
+CLEAVE_HIP_API int32_t cleave_hip_sgd_update_f32_host(float* w, int64_t wlen, const float* g, int64_t glen,
+                                                      float lr);
+CLEAVE_HIP_API int32_t cleave_hip_add_row_bias_f32_host(const float* a, int64_t alen, const float* bias,
+                                                        int64_t blen, float* out, int64_t outlen, int32_t rows,
+                                                        int32_t cols);
+CLEAVE_HIP_API int32_t cleave_hip_sum_rows_f32_host(const float* g, int64_t glen, float* out, int64_t outlen,
+                                                    int32_t rows, int32_t cols);
+
+/* Sum / Mean / Max (stdlib/nn/nn.cleave:111-149): the value is returned, as
+ * by the stdlib functions; NaN (argmax -1, u64 sum 0) after an error. */
+CLEAVE_HIP_API float cleave_hip_sum_f32_host(const float* x, int64_t len);
+CLEAVE_HIP_API float cleave_hip_mean_f32_host(const float* x, int64_t len);
+CLEAVE_HIP_API float cleave_hip_max_of_f32_host(const float* x, int64_t len);
+CLEAVE_HIP_API int64_t cleave_hip_argmax_f32_host(const float* x, int64_t len);
+CLEAVE_HIP_API uint64_t cleave_hip_sum_u32_u64_host(const uint32_t* x, int64_t len);
+
+/* Index<Tensor> (stdlib/linalg/tensor.cleave:113-133). */
+CLEAVE_HIP_API float cleave_hip_index_f32_host(const float* t, int64_t len, const int32_t* dims, int64_t ndims,
+                                               const int32_t* idx, int64_t nidx);
+CLEAVE_HIP_API int32_t cleave_hip_index_bwd_f32_host(float g, float* dt, int64_t len, const int32_t* dims,
+                                                     int64_t ndims, const int32_t* idx, int64_t nidx);
+
+/* escape_count map (examples/mandelbrot.cleave:14-26). */
+CLEAVE_HIP_API int32_t cleave_hip_mandelbrot_u32_host(uint32_t* out, int64_t outlen, int32_t width,
+                                                      int32_t height, float x0, float y0, float dx, float dy,
+                                                      int32_t max_iter);
+
+/* MLP step (examples/xor_tensor.cleave:38-92 style); `loss` is a host float
+ * (one element) when non-null. */
+CLEAVE_HIP_API int32_t cleave_hip_mlp_step_f32_host(const float* x, int64_t xlen, const float* y, int64_t ylen,
+                                                    float* w1, int64_t w1len, float* w2, int64_t w2len,
+                                                    float* dw1, int64_t dw1len, float* dw2, int64_t dw2len,
+                                                    float* loss, int32_t B, int32_t D, int32_t Hd, float lr);
 
 #ifdef __cplusplus
 }

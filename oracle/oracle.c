@@ -361,6 +361,17 @@ void or_mandelbrot_rows(uint32_t* out, int32_t width, int32_t height, float x0, 
     }
 }
 
+void or_mandelbrot_rows_mt(uint32_t* out, int32_t width, int32_t height, float x0, float y0,
+                           float dx, float dy, int32_t max_iter, int32_t row0, int32_t row1,
+                           int32_t threads) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)
+#endif
+    for (int32_t r = row0; r < row1; ++r)
+        or_mandelbrot_rows(out, width, height, x0, y0, dx, dy, max_iter, r, r + 1);
+    (void)threads;
+}
+
 void or_mandelbrot_mt(uint32_t* out, int32_t width, int32_t height, float x0, float y0,
                       float dx, float dy, int32_t max_iter, int32_t threads) {
 #ifdef _OPENMP
@@ -449,6 +460,114 @@ float or_mlp_step_f32(const float* X, const float* y, float* W1, float* W2, int3
     free(H);
     free(d2);
     return loss;
+}
+
+/* Selected gradient entries of the step above, for checks at sizes where
+ * the whole step is too slow.  The forward pass, d2 and the loss are computed
+ * exactly as in or_mlp_step_f32 (rows split over threads; the row products
+ * run 4 columns per vector instruction, each column still one k-ascending
+ * chain of unfused mul/add, so the bits are those of the scalar loop).  Then
+ * dW2[n2[e]] = sum_m h[m,n] d2[m] and dW1[k1[e], n1[e]] = sum_m x[m,k] d1[m,n],
+ * d1 = (d2[m] W2[n]) h (1 - h), each m-ascending as in or_mlp_step_f32.
+ * abs1/abs2 receive the sums of |operand products| (the GEMM tolerance's
+ * denominators).  Returns the loss, or NaN when Hd % 4 != 0. */
+typedef float or_v4f __attribute__((vector_size(16)));
+
+float or_mlp_grad_entries(const float* X, const float* y, const float* W1, const float* W2,
+                          int32_t B, int32_t D, int32_t Hd, const int32_t* k1, const int32_t* n1,
+                          int64_t e1, float* dw1, float* abs1, const int32_t* n2, int64_t e2,
+                          float* dw2, float* abs2, int32_t threads) {
+    if (threads < 1) threads = 1;
+    if (Hd % 4 != 0) return NAN;
+    /* columns of H the sampled entries read, in one list */
+    int32_t* col_of = (int32_t*)malloc(sizeof(int32_t) * (size_t)Hd);
+    for (int32_t n = 0; n < Hd; ++n) col_of[n] = -1;
+    int32_t ncols = 0;
+    for (int64_t e = 0; e < e1; ++e)
+        if (col_of[n1[e]] < 0) col_of[n1[e]] = ncols++;
+    for (int64_t e = 0; e < e2; ++e)
+        if (col_of[n2[e]] < 0) col_of[n2[e]] = ncols++;
+    int32_t* cols = (int32_t*)malloc(sizeof(int32_t) * (size_t)(ncols > 0 ? ncols : 1));
+    for (int32_t n = 0; n < Hd; ++n)
+        if (col_of[n] >= 0) cols[col_of[n]] = n;
+    float* Hs = (float*)malloc(sizeof(float) * (size_t)B * (size_t)(ncols > 0 ? ncols : 1));
+    float* d2 = (float*)malloc(sizeof(float) * (size_t)B);
+    float* sq = (float*)malloc(sizeof(float) * (size_t)B);
+#ifdef _OPENMP
+#pragma omp parallel num_threads(threads)
+#endif
+    {
+        float* h = (float*)malloc(sizeof(float) * (size_t)Hd);
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+        for (int32_t m = 0; m < B; ++m) {
+            for (int32_t n = 0; n < Hd; ++n) h[n] = 0.0f;
+            for (int32_t k = 0; k < D; ++k) {
+                const float x = X[(int64_t)m * D + k];
+                const or_v4f xv = {x, x, x, x};
+                const float* w = &W1[(int64_t)k * Hd];
+                for (int32_t n = 0; n < Hd; n += 4) {
+                    or_v4f hv, wv;
+                    memcpy(&hv, &h[n], sizeof hv);
+                    memcpy(&wv, &w[n], sizeof wv);
+                    hv = hv + xv * wv; /* per column: h = h + x*w, k ascending */
+                    memcpy(&h[n], &hv, sizeof hv);
+                }
+            }
+            for (int32_t n = 0; n < Hd; ++n) h[n] = or_sigmoid_scalar(h[n]);
+            float z = 0.0f;
+            for (int32_t n = 0; n < Hd; ++n) z = z + h[n] * W2[n];
+            const float yh = or_sigmoid_scalar(z);
+            const float e = yh - y[m];
+            sq[m] = e * e;
+            const float gy = (e + e) / (float)B;
+            d2[m] = gy * yh * (1.0f - yh);
+            for (int32_t c = 0; c < ncols; ++c) Hs[(int64_t)m * ncols + c] = h[cols[c]];
+        }
+        free(h);
+    }
+    float acc = 0.0f;
+    for (int32_t m = 0; m < B; ++m) acc = (m == 0) ? sq[m] : acc + sq[m];
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
+#endif
+    for (int64_t e = 0; e < e2; ++e) {
+        const int32_t c = col_of[n2[e]];
+        float g = 0.0f;
+        double a = 0.0;
+        for (int32_t m = 0; m < B; ++m) {
+            const float hv = Hs[(int64_t)m * ncols + c];
+            g = g + hv * d2[m];
+            a += fabs((double)hv) * fabs((double)d2[m]);
+        }
+        dw2[e] = g;
+        if (abs2) abs2[e] = (float)a;
+    }
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
+#endif
+    for (int64_t e = 0; e < e1; ++e) {
+        const int32_t c = col_of[n1[e]], k = k1[e];
+        const float w2 = W2[n1[e]];
+        float g = 0.0f;
+        double a = 0.0;
+        for (int32_t m = 0; m < B; ++m) {
+            const float hv = Hs[(int64_t)m * ncols + c];
+            const float d1 = (d2[m] * w2) * hv * (1.0f - hv);
+            const float x = X[(int64_t)m * D + k];
+            g = g + x * d1;
+            a += fabs((double)x) * fabs((double)d1);
+        }
+        dw1[e] = g;
+        if (abs1) abs1[e] = (float)a;
+    }
+    free(col_of);
+    free(cols);
+    free(Hs);
+    free(d2);
+    free(sq);
+    return acc / (float)B;
 }
 
 double or_mlp_loss_f64(const float* X, const float* y, const float* W1, const float* W2,

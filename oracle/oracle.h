@@ -139,6 +139,10 @@ void or_mandelbrot_rows(uint32_t* out, int32_t width, int32_t height, float x0, 
                         float dx, float dy, int32_t max_iter, int32_t row0, int32_t row1);
 void or_mandelbrot_mt(uint32_t* out, int32_t width, int32_t height, float x0, float y0,
                       float dx, float dy, int32_t max_iter, int32_t threads);
+/* Rows [row0,row1) only, split across threads (bit-identical to the rows form). */
+void or_mandelbrot_rows_mt(uint32_t* out, int32_t width, int32_t height, float x0, float y0,
+                           float dx, float dy, int32_t max_iter, int32_t row0, int32_t row1,
+                           int32_t threads);
 
 /* ---- 2-layer MLP step (style of examples/xor_tensor.cleave:38-92) ----
  * H = sigmoid(X W1); yhat = sigmoid(H W2); L = mean((yhat - y)^2);
@@ -149,6 +153,14 @@ void or_mandelbrot_mt(uint32_t* out, int32_t width, int32_t height, float x0, fl
 float or_mlp_step_f32(const float* X, const float* y, float* W1, float* W2, int32_t B,
                       int32_t D, int32_t Hd, float lr, float* dW1, float* dW2,
                       int32_t threads);
+/* Selected entries of that step's gradients (dW1[k1[e], n1[e]], dW2[n2[e]])
+ * and its loss, with the forward pass computed as above; for full-size checks.
+ * abs1/abs2 receive sum |x||d1| and sum |h||d2| (tolerance denominators).
+ * Pinned: bitwise equal to or_mlp_step_f32's entries on small shapes. */
+float or_mlp_grad_entries(const float* X, const float* y, const float* W1, const float* W2,
+                          int32_t B, int32_t D, int32_t Hd, const int32_t* k1, const int32_t* n1,
+                          int64_t e1, float* dw1, float* abs1, const int32_t* n2, int64_t e2,
+                          float* dw2, float* abs2, int32_t threads);
 /* Loss only, in double (for finite-difference gradient checks). */
 double or_mlp_loss_f64(const float* X, const float* y, const float* W1, const float* W2,
                        int32_t B, int32_t D, int32_t Hd);

@@ -63,6 +63,9 @@ _SIGS = {
     "or_mandelbrot_mt": (None, [_p, _i32, _i32, _f, _f, _f, _f, _i32, _i32]),
     "or_mlp_step_f32": (_f, [_p, _p, _p, _p, _i32, _i32, _i32, _f, _p, _p, _i32]),
     "or_mlp_loss_f64": (C.c_double, [_p, _p, _p, _p, _i32, _i32, _i32]),
+    "or_mlp_grad_entries": (_f, [_p, _p, _p, _p, _i32, _i32, _i32, _p, _p, _i64, _p, _p, _p, _i64, _p, _p,
+                                 _i32]),
+    "or_mandelbrot_rows_mt": (None, [_p, _i32, _i32, _f, _f, _f, _f, _i32, _i32, _i32, _i32]),
     "or_xor_tensor_train": (None, [_i32, _f, _p]),
 }
 
@@ -294,8 +297,14 @@ def escape_count(cr: float, ci: float, max_iter: int, latch: bool = False) -> in
 
 
 def mandelbrot(width, height, x0, y0, dx, dy, max_iter, threads: int = 0, rows=None):
+    """Escape counts of the grid; with `rows` = (r0, r1) only those rows are
+    computed (the rest of the returned array stays zero), on `threads`
+    threads when threads > 0."""
     out = np.zeros((height, width), np.uint32)
-    if rows is not None:
+    if rows is not None and threads > 0:
+        lib().or_mandelbrot_rows_mt(_ptr(out), width, height, x0, y0, dx, dy, max_iter, rows[0], rows[1],
+                                    threads)
+    elif rows is not None:
         lib().or_mandelbrot_rows(_ptr(out), width, height, x0, y0, dx, dy, max_iter, rows[0], rows[1])
     elif threads > 0:
         lib().or_mandelbrot_mt(_ptr(out), width, height, x0, y0, dx, dy, max_iter, threads)
@@ -317,6 +326,23 @@ def mlp_step(X, y, W1, W2, lr: float, threads: int = 1):
     loss = lib().or_mlp_step_f32(_ptr(X), _ptr(y), _ptr(W1n), _ptr(W2n), B, D, Hd, lr, _ptr(dW1),
                                  _ptr(dW2), threads)
     return float(loss), dW1, dW2, W1n, W2n
+
+
+def mlp_grad_entries(X, y, W1, W2, k1, n1, n2, threads: int = 16):
+    """Selected entries of one step's gradients, computed as mlp_step computes
+    them: returns (loss, dW1[k1, n1], sum|x||d1|, dW2[n2], sum|h||d2|)."""
+    X, y, W1, W2 = _f32(X), _f32(y), _f32(W1), _f32(W2)
+    k1 = np.ascontiguousarray(k1, np.int32)
+    n1 = np.ascontiguousarray(n1, np.int32)
+    n2 = np.ascontiguousarray(n2, np.int32)
+    B, D = X.shape
+    Hd = W1.shape[1]
+    dw1, abs1 = np.empty(k1.size, np.float32), np.empty(k1.size, np.float32)
+    dw2, abs2 = np.empty(n2.size, np.float32), np.empty(n2.size, np.float32)
+    loss = lib().or_mlp_grad_entries(_ptr(X), _ptr(y), _ptr(W1), _ptr(W2), B, D, Hd, _ptr(k1), _ptr(n1),
+                                     k1.size, _ptr(dw1), _ptr(abs1), _ptr(n2), n2.size, _ptr(dw2),
+                                     _ptr(abs2), threads)
+    return float(loss), dw1, abs1, dw2, abs2
 
 
 def mlp_loss_f64(X, y, W1, W2) -> float:

@@ -132,7 +132,8 @@ def _lib_noabort():
     ("cleave_hip_matmul_f32", (None, 4, None, 4, None, 4, 2, 2, 2, 2, 0), "trans"),
     ("cleave_hip_matmul_f32", (None, 0, None, 0, None, 0, 0, 2, 2, 0, 0), "positive"),
     ("cleave_hip_matmul_bf16", (None, 4, None, 6, None, 4, 2, 2, 2, 0, 0), "blen"),
-    ("cleave_hip_matmul_batched_bf16", (None, 8, None, 8, None, 7, 2, 2, 2, 2), "lengths"),
+    ("cleave_hip_matmul_batched_bf16", (None, 8, None, 8, None, 7, 2, 2, 2, 2, 0, 0), "lengths"),
+    ("cleave_hip_matmul_batched_bf16", (None, 8, None, 8, None, 8, 2, 2, 2, 2, 0, 3), "trans"),
     ("cleave_hip_matmul_batched_f32", (None, 8, None, 8, None, 8, 0, 2, 2, 2, 0, 0), "batch"),
     ("cleave_hip_add_f32", (None, 3, None, 4, None, 3), "broadcast"),
     ("cleave_hip_sigmoid_f32", (None, 3, None, 2, ), "length"),

@@ -45,12 +45,14 @@ def test_matmul_against_ring_zero_is_exactly_zero(hip):
 
 
 def test_config1_256_cube_uniform_seed0(hip, oracle):
+    # A and B are the first and second 256^2 draws of the seed-0 uniform[-1,1)
+    # stream: one fill of 2 x 256^2 values, split in two
     n = 256
-    a = hip.fill_uniform(hip.empty((n, n)), seed=0)
-    b = hip.fill_uniform(hip.empty((n, n)), seed=1)
+    ab = hip.fill_uniform(hip.empty(2 * n * n), seed=0)
+    a, b = ab.sub(0, (n, n)), ab.sub(n * n, (n, n))
     A, B = a.numpy(), b.numpy()
     # the device generator is the oracle's generator, bit for bit
-    assert np.array_equal(A.ravel(), oracle.uniform(n * n, seed=0))
+    assert np.array_equal(np.concatenate([A.ravel(), B.ravel()]), oracle.uniform(2 * n * n, seed=0))
     got = hip.matmul(a, b).numpy()
     ref = oracle.matmul(A, B, threads=16)
     assert_gemm_close(got, ref, np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64), n, "256^3")
@@ -66,7 +68,7 @@ def test_shapes_and_layouts(hip, oracle, M, N, K, ta, tb):
     _full_check(hip, oracle, A, B, bool(ta), bool(tb), f"{M}x{N}x{K} ta={ta} tb={tb}")
 
 
-@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_config2_4096_cube_sampled_and_linearity(hip, oracle, ta, tb):
     n = 4096
     a = hip.fill_normal(hip.empty((n, n)), seed=11)
@@ -82,6 +84,12 @@ def test_config2_4096_cube_sampled_and_linearity(hip, oracle, ta, tb):
     rows = Ad @ Bd.sum(axis=1)
     den = np.abs(Ad) @ np.abs(Bd).sum(axis=1)
     assert np.max(np.abs(C.astype(np.float64).sum(axis=1) - rows) / den) <= 1e-5 * np.sqrt(n)
+    # every column: 1^T C = (1^T A) B, in float64, within the same bound; with
+    # the row identity, an entry stored in the wrong column of its row (or
+    # the wrong row of its column) moves a sum
+    cols = Ad.sum(axis=0) @ Bd
+    cden = np.abs(Ad).sum(axis=0) @ np.abs(Bd)
+    assert np.max(np.abs(C.astype(np.float64).sum(axis=0) - cols) / cden) <= 1e-5 * np.sqrt(n)
 
 
 def test_deterministic(hip):
@@ -150,6 +158,27 @@ def test_bf16_batched_tiled_every_entry(hip, oracle):
         ref = oracle.matmul(Au, Bu, threads=8)
         den = np.abs(Au).astype(np.float64) @ np.abs(Bu).astype(np.float64)
         assert_gemm_close(got[i], ref, den, K, f"batched bf16 entry {i}")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("bsz,M,N,K", [(4, 256, 256, 128), (64, 512, 512, 512)])
+def test_bf16_batched_every_layout(hip, oracle, bsz, M, N, K, ta, tb):
+    # The batched halves of the product rule (stdlib/linalg/matrix.cleave:24):
+    # each batch entry stored K x M (trans_a) or N x K (trans_b).  4 x 256^2 runs
+    # the 128 x 128 tiled kernel; 64 x 512^3 (config 5) the 256 x 256 one.
+    # Three entries of each are checked in full against the oracle.
+    a = hip.to_bf16(hip.fill_normal(hip.empty((bsz, K, M) if ta else (bsz, M, K)), seed=131 + 2 * ta + tb,
+                                    std=0.02))
+    b = hip.to_bf16(hip.fill_normal(hip.empty((bsz, N, K) if tb else (bsz, K, N)), seed=141 + 2 * ta + tb,
+                                    std=0.02))
+    got = hip.matmul_batched(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    A, B = a.numpy(), b.numpy()
+    for i in (0, bsz // 2 + 1, bsz - 1):
+        Au = oracle.bf16_to_f32(A[i]).reshape(A.shape[1:])
+        Bu = oracle.bf16_to_f32(B[i]).reshape(B.shape[1:])
+        ref = oracle.matmul(Au, Bu, trans_a=bool(ta), trans_b=bool(tb), threads=16)
+        den = (np.abs(Au.T if ta else Au).astype(np.float64) @ np.abs(Bu.T if tb else Bu).astype(np.float64))
+        assert_gemm_close(got[i], ref, den, K, f"batched bf16 ta={ta} tb={tb} #{i}")
 
 
 def test_bf16_tiled_output_is_overwritten_and_deterministic(hip):
@@ -246,17 +275,21 @@ def test_bf16_pingpong_every_layout(hip, oracle, ta, tb):
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("K", [16, 48, 80])
 def test_f32_pingpong_short_k(hip, oracle, K, ta, tb):
-    # 1, 3 and 5 k-tiles of 16: the ring of four LDS stages is never filled,
-    # or wraps once, so the copies past the last k-tile (clamped to it) and
-    # the prologue's two tiles are all exercised
+    # 4096 x 4096 outputs: the f32 ping-pong kernel of the headline, one tile
+    # per CU.  1, 3 and 5 k-tiles of 16: the ring of four LDS stages is never
+    # filled, or wraps once, so the copies past the last k-tile (clamped to
+    # it) and the prologue's two tiles are all exercised.  EVERY entry of C is
+    # compared with the oracle's sequential loop: an epilogue that stores a
+    # value in the wrong column of its row would keep every row sum.
     M = N = 4096
     a = hip.fill_normal(hip.empty((K, M) if ta else (M, K)), seed=81 + K + 2 * ta + tb)
     b = hip.fill_normal(hip.empty((N, K) if tb else (K, N)), seed=91 + K + 2 * ta + tb)
     c = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
     A, B = a.numpy(), b.numpy()
-    ii, jj = sample_entries(M, N, 1024, seed=K + ta + 2 * tb)
-    ref, absden = oracle.matmul_entries(A, B, M, N, K, ii, jj, trans_a=bool(ta), trans_b=bool(tb))
-    assert_gemm_close(c[ii, jj], ref, absden, K, f"f32 short K={K} ta={ta} tb={tb}")
+    ref = oracle.matmul(A, B, trans_a=bool(ta), trans_b=bool(tb), threads=16)
+    Aa = np.abs(A.T if ta else A).astype(np.float64)
+    Ba = np.abs(B.T if tb else B).astype(np.float64)
+    assert_gemm_close(c, ref, Aa @ Ba, K, f"f32 short K={K} ta={ta} tb={tb}, every entry")
     # every row sum, in float64
     Ad = (A.T if ta else A).astype(np.float64)
     Bd = (B.T if tb else B).astype(np.float64)

@@ -132,6 +132,23 @@ def test_bf16_matmul_entries_use_upcast_values(oracle):
     assert np.array_equal(vals.reshape(M, N), ref)
 
 
+def test_bf16_matmul_rows_equal_the_entries_form_bitwise(oracle):
+    # or_matmul_bf16_rows (the bf16 CPU baseline's loop) computes what the
+    # entries form computes, bit for bit, on every entry of a band of rows;
+    # a swapped index or a dropped term would change values.
+    rng = np.random.default_rng(6)
+    M, N, K = 13, 21, 67
+    Ab = oracle.to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    Bb = oracle.to_bf16(rng.standard_normal((K, N)).astype(np.float32))
+    rows = oracle.matmul_bf16_rows(Ab, Bb, M, N, K, 3, 11)
+    ii, jj = np.repeat(np.arange(3, 11), N), np.tile(np.arange(N), 8)
+    vals, _ = oracle.matmul_entries(Ab, Bb, M, N, K, ii, jj, bf16=True)
+    assert np.array_equal(rows.ravel(), vals)
+    # and both equal the f32 loop on the upcast values
+    ref = oracle.matmul(oracle.bf16_to_f32(Ab).reshape(M, K), oracle.bf16_to_f32(Bb).reshape(K, N))
+    assert np.array_equal(rows, ref[3:11])
+
+
 # ---- elementwise --------------------------------------------------------------
 
 def test_elementwise_golden(oracle, golden):
@@ -367,6 +384,16 @@ def test_escape_count_conjugate_symmetry_and_float64_agreement(oracle):
         assert oracle.escape_count(cr, ci, 300) == n64
 
 
+def test_mandelbrot_threaded_row_band_is_the_rows_form(oracle):
+    w, h = 200, 120
+    args = (w, h, -2.0, -1.5, 3.0 / w, 3.0 / h, 300)
+    band = oracle.mandelbrot(*args, threads=4, rows=(17, 90))
+    seq = oracle.mandelbrot(*args, rows=(17, 90))
+    assert np.array_equal(band, seq)
+    assert np.array_equal(band[17:90], oracle.mandelbrot(*args)[17:90])
+    assert not band[:17].any() and not band[90:].any()
+
+
 # ---- MLP + autograd ----------------------------------------------------------------
 
 def test_mlp_gradients_against_finite_differences(oracle):
@@ -408,6 +435,23 @@ def test_mlp_sgd_update_is_w_minus_lr_g(oracle):
     assert np.array_equal(W2n, W2 - lr * dW2)
     _, dW1t, _, _, _ = oracle.mlp_step(X, y, W1, W2, lr=0.0, threads=4)
     assert np.array_equal(dW1t, dW1)  # threading does not change any bit
+
+
+@pytest.mark.parametrize("B,D,Hd", [(64, 32, 48), (130, 20, 36), (256, 64, 128)])
+def test_mlp_grad_entries_equal_the_full_step_bitwise(oracle, B, D, Hd):
+    # The sampled-gradient oracle used at full size computes each entry exactly
+    # as the whole step does: every entry of dW1 and dW2, and the loss.
+    rng = np.random.default_rng(B + D + Hd)
+    X = rng.standard_normal((B, D)).astype(np.float32)
+    y = (rng.random(B) < 0.5).astype(np.float32)
+    W1 = rng.uniform(-0.3, 0.3, (D, Hd)).astype(np.float32)
+    W2 = rng.uniform(-0.3, 0.3, Hd).astype(np.float32)
+    L, dW1, dW2, _, _ = oracle.mlp_step(X, y, W1, W2, lr=0.01)
+    kk, nn = np.meshgrid(np.arange(D), np.arange(Hd), indexing="ij")
+    L2, g1, a1, g2, a2 = oracle.mlp_grad_entries(X, y, W1, W2, kk.ravel(), nn.ravel(), np.arange(Hd), threads=4)
+    assert L2 == L
+    assert np.array_equal(g1, dW1.ravel()) and np.array_equal(g2, dW2)
+    assert np.all(a1 >= np.abs(g1)) and np.all(a2 >= np.abs(g2))
 
 
 def test_xor_tensor_training_matches_reference_record(oracle, golden):
