@@ -82,6 +82,7 @@ SIGNATURES: dict[str, tuple] = {
     "cleave_hip_reduce_sum_f32": (i32, [vp, i64, vp]),
     "cleave_hip_reduce_max_f32": (i32, [vp, i64, vp, vp]),
     "cleave_hip_reduce_sum_u32_u64": (i32, [vp, i64, vp]),
+    "cleave_hip_reduce_sum_f32_noalloc": (i32, [vp, i64, vp]),
     "cleave_hip_sum_f32": (f32, [vp, i64]),
     "cleave_hip_mean_f32": (f32, [vp, i64]),
     "cleave_hip_max_of_f32": (f32, [vp, i64]),

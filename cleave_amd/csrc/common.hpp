@@ -34,6 +34,13 @@ void* scratch(int slot, size_t bytes);
 // Number of compute units (for grid sizing of persistent/strided kernels).
 int num_cus();
 
+// Workspace of the allocation-free entry point (cleave_hip_reduce_sum_f32_noalloc):
+// a static device array of kNoAllocFloats floats, its device address resolved
+// once at init with the library's device current.  nullptr when that failed.
+// Every call shares it: calls that overlap on one device race.
+constexpr int kNoAllocFloats = 16384;  // 64 KiB
+float* noalloc_workspace();
+
 // Tensor operands of the device entry points must be device memory: a host
 // address handed to a kernel faults the GPU.  Fails with CLEAVE_HIP_ERR_ARG
 // when `p` is not device (or managed) memory of this process, or when its

@@ -264,6 +264,30 @@ int32_t cleave_hip_reduce_sum_f32(const float* x, int64_t len, float* out_dev) {
     return CLEAVE_HIP_OK;
 }
 
+// cleave_hip_reduce_sum_f32 with its stage-1 partials in the library's static
+// workspace instead of allocated scratch: the same kernels, grid and result,
+// and no hipMalloc/hipFree on any call.  The partials are all written by
+// stage 1 before stage 2 reads them, so nothing needs clearing between calls.
+int32_t cleave_hip_reduce_sum_f32_noalloc(const float* x, int64_t len, float* out_dev) {
+    const char* fn = "cleave_hip_reduce_sum_f32_noalloc";
+    CH_REQUIRE(len >= 1, "%s: length must be >= 1 (sum reads v[0])", fn);
+    CH_REQUIRE(x && out_dev, "%s: null buffer", fn);
+    CH_INIT_OR_RETURN();
+    CH_DEVICE(fn, x, len * 4);
+    CH_DEVICE(fn, out_dev, 4);
+    float* part = ch::noalloc_workspace();
+    if (!part) return ch::fail(CLEAVE_HIP_ERR_RUNTIME, "%s: the static workspace has no device address", fn);
+    const int aligned = aligned16(x);
+    unsigned blocks = stage1_blocks(aligned ? len / 4 + 1 : len / kUnroll + 1);
+    CH_REQUIRE(blocks <= (unsigned)ch::kNoAllocFloats,
+               "%s: %u partial sums exceed the static workspace of %d floats", fn, blocks, ch::kNoAllocFloats);
+    sum_f32_stage1<<<blocks, kThreads, 0, ch::stream()>>>(x, len, part, aligned);
+    CH_LAUNCHED("sum_f32_stage1");
+    sum_f32_stage2<<<1, kThreads, 0, ch::stream()>>>(part, (int)blocks, out_dev);
+    CH_LAUNCHED("sum_f32_stage2");
+    return CLEAVE_HIP_OK;
+}
+
 int32_t cleave_hip_reduce_max_f32(const float* x, int64_t len, float* max_dev, int64_t* argmax_dev) {
     CH_REQUIRE(len >= 1, "cleave_hip_reduce_max_f32: length must be >= 1 (max_of reads v[0])");
     CH_REQUIRE(x && (max_dev || argmax_dev), "cleave_hip_reduce_max_f32: null buffer");

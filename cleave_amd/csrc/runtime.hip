@@ -11,6 +11,13 @@
 
 #include "common.hpp"
 
+// The allocation-free entry point's workspace: in the code object's global
+// segment, so each device the library loads on holds its own copy until the
+// process ends, and no call allocates it.  In host code `scratch` names a host
+// stand-in, never the device array: kernels are handed the address that
+// hipGetSymbolAddress returns (State::noalloc below).
+static __device__ __align__(256) float scratch[ch::kNoAllocFloats];
+
 namespace ch {
 
 namespace {
@@ -21,6 +28,7 @@ struct State {
     int cus = 0;
     void* scratch[8] = {};
     size_t scratch_bytes[8] = {};
+    float* noalloc = nullptr;  // device address of ::scratch on device 0
 };
 State g;
 int g_abort_on_error = 1;
@@ -30,6 +38,7 @@ thread_local char t_last_msg[512] = "";
 
 hipStream_t stream() { return g.stream; }
 int num_cus() { return g.cus; }
+float* noalloc_workspace() { return g.noalloc; }
 
 int32_t fail(int32_t code, const char* fmt, ...) {
     va_list ap;
@@ -69,6 +78,13 @@ int32_t ensure_init() {
         g.cus = prop.multiProcessorCount;
         // Default priority stream, non-blocking w.r.t. the legacy null stream.
         if (hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking) != hipSuccess) return;
+        // The library runs on device 0 only, which is current here: resolve
+        // that device's copy of the static workspace once.
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(::scratch)) == hipSuccess && p != nullptr)
+            g.noalloc = static_cast<float*>(p);
+        else
+            (void)hipGetLastError();  // only the allocation-free entry point needs it
         g.init_status = CLEAVE_HIP_OK;
     });
     if (g.init_status != CLEAVE_HIP_OK)

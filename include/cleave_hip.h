@@ -221,6 +221,16 @@ CLEAVE_HIP_API int32_t cleave_hip_reduce_sum_f32(const float* x, int64_t len, fl
 CLEAVE_HIP_API int32_t cleave_hip_reduce_max_f32(const float* x, int64_t len, float* max_dev,
                                   int64_t* argmax_dev);
 CLEAVE_HIP_API int32_t cleave_hip_reduce_sum_u32_u64(const uint32_t* x, int64_t len, uint64_t* out_dev);
+/* cleave_hip_reduce_sum_f32 that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same kernels, grid and result as cleave_hip_reduce_sum_f32;
+ * its partial sums live in a static 64 KiB device workspace (16384 floats,
+ * one per stage-1 block; a call needing more is CLEAVE_HIP_ERR_ARG) whose
+ * address the library's init resolves, so call cleave_hip_init() first if
+ * the first call must not initialise.  Every call on a device shares that
+ * workspace: calls that overlap on one device race. */
+CLEAVE_HIP_API int32_t cleave_hip_reduce_sum_f32_noalloc(const float* x, int64_t len, float* out_dev);
 /* Host-returning forms, like the stdlib functions (synchronise). */
 CLEAVE_HIP_API float cleave_hip_sum_f32(const float* x, int64_t len);
 CLEAVE_HIP_API float cleave_hip_mean_f32(const float* x, int64_t len);
