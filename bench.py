@@ -284,6 +284,43 @@ def cpu_secondary(orc, name, budget_s, **kw):
     raise KeyError(name)
 
 
+def host_boundary(steps):
+    """Rates of the `_host` entry points (cleave's extern boundary: pageable
+    host arrays staged through HBM, results copied back, stream synchronised)
+    at the BASELINE shapes, wall clock per call.  PCIe-inclusive figures for
+    the record; the headline `value` never includes a host transfer."""
+    import numpy as np
+
+    from cleave_amd import host
+
+    out = {}
+
+    def run(name, fn, work, unit, reps):
+        fn()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        dt = (time.perf_counter() - t0) / reps
+        out[name] = {"ms_per_call": round(dt * 1e3, 3), unit: round(work / dt / 1e9, 2)}
+        log(f"host boundary {name}: {dt * 1e3:.2f} ms per call")
+
+    rng = np.random.default_rng(5)
+    n = 4096
+    A = rng.standard_normal((n, n), dtype=np.float32)
+    B = rng.standard_normal((n, n), dtype=np.float32)
+    run("matmul_f32_host_4096", lambda: host.matmul(A, B), 2.0 * n ** 3, "GFLOP/s", max(3, steps // 4))
+    n1 = 256
+    A1, B1 = A[:n1, :n1].copy(), B[:n1, :n1].copy()
+    run("matmul_f32_host_256", lambda: host.matmul(A1, B1), 2.0 * n1 ** 3, "GFLOP/s", 50)
+    v = rng.standard_normal(1 << 28, dtype=np.float32)
+    run("sum_f32_host_268M", lambda: host.sum(v), 4.0 * v.size, "GB/s_of_input", max(3, steps // 4))
+    del v
+    g = 16384
+    run("escape_counts_host_16384", lambda: host.escape_counts(g, g, -2.0, -1.5, 3.0 / g, 3.0 / g, 1000),
+        float(g * g), "Gpixel/s", 3)
+    return out
+
+
 COPY_ELEMS = 1 << 26  # 256 MiB of f32 read, 256 MiB written per launch
 
 
@@ -313,6 +350,8 @@ def main():
     ap.add_argument("--vendor", action="store_true",
                     help="also time torch.matmul (hipBLASLt) on the GEMM shapes, same device")
     ap.add_argument("--vendor-only", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--host-boundary", action="store_true",
+                    help="only time the _host entry points (host arrays across the C ABI, PCIe included)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run the copy kernel used to scale rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
@@ -335,6 +374,9 @@ def main():
     steps, warmup = args.steps, args.warmup
     if args.calibrate_copy:
         calibrate_copy(ca, steps)
+        return
+    if args.host_boundary:
+        print(json.dumps({"host_boundary": host_boundary(steps)}), flush=True)
         return
 
     # ---- headline: f32 4096^3 NN --------------------------------------------

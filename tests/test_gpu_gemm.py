@@ -405,3 +405,28 @@ def test_infinities_and_nans_propagate_like_the_loop(hip, oracle, dtype):
     clean[[3, 7, 11]] = False
     clean[:, [20, 4000]] = False
     assert np.isfinite(got[clean]).all()
+
+
+@pytest.mark.parametrize("dtype,off", [("f32", 1), ("f32", 2), ("bf16", 1), ("bf16", 4)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+def test_misaligned_operand_views(hip, oracle, dtype, off, ta, tb):
+    # Operands starting `off` elements into their buffers (4 or 8 bytes for
+    # f32, 2 or 8 bytes for bf16) at a shape the fast kernels would otherwise
+    # take (multiples of 128 and 256): the launchers check the base pointers'
+    # 16-byte alignment and send such views to the guarded general kernel.
+    M, N, K = 256, 256, 128
+    rng = np.random.default_rng(7 * off + 2 * ta + tb)
+    A32 = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B32 = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    if dtype == "bf16":
+        A, B = oracle.to_bf16(A32), oracle.to_bf16(B32)
+        Au, Bu = oracle.bf16_to_f32(A).reshape(A.shape), oracle.bf16_to_f32(B).reshape(B.shape)
+    else:
+        A, B, Au, Bu = A32, B32, A32, B32
+    abuf = hip.from_numpy(np.concatenate([np.zeros(off, A.dtype), A.ravel()]), dtype)
+    bbuf = hip.from_numpy(np.concatenate([np.zeros(off, B.dtype), B.ravel()]), dtype)
+    a, b = abuf.sub(off, A.shape), bbuf.sub(off, B.shape)
+    got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    ref = oracle.matmul(Au, Bu, trans_a=bool(ta), trans_b=bool(tb))
+    den = np.abs(Au.T if ta else Au).astype(np.float64) @ np.abs(Bu.T if tb else Bu).astype(np.float64)
+    assert_gemm_close(got, ref, den, K, f"{dtype} view at +{off} ta={ta} tb={tb}")
