@@ -249,12 +249,13 @@ bool launch_pingpong(const uint16_t* a, const uint16_t* b, float* c, int M, int 
     return true;
 }
 
-// Layouts with one k-contiguous operand (A·B, Aᵀ·Bᵀ): the ping-pong kernel
-// that copies that operand two k-tiles at a time (gemm_bf16_pingpong.hpp).
+// Layouts with a k-contiguous operand (A·B, Aᵀ·Bᵀ, A·Bᵀ): the ping-pong
+// kernel that copies such an operand two k-tiles at a time, as whole 128-byte
+// rows (gemm_bf16_pingpong.hpp; for A·Bᵀ, A is the paired one).
 template <bool TA, bool TB>
 bool launch_pairs(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
                   int32_t* status) {
-    if constexpr (TA != TB) {
+    if constexpr (TA && !TB) {  // Aᵀ·B: no k-contiguous operand to pair
         return false;
     } else {
         using P = ch::Bf16PingPongPairs<!TA, TB>;

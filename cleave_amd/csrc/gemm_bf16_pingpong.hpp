@@ -172,9 +172,14 @@ namespace ch {
 // or earlier, and exactly 8 instructions follow them: M(u - 1) and M(u)
 // issue 2 single instructions each and one of them, being even, a pair.  So
 // every M phase ends in s_waitcnt vmcnt(8).
+// A·Bᵀ, whose operands are both k-contiguous, pairs A and keeps B as the
+// single operand, copied as 64-byte row segments into k-contiguous single
+// stages: two pair rings would not fit 160 KiB with copies issued far
+// enough ahead.
 template <bool AKC, bool BKC>
 struct Bf16PingPongPairs {
-    static_assert(AKC != BKC, "exactly one k-contiguous operand");
+    static_assert(AKC || BKC, "at least one k-contiguous operand");
+    static constexpr bool SKC = AKC && BKC;  // the single operand is k-contiguous too
     static constexpr int BM = 256, BN = 256, BK = 32, NW = 8, WN = 4, THREADS = 64 * NW;
     static constexpr int TM = 128, TN = 64, FM = TM / 16, FN = TN / 16;
     static constexpr int PAIR_BYTES = 256 * 2 * BK * 2, SINGLE_BYTES = 256 * BK * 2;
@@ -232,7 +237,8 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
         const int c = (lane & 7) ^ ((r >> 1) & 7);
         pvoff[j] = (uint32_t)(((int64_t)(pr0 + r) * pld + 8 * c) * 2);
     }
-    TileCopy<false, 256, BK, NW> scopy;
+    constexpr bool SKC = P::SKC;
+    TileCopy<SKC, 256, BK, NW> scopy;
     scopy.init(sld, sr0, wave, lane);
     const uint32_t sstep = (uint32_t)scopy.kstep(sld);
     auto issue_pair = [&](auto stage, int p) {
@@ -268,7 +274,7 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
             }
 #pragma unroll
         for (int f = 0; f < NSF; ++f) {
-            rs[f] = lds0 + (uint32_t)P::SINGLE_REGION + frag16_offset<false, 256, BK>(srow0 + f * 16, lane);
+            rs[f] = lds0 + (uint32_t)P::SINGLE_REGION + frag16_offset<SKC, 256, BK>(srow0 + f * 16, lane);
             opaque(rs[f]);
         }
     }
@@ -293,7 +299,9 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
         }
 #pragma unroll
         for (int f = 0; f < NSF; ++f) {
-            const v8bf v = read16_mn_at<256>(rs[f] + (uint32_t)(SS * P::SINGLE_BYTES));
+            v8bf v;
+            if constexpr (SKC) v = read16_kc_at(rs[f] + (uint32_t)(SS * P::SINGLE_BYTES));
+            else v = read16_mn_at<256>(rs[f] + (uint32_t)(SS * P::SINGLE_BYTES));
             if constexpr (AKC) fb[f] = v;
             else fa[f] = v;
         }
