@@ -321,6 +321,27 @@ def host_boundary(steps):
     return out
 
 
+def gemm_bf16_layouts(ca, layouts, steps):
+    """The bf16 8192^3 product of the bench, in each of the given layouts
+    ("nn", "nt", "tn", "tt": op(A) op(B)), timed with HIP events after a 0.5 s
+    clock-settling warm-up.  For comparing kernels and collecting counters."""
+    m = 8192
+    a32 = ca.fill_normal(ca.empty((m, m)), seed=201, std=0.02)
+    ab = ca.to_bf16(a32)
+    ca.fill_normal(a32, seed=202, std=0.02)
+    bb = ca.to_bf16(a32)
+    del a32
+    c = ca.empty((m, m))
+    out = {}
+    for lay in layouts:
+        ta, tb = lay[0] == "t", lay[1] == "t"
+        _, ev = timed(ca, lambda: ca.matmul(ab, bb, trans_a=ta, trans_b=tb, out=c), steps, 3, 0.5)
+        out[lay] = {"kernel_ms": round(ev, 4), "TFLOP/s": round(2.0 * m ** 3 / (ev * 1e-3) / 1e12, 1),
+                    "frac_bf16_mfma": round(2.0 * m ** 3 / (ev * 1e-3) / 1e12 / PEAK_BF16_MFMA, 4)}
+        log(f"gemm bf16 8192^3 {lay}: {ev:.4f} ms")
+    return out
+
+
 COPY_ELEMS = 1 << 26  # 256 MiB of f32 read, 256 MiB written per launch
 
 
@@ -350,6 +371,8 @@ def main():
     ap.add_argument("--vendor", action="store_true",
                     help="also time torch.matmul (hipBLASLt) on the GEMM shapes, same device")
     ap.add_argument("--vendor-only", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--gemm-bf16", metavar="LAYOUTS", default=None,
+                    help="only time the bf16 8192^3 product in the comma-separated layouts (nn,nt,tn,tt)")
     ap.add_argument("--host-boundary", action="store_true",
                     help="only time the _host entry points (host arrays across the C ABI, PCIe included)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -374,6 +397,10 @@ def main():
     steps, warmup = args.steps, args.warmup
     if args.calibrate_copy:
         calibrate_copy(ca, steps)
+        return
+    if args.gemm_bf16:
+        print(json.dumps({"gemm_bf16_8192": gemm_bf16_layouts(ca, args.gemm_bf16.split(","), steps),
+                          "library": str(ca._lib.LIB_PATH)}), flush=True)
         return
     if args.host_boundary:
         print(json.dumps({"host_boundary": host_boundary(steps)}), flush=True)

@@ -6,15 +6,17 @@ the `extern(symbol) fn ...` declarations of /root/reference/stdlib/io/io.cleave:
 every function gets explicit argtypes/restype, the library's abort-on-error
 mode is switched off, and a negative status becomes a CleaveHipError.
 
-The library is loaded from this package directory only.  If it has not been
-built, import fails loudly -- there is no CPU fallback.
+The library is loaded from this package directory (or, for comparing two
+builds, from the path in CLEAVE_HIP_LIBRARY).  If it has not been built,
+import fails loudly -- there is no CPU fallback.
 """
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libcleave_hip.so"
+LIB_PATH = Path(os.environ.get("CLEAVE_HIP_LIBRARY") or (Path(__file__).resolve().parent / "libcleave_hip.so"))
 
 OK, ERR_RUNTIME, ERR_ARG, ERR_OOM = 0, -1, -2, -3
 
