@@ -342,6 +342,28 @@ def gemm_bf16_layouts(ca, layouts, steps):
     return out
 
 
+def gemm_bf16_batched_layouts(ca, layouts, steps):
+    """The batched bf16 64 x 512^3 product of the bench, in each of the given
+    layouts, timed like gemm_bf16_layouts; also as a fraction of HBM for the
+    compulsory bytes (bf16 A and B read once, f32 C written once)."""
+    bs, k = 64, 512
+    t32 = ca.fill_normal(ca.empty((bs, k, k)), seed=301, std=0.02)
+    xb = ca.to_bf16(t32)
+    ca.fill_normal(t32, seed=302, std=0.02)
+    yb = ca.to_bf16(t32)
+    del t32
+    zb = ca.empty((bs, k, k))
+    hbm = bs * k * k * (2 + 2 + 4)
+    out = {}
+    for lay in layouts:
+        ta, tb = lay[0] == "t", lay[1] == "t"
+        _, ev = timed(ca, lambda: ca.matmul_batched(xb, yb, trans_a=ta, trans_b=tb, out=zb), steps * 4, 3, 0.3)
+        out[lay] = {"kernel_ms": round(ev, 5), "frac_hbm": round(hbm / (ev * 1e-3) / 1e9 / PEAK_HBM, 4),
+                    "frac_bf16_mfma": round(2.0 * bs * k ** 3 / (ev * 1e-3) / 1e12 / PEAK_BF16_MFMA, 4)}
+        log(f"gemm bf16 batched 64 x 512^3 {lay}: {ev * 1e3:.2f} us")
+    return out
+
+
 COPY_ELEMS = 1 << 26  # 256 MiB of f32 read, 256 MiB written per launch
 
 
@@ -373,6 +395,8 @@ def main():
     ap.add_argument("--vendor-only", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--gemm-bf16", metavar="LAYOUTS", default=None,
                     help="only time the bf16 8192^3 product in the comma-separated layouts (nn,nt,tn,tt)")
+    ap.add_argument("--gemm-bf16-batched", metavar="LAYOUTS", default=None,
+                    help="only time the batched bf16 64 x 512^3 product in the given layouts")
     ap.add_argument("--host-boundary", action="store_true",
                     help="only time the _host entry points (host arrays across the C ABI, PCIe included)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -401,6 +425,10 @@ def main():
     if args.gemm_bf16:
         print(json.dumps({"gemm_bf16_8192": gemm_bf16_layouts(ca, args.gemm_bf16.split(","), steps),
                           "library": str(ca._lib.LIB_PATH)}), flush=True)
+        return
+    if args.gemm_bf16_batched:
+        print(json.dumps({"gemm_bf16_batched_64x512": gemm_bf16_batched_layouts(
+            ca, args.gemm_bf16_batched.split(","), steps), "library": str(ca._lib.LIB_PATH)}), flush=True)
         return
     if args.host_boundary:
         print(json.dumps({"host_boundary": host_boundary(steps)}), flush=True)
