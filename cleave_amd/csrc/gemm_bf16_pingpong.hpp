@@ -33,8 +33,10 @@ struct Bf16PingPong {
 
     static bool fits(int M, int N, int K, int64_t lda, int64_t ldb) {
         const bool dims = M % BM == 0 && N % BN == 0 && K % BK == 0 && lda % 8 == 0 && ldb % 8 == 0;
-        const uint64_t a_span = (AKC ? (uint64_t)M : (uint64_t)BK + 1) * (uint64_t)lda * 2;
-        const uint64_t b_span = (BKC ? (uint64_t)N : (uint64_t)BK + 1) * (uint64_t)ldb * 2;
+        // the 32-bit lane offsets span one tile: BM (BN) rows of a k-contiguous
+        // operand, BK k-rows of an m/n-contiguous one
+        const uint64_t a_span = (AKC ? (uint64_t)BM : (uint64_t)BK + 1) * (uint64_t)lda * 2;
+        const uint64_t b_span = (BKC ? (uint64_t)BN : (uint64_t)BK + 1) * (uint64_t)ldb * 2;
         return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
     }
 };
@@ -70,15 +72,17 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
     const uint32_t lds0 = lds_addr(smem);
     const int nk = K / BK;
     const uint32_t step_a32 = (uint32_t)step_a, step_b32 = (uint32_t)step_b;
+    const char* a_src = reinterpret_cast<const char*>(A) + copy_a.base_offset(lda, m0);
+    const char* b_src = reinterpret_cast<const char*>(B) + copy_b.base_offset(ldb, n0);
     auto issue = [&](int kt) {  // k-tile min(kt, nk-1) into stage kt % S
         const int src = min(kt, nk - 1);
         const uint32_t dst = lds0 + (uint32_t)((kt % S) * P::STAGE_BYTES);
         if constexpr (OFF32) {
-            copy_a.issue(reinterpret_cast<const char*>(A) + (uint32_t)src * step_a32, dst, wave);
-            copy_b.issue(reinterpret_cast<const char*>(B) + (uint32_t)src * step_b32, dst + P::A_BYTES, wave);
+            copy_a.issue(a_src + (uint32_t)src * step_a32, dst, wave);
+            copy_b.issue(b_src + (uint32_t)src * step_b32, dst + P::A_BYTES, wave);
         } else {
-            copy_a.issue(reinterpret_cast<const char*>(A) + src * step_a, dst, wave);
-            copy_b.issue(reinterpret_cast<const char*>(B) + src * step_b, dst + P::A_BYTES, wave);
+            copy_a.issue(a_src + src * step_a, dst, wave);
+            copy_b.issue(b_src + src * step_b, dst + P::A_BYTES, wave);
         }
     };
 
@@ -188,12 +192,13 @@ struct Bf16PingPongPairs {
     static constexpr int LDS_BYTES = SINGLE_REGION + SINGLES * SINGLE_BYTES;
     static_assert(LDS_BYTES <= 160 * 1024, "LDS per workgroup");
 
-    // Also requires every byte offset a copy forms (the whole k-contiguous
-    // operand, K rows of the m/n-contiguous one) under 4 GiB.
+    // Also requires every 32-bit byte offset a copy forms under 4 GiB: 256
+    // rows of a k-contiguous operand (its tile's first row is in the 64-bit
+    // base), K rows of an m/n-contiguous one.
     static bool fits(int M, int N, int K, int64_t lda, int64_t ldb) {
         const bool dims = M % BM == 0 && N % BN == 0 && K % (2 * BK) == 0 && lda % 8 == 0 && ldb % 8 == 0;
-        const uint64_t a_span = (uint64_t)(AKC ? M : K + 1) * (uint64_t)lda * 2;
-        const uint64_t b_span = (uint64_t)(BKC ? N : K + 1) * (uint64_t)ldb * 2;
+        const uint64_t a_span = (uint64_t)(AKC ? BM : K + 1) * (uint64_t)lda * 2;
+        const uint64_t b_span = (uint64_t)(BKC ? BN : K + 1) * (uint64_t)ldb * 2;
         return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
     }
 };
@@ -222,10 +227,14 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
     const int nk = K / BK, np = nk / 2;
 
     // the paired (k-contiguous) operand and the single (m/n-contiguous) one
-    const char* pbase = reinterpret_cast<const char*>(AKC ? A : B);
-    const char* sbase = reinterpret_cast<const char*>(AKC ? B : A);
+    // (the paired tile's first row is in its 64-bit base, so the 32-bit lane
+    // offsets span 256 rows)
     const int64_t pld = AKC ? lda : ldb, sld = AKC ? ldb : lda;
     const int pr0 = AKC ? m0 : n0, sr0 = AKC ? n0 : m0;
+    constexpr bool SKC = P::SKC;
+    using SCopy = TileCopy<SKC, 256, BK, NW>;
+    const char* pbase = reinterpret_cast<const char*>(AKC ? A : B) + (int64_t)pr0 * pld * 2;
+    const char* sbase = reinterpret_cast<const char*>(AKC ? B : A) + SCopy::base_offset(sld, sr0);
 
     // pair copy: instruction q = wave + 8 j moves rows 8q .. 8q+7; lane l takes
     // row 8q + l/8 and slot l%8, which holds chunk (l%8) ^ ((row >> 1) & 7)
@@ -235,10 +244,9 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
         const int q = wave + NW * j;
         const int r = 8 * q + (lane >> 3);
         const int c = (lane & 7) ^ ((r >> 1) & 7);
-        pvoff[j] = (uint32_t)(((int64_t)(pr0 + r) * pld + 8 * c) * 2);
+        pvoff[j] = (uint32_t)(((int64_t)r * pld + 8 * c) * 2);
     }
-    constexpr bool SKC = P::SKC;
-    TileCopy<SKC, 256, BK, NW> scopy;
+    SCopy scopy;
     scopy.init(sld, sr0, wave, lane);
     const uint32_t sstep = (uint32_t)scopy.kstep(sld);
     auto issue_pair = [&](auto stage, int p) {

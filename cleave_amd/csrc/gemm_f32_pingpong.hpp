@@ -79,8 +79,11 @@ struct F32PingPong {
 
     static bool fits(int M, int N, int K, int64_t lda, int64_t ldb) {
         const bool dims = M % BM == 0 && N % BN == 0 && K % BK == 0 && lda % 4 == 0 && ldb % 4 == 0;
-        const uint64_t a_span = (AKC ? (uint64_t)M : (uint64_t)BK + 1) * (uint64_t)lda * 4;
-        const uint64_t b_span = (BKC ? (uint64_t)N : (uint64_t)BK + 1) * (uint64_t)ldb * 4;
+        // the 32-bit offsets span one tile: BM (BN) rows of a k-contiguous
+        // operand (its first row is in the buffer resource's base), BK k-rows
+        // of an m/n-contiguous one
+        const uint64_t a_span = (AKC ? (uint64_t)BM : (uint64_t)BK + 1) * (uint64_t)lda * 4;
+        const uint64_t b_span = (BKC ? (uint64_t)BN : (uint64_t)BK + 1) * (uint64_t)ldb * 4;
         return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
     }
 };
@@ -210,9 +213,9 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
     // k-contiguous operands: staged through registers.
     Staged<NW, KROW, ROW> st_a, st_b;
     if constexpr (!AKC) dma_a.init(lda, m0, wave, lane, region_a);
-    else st_a.init(lda, m0, wave, lane, region_a);
+    else st_a.init(lda, 0, wave, lane, region_a);
     if constexpr (!BKC) dma_b.init(ldb, n0, wave, lane, region_b);
-    else st_b.init(ldb, n0, wave, lane, region_b);
+    else st_b.init(ldb, 0, wave, lane, region_b);
     // byte step of an operand's base per k-tile
     const int64_t step_a = AKC ? (int64_t)BK * 4 : (int64_t)BK * lda * 4;
     const int64_t step_b = BKC ? (int64_t)BK * 4 : (int64_t)BK * ldb * 4;
@@ -235,7 +238,10 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
                 dma16(d2 + (int64_t)src * BK, (uint32_t)(lane * 16), region_d2 + (uint32_t)((kt % S) * BK * 4));
         }
     };
-    const __amdgpu_buffer_rsrc_t rsrc_a = raw_rsrc(A), rsrc_b = raw_rsrc(B);
+    // a k-contiguous operand's resource starts at its tile's first row: the
+    // 32-bit offsets then span 256 rows, so an operand of any size is reached
+    const __amdgpu_buffer_rsrc_t rsrc_a = raw_rsrc(A + (AKC ? (int64_t)m0 * lda : 0));
+    const __amdgpu_buffer_rsrc_t rsrc_b = raw_rsrc(B + (BKC ? (int64_t)n0 * ldb : 0));
     auto load_staged = [&](int kt) {
         const uint32_t src = (uint32_t)min(kt, nk - 1);
         if constexpr (AKC) st_a.load(rsrc_a, src * (uint32_t)step_a, st_a.data);

@@ -28,12 +28,14 @@ struct F32Tiled {
     static_assert(LDS_BYTES <= 160 * 1024, "LDS per workgroup");
 
     // Shapes this kernel takes without bounds checks.  The copies address an
-    // operand with 32-bit byte offsets from a per-k-tile scalar base, so the
-    // addressed span of each operand must stay under 4 GiB.
+    // operand with 32-bit byte offsets from a per-tile, per-k-tile scalar
+    // base, so the span those offsets reach must stay under 4 GiB.
     static bool fits(int M, int N, int K, int64_t lda, int64_t ldb) {
         const bool dims = M % BM == 0 && N % BN == 0 && K % BK == 0 && lda % 8 == 0 && ldb % 8 == 0;
-        const uint64_t a_span = (AKC ? (uint64_t)M : (uint64_t)BK + 1) * (uint64_t)lda * 4;
-        const uint64_t b_span = (BKC ? (uint64_t)N : (uint64_t)BK + 1) * (uint64_t)ldb * 4;
+        // that span: BM (BN) rows of a k-contiguous operand, BK k-rows of an
+        // m/n-contiguous one
+        const uint64_t a_span = (AKC ? (uint64_t)BM : (uint64_t)BK + 1) * (uint64_t)lda * 4;
+        const uint64_t b_span = (BKC ? (uint64_t)BN : (uint64_t)BK + 1) * (uint64_t)ldb * 4;
         return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
     }};
 
@@ -62,11 +64,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
     copy_a.init(lda, m0, wave, lane);
     copy_b.init(ldb, n0, wave, lane);
     const int64_t step_a = copy_a.kstep(lda), step_b = copy_b.kstep(ldb);
+    const char* a_src = reinterpret_cast<const char*>(A) + copy_a.base_offset(lda, m0);
+    const char* b_src = reinterpret_cast<const char*>(B) + copy_b.base_offset(ldb, n0);
     const uint32_t lds0 = lds_addr(smem);
     auto issue = [&](int kt, int stage) {
         const uint32_t dst = lds0 + (uint32_t)(stage * P::STAGE_BYTES);
-        copy_a.issue(reinterpret_cast<const char*>(A) + kt * step_a, dst, wave);
-        copy_b.issue(reinterpret_cast<const char*>(B) + kt * step_b, dst + P::A_BYTES, wave);
+        copy_a.issue(a_src + kt * step_a, dst, wave);
+        copy_b.issue(b_src + kt * step_b, dst + P::A_BYTES, wave);
     };
 
     v16f acc[FM][FN];

@@ -92,11 +92,15 @@ __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t
     asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds_dst) : "memory");
 }
 
-// Per-lane byte offsets (relative to the operand base of k-tile 0) of this
-// wave's NI/NW copy instructions for one operand tile, and the byte step that
-// moves them to the next k-tile (added to the scalar base).
-//   KC: tile [R rows][BK]; instruction q covers rows q*RPI .. +RPI-1.
-//   MN: tile [BK][R];      instruction q covers k-rows q*KPI .. +KPI-1.
+// Per-lane byte offsets of this wave's NI/NW copy instructions for one
+// operand tile, and the byte step that moves them to the next k-tile (added
+// to the scalar base).
+//   KC: tile [R rows][BK]; instruction q covers rows q*RPI .. +RPI-1.  The
+//       offsets count from the tile's first row, which base_offset() puts in
+//       the 64-bit scalar base: the 32-bit lane offsets then span R rows, so
+//       an operand of any size is reached.
+//   MN: tile [BK][R];      instruction q covers k-rows q*KPI .. +KPI-1, from
+//       the tile's first column r0 (BK rows of the operand, whatever its size).
 // Instruction q's LDS destination is tile_base + 1024*q.
 template <bool KC, int R, int BK, int NW, int ESZ = 2>
 struct TileCopy {
@@ -113,7 +117,7 @@ struct TileCopy {
                 const int q = wave + NW * j;
                 const int r = q * RPI + lane / CPR;
                 const int c = kc_slot<CPR, ESZ>(r, lane % CPR);  // slot lane%CPR holds chunk c
-                voff[j] = (uint32_t)(((int64_t)(r0 + r) * ld + EPC * c) * ESZ);
+                voff[j] = (uint32_t)(((int64_t)r * ld + EPC * c) * ESZ);
             }
         } else {
             constexpr int CPR = R / EPC, KPI = 64 / CPR;
@@ -126,6 +130,12 @@ struct TileCopy {
                 voff[j] = (uint32_t)(((int64_t)kr * ld + r0 + EPC * c) * ESZ);
             }
         }
+    }
+    // Byte offset of the tile starting at row (KC) or column (MN) r0 from the
+    // operand's base, to add to the scalar base (the MN column offset is in
+    // the lane offsets already).
+    static __device__ __forceinline__ int64_t base_offset(int64_t ld, int r0) {
+        return KC ? (int64_t)r0 * ld * ESZ : 0;
     }
     // Byte step of the scalar base per k-tile.
     static __device__ __forceinline__ int64_t kstep(int64_t ld) {

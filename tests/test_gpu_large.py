@@ -1,10 +1,10 @@
 """Maximum sizes: arrays past 2^31 elements and GEMM operands past 4 GiB.
 
 The maps, reductions, Index and the escape-count map index with 64-bit
-integers; the fast GEMM kernels address operands with 32-bit per-lane offsets
-and hand an operand spanning 4 GiB or more to the general kernel, which
-indexes with 64-bit integers.  Each case checks sampled entries against the
-oracle (or exact closed forms) without copying the arrays back whole.
+integers; the fast GEMM kernels address a tile with 32-bit per-lane offsets
+from a 64-bit per-tile base, so an operand spanning 4 GiB or more stays on
+them.  Each case checks sampled entries against the oracle (or exact closed
+forms) without copying the arrays back whole.
 One MI355X holds 288 GB; the largest case here allocates 24 GiB.
 """
 from __future__ import annotations
@@ -95,10 +95,10 @@ def test_index_past_2pow31(hip, oracle):
 
 
 @pytest.mark.parametrize("dtype,M,K,tb", [("f32", 1 << 20, 1024, 0), ("f32", 1 << 20, 1024, 1),
-                                         ("bf16", 1 << 21, 1024, 0)])
+                                         ("bf16", 1 << 21, 1024, 0), ("bf16", 1 << 21, 1024, 1)])
 def test_gemm_operand_past_4gib(hip, oracle, dtype, M, K, tb):
-    # A (M x K) spans exactly 4 GiB, one past what the fast kernels' 32-bit
-    # lane offsets reach; with tb, B (N x K) is the k-contiguous operand too.
+    # A (M x K) spans exactly 4 GiB, one byte past what a 32-bit offset from
+    # the operand's base reaches; with tb, B (N x K) is k-contiguous too.
     # The product must still be the reference loop's, within the GEMM bound.
     N = 256
     print(f"{dtype} gemm {M}x{N}x{K} tb={tb}: A spans {M * K * (4 if dtype == 'f32' else 2) / 2**30:.1f} GiB",
