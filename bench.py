@@ -342,6 +342,18 @@ def gemm_bf16_layouts(ca, layouts, steps):
     return out
 
 
+def copy_same_bytes(ca, nbytes, steps):
+    """Kernel time of the library's streaming map (neg: 4 bytes read and 4
+    written per element) moving nbytes / 2 each way: the floor a kernel that
+    moves the same compulsory bytes meets at this size on this box."""
+    n = nbytes // 8
+    x = ca.fill_normal(ca.empty(n), seed=7)
+    y = ca.empty(n)
+    _, ev = timed(ca, lambda: ca.neg(x, out=y), steps, 3, 0.3)
+    del x, y
+    return ev
+
+
 def gemm_bf16_batched_layouts(ca, layouts, steps):
     """The batched bf16 64 x 512^3 product of the bench, in each of the given
     layouts, timed like gemm_bf16_layouts; also as a fraction of HBM for the
@@ -361,6 +373,9 @@ def gemm_bf16_batched_layouts(ca, layouts, steps):
         out[lay] = {"kernel_ms": round(ev, 5), "frac_hbm": round(hbm / (ev * 1e-3) / 1e9 / PEAK_HBM, 4),
                     "frac_bf16_mfma": round(2.0 * bs * k ** 3 / (ev * 1e-3) / 1e12 / PEAK_BF16_MFMA, 4)}
         log(f"gemm bf16 batched 64 x 512^3 {lay}: {ev * 1e3:.2f} us")
+    cp = copy_same_bytes(ca, hbm, steps * 4)
+    out["copy_same_bytes"] = {"kernel_ms": round(cp, 5), "frac_hbm": round(hbm / (cp * 1e-3) / 1e9 / PEAK_HBM, 4)}
+    log(f"streaming copy of the same {hbm >> 20} MiB: {cp * 1e3:.2f} us")
     return out
 
 
@@ -489,8 +504,9 @@ def main():
         secondary["gemm_f32_256"] = {"GFLOP/s": round(fl1 * 200 / wall_s / 1e9, 1), "kernel_ms": round(ev, 5),
                                      "kernel_GFLOP/s": round(fl1 / (ev * 1e-3) / 1e9, 1),
                                      "frac_fp32_mfma": round(fl1 / (ev * 1e-3) / 1e12 / PEAK_FP32_MFMA, 4),
-                                     "note": "launch-bound: one 256^3 product is 4 tiles of 128 x 128; wall "
-                                             "GFLOP/s includes the host call per step"}
+                                     "note": "latency-bound: one 256^3 product is 16 tiles of 64 x 64 on 16 "
+                                             "CUs, each 128 serial fp32 MFMAs per wave after one copy wait; "
+                                             "wall GFLOP/s includes the host call per step"}
         log(f"gemm_f32_256: {fl1 / (ev * 1e-3) / 1e9:.0f} GFLOP/s kernel")
         if want_cpu:
             secondary["gemm_f32_256"]["cpu_baseline"] = cpu_secondary(orc, "gemm_f32_256", cb,
@@ -542,7 +558,14 @@ def main():
                                                  "frac_bf16_mfma": round(ach / PEAK_BF16_MFMA, 4),
                                                  "hbm_GB/s": round(hbm / (ev * 1e-3) / 1e9, 1),
                                                  "frac_hbm": round(hbm / (ev * 1e-3) / 1e9 / PEAK_HBM, 4)}
-        log(f"gemm_bf16_batched_64x512: {ach:.1f} TFLOP/s")
+        # the same bytes moved by the library's streaming map, same run
+        cp = copy_same_bytes(ca, hbm, sec_steps * 4)
+        secondary["gemm_bf16_batched_64x512"].update(
+            {"copy_same_bytes_ms": round(cp, 5), "frac_of_copy": round(cp / ev, 4),
+             "note": "the compulsory bytes (bf16 A, B read; f32 C written: 64 MiB each way) moved by "
+                     "the library's streaming map in one launch take copy_same_bytes_ms; frac_of_copy "
+                     "= that time / the product's"})
+        log(f"gemm_bf16_batched_64x512: {ach:.1f} TFLOP/s; a streaming copy of the same bytes {cp * 1e3:.2f} us")
         if want_cpu:
             secondary["gemm_bf16_batched_64x512"]["cpu_baseline"] = cpu_secondary(
                 orc, "gemm_bf16_batched_64x512", cb, A=xb.numpy()[0], B=yb.numpy()[0], bs=bs, k=k)

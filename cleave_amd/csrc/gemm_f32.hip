@@ -3,8 +3,9 @@
 // Shapes that divide a 256 x 256 x 16 tile, with a tile per CU, run the
 // ping-pong kernel of gemm_f32_pingpong.hpp; shapes that divide a
 // 128 x 128 x 16 tile run the large-tile kernel of gemm_f32_tiled.hpp (LDS
-// filled by global_load_lds, four MFMA k-steps per 16-byte operand read).
-// Everything else runs the general kernel below.
+// filled by global_load_lds, four MFMA k-steps per 16-byte operand read);
+// small products that divide 64 x 64 x 16 run it with 64 x 64 tiles and a
+// 16-deep ring.  Everything else runs the general kernel below.
 //
 // Replaces linalg.matmul as cleave lowers it (stdlib/linalg/matrix.cleave:27-61,
 // region cleave/src/mlir_lower.rs:2089-2120): C = 0; C[i,j] += A[i,k]*B[k,j].
@@ -270,6 +271,14 @@ int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, in
         const int64_t big_tiles = (int64_t)(M / 256) * (N / 256) * batch;
         if (big_tiles >= ch::num_cus() &&
             launch_pingpong<TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
+            return st;
+        // Fewer 128 x 128 tiles than a quarter of the CUs (config 1's 256^3
+        // is 4): 64 x 64 tiles put the product on 4x the CUs, and a 16-deep
+        // ring (128 KiB) holds 256 k at once, so a short product waits for
+        // its copies once instead of once per k-tile.
+        const int64_t tiles128 = (int64_t)(M / 128) * (N / 128) * batch;
+        if (tiles128 * 4 < ch::num_cus() &&
+            launch_tiled<64, 64, 16, 2, 2, 16, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
             return st;
         if (launch_tiled<128, 128, 16, 2, 2, 2, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
             return st;

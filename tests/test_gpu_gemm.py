@@ -69,6 +69,17 @@ def test_shapes_and_layouts(hip, oracle, M, N, K, ta, tb):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (192, 320, 48), (64, 64, 16), (64, 128, 1040)])
+def test_small_products_on_64_tiles(hip, oracle, M, N, K, ta, tb):
+    # Products with few 128 x 128 tiles run 64 x 64 tiles and a 16-deep ring
+    # (config 1's 256^3 among them); K = 1040 wraps the ring four times.
+    rng = np.random.default_rng(M * 7 + N * 3 + K + 10 * ta + tb)
+    A = rng.uniform(-1, 1, (K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (N, K) if tb else (K, N)).astype(np.float32)
+    _full_check(hip, oracle, A, B, ta, tb, f"{M}x{N}x{K} ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_config2_4096_cube_sampled_and_linearity(hip, oracle, ta, tb):
     n = 4096
     a = hip.fill_normal(hip.empty((n, n)), seed=11)
