@@ -263,7 +263,11 @@ bool launch_pairs(const uint16_t* a, const uint16_t* b, float* c, int M, int N, 
         if (!P::fits(M, N, K, lda, ldb) || ((uintptr_t)a & 15) || ((uintptr_t)b & 15)) return false;
         const int tiles_m = M / P::BM, tiles_n = N / P::BN;
         if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
-        dim3 grid((unsigned)(tiles_m * tiles_n * batch));
+        // one workgroup per CU (all of the LDS), each looping over its tiles;
+        // a multiple of 8 keeps every tile of a workgroup on one XCD
+        const int total = tiles_m * tiles_n * batch;
+        const int resident = ch::num_cus() / 8 * 8;
+        dim3 grid((unsigned)(total < resident ? total : resident));
         ch::gemm_bf16_pingpong_pairs_kernel<!TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
             a, b, c, M, N, K, lda, ldb, (int64_t)M * K, (int64_t)K * N, (int64_t)M * N, tiles_m, tiles_n, batch);
         *status = ch::check_hip(hipGetLastError(), "gemm_bf16_pingpong_pairs_kernel");

@@ -217,24 +217,32 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int grp = wave / P::WN, wn = wave % P::WN;
-    int bt, tm, tn;
-    ch::block_coords(blockIdx.x, tiles_m, tiles_n, batch, bt, tm, tn);
-    const int m0 = tm * P::BM, n0 = tn * P::BN;
-    A += (int64_t)bt * strideA;
-    B += (int64_t)bt * strideB;
-    C += (int64_t)bt * strideC;
     const uint32_t lds0 = lds_addr(smem);
     const int nk = K / BK, np = nk / 2;
 
-    // the paired (k-contiguous) operand and the single (m/n-contiguous) one
-    // (the paired tile's first row is in its 64-bit base, so the 32-bit lane
-    // offsets span 256 rows)
+    // The paired (k-contiguous) operand and the single one.  Each copy's
+    // 64-bit scalar base holds the tile's first row (paired operand; single
+    // operand when k-contiguous) or first column (single, m/n-contiguous),
+    // so the 32-bit lane offsets below are the same for every tile.
     const int64_t pld = AKC ? lda : ldb, sld = AKC ? ldb : lda;
-    const int pr0 = AKC ? m0 : n0, sr0 = AKC ? n0 : m0;
     constexpr bool SKC = P::SKC;
     using SCopy = TileCopy<SKC, 256, BK, NW>;
-    const char* pbase = reinterpret_cast<const char*>(AKC ? A : B) + (int64_t)pr0 * pld * 2;
-    const char* sbase = reinterpret_cast<const char*>(AKC ? B : A) + SCopy::base_offset(sld, sr0);
+    const char* pbase;
+    const char* sbase;
+    float* Ct;
+    int m0, n0;
+    auto set_tile = [&](int t) {
+        int bt, tm, tn;
+        ch::block_coords(t, tiles_m, tiles_n, batch, bt, tm, tn);
+        m0 = tm * P::BM;
+        n0 = tn * P::BN;
+        const int pr0 = AKC ? m0 : n0, sr0 = AKC ? n0 : m0;
+        const uint16_t* Ab = A + (int64_t)bt * strideA;
+        const uint16_t* Bb = B + (int64_t)bt * strideB;
+        pbase = reinterpret_cast<const char*>(AKC ? Ab : Bb) + (int64_t)pr0 * pld * 2;
+        sbase = reinterpret_cast<const char*>(AKC ? Bb : Ab) + (SKC ? (int64_t)sr0 * sld * 2 : (int64_t)sr0 * 2);
+        Ct = C + (int64_t)bt * strideC;
+    };
 
     // pair copy: instruction q = wave + 8 j moves rows 8q .. 8q+7; lane l takes
     // row 8q + l/8 and slot l%8, which holds chunk (l%8) ^ ((row >> 1) & 7)
@@ -247,7 +255,7 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
         pvoff[j] = (uint32_t)(((int64_t)r * pld + 8 * c) * 2);
     }
     SCopy scopy;
-    scopy.init(sld, sr0, wave, lane);
+    scopy.init(sld, 0, wave, lane);
     const uint32_t sstep = (uint32_t)scopy.kstep(sld);
     auto issue_pair = [&](auto stage, int p) {
         constexpr int PS = decltype(stage)::value;
@@ -288,10 +296,12 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
     }
 
     v4f acc[FM][FN];
+    auto zero_acc = [&]() {
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = v4f{};
+            for (int j = 0; j < FN; ++j) acc[i][j] = v4f{};
+    };
     v8bf fa[FM], fb[FN];
 
     // M phase of k-tile u (ST = u % 12): fragments, then the copies, then the wait.
@@ -328,15 +338,47 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
     };
     // Prologue in the steady state's order (pair 0, single 0, pair 1, single
     // 1, single 2): k-tile 0 has landed once 8 later instructions remain.
-    issue_pair(std::integral_constant<int, 0>{}, 0);
-    issue_single(std::integral_constant<int, 0>{}, 0);
-    issue_pair(std::integral_constant<int, 1>{}, 1);
-    issue_single(std::integral_constant<int, 1>{}, 1);
-    issue_single(std::integral_constant<int, 2>{}, 2);
-    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    pingpong_schedule<1, P::PERIOD>(nk, grp, [](int) {}, m_phase, c_phase, /*prologue_copies=*/false);
+    auto prologue = [&]() {
+        issue_pair(std::integral_constant<int, 0>{}, 0);
+        issue_single(std::integral_constant<int, 0>{}, 0);
+        issue_pair(std::integral_constant<int, 1>{}, 1);
+        issue_single(std::integral_constant<int, 1>{}, 1);
+        issue_single(std::integral_constant<int, 2>{}, 2);
+    };
 
-    store_acc16_lines(C, N, m0 + grp * P::TM, n0 + wn * P::TN, acc, lane);
+    // Tiles blockIdx.x, + gridDim.x, ...: a grid of fewer workgroups than
+    // tiles keeps each workgroup on its CU from one tile to the next.  Between
+    // tiles, the next tile's prologue copies go out before this tile's C
+    // stores, so their latency overlaps the stores' drain, and no workgroup
+    // is torn down and launched again.  (gridDim.x is a multiple of 8, so
+    // every tile of a workgroup falls to the XCD block_coords planned for it.)
+    const int total = tiles_m * tiles_n * batch;
+    int tile = blockIdx.x;
+    set_tile(tile);
+    zero_acc();
+    prologue();
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    auto next_tile = [&]() {
+        float* const Cdone = Ct;
+        const int r0 = m0 + grp * P::TM, c0 = n0 + wn * P::TN;
+        tile += (int)gridDim.x;
+        if (tile >= total) {
+            store_acc16_lines(Cdone, N, r0, c0, acc, lane);
+            return false;
+        }
+        // every wave's copies have landed (each waited for its own) before
+        // the ring takes the next tile
+        asm volatile("s_barrier" ::: "memory");
+        set_tile(tile);
+        prologue();
+        store_acc16_lines(Cdone, N, r0, c0, acc, lane);
+        zero_acc();
+        // everything but the last 8 stores has landed: the whole prologue,
+        // so k-tile 0 of the next tile (the next M phase waits for the rest)
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        return true;
+    };
+    pingpong_schedule_tiles<P::PERIOD>(nk, grp, m_phase, c_phase, next_tile);
 }
 
 }  // namespace ch

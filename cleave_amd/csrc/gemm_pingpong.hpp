@@ -110,4 +110,48 @@ __device__ __forceinline__ void pingpong_schedule(int nk, int grp, Issue&& issue
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// pingpong_schedule over a sequence of tiles, for a workgroup that stays on
+// its CU from one tile to the next.  The caller has put the first tile's
+// k-tile 0 in stage 0 and started the copies of its next tiles (as with
+// prologue_copies false).  After each tile's last phase every wave waits for
+// its copies (vmcnt(0)) and calls next_tile(), which returns false after the
+// last tile; otherwise it must leave the next tile in the state the first one
+// started in.  next_tile() may use barriers: both groups call it once per
+// tile.  The tile loop sits inside each group's branch, so neither group's
+// registers stay allocated through the other group's loop.
+template <int S, class MPhase, class CPhase, class NextTile>
+__device__ __forceinline__ void pingpong_schedule_tiles(int nk, int grp, MPhase&& m_phase, CPhase&& c_phase,
+                                                        NextTile&& next_tile) {
+    auto step0 = [&](auto next_stage, int s) {
+        c_phase(s);
+        asm volatile("s_barrier" ::: "memory");
+        if (s + 1 < nk) m_phase(next_stage, s + 1);
+        asm volatile("s_barrier" ::: "memory");
+    };
+    auto step1 = [&](auto stage, int s) {
+        m_phase(stage, s);
+        asm volatile("s_barrier" ::: "memory");
+        c_phase(s);
+        asm volatile("s_barrier" ::: "memory");
+    };
+    if (grp == 0) {
+        do {
+            asm volatile("s_barrier" ::: "memory");
+            m_phase(PingPongStage<0>{}, 0);
+            asm volatile("s_barrier" ::: "memory");
+            for (int s = 0; s < nk; s += S)
+                pingpong_unrolled<S, 1>(s, nk, step0, std::make_integer_sequence<int, S>{});
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        } while (next_tile());
+    } else {
+        do {
+            asm volatile("s_barrier" ::: "memory");
+            asm volatile("s_barrier" ::: "memory");
+            for (int s = 0; s < nk; s += S)
+                pingpong_unrolled<S, 0>(s, nk, step1, std::make_integer_sequence<int, S>{});
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        } while (next_tile());
+    }
+}
+
 }  // namespace ch
