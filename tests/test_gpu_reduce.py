@@ -98,3 +98,22 @@ def test_empty_inputs_are_rejected(hip):
         hip.sum(d)
     with pytest.raises(hip.CleaveHipError):
         hip.max_of(d)
+
+
+def test_one_launch_reductions_back_to_back(hip, oracle):
+    # Each reduction is one launch whose last block folds the partials and
+    # resets a completion counter for the next launch.  Interleave the three
+    # kinds over grids of 1 to thousands of blocks, several times, and check
+    # every result: a counter left non-zero would lose a result or fold early.
+    sizes = [1, (1 << 24) + 5, 3, 4096, (1 << 20) + 1, 1, (1 << 22) + 17]
+    rng = np.random.default_rng(77)
+    for rep in range(3):
+        for n in sizes:
+            x = rng.standard_normal(n).astype(np.float32)
+            c = rng.integers(0, 1 << 32, n, dtype=np.uint64).astype(np.uint32)
+            d, dc = hip.from_numpy(x), hip.from_numpy(c)
+            scale = float(np.sum(np.abs(x), dtype=np.float64))
+            assert abs(hip.sum(d) - oracle.sum_f32(x)) <= 1e-5 * scale, (rep, n)
+            assert hip.max_of(d) == oracle.max_of(x), (rep, n)
+            assert hip.argmax(d) == oracle.argmax(x), (rep, n)
+            assert hip.sum_u64(dc) == int(c.astype(np.uint64).sum()), (rep, n)
