@@ -172,11 +172,13 @@ def test_bf16_batched_tiled_every_entry(hip, oracle):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-@pytest.mark.parametrize("bsz,M,N,K", [(4, 256, 256, 128), (64, 512, 512, 512)])
+@pytest.mark.parametrize("bsz,M,N,K", [(4, 256, 256, 128), (64, 512, 512, 512), (80, 512, 512, 1024)])
 def test_bf16_batched_every_layout(hip, oracle, bsz, M, N, K, ta, tb):
     # The batched halves of the product rule (stdlib/linalg/matrix.cleave:24):
     # each batch entry stored K x M (trans_a) or N x K (trans_b).  4 x 256^2 runs
-    # the 128 x 128 tiled kernel; 64 x 512^3 (config 5) the 256 x 256 one.
+    # the 128 x 128 tiled kernel; 64 x 512^3 (config 5) the 256 x 256 one;
+    # 80 x 512^2 x 1024 (320 tiles) a ping-pong kernel, whose paired-copy form
+    # keeps 256 workgroups, 64 of them taking a tile of a second batch entry.
     # Three entries of each are checked in full against the oracle.
     a = hip.to_bf16(hip.fill_normal(hip.empty((bsz, K, M) if ta else (bsz, M, K)), seed=131 + 2 * ta + tb,
                                     std=0.02))
@@ -324,14 +326,16 @@ def test_f32_batched_through_pingpong(hip, oracle):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-def test_bf16_pingpong_every_entry(hip, oracle, ta, tb):
-    # Two rounds of 256 x 256 tiles go to a ping-pong kernel (the paired-copy
-    # one for A·B and Aᵀ·Bᵀ).  Its epilogue swaps 16-lane rows between
-    # accumulator blocks to store whole 128-byte rows; every entry of C is
-    # checked, since a value stored in the wrong column of its row would keep
-    # the row sums the sampled tests also check.
-    M, N, K = 4096, 8192, 128
-    rng = np.random.default_rng(40 + 2 * ta + tb)
+@pytest.mark.parametrize("M,N,K", [(4096, 8192, 128), (3840, 5120, 128)])
+def test_bf16_pingpong_every_entry(hip, oracle, M, N, K, ta, tb):
+    # Two rounds of 256 x 256 tiles (512, or 300: 44 workgroups of 256 take a
+    # second tile) go to a ping-pong kernel (the paired-copy one, which keeps
+    # one workgroup per CU looping over its tiles, for A·B, A·Bᵀ and Aᵀ·Bᵀ).
+    # Its epilogue swaps 16-lane rows between accumulator blocks to store
+    # whole 128-byte rows; every entry of C is checked, since a value stored
+    # in the wrong column of its row would keep the row sums the sampled
+    # tests also check.
+    rng = np.random.default_rng(40 + 2 * ta + tb + M)
     A = oracle.to_bf16(rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32))
     B = oracle.to_bf16(rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32))
     got = hip.matmul(hip.from_numpy(A, "bf16"), hip.from_numpy(B, "bf16"), trans_a=bool(ta),
