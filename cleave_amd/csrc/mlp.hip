@@ -184,7 +184,16 @@ __global__ __launch_bounds__(kThreads) void loss_kernel(const float* __restrict_
                                                         float* __restrict__ loss) {
     __shared__ float part[kThreads / 64];
     float acc = 0.0f;
-    for (int i = threadIdx.x; i < n; i += kThreads) acc += v[i];
+    // v[t], v[t + 256], ... in that order, kPartUnroll loads in flight
+    int i = threadIdx.x;
+    for (; i + (kPartUnroll - 1) * kThreads < n; i += kPartUnroll * kThreads) {
+        float w[kPartUnroll];
+#pragma unroll
+        for (int u = 0; u < kPartUnroll; ++u) w[u] = v[i + u * kThreads];
+#pragma unroll
+        for (int u = 0; u < kPartUnroll; ++u) acc += w[u];
+    }
+    for (; i < n; i += kThreads) acc += v[i];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
