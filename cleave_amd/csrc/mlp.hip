@@ -150,7 +150,15 @@ __global__ __launch_bounds__(kThreads) void sum_slices_sgd_kernel(const float* _
                                                                   float* __restrict__ w, float lr) {
     for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
         float g = part[i];
-        for (int s = 1; s < slices; ++s) g += part[(int64_t)s * n + i];
+        int s = 1;
+        for (; s + kPartUnroll <= slices; s += kPartUnroll) {  // kPartUnroll loads in flight, same order
+            float v[kPartUnroll];
+#pragma unroll
+            for (int u = 0; u < kPartUnroll; ++u) v[u] = part[(int64_t)(s + u) * n + i];
+#pragma unroll
+            for (int u = 0; u < kPartUnroll; ++u) g += v[u];
+        }
+        for (; s < slices; ++s) g += part[(int64_t)s * n + i];
         if (dw) dw[i] = g;
         if (lr != 0.0f) w[i] = w[i] - lr * g;
     }
