@@ -504,9 +504,10 @@ def main():
         secondary["gemm_f32_256"] = {"GFLOP/s": round(fl1 * 200 / wall_s / 1e9, 1), "kernel_ms": round(ev, 5),
                                      "kernel_GFLOP/s": round(fl1 / (ev * 1e-3) / 1e9, 1),
                                      "frac_fp32_mfma": round(fl1 / (ev * 1e-3) / 1e12 / PEAK_FP32_MFMA, 4),
-                                     "note": "latency-bound: one 256^3 product is 16 tiles of 64 x 64 on 16 "
-                                             "CUs, each 128 serial fp32 MFMAs per wave after one copy wait; "
-                                             "wall GFLOP/s includes the host call per step"}
+                                     "note": "latency-bound: one 256^3 product is 64 tiles of 32 x 32, one per "
+                                             "workgroup, K split over its 4 waves (32 fp32 MFMAs each after "
+                                             "one wait for all their loads); wall GFLOP/s includes the host "
+                                             "call per step"}
         log(f"gemm_f32_256: {fl1 / (ev * 1e-3) / 1e9:.0f} GFLOP/s kernel")
         if want_cpu:
             secondary["gemm_f32_256"]["cpu_baseline"] = cpu_secondary(orc, "gemm_f32_256", cb,

@@ -4,7 +4,8 @@
 // ping-pong kernel of gemm_f32_pingpong.hpp; shapes that divide a
 // 128 x 128 x 16 tile run the large-tile kernel of gemm_f32_tiled.hpp (LDS
 // filled by global_load_lds, four MFMA k-steps per 16-byte operand read);
-// small products that divide 64 x 64 x 16 run it with 64 x 64 tiles and a
+// small products run 32 x 32 tiles with K split over a workgroup's waves
+// (gemm_f32_small.hpp), or the large-tile kernel with 64 x 64 tiles and a
 // 16-deep ring.  Everything else runs the general kernel below.
 //
 // Replaces linalg.matmul as cleave lowers it (stdlib/linalg/matrix.cleave:27-61,
@@ -31,6 +32,7 @@
 #include "common.hpp"
 #include "gemm_common.hpp"
 #include "gemm_f32_pingpong.hpp"
+#include "gemm_f32_small.hpp"
 #include "gemm_f32_tiled.hpp"
 
 namespace {
@@ -244,6 +246,24 @@ bool launch_tiled(const float* a, const float* b, float* c, int M, int N, int K,
     return true;
 }
 
+// Small-product kernel (gemm_f32_small.hpp): 32 x 32 tiles, K split over
+// K/64 waves of the workgroup; false when the shape does not fit it.
+template <bool TA, bool TB>
+bool launch_small(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
+                  int64_t ldb, int batch, int64_t sA, int64_t sB, int64_t sC, int32_t* status) {
+    using P = ch::F32Small;
+    if (!P::fits(M, N, K, lda, ldb, !TA, TB)) return false;
+    if (!TA && (((uintptr_t)a & 15) || (sA % 4))) return false;  // 16-byte loads along k
+    if (TB && (((uintptr_t)b & 15) || (sB % 4))) return false;
+    const int tiles_m = M / P::TILE, tiles_n = N / P::TILE;
+    if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
+    dim3 grid((unsigned)(tiles_m * tiles_n * batch));
+    ch::gemm_f32_small_kernel<!TA, TB><<<grid, 64 * (K / P::KW), 0, ch::stream()>>>(
+        a, b, c, M, N, K, lda, ldb, sA, sB, sC, tiles_m, tiles_n, batch);
+    *status = ch::check_hip(hipGetLastError(), "gemm_f32_small_kernel");
+    return true;
+}
+
 // Ping-pong kernel (gemm_f32_pingpong.hpp) when the shape divides its
 // 256 x 256 x 16 tile; false when it does not.
 template <bool TA, bool TB>
@@ -272,10 +292,17 @@ int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, in
         if (big_tiles >= ch::num_cus() &&
             launch_pingpong<TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
             return st;
-        // Fewer 128 x 128 tiles than a quarter of the CUs (config 1's 256^3
-        // is 4): 64 x 64 tiles put the product on 4x the CUs, and a 16-deep
-        // ring (128 KiB) holds 256 k at once, so a short product waits for
-        // its copies once instead of once per k-tile.
+        // At most one 32 x 32 tile per CU with K <= 1024 (config 1's 256^3 is
+        // 64 tiles): a tile per workgroup, K split over its waves, 32 MFMAs
+        // per wave.
+        const int64_t tiles32 = (int64_t)(M / 32) * (N / 32) * batch;
+        if (tiles32 <= ch::num_cus() &&
+            launch_small<TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
+            return st;
+        // Fewer 128 x 128 tiles than a quarter of the CUs: 64 x 64 tiles put
+        // the product on 4x the CUs, and a 16-deep ring (128 KiB) holds 256 k
+        // at once, so a short product waits for its copies once instead of
+        // once per k-tile.
         const int64_t tiles128 = (int64_t)(M / 128) * (N / 128) * batch;
         if (tiles128 * 4 < ch::num_cus() &&
             launch_tiled<64, 64, 16, 2, 2, 16, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))

@@ -69,10 +69,14 @@ def test_shapes_and_layouts(hip, oracle, M, N, K, ta, tb):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (192, 320, 48), (64, 64, 16), (64, 128, 1040)])
-def test_small_products_on_64_tiles(hip, oracle, M, N, K, ta, tb):
-    # Products with few 128 x 128 tiles run 64 x 64 tiles and a 16-deep ring
-    # (config 1's 256^3 among them); K = 1040 wraps the ring four times.
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (32, 32, 64), (96, 160, 320), (512, 512, 1024),
+                                   (192, 320, 48), (64, 64, 16), (64, 128, 1040)])
+def test_small_products(hip, oracle, M, N, K, ta, tb):
+    # Products with at most one 32 x 32 tile per CU and K a multiple of 64 up
+    # to 1024 run one tile per workgroup with K split over K/64 waves (config
+    # 1's 256^3: 64 tiles, 4 waves; 512^2 x 1024: 16 waves); the others with
+    # few 128 x 128 tiles run 64 x 64 tiles and a 16-deep ring, which K = 1040
+    # wraps four times.
     rng = np.random.default_rng(M * 7 + N * 3 + K + 10 * ta + tb)
     A = rng.uniform(-1, 1, (K, M) if ta else (M, K)).astype(np.float32)
     B = rng.uniform(-1, 1, (N, K) if tb else (K, N)).astype(np.float32)
@@ -110,6 +114,21 @@ def test_deterministic(hip):
     c1 = hip.matmul(a, b).numpy()
     c2 = hip.matmul(a, b).numpy()
     assert np.array_equal(c1, c2)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_batched_f32_small_products(hip, oracle, ta, tb):
+    # 6 products of 64 x 96 x 192: 36 tiles of 32 x 32 over the batch, K split
+    # over 3 waves; every entry of every product against the oracle.
+    bsz, M, N, K = 6, 64, 96, 192
+    rng = np.random.default_rng(90 + 2 * ta + tb)
+    A = rng.uniform(-1, 1, (bsz, K, M) if ta else (bsz, M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (bsz, N, K) if tb else (bsz, K, N)).astype(np.float32)
+    got = hip.matmul_batched(hip.from_numpy(A), hip.from_numpy(B), trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    for i in range(bsz):
+        ref = oracle.matmul(A[i], B[i], trans_a=bool(ta), trans_b=bool(tb))
+        den = np.abs(A[i].T if ta else A[i]).astype(np.float64) @ np.abs(B[i].T if tb else B[i]).astype(np.float64)
+        assert_gemm_close(got[i], ref, den, K, f"batched small f32 ta={ta} tb={tb} #{i}")
 
 
 def test_batched_f32(hip, oracle):
