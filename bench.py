@@ -37,7 +37,7 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense FP32 matrix
 PEAK_BF16_MFMA = 2516.6  # TFLOP/s, MI355X dense BF16 matrix
-MANDEL_VALU_PER_ITER = 9  # 8 arithmetic + the escape compare, per iteration of the escape-count kernel
+MANDEL_VALU_PER_ITER = 8  # 7 arithmetic (2p + ci as one exact fma) + the escape compare, per iteration
 PEAK_FP32_VALU_NOFMA = 78.6  # T op/s: MI355X FP32 vector peak 157.3 TFLOP/s counts an FMA as 2; one non-FMA op per lane-cycle is half
 PEAK_HBM = 8000.0  # GB/s
 HEADLINE_WARM_S = 0.4  # seconds of sustained load before the headline's timed steps
@@ -601,9 +601,9 @@ def main():
         # max_iter for pixels that never escape: a lower bound of the executed work
         total = ca.sum_u64(cnt)
         # The reference's iteration is 11 FLOP; the kernel executes it in
-        # MANDEL_VALU_PER_ITER VALU instructions (two products are reused and
-        # zr*zi + zi*zr is p + p, both exact), so the ceiling is the VALU issue
-        # rate over that count.
+        # MANDEL_VALU_PER_ITER VALU instructions (two products are reused,
+        # zr*zi + zi*zr is p + p, and (p + p) + ci is one fma: all exact), so the
+        # ceiling is the VALU issue rate over that count.
         rate = total / (ev * 1e-3)
         secondary["mandelbrot_16384_1000"] = {
             "ms": round(ev, 3), "pixel_iter_per_s": round(rate, 1),

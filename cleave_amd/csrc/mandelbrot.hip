@@ -10,9 +10,15 @@
 // of its lanes have escaped, which returns the same n.
 //
 // Bit-exactness: the library is compiled with -ffp-contract=off, so no mul+add
-// is fused.  Two rewrites are exact and save work: the zr*zr and zi*zi of the
-// |z|^2 test are the same rounded products the next step's re needs, and
-// zr*zi + zi*zr == 2*(zr*zi) exactly (same rounded product added to itself).
+// is fused behind the code's back.  Three rewrites are exact and save work:
+//   * the zr*zr and zi*zi of the |z|^2 test are the same rounded products the
+//     next step's re needs;
+//   * zr*zi + zi*zr == p + p with p = fl(zr*zi) (the same rounded product
+//     added to itself), and p + p == 2p exactly;
+//   * so im + ci = fl(fl(2p) + ci) = fl(2p + ci) = fma(2, p, ci): 2p is exact
+//     in binary floating point (subnormals included), so the fma's single
+//     rounding is the two-step sum's second one.  Where 2p overflows, |ci|
+//     is far below half an ulp of FLT_MAX and both forms give the same inf.
 //
 // Mapping: one wave per 8 x 8 pixel block (neighbouring pixels have similar
 // iteration counts, so waves diverge less than with 64 x 1 strips); a
@@ -26,14 +32,15 @@ namespace {
 // kept as a wave mask (the escape compare writes a mask, a scalar AND narrows
 // it).  A lane whose first escape is iteration n gets count n, and one that
 // never escapes gets max_iter (the reference's `escaped`/`count` latch,
-// examples/mandelbrot.cleave:14-26).  Per iteration: 8 arithmetic ops and a
+// examples/mandelbrot.cleave:14-26).  Per iteration: 7 arithmetic ops and a
 // compare on the VALU, one scalar AND -- no branch, no count update.  Only in
 // a block where some lane escapes are the escaping lanes' counts formed, from
 // the block's masks: n = the block's first iteration + the number of the
 // block's masks that still hold the lane.  The wave leaves once no lane is
-// alive.  At 16384^2 x 1000 blocks of 8 measured 6.10 ms, blocks of 16
-// 6.28 ms, and a count added every iteration 6.69 ms; on another box blocks
-// of 4, 6, 8 and 12 measured 6.40, 6.19, 6.12 and 6.21 ms.
+// alive.  With 9 VALU per iteration (before 2p + ci became one fma), at
+// 16384^2 x 1000 blocks of 8 measured 6.10 ms, blocks of 16 6.28 ms, and a
+// count added every iteration 6.69 ms; on another box blocks of 4, 6, 8 and
+// 12 measured 6.40, 6.19, 6.12 and 6.21 ms.  The fma form: 5.61 ms.
 constexpr int kBlockIters = 8;
 
 // count + 1 in the lanes set in `lanes` (a wave lane mask), as one
@@ -76,9 +83,8 @@ __global__ __launch_bounds__(256) void mandelbrot_kernel(uint32_t* __restrict__ 
         for (int u = 0; u < kBlockIters; ++u) {
             const float p = zr * zi;
             const float re = zr2 - zi2;
-            const float im = p + p;
             zr = re + cr;
-            zi = im + ci;
+            zi = __builtin_fmaf(2.0f, p, ci);  // (p + p) + ci, exactly
             zr2 = zr * zr;
             zi2 = zi * zi;
             alive &= __builtin_amdgcn_ballot_w64(!(zr2 + zi2 > 4.0f));
@@ -98,9 +104,8 @@ __global__ __launch_bounds__(256) void mandelbrot_kernel(uint32_t* __restrict__ 
         const uint64_t before = alive;
         const float p = zr * zi;
         const float re = zr2 - zi2;
-        const float im = p + p;
         zr = re + cr;
-        zi = im + ci;
+        zi = __builtin_fmaf(2.0f, p, ci);
         zr2 = zr * zr;
         zi2 = zi * zi;
         alive &= __builtin_amdgcn_ballot_w64(!(zr2 + zi2 > 4.0f));
