@@ -170,12 +170,15 @@ namespace ch {
 // XOR spreads the 8 row pairs over the 8 slots, so the quarter covers all
 // 256 bytes of the banks once.
 //
-// Copy schedule, per M phase u: the pair u/2 + 2 (at even u, 4 instructions
-// per wave) and then the single k-tile u + 3 (2 per wave), both clamped to
-// the last one.  This wave's copies of k-tile u + 1 were issued at M(u - 2)
-// or earlier, and exactly 8 instructions follow them: M(u - 1) and M(u)
-// issue 2 single instructions each and one of them, being even, a pair.  So
-// every M phase ends in s_waitcnt vmcnt(8).
+// Copy schedule, per M phase u: half u % 2 of the pair u/2 + 2 (2
+// instructions per wave: even u the first, odd u the second) and then the
+// single k-tile u + 3 (2 per wave), both clamped to the last one, so every M
+// phase issues the same 4 (issuing a whole pair at even u made the even
+// phases' copy bursts 3x the odd ones').  This wave's copies of k-tile u + 1
+// were issued at M(u - 2) or earlier, and exactly 8 instructions follow
+// them: those of M(u - 1) and M(u).  So every M phase ends in s_waitcnt
+// vmcnt(8).  M(0) would need vmcnt(6), so the prologue instead waits until
+// k-tiles 0 and 1 have both landed.
 // A·Bᵀ, whose operands are both k-contiguous, pairs A and keeps B as the
 // single operand, copied as 64-byte row segments into k-contiguous single
 // stages: two pair rings would not fit 160 KiB with copies issued far
@@ -257,12 +260,17 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
     SCopy scopy;
     scopy.init(sld, 0, wave, lane);
     const uint32_t sstep = (uint32_t)scopy.kstep(sld);
-    auto issue_pair = [&](auto stage, int p) {
-        constexpr int PS = decltype(stage)::value;
+    // half h of pair p: instructions j = 2h, 2h + 1 (rows 8q .. 8q+7, q = wave + 8j)
+    auto issue_pair_half = [&](auto stage, auto half, int p) {
+        constexpr int PS = decltype(stage)::value, HF = decltype(half)::value;
         const char* src = pbase + (uint32_t)min(p, np - 1) * (uint32_t)(2 * BK * 2);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 2 * HF; j < 2 * HF + 2; ++j)
             dma16(src, pvoff[j], lds0 + (uint32_t)(PS * P::PAIR_BYTES + 1024 * (wave + NW * j)));
+    };
+    auto issue_pair = [&](auto stage, int p) {
+        issue_pair_half(stage, std::integral_constant<int, 0>{}, p);
+        issue_pair_half(stage, std::integral_constant<int, 1>{}, p);
     };
     auto issue_single = [&](auto stage, int kt) {
         constexpr int SS = decltype(stage)::value;
@@ -323,7 +331,8 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
             if constexpr (AKC) fb[f] = v;
             else fa[f] = v;
         }
-        if constexpr (H == 0) issue_pair(std::integral_constant<int, (ST / 2 + 2) % PAIRS>{}, u / 2 + 2);
+        issue_pair_half(std::integral_constant<int, (ST / 2 + 2) % PAIRS>{}, std::integral_constant<int, H>{},
+                        u / 2 + 2);
         issue_single(std::integral_constant<int, (ST + 3) % SINGLES>{}, u + 3);
         asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
     };
@@ -336,8 +345,8 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
         __builtin_amdgcn_s_setprio(0);
     };
-    // Prologue in the steady state's order (pair 0, single 0, pair 1, single
-    // 1, single 2): k-tile 0 has landed once 8 later instructions remain.
+    // Prologue: pair 0, single 0, pair 1, single 1, single 2; k-tiles 0 and 1
+    // have landed once only single 2's 2 instructions remain.
     auto prologue = [&]() {
         issue_pair(std::integral_constant<int, 0>{}, 0);
         issue_single(std::integral_constant<int, 0>{}, 0);
@@ -357,7 +366,7 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
     set_tile(tile);
     zero_acc();
     prologue();
-    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
     auto next_tile = [&]() {
         float* const Cdone = Ct;
         const int r0 = m0 + grp * P::TM, c0 = n0 + wn * P::TN;
