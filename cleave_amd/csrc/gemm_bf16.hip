@@ -266,7 +266,8 @@ bool launch_pairs(const uint16_t* a, const uint16_t* b, float* c, int M, int N, 
         // one workgroup per CU (all of the LDS), each looping over its tiles;
         // a multiple of 8 keeps every tile of a workgroup on one XCD
         const int total = tiles_m * tiles_n * batch;
-        const int resident = ch::num_cus() / 8 * 8;
+        const int cus = ch::num_cus();
+        const int resident = cus >= 8 ? cus / 8 * 8 : (cus > 0 ? cus : 1);
         dim3 grid((unsigned)(total < resident ? total : resident));
         ch::gemm_bf16_pingpong_pairs_kernel<!TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
             a, b, c, M, N, K, lda, ldb, (int64_t)M * K, (int64_t)K * N, (int64_t)M * N, tiles_m, tiles_n, batch);
