@@ -441,16 +441,25 @@ float or_mlp_step_f32(const float* X, const float* y, float* W1, float* W2, int3
             h[n] = g * h[n] * (1.0f - h[n]);
         }
     }
+    /* Blocks of 32 rows of dW1 per task, m outermost inside a block: every
+       entry dW1[k][n] is still its m-ascending chain of unfused mul/add, but
+       a block's 32 rows stay in cache while the d1 rows stream past once per
+       block (one k at a time re-read all of d1 for every k). */
+    const int32_t KB = 32;
 #ifdef _OPENMP
 #pragma omp parallel for schedule(static) num_threads(threads)
 #endif
-    for (int32_t k = 0; k < D; ++k) {
-        float* dw = &dW1[(int64_t)k * Hd];
-        for (int32_t n = 0; n < Hd; ++n) dw[n] = 0.0f;
+    for (int32_t kb = 0; kb < D; kb += KB) {
+        const int32_t ke = kb + KB < D ? kb + KB : D;
+        for (int32_t k = kb; k < ke; ++k)
+            for (int32_t n = 0; n < Hd; ++n) dW1[(int64_t)k * Hd + n] = 0.0f;
         for (int32_t m = 0; m < B; ++m) {
-            float x = X[(int64_t)m * D + k];
             const float* d1 = &H[(int64_t)m * Hd];
-            for (int32_t n = 0; n < Hd; ++n) dw[n] = dw[n] + x * d1[n];
+            for (int32_t k = kb; k < ke; ++k) {
+                float x = X[(int64_t)m * D + k];
+                float* dw = &dW1[(int64_t)k * Hd];
+                for (int32_t n = 0; n < Hd; ++n) dw[n] = dw[n] + x * d1[n];
+            }
         }
     }
     if (lr != 0.0f) {

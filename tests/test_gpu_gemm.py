@@ -107,6 +107,26 @@ def test_config2_4096_cube_sampled_and_linearity(hip, oracle, ta, tb):
     assert np.max(np.abs(C.astype(np.float64).sum(axis=0) - cols) / cden) <= 1e-5 * np.sqrt(n)
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+def test_config2_4096_cube_every_entry(hip, oracle, ta, tb):
+    # Config 2 in full: every entry of the 4096^3 product (A·B, A·Bᵀ, Aᵀ·B)
+    # against the reference loop.  The oracle's A·Bᵀ loop, whose operands are
+    # both k-contiguous, runs several times faster than its A·B loop and gives
+    # the same bits -- each entry is the same k-ascending chain of unfused
+    # mul/add however the operands are stored (test_oracle.py pins that) --
+    # so the reference for every layout runs on k-contiguous copies.
+    n = 4096
+    a = hip.fill_normal(hip.empty((n, n)), seed=61 + 2 * ta + tb)
+    b = hip.fill_normal(hip.empty((n, n)), seed=71 + 2 * ta + tb)
+    c = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    A, B = a.numpy(), b.numpy()
+    Ak = np.ascontiguousarray(A.T) if ta else A  # M x K
+    Bk = B if tb else np.ascontiguousarray(B.T)  # N x K
+    ref = oracle.matmul(Ak, Bk, trans_b=True, threads=16)
+    den = np.abs(Ak).astype(np.float64) @ np.abs(Bk).astype(np.float64).T
+    assert_gemm_close(c, ref, den, n, f"4096^3 every entry ta={ta} tb={tb}")
+
+
 def test_deterministic(hip):
     n = 1024
     a = hip.fill_normal(hip.empty((n, n)), seed=3)
@@ -248,6 +268,16 @@ def test_config5_bf16_8192_cube(hip, oracle):
     rows = Ad @ Bd.sum(axis=1)
     den = np.abs(Ad) @ np.abs(Bd).sum(axis=1)
     assert np.max(np.abs(C.astype(np.float64).sum(axis=1) - rows) / den) <= 1e-5 * np.sqrt(n)
+    del Ad, Bd
+    # Every entry: the oracle's f32 loop on the upcast values, run as its
+    # k-contiguous (A·Bᵀ) loop on a transposed copy of B, which gives the same
+    # bits as its A·B loop (pinned in test_oracle.py) several times faster.
+    Au = oracle.bf16_to_f32(A).reshape(n, n)
+    Bt = np.ascontiguousarray(oracle.bf16_to_f32(B).reshape(n, n).T)
+    full = oracle.matmul(Au, Bt, trans_b=True, threads=16)
+    den = np.abs(Au) @ np.abs(Bt).T  # f32 is ample for a tolerance's scale
+    assert_gemm_close(C, full, den, n, "bf16 8192^3 every entry")
+    assert np.all(np.abs(C - full) <= 1e-2 * np.abs(full) + 1e-2 * den / np.sqrt(n))
 
 
 def test_config5_batched_bf16_64x512(hip, oracle):

@@ -121,6 +121,45 @@ def test_xor_tensor_record_through_gpu_primitives(hip, golden):
     assert np.allclose(preds, g["predictions"], atol=2e-6, rtol=0), preds
 
 
+def test_config4_full_size_step_every_entry(hip, oracle):
+    # BASELINE config 4 at full size, every gradient entry: the oracle's whole
+    # step (or_mlp_step_f32 on 16 threads; its dW1 loop is blocked over rows
+    # of dW1 but keeps every entry's m-ascending order) against the device's,
+    # each of the 4M dW1 and 4096 dW2 entries within the GEMM bound of its
+    # K = 65536 contraction, the loss within rel 1e-5, and both updated weights.
+    B, D, Hd, lr = 65536, 1024, 4096, 0.01
+    rng = np.random.default_rng(7)
+    x = hip.fill_normal(hip.empty((B, D)), seed=71)
+    yv = hip.fill_bernoulli(hip.empty(B), seed=72)
+    W1 = _xavier(rng, D, Hd, (D, Hd))
+    W2 = _xavier(rng, Hd, 1, Hd)
+    w1, w2 = hip.from_numpy(W1), hip.from_numpy(W2)
+    dw1, dw2, loss = hip.empty((D, Hd)), hip.empty(Hd), hip.empty(1)
+    hip.mlp_step(x, yv, w1, w2, lr, dw1=dw1, dw2=dw2, loss=loss)
+    X, y = x.numpy(), yv.numpy()
+    L, g1, g2, W1n, W2n = oracle.mlp_step(X, y, W1, W2, lr, threads=16)
+    assert abs(float(loss.numpy()[0]) - L) <= 1e-5 * L
+    # the bound's scale: |X|^T |d1| and |H|^T |d2|, from an f32 forward pass
+    # (ample for a tolerance's scale)
+    H = 1.0 / (1.0 + np.exp(-(X @ W1)))
+    yh = 1.0 / (1.0 + np.exp(-(H @ W2)))
+    d2 = np.abs((2.0 / B) * (yh - y) * yh * (1.0 - yh)).astype(np.float32)
+    a1 = np.abs(X).T @ (np.abs(W2)[None, :] * (H * (1.0 - H)) * d2[:, None])
+    a2 = np.abs(H).T @ d2
+    del H
+    tol = 1e-5 * np.sqrt(B)
+    got1, got2 = dw1.numpy(), dw2.numpy()
+    e1 = np.abs(got1.astype(np.float64) - g1) / np.maximum(a1, 1e-30)
+    e2 = np.abs(got2.astype(np.float64) - g2) / np.maximum(a2, 1e-30)
+    assert e1.max() <= tol, f"dW1 normalised error {e1.max():.3e} > {tol:.3e}"
+    assert e2.max() <= tol, f"dW2 normalised error {e2.max():.3e} > {tol:.3e}"
+    # the SGD updates: W - lr * g in f32 on the device's gradients, within the
+    # gradients' bound of the oracle's updated weights
+    assert np.array_equal(w1.numpy(), W1 - np.float32(lr) * got1)
+    assert np.array_equal(w2.numpy(), W2 - np.float32(lr) * got2)
+    assert np.all(np.abs(w1.numpy().astype(np.float64) - W1n) <= lr * tol * a1 + 2.5e-7 * np.abs(W1n))
+
+
 def test_config4_full_size_step(hip, oracle):
     # BASELINE config 4 at full size.  Loss and 2 x 384 sampled gradient
     # entries against the oracle's sequential restatement (or_mlp_grad_entries:
