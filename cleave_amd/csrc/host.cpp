@@ -6,19 +6,206 @@
 // cleave-rt/src/lib.rs:86-90).  These entry points accept exactly that: every
 // tensor operand is a borrowed, possibly pageable host array, valid only for
 // the call.  Each one
-//   1. copies its input arrays into a staging arena in HBM (hipMemcpyAsync on
-//      the library stream; the arena is library scratch, grown on demand and
-//      kept),
+//   1. copies its input arrays into a staging arena in HBM (on the library
+//      stream; the arena is library scratch, grown on demand and kept),
 //   2. runs the device entry point on the staged copies (same kernels, same
 //      argument checks, same error contract),
 //   3. copies its output arrays back and waits for the stream,
 // so on return every output array holds its result and every array may be
 // reused.  A failed call leaves the output arrays unwritten.
+//
+// Copies of more than 4 MiB go through two pinned bounce buffers of 16 MiB:
+// host threads copy one chunk between the pageable array and a bounce buffer
+// while the DMA engine moves the other one, so the pageable side is copied
+// (and its pages touched) by several cores at once instead of by the
+// runtime's one staging thread.  Smaller copies are one hipMemcpyAsync.
+#include <algorithm>
 #include <cmath>
+#include <condition_variable>
+#include <cstring>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+#include <unistd.h>
 
 #include "common.hpp"
 
 namespace {
+
+constexpr size_t kBounceBytes = size_t(16) << 20;
+constexpr size_t kDirectMax = size_t(4) << 20;
+constexpr size_t kCopySlice = size_t(2) << 20;  // least bytes per copying thread
+
+// Two pinned bounce buffers and the events that say when the DMA engine is
+// done with each; allocated on the first large copy and kept until the
+// process ends.
+struct Bounce {
+    char* buf[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    bool ready = false;
+};
+Bounce g_bounce;
+
+int32_t bounce_init() {
+    if (g_bounce.ready) return CLEAVE_HIP_OK;
+    for (int b = 0; b < 2; ++b) {
+        int32_t st = ch::check_hip(hipHostMalloc((void**)&g_bounce.buf[b], kBounceBytes, hipHostMallocDefault),
+                                   "hipHostMalloc (bounce buffer)");
+        if (st != CLEAVE_HIP_OK) return st;
+        st = ch::check_hip(hipEventCreateWithFlags(&g_bounce.done[b], hipEventDisableTiming),
+                           "hipEventCreateWithFlags (bounce buffer)");
+        if (st != CLEAVE_HIP_OK) return st;
+    }
+    g_bounce.ready = true;
+    return CLEAVE_HIP_OK;
+}
+
+// Worker threads for the bounce copies: up to 7 beside the caller, started
+// on the first large copy and stopped when the process ends.
+class CopyPool {
+  public:
+    ~CopyPool() {
+        if (!started_ || getpid() != pid_) {  // a forked child has no workers to join
+            for (auto& t : th_) t.detach();
+            return;
+        }
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            stop_ = true;
+        }
+        work_.notify_all();
+        for (auto& t : th_) t.join();
+    }
+    size_t workers() {
+        if (started_ && getpid() != pid_) return 0;  // forked child: copy on this thread
+        if (!started_) {
+            pid_ = getpid();
+            const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+            const unsigned n = std::min(7u, hw > 1 ? hw - 1 : 0u);
+            for (unsigned i = 0; i < n; ++i) th_.emplace_back([this] { run(); });
+            started_ = true;
+        }
+        return th_.size();
+    }
+    // memcpy of n bytes, split over the workers and the calling thread.
+    void copy(void* dst, const void* src, size_t n) {
+        const size_t parts = std::min<size_t>(workers() + 1, std::max<size_t>(1, n / kCopySlice));
+        if (parts <= 1) {
+            memcpy(dst, src, n);
+            return;
+        }
+        const size_t step = (n / parts + 63) & ~size_t(63);
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            for (size_t p = 1; p < parts; ++p) {
+                const size_t off = std::min(n, p * step), len = std::min(n, off + step) - off;
+                if (len) {
+                    tasks_.push_back(Task{(char*)dst + off, (const char*)src + off, len});
+                    ++pending_;
+                }
+            }
+        }
+        work_.notify_all();
+        memcpy(dst, src, std::min(step, n));
+        std::unique_lock<std::mutex> lk(mu_);
+        done_.wait(lk, [this] { return pending_ == 0; });
+    }
+
+  private:
+    struct Task {
+        char* dst;
+        const char* src;
+        size_t n;
+    };
+    void run() {
+        std::unique_lock<std::mutex> lk(mu_);
+        for (;;) {
+            work_.wait(lk, [this] { return stop_ || !tasks_.empty(); });
+            if (tasks_.empty()) return;  // stop_ and nothing left
+            const Task t = tasks_.back();
+            tasks_.pop_back();
+            lk.unlock();
+            memcpy(t.dst, t.src, t.n);
+            lk.lock();
+            if (--pending_ == 0) done_.notify_all();
+        }
+    }
+    std::vector<std::thread> th_;
+    std::vector<Task> tasks_;
+    std::mutex mu_;
+    std::condition_variable work_, done_;
+    size_t pending_ = 0;
+    bool stop_ = false, started_ = false;
+    pid_t pid_ = 0;
+};
+CopyPool g_pool;
+
+void parallel_copy(void* dst, const void* src, size_t n) { g_pool.copy(dst, src, n); }
+
+// host -> device on the library stream.  Returns when the host array may be
+// reused (every chunk is in a bounce buffer or already copied).
+int32_t to_device(void* dev, const void* host, size_t n) {
+    if (n <= kDirectMax)
+        return ch::check_hip(hipMemcpyAsync(dev, host, n, hipMemcpyHostToDevice, ch::stream()),
+                             "hipMemcpyAsync (host array to staging)");
+    int32_t st = bounce_init();
+    if (st != CLEAVE_HIP_OK) return st;
+    for (size_t off = 0, i = 0; off < n; off += kBounceBytes, ++i) {
+        const int b = (int)(i & 1);
+        const size_t len = std::min(kBounceBytes, n - off);
+        // the DMA of the chunk two back, out of this buffer, is done
+        st = ch::check_hip(hipEventSynchronize(g_bounce.done[b]), "hipEventSynchronize (bounce buffer)");
+        if (st != CLEAVE_HIP_OK) return st;
+        parallel_copy(g_bounce.buf[b], (const char*)host + off, len);
+        st = ch::check_hip(hipMemcpyAsync((char*)dev + off, g_bounce.buf[b], len, hipMemcpyHostToDevice, ch::stream()),
+                           "hipMemcpyAsync (bounce buffer to staging)");
+        if (st != CLEAVE_HIP_OK) return st;
+        st = ch::check_hip(hipEventRecord(g_bounce.done[b], ch::stream()), "hipEventRecord (bounce buffer)");
+        if (st != CLEAVE_HIP_OK) return st;
+    }
+    return CLEAVE_HIP_OK;
+}
+
+// device -> host, after everything already queued on the library stream.
+// Large copies have landed in the host array on return; small ones when the
+// stream is next synchronised.
+int32_t to_host(void* host, const void* dev, size_t n) {
+    if (n <= kDirectMax)
+        return ch::check_hip(hipMemcpyAsync(host, dev, n, hipMemcpyDeviceToHost, ch::stream()),
+                             "hipMemcpyAsync (staging to host array)");
+    int32_t st = bounce_init();
+    if (st != CLEAVE_HIP_OK) return st;
+    const size_t chunks = (n + kBounceBytes - 1) / kBounceBytes;
+    auto dma = [&](size_t i) {
+        const int b = (int)(i & 1);
+        const size_t off = i * kBounceBytes, len = std::min(kBounceBytes, n - off);
+        int32_t s2 = ch::check_hip(hipMemcpyAsync(g_bounce.buf[b], (const char*)dev + off, len, hipMemcpyDeviceToHost,
+                                                  ch::stream()),
+                                   "hipMemcpyAsync (staging to bounce buffer)");
+        if (s2 == CLEAVE_HIP_OK)
+            s2 = ch::check_hip(hipEventRecord(g_bounce.done[b], ch::stream()), "hipEventRecord (bounce buffer)");
+        return s2;
+    };
+    for (size_t i = 0; i < std::min<size_t>(2, chunks); ++i) {
+        // the buffer is free: no earlier copy of this call used it, and an
+        // earlier call finished with it before returning
+        st = dma(i);
+        if (st != CLEAVE_HIP_OK) return st;
+    }
+    for (size_t i = 0; i < chunks; ++i) {
+        const int b = (int)(i & 1);
+        const size_t off = i * kBounceBytes, len = std::min(kBounceBytes, n - off);
+        st = ch::check_hip(hipEventSynchronize(g_bounce.done[b]), "hipEventSynchronize (bounce buffer)");
+        if (st != CLEAVE_HIP_OK) return st;
+        parallel_copy((char*)host + off, g_bounce.buf[b], len);
+        if (i + 2 < chunks) {
+            st = dma(i + 2);
+            if (st != CLEAVE_HIP_OK) return st;
+        }
+    }
+    return CLEAVE_HIP_OK;
+}
 
 // Scratch slot of the staging arena (slots 0-5 belong to the reductions, the
 // MLP step and the column sums).
@@ -61,9 +248,7 @@ class Staged {
         for (int i = 0; i < n_; ++i) {
             const Arg& a = args_[i];
             if (a.in && a.len > 0) {
-                const int32_t st = ch::check_hip(hipMemcpyAsync(base_ + a.off, a.host, (size_t)a.len * a.esz,
-                                                                hipMemcpyHostToDevice, ch::stream()),
-                                                 "hipMemcpyAsync (host array to staging)");
+                const int32_t st = to_device(base_ + a.off, a.host, (size_t)a.len * a.esz);
                 if (st != CLEAVE_HIP_OK) return drain(st);
             }
         }
@@ -84,9 +269,7 @@ class Staged {
             for (int i = 0; i < n_; ++i) {
                 const Arg& a = args_[i];
                 if (a.out && a.len > 0) {
-                    st = ch::check_hip(hipMemcpyAsync(const_cast<void*>(a.host), base_ + a.off,
-                                                      (size_t)a.len * a.esz, hipMemcpyDeviceToHost, ch::stream()),
-                                       "hipMemcpyAsync (staging to host array)");
+                    st = to_host(const_cast<void*>(a.host), base_ + a.off, (size_t)a.len * a.esz);
                     if (st != CLEAVE_HIP_OK) break;
                 }
             }

@@ -291,11 +291,14 @@ def test_config5_batched_bf16_64x512(hip, oracle):
         ii, jj = sample_entries(n, n, 128, seed=i)
         ref, absden = oracle.matmul_entries(A[i], B[i], n, n, n, ii, jj, bf16=True)
         assert_gemm_close(C[i][ii, jj], ref, absden, n, f"batched bf16 #{i}")
-    # full check of one batch entry
-    Au = oracle.bf16_to_f32(A[5]).reshape(n, n)
-    Bu = oracle.bf16_to_f32(B[5]).reshape(n, n)
-    ref = oracle.matmul(Au, Bu, threads=16)
-    assert_gemm_close(C[5], ref, np.abs(Au).astype(np.float64) @ np.abs(Bu).astype(np.float64), n, "batch 5 full")
+    # every entry of every product (the oracle's k-contiguous loop on a
+    # transposed copy of B: the same bits as its A·B loop)
+    for i in range(bsz):
+        Au = oracle.bf16_to_f32(A[i]).reshape(n, n)
+        Bt = np.ascontiguousarray(oracle.bf16_to_f32(B[i]).reshape(n, n).T)
+        ref = oracle.matmul(Au, Bt, trans_b=True, threads=16)
+        den = np.abs(Au).astype(np.float64) @ np.abs(Bt).astype(np.float64).T
+        assert_gemm_close(C[i], ref, den, n, f"batch {i} every entry")
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])

@@ -165,6 +165,35 @@ def test_mlp_step_host(host, oracle):
     assert np.allclose(w1, W1r, rtol=1e-6, atol=1e-8) and np.allclose(w2, W2r, rtol=1e-6, atol=1e-8)
 
 
+def test_large_host_arrays_through_the_bounce_buffers(host, oracle):
+    # Copies above 4 MiB go through two pinned 16 MiB bounce buffers in
+    # chunks, host threads copying one while the DMA engine moves the other.
+    # Lengths with a ragged last chunk, an exact multiple of the chunk, several
+    # operands per call, in place (sgd_update), and an output-only array.
+    rng = np.random.default_rng(123)
+    n = (1 << 24) + 13  # 64 MiB + 52 B: five chunks, the last one short
+    a = rng.standard_normal(n, dtype=np.float32)
+    b = rng.standard_normal(n, dtype=np.float32)
+    assert np.array_equal(host.add(a, b), oracle.add(a, b))
+    assert np.array_equal(host.sub(a, b), oracle.sub(a, b))
+    s = host.sum(a)
+    assert abs(s - oracle.sum_f32(a)) <= 1e-5 * float(np.sum(np.abs(a), dtype=np.float64))
+    assert host.max_of(a) == oracle.max_of(a)
+    w = b.copy()
+    host.sgd_update(w, a, 0.01)
+    assert np.array_equal(w, b - np.float32(0.01) * a)
+    m = 2048  # 16 MiB operands: exactly one chunk each
+    A = rng.standard_normal((m, 256), dtype=np.float32)
+    B = rng.standard_normal((256, m), dtype=np.float32)
+    got = host.matmul(A, B)  # 16 MiB output
+    ref = oracle.matmul(A, B, threads=16)
+    assert_gemm_close(got, ref, _absden(A, B), 256, "host matmul with 16 MiB output")
+    w_, h_ = 4096, 4097  # 64 MiB of counts, output only
+    cnt = host.escape_counts(w_, h_, -2.0, -1.5, 3.0 / w_, 3.0 / h_, 64)
+    ref = oracle.mandelbrot(w_, h_, -2.0, -1.5, np.float32(3.0 / w_), np.float32(3.0 / h_), 64, threads=16)
+    assert np.array_equal(cnt.reshape(h_, w_), ref)
+
+
 def test_host_forms_take_empty_arrays(host):
     e = np.empty(0, np.float32)
     assert host.add(e, e).size == 0 and host.relu(e).size == 0
