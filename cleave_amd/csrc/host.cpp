@@ -12,7 +12,8 @@
 //      argument checks, same error contract),
 //   3. copies its output arrays back and waits for the stream,
 // so on return every output array holds its result and every array may be
-// reused.  A failed call leaves the output arrays unwritten.
+// reused.  A call whose device entry point fails (bad lengths, shapes or
+// flags, a launch error) leaves the output arrays unwritten.
 //
 // Copies of more than 4 MiB go through two pinned bounce buffers of 16 MiB:
 // host threads copy one chunk between the pageable array and a bounce buffer
