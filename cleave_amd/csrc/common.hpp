@@ -30,6 +30,9 @@ int32_t check_hip(hipError_t e, const char* what);
 // Scratch device memory owned by the library (grown on demand, never shrunk).
 // `slot` selects an independent buffer.
 void* scratch(int slot, size_t bytes);
+// Same buffer, but a failed allocation returns nullptr without recording an
+// error (for callers that have another way to do the work).
+void* scratch_try(int slot, size_t bytes);
 
 // Number of compute units (for grid sizing of persistent/strided kernels).
 int num_cus();

@@ -4,8 +4,9 @@
 // Shapes that divide a 256 x 256 x 32 tile run the ping-pong kernel of
 // gemm_bf16_pingpong.hpp; 128 x 128 x 64 tiles run the large-tile kernel of
 // gemm_bf16_tiled.hpp (LDS filled by global_load_lds,
-// transposing LDS reads for m/n-contiguous operands).  Everything else runs
-// the general kernel below, which guards every access.
+// transposing LDS reads for m/n-contiguous operands).  Large products of
+// other shapes run those kernels on zero-padded copies (gemm_pad.hpp); the
+// rest run the general kernel below, which guards every access.
 //
 // Same operator as gemm_f32.hip (linalg.matmul of stdlib/linalg/matrix.cleave:
 // 27-61) with bf16 operands; the reference is f32/f64 only, so this is an
@@ -21,6 +22,7 @@
 #include "gemm_bf16_pingpong.hpp"
 #include "gemm_bf16_tiled.hpp"
 #include "gemm_common.hpp"
+#include "gemm_pad.hpp"
 
 namespace {
 
@@ -276,9 +278,9 @@ bool launch_pairs(const uint16_t* a, const uint16_t* b, float* c, int M, int N, 
     }
 }
 
+// The aligned kernels; false when none takes the shape.
 template <bool TA, bool TB>
-int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch) {
-    int32_t st = CLEAVE_HIP_OK;
+bool launch_fast(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch, int32_t* st) {
     // 256 x 256 tiles, when that still gives every CU a tile: the ping-pong
     // kernel (k-tiles of 32), or the tiled kernel (k-tiles of 64).  With one
     // round of tiles and K up to 512 the two measured equal (64 x 512^3:
@@ -291,14 +293,39 @@ int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N,
     const int64_t big_tiles = (int64_t)(M / 256) * (N / 256) * batch;
     if (big_tiles >= ch::num_cus()) {
         const bool short_single_round = big_tiles <= ch::num_cus() && K <= 512;
-        if (!short_single_round && launch_pairs<TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
-        if (!short_single_round && launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
-        if (launch_tiled<256, 256, 64, 2, 4, 2, 16, TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
-        if (launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
+        if (!short_single_round && launch_pairs<TA, TB>(a, b, c, M, N, K, batch, st)) return true;
+        if (!short_single_round && launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, st)) return true;
+        if (launch_tiled<256, 256, 64, 2, 4, 2, 16, TA, TB>(a, b, c, M, N, K, batch, st)) return true;
+        if (launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, st)) return true;
     }
     // 128 x 128 x 64 tile, 4 waves of 64 x 64 in 32 x 32 x 16 MFMAs, three
     // LDS stages (96 KiB)
-    if (launch_tiled<128, 128, 64, 2, 2, 3, 32, TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
+    return launch_tiled<128, 128, 64, 2, 2, 3, 32, TA, TB>(a, b, c, M, N, K, batch, st);
+}
+
+// Products of at least this many flops (2 M N K per product) that no aligned
+// kernel takes run on zero-padded copies (gemm_pad.hpp); smaller ones run
+// the general kernel, one launch against the padded route's four (~12 us
+// together).  Measured crossing: ~115^3 (100^3 11.1 us general, 12.1 padded;
+// 127 x 129 x 131 14.1 against 12.0).
+constexpr double kPadMinFlops = 1u << 22;
+// 256 x 256 tiles (8192^3) 0.55 of peak; 128 x 128 tiles (8320^3) 0.31, one
+// workgroup per CU (96 KiB of LDS).
+constexpr ch::PadModel kPadModel{0.55, 0.31, true};
+
+template <bool TA, bool TB>
+int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch) {
+    int32_t st = CLEAVE_HIP_OK;
+    if (launch_fast<TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
+    if (2.0 * M * N * K * batch >= kPadMinFlops) {
+        const ch::PadPlan p = ch::pad_plan(M, N, K, batch, TA, TB, a, b, 2, ch::num_cus(), kPadModel);
+        auto gemm = [batch](const uint16_t* pa, const uint16_t* pb, float* pc, int Mp, int Np, int Kp) {
+            int32_t s = CLEAVE_HIP_OK;
+            if (launch_fast<TA, TB>(pa, pb, pc, Mp, Np, Kp, batch, &s)) return s;
+            return launch<TA, TB>(pa, pb, pc, Mp, Np, Kp, batch);
+        };
+        if (ch::run_padded(p, a, b, c, batch, TA, TB, gemm, &st)) return st;
+    }
     return launch<TA, TB>(a, b, c, M, N, K, batch);
 }
 

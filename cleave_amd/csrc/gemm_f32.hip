@@ -6,7 +6,8 @@
 // filled by global_load_lds, four MFMA k-steps per 16-byte operand read);
 // small products run 32 x 32 tiles with K split over a workgroup's waves
 // (gemm_f32_small.hpp), or the large-tile kernel with 64 x 64 tiles and a
-// 16-deep ring.  Everything else runs the general kernel below.
+// 16-deep ring.  Large products of other shapes run those kernels on
+// zero-padded copies (gemm_pad.hpp); the rest run the general kernel below.
 //
 // Replaces linalg.matmul as cleave lowers it (stdlib/linalg/matrix.cleave:27-61,
 // region cleave/src/mlir_lower.rs:2089-2120): C = 0; C[i,j] += A[i,k]*B[k,j].
@@ -34,6 +35,7 @@
 #include "gemm_f32_pingpong.hpp"
 #include "gemm_f32_small.hpp"
 #include "gemm_f32_tiled.hpp"
+#include "gemm_pad.hpp"
 
 namespace {
 
@@ -281,34 +283,67 @@ bool launch_pingpong(const float* a, const float* b, float* c, int M, int N, int
     return true;
 }
 
+// The aligned kernels; false when none takes the shape.
 template <bool TA, bool TB>
-int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
-               int64_t ldb, int64_t ldc, int batch, int64_t sA, int64_t sB, int64_t sC) {
-    int32_t st = CLEAVE_HIP_OK;
+bool launch_fast(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
+                 int64_t ldb, int64_t ldc, int batch, int64_t sA, int64_t sB, int64_t sC, int32_t* st) {
     if (ldc == N) {
         // 256 x 256 x 16 tile (ping-pong, 8 waves of 128 x 64) when it still
         // yields a tile per CU, else 128 x 128 x 16 (4 waves of 64 x 64).
         const int64_t big_tiles = (int64_t)(M / 256) * (N / 256) * batch;
         if (big_tiles >= ch::num_cus() &&
-            launch_pingpong<TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
-            return st;
+            launch_pingpong<TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
+            return true;
         // At most one 32 x 32 tile per CU with K <= 1024 (config 1's 256^3 is
         // 64 tiles): a tile per workgroup, K split over its waves, 32 MFMAs
         // per wave.
         const int64_t tiles32 = (int64_t)(M / 32) * (N / 32) * batch;
         if (tiles32 <= ch::num_cus() &&
-            launch_small<TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
-            return st;
+            launch_small<TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
+            return true;
         // Fewer 128 x 128 tiles than a quarter of the CUs: 64 x 64 tiles put
         // the product on 4x the CUs, and a 16-deep ring (128 KiB) holds 256 k
         // at once, so a short product waits for its copies once instead of
         // once per k-tile.
         const int64_t tiles128 = (int64_t)(M / 128) * (N / 128) * batch;
         if (tiles128 * 4 < ch::num_cus() &&
-            launch_tiled<64, 64, 16, 2, 2, 16, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
-            return st;
-        if (launch_tiled<128, 128, 16, 2, 2, 2, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
-            return st;
+            launch_tiled<64, 64, 16, 2, 2, 16, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
+            return true;
+        if (launch_tiled<128, 128, 16, 2, 2, 2, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
+            return true;
+    }
+    return false;
+}
+
+// Products of at least this many flops (2 M N K per product) that no aligned
+// kernel takes run on zero-padded copies (gemm_pad.hpp); smaller ones run
+// the general kernel, one launch against the padded route's four (~12 us
+// together).  Measured crossing: ~80^3 (64 x 64 x 63 10.2 us general, 12.4
+// padded; 100^3 15.9 against 12.5).
+constexpr double kPadMinFlops = 1u << 20;
+// 256 x 256 tiles (4096^3) 0.86 of peak, one workgroup per CU; 128 x 128
+// tiles (4224^3) 0.78, four workgroups per CU.  4097^3 measured 1.23 ms
+// padded to 4224^3, 1.83 ms padded to 4352^2 x 4160 (289 tiles of 256).
+constexpr ch::PadModel kPadModel{0.86, 0.78, false};
+
+template <bool TA, bool TB>
+int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
+               int64_t ldb, int64_t ldc, int batch, int64_t sA, int64_t sB, int64_t sC) {
+    int32_t st = CLEAVE_HIP_OK;
+    if (launch_fast<TA, TB>(a, b, c, M, N, K, lda, ldb, ldc, batch, sA, sB, sC, &st)) return st;
+    // whole packed products only (not the K-slices of a split product)
+    const bool packed = lda == (TA ? M : K) && ldb == (TB ? K : N) && ldc == N && sA == (int64_t)M * K &&
+                        sB == (int64_t)K * N && sC == (int64_t)M * N;
+    if (packed && 2.0 * M * N * K * batch >= kPadMinFlops) {
+        const ch::PadPlan p = ch::pad_plan(M, N, K, batch, TA, TB, a, b, 4, ch::num_cus(), kPadModel);
+        auto gemm = [batch](const float* pa, const float* pb, float* pc, int Mp, int Np, int Kp) {
+            const int64_t plda = TA ? Mp : Kp, pldb = TB ? Kp : Np;
+            const int64_t psA = (int64_t)Mp * Kp, psB = (int64_t)Kp * Np, psC = (int64_t)Mp * Np;
+            int32_t s = CLEAVE_HIP_OK;
+            if (launch_fast<TA, TB>(pa, pb, pc, Mp, Np, Kp, plda, pldb, Np, batch, psA, psB, psC, &s)) return s;
+            return launch_general<TA, TB>(pa, pb, pc, Mp, Np, Kp, plda, pldb, Np, batch, psA, psB, psC);
+        };
+        if (ch::run_padded(p, a, b, c, batch, TA, TB, gemm, &st)) return st;
     }
     return launch_general<TA, TB>(a, b, c, M, N, K, lda, ldb, ldc, batch, sA, sB, sC);
 }

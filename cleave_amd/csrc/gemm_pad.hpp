@@ -1,0 +1,188 @@
+// gemm_pad.hpp -- ragged GEMM shapes through the aligned kernels.
+//
+// The fast kernels want M and N multiples of their block tile, K a multiple
+// of their k-tile and 16-byte aligned rows.  A large product that misses
+// those runs on zero-padded copies instead: each operand that does not
+// already fit is copied, in the caller's layout, into a buffer whose extents
+// are rounded up (K to 64, M and N to 128 or 256) with zeros past the valid
+// region; the product is computed on the padded shape; and, when M or N was
+// rounded up, the valid M x N corner of the padded C is copied out.
+//
+// The zeros change no valid entry: a padded k adds 0 * 0 = +0 to a sum that
+// starts at +0 (x + (+0) == x for every x but -0, and a sum started at +0
+// never is -0), and padded rows or columns only feed entries of C that are
+// not copied out.
+#pragma once
+
+#include "common.hpp"
+
+namespace ch {
+
+struct PadPlan {
+    bool ok;         // the padded extents fit the kernels' int arguments
+    int M, N, K;     // valid shape
+    int Mp, Np, Kp;  // padded shape
+    bool copy_a, copy_b, crop_c;
+    size_t bytes_a, bytes_b, bytes_c;  // scratch bytes of each padded operand (0: used in place)
+};
+
+inline int64_t pad_up(int x, int q) { return ((int64_t)x + q - 1) / q * q; }
+
+// Measured throughput of the aligned kernels, as a fraction of peak; they
+// price the two paddings.
+struct PadModel {
+    double eff256;  // 256 x 256 tiles, one workgroup per CU
+    double eff128;  // 128 x 128 tiles
+    bool rounds128; // 128 x 128 tiles also run one workgroup per CU
+};
+
+// Padded shape: K to a multiple of 64; M and N to multiples of 128, or of 256
+// when that still gives every CU a 256 x 256 tile and is estimated faster.
+// Time ~ padded area / efficiency, and, where a CU holds one workgroup, / the
+// fill of the rounds of tiles (the last round may leave CUs idle; where a CU
+// holds several, a lone workgroup runs faster and this is not counted).  An
+// operand whose stored extents and alignment already match is used in place.
+inline PadPlan pad_plan(int M, int N, int K, int batch, bool ta, bool tb, const void* a, const void* b,
+                        int esz, int cus, const PadModel& model) {
+    PadPlan p{};
+    p.M = M, p.N = N, p.K = K;
+    const int64_t kp = pad_up(K, 64);
+    const int64_t m2 = pad_up(M, 256), n2 = pad_up(N, 256), m1 = pad_up(M, 128), n1 = pad_up(N, 128);
+    auto cost = [](double area, int64_t tiles, int64_t per_round, double eff) {
+        const int64_t rounds = (tiles + per_round - 1) / per_round;
+        return area / (eff * ((double)tiles / (double)(rounds * per_round)));
+    };
+    const int64_t t2 = (m2 / 256) * (n2 / 256) * batch, t1 = (m1 / 128) * (n1 / 128) * batch;
+    const int c = cus > 0 ? cus : 1;
+    const double c128 = model.rounds128 ? cost((double)m1 * n1, t1, c, model.eff128)
+                                        : (double)m1 * n1 / model.eff128;
+    const bool use256 = t2 >= c && cost((double)m2 * n2, t2, c, model.eff256) < c128;
+    const int64_t mp = use256 ? m2 : m1, np = use256 ? n2 : n1;
+    p.ok = mp <= INT32_MAX && np <= INT32_MAX && kp <= INT32_MAX;
+    if (!p.ok) return p;
+    p.Mp = (int)mp, p.Np = (int)np, p.Kp = (int)kp;
+    const bool a_al = ((uintptr_t)a & 15) == 0 && ((int64_t)(ta ? M : K) * esz) % 16 == 0;
+    const bool b_al = ((uintptr_t)b & 15) == 0 && ((int64_t)(tb ? K : N) * esz) % 16 == 0;
+    p.copy_a = !(p.Mp == M && p.Kp == K && a_al);
+    p.copy_b = !(p.Np == N && p.Kp == K && b_al);
+    p.crop_c = !(p.Mp == M && p.Np == N);
+    // round each buffer to 256 bytes so the next one stays aligned
+    auto r256 = [](size_t x) { return (x + 255) / 256 * 256; };
+    p.bytes_a = p.copy_a ? r256((size_t)batch * p.Mp * p.Kp * esz) : 0;
+    p.bytes_b = p.copy_b ? r256((size_t)batch * p.Kp * p.Np * esz) : 0;
+    p.bytes_c = p.crop_c ? r256((size_t)batch * p.Mp * p.Np * sizeof(float)) : 0;
+    return p;
+}
+
+// dst (batch matrices of rows_p x cols_p, row pitch cols_p) = src (batch
+// matrices of rows x cols, row pitch cols), zeros past row `rows` and
+// column `cols`.  One workgroup per destination row (grid-strided), each
+// thread 8 consecutive elements; cols_p % 8 == 0 and dst 16-byte aligned.
+// vec_src: src rows are 16-byte aligned, so whole chunks load as vectors.
+template <typename T>
+__global__ __launch_bounds__(256) void pad_copy_kernel(const T* __restrict__ src, T* __restrict__ dst, int rows,
+                                                       int cols, int rows_p, int cols_p, int64_t total_rows,
+                                                       bool vec_src) {
+    typedef T v8 __attribute__((ext_vector_type(8), aligned(16)));  // 16-byte alignment is all that is checked
+    for (int64_t rr = blockIdx.x; rr < total_rows; rr += gridDim.x) {
+        const int64_t bt = rr / rows_p;
+        const int r = (int)(rr - bt * rows_p);
+        const T* s = src + (bt * rows + r) * (int64_t)cols;
+        T* d = dst + rr * (int64_t)cols_p;
+        for (int c0 = threadIdx.x * 8; c0 < cols_p; c0 += 256 * 8) {
+            v8 v;
+            if (r < rows && c0 + 8 <= cols) {
+                if (vec_src) {
+                    v = *reinterpret_cast<const v8*>(s + c0);
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) v[t] = s[c0 + t];
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) v[t] = (r < rows && c0 + t < cols) ? s[c0 + t] : (T)0;
+            }
+            *reinterpret_cast<v8*>(d + c0) = v;
+        }
+    }
+}
+
+// dst (batch x M x N, pitch N) = the top-left M x N of each src matrix
+// (batch x Mp x Np, pitch Np); Np % 4 == 0 and src 16-byte aligned (for
+// T = float).
+template <typename T>
+__global__ __launch_bounds__(256) void crop_kernel(const T* __restrict__ src, T* __restrict__ dst, int M, int N,
+                                                   int Mp, int Np, int64_t total_rows, bool vec_dst) {
+    typedef T v4 __attribute__((ext_vector_type(4)));
+    for (int64_t rr = blockIdx.x; rr < total_rows; rr += gridDim.x) {
+        const int64_t bt = rr / M;
+        const int r = (int)(rr - bt * M);
+        const T* s = src + (bt * Mp + r) * (int64_t)Np;
+        T* d = dst + rr * (int64_t)N;
+        for (int c0 = threadIdx.x * 4; c0 < N; c0 += 256 * 4) {
+            const v4 v = *reinterpret_cast<const v4*>(s + c0);
+            if (vec_dst && c0 + 4 <= N) {
+                *reinterpret_cast<v4*>(d + c0) = v;
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    if (c0 + t < N) d[c0 + t] = v[t];
+            }
+        }
+    }
+}
+
+// Grid of the row-strided copy kernels: one workgroup per row, at most 64
+// per CU.
+inline unsigned pad_grid(int64_t total_rows, int cus) {
+    const int64_t cap = (int64_t)(cus > 0 ? cus : 1) * 64;
+    return (unsigned)(total_rows < cap ? total_rows : cap);
+}
+
+// Runs `gemm(a, b, c, Mp, Np, Kp)` (which must take the padded shape with
+// 16-byte aligned rows) on padded copies as `p` plans them, then crops C.
+// Returns false, launching nothing, when the scratch buffer cannot be had.
+template <typename T, typename Gemm>
+bool run_padded(const PadPlan& p, const T* a, const T* b, float* c, int batch, bool ta, bool tb, Gemm gemm,
+                int32_t* status) {
+    constexpr int kSlot = 7;
+    if (!p.ok) return false;
+    const size_t total = p.bytes_a + p.bytes_b + p.bytes_c;
+    char* base = (char*)scratch_try(kSlot, total ? total : 256);
+    if (!base) return false;
+    const int cus = num_cus();
+    const T* pa = a;
+    const T* pb = b;
+    float* pc = c;
+    if (p.copy_a) {
+        T* d = (T*)base;
+        const int rows = ta ? p.K : p.M, cols = ta ? p.M : p.K;
+        const int rows_p = ta ? p.Kp : p.Mp, cols_p = ta ? p.Mp : p.Kp;
+        const int64_t tr = (int64_t)batch * rows_p;
+        const bool vec = ((uintptr_t)a & 15) == 0 && ((int64_t)cols * sizeof(T)) % 16 == 0;
+        pad_copy_kernel<T><<<pad_grid(tr, cus), 256, 0, stream()>>>(a, d, rows, cols, rows_p, cols_p, tr, vec);
+        pa = d;
+    }
+    if (p.copy_b) {
+        T* d = (T*)(base + p.bytes_a);
+        const int rows = tb ? p.N : p.K, cols = tb ? p.K : p.N;
+        const int rows_p = tb ? p.Np : p.Kp, cols_p = tb ? p.Kp : p.Np;
+        const int64_t tr = (int64_t)batch * rows_p;
+        const bool vec = ((uintptr_t)b & 15) == 0 && ((int64_t)cols * sizeof(T)) % 16 == 0;
+        pad_copy_kernel<T><<<pad_grid(tr, cus), 256, 0, stream()>>>(b, d, rows, cols, rows_p, cols_p, tr, vec);
+        pb = d;
+    }
+    if (p.crop_c) pc = (float*)(base + p.bytes_a + p.bytes_b);
+    int32_t st = check_hip(hipGetLastError(), "pad_copy_kernel");
+    if (st == CLEAVE_HIP_OK) st = gemm(pa, pb, pc, p.Mp, p.Np, p.Kp);
+    if (st == CLEAVE_HIP_OK && p.crop_c) {
+        const int64_t tr = (int64_t)batch * p.M;
+        const bool vec = ((uintptr_t)c & 15) == 0 && p.N % 4 == 0;
+        crop_kernel<float><<<pad_grid(tr, cus), 256, 0, stream()>>>(pc, c, p.M, p.N, p.Mp, p.Np, tr, vec);
+        st = check_hip(hipGetLastError(), "crop_kernel");
+    }
+    *status = st;
+    return true;
+}
+
+}  // namespace ch

@@ -93,6 +93,12 @@ int32_t ensure_init() {
 }
 
 void* scratch(int slot, size_t bytes) {
+    void* p = scratch_try(slot, bytes);
+    if (!p) fail(CLEAVE_HIP_ERR_OOM, "scratch allocation of %zu bytes failed", bytes);
+    return p;
+}
+
+void* scratch_try(int slot, size_t bytes) {
     if (slot < 0 || slot >= 8) return nullptr;
     if (g.scratch_bytes[slot] >= bytes && g.scratch[slot]) return g.scratch[slot];
     if (g.scratch[slot]) {
@@ -105,7 +111,6 @@ void* scratch(int slot, size_t bytes) {
     void* p = nullptr;
     if (hipMalloc(&p, bytes) != hipSuccess) {
         (void)hipGetLastError();
-        fail(CLEAVE_HIP_ERR_OOM, "scratch allocation of %zu bytes failed", bytes);
         return nullptr;
     }
     g.scratch[slot] = p;

@@ -497,3 +497,108 @@ def test_misaligned_operand_views(hip, oracle, dtype, off, ta, tb):
     ref = oracle.matmul(Au, Bu, trans_a=bool(ta), trans_b=bool(tb))
     den = np.abs(Au.T if ta else Au).astype(np.float64) @ np.abs(Bu.T if tb else Bu).astype(np.float64)
     assert_gemm_close(got, ref, den, K, f"{dtype} view at +{off} ta={ta} tb={tb}")
+
+
+def _operands(oracle, dtype, M, N, K, ta, tb, seed, batch=None):
+    rng = np.random.default_rng(seed)
+    lead = () if batch is None else (batch,)
+    A32 = rng.standard_normal(lead + ((K, M) if ta else (M, K))).astype(np.float32)
+    B32 = rng.standard_normal(lead + ((N, K) if tb else (K, N))).astype(np.float32)
+    if dtype == "bf16":
+        A, B = oracle.to_bf16(A32), oracle.to_bf16(B32)
+        return A, B, oracle.bf16_to_f32(A).reshape(A.shape), oracle.bf16_to_f32(B).reshape(B.shape)
+    return A32, B32, A32, B32
+
+
+# Ragged shapes large enough for the zero-padded route (the aligned kernels
+# on padded copies of the operands, the valid corner of C copied out): every
+# dimension ragged, K alone ragged (C written in place), M alone ragged (B
+# used in place), N alone ragged (A used in place).
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(1000, 1000, 1000), (640, 2048, 520), (1031, 768, 512), (2048, 1100, 256)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_padded_ragged_every_entry(hip, oracle, dtype, M, N, K, ta, tb):
+    A, B, Au, Bu = _operands(oracle, dtype, M, N, K, ta, tb, seed=M + 3 * N + 7 * K + 2 * ta + tb)
+    got = hip.matmul(hip.from_numpy(A, dtype), hip.from_numpy(B, dtype), trans_a=bool(ta),
+                     trans_b=bool(tb)).numpy()
+    assert got.shape == (M, N)
+    ref = oracle.matmul(Au, Bu, trans_a=bool(ta), trans_b=bool(tb), threads=16)
+    den = np.abs(Au.T if ta else Au).astype(np.float64) @ np.abs(Bu.T if tb else Bu).astype(np.float64)
+    assert_gemm_close(got, ref, den, K, f"padded {dtype} {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_padded_large_ragged_every_entry(hip, oracle, dtype):
+    # 3000 x 5000 x 2000: M, N and K all ragged, padded to the 256 x 256
+    # kernels' tiles; every entry against the loop (its A·Bᵀ form on a
+    # transposed copy of B, bit for bit its A·B loop)
+    M, N, K = 3000, 5000, 2000
+    A, B, Au, Bu = _operands(oracle, dtype, M, N, K, 0, 0, seed=41)
+    got = hip.matmul(hip.from_numpy(A, dtype), hip.from_numpy(B, dtype)).numpy()
+    Bt = np.ascontiguousarray(Bu.T)
+    ref = oracle.matmul(Au, Bt, trans_b=True, threads=16)
+    den = np.abs(Au) @ np.abs(Bt).T
+    assert_gemm_close(got, ref, den, K, f"padded {dtype} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("dtype,off", [("f32", 1), ("bf16", 1), ("bf16", 4)])
+def test_padded_misaligned_views(hip, oracle, dtype, off):
+    # Views starting `off` elements into their buffers at an aligned shape
+    # large enough for the padded route: the operands are copied (element by
+    # element, the source rows not being 16-byte aligned) into aligned buffers.
+    M, N, K = 1024, 1024, 512
+    A, B, Au, Bu = _operands(oracle, dtype, M, N, K, 0, 1, seed=77 + off)
+    abuf = hip.from_numpy(np.concatenate([np.zeros(off, A.dtype), A.ravel()]), dtype)
+    bbuf = hip.from_numpy(np.concatenate([np.zeros(off, B.dtype), B.ravel()]), dtype)
+    a, b = abuf.sub(off, A.shape), bbuf.sub(off, B.shape)
+    got = hip.matmul(a, b, trans_b=True).numpy()
+    ref = oracle.matmul(Au, Bu, trans_b=True, threads=16)
+    den = np.abs(Au).astype(np.float64) @ np.abs(Bu.T).astype(np.float64)
+    assert_gemm_close(got, ref, den, K, f"padded {dtype} view at +{off}")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_padded_batched_every_entry(hip, oracle, dtype, ta, tb):
+    bsz, M, N, K = 5, 700, 900, 300
+    A, B, Au, Bu = _operands(oracle, dtype, M, N, K, ta, tb, seed=5 + ta + tb, batch=bsz)
+    got = hip.matmul_batched(hip.from_numpy(A, dtype), hip.from_numpy(B, dtype), trans_a=bool(ta),
+                             trans_b=bool(tb)).numpy()
+    assert got.shape == (bsz, M, N)
+    for i in range(bsz):
+        ref = oracle.matmul(Au[i], Bu[i], trans_a=bool(ta), trans_b=bool(tb), threads=16)
+        den = np.abs(Au[i].T if ta else Au[i]).astype(np.float64) @ \
+            np.abs(Bu[i].T if tb else Bu[i]).astype(np.float64)
+        assert_gemm_close(got[i], ref, den, K, f"padded batched {dtype} entry {i}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_padded_infinities_and_nans(hip, oracle, dtype):
+    # The padded rows, columns and k add zeros only: an Inf or NaN reaches
+    # exactly the entries its row or column feeds, and 0 * Inf = NaN of a
+    # padded partner never lands in a valid entry.
+    M, N, K = 1000, 1001, 70
+    rng = np.random.default_rng(29)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    A[999, 69] = np.inf          # last row, last k: its padded neighbours are zeros
+    A[5, 3] = np.nan
+    B[69, 1000] = -np.inf        # last k, last column
+    B[2, 7] = 0.0
+    A[9, 2] = np.inf             # Inf times 0 -> NaN at (9, 7)
+    if dtype == "bf16":
+        a, b = hip.from_numpy(oracle.to_bf16(A)), hip.from_numpy(oracle.to_bf16(B))
+        Au, Bu = oracle.bf16_to_f32(a.numpy()).reshape(M, K), oracle.bf16_to_f32(b.numpy()).reshape(K, N)
+    else:
+        a, b = hip.from_numpy(A), hip.from_numpy(B)
+        Au, Bu = A, B
+    got = hip.matmul(a, b).numpy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = Au.astype(np.float64) @ Bu.astype(np.float64)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref))
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))
+    assert np.isnan(got[9, 7]) and np.isnan(got[5]).all()
+    fin = np.isfinite(ref)
+    den = np.abs(Au).astype(np.float64) @ np.abs(Bu).astype(np.float64)
+    assert np.all(np.abs(got[fin] - ref[fin]) <= 1e-5 * np.sqrt(K) * den[fin])
