@@ -290,17 +290,36 @@ bool launch_fast(const uint16_t* a, const uint16_t* b, float* c, int M, int N, i
     // us), and with several rounds more so.  With whole-line C stores in all
     // three, 64 x 512^3 measured 24.3-24.5 us tiled, 24.8-24.9 paired-copy
     // ping-pong, 25.0-25.7 single-stage ping-pong (same box).
+    //
+    // Also with fewer 256 x 256 tiles than CUs, from half as many: one round
+    // of them beat the 128 x 128 tiles' two or three rounds (3072^3, 144
+    // tiles: 65.7 against 85.3 us; 3072 x 4096 x 2048, 192 tiles: 52.9
+    // against 69.2 us), and lost below (2560^3, 100 tiles: 52.9 against
+    // 45.9 us; 2048^3, 64 tiles: 39.6 against 26.1 us).
+    const int cus = ch::num_cus();
     const int64_t big_tiles = (int64_t)(M / 256) * (N / 256) * batch;
-    if (big_tiles >= ch::num_cus()) {
-        const bool short_single_round = big_tiles <= ch::num_cus() && K <= 512;
+    if (big_tiles * 2 >= cus) {
+        const bool short_single_round = big_tiles <= cus && K <= 512;
         if (!short_single_round && launch_pairs<TA, TB>(a, b, c, M, N, K, batch, st)) return true;
         if (!short_single_round && launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, st)) return true;
         if (launch_tiled<256, 256, 64, 2, 4, 2, 16, TA, TB>(a, b, c, M, N, K, batch, st)) return true;
         if (launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, st)) return true;
     }
-    // 128 x 128 x 64 tile, 4 waves of 64 x 64 in 32 x 32 x 16 MFMAs, three
-    // LDS stages (96 KiB)
-    return launch_tiled<128, 128, 64, 2, 2, 3, 32, TA, TB>(a, b, c, M, N, K, batch, st);
+    // 128 x 128 x 64 tiles, 4 waves of 64 x 64 in 32 x 32 x 16 MFMAs.  Up to
+    // one round of them: three LDS stages (96 KiB, one workgroup per CU), or,
+    // with a k-contiguous A, 64 x 128 tiles (two workgroups per CU) -- 1024^3
+    // 9.7 against 12.8 us, 512^3 6.0 against 7.9, 2048^3 26.1 against 27.3.
+    // Several rounds: two stages (64 KiB), two workgroups per CU -- 4224^3
+    // 214 against 225 us, 2304^3 37.1 against 47.3, 3072 x 4096 x 2048 69.2
+    // against 85.9.
+    const int64_t tiles128 = (int64_t)(M / 128) * (N / 128) * batch;
+    if (tiles128 <= cus) {
+        if constexpr (!TA) {
+            if (launch_tiled<64, 128, 64, 2, 2, 3, 32, TA, TB>(a, b, c, M, N, K, batch, st)) return true;
+        }
+        return launch_tiled<128, 128, 64, 2, 2, 3, 32, TA, TB>(a, b, c, M, N, K, batch, st);
+    }
+    return launch_tiled<128, 128, 64, 2, 2, 2, 32, TA, TB>(a, b, c, M, N, K, batch, st);
 }
 
 // Products of at least this many flops (2 M N K per product) that no aligned
@@ -309,9 +328,9 @@ bool launch_fast(const uint16_t* a, const uint16_t* b, float* c, int M, int N, i
 // together).  Measured crossing: ~115^3 (100^3 11.1 us general, 12.1 padded;
 // 127 x 129 x 131 14.1 against 12.0).
 constexpr double kPadMinFlops = 1u << 22;
-// 256 x 256 tiles (8192^3) 0.55 of peak; 128 x 128 tiles (8320^3) 0.31, one
-// workgroup per CU (96 KiB of LDS).
-constexpr ch::PadModel kPadModel{0.55, 0.31, true};
+// 256 x 256 tiles (8192^3) 0.55 of peak, also from half a round of them;
+// 128 x 128 tiles (8320^3) 0.31.
+constexpr ch::PadModel kPadModel{0.55, 0.31, true, 0.5};
 
 template <bool TA, bool TB>
 int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch) {

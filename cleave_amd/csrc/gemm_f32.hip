@@ -3,11 +3,12 @@
 // Shapes that divide a 256 x 256 x 16 tile, with a tile per CU, run the
 // ping-pong kernel of gemm_f32_pingpong.hpp; shapes that divide a
 // 128 x 128 x 16 tile run the large-tile kernel of gemm_f32_tiled.hpp (LDS
-// filled by global_load_lds, four MFMA k-steps per 16-byte operand read);
-// small products run 32 x 32 tiles with K split over a workgroup's waves
-// (gemm_f32_small.hpp), or the large-tile kernel with 64 x 64 tiles and a
-// 16-deep ring.  Large products of other shapes run those kernels on
-// zero-padded copies (gemm_pad.hpp); the rest run the general kernel below.
+// filled by global_load_lds, four MFMA k-steps per 16-byte operand read),
+// also on 128 x 64 tiles when those balance the CUs better; small products
+// run 32 x 32 tiles with K split over a workgroup's waves
+// (gemm_f32_small.hpp), or the large-tile kernel with 64 x 64 tiles.  Large
+// products of other shapes run those kernels on zero-padded copies
+// (gemm_pad.hpp); the rest run the general kernel below.
 //
 // Replaces linalg.matmul as cleave lowers it (stdlib/linalg/matrix.cleave:27-61,
 // region cleave/src/mlir_lower.rs:2089-2120): C = 0; C[i,j] += A[i,k]*B[k,j].
@@ -294,21 +295,36 @@ bool launch_fast(const float* a, const float* b, float* c, int M, int N, int K, 
         if (big_tiles >= ch::num_cus() &&
             launch_pingpong<TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
             return true;
-        // At most one 32 x 32 tile per CU with K <= 1024 (config 1's 256^3 is
+        // Up to two 32 x 32 tiles per CU with K <= 1024 (config 1's 256^3 is
         // 64 tiles): a tile per workgroup, K split over its waves, 32 MFMAs
-        // per wave.
+        // per wave.  Measured against 64 x 64 tiles: 512^3 6.2 against
+        // 11.7 us, 640^3 (400 tiles) 12.7 against 14.5, 512 x 1024 x 512
+        // (512 tiles) 10.1 against 12.1; 768^3 (576 tiles) 19.2 against 17.4.
+        const int cus = ch::num_cus();
         const int64_t tiles32 = (int64_t)(M / 32) * (N / 32) * batch;
-        if (tiles32 <= ch::num_cus() &&
+        if (tiles32 <= 2 * cus &&
             launch_small<TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
             return true;
-        // Fewer 128 x 128 tiles than a quarter of the CUs: 64 x 64 tiles put
-        // the product on 4x the CUs, and a 16-deep ring (128 KiB) holds 256 k
-        // at once, so a short product waits for its copies once instead of
-        // once per k-tile.
+        // Fewer 128 x 128 tiles than CUs: 64 x 64 tiles with a 4-deep ring
+        // (five workgroups per CU) put the product on 4x the CUs.  1024^3 23.9
+        // against 66.7 us on 128 x 128 tiles, 1280^3 49.0 against 84.7,
+        // 1536^3 82.9 against 103; a 16-deep ring measured 2-18% slower.
         const int64_t tiles128 = (int64_t)(M / 128) * (N / 128) * batch;
-        if (tiles128 * 4 < ch::num_cus() &&
-            launch_tiled<64, 64, 16, 2, 2, 16, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
+        if (tiles128 < cus &&
+            launch_tiled<64, 64, 16, 2, 2, 4, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
             return true;
+        // 128 x 128 tiles run four workgroups per CU, 128 x 64 tiles six.
+        // Where the last round of 128 x 128 tiles would fill under 70% of
+        // the CUs' slots, the twice as many 128 x 64 tiles balance better:
+        // 2304^3 (324 tiles) 233 against 282 us, 3072^3 (576) 489 against
+        // 551, 4224^3 (1089) 1122 against 1222; at 3072 x 4096 x 2048 (768,
+        // 75%) 414 against 397, at 4096^2 x 1024 (1024, full) 289 against 271.
+        if (tiles128 > cus) {
+            const int64_t slots = 4 * (int64_t)cus, rounds = (tiles128 + slots - 1) / slots;
+            if ((double)tiles128 < 0.7 * (double)(rounds * slots) &&
+                launch_tiled<128, 64, 16, 2, 2, 2, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
+                return true;
+        }
         if (launch_tiled<128, 128, 16, 2, 2, 2, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
             return true;
     }
@@ -324,7 +340,7 @@ constexpr double kPadMinFlops = 1u << 20;
 // 256 x 256 tiles (4096^3) 0.86 of peak, one workgroup per CU; 128 x 128
 // tiles (4224^3) 0.78, four workgroups per CU.  4097^3 measured 1.23 ms
 // padded to 4224^3, 1.83 ms padded to 4352^2 x 4160 (289 tiles of 256).
-constexpr ch::PadModel kPadModel{0.86, 0.78, false};
+constexpr ch::PadModel kPadModel{0.86, 0.78, false, 1.0};
 
 template <bool TA, bool TB>
 int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,

@@ -31,13 +31,15 @@ inline int64_t pad_up(int x, int q) { return ((int64_t)x + q - 1) / q * q; }
 // Measured throughput of the aligned kernels, as a fraction of peak; they
 // price the two paddings.
 struct PadModel {
-    double eff256;  // 256 x 256 tiles, one workgroup per CU
-    double eff128;  // 128 x 128 tiles
-    bool rounds128; // 128 x 128 tiles also run one workgroup per CU
+    double eff256;    // 256 x 256 tiles, one workgroup per CU
+    double eff128;    // 128 x 128 tiles
+    bool rounds128;   // price 128 x 128 tiles by rounds too
+    double min256;    // fewest 256 x 256 tiles the kernels take, per CU
 };
 
 // Padded shape: K to a multiple of 64; M and N to multiples of 128, or of 256
-// when that still gives every CU a 256 x 256 tile and is estimated faster.
+// when that gives the 256 x 256 kernels enough tiles (model.min256 per CU)
+// and is estimated faster.
 // Time ~ padded area / efficiency, and, where a CU holds one workgroup, / the
 // fill of the rounds of tiles (the last round may leave CUs idle; where a CU
 // holds several, a lone workgroup runs faster and this is not counted).  An
@@ -56,7 +58,7 @@ inline PadPlan pad_plan(int M, int N, int K, int batch, bool ta, bool tb, const 
     const int c = cus > 0 ? cus : 1;
     const double c128 = model.rounds128 ? cost((double)m1 * n1, t1, c, model.eff128)
                                         : (double)m1 * n1 / model.eff128;
-    const bool use256 = t2 >= c && cost((double)m2 * n2, t2, c, model.eff256) < c128;
+    const bool use256 = (double)t2 >= model.min256 * c && cost((double)m2 * n2, t2, c, model.eff256) < c128;
     const int64_t mp = use256 ? m2 : m1, np = use256 ? n2 : n1;
     p.ok = mp <= INT32_MAX && np <= INT32_MAX && kp <= INT32_MAX;
     if (!p.ok) return p;

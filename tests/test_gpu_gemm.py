@@ -602,3 +602,28 @@ def test_padded_infinities_and_nans(hip, oracle, dtype):
     fin = np.isfinite(ref)
     den = np.abs(Au).astype(np.float64) @ np.abs(Bu).astype(np.float64)
     assert np.all(np.abs(got[fin] - ref[fin]) <= 1e-5 * np.sqrt(K) * den[fin])
+
+
+# The aligned kernels are chosen by tile count (on a 256-CU MI355X): f32 runs
+# the small kernel up to 512 tiles of 32 x 32 (640^3), 64 x 64 tiles below
+# 256 tiles of 128 x 128 (1024^2 x 512, 1280^2 x 256), 128 x 64 tiles where
+# the last round of 128 x 128 tiles would be under 70% full (2304^2 x 128)
+# and 128 x 128 tiles for one full round (2048^2 x 128); bf16 runs 64 x 128
+# tiles for up to a round of 128 x 128 (1024^2 x 512; 128 x 128 with an
+# m-contiguous A), two-stage 128 x 128 tiles for several rounds
+# (2304^2 x 128), and 256 x 256 tiles from 128 of them (3072^2 x 128 tiled,
+# 3072^2 x 640 ping-pong).  Every entry, every layout.
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("dtype,M,N,K", [
+    ("f32", 640, 640, 640), ("f32", 1024, 1024, 512), ("f32", 1280, 1280, 256),
+    ("f32", 2304, 2304, 128), ("f32", 2048, 2048, 128),
+    ("bf16", 1024, 1024, 512), ("bf16", 2304, 2304, 128), ("bf16", 3072, 3072, 128),
+    ("bf16", 3072, 3072, 640),
+])
+def test_tile_choices_every_entry(hip, oracle, dtype, M, N, K, ta, tb):
+    A, B, Au, Bu = _operands(oracle, dtype, M, N, K, ta, tb, seed=M + N + K + 2 * ta + tb)
+    got = hip.matmul(hip.from_numpy(A, dtype), hip.from_numpy(B, dtype), trans_a=bool(ta),
+                     trans_b=bool(tb)).numpy()
+    ref = oracle.matmul(Au, Bu, trans_a=bool(ta), trans_b=bool(tb), threads=16)
+    den = np.abs(Au.T if ta else Au).astype(np.float64) @ np.abs(Bu.T if tb else Bu).astype(np.float64)
+    assert_gemm_close(got, ref, den, K, f"{dtype} {M}x{N}x{K} ta={ta} tb={tb}")
