@@ -281,7 +281,7 @@ bool launch_pairs(const uint16_t* a, const uint16_t* b, float* c, int M, int N, 
 // The aligned kernels; false when none takes the shape.
 template <bool TA, bool TB>
 bool launch_fast(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch, int32_t* st) {
-    // 256 x 256 tiles, when that still gives every CU a tile: the ping-pong
+    // 256 x 256 tiles, when there are enough of them (below): the ping-pong
     // kernel (k-tiles of 32), or the tiled kernel (k-tiles of 64).  With one
     // round of tiles and K up to 512 the two measured equal (64 x 512^3:
     // 25.0-29.3 against 25.5-26.9 us over two runs; 4096^2 x 512: 26.1-26.7
@@ -291,8 +291,8 @@ bool launch_fast(const uint16_t* a, const uint16_t* b, float* c, int M, int N, i
     // three, 64 x 512^3 measured 24.3-24.5 us tiled, 24.8-24.9 paired-copy
     // ping-pong, 25.0-25.7 single-stage ping-pong (same box).
     //
-    // Also with fewer 256 x 256 tiles than CUs, from half as many: one round
-    // of them beat the 128 x 128 tiles' two or three rounds (3072^3, 144
+    // Enough means at least half as many tiles as CUs: one partial round of
+    // them beat the 128 x 128 tiles' two or three rounds (3072^3, 144
     // tiles: 65.7 against 85.3 us; 3072 x 4096 x 2048, 192 tiles: 52.9
     // against 69.2 us), and lost below (2560^3, 100 tiles: 52.9 against
     // 45.9 us; 2048^3, 64 tiles: 39.6 against 26.1 us).
