@@ -19,7 +19,7 @@
 namespace ch {
 
 struct PadPlan {
-    bool ok;         // the padded extents fit the kernels' int arguments
+    bool ok;         // the padded extents fit int and at most triple the work
     int M, N, K;     // valid shape
     int Mp, Np, Kp;  // padded shape
     bool copy_a, copy_b, crop_c;
@@ -60,7 +60,11 @@ inline PadPlan pad_plan(int M, int N, int K, int batch, bool ta, bool tb, const 
                                         : (double)m1 * n1 / model.eff128;
     const bool use256 = (double)t2 >= model.min256 * c && cost((double)m2 * n2, t2, c, model.eff256) < c128;
     const int64_t mp = use256 ? m2 : m1, np = use256 ? n2 : n1;
-    p.ok = mp <= INT32_MAX && np <= INT32_MAX && kp <= INT32_MAX;
+    // Padding at most triples the work: smaller products (16^3 padded to
+    // 128 x 128 x 64 is 256x) stay on the general kernel, which computes
+    // whole tiles too but moves no padded copies.
+    p.ok = mp <= INT32_MAX && np <= INT32_MAX && kp <= INT32_MAX &&
+           (double)mp * np * kp <= 3.0 * M * N * K;
     if (!p.ok) return p;
     p.Mp = (int)mp, p.Np = (int)np, p.Kp = (int)kp;
     const bool a_al = ((uintptr_t)a & 15) == 0 && ((int64_t)(ta ? M : K) * esz) % 16 == 0;

@@ -627,3 +627,17 @@ def test_tile_choices_every_entry(hip, oracle, dtype, M, N, K, ta, tb):
     ref = oracle.matmul(Au, Bu, trans_a=bool(ta), trans_b=bool(tb), threads=16)
     den = np.abs(Au.T if ta else Au).astype(np.float64) @ np.abs(Bu.T if tb else Bu).astype(np.float64)
     assert_gemm_close(got, ref, den, K, f"{dtype} {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_many_tiny_products_stay_on_the_general_kernel(hip, oracle, dtype):
+    # 2048 products of 16 x 24 x 20: above the padded route's size threshold
+    # in total, but padding each to whole tiles would multiply the work, so
+    # they run the guarded general kernel; every entry of every product.
+    bsz, M, N, K = 2048, 16, 24, 20
+    A, B, Au, Bu = _operands(oracle, dtype, M, N, K, 0, 1, seed=61, batch=bsz)
+    got = hip.matmul_batched(hip.from_numpy(A, dtype), hip.from_numpy(B, dtype), trans_b=True).numpy()
+    den = np.einsum("bmk,bnk->bmn", np.abs(Au).astype(np.float64), np.abs(Bu).astype(np.float64))
+    for i in range(bsz):
+        ref = oracle.matmul(Au[i], Bu[i], trans_b=True)
+        assert_gemm_close(got[i], ref, den[i], K, f"tiny {dtype} product {i}")
