@@ -27,8 +27,14 @@ void clear_error();
 // Checks a HIP call; on error records it and returns CLEAVE_HIP_ERR_RUNTIME.
 int32_t check_hip(hipError_t e, const char* what);
 
+// Buffers of cleave_hip_buf_alloc / cleave_hip_buf_free (a cache of freed
+// blocks in runtime.hip).
+void* buf_alloc(uint64_t bytes);
+void buf_free(void* buf);
+
 // Scratch device memory owned by the library (grown on demand, never shrunk).
-// `slot` selects an independent buffer.
+// `slot` (0 .. kScratchSlots-1) selects an independent buffer.
+constexpr int kScratchSlots = 16;
 void* scratch(int slot, size_t bytes);
 // Same buffer, but a failed allocation returns nullptr without recording an
 // error (for callers that have another way to do the work).

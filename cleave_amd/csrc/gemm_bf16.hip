@@ -24,6 +24,11 @@
 #include "gemm_common.hpp"
 #include "gemm_pad.hpp"
 
+namespace ch {
+int32_t matmul_vector_bf16(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch, int ta,
+                           int tb);
+}
+
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -350,6 +355,8 @@ int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N,
 
 int32_t dispatch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
                  int ta, int tb) {
+    // a dimension of 1: matrix-vector or outer products (gemv.hip)
+    if (M == 1 || N == 1 || K == 1) return ch::matmul_vector_bf16(a, b, c, M, N, K, batch, ta, tb);
     if (!ta && !tb) return launch_any<false, false>(a, b, c, M, N, K, batch);
     if (!ta && tb) return launch_any<false, true>(a, b, c, M, N, K, batch);
     if (ta && !tb) return launch_any<true, false>(a, b, c, M, N, K, batch);

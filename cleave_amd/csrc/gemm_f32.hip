@@ -38,6 +38,10 @@
 #include "gemm_f32_tiled.hpp"
 #include "gemm_pad.hpp"
 
+namespace ch {
+int32_t matmul_vector_f32(const float* a, const float* b, float* c, int M, int N, int K, int batch, int ta, int tb);
+}
+
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -367,8 +371,47 @@ int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, in
 // batch >= 1 independent products packed back to back, or (splits > 1, batch
 // must be 1) one product whose K range is cut into `splits` equal slices,
 // slice s writing its partial sum to c + s*M*N.
+// c[i] = part[0][i] + part[1][i] + ... + part[S-1][i], in slice order; n is
+// a multiple of 4 and every slice 16-byte aligned.
+__global__ __launch_bounds__(256) void sum_slices_kernel(const float* __restrict__ part, float* __restrict__ c,
+                                                         int64_t n, int S) {
+    for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < n; i += (int64_t)gridDim.x * 256 * 4) {
+        f4 acc = *reinterpret_cast<const f4*>(part + i);
+        for (int s = 1; s < S; ++s) acc = acc + *reinterpret_cast<const f4*>(part + (int64_t)s * n + i);
+        *reinterpret_cast<f4*>(c + i) = acc;
+    }
+}
+
+// K slices for a product with fewer 256 x 256 tiles than CUs and a long K:
+// S (a power of two) slices fill the CUs with ping-pong tiles, each slice at
+// least 2048 deep so that the partial sums' extra traffic (S + 1 passes over
+// C) stays a few percent of the product.  1 = no split.  The slices add in
+// order, so results are deterministic.
+int split_count(int M, int N, int K) {
+    if (M % 256 || N % 256) return 1;
+    const int64_t tiles = (int64_t)(M / 256) * (N / 256);
+    int S = 1;
+    while (tiles * S * 2 <= ch::num_cus() && K % (16 * S * 2) == 0 && K / (S * 2) >= 2048) S *= 2;
+    // the slices must fill the CUs for the ping-pong kernel to take them
+    return tiles * S >= ch::num_cus() ? S : 1;
+}
+
 int32_t dispatch(const float* a, const float* b, float* c, int M, int N, int K, int batch,
                  int ta, int tb, int splits) {
+    // a dimension of 1: matrix-vector or outer products (gemv.hip)
+    if (splits <= 1 && (M == 1 || N == 1 || K == 1)) return ch::matmul_vector_f32(a, b, c, M, N, K, batch, ta, tb);
+    if (splits <= 1 && batch == 1 && ((uintptr_t)c & 15) == 0) {
+        const int S = split_count(M, N, K);
+        float* part = S > 1 ? (float*)ch::scratch_try(9, sizeof(float) * (size_t)S * M * N) : nullptr;
+        if (part) {
+            const int32_t st = dispatch(a, b, part, M, N, K, 1, ta, tb, S);
+            if (st != CLEAVE_HIP_OK) return st;
+            const int64_t n = (int64_t)M * N, blocks = (n / 4 + 255) / 256;
+            const int64_t cap = (int64_t)ch::num_cus() * 8;
+            sum_slices_kernel<<<(unsigned)(blocks < cap ? blocks : cap), 256, 0, ch::stream()>>>(part, c, n, S);
+            return ch::check_hip(hipGetLastError(), "sum_slices_kernel");
+        }
+    }
     const int64_t lda = ta ? M : K, ldb = tb ? K : N, ldc = N;
     int64_t sA = (int64_t)M * K, sB = (int64_t)K * N, sC = (int64_t)M * N;
     int kk = K;

@@ -7,7 +7,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
+#include <vector>
 
 #include "common.hpp"
 
@@ -26,8 +28,8 @@ struct State {
     int32_t init_status = CLEAVE_HIP_ERR_RUNTIME;
     hipStream_t stream = nullptr;
     int cus = 0;
-    void* scratch[8] = {};
-    size_t scratch_bytes[8] = {};
+    void* scratch[kScratchSlots] = {};
+    size_t scratch_bytes[kScratchSlots] = {};
     float* noalloc = nullptr;  // device address of ::scratch on device 0
 };
 State g;
@@ -99,7 +101,7 @@ void* scratch(int slot, size_t bytes) {
 }
 
 void* scratch_try(int slot, size_t bytes) {
-    if (slot < 0 || slot >= 8) return nullptr;
+    if (slot < 0 || slot >= kScratchSlots) return nullptr;
     if (g.scratch_bytes[slot] >= bytes && g.scratch[slot]) return g.scratch[slot];
     if (g.scratch[slot]) {
         // The old buffer may still be read by queued work.
@@ -118,6 +120,108 @@ void* scratch_try(int slot, size_t bytes) {
     return p;
 }
 
+namespace {
+// Buffers of cleave_hip_buf_alloc.  A freed buffer goes to a cache of free
+// blocks by size, for the next request of that size.  Everything runs on the
+// library stream, so work queued by the next owner runs after every use by
+// the previous one, and a free needs no synchronisation.  (hipFree took
+// ~250 us for 1 GiB, after the stream synchronisation it needs, with the GPU
+// idle meanwhile; a reverse-mode training step frees several such buffers.)
+// Blocks are rounded up to 512 bytes, or to 2 MiB above 1 MiB.  The cache
+// holds at most kPoolCap bytes, and is emptied (stream synchronised, blocks
+// freed) when hipMalloc fails, before the allocation is tried again.
+struct BufPool {
+    std::mutex mu;
+    std::map<uintptr_t, std::pair<uint64_t, size_t>> live;  // base -> (bytes asked for, block size)
+    std::multimap<size_t, void*> cached;                     // block size -> free block
+    size_t cached_bytes = 0;
+};
+BufPool g_pool;
+constexpr size_t kPoolCap = size_t(32) << 30;
+
+size_t block_size(uint64_t bytes) {
+    const uint64_t q = bytes <= (uint64_t(1) << 20) ? 512 : (uint64_t(2) << 20);
+    return (size_t)((bytes + q - 1) / q * q);
+}
+
+void release_cached() {
+    std::vector<void*> blocks;
+    {
+        std::lock_guard<std::mutex> lk(g_pool.mu);
+        for (auto& kv : g_pool.cached) blocks.push_back(kv.second);
+        g_pool.cached.clear();
+        g_pool.cached_bytes = 0;
+    }
+    if (blocks.empty()) return;
+    (void)hipStreamSynchronize(g.stream);
+    for (void* b : blocks) (void)hipFree(b);
+    (void)hipGetLastError();
+}
+
+// The bytes from p to the end of the library buffer holding it (what its
+// owner asked for; 0 past that); false when p is in no such buffer.
+bool pool_extent(const void* p, uint64_t* avail) {
+    const uintptr_t q = (uintptr_t)p;
+    std::lock_guard<std::mutex> lk(g_pool.mu);
+    auto it = g_pool.live.upper_bound(q);
+    if (it == g_pool.live.begin()) return false;
+    --it;
+    const uintptr_t base = it->first;
+    if (q >= base + it->second.second) return false;
+    *avail = q < base + it->second.first ? base + it->second.first - q : 0;
+    return true;
+}
+}  // namespace
+
+void* buf_alloc(uint64_t bytes) {
+    const size_t sz = block_size(bytes);
+    void* p = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_pool.mu);
+        auto it = g_pool.cached.find(sz);
+        if (it != g_pool.cached.end()) {
+            p = it->second;
+            g_pool.cached.erase(it);
+            g_pool.cached_bytes -= sz;
+        }
+    }
+    if (!p) {
+        hipError_t e = hipMalloc(&p, sz);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            release_cached();
+            e = hipMalloc(&p, sz);
+        }
+        if (e != hipSuccess) {
+            check_hip(e, "hipMalloc");
+            return nullptr;
+        }
+    }
+    std::lock_guard<std::mutex> lk(g_pool.mu);
+    g_pool.live[(uintptr_t)p] = {bytes, sz};
+    return p;
+}
+
+void buf_free(void* buf) {
+    {
+        std::lock_guard<std::mutex> lk(g_pool.mu);
+        auto it = g_pool.live.find((uintptr_t)buf);
+        if (it != g_pool.live.end()) {
+            const size_t sz = it->second.second;
+            g_pool.live.erase(it);
+            if (g_pool.cached_bytes + sz <= kPoolCap) {
+                g_pool.cached.emplace(sz, buf);
+                g_pool.cached_bytes += sz;
+                return;
+            }
+        }
+    }
+    // Not cached (the cache is full, or the buffer is not the library's):
+    // queued work may still use it.
+    if (check_hip(hipStreamSynchronize(g.stream), "hipStreamSynchronize") != CLEAVE_HIP_OK) return;
+    check_hip(hipFree(buf), "hipFree");
+}
+
 int32_t require_device(const char* fn, const char* what, const void* p, uint64_t bytes) {
     hipPointerAttribute_t at{};
     if (hipPointerGetAttributes(&at, p) != hipSuccess) {
@@ -133,6 +237,14 @@ int32_t require_device(const char* fn, const char* what, const void* p, uint64_t
         return fail(CLEAVE_HIP_ERR_ARG,
                     "%s: %s (%p) is not device memory (memory type %d); pass a buffer from "
                     "cleave_hip_buf_alloc (the _host entry points take host arrays)", fn, what, p, (int)at.type);
+    uint64_t avail = 0;
+    if (pool_extent(p, &avail)) {
+        if (bytes > avail)
+            return fail(CLEAVE_HIP_ERR_ARG,
+                        "%s: %s needs %llu bytes from %p, but its allocation holds %llu bytes from there", fn, what,
+                        (unsigned long long)bytes, p, (unsigned long long)avail);
+        return CLEAVE_HIP_OK;
+    }
     hipDeviceptr_t base = nullptr;
     size_t size = 0;
     if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p) == hipSuccess) {
@@ -238,21 +350,13 @@ void* cleave_hip_buf_alloc(int64_t bytes) {
         ch::fail(CLEAVE_HIP_ERR_ARG, "cleave_hip_buf_alloc: bytes must be > 0 (got %lld)", (long long)bytes);
         return nullptr;
     }
-    void* p = nullptr;
-    hipError_t e = hipMalloc(&p, (size_t)bytes);
-    if (e != hipSuccess) {
-        ch::check_hip(e, "hipMalloc");
-        return nullptr;
-    }
-    return p;
+    return ch::buf_alloc((uint64_t)bytes);
 }
 
 void cleave_hip_buf_free(void* buf) {
     if (!buf) return;
     if (ch::ensure_init() != CLEAVE_HIP_OK) return;
-    // Queued work may still use the buffer.
-    if (ch::check_hip(hipStreamSynchronize(ch::stream()), "hipStreamSynchronize") != CLEAVE_HIP_OK) return;
-    ch::check_hip(hipFree(buf), "hipFree");
+    ch::buf_free(buf);
 }
 
 int64_t cleave_hip_upload(void* dst_dev, const void* src_host, int64_t bytes) {

@@ -70,7 +70,12 @@ CLEAVE_HIP_API int32_t cleave_hip_device_available(void);
 
 /* Device allocation, 256-byte aligned.  Mirrors cleave_alloc
  * (cleave-rt/src/lib.rs:56-71; that one is 16-byte aligned and never freed);
- * here the library owns the memory and cleave_hip_buf_free releases it. */
+ * here the library owns the memory and cleave_hip_buf_free releases it: into
+ * a cache of free blocks that later allocations of the same size reuse
+ * without a device synchronisation (work on the library stream is ordered).
+ * The cache holds at most 32 GiB and is returned to the device when an
+ * allocation would otherwise fail.  A device entry point refuses an operand
+ * that runs past the bytes its buffer was allocated with. */
 CLEAVE_HIP_API void* cleave_hip_buf_alloc(int64_t bytes);
 CLEAVE_HIP_API void cleave_hip_buf_free(void* buf);
 /* Host <-> device copies on the library stream; both return the byte count

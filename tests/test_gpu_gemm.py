@@ -641,3 +641,22 @@ def test_many_tiny_products_stay_on_the_general_kernel(hip, oracle, dtype):
     for i in range(bsz):
         ref = oracle.matmul(Au[i], Bu[i], trans_b=True)
         assert_gemm_close(got[i], ref, den[i], K, f"tiny {dtype} product {i}")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(1024, 4096, 8192), (512, 512, 16384), (2048, 2048, 8192)])
+def test_f32_k_split_every_entry(hip, oracle, M, N, K, ta, tb):
+    # Fewer 256 x 256 tiles than CUs and a long K: the product runs as 4 or 8
+    # K slices on the ping-pong kernel, then the slices are added in order.
+    # Every entry against the loop (its A.B^T form on transposed copies, bit
+    # for bit its A.B loop), and bitwise the same on a second call.
+    A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=M + N + K + 2 * ta + tb)
+    a, b = hip.from_numpy(A), hip.from_numpy(B)
+    got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    again = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    Ak = np.ascontiguousarray(Au.T if ta else Au)
+    Bk = np.ascontiguousarray(Bu if tb else Bu.T)
+    ref = oracle.matmul(Ak, Bk, trans_b=True, threads=16)
+    den = np.abs(Ak) @ np.abs(Bk).T
+    assert_gemm_close(got, ref, den, K, f"k-split {M}x{N}x{K} ta={ta} tb={tb}")
