@@ -591,6 +591,32 @@ def main():
         if want_cpu:
             secondary["mlp_step_65536x1024x4096"]["cpu_baseline"] = cpu_secondary(
                 orc, "mlp_step_65536x1024x4096", cb, X=x.numpy(), y=yv.numpy(), W1=w1.numpy(), W2=w2.numpy(), B=B_)
+        # The same step written as a program of the library's operators and
+        # differentiated by the reverse-mode tape (cleave_amd.autograd): the
+        # GEMMs, sigmoid maps and their reverse rules, the N = 1 and K = 1
+        # products of the second layer, the mean, and two SGD updates, each a
+        # separate launch.
+        from cleave_amd import autograd as ad
+        fused_ms = ev
+        X_, Y_ = ad.const(x), ad.const(yv.view((B_, 1)))
+        w2c = w2.view((H_, 1))
+
+        def tape_step():
+            W1, W2 = ad.param(w1), ad.param(w2c)
+            e = ad.sigmoid(ad.sigmoid(X_ @ W1) @ W2) - Y_
+            ad.backward(ad.mean(e * e))
+            ca.sgd_update(w1, W1.grad, 0.01)
+            ca.sgd_update(w2c, W2.grad, 0.01)
+
+        wall_s, ev = timed(ca, tape_step, mlp_steps, 2, 0.3)
+        secondary["mlp_step_tape_65536x1024x4096"] = {
+            "steps_per_s": round(mlp_steps / wall_s, 3), "ms_per_step": round(ev, 3),
+            "gemm_TFLOP/s": round(gemm_fl / (ev * 1e-3) / 1e12, 2),
+            "fused_over_tape": round(fused_ms / ev, 3),
+            "note": "reverse-mode derive() over a tape of separate launches (cleave_amd.autograd); the CPU "
+                    "baseline is mlp_step_65536x1024x4096's, the same step"}
+        log(f"mlp step through the tape: {mlp_steps / wall_s:.2f} steps/s ({ev:.2f} ms)")
+        del X_, Y_, w2c
         del x, yv, w1, w2
         # escape-count map + u64 sum (config 3)
         g = 16384

@@ -644,7 +644,7 @@ def test_many_tiny_products_stay_on_the_general_kernel(hip, oracle, dtype):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-@pytest.mark.parametrize("M,N,K", [(1024, 4096, 8192), (512, 512, 16384), (2048, 2048, 8192)])
+@pytest.mark.parametrize("M,N,K", [(1024, 4096, 8192), (1024, 2048, 16384), (2048, 2048, 8192)])
 def test_f32_k_split_every_entry(hip, oracle, M, N, K, ta, tb):
     # Fewer 256 x 256 tiles than CUs and a long K: the product runs as 4 or 8
     # K slices on the ping-pong kernel, then the slices are added in order.
