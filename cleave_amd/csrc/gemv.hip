@@ -257,6 +257,10 @@ __global__ __launch_bounds__(kThreads) void wsum_stage2(const float* __restrict_
 }
 
 // ---- outer product ------------------------------------------------------------------
+//
+// C[b][i][j] = 0 + a[b][i] b[b][j]: one workgroup per row (grid-strided), four
+// columns per thread.  0 + p is p except that a -0 product becomes +0, as in
+// the reference's C = 0; C += a*b.
 
 // Four consecutive values as floats: one 16-byte (f32) or 8-byte (bf16) load;
 // p must be aligned to that size.
@@ -274,10 +278,7 @@ __device__ __forceinline__ void load4(const uint16_t* p, float (&o)[4]) {
     o[2] = __uint_as_float(r[1] << 16);
     o[3] = __uint_as_float(r[1] & 0xFFFF0000u);
 }
-//
-// C[b][i][j] = 0 + a[b][i] b[b][j]: one workgroup per row (grid-strided), four
-// columns per thread.  0 + p is p except that a -0 product becomes +0, as in
-// the reference's C = 0; C += a*b.
+
 template <typename T>
 __global__ __launch_bounds__(kThreads) void outer_kernel(const T* __restrict__ a, const T* __restrict__ bv,
                                                          float* __restrict__ C, int M, int N, int64_t rows,
