@@ -27,6 +27,8 @@
 namespace ch {
 int32_t matmul_vector_bf16(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch, int ta,
                            int tb);
+int32_t matmul_skinny_bf16(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch, int ta,
+                           int tb);
 }
 
 namespace {
@@ -341,6 +343,10 @@ template <bool TA, bool TB>
 int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch) {
     int32_t st = CLEAVE_HIP_OK;
     if (launch_fast<TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
+    // one output dimension of at most 32: stream the long operand (gemv.hip);
+    // tiny products (under 2^20 flops) stay on the general kernel (one launch)
+    if ((M <= 32 || N <= 32) && 2.0 * M * N * K * batch >= (1u << 20))
+        return ch::matmul_skinny_bf16(a, b, c, M, N, K, batch, TA, TB);
     if (2.0 * M * N * K * batch >= kPadMinFlops) {
         const ch::PadPlan p = ch::pad_plan(M, N, K, batch, TA, TB, a, b, 2, ch::num_cus(), kPadModel);
         auto gemm = [batch](const uint16_t* pa, const uint16_t* pb, float* pc, int Mp, int Np, int Kp) {

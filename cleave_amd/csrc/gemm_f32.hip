@@ -40,6 +40,7 @@
 
 namespace ch {
 int32_t matmul_vector_f32(const float* a, const float* b, float* c, int M, int N, int K, int batch, int ta, int tb);
+int32_t matmul_skinny_f32(const float* a, const float* b, float* c, int M, int N, int K, int batch, int ta, int tb);
 }
 
 namespace {
@@ -341,6 +342,9 @@ bool launch_fast(const float* a, const float* b, float* c, int M, int N, int K, 
 // together).  Measured crossing: ~80^3 (64 x 64 x 63 10.2 us general, 12.4
 // padded; 100^3 15.9 against 12.5).
 constexpr double kPadMinFlops = 1u << 20;
+// Skinny products (gemv.hip) from the same size: 3 x 5 x 7 took 7.2 us there
+// (two launches) against 4.7 us on the general kernel.
+constexpr double kSkinnyMinFlops = 1u << 20;
 // 256 x 256 tiles (4096^3) 0.86 of peak, one workgroup per CU; 128 x 128
 // tiles (4224^3) 0.78, four workgroups per CU.  4097^3 measured 1.23 ms
 // padded to 4224^3, 1.83 ms padded to 4352^2 x 4160 (289 tiles of 256).
@@ -354,6 +358,10 @@ int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, in
     // whole packed products only (not the K-slices of a split product)
     const bool packed = lda == (TA ? M : K) && ldb == (TB ? K : N) && ldc == N && sA == (int64_t)M * K &&
                         sB == (int64_t)K * N && sC == (int64_t)M * N;
+    // one output dimension of at most 32: stream the long operand (gemv.hip);
+    // tiny products stay on the general kernel (one launch)
+    if (packed && (M <= 32 || N <= 32) && 2.0 * M * N * K * batch >= kSkinnyMinFlops)
+        return ch::matmul_skinny_f32(a, b, c, M, N, K, batch, TA, TB);
     if (packed && 2.0 * M * N * K * batch >= kPadMinFlops) {
         const ch::PadPlan p = ch::pad_plan(M, N, K, batch, TA, TB, a, b, 4, ch::num_cus(), kPadModel);
         auto gemm = [batch](const float* pa, const float* pb, float* pc, int Mp, int Np, int Kp) {

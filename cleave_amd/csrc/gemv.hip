@@ -308,6 +308,167 @@ __global__ __launch_bounds__(kThreads) void outer_kernel(const T* __restrict__ a
     }
 }
 
+// ---- skinny products: one output dimension of at most 32 --------------------------
+//
+// Y[i][s] = sum_k X[i][k] V(s, k) for i < R, s < S <= SB, with X k-contiguous
+// (pitch K) and V(s, k) = V[s*vs_s + k*vs_k].  A workgroup owns 32 rows of X,
+// eight lanes per row; it walks K in chunks of 256, staging V's chunk in LDS
+// as [SB][k] (zeros past S and K), and lane l of a row takes the 16-byte
+// pieces l, l + 8, ... of the chunk, so eight lanes read one 128-byte line.
+// Staged as [k][SB], the lanes' reads of four k apart fell on the same banks:
+// 65536 x N x 4096 took 0.93 ms at N = 10 and 1.86 ms at N = 32.
+// Each value of X meets SB values of V (fma); the row's eight lanes are then
+// added by a shuffle tree.  Batch entries along blockIdx.y.
+constexpr int kSkinnyKC = 256, kSkinnyRows = kThreads / 8;
+
+template <typename T, int SB, bool VEC>
+__global__ __launch_bounds__(kThreads) void skinny_dots_kernel(
+    const T* __restrict__ X, const T* __restrict__ V, float* __restrict__ y, int64_t R, int S, int K,
+    int64_t vs_s, int64_t vs_k, int64_t ys_i, int64_t ys_s, int64_t x_batch, int64_t v_batch, int64_t y_batch) {
+    // rows padded by 4 floats: the staging writes of consecutive s then spread over the banks
+    __shared__ __attribute__((aligned(16))) float vs[SB][kSkinnyKC + 4];
+    const int64_t b = blockIdx.y;
+    X += b * x_batch;
+    V += b * v_batch;
+    y += b * y_batch;
+    const int l8 = threadIdx.x & 7;
+    const int64_t row = (int64_t)blockIdx.x * kSkinnyRows + (threadIdx.x >> 3);
+    const T* x = X + (row < R ? row : 0) * (int64_t)K;
+    float acc[SB];
+#pragma unroll
+    for (int s = 0; s < SB; ++s) acc[s] = 0.0f;
+    for (int kc0 = 0; kc0 < K; kc0 += kSkinnyKC) {
+        __syncthreads();  // the previous chunk's readers are done
+        // consecutive threads read consecutive elements of V: along k when V's
+        // rows are k-contiguous, along s when V is stored k-major
+        if (vs_k == 1) {
+            for (int i = threadIdx.x; i < kSkinnyKC * SB; i += kThreads) {
+                const int s = i / kSkinnyKC, k = i % kSkinnyKC;
+                vs[s][k] = (s < S && kc0 + k < K) ? to_f32(V[s * vs_s + (int64_t)(kc0 + k)]) : 0.0f;
+            }
+        } else {
+            for (int i = threadIdx.x; i < kSkinnyKC * SB; i += kThreads) {
+                const int k = i / SB, s = i % SB;
+                vs[s][k] = (s < S && kc0 + k < K) ? to_f32(V[s * vs_s + (int64_t)(kc0 + k) * vs_k]) : 0.0f;
+            }
+        }
+        __syncthreads();
+        if (row < R) {
+#pragma unroll 2
+            for (int j = 0; j < kSkinnyKC / 32; ++j) {
+                const int kl = 32 * j + 4 * l8;  // this lane's 4 k of the chunk
+                float xv[4];
+                if constexpr (VEC) {
+                    if (kc0 + kl >= K) continue;  // K % 4 == 0: whole pieces only
+                    load4(x + kc0 + kl, xv);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) xv[e] = kc0 + kl + e < K ? to_f32(x[kc0 + kl + e]) : 0.0f;
+                }
+                // vs[s][kl .. kl+3]: the row's eight lanes read one 128-byte
+                // stretch of a row of vs, so the reads do not conflict
+#pragma unroll
+                for (int s = 0; s < SB; ++s) {
+                    typedef float f4 __attribute__((ext_vector_type(4)));
+                    const f4 v4 = *reinterpret_cast<const f4*>(&vs[s][kl]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[s] = __builtin_fmaf(xv[e], v4[e], acc[s]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < SB; ++s)
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) acc[s] = acc[s] + __shfl_xor(acc[s], o);
+    if (row < R && l8 == 0) {
+#pragma unroll
+        for (int s = 0; s < SB; ++s)
+            if (s < S) y[row * ys_i + s * ys_s] = acc[s];
+    }
+}
+
+// Y[j][s] = sum_k X[k][j] W(k, s) for j < J, s < S <= SB, with X j-contiguous
+// (pitch J) and W(k, s) = W[k*ws_k + s*ws_s].  Stage 1: a thread owns four
+// columns (VEC) or one and walks a group of rows in ascending order, W's rows
+// of the group staged in LDS 64 at a time, into part[b][group][s][j]; stage 2
+// adds the groups in ascending order.
+constexpr int kSkinnyWK = 64;
+
+template <typename T, int SB, bool VEC>
+__global__ __launch_bounds__(kThreads) void skinny_sums_stage1(
+    const T* __restrict__ X, const T* __restrict__ W, float* __restrict__ part, int K, int64_t J, int S,
+    int64_t ws_k, int64_t ws_s, int64_t nseg, int64_t groups, int64_t rpg, int64_t x_batch, int64_t w_batch) {
+    constexpr int E = VEC ? 4 : 1;
+    __shared__ float ws[kSkinnyWK][SB];
+    const int64_t b = blockIdx.y;
+    X += b * x_batch;
+    W += b * w_batch;
+    const int64_t seg = blockIdx.x % nseg, group = blockIdx.x / nseg;
+    const int64_t c = (seg * kThreads + threadIdx.x) * E;
+    const int64_t r0 = group * rpg;
+    const int64_t r1 = r0 + rpg < K ? r0 + rpg : K;
+    float acc[SB][E];
+#pragma unroll
+    for (int s = 0; s < SB; ++s)
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[s][e] = 0.0f;
+    for (int64_t k0 = r0; k0 < r1; k0 += kSkinnyWK) {
+        __syncthreads();
+        for (int i = threadIdx.x; i < kSkinnyWK * SB; i += kThreads) {
+            const int k = i / SB, s = i % SB;
+            ws[k][s] = (s < S && k0 + k < r1) ? to_f32(W[(k0 + k) * ws_k + s * ws_s]) : 0.0f;
+        }
+        __syncthreads();
+        if (c < J) {
+            const int64_t kn = r1 - k0 < kSkinnyWK ? r1 - k0 : kSkinnyWK;
+            for (int k = 0; k < kn; ++k) {
+                float xv[E];
+                const T* xr = X + (k0 + k) * J + c;
+                if constexpr (VEC) {
+                    load4(xr, xv);
+                } else {
+                    xv[0] = to_f32(xr[0]);
+                }
+#pragma unroll
+                for (int s = 0; s < SB; ++s)
+#pragma unroll
+                    for (int e = 0; e < E; ++e) acc[s][e] = __builtin_fmaf(xv[e], ws[k][s], acc[s][e]);
+            }
+        }
+    }
+    if (c >= J) return;
+    float* p = part + (b * groups + group) * (int64_t)S * J + c;
+#pragma unroll
+    for (int s = 0; s < SB; ++s)
+        if (s < S) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) p[s * J + e] = acc[s][e];
+        }
+}
+
+__global__ __launch_bounds__(kThreads) void skinny_sums_stage2(const float* __restrict__ part, float* __restrict__ y,
+                                                               int64_t J, int S, int64_t groups, int64_t ys_j,
+                                                               int64_t ys_s, int64_t y_batch) {
+    const int64_t b = blockIdx.y;
+    const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;  // s * J + j
+    if (t >= (int64_t)S * J) return;
+    const int64_t s = t / J, j = t - s * J;
+    const int64_t gs = (int64_t)S * J;
+    const float* p = part + b * groups * gs + t;
+    float acc = p[0];
+    int64_t g = 1;
+    for (; g + 8 <= groups; g += 8) {  // eight loads in flight, added in order
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = p[(g + u) * gs];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = acc + v[u];
+    }
+    for (; g < groups; ++g) acc = acc + p[g * gs];
+    y[b * y_batch + j * ys_j + s * ys_s] = acc;
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 unsigned capped_grid(int64_t blocks) {
@@ -388,6 +549,93 @@ int32_t outer(const T* a, const T* b, float* c, int M, int N, int batch) {
     return ch::check_hip(hipGetLastError(), "outer_kernel");
 }
 
+template <typename T, int SB>
+int32_t skinny_dots_sb(const T* X, const T* V, float* y, int64_t R, int S, int K, int64_t vs_s, int64_t vs_k,
+                       int64_t ys_i, int64_t ys_s, int64_t x_batch, int64_t v_batch, int64_t y_batch, int batch) {
+    const bool vec = K % 4 == 0 && ((uintptr_t)X % (4 * sizeof(T))) == 0;
+    const dim3 g((unsigned)((R + kSkinnyRows - 1) / kSkinnyRows), (unsigned)batch);
+    if (vec)
+        skinny_dots_kernel<T, SB, true><<<g, kThreads, 0, ch::stream()>>>(X, V, y, R, S, K, vs_s, vs_k, ys_i, ys_s,
+                                                                         x_batch, v_batch, y_batch);
+    else
+        skinny_dots_kernel<T, SB, false><<<g, kThreads, 0, ch::stream()>>>(X, V, y, R, S, K, vs_s, vs_k, ys_i, ys_s,
+                                                                          x_batch, v_batch, y_batch);
+    return ch::check_hip(hipGetLastError(), "skinny_dots_kernel");
+}
+
+template <typename T, int SB>
+int32_t skinny_sums_sb(const T* X, const T* W, float* y, int K, int64_t J, int S, int64_t ws_k, int64_t ws_s,
+                       int64_t ys_j, int64_t ys_s, int64_t x_batch, int64_t w_batch, int64_t y_batch, int batch) {
+    const bool vec = J % 4 == 0 && ((uintptr_t)X % (4 * sizeof(T))) == 0;
+    const int E = vec ? 4 : 1;
+    const int64_t nseg = ((J + E - 1) / E + kThreads - 1) / kThreads;
+    // about four blocks per CU over the batch, and partials (S values per
+    // column per group) at most a quarter of the bytes of X
+    int64_t groups = 4LL * ch::num_cus() / (nseg * batch);
+    const int64_t by_bytes = (int64_t)K * (int64_t)sizeof(T) / (16LL * S);
+    if (groups > by_bytes) groups = by_bytes;
+    if (groups < 1) groups = 1;
+    if (groups > K) groups = K;
+    const int64_t rpg = (K + groups - 1) / groups;
+    groups = (K + rpg - 1) / rpg;
+    float* part = (float*)ch::scratch(8, sizeof(float) * (size_t)(batch * groups * S * J));
+    if (!part) return CLEAVE_HIP_ERR_OOM;
+    const dim3 g1((unsigned)(nseg * groups), (unsigned)batch);
+    if (vec)
+        skinny_sums_stage1<T, SB, true><<<g1, kThreads, 0, ch::stream()>>>(X, W, part, K, J, S, ws_k, ws_s, nseg,
+                                                                           groups, rpg, x_batch, w_batch);
+    else
+        skinny_sums_stage1<T, SB, false><<<g1, kThreads, 0, ch::stream()>>>(X, W, part, K, J, S, ws_k, ws_s, nseg,
+                                                                            groups, rpg, x_batch, w_batch);
+    int32_t st = ch::check_hip(hipGetLastError(), "skinny_sums_stage1");
+    if (st != CLEAVE_HIP_OK) return st;
+    const dim3 g2((unsigned)(((int64_t)S * J + kThreads - 1) / kThreads), (unsigned)batch);
+    skinny_sums_stage2<<<g2, kThreads, 0, ch::stream()>>>(part, y, J, S, groups, ys_j, ys_s, y_batch);
+    return ch::check_hip(hipGetLastError(), "skinny_sums_stage2");
+}
+
+template <typename T>
+int32_t skinny_dots(const T* X, const T* V, float* y, int64_t R, int S, int K, int64_t vs_s, int64_t vs_k,
+                    int64_t ys_i, int64_t ys_s, int64_t x_batch, int64_t v_batch, int64_t y_batch, int batch) {
+    if (S <= 4) return skinny_dots_sb<T, 4>(X, V, y, R, S, K, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch, y_batch, batch);
+    if (S <= 8) return skinny_dots_sb<T, 8>(X, V, y, R, S, K, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch, y_batch, batch);
+    if (S <= 16)
+        return skinny_dots_sb<T, 16>(X, V, y, R, S, K, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch, y_batch, batch);
+    return skinny_dots_sb<T, 32>(X, V, y, R, S, K, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch, y_batch, batch);
+}
+
+template <typename T>
+int32_t skinny_sums(const T* X, const T* W, float* y, int K, int64_t J, int S, int64_t ws_k, int64_t ws_s,
+                    int64_t ys_j, int64_t ys_s, int64_t x_batch, int64_t w_batch, int64_t y_batch, int batch) {
+    if (S <= 4) return skinny_sums_sb<T, 4>(X, W, y, K, J, S, ws_k, ws_s, ys_j, ys_s, x_batch, w_batch, y_batch, batch);
+    if (S <= 8) return skinny_sums_sb<T, 8>(X, W, y, K, J, S, ws_k, ws_s, ys_j, ys_s, x_batch, w_batch, y_batch, batch);
+    if (S <= 16)
+        return skinny_sums_sb<T, 16>(X, W, y, K, J, S, ws_k, ws_s, ys_j, ys_s, x_batch, w_batch, y_batch, batch);
+    return skinny_sums_sb<T, 32>(X, W, y, K, J, S, ws_k, ws_s, ys_j, ys_s, x_batch, w_batch, y_batch, batch);
+}
+
+// C (batch x M x N) = op(A) op(B) with min(M, N) <= 32: the matrix operand
+// whose long side is the output's streams once; the small operand is staged
+// in LDS.  A, B, C packed back to back per product.
+template <typename T>
+int32_t skinny_product(const T* a, const T* b, float* c, int M, int N, int K, int batch, int ta, int tb) {
+    const int64_t sa = (int64_t)M * K, sb = (int64_t)K * N, sc = (int64_t)M * N;
+    if (N <= M) {
+        // S = N: C[m][n] = sum_k op(A)[m][k] op(B)[k][n]; B(n, k) at tb ? n*K + k : k*N + n
+        const int64_t vs_s = tb ? K : 1, vs_k = tb ? 1 : N;
+        if (!ta)  // A is M x K: rows of A against the N vectors of B
+            return skinny_dots(a, b, c, M, N, K, vs_s, vs_k, (int64_t)N, 1, sa, sb, sc, batch);
+        // A is stored K x M: C[m][n] = sum_k A[k][m] B(n, k)
+        return skinny_sums(a, b, c, K, M, N, vs_k, vs_s, (int64_t)N, 1, sa, sb, sc, batch);
+    }
+    // S = M: C[m][n] = sum_k A(m, k) op(B)[k][n]; A(m, k) at ta ? k*M + m : m*K + k
+    const int64_t vs_s = ta ? 1 : K, vs_k = ta ? M : 1;
+    if (tb)  // B is stored N x K: rows of B against the M vectors of A
+        return skinny_dots(b, a, c, N, M, K, vs_s, vs_k, 1, (int64_t)N, sb, sa, sc, batch);
+    // B is K x N: C[m][n] = sum_k B[k][n] A(m, k)
+    return skinny_sums(b, a, c, K, N, M, vs_k, vs_s, 1, (int64_t)N, sb, sa, sc, batch);
+}
+
 // C (batch x M x N) = op(A) op(B) with M, N or K equal to 1; A, B, C packed
 // back to back per product.
 template <typename T>
@@ -408,6 +656,13 @@ int32_t vector_product(const T* a, const T* b, float* c, int M, int N, int K, in
 namespace ch {
 int32_t matmul_vector_f32(const float* a, const float* b, float* c, int M, int N, int K, int batch, int ta, int tb) {
     return vector_product(a, b, c, M, N, K, batch, ta, tb);
+}
+int32_t matmul_skinny_f32(const float* a, const float* b, float* c, int M, int N, int K, int batch, int ta, int tb) {
+    return skinny_product(a, b, c, M, N, K, batch, ta, tb);
+}
+int32_t matmul_skinny_bf16(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch, int ta,
+                           int tb) {
+    return skinny_product(a, b, c, M, N, K, batch, ta, tb);
 }
 int32_t matmul_vector_bf16(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch, int ta,
                            int tb) {

@@ -113,3 +113,45 @@ def test_negative_zero_products_become_positive_zero(hip):
     got = hip.matmul(hip.from_numpy(a), hip.from_numpy(b)).numpy()
     want = (np.float32(0.0) + a @ b).astype(np.float32)
     assert np.array_equal(np.signbit(got), np.signbit(want)) and not np.signbit(got[0, 0])
+
+
+# One output dimension of at most 32 (the skinny kernels of gemv.hip): the
+# matrix operand along the long output dimension streams once, the small one
+# is staged in LDS; bucketed at 4, 8, 16 and 32 vectors.
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [
+    (1000, 10, 777), (4096, 3, 4096), (513, 32, 100), (2000, 17, 1),     # N small
+    (10, 4096, 1000), (5, 777, 65536), (31, 2000, 33), (2, 3, 2),        # M small
+    (32, 32, 1000), (7, 9, 300000),                                       # both small, long K
+])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_skinny_shapes_every_entry(hip, oracle, dtype, M, N, K, ta, tb):
+    A, B, Au, Bu = _operands(oracle, dtype, M, N, K, ta, tb, seed=2 * M + 5 * N + K + 2 * ta + tb)
+    got = hip.matmul(hip.from_numpy(A, dtype), hip.from_numpy(B, dtype), trans_a=bool(ta),
+                     trans_b=bool(tb)).numpy()
+    assert got.shape == (M, N)
+    _check(got, Au, Bu, oracle, ta, tb, K, f"{dtype} {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(300, 7, 257), (7, 300, 257)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_skinny_shapes_batched(hip, oracle, dtype, M, N, K, ta, tb):
+    bsz = 5
+    A, B, Au, Bu = _operands(oracle, dtype, M, N, K, ta, tb, seed=3 * M + N + K, batch=bsz)
+    got = hip.matmul_batched(hip.from_numpy(A, dtype), hip.from_numpy(B, dtype), trans_a=bool(ta),
+                             trans_b=bool(tb)).numpy()
+    for i in range(bsz):
+        _check(got[i], Au[i], Bu[i], oracle, ta, tb, K, f"batched {dtype} {M}x{N}x{K} entry {i}")
+
+
+@pytest.mark.parametrize("dtype,off", [("f32", 1), ("bf16", 1)])
+@pytest.mark.parametrize("M,N,K,ta,tb", [(600, 12, 640, 0, 0), (600, 12, 640, 1, 1), (12, 600, 640, 0, 1),
+                                         (12, 600, 640, 1, 0)])
+def test_skinny_shapes_misaligned_views(hip, oracle, dtype, off, M, N, K, ta, tb):
+    A, B, Au, Bu = _operands(oracle, dtype, M, N, K, ta, tb, seed=29 + off)
+    abuf = hip.from_numpy(np.concatenate([np.zeros(off, A.dtype), A.ravel()]), dtype)
+    bbuf = hip.from_numpy(np.concatenate([np.zeros(off, B.dtype), B.ravel()]), dtype)
+    a, b = abuf.sub(off, A.shape), bbuf.sub(off, B.shape)
+    got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    _check(got, Au, Bu, oracle, ta, tb, K, f"{dtype} view at +{off} {M}x{N}x{K}")
