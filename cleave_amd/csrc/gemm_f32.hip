@@ -385,23 +385,42 @@ __global__ __launch_bounds__(256) void sum_slices_kernel(const float* __restrict
                                                          int64_t n, int S) {
     for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < n; i += (int64_t)gridDim.x * 256 * 4) {
         f4 acc = *reinterpret_cast<const f4*>(part + i);
-        for (int s = 1; s < S; ++s) acc = acc + *reinterpret_cast<const f4*>(part + (int64_t)s * n + i);
+        int s = 1;
+        for (; s + 8 <= S; s += 8) {  // eight loads in flight, added in order
+            f4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const f4*>(part + (int64_t)(s + u) * n + i);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = acc + v[u];
+        }
+        for (; s < S; ++s) acc = acc + *reinterpret_cast<const f4*>(part + (int64_t)s * n + i);
         *reinterpret_cast<f4*>(c + i) = acc;
     }
 }
 
-// K slices for a product with fewer 256 x 256 tiles than CUs and a long K:
-// S (a power of two) slices fill the CUs with ping-pong tiles, each slice at
-// least 2048 deep so that the partial sums' extra traffic (S + 1 passes over
-// C) stays a few percent of the product.  1 = no split.  The slices add in
-// order, so results are deterministic.
+// K slices for a product with few tiles and a long K.  S (a power of two)
+// slices are computed as S products into a scratch buffer and added in order
+// (deterministic).  Shapes of 256 x 256 tiles: slices that fill the CUs with
+// ping-pong tiles, each at least 2048 deep, so that the partial sums' extra
+// traffic (S + 1 passes over C) stays a few percent of the product.
+// Otherwise, with fewer 64 x 64 tiles than CUs: up to two workgroups per CU
+// on the small-product or 64 x 64 kernels, each slice at least 512 deep.
+// 1 = no split.
 int split_count(int M, int N, int K) {
-    if (M % 256 || N % 256) return 1;
-    const int64_t tiles = (int64_t)(M / 256) * (N / 256);
+    const int cus = ch::num_cus();
+    if (M % 256 == 0 && N % 256 == 0) {
+        const int64_t tiles = (int64_t)(M / 256) * (N / 256);
+        int S = 1;
+        while (tiles * S * 2 <= cus && K % (16 * S * 2) == 0 && K / (S * 2) >= 2048) S *= 2;
+        // the slices must fill the CUs for the ping-pong kernel to take them
+        if (tiles * S >= cus) return S;
+    }
+    if (M % 64 || N % 64) return 1;
+    const int64_t tiles = (int64_t)(M / 64) * (N / 64);
+    if (tiles >= cus) return 1;
     int S = 1;
-    while (tiles * S * 2 <= ch::num_cus() && K % (16 * S * 2) == 0 && K / (S * 2) >= 2048) S *= 2;
-    // the slices must fill the CUs for the ping-pong kernel to take them
-    return tiles * S >= ch::num_cus() ? S : 1;
+    while (tiles * S * 2 <= 2 * cus && K % (64 * S * 2) == 0 && K / (S * 2) >= 512) S *= 2;
+    return S;
 }
 
 int32_t dispatch(const float* a, const float* b, float* c, int M, int N, int K, int batch,
