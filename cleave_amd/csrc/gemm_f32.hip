@@ -289,6 +289,69 @@ bool launch_pingpong(const float* a, const float* b, float* c, int M, int N, int
     return true;
 }
 
+// c[i] = part[0][i] + part[1][i] + ... + part[S-1][i], in slice order; n is
+// a multiple of 4 and every slice 16-byte aligned.
+__global__ __launch_bounds__(256) void sum_slices_kernel(const float* __restrict__ part, float* __restrict__ c,
+                                                         int64_t n, int S) {
+    for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < n; i += (int64_t)gridDim.x * 256 * 4) {
+        f4 acc = *reinterpret_cast<const f4*>(part + i);
+        int s = 1;
+        for (; s + 8 <= S; s += 8) {  // eight loads in flight, added in order
+            f4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const f4*>(part + (int64_t)(s + u) * n + i);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = acc + v[u];
+        }
+        for (; s < S; ++s) acc = acc + *reinterpret_cast<const f4*>(part + (int64_t)s * n + i);
+        *reinterpret_cast<f4*>(c + i) = acc;
+    }
+}
+
+// K slices for a product with few tiles and a long K.  S (a power of two)
+// slices are computed as S products into a scratch buffer and added in order
+// (deterministic).  Shapes of 256 x 256 tiles: slices that fill the CUs with
+// ping-pong tiles, each at least 2048 deep, so that the partial sums' extra
+// traffic (S + 1 passes over C) stays a few percent of the product.
+// Otherwise, with fewer 64 x 64 tiles than CUs: up to two workgroups per CU
+// on the small-product or 64 x 64 kernels, each slice at least 512 deep.
+// 1 = no split.
+int split_count(int M, int N, int K) {
+    const int cus = ch::num_cus();
+    if (M % 256 == 0 && N % 256 == 0) {
+        const int64_t tiles = (int64_t)(M / 256) * (N / 256);
+        int S = 1;
+        while (tiles * S * 2 <= cus && K % (16 * S * 2) == 0 && K / (S * 2) >= 2048) S *= 2;
+        // the slices must fill the CUs for the ping-pong kernel to take them
+        if (tiles * S >= cus) return S;
+    }
+    if (M % 64 || N % 64) return 1;
+    const int64_t tiles = (int64_t)(M / 64) * (N / 64);
+    if (tiles >= cus) return 1;
+    int S = 1;
+    while (tiles * S * 2 <= 2 * cus && K % (64 * S * 2) == 0 && K / (S * 2) >= 512) S *= 2;
+    return S;
+}
+
+int32_t dispatch(const float* a, const float* b, float* c, int M, int N, int K, int batch, int ta, int tb,
+                 int splits);
+
+// One product (batch 1) as split_count's K slices, when it asks for more than
+// one and the slice buffer can be had: *st is the outcome; false when not split.
+bool try_k_split(const float* a, const float* b, float* c, int M, int N, int K, int ta, int tb, int32_t* st) {
+    if (((uintptr_t)c & 15) != 0) return false;
+    const int S = split_count(M, N, K);
+    float* part = S > 1 ? (float*)ch::scratch_try(9, sizeof(float) * (size_t)S * M * N) : nullptr;
+    if (!part) return false;
+    *st = dispatch(a, b, part, M, N, K, 1, ta, tb, S);
+    if (*st != CLEAVE_HIP_OK) return true;
+    const int64_t n = (int64_t)M * N, blocks = (n / 4 + 255) / 256;
+    const int64_t cap = (int64_t)ch::num_cus() * 8;
+    sum_slices_kernel<<<(unsigned)(blocks < cap ? blocks : cap), 256, 0, ch::stream()>>>(part, c, n, S);
+    *st = ch::check_hip(hipGetLastError(), "sum_slices_kernel");
+    return true;
+}
+
 // The aligned kernels; false when none takes the shape.
 template <bool TA, bool TB>
 bool launch_fast(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
@@ -368,6 +431,7 @@ int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, in
             const int64_t plda = TA ? Mp : Kp, pldb = TB ? Kp : Np;
             const int64_t psA = (int64_t)Mp * Kp, psB = (int64_t)Kp * Np, psC = (int64_t)Mp * Np;
             int32_t s = CLEAVE_HIP_OK;
+            if (batch == 1 && try_k_split(pa, pb, pc, Mp, Np, Kp, TA, TB, &s)) return s;
             if (launch_fast<TA, TB>(pa, pb, pc, Mp, Np, Kp, plda, pldb, Np, batch, psA, psB, psC, &s)) return s;
             return launch_general<TA, TB>(pa, pb, pc, Mp, Np, Kp, plda, pldb, Np, batch, psA, psB, psC);
         };
@@ -379,66 +443,12 @@ int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, in
 // batch >= 1 independent products packed back to back, or (splits > 1, batch
 // must be 1) one product whose K range is cut into `splits` equal slices,
 // slice s writing its partial sum to c + s*M*N.
-// c[i] = part[0][i] + part[1][i] + ... + part[S-1][i], in slice order; n is
-// a multiple of 4 and every slice 16-byte aligned.
-__global__ __launch_bounds__(256) void sum_slices_kernel(const float* __restrict__ part, float* __restrict__ c,
-                                                         int64_t n, int S) {
-    for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < n; i += (int64_t)gridDim.x * 256 * 4) {
-        f4 acc = *reinterpret_cast<const f4*>(part + i);
-        int s = 1;
-        for (; s + 8 <= S; s += 8) {  // eight loads in flight, added in order
-            f4 v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const f4*>(part + (int64_t)(s + u) * n + i);
-#pragma unroll
-            for (int u = 0; u < 8; ++u) acc = acc + v[u];
-        }
-        for (; s < S; ++s) acc = acc + *reinterpret_cast<const f4*>(part + (int64_t)s * n + i);
-        *reinterpret_cast<f4*>(c + i) = acc;
-    }
-}
-
-// K slices for a product with few tiles and a long K.  S (a power of two)
-// slices are computed as S products into a scratch buffer and added in order
-// (deterministic).  Shapes of 256 x 256 tiles: slices that fill the CUs with
-// ping-pong tiles, each at least 2048 deep, so that the partial sums' extra
-// traffic (S + 1 passes over C) stays a few percent of the product.
-// Otherwise, with fewer 64 x 64 tiles than CUs: up to two workgroups per CU
-// on the small-product or 64 x 64 kernels, each slice at least 512 deep.
-// 1 = no split.
-int split_count(int M, int N, int K) {
-    const int cus = ch::num_cus();
-    if (M % 256 == 0 && N % 256 == 0) {
-        const int64_t tiles = (int64_t)(M / 256) * (N / 256);
-        int S = 1;
-        while (tiles * S * 2 <= cus && K % (16 * S * 2) == 0 && K / (S * 2) >= 2048) S *= 2;
-        // the slices must fill the CUs for the ping-pong kernel to take them
-        if (tiles * S >= cus) return S;
-    }
-    if (M % 64 || N % 64) return 1;
-    const int64_t tiles = (int64_t)(M / 64) * (N / 64);
-    if (tiles >= cus) return 1;
-    int S = 1;
-    while (tiles * S * 2 <= 2 * cus && K % (64 * S * 2) == 0 && K / (S * 2) >= 512) S *= 2;
-    return S;
-}
-
 int32_t dispatch(const float* a, const float* b, float* c, int M, int N, int K, int batch,
                  int ta, int tb, int splits) {
     // a dimension of 1: matrix-vector or outer products (gemv.hip)
     if (splits <= 1 && (M == 1 || N == 1 || K == 1)) return ch::matmul_vector_f32(a, b, c, M, N, K, batch, ta, tb);
-    if (splits <= 1 && batch == 1 && ((uintptr_t)c & 15) == 0) {
-        const int S = split_count(M, N, K);
-        float* part = S > 1 ? (float*)ch::scratch_try(9, sizeof(float) * (size_t)S * M * N) : nullptr;
-        if (part) {
-            const int32_t st = dispatch(a, b, part, M, N, K, 1, ta, tb, S);
-            if (st != CLEAVE_HIP_OK) return st;
-            const int64_t n = (int64_t)M * N, blocks = (n / 4 + 255) / 256;
-            const int64_t cap = (int64_t)ch::num_cus() * 8;
-            sum_slices_kernel<<<(unsigned)(blocks < cap ? blocks : cap), 256, 0, ch::stream()>>>(part, c, n, S);
-            return ch::check_hip(hipGetLastError(), "sum_slices_kernel");
-        }
-    }
+    int32_t st = CLEAVE_HIP_OK;
+    if (splits <= 1 && batch == 1 && try_k_split(a, b, c, M, N, K, ta, tb, &st)) return st;
     const int64_t lda = ta ? M : K, ldb = tb ? K : N, ldc = N;
     int64_t sA = (int64_t)M * K, sB = (int64_t)K * N, sC = (int64_t)M * N;
     int kk = K;

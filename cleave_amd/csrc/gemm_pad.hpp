@@ -4,7 +4,7 @@
 // of their k-tile and 16-byte aligned rows.  A large product that misses
 // those runs on zero-padded copies instead: each operand that does not
 // already fit is copied, in the caller's layout, into a buffer whose extents
-// are rounded up (K to 64, M and N to 128 or 256) with zeros past the valid
+// are rounded up (K to 64 or 2048, M and N to 128 or 256) with zeros past the valid
 // region; the product is computed on the padded shape; and, when M or N was
 // rounded up, the valid M x N corner of the padded C is copied out.
 //
@@ -37,7 +37,7 @@ struct PadModel {
     double min256;    // fewest 256 x 256 tiles the kernels take, per CU
 };
 
-// Padded shape: K to a multiple of 64; M and N to multiples of 128, or of 256
+// Padded shape: K to a multiple of 64 (of 2048 from 16384); M and N to multiples of 128, or of 256
 // when that gives the 256 x 256 kernels enough tiles (model.min256 per CU)
 // and is estimated faster.
 // Time ~ padded area / efficiency, and, where a CU holds one workgroup, / the
@@ -48,7 +48,9 @@ inline PadPlan pad_plan(int M, int N, int K, int batch, bool ta, bool tb, const 
                         int esz, int cus, const PadModel& model) {
     PadPlan p{};
     p.M = M, p.N = N, p.K = K;
-    const int64_t kp = pad_up(K, 64);
+    // a long K goes to a multiple of 2048 (at most 1/8 more), so that the
+    // padded product can still be cut into K slices of equal depth
+    const int64_t kp = pad_up(K, K >= 16384 ? 2048 : 64);
     const int64_t m2 = pad_up(M, 256), n2 = pad_up(N, 256), m1 = pad_up(M, 128), n1 = pad_up(N, 128);
     auto cost = [](double area, int64_t tiles, int64_t per_round, double eff) {
         const int64_t rounds = (tiles + per_round - 1) / per_round;

@@ -662,3 +662,17 @@ def test_f32_k_split_every_entry(hip, oracle, M, N, K, ta, tb):
     ref = oracle.matmul(Ak, Bk, trans_b=True, threads=16)
     den = np.abs(Ak) @ np.abs(Bk).T
     assert_gemm_close(got, ref, den, K, f"k-split {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(100, 100, 100000), (70, 300, 30000)])
+def test_f32_ragged_long_k_every_entry(hip, oracle, M, N, K, ta, tb):
+    # Ragged and long K: zero-padded copies (to 128 x 128 or 128 x 384), then
+    # K slices of the padded product; every entry against the loop.
+    A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=M + N + K + ta)
+    got = hip.matmul(hip.from_numpy(A), hip.from_numpy(B), trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    Ak = np.ascontiguousarray(Au.T if ta else Au)
+    Bk = np.ascontiguousarray(Bu if tb else Bu.T)
+    ref = oracle.matmul(Ak, Bk, trans_b=True, threads=16)
+    den = np.abs(Ak).astype(np.float64) @ np.abs(Bk).astype(np.float64).T
+    assert_gemm_close(got, ref, den, K, f"ragged long-K {M}x{N}x{K} ta={ta} tb={tb}")
