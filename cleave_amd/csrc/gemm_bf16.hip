@@ -29,6 +29,7 @@ int32_t matmul_vector_bf16(const uint16_t* a, const uint16_t* b, float* c, int M
                            int tb);
 int32_t matmul_skinny_bf16(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch, int ta,
                            int tb);
+int32_t sum_slices_f32(const float* part, float* c, int64_t n, int S);
 }
 
 namespace {
@@ -122,8 +123,9 @@ template <bool TA, bool TB, bool EDGE>
 __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const uint16_t* __restrict__ A,
                                                        const uint16_t* __restrict__ B,
                                                        float* __restrict__ C, int M, int N, int K,
-                                                       int64_t strideA, int64_t strideB,
-                                                       int64_t strideC, int tiles_m, int tiles_n) {
+                                                       int64_t lda, int64_t ldb, int64_t strideA,
+                                                       int64_t strideB, int64_t strideC, int tiles_m,
+                                                       int tiles_n) {
     constexpr bool AK = !TA;  // A k-contiguous when stored M x K
     constexpr bool BKC = TB;  // B k-contiguous when stored N x K
     __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][PITCH];
@@ -137,7 +139,6 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const uint16_t* __restric
     A += (int64_t)blockIdx.y * strideA;
     B += (int64_t)blockIdx.y * strideB;
     C += (int64_t)blockIdx.y * strideC;
-    const int64_t lda = TA ? M : K, ldb = TB ? K : N;
 
     Stage<AK> sa;
     Stage<BKC> sb;
@@ -196,21 +197,34 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const uint16_t* __restric
             }
 }
 
+// Operand pitches and per-product strides, in elements: packed products, or
+// the K slices of one product (gemm_bf16's split below).
+struct Strides {
+    int64_t lda, ldb, sA, sB, sC;
+};
 template <bool TA, bool TB>
-int32_t launch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch) {
-    const int64_t sA = (int64_t)M * K, sB = (int64_t)K * N, sC = (int64_t)M * N;
+Strides packed(int M, int N, int K) {
+    return {TA ? M : K, TB ? K : N, (int64_t)M * K, (int64_t)K * N, (int64_t)M * N};
+}
+// Every product's operand base 16-byte aligned.
+bool bases_aligned(const uint16_t* a, const uint16_t* b, const Strides& s) {
+    return ((uintptr_t)a & 15) == 0 && ((uintptr_t)b & 15) == 0 && s.sA % 8 == 0 && s.sB % 8 == 0;
+}
+
+template <bool TA, bool TB>
+int32_t launch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch, const Strides& s) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)batch);
     // 4-byte (transposed) or 16-byte (k-contiguous) global reads need the
     // matching alignment of every row start.
-    const bool fast = (M % BM == 0) && (N % BN == 0) && (K % BK == 0) &&
-                      ((uintptr_t)a & 15) == 0 && ((uintptr_t)b & 15) == 0;
+    const bool fast = (M % BM == 0) && (N % BN == 0) && (K % BK == 0) && s.lda % 8 == 0 && s.ldb % 8 == 0 &&
+                      bases_aligned(a, b, s);
     if (fast)
-        gemm_bf16_kernel<TA, TB, false><<<grid, NT, 0, ch::stream()>>>(a, b, c, M, N, K, sA, sB, sC,
-                                                                       tiles_m, tiles_n);
+        gemm_bf16_kernel<TA, TB, false><<<grid, NT, 0, ch::stream()>>>(a, b, c, M, N, K, s.lda, s.ldb, s.sA, s.sB,
+                                                                       s.sC, tiles_m, tiles_n);
     else
-        gemm_bf16_kernel<TA, TB, true><<<grid, NT, 0, ch::stream()>>>(a, b, c, M, N, K, sA, sB, sC,
-                                                                      tiles_m, tiles_n);
+        gemm_bf16_kernel<TA, TB, true><<<grid, NT, 0, ch::stream()>>>(a, b, c, M, N, K, s.lda, s.ldb, s.sA, s.sB,
+                                                                      s.sC, tiles_m, tiles_n);
     CH_LAUNCHED("gemm_bf16_kernel");
     return CLEAVE_HIP_OK;
 }
@@ -218,16 +232,16 @@ int32_t launch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int
 // Large-tile kernel (gemm_bf16_tiled.hpp) for shapes that divide its tile.
 // Returns false when the shape or alignment does not fit.
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int MI, bool TA, bool TB>
-bool launch_tiled(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
+bool launch_tiled(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch, const Strides& s,
                   int32_t* status) {
     using P = ch::Bf16Tiled<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI>;
-    const int64_t lda = TA ? M : K, ldb = TB ? K : N;
-    if (!P::fits(M, N, K, lda, ldb) || ((uintptr_t)a & 15) || ((uintptr_t)b & 15)) return false;
+    const int64_t lda = s.lda, ldb = s.ldb;
+    if (!P::fits(M, N, K, lda, ldb) || !bases_aligned(a, b, s)) return false;
     const int tiles_m = M / BM, tiles_n = N / BN;
     if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
     dim3 grid((unsigned)(tiles_m * tiles_n * batch));
     ch::gemm_bf16_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI><<<grid, P::THREADS, 0, ch::stream()>>>(
-        a, b, c, M, N, K, lda, ldb, (int64_t)M * K, (int64_t)K * N, (int64_t)M * N, tiles_m, tiles_n, batch);
+        a, b, c, M, N, K, lda, ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch);
     *status = ch::check_hip(hipGetLastError(), "gemm_bf16_tiled_kernel");
     return true;
 }
@@ -236,10 +250,10 @@ bool launch_tiled(const uint16_t* a, const uint16_t* b, float* c, int M, int N, 
 // of five k-tiles (all 160 KiB of LDS).
 template <bool TA, bool TB>
 bool launch_pingpong(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
-                     int32_t* status) {
+                     const Strides& s, int32_t* status) {
     using P = ch::Bf16PingPong<!TA, TB>;
-    const int64_t lda = TA ? M : K, ldb = TB ? K : N;
-    if (!P::fits(M, N, K, lda, ldb) || ((uintptr_t)a & 15) || ((uintptr_t)b & 15)) return false;
+    const int64_t lda = s.lda, ldb = s.ldb;
+    if (!P::fits(M, N, K, lda, ldb) || !bases_aligned(a, b, s)) return false;
     const int tiles_m = M / P::BM, tiles_n = N / P::BN;
     if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
     dim3 grid((unsigned)(tiles_m * tiles_n * batch));
@@ -247,7 +261,7 @@ bool launch_pingpong(const uint16_t* a, const uint16_t* b, float* c, int M, int 
     // operands step 64 bytes per k-tile, m/n-contiguous ones 32 rows
     const uint64_t last_a = (uint64_t)K * (TA ? (uint64_t)lda * 2 : 2);
     const uint64_t last_b = (uint64_t)K * (TB ? 2 : (uint64_t)ldb * 2);
-    const int64_t sa = (int64_t)M * K, sb = (int64_t)K * N, sc = (int64_t)M * N;
+    const int64_t sa = s.sA, sb = s.sB, sc = s.sC;
     if (last_a < (1ull << 32) && last_b < (1ull << 32))
         ch::gemm_bf16_pingpong_kernel<!TA, TB, true><<<grid, P::THREADS, 0, ch::stream()>>>(
             a, b, c, M, N, K, lda, ldb, sa, sb, sc, tiles_m, tiles_n, batch);
@@ -262,14 +276,14 @@ bool launch_pingpong(const uint16_t* a, const uint16_t* b, float* c, int M, int 
 // kernel that copies such an operand two k-tiles at a time, as whole 128-byte
 // rows (gemm_bf16_pingpong.hpp; for A·Bᵀ, A is the paired one).
 template <bool TA, bool TB>
-bool launch_pairs(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
+bool launch_pairs(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch, const Strides& s,
                   int32_t* status) {
     if constexpr (TA && !TB) {  // Aᵀ·B: no k-contiguous operand to pair
         return false;
     } else {
         using P = ch::Bf16PingPongPairs<!TA, TB>;
-        const int64_t lda = TA ? M : K, ldb = TB ? K : N;
-        if (!P::fits(M, N, K, lda, ldb) || ((uintptr_t)a & 15) || ((uintptr_t)b & 15)) return false;
+        const int64_t lda = s.lda, ldb = s.ldb;
+        if (!P::fits(M, N, K, lda, ldb) || !bases_aligned(a, b, s)) return false;
         const int tiles_m = M / P::BM, tiles_n = N / P::BN;
         if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
         // one workgroup per CU (all of the LDS), each looping over its tiles;
@@ -279,7 +293,7 @@ bool launch_pairs(const uint16_t* a, const uint16_t* b, float* c, int M, int N, 
         const int resident = cus >= 8 ? cus / 8 * 8 : (cus > 0 ? cus : 1);
         dim3 grid((unsigned)(total < resident ? total : resident));
         ch::gemm_bf16_pingpong_pairs_kernel<!TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
-            a, b, c, M, N, K, lda, ldb, (int64_t)M * K, (int64_t)K * N, (int64_t)M * N, tiles_m, tiles_n, batch);
+            a, b, c, M, N, K, lda, ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch);
         *status = ch::check_hip(hipGetLastError(), "gemm_bf16_pingpong_pairs_kernel");
         return true;
     }
@@ -287,7 +301,8 @@ bool launch_pairs(const uint16_t* a, const uint16_t* b, float* c, int M, int N, 
 
 // The aligned kernels; false when none takes the shape.
 template <bool TA, bool TB>
-bool launch_fast(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch, int32_t* st) {
+bool launch_fast(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch, const Strides& s,
+                 int32_t* st) {
     // 256 x 256 tiles, when there are enough of them (below): the ping-pong
     // kernel (k-tiles of 32), or the tiled kernel (k-tiles of 64).  With one
     // round of tiles and K up to 512 the two measured equal (64 x 512^3:
@@ -307,10 +322,10 @@ bool launch_fast(const uint16_t* a, const uint16_t* b, float* c, int M, int N, i
     const int64_t big_tiles = (int64_t)(M / 256) * (N / 256) * batch;
     if (big_tiles * 2 >= cus) {
         const bool short_single_round = big_tiles <= cus && K <= 512;
-        if (!short_single_round && launch_pairs<TA, TB>(a, b, c, M, N, K, batch, st)) return true;
-        if (!short_single_round && launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, st)) return true;
-        if (launch_tiled<256, 256, 64, 2, 4, 2, 16, TA, TB>(a, b, c, M, N, K, batch, st)) return true;
-        if (launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, st)) return true;
+        if (!short_single_round && launch_pairs<TA, TB>(a, b, c, M, N, K, batch, s, st)) return true;
+        if (!short_single_round && launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, s, st)) return true;
+        if (launch_tiled<256, 256, 64, 2, 4, 2, 16, TA, TB>(a, b, c, M, N, K, batch, s, st)) return true;
+        if (launch_pingpong<TA, TB>(a, b, c, M, N, K, batch, s, st)) return true;
     }
     // 128 x 128 x 64 tiles, 4 waves of 64 x 64 in 32 x 32 x 16 MFMAs.  Up to
     // one round of them: three LDS stages (96 KiB, one workgroup per CU), or,
@@ -322,11 +337,39 @@ bool launch_fast(const uint16_t* a, const uint16_t* b, float* c, int M, int N, i
     const int64_t tiles128 = (int64_t)(M / 128) * (N / 128) * batch;
     if (tiles128 <= cus) {
         if constexpr (!TA) {
-            if (launch_tiled<64, 128, 64, 2, 2, 3, 32, TA, TB>(a, b, c, M, N, K, batch, st)) return true;
+            if (launch_tiled<64, 128, 64, 2, 2, 3, 32, TA, TB>(a, b, c, M, N, K, batch, s, st)) return true;
         }
-        return launch_tiled<128, 128, 64, 2, 2, 3, 32, TA, TB>(a, b, c, M, N, K, batch, st);
+        return launch_tiled<128, 128, 64, 2, 2, 3, 32, TA, TB>(a, b, c, M, N, K, batch, s, st);
     }
-    return launch_tiled<128, 128, 64, 2, 2, 2, 32, TA, TB>(a, b, c, M, N, K, batch, st);
+    return launch_tiled<128, 128, 64, 2, 2, 2, 32, TA, TB>(a, b, c, M, N, K, batch, s, st);
+}
+
+// K slices of one product with few 128 x 128 tiles and a long K: up to one
+// workgroup per CU, each slice at least 1024 deep (the slices' partial sums
+// are then small next to the product).  1 = no split.
+int split_count(int M, int N, int K) {
+    const int cus = ch::num_cus();
+    const int64_t tiles = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+    if (tiles * 2 > cus) return 1;
+    int S = 1;
+    while (tiles * S * 2 <= cus && K % (64 * S * 2) == 0 && K / (S * 2) >= 1024) S *= 2;
+    return S;
+}
+
+// One product as split_count's K slices into a scratch buffer, added in
+// order (ch::sum_slices_f32, deterministic); false when not split.
+template <bool TA, bool TB>
+bool try_k_split(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int32_t* st) {
+    const int64_t n = (int64_t)M * N;
+    if (((uintptr_t)c & 15) != 0 || n % 4 != 0) return false;
+    const int S = split_count(M, N, K);
+    float* part = S > 1 ? (float*)ch::scratch_try(10, sizeof(float) * (size_t)(S * n)) : nullptr;
+    if (!part) return false;
+    const int kk = K / S;
+    const Strides sl{TA ? M : K, TB ? K : N, TA ? (int64_t)kk * M : kk, TB ? kk : (int64_t)kk * N, n};
+    if (!launch_fast<TA, TB>(a, b, part, M, N, kk, S, sl, st)) *st = launch<TA, TB>(a, b, part, M, N, kk, S, sl);
+    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, n, S);
+    return true;
 }
 
 // Products of at least this many flops (2 M N K per product) that no aligned
@@ -342,7 +385,7 @@ constexpr ch::PadModel kPadModel{0.55, 0.31, true, 0.5};
 template <bool TA, bool TB>
 int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch) {
     int32_t st = CLEAVE_HIP_OK;
-    if (launch_fast<TA, TB>(a, b, c, M, N, K, batch, &st)) return st;
+    if (launch_fast<TA, TB>(a, b, c, M, N, K, batch, packed<TA, TB>(M, N, K), &st)) return st;
     // one output dimension of at most 32: stream the long operand (gemv.hip);
     // tiny products (under 2^20 flops) stay on the general kernel (one launch)
     if ((M <= 32 || N <= 32) && 2.0 * M * N * K * batch >= (1u << 20))
@@ -351,18 +394,27 @@ int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N,
         const ch::PadPlan p = ch::pad_plan(M, N, K, batch, TA, TB, a, b, 2, ch::num_cus(), kPadModel);
         auto gemm = [batch](const uint16_t* pa, const uint16_t* pb, float* pc, int Mp, int Np, int Kp) {
             int32_t s = CLEAVE_HIP_OK;
-            if (launch_fast<TA, TB>(pa, pb, pc, Mp, Np, Kp, batch, &s)) return s;
-            return launch<TA, TB>(pa, pb, pc, Mp, Np, Kp, batch);
+            if (batch == 1 && try_k_split<TA, TB>(pa, pb, pc, Mp, Np, Kp, &s)) return s;
+            if (launch_fast<TA, TB>(pa, pb, pc, Mp, Np, Kp, batch, packed<TA, TB>(Mp, Np, Kp), &s)) return s;
+            return launch<TA, TB>(pa, pb, pc, Mp, Np, Kp, batch, packed<TA, TB>(Mp, Np, Kp));
         };
         if (ch::run_padded(p, a, b, c, batch, TA, TB, gemm, &st)) return st;
     }
-    return launch<TA, TB>(a, b, c, M, N, K, batch);
+    return launch<TA, TB>(a, b, c, M, N, K, batch, packed<TA, TB>(M, N, K));
 }
 
 int32_t dispatch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
                  int ta, int tb) {
     // a dimension of 1: matrix-vector or outer products (gemv.hip)
     if (M == 1 || N == 1 || K == 1) return ch::matmul_vector_bf16(a, b, c, M, N, K, batch, ta, tb);
+    // few tiles and a long K: K slices
+    int32_t st = CLEAVE_HIP_OK;
+    if (batch == 1) {
+        if (!ta && !tb && try_k_split<false, false>(a, b, c, M, N, K, &st)) return st;
+        if (!ta && tb && try_k_split<false, true>(a, b, c, M, N, K, &st)) return st;
+        if (ta && !tb && try_k_split<true, false>(a, b, c, M, N, K, &st)) return st;
+        if (ta && tb && try_k_split<true, true>(a, b, c, M, N, K, &st)) return st;
+    }
     if (!ta && !tb) return launch_any<false, false>(a, b, c, M, N, K, batch);
     if (!ta && tb) return launch_any<false, true>(a, b, c, M, N, K, batch);
     if (ta && !tb) return launch_any<true, false>(a, b, c, M, N, K, batch);

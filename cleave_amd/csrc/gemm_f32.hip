@@ -336,6 +336,20 @@ int split_count(int M, int N, int K) {
 int32_t dispatch(const float* a, const float* b, float* c, int M, int N, int K, int batch, int ta, int tb,
                  int splits);
 
+}  // namespace
+
+namespace ch {
+// c = the S slices of part added in order; n % 4 == 0, c and part 16-byte
+// aligned.  Also the bf16 products' K slices (gemm_bf16.hip).
+int32_t sum_slices_f32(const float* part, float* c, int64_t n, int S) {
+    const int64_t blocks = (n / 4 + 255) / 256, cap = (int64_t)ch::num_cus() * 8;
+    sum_slices_kernel<<<(unsigned)(blocks < cap ? blocks : cap), 256, 0, ch::stream()>>>(part, c, n, S);
+    return ch::check_hip(hipGetLastError(), "sum_slices_kernel");
+}
+}  // namespace ch
+
+namespace {
+
 // One product (batch 1) as split_count's K slices, when it asks for more than
 // one and the slice buffer can be had: *st is the outcome; false when not split.
 bool try_k_split(const float* a, const float* b, float* c, int M, int N, int K, int ta, int tb, int32_t* st) {
@@ -344,11 +358,7 @@ bool try_k_split(const float* a, const float* b, float* c, int M, int N, int K, 
     float* part = S > 1 ? (float*)ch::scratch_try(9, sizeof(float) * (size_t)S * M * N) : nullptr;
     if (!part) return false;
     *st = dispatch(a, b, part, M, N, K, 1, ta, tb, S);
-    if (*st != CLEAVE_HIP_OK) return true;
-    const int64_t n = (int64_t)M * N, blocks = (n / 4 + 255) / 256;
-    const int64_t cap = (int64_t)ch::num_cus() * 8;
-    sum_slices_kernel<<<(unsigned)(blocks < cap ? blocks : cap), 256, 0, ch::stream()>>>(part, c, n, S);
-    *st = ch::check_hip(hipGetLastError(), "sum_slices_kernel");
+    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, (int64_t)M * N, S);
     return true;
 }
 
