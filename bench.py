@@ -225,6 +225,12 @@ def cpu_secondary(orc, name, budget_s, **kw):
         rows, dt = cpu_rows(lambda r0, r1: orc.matmul_bf16_rows(A, B, k, k, k, r0, r1), k, budget_s)
         return _cpu_entry(round(2.0 * rows * k * k / dt / 1e9, 4), "GFLOP/s",
                           f"rows 1..{rows} of product 0 of {bs}, restated f32 loop on upcast bf16, {dt:.1f} s")
+    if name == "matvec_f32_65536x4096":
+        A, x, m, k = kw["A"], kw["x"], kw["m"], kw["k"]
+        rows, dt = cpu_rows(lambda r0, r1: orc.matmul_rows(A, x, m, 1, k, r0, r1, False, False), m, budget_s)
+        return _cpu_entry(round(rows * k * 4 / dt / 1e9, 4), "GB/s",
+                          f"rows 1..{rows} of the {m} x {k} matrix against the vector, restated k-ascending "
+                          f"loop, {dt:.2f} s (matrix bytes per second)")
     if name == "mlp_step_65536x1024x4096":
         X, y, W1, W2, B_ = kw["X"], kw["y"], kw["W1"], kw["W2"], kw["B"]
         # a step costs f (the SGD update, batch-independent) + rows * r; two
@@ -618,6 +624,23 @@ def main():
         log(f"mlp step through the tape: {mlp_steps / wall_s:.2f} steps/s ({ev:.2f} ms)")
         del X_, Y_, w2c
         del x, yv, w1, w2
+        # a matrix-vector product (a2 at N = 1: the reference's matmul by a
+        # column vector, gemv.hip), HBM-bound on the matrix
+        mv_m, mv_k = 65536, 4096
+        mva = ca.fill_normal(ca.empty((mv_m, mv_k)), seed=405)
+        mvx = ca.fill_normal(ca.empty((mv_k, 1)), seed=406)
+        mvy = ca.empty((mv_m, 1))
+        wall_s, ev = timed(ca, lambda: ca.matmul(mva, mvx, out=mvy), sec_steps, 2, 0.2)
+        mv_bytes = (mv_m * mv_k + mv_k + mv_m) * 4
+        secondary["matvec_f32_65536x4096"] = {
+            "ms": round(ev, 4), "GB/s": round(mv_bytes / (ev * 1e-3) / 1e9, 1),
+            "frac_hbm": round(mv_bytes / (ev * 1e-3) / 1e9 / PEAK_HBM, 4),
+            "note": "one wave-slice per row, 16-byte loads, shuffle-tree sums (gemv.hip)"}
+        log(f"matvec: {mv_bytes / (ev * 1e-3) / 1e9:.0f} GB/s")
+        if want_cpu:
+            secondary["matvec_f32_65536x4096"]["cpu_baseline"] = cpu_secondary(
+                orc, "matvec_f32_65536x4096", cb, A=mva.numpy(), x=mvx.numpy(), m=mv_m, k=mv_k)
+        del mva, mvx, mvy
         # escape-count map + u64 sum (config 3)
         g = 16384
         d = np.float32(3.0 / g)
