@@ -11,11 +11,12 @@ Prints ONE JSON line on stdout:
                library stream around the timed launches, vs 157.3 TFLOP/s FP32 MFMA
   cpu_baseline the oracle's reference-faithful i-j-k loop, one core, on a row band
                of the same product, extrapolated to GFLOP/s
-  secondary    the other BASELINE configs (bf16 8192^3, batched bf16, f32 A B^T /
-               A^T B, MLP steps/s, escape-count map, u64 count sum) and the maps,
-               reductions and row-broadcast bias, each with its own HIP-event
-               roofline figure and (unless --no-cpu) a single-core CPU baseline
-               from the restated loops on a bounded sample
+  secondary    the other BASELINE configs (f32 256^3, bf16 8192^3, batched bf16,
+               f32 A B^T / A^T B, MLP steps/s, escape-count map, u64 count sum), the
+               MLP step through the reverse-mode tape, a matrix-vector product, and
+               the maps, reductions and row-broadcast bias, each with its own
+               HIP-event roofline figure and (unless --no-cpu) a single-core CPU
+               baseline from the restated loops on a bounded sample
   vendor_same_device
                (--vendor only) torch.matmul / torch.bmm on the GEMM shapes, timed the
                same way in a child process on the same device
