@@ -407,9 +407,10 @@ int32_t dispatch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, i
                  int ta, int tb) {
     // a dimension of 1: matrix-vector or outer products (gemv.hip)
     if (M == 1 || N == 1 || K == 1) return ch::matmul_vector_bf16(a, b, c, M, N, K, batch, ta, tb);
-    // few tiles and a long K: K slices
+    // few tiles and a long K: K slices (an output dimension of at most 32
+    // streams its long operand instead, in launch_any)
     int32_t st = CLEAVE_HIP_OK;
-    if (batch == 1) {
+    if (batch == 1 && M > 32 && N > 32) {
         if (!ta && !tb && try_k_split<false, false>(a, b, c, M, N, K, &st)) return st;
         if (!ta && tb && try_k_split<false, true>(a, b, c, M, N, K, &st)) return st;
         if (ta && !tb && try_k_split<true, false>(a, b, c, M, N, K, &st)) return st;

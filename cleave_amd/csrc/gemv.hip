@@ -310,163 +310,308 @@ __global__ __launch_bounds__(kThreads) void outer_kernel(const T* __restrict__ a
 
 // ---- skinny products: one output dimension of at most 32 --------------------------
 //
-// Y[i][s] = sum_k X[i][k] V(s, k) for i < R, s < S <= SB, with X k-contiguous
-// (pitch K) and V(s, k) = V[s*vs_s + k*vs_k].  A workgroup owns 32 rows of X,
-// eight lanes per row; it walks K in chunks of 256, staging V's chunk in LDS
-// as [SB][k] (zeros past S and K), and lane l of a row takes the 16-byte
-// pieces l, l + 8, ... of the chunk, so eight lanes read one 128-byte line.
-// Staged as [k][SB], the lanes' reads of four k apart fell on the same banks:
-// 65536 x N x 4096 took 0.93 ms at N = 10 and 1.86 ms at N = 32.
-// Each value of X meets SB values of V (fma); the row's eight lanes are then
-// added by a shuffle tree.  Batch entries along blockIdx.y.
-constexpr int kSkinnyKC = 256, kSkinnyRows = kThreads / 8;
+// Y[r][s] = sum_k X(r, k) V(s, k) for r < R, s < S <= 32, with X(r, k) =
+// X[r*xs_r + k*xs_k] and V(s, k) = V[s*vs_s + k*vs_k]: X is the operand along
+// the long output dimension, stored k-contiguous (xs_k == 1) or r-contiguous,
+// and V the small one, in either layout.  On 128 x 128 tiles these products
+// wasted most of every MFMA; with VALU fmas (each X value meeting its S values
+// of V) they were bound by the fmas and the LDS reads of V from about 10
+// vectors on (65536 x 32 x 4096 f32: 706 us, 0.19 of HBM; here 248 us).
+//
+// A wave owns RB blocks of MR rows and all MR columns over one group of k: the
+// MFMA's A operand is X, its B operand V, which each lane loads straight from
+// memory (V is small and stays in L2).  Columns past S and rows past R read
+// clamped addresses; the MFMA keeps rows and columns apart, so what they
+// compute is never stored.  k past K reads as zero in both operands.  One
+// group per wave writes Y; several write their blocks to part[b][group][rb] in
+// accumulator order and skinny_mfma_fold adds the groups in ascending order.
+// The sums run in an order fixed by the shape.
+//
+// Instruction per type and MR (lane l; q = the lane's k quarter or half):
+//   f32, 32: v_mfma_f32_32x32x2f32, a block of 8 k in four steps, half-wave
+//            q = l/32 taking k = 4q + e at step e; accumulator v of lane l is
+//            column l%32, row 8(v/4) + 4q + v%4;
+//   f32, 16: v_mfma_f32_16x16x4f32, a block of 16 k in four steps, quarter
+//            q = l/16 taking k = 4q + e; accumulator v: column l%16, row 4q + v;
+//   bf16, 32: v_mfma_f32_32x32x16_bf16, one step per block of 16 k, half-wave
+//            q taking k = 8q .. 8q+7; accumulators as f32, 32.
+// At 32 columns a 32 x 32 x 2 step takes 64 cycles for 256 bytes of f32 X,
+// about the HBM's share of a SIMD; the 16 x 16 x 4 form moves twice that.
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef short s8v __attribute__((ext_vector_type(8)));
+typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
 
-template <typename T, int SB, bool VEC>
-__global__ __launch_bounds__(kThreads) void skinny_dots_kernel(
-    const T* __restrict__ X, const T* __restrict__ V, float* __restrict__ y, int64_t R, int S, int K,
-    int64_t vs_s, int64_t vs_k, int64_t ys_i, int64_t ys_s, int64_t x_batch, int64_t v_batch, int64_t y_batch) {
-    // rows padded by 4 floats: the staging writes of consecutive s then spread over the banks
-    __shared__ __attribute__((aligned(16))) float vs[SB][kSkinnyKC + 4];
+template <typename T, int MR>
+struct SkMfma;
+// LINES: 128-byte lines of each row per staged group (XS), measured per form
+template <>
+struct SkMfma<float, 32> {
+    static constexpr int KBLK = 8, ACC = 16, LINES = 2;
+    typedef f4v frag;
+    typedef f16v acc_t;
+    __device__ static int kofs(int lane) { return 4 * (lane >> 5); }
+    __device__ static int row(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
+    __device__ static void mma(const frag& a, const frag& b, acc_t& c) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], b[e], c, 0, 0, 0);
+    }
+};
+template <>
+struct SkMfma<float, 16> {
+    static constexpr int KBLK = 16, ACC = 4, LINES = 1;
+    typedef f4v frag;
+    typedef f4v acc_t;
+    __device__ static int kofs(int lane) { return 4 * (lane >> 4); }
+    __device__ static int row(int v, int lane) { return 4 * (lane >> 4) + v; }
+    __device__ static void mma(const frag& a, const frag& b, acc_t& c) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], c, 0, 0, 0);
+    }
+};
+template <>
+struct SkMfma<uint16_t, 32> {
+    static constexpr int KBLK = 16, ACC = 16, LINES = 2;
+    typedef s8v frag;
+    typedef f16v acc_t;
+    __device__ static int kofs(int lane) { return 8 * (lane >> 5); }
+    __device__ static int row(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
+    __device__ static void mma(const frag& a, const frag& b, acc_t& c) {
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf8v, a), __builtin_bit_cast(bf8v, b), c, 0, 0,
+                                                    0);
+    }
+};
+
+// E values p[0], p[st], ... as one fragment: a 16-byte load (VEC: st == 1 and p
+// 16-byte aligned) or E loads.
+template <bool VEC>
+__device__ __forceinline__ f4v sk_run(const float* p, int64_t st) {
+    if constexpr (VEC) return *reinterpret_cast<const f4v*>(p);
+    f4v v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = p[e * st];
+    return v;
+}
+template <bool VEC>
+__device__ __forceinline__ s8v sk_run(const uint16_t* p, int64_t st) {
+    if constexpr (VEC) return *reinterpret_cast<const s8v*>(p);
+    s8v v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (short)p[e * st];
+    return v;
+}
+// The same for the last, partial block: values at k + e >= K are zero.
+__device__ __forceinline__ f4v sk_run_tail(const float* p, int64_t st, int64_t k, int K) {
+    f4v v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = k + e < K ? p[e * st] : 0.0f;
+    return v;
+}
+__device__ __forceinline__ s8v sk_run_tail(const uint16_t* p, int64_t st, int64_t k, int K) {
+    s8v v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = k + e < K ? (short)p[e * st] : (short)0;
+    return v;
+}
+
+constexpr int kSkMfmaUnroll = 4;  // blocks of k whose loads are issued together (unstaged X)
+
+// X k-contiguous with 16-byte aligned rows (XS): the wave's 32 rows are staged
+// through its own LDS, F::LINES x 128 bytes of each row at a time, so that each
+// load instruction reads whole 128-byte lines (8 rows of 8 lanes); read
+// straight into the MFMA layout, an instruction took 16-32 rows at 32-64
+// bytes each and the kernel ran at 0.40-0.54 of HBM.  Row r's 16-byte chunk c
+// sits in slot c ^ ((r >> 1) & 7): sixteen lanes reading one chunk of 16
+// consecutive rows, or writing two rows, then cover all 64 banks once.  Only
+// the wave touches its region, and a wave's LDS instructions execute in
+// order, so no barrier is needed; the asm statements keep the compiler from
+// moving the reads above the writes (or the next writes above the reads).
+template <typename T, int MR, int RB, bool XS, bool VV>
+__global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
+    const T* __restrict__ X, const T* __restrict__ V, float* __restrict__ y, float* __restrict__ part, int64_t R,
+    int S, int K, int64_t xs_r, int64_t xs_k, int64_t vs_s, int64_t vs_k, int64_t ys_i, int64_t ys_s,
+    int64_t x_batch, int64_t v_batch, int64_t y_batch, int64_t nrb, int groups, int bpg) {
+    using F = SkMfma<T, MR>;
+    using frag = typename F::frag;
+    static_assert(MR * RB == 32, "a wave owns 32 rows");
+    constexpr int U = kSkMfmaUnroll;
+    __shared__ f4v stage[XS ? kThreads / 64 : 1][XS ? 256 * F::LINES : 1];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t task = (int64_t)blockIdx.x * (kThreads / 64) + wave;
+    if (task >= nrb * groups) return;  // whole waves, and the kernel has no barrier
+    const int64_t rb = task % nrb;
+    const int g = (int)(task / nrb);
     const int64_t b = blockIdx.y;
     X += b * x_batch;
     V += b * v_batch;
-    y += b * y_batch;
-    const int l8 = threadIdx.x & 7;
-    const int64_t row = (int64_t)blockIdx.x * kSkinnyRows + (threadIdx.x >> 3);
-    const T* x = X + (row < R ? row : 0) * (int64_t)K;
-    float acc[SB];
+    const int kq = F::kofs(lane);
+    const int64_t row0 = rb * 32;
+    const T* xr[RB];
 #pragma unroll
-    for (int s = 0; s < SB; ++s) acc[s] = 0.0f;
-    for (int kc0 = 0; kc0 < K; kc0 += kSkinnyKC) {
-        __syncthreads();  // the previous chunk's readers are done
-        // consecutive threads read consecutive elements of V: along k when V's
-        // rows are k-contiguous, along s when V is stored k-major
-        if (vs_k == 1) {
-            for (int i = threadIdx.x; i < kSkinnyKC * SB; i += kThreads) {
-                const int s = i / kSkinnyKC, k = i % kSkinnyKC;
-                vs[s][k] = (s < S && kc0 + k < K) ? to_f32(V[s * vs_s + (int64_t)(kc0 + k)]) : 0.0f;
-            }
-        } else {
-            for (int i = threadIdx.x; i < kSkinnyKC * SB; i += kThreads) {
-                const int k = i / SB, s = i % SB;
-                vs[s][k] = (s < S && kc0 + k < K) ? to_f32(V[s * vs_s + (int64_t)(kc0 + k) * vs_k]) : 0.0f;
-            }
+    for (int i = 0; i < RB; ++i) {
+        const int64_t r = row0 + i * MR + (lane % MR);
+        xr[i] = X + (r < R ? r : R - 1) * xs_r;
+    }
+    const int sl = lane % MR;
+    const T* vr = V + (int64_t)(sl < S ? sl : S - 1) * vs_s;
+    typename F::acc_t acc[RB];
+#pragma unroll
+    for (int i = 0; i < RB; ++i) acc[i] = typename F::acc_t{};
+
+    const int nblk = (K + F::KBLK - 1) / F::KBLK, nfull = K / F::KBLK;
+    int blk = g * bpg;
+    const int b1 = blk + bpg < nblk ? blk + bpg : nblk;
+    const int bf = b1 < nfull ? b1 : nfull;
+    if constexpr (XS) {
+        constexpr int UBL = 128 / (F::KBLK * (int)sizeof(T));  // blocks per 128 bytes of a row
+        constexpr int UB = UBL * F::LINES;                       // blocks per staged group
+        constexpr int CPB = F::KBLK * (int)sizeof(T) / 16;      // 16-byte chunks of a row per block
+        // copy: instruction (l, j) moves line l of rows 8j + lane/8, chunk lane%8
+        const char* src[4];
+        int dsl[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = 8 * j + (lane >> 3);
+            const int64_t rr = row0 + r < R ? row0 + r : R - 1;
+            src[j] = reinterpret_cast<const char*>(X + rr * xs_r) + (lane & 7) * 16;
+            dsl[j] = r * 8 + ((lane & 7) ^ ((r >> 1) & 7));
         }
-        __syncthreads();
-        if (row < R) {
-#pragma unroll 2
-            for (int j = 0; j < kSkinnyKC / 32; ++j) {
-                const int kl = 32 * j + 4 * l8;  // this lane's 4 k of the chunk
-                float xv[4];
-                if constexpr (VEC) {
-                    if (kc0 + kl >= K) continue;  // K % 4 == 0: whole pieces only
-                    load4(x + kc0 + kl, xv);
-                } else {
+        // reads: row block i, lane row i*MR + lane%MR, chunk (u % UBL)*CPB + lane/MR of line u / UBL
+        int rdx[RB];
+        const int cq = lane / MR;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) xv[e] = kc0 + kl + e < K ? to_f32(x[kc0 + kl + e]) : 0.0f;
-                }
-                // vs[s][kl .. kl+3]: the row's eight lanes read one 128-byte
-                // stretch of a row of vs, so the reads do not conflict
+        for (int i = 0; i < RB; ++i) {
+            const int r = i * MR + (lane % MR);
+            rdx[i] = r * 8;
+        }
+        f4v* st = stage[wave];
+        const int ng = (bf - blk) / UB;
+        f4v data[F::LINES][4];
+        frag vc[UB], vn[UB];
+        auto load_x = [&](int b0) {
+            const int64_t kb = (int64_t)b0 * F::KBLK * (int64_t)sizeof(T);
 #pragma unroll
-                for (int s = 0; s < SB; ++s) {
-                    typedef float f4 __attribute__((ext_vector_type(4)));
-                    const f4 v4 = *reinterpret_cast<const f4*>(&vs[s][kl]);
+            for (int l = 0; l < F::LINES; ++l)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[s] = __builtin_fmaf(xv[e], v4[e], acc[s]);
-                }
+                for (int j = 0; j < 4; ++j) data[l][j] = *reinterpret_cast<const f4v*>(src[j] + kb + 128 * l);
+        };
+        auto load_v = [&](int b0, frag(&vv)[UB]) {
+#pragma unroll
+            for (int u = 0; u < UB; ++u) {
+                const int64_t k = (int64_t)(b0 + u) * F::KBLK + kq;
+                vv[u] = sk_run<VV>(vr + k * vs_k, vs_k);
             }
+        };
+        if (ng > 0) {
+            load_x(blk);
+            load_v(blk, vc);
+        }
+        for (int gi = 0; gi < ng; ++gi, blk += UB) {
+#pragma unroll
+            for (int l = 0; l < F::LINES; ++l)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) st[l * 256 + dsl[j]] = data[l][j];
+            asm volatile("" ::: "memory");
+            if (gi + 1 < ng) {  // the next group's X and V, in flight during this group's math
+                load_x(blk + UB);
+                load_v(blk + UB, vn);
+            }
+#pragma unroll
+            for (int u = 0; u < UB; ++u)
+#pragma unroll
+                for (int i = 0; i < RB; ++i) {
+                    const int r = i * MR + (lane % MR);
+                    const int c = (u % UBL) * CPB + cq;
+                    const f4v t = st[(u / UBL) * 256 + rdx[i] + (c ^ ((r >> 1) & 7))];
+                    F::mma(__builtin_bit_cast(frag, t), vc[u], acc[i]);
+                }
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int u = 0; u < UB; ++u) vc[u] = vn[u];
+        }
+    } else {
+        for (; blk + U <= bf; blk += U) {
+            frag a[U][RB], v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t k = (int64_t)(blk + u) * F::KBLK + kq;
+#pragma unroll
+                for (int i = 0; i < RB; ++i) a[u][i] = sk_run<false>(xr[i] + k * xs_k, xs_k);
+                v[u] = sk_run<VV>(vr + k * vs_k, vs_k);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int i = 0; i < RB; ++i) F::mma(a[u][i], v[u], acc[i]);
         }
     }
+    for (; blk < bf; ++blk) {
+        const int64_t k = (int64_t)blk * F::KBLK + kq;
+        frag a[RB];
 #pragma unroll
-    for (int s = 0; s < SB; ++s)
+        for (int i = 0; i < RB; ++i) a[i] = sk_run<XS>(xr[i] + k * xs_k, xs_k);
+        const frag v = sk_run<VV>(vr + k * vs_k, vs_k);
 #pragma unroll
-        for (int o = 1; o < 8; o <<= 1) acc[s] = acc[s] + __shfl_xor(acc[s], o);
-    if (row < R && l8 == 0) {
+        for (int i = 0; i < RB; ++i) F::mma(a[i], v, acc[i]);
+    }
+    if (blk < b1) {  // the partial last block
+        const int64_t k = (int64_t)blk * F::KBLK + kq;
+        frag a[RB];
 #pragma unroll
-        for (int s = 0; s < SB; ++s)
-            if (s < S) y[row * ys_i + s * ys_s] = acc[s];
+        for (int i = 0; i < RB; ++i) a[i] = sk_run_tail(xr[i] + k * xs_k, xs_k, k, K);
+        const frag v = sk_run_tail(vr + k * vs_k, vs_k, k, K);
+#pragma unroll
+        for (int i = 0; i < RB; ++i) F::mma(a[i], v, acc[i]);
+    }
+
+    if (groups == 1) {
+        y += b * y_batch;
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+            for (int v = 0; v < F::ACC; ++v) {
+                const int64_t r = row0 + i * MR + F::row(v, lane);
+                if (r < R && sl < S) y[r * ys_i + sl * ys_s] = acc[i][v];
+            }
+    } else {
+        float* p = part + ((b * groups + g) * nrb + rb) * (RB * F::ACC * 64) + lane;
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+            for (int v = 0; v < F::ACC; ++v) p[(i * F::ACC + v) * 64] = acc[i][v];
     }
 }
 
-// Y[j][s] = sum_k X[k][j] W(k, s) for j < J, s < S <= SB, with X j-contiguous
-// (pitch J) and W(k, s) = W[k*ws_k + s*ws_s].  Stage 1: a thread owns four
-// columns (VEC) or one and walks a group of rows in ascending order, W's rows
-// of the group staged in LDS 64 at a time, into part[b][group][s][j]; stage 2
-// adds the groups in ascending order.
-constexpr int kSkinnyWK = 64;
-
-template <typename T, int SB, bool VEC>
-__global__ __launch_bounds__(kThreads) void skinny_sums_stage1(
-    const T* __restrict__ X, const T* __restrict__ W, float* __restrict__ part, int K, int64_t J, int S,
-    int64_t ws_k, int64_t ws_s, int64_t nseg, int64_t groups, int64_t rpg, int64_t x_batch, int64_t w_batch) {
-    constexpr int E = VEC ? 4 : 1;
-    __shared__ float ws[kSkinnyWK][SB];
+// Y from the groups' partial blocks, added in ascending group order (eight
+// loads in flight); one thread per accumulator element of a batch entry.
+template <typename T, int MR, int RB>
+__global__ __launch_bounds__(kThreads) void skinny_mfma_fold(const float* __restrict__ part, float* __restrict__ y,
+                                                             int64_t R, int S, int64_t ys_i, int64_t ys_s,
+                                                             int64_t y_batch, int64_t nrb, int groups) {
+    using F = SkMfma<T, MR>;
+    constexpr int PER_RB = RB * F::ACC * 64;
+    const int64_t per = nrb * PER_RB;  // floats per batch entry and group
+    const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (t >= per) return;
     const int64_t b = blockIdx.y;
-    X += b * x_batch;
-    W += b * w_batch;
-    const int64_t seg = blockIdx.x % nseg, group = blockIdx.x / nseg;
-    const int64_t c = (seg * kThreads + threadIdx.x) * E;
-    const int64_t r0 = group * rpg;
-    const int64_t r1 = r0 + rpg < K ? r0 + rpg : K;
-    float acc[SB][E];
-#pragma unroll
-    for (int s = 0; s < SB; ++s)
-#pragma unroll
-        for (int e = 0; e < E; ++e) acc[s][e] = 0.0f;
-    for (int64_t k0 = r0; k0 < r1; k0 += kSkinnyWK) {
-        __syncthreads();
-        for (int i = threadIdx.x; i < kSkinnyWK * SB; i += kThreads) {
-            const int k = i / SB, s = i % SB;
-            ws[k][s] = (s < S && k0 + k < r1) ? to_f32(W[(k0 + k) * ws_k + s * ws_s]) : 0.0f;
-        }
-        __syncthreads();
-        if (c < J) {
-            const int64_t kn = r1 - k0 < kSkinnyWK ? r1 - k0 : kSkinnyWK;
-            for (int k = 0; k < kn; ++k) {
-                float xv[E];
-                const T* xr = X + (k0 + k) * J + c;
-                if constexpr (VEC) {
-                    load4(xr, xv);
-                } else {
-                    xv[0] = to_f32(xr[0]);
-                }
-#pragma unroll
-                for (int s = 0; s < SB; ++s)
-#pragma unroll
-                    for (int e = 0; e < E; ++e) acc[s][e] = __builtin_fmaf(xv[e], ws[k][s], acc[s][e]);
-            }
-        }
-    }
-    if (c >= J) return;
-    float* p = part + (b * groups + group) * (int64_t)S * J + c;
-#pragma unroll
-    for (int s = 0; s < SB; ++s)
-        if (s < S) {
-#pragma unroll
-            for (int e = 0; e < E; ++e) p[s * J + e] = acc[s][e];
-        }
-}
-
-__global__ __launch_bounds__(kThreads) void skinny_sums_stage2(const float* __restrict__ part, float* __restrict__ y,
-                                                               int64_t J, int S, int64_t groups, int64_t ys_j,
-                                                               int64_t ys_s, int64_t y_batch) {
-    const int64_t b = blockIdx.y;
-    const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;  // s * J + j
-    if (t >= (int64_t)S * J) return;
-    const int64_t s = t / J, j = t - s * J;
-    const int64_t gs = (int64_t)S * J;
-    const float* p = part + b * groups * gs + t;
+    const float* p = part + b * groups * per + t;
     float acc = p[0];
-    int64_t g = 1;
-    for (; g + 8 <= groups; g += 8) {  // eight loads in flight, added in order
+    int g = 1;
+    for (; g + 8 <= groups; g += 8) {
         float v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = p[(g + u) * gs];
+        for (int u = 0; u < 8; ++u) v[u] = p[(int64_t)(g + u) * per];
 #pragma unroll
         for (int u = 0; u < 8; ++u) acc = acc + v[u];
     }
-    for (; g < groups; ++g) acc = acc + p[g * gs];
-    y[b * y_batch + j * ys_j + s * ys_s] = acc;
+    for (; g < groups; ++g) acc = acc + p[(int64_t)g * per];
+    const int64_t rb = t / PER_RB;
+    const int rem = (int)(t - rb * PER_RB);
+    const int i = rem / (F::ACC * 64), v = (rem / 64) % F::ACC, lane = rem % 64;
+    const int64_t r = (rb * RB + i) * MR + F::row(v, lane);
+    const int s = lane % MR;
+    if (r < R && s < S) y[b * y_batch + r * ys_i + s * ys_s] = acc;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -549,91 +694,93 @@ int32_t outer(const T* a, const T* b, float* c, int M, int N, int batch) {
     return ch::check_hip(hipGetLastError(), "outer_kernel");
 }
 
-template <typename T, int SB>
-int32_t skinny_dots_sb(const T* X, const T* V, float* y, int64_t R, int S, int K, int64_t vs_s, int64_t vs_k,
-                       int64_t ys_i, int64_t ys_s, int64_t x_batch, int64_t v_batch, int64_t y_batch, int batch) {
-    const bool vec = K % 4 == 0 && ((uintptr_t)X % (4 * sizeof(T))) == 0;
-    const dim3 g((unsigned)((R + kSkinnyRows - 1) / kSkinnyRows), (unsigned)batch);
-    if (vec)
-        skinny_dots_kernel<T, SB, true><<<g, kThreads, 0, ch::stream()>>>(X, V, y, R, S, K, vs_s, vs_k, ys_i, ys_s,
-                                                                         x_batch, v_batch, y_batch);
-    else
-        skinny_dots_kernel<T, SB, false><<<g, kThreads, 0, ch::stream()>>>(X, V, y, R, S, K, vs_s, vs_k, ys_i, ys_s,
-                                                                          x_batch, v_batch, y_batch);
-    return ch::check_hip(hipGetLastError(), "skinny_dots_kernel");
+template <typename T, int MR, int RB, bool XS, bool VV>
+int32_t skinny_mfma_launch(const T* X, const T* V, float* y, float* part, int64_t R, int S, int K, int64_t xs_r,
+                           int64_t xs_k, int64_t vs_s, int64_t vs_k, int64_t ys_i, int64_t ys_s, int64_t x_batch,
+                           int64_t v_batch, int64_t y_batch, int batch, int64_t nrb, int groups, int bpg) {
+    const int64_t waves = nrb * groups;
+    const dim3 g((unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64)), (unsigned)batch);
+    skinny_mfma_kernel<T, MR, RB, XS, VV><<<g, kThreads, 0, ch::stream()>>>(
+        X, V, y, part, R, S, K, xs_r, xs_k, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch, y_batch, nrb, groups, bpg);
+    int32_t st = ch::check_hip(hipGetLastError(), "skinny_mfma_kernel");
+    if (st != CLEAVE_HIP_OK || groups == 1) return st;
+    const int64_t per = nrb * RB * SkMfma<T, MR>::ACC * 64;
+    const dim3 g2((unsigned)((per + kThreads - 1) / kThreads), (unsigned)batch);
+    skinny_mfma_fold<T, MR, RB><<<g2, kThreads, 0, ch::stream()>>>(part, y, R, S, ys_i, ys_s, y_batch, nrb, groups);
+    return ch::check_hip(hipGetLastError(), "skinny_mfma_fold");
 }
 
-template <typename T, int SB>
-int32_t skinny_sums_sb(const T* X, const T* W, float* y, int K, int64_t J, int S, int64_t ws_k, int64_t ws_s,
-                       int64_t ys_j, int64_t ys_s, int64_t x_batch, int64_t w_batch, int64_t y_batch, int batch) {
-    const bool vec = J % 4 == 0 && ((uintptr_t)X % (4 * sizeof(T))) == 0;
-    const int E = vec ? 4 : 1;
-    const int64_t nseg = ((J + E - 1) / E + kThreads - 1) / kThreads;
-    // about four blocks per CU over the batch, and partials (S values per
-    // column per group) at most a quarter of the bytes of X
-    int64_t groups = 4LL * ch::num_cus() / (nseg * batch);
-    const int64_t by_bytes = (int64_t)K * (int64_t)sizeof(T) / (16LL * S);
-    if (groups > by_bytes) groups = by_bytes;
+// Y (R x S, element (r, s) at r*ys_i + s*ys_s) = X V^T on the matrix cores, S <= 32.
+template <typename T, int MR, int RB>
+int32_t skinny_mfma_mr(const T* X, const T* V, float* y, int64_t R, int S, int K, int64_t xs_r, int64_t xs_k,
+                       int64_t vs_s, int64_t vs_k, int64_t ys_i, int64_t ys_s, int64_t x_batch, int64_t v_batch,
+                       int64_t y_batch, int batch) {
+    using F = SkMfma<T, MR>;
+    constexpr int64_t esz = sizeof(T);
+    // 16-byte loads along k (X staged through LDS): unit k stride, and every
+    // row (and batch entry) start aligned
+    const bool xv = xs_k == 1 && aligned16(X) && (xs_r * esz) % 16 == 0 && (x_batch * esz) % 16 == 0;
+    const bool vv = vs_k == 1 && aligned16(V) && (vs_s * esz) % 16 == 0 && (v_batch * esz) % 16 == 0;
+    const int64_t nrb = (R + MR * RB - 1) / (MR * RB);
+    const int nblk = (K + F::KBLK - 1) / F::KBLK;
+    // Groups of k: enough waves for 8 per CU over the batch (16 with X
+    // unstaged), each group at least 8 blocks deep, and the partial blocks at
+    // most an eighth of X's bytes.
+    const int cus = ch::num_cus() > 0 ? ch::num_cus() : 1;
+    const int64_t want = (xv ? 8LL : 16LL) * cus;
+    int64_t groups = (want + nrb * batch - 1) / (nrb * batch);
+    groups = std::min<int64_t>(groups, std::max(1, nblk / 8));
+    const int64_t part_per_group = nrb * (int64_t)(MR * RB * MR) * 4;  // bytes per batch entry
+    groups = std::min<int64_t>(groups, std::max<int64_t>(1, R * K * esz / 8 / part_per_group));
     if (groups < 1) groups = 1;
-    if (groups > K) groups = K;
-    const int64_t rpg = (K + groups - 1) / groups;
-    groups = (K + rpg - 1) / rpg;
-    float* part = (float*)ch::scratch(8, sizeof(float) * (size_t)(batch * groups * S * J));
-    if (!part) return CLEAVE_HIP_ERR_OOM;
-    const dim3 g1((unsigned)(nseg * groups), (unsigned)batch);
-    if (vec)
-        skinny_sums_stage1<T, SB, true><<<g1, kThreads, 0, ch::stream()>>>(X, W, part, K, J, S, ws_k, ws_s, nseg,
-                                                                           groups, rpg, x_batch, w_batch);
-    else
-        skinny_sums_stage1<T, SB, false><<<g1, kThreads, 0, ch::stream()>>>(X, W, part, K, J, S, ws_k, ws_s, nseg,
-                                                                            groups, rpg, x_batch, w_batch);
-    int32_t st = ch::check_hip(hipGetLastError(), "skinny_sums_stage1");
-    if (st != CLEAVE_HIP_OK) return st;
-    const dim3 g2((unsigned)(((int64_t)S * J + kThreads - 1) / kThreads), (unsigned)batch);
-    skinny_sums_stage2<<<g2, kThreads, 0, ch::stream()>>>(part, y, J, S, groups, ys_j, ys_s, y_batch);
-    return ch::check_hip(hipGetLastError(), "skinny_sums_stage2");
+    int bpg = (int)((nblk + groups - 1) / groups);
+    if (xv) {  // staged groups start on 128 bytes of the rows
+        constexpr int ub = 128 * F::LINES / (F::KBLK * (int)sizeof(T));
+        bpg = (bpg + ub - 1) / ub * ub;
+    }
+    groups = (nblk + bpg - 1) / bpg;
+    float* part = nullptr;
+    if (groups > 1) {
+        part = (float*)ch::scratch(8, (size_t)(batch * groups * part_per_group));
+        if (!part) return CLEAVE_HIP_ERR_OOM;
+    }
+#define CH_SK_ARGS X, V, y, part, R, S, K, xs_r, xs_k, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch, y_batch, batch, nrb, \
+                   (int)groups, bpg
+    if (xv && vv) return skinny_mfma_launch<T, MR, RB, true, true>(CH_SK_ARGS);
+    if (xv) return skinny_mfma_launch<T, MR, RB, true, false>(CH_SK_ARGS);
+    if (vv) return skinny_mfma_launch<T, MR, RB, false, true>(CH_SK_ARGS);
+    return skinny_mfma_launch<T, MR, RB, false, false>(CH_SK_ARGS);
+#undef CH_SK_ARGS
 }
 
-template <typename T>
-int32_t skinny_dots(const T* X, const T* V, float* y, int64_t R, int S, int K, int64_t vs_s, int64_t vs_k,
-                    int64_t ys_i, int64_t ys_s, int64_t x_batch, int64_t v_batch, int64_t y_batch, int batch) {
-    if (S <= 4) return skinny_dots_sb<T, 4>(X, V, y, R, S, K, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch, y_batch, batch);
-    if (S <= 8) return skinny_dots_sb<T, 8>(X, V, y, R, S, K, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch, y_batch, batch);
+int32_t skinny_mfma(const float* X, const float* V, float* y, int64_t R, int S, int K, int64_t xs_r, int64_t xs_k,
+                    int64_t vs_s, int64_t vs_k, int64_t ys_i, int64_t ys_s, int64_t x_batch, int64_t v_batch,
+                    int64_t y_batch, int batch) {
     if (S <= 16)
-        return skinny_dots_sb<T, 16>(X, V, y, R, S, K, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch, y_batch, batch);
-    return skinny_dots_sb<T, 32>(X, V, y, R, S, K, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch, y_batch, batch);
+        return skinny_mfma_mr<float, 16, 2>(X, V, y, R, S, K, xs_r, xs_k, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch,
+                                            y_batch, batch);
+    return skinny_mfma_mr<float, 32, 1>(X, V, y, R, S, K, xs_r, xs_k, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch,
+                                        y_batch, batch);
+}
+int32_t skinny_mfma(const uint16_t* X, const uint16_t* V, float* y, int64_t R, int S, int K, int64_t xs_r,
+                    int64_t xs_k, int64_t vs_s, int64_t vs_k, int64_t ys_i, int64_t ys_s, int64_t x_batch,
+                    int64_t v_batch, int64_t y_batch, int batch) {
+    return skinny_mfma_mr<uint16_t, 32, 1>(X, V, y, R, S, K, xs_r, xs_k, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch,
+                                           y_batch, batch);
 }
 
-template <typename T>
-int32_t skinny_sums(const T* X, const T* W, float* y, int K, int64_t J, int S, int64_t ws_k, int64_t ws_s,
-                    int64_t ys_j, int64_t ys_s, int64_t x_batch, int64_t w_batch, int64_t y_batch, int batch) {
-    if (S <= 4) return skinny_sums_sb<T, 4>(X, W, y, K, J, S, ws_k, ws_s, ys_j, ys_s, x_batch, w_batch, y_batch, batch);
-    if (S <= 8) return skinny_sums_sb<T, 8>(X, W, y, K, J, S, ws_k, ws_s, ys_j, ys_s, x_batch, w_batch, y_batch, batch);
-    if (S <= 16)
-        return skinny_sums_sb<T, 16>(X, W, y, K, J, S, ws_k, ws_s, ys_j, ys_s, x_batch, w_batch, y_batch, batch);
-    return skinny_sums_sb<T, 32>(X, W, y, K, J, S, ws_k, ws_s, ys_j, ys_s, x_batch, w_batch, y_batch, batch);
-}
-
-// C (batch x M x N) = op(A) op(B) with min(M, N) <= 32: the matrix operand
-// whose long side is the output's streams once; the small operand is staged
-// in LDS.  A, B, C packed back to back per product.
+// C (batch x M x N) = op(A) op(B) with min(M, N) <= 32 on the matrix cores:
+// X is the operand along the long output dimension, V the other.  A, B, C
+// packed back to back per product.
 template <typename T>
 int32_t skinny_product(const T* a, const T* b, float* c, int M, int N, int K, int batch, int ta, int tb) {
     const int64_t sa = (int64_t)M * K, sb = (int64_t)K * N, sc = (int64_t)M * N;
-    if (N <= M) {
-        // S = N: C[m][n] = sum_k op(A)[m][k] op(B)[k][n]; B(n, k) at tb ? n*K + k : k*N + n
-        const int64_t vs_s = tb ? K : 1, vs_k = tb ? 1 : N;
-        if (!ta)  // A is M x K: rows of A against the N vectors of B
-            return skinny_dots(a, b, c, M, N, K, vs_s, vs_k, (int64_t)N, 1, sa, sb, sc, batch);
-        // A is stored K x M: C[m][n] = sum_k A[k][m] B(n, k)
-        return skinny_sums(a, b, c, K, M, N, vs_k, vs_s, (int64_t)N, 1, sa, sb, sc, batch);
-    }
-    // S = M: C[m][n] = sum_k A(m, k) op(B)[k][n]; A(m, k) at ta ? k*M + m : m*K + k
-    const int64_t vs_s = ta ? 1 : K, vs_k = ta ? M : 1;
-    if (tb)  // B is stored N x K: rows of B against the M vectors of A
-        return skinny_dots(b, a, c, N, M, K, vs_s, vs_k, 1, (int64_t)N, sb, sa, sc, batch);
-    // B is K x N: C[m][n] = sum_k B[k][n] A(m, k)
-    return skinny_sums(b, a, c, K, N, M, vs_k, vs_s, 1, (int64_t)N, sb, sa, sc, batch);
+    if (N <= M)  // X(m, k) = op(A)[m][k], V(n, k) = op(B)[k][n]
+        return skinny_mfma(a, b, c, M, N, K, ta ? 1 : K, ta ? M : 1, tb ? K : 1, tb ? 1 : N, (int64_t)N, 1, sa, sb,
+                           sc, batch);
+    // X(n, k) = op(B)[k][n], V(m, k) = op(A)[m][k]
+    return skinny_mfma(b, a, c, N, M, K, tb ? K : 1, tb ? 1 : N, ta ? 1 : K, ta ? M : 1, 1, (int64_t)N, sb, sa, sc,
+                       batch);
 }
 
 // C (batch x M x N) = op(A) op(B) with M, N or K equal to 1; A, B, C packed

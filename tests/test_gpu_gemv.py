@@ -115,14 +115,17 @@ def test_negative_zero_products_become_positive_zero(hip):
     assert np.array_equal(np.signbit(got), np.signbit(want)) and not np.signbit(got[0, 0])
 
 
-# One output dimension of at most 32 (the skinny kernels of gemv.hip): the
-# matrix operand along the long output dimension streams once, the small one
-# is staged in LDS; bucketed at 4, 8, 16 and 32 vectors.
+# One output dimension of at most 32 (the skinny kernels of gemv.hip, on the
+# matrix cores): the matrix operand along the long output dimension streams
+# once, 32 of its rows per wave (16 x 16 tiles up to 16 vectors, 32 x 32 from
+# 17), staged through LDS when its rows are k-contiguous; long K in groups
+# whose partial tiles are added in order.
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [
     (1000, 10, 777), (4096, 3, 4096), (513, 32, 100), (2000, 17, 1),     # N small
     (10, 4096, 1000), (5, 777, 65536), (31, 2000, 33), (2, 3, 2),        # M small
     (32, 32, 1000), (7, 9, 300000),                                       # both small, long K
+    (20000, 20, 3), (30000, 8, 5), (16, 700, 4100),                       # K under one block; K tail
 ])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_skinny_shapes_every_entry(hip, oracle, dtype, M, N, K, ta, tb):
@@ -155,3 +158,33 @@ def test_skinny_shapes_misaligned_views(hip, oracle, dtype, off, M, N, K, ta, tb
     a, b = abuf.sub(off, A.shape), bbuf.sub(off, B.shape)
     got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
     _check(got, Au, Bu, oracle, ta, tb, K, f"{dtype} view at +{off} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(700, 10, 300), (10, 700, 300), (450, 24, 200)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_skinny_clamped_rows_and_columns_stay_apart(hip, oracle, dtype, M, N, K, ta, tb):
+    # Rows past the long dimension read its last row, and columns past the
+    # short one read its last column: an Inf in op(A)'s last row and a NaN in
+    # op(B)'s last column (the clamp targets in either orientation) must reach
+    # only the entries the loop gives them.
+    A, B, Au, Bu = _operands(oracle, dtype, M, N, K, ta, tb, seed=7 * M + N + ta + 2 * tb)
+    Af = (Au.T if ta else Au).copy()  # op(A), op(B) as float32
+    Bf = (Bu.T if tb else Bu).copy()
+    Af[M - 1, 5] = np.inf
+    Bf[7, N - 1] = np.nan
+    As, Bs = (Af.T if ta else Af).copy(), (Bf.T if tb else Bf).copy()
+    if dtype == "bf16":
+        As, Bs = oracle.to_bf16(As), oracle.to_bf16(Bs)
+    got = hip.matmul(hip.from_numpy(As, dtype), hip.from_numpy(Bs, dtype), trans_a=bool(ta),
+                     trans_b=bool(tb)).numpy()
+    ref = oracle.matmul(Af, Bf, threads=16)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isinf(got), np.isinf(ref))
+    inf = np.isinf(ref)
+    assert inf.any() and np.isnan(ref).any()
+    assert np.array_equal(np.sign(got[inf]), np.sign(ref[inf]))
+    # the rest: rows 0 .. M-2 and columns 0 .. N-2 are untouched by either value
+    ca, cb = Af[:M - 1], Bf[:, :N - 1]
+    den = np.abs(ca).astype(np.float64) @ np.abs(cb).astype(np.float64)
+    assert_gemm_close(got[:M - 1, :N - 1], ref[:M - 1, :N - 1], den, K, f"{dtype} {M}x{N}x{K} away from the specials")
