@@ -273,17 +273,17 @@ bool launch_small(const float* a, const float* b, float* c, int M, int N, int K,
 }
 
 // Ping-pong kernel (gemm_f32_pingpong.hpp) when the shape divides its
-// 256 x 256 x 16 tile; false when it does not.
-template <bool TA, bool TB>
+// TILE x TILE x 16 tile; false when it does not.
+template <bool TA, bool TB, int TILE = 256>
 bool launch_pingpong(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
                      int64_t ldb, int batch, int64_t sA, int64_t sB, int64_t sC, int32_t* status) {
-    using P = ch::F32PingPong<!TA, TB>;
+    using P = ch::F32PingPong<!TA, TB, 0, TILE>;
     if (!P::fits(M, N, K, lda, ldb) || ((uintptr_t)a & 15) || ((uintptr_t)b & 15) || (sA % 4) || (sB % 4))
         return false;
     const int tiles_m = M / P::BM, tiles_n = N / P::BN;
     if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
     dim3 grid((unsigned)(tiles_m * tiles_n * batch));
-    ch::gemm_f32_pingpong_kernel<!TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
+    ch::gemm_f32_pingpong_kernel<!TA, TB, 0, TILE><<<grid, P::THREADS, 0, ch::stream()>>>(
         a, b, c, M, N, K, lda, ldb, sA, sB, sC, tiles_m, tiles_n, batch, ch::MlpFuse{});
     *status = ch::check_hip(hipGetLastError(), "gemm_f32_pingpong_kernel");
     return true;
@@ -368,7 +368,7 @@ bool launch_fast(const float* a, const float* b, float* c, int M, int N, int K, 
                  int64_t ldb, int64_t ldc, int batch, int64_t sA, int64_t sB, int64_t sC, int32_t* st) {
     if (ldc == N) {
         // 256 x 256 x 16 tile (ping-pong, 8 waves of 128 x 64) when it still
-        // yields a tile per CU, else 128 x 128 x 16 (4 waves of 64 x 64).
+        // yields a tile per CU; smaller shapes below.
         const int64_t big_tiles = (int64_t)(M / 256) * (N / 256) * batch;
         if (big_tiles >= ch::num_cus() &&
             launch_pingpong<TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
@@ -391,6 +391,19 @@ bool launch_fast(const float* a, const float* b, float* c, int M, int N, int K, 
         if (tiles128 < cus &&
             launch_tiled<64, 64, 16, 2, 2, 4, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
             return true;
+        // From a full round of 128 x 128 tiles, the ping-pong kernel on them
+        // (8 waves of 64 x 32, a 6-deep ring: one workgroup per CU), where its
+        // last round is at least 77% full.  Against the tiled kernels below:
+        // 2048^3 117.6 against 131.2 us, 2048^2 x 4096 229.6 against 256.8,
+        // 3072 x 4096 x 2048 (three rounds) 349.7 against 363.4, 2560^3 (400
+        // tiles, 78%) 285.0 against 304.1; 3072^3 (576, 75%) 510.4 against
+        // 453.8 and 2304^3 (324, 63%) 256.7 against 208.2 stay tiled.
+        if (tiles128 >= cus) {
+            const int64_t rounds = (tiles128 + cus - 1) / cus;
+            if ((double)tiles128 >= 0.77 * (double)(rounds * cus) &&
+                launch_pingpong<TA, TB, 128>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
+                return true;
+        }
         // 128 x 128 tiles run four workgroups per CU, 128 x 64 tiles six.
         // Where the last round of 128 x 128 tiles would fill under 70% of
         // the CUs' slots, the twice as many 128 x 64 tiles balance better:

@@ -1,12 +1,15 @@
 // gemm_f32_pingpong.hpp -- f32 GEMM on the ping-pong schedule of
-// gemm_pingpong.hpp (gfx950, v_mfma_f32_32x32x2f32, 256 x 256 x 16 tiles).
+// gemm_pingpong.hpp (gfx950, v_mfma_f32_32x32x2f32, 256 x 256 x 16 tiles,
+// or 128 x 128 x 16 for products with fewer 256 x 256 tiles than CUs).
 //
-// Eight waves; each owns a 128 x 64 block of C (4 x 2 tiles of 32 x 32).
-// Waves 0-3 (group 0, rows 0-127) and 4-7 (group 1, rows 128-255) sit one
-// per SIMD.  A C phase is the k-tile's 64 MFMAs (two 8-deep k-blocks of four
-// k=2 steps), 4096 matrix-core cycles, so the two barriers per k-tile cost
-// little next to it; the single-barrier schedule of gemm_f32_tiled.hpp
-// stops both waves of a SIMD at every k-tile.
+// Eight waves; each owns a 128 x 64 block of C (4 x 2 tiles of 32 x 32), or
+// 64 x 32 on 128 x 128 tiles.  Waves 0-3 (group 0, the upper half of the
+// tile's rows) and 4-7 (group 1, the lower half) sit one per SIMD.  A C phase
+// is the k-tile's 64 MFMAs (two 8-deep k-blocks of four k=2 steps), 4096
+// matrix-core cycles (16 MFMAs on 128 x 128 tiles), so the two barriers per
+// k-tile cost little next to it; the single-barrier schedule of
+// gemm_f32_tiled.hpp stops both waves of a SIMD at every k-tile (2048^3:
+// 131 us there, 118 us here on 128 x 128 tiles).
 //
 // Both operands sit in LDS k-major, whatever their layout in global memory,
 // and every fragment is read with ds_read2st64_b32 (two k-rows, one float
@@ -22,7 +25,11 @@
 // LDS holds each operand as [16 k-rows][4 stages][256 floats] (64 KiB; A at
 // 0, B at 64 KiB): one k-row of one stage is the 1 KiB a copy instruction
 // writes, and every fragment, k-row and stage of an operand is one
-// loop-invariant register plus an immediate offset below 64 KiB.  So the M
+// loop-invariant register plus an immediate offset below 64 KiB.  128 x 128
+// tiles keep [6 stages][16 k-rows][128 floats] (48 KiB per operand; a copy
+// instruction writes two k-rows; 96 KiB in all, so one workgroup per CU:
+// with four stages two shared a CU and three full rounds of tiles ran 417
+// against 350 us).  So the M
 // phase issues no VALU instruction; the accumulators live in AGPRs.
 // Within a 1 KiB row, 16-byte chunk c of k-row kr sits in slot pp_slot(kr, c)
 // = c ^ 8*bit2(kr) ^ 4*bit3(kr).  Bit 2 puts the two half-waves of a fragment
@@ -58,24 +65,31 @@
 
 namespace ch {
 
-template <bool AKC, bool BKC, int MODE = 0>
+template <bool AKC, bool BKC, int MODE = 0, int TILE = 256>
 struct F32PingPong {
-    static constexpr int BM = 256, BN = 256, BK = 16, NW = 8, WN = 4, THREADS = 64 * NW;
-    static constexpr int TM = 128, TN = 64, FM = TM / 32, FN = TN / 32, KB = BK / 8, STAGES = kPingPongStages;
+    static constexpr int BM = TILE, BN = TILE, BK = 16, NW = 8, WN = 4, THREADS = 64 * NW;
+    static constexpr int TM = TILE / 2, TN = TILE / 4, FM = TM / 32, FN = TN / 32, KB = BK / 8;
+    static constexpr int STAGES = TILE == 256 ? kPingPongStages : 6;
     static constexpr int A_BYTES = BM * BK * 4, B_BYTES = BN * BK * 4;  // one stage of one operand
     static constexpr int ROW = BM * 4;                                    // one k-row of one stage
-    static constexpr int KROW = STAGES * ROW;                             // k-row pitch
-    static constexpr int OP_BYTES = BK * KROW;                           // A at 0, B at OP_BYTES
-    static constexpr int D2_BYTES = MODE == 2 ? STAGES * BK * 4 : 0;        // MODE 2: d2 per stage
+    // Strides of k-row and stage within an operand's region: 256 x 256 tiles
+    // [16 k-rows][4 stages][256] (a copy instruction's 1 KiB is one k-row of
+    // one stage); 128 x 128 tiles [4 stages][16 k-rows][128] (its 1 KiB is two
+    // consecutive k-rows).
+    static constexpr int KSTR = TILE == 256 ? STAGES * ROW : ROW;
+    static constexpr int SSTR = TILE == 256 ? ROW : BK * ROW;
+    static constexpr int OP_BYTES = BK * STAGES * ROW;                   // A at 0, B at OP_BYTES
+    static constexpr int D2_BYTES = MODE == 2 ? STAGES * BK * 4 : 0;    // MODE 2: d2 per stage
     static constexpr int LDS_BYTES = 2 * OP_BYTES + D2_BYTES;
     // Per wave and k-tile: global_load_lds instructions of the m/n-contiguous
     // operands (and of d2).
     static constexpr int OP_LOADS = A_BYTES / 1024 / NW;  // per operand
     static constexpr int LDMA = OP_LOADS * ((AKC ? 0 : 1) + (BKC ? 0 : 1)) + (MODE == 2 ? 1 : 0);
-    static_assert(A_BYTES == B_BYTES && OP_LOADS == 2 && OP_BYTES == 65536, "operand tiles of 16 KiB");
+    static_assert(TILE == 256 || TILE == 128, "256 x 256 or 128 x 128 tiles");
+    static_assert(A_BYTES == B_BYTES && OP_LOADS >= 1 && OP_BYTES <= 65536, "an operand's ring within 64 KiB");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS per workgroup");
-    static_assert(MODE == 0 || (MODE == 1 && AKC && !BKC) || (MODE == 2 && !AKC && !BKC),
-                  "MODE 1 is the NN form, MODE 2 the TN form");
+    static_assert(MODE == 0 || (MODE == 1 && AKC && !BKC && TILE == 256) || (MODE == 2 && !AKC && !BKC && TILE == 256),
+                  "MODE 1 is the NN form, MODE 2 the TN form, both on 256 x 256 tiles");
 
     static bool fits(int M, int N, int K, int64_t lda, int64_t ldb) {
         const bool dims = M % BM == 0 && N % BN == 0 && K % BK == 0 && lda % 4 == 0 && ldb % 4 == 0;
@@ -115,16 +129,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* p) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)0xFFFFFFFF, 0x00020000);
 }
 
-// Staged copy of a k-contiguous operand tile [256 rows][16 k] into its
-// k-major LDS region.  Load q (q = wave + 8 j) covers rows 16q .. 16q+15,
-// lane l taking row 16q + l/4, k-chunk l%4 (64 bytes of each row per load);
-// its four floats go to k-rows 4*(l%4) + s, column row.  One register set
-// (data) in the loop: the M phase writes tile u+1 to LDS before loading tile
-// u+2 into it.
-template <int NW, int KROW, int ROW>
+// Staged copy of a k-contiguous operand tile [R rows][16 k] into its
+// k-major LDS region (k-row stride KSTR, stage stride SSTR).  Load q
+// (q = wave + 8 j) covers rows 16q .. 16q+15, lane l taking row 16q + l/4,
+// k-chunk l%4 (64 bytes of each row per load); its four floats go to k-rows
+// 4*(l%4) + s, column row.  One register set (data) in the loop: the M phase
+// writes tile u+1 to LDS before loading tile u+2 into it.
+template <int NW, int R, int KSTR, int SSTR>
 struct Staged {
-    static constexpr int R = 256, BK = 16, PER_WAVE = R * BK * 4 / 1024 / NW;
-    static_assert(PER_WAVE == 2, "two loads per wave");
+    static constexpr int BK = 16, PER_WAVE = R * BK * 4 / 1024 / NW;
+    static_assert(PER_WAVE >= 1, "a load per wave");
     uint32_t voff[PER_WAVE];
     uint32_t waddr[PER_WAVE];  // LDS address of (k-row 4*kc, stage 0, column row)
     tiles::v4f data[PER_WAVE];
@@ -136,7 +150,7 @@ struct Staged {
             const int row = 16 * q + (lane >> 2), kc = lane & 3;
             voff[j] = (uint32_t)(((int64_t)(r0 + row) * ld + 4 * kc) * 4);
             // pp_slot(4*kc + s, row/4) does not depend on s
-            waddr[j] = region + (uint32_t)(4 * kc * KROW + pp_slot(4 * kc, row >> 2) * 16 + (row & 3) * 4);
+            waddr[j] = region + (uint32_t)(4 * kc * KSTR + pp_slot(4 * kc, row >> 2) * 16 + (row & 3) * 4);
             opaque(voff[j]);
             opaque(waddr[j]);
         }
@@ -151,27 +165,29 @@ struct Staged {
 #pragma unroll
         for (int j = 0; j < PER_WAVE; ++j)
 #pragma unroll
-            for (int s = 0; s < 4; ++s) lds_ptr_w(waddr[j] + ST * ROW + s * KROW)[0] = d[j][s];
+            for (int s = 0; s < 4; ++s) lds_ptr_w(waddr[j] + ST * SSTR + s * KSTR)[0] = d[j][s];
     }
 };
 
-// global_load_lds copy of an m/n-contiguous operand tile [16 k][256 rows]:
-// instruction q (q = wave + 8 j) moves k-row q, lane l fetching the 16-byte
-// chunk that belongs in slot l of the row.
-template <int NW, int KROW>
+// global_load_lds copy of an m/n-contiguous operand tile [16 k][R rows]:
+// instruction q (q = wave + 8 j) moves k-rows RPI*q .. RPI*q + RPI-1 (one row
+// of 256 floats, or two of 128, stored KSTR apart: contiguous when RPI is 2),
+// lane l fetching the 16-byte chunk that belongs in slot l % CPR of its row.
+template <int NW, int R, int KSTR>
 struct Direct {
-    static constexpr int R = 256, BK = 16, PER_WAVE = BK / NW;
-    static_assert(PER_WAVE == 2, "two k-rows per wave");
+    static constexpr int BK = 16, CPR = R / 4, RPI = 64 / CPR, PER_WAVE = BK / RPI / NW;
+    static_assert(PER_WAVE >= 1 && (RPI == 1 || KSTR == R * 4), "an instruction's k-rows are contiguous");
     uint32_t voff[PER_WAVE];
-    uint32_t dst[PER_WAVE];  // LDS address of k-row q, stage 0 (SGPR-uniform)
+    uint32_t dst[PER_WAVE];  // LDS address of the instruction's first k-row, stage 0 (SGPR-uniform)
 
     __device__ __forceinline__ void init(int64_t ld, int r0, int wave, int lane, uint32_t region) {
 #pragma unroll
         for (int j = 0; j < PER_WAVE; ++j) {
-            const int kr = wave + NW * j;
-            const int c = pp_slot(kr, lane);  // slot lane holds chunk c (the XOR is its own inverse)
+            const int q = wave + NW * j;
+            const int kr = RPI * q + lane / CPR;
+            const int c = pp_slot(kr, lane % CPR);  // slot lane % CPR holds chunk c (the XOR is its own inverse)
             voff[j] = (uint32_t)(((int64_t)kr * ld + r0 + 4 * c) * 4);
-            dst[j] = region + (uint32_t)(kr * KROW);
+            dst[j] = region + (uint32_t)(RPI * q * KSTR);
         }
     }
     __device__ __forceinline__ void issue(const char* sbase_kt, uint32_t stage_off) const {
@@ -182,16 +198,16 @@ struct Direct {
 
 }  // namespace f32pp
 
-template <bool AKC, bool BKC, int MODE = 0>
+template <bool AKC, bool BKC, int MODE = 0, int TILE = 256>
 __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
     int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC, int tiles_m, int tiles_n,
     int batch, MlpFuse fuse) {
     using namespace ch::tiles;
     using namespace ch::f32pp;
-    using P = F32PingPong<AKC, BKC, MODE>;
+    using P = F32PingPong<AKC, BKC, MODE, TILE>;
     constexpr int FM = P::FM, FN = P::FN, NW = P::NW, BK = P::BK, KB = P::KB, S = P::STAGES;
-    constexpr int ROW = P::ROW, KROW = P::KROW;
+    constexpr int KSTR = P::KSTR, SSTR = P::SSTR;
     constexpr bool STAGED = AKC || BKC;
     __shared__ __attribute__((aligned(1024))) char smem[P::LDS_BYTES];
 
@@ -209,9 +225,10 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
 
     const uint32_t region_a = lds0, region_b = lds0 + P::OP_BYTES;
     // m/n-contiguous operands: global_load_lds into the k-major tile.
-    Direct<NW, KROW> dma_a, dma_b;
+    Direct<NW, TILE, KSTR> dma_a, dma_b;
     // k-contiguous operands: staged through registers.
-    Staged<NW, KROW, ROW> st_a, st_b;
+    using StagedT = Staged<NW, TILE, KSTR, SSTR>;
+    StagedT st_a, st_b;
     if constexpr (!AKC) dma_a.init(lda, m0, wave, lane, region_a);
     else st_a.init(lda, 0, wave, lane, region_a);
     if constexpr (!BKC) dma_b.init(ldb, n0, wave, lane, region_b);
@@ -229,7 +246,7 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
     const float* d2 = MODE == 2 ? fuse.d2 + (int64_t)bt * K : nullptr;
     const uint32_t region_d2 = lds0 + 2u * P::OP_BYTES;
     auto issue_dma = [&](int kt) {
-        const uint32_t stage_off = (uint32_t)((kt % S) * ROW);
+        const uint32_t stage_off = (uint32_t)((kt % S) * SSTR);
         const int src = min(kt, nk - 1);
         if constexpr (!AKC) dma_a.issue(a_base + src * step_a, stage_off);
         if constexpr (!BKC) dma_b.issue(b_base + src * step_b, stage_off);
@@ -254,7 +271,7 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
     };
 
     // Fragment read addresses: fragment f (A: f < FM, B: f >= FM) of k-block
-    // kb, step s, stage ST sits at rd[kb][f] + (8kb + s)*KROW + ST*ROW.
+    // kb, step s, stage ST sits at rd[kb][f] + (8kb + s)*KSTR + ST*SSTR.
     // Half-wave h reads k-rows kr = 8kb + 4h + s, whose slot depends on kr
     // through bit 2 (= h) and bit 3 (= kb).
     uint32_t rd[KB][FM + FN];
@@ -268,7 +285,7 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
                     f < FM ? grp * P::TM + f * 32 + (lane & 31) : wn * P::TN + (f - FM) * 32 + (lane & 31);
                 const int kr = 8 * kb + 4 * h;
                 rd[kb][f] = (f < FM ? region_a : region_b) +
-                            (uint32_t)(4 * h * KROW + pp_slot(kr, col >> 2) * 16 + (col & 3) * 4);
+                            (uint32_t)(4 * h * KSTR + pp_slot(kr, col >> 2) * 16 + (col & 3) * 4);
                 opaque(rd[kb][f]);
             }
     }
@@ -309,7 +326,7 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                const uint32_t off = (8 * kb + s) * KROW + ST * ROW;
+                const uint32_t off = (8 * kb + s) * KSTR + ST * SSTR;
 #pragma unroll
                 for (int i = 0; i < FM; ++i) fa[kb][i][s] = *lds_ptr(rd[kb][i] + off);
 #pragma unroll
@@ -327,7 +344,7 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
             issue_dma(u + S - 1);
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         } else {
-            pingpong_copy<P::LDMA>(u, issue_dma);
+            pingpong_copy<P::LDMA, S>(u, issue_dma);
         }
     };
     // Half-wave h holds k = 8*kb + 4*h + s at step s for both operands, so the
@@ -366,26 +383,25 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
     };
 
     if constexpr (STAGED) {
-        // Prologue: tiles 0 and 1 in stages 0 and 1 (staged parts written,
-        // copied parts landed), the copy of tile 2 in flight.  Tile 1's staged
+        // Prologue: tiles 0 and 1 in stages 0 and 1 (staged parts written),
+        // the copied parts of tiles 0 .. S-2 landed.  Tile 1's staged
         // registers are temporaries: no staged register is live when the
         // groups' loops begin.
         {
-            v4f t1a[2], t1b[2];
+            v4f t1a[StagedT::PER_WAVE], t1b[StagedT::PER_WAVE];
             load_staged(0);
             if constexpr (AKC) st_a.load(rsrc_a, (uint32_t)min(1, nk - 1) * (uint32_t)step_a, t1a);
             if constexpr (BKC) st_b.load(rsrc_b, (uint32_t)min(1, nk - 1) * (uint32_t)step_b, t1b);
-            issue_dma(0);
-            issue_dma(1);
-            issue_dma(2);
+#pragma unroll
+            for (int t = 0; t < S - 1; ++t) issue_dma(t);
             store_staged(PingPongStage<0>{});
             if constexpr (AKC) st_a.template store<1>(t1a);
             if constexpr (BKC) st_b.template store<1>(t1b);
             asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
         }
-        pingpong_schedule<P::LDMA>(nk, grp, [](int) {}, m_phase, c_phase, /*prologue_copies=*/false);
+        pingpong_schedule<P::LDMA, S>(nk, grp, [](int) {}, m_phase, c_phase, /*prologue_copies=*/false);
     } else {
-        pingpong_schedule<P::LDMA>(nk, grp, issue_dma, m_phase, c_phase, /*prologue_copies=*/true);
+        pingpong_schedule<P::LDMA, S>(nk, grp, issue_dma, m_phase, c_phase, /*prologue_copies=*/true);
     }
 
     // 32 x 32 accumulator layout: lane holds column l%32, rows 8*(v/4) + 4*(l/32) + v%4.

@@ -606,9 +606,11 @@ def test_padded_infinities_and_nans(hip, oracle, dtype):
 
 # The aligned kernels are chosen by tile count (on a 256-CU MI355X): f32 runs
 # the small kernel up to 512 tiles of 32 x 32 (640^3), 64 x 64 tiles below
-# 256 tiles of 128 x 128 (1024^2 x 512, 1280^2 x 256), 128 x 64 tiles where
-# the last round of 128 x 128 tiles would be under 70% full (2304^2 x 128)
-# and 128 x 128 tiles for one full round (2048^2 x 128); bf16 runs 64 x 128
+# 256 tiles of 128 x 128 (1024^2 x 512, 1280^2 x 256), the ping-pong kernel on
+# 128 x 128 tiles from one full round of them whose last round is at least
+# 77% full (2048^2 x 128; x 16, one k-tile; 2048 x 4096 x 48; 2560^2 x 64;
+# three rounds at 3072 x 4096 x 32), 128 x 64 tiles where the last round of
+# four workgroups per CU would be under 70% full (2304^2 x 128); bf16 runs 64 x 128
 # tiles for up to a round of 128 x 128 (1024^2 x 512; 128 x 128 with an
 # m-contiguous A), two-stage 128 x 128 tiles for several rounds
 # (2304^2 x 128), and 256 x 256 tiles from 128 of them (3072^2 x 128 tiled,
@@ -616,7 +618,8 @@ def test_padded_infinities_and_nans(hip, oracle, dtype):
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("dtype,M,N,K", [
     ("f32", 640, 640, 640), ("f32", 1024, 1024, 512), ("f32", 1280, 1280, 256),
-    ("f32", 2304, 2304, 128), ("f32", 2048, 2048, 128),
+    ("f32", 2304, 2304, 128), ("f32", 2048, 2048, 128), ("f32", 2048, 2048, 16), ("f32", 2048, 4096, 48),
+    ("f32", 2560, 2560, 64), ("f32", 3072, 4096, 32),
     ("bf16", 1024, 1024, 512), ("bf16", 2304, 2304, 128), ("bf16", 3072, 3072, 128),
     ("bf16", 3072, 3072, 640),
 ])
@@ -627,6 +630,18 @@ def test_tile_choices_every_entry(hip, oracle, dtype, M, N, K, ta, tb):
     ref = oracle.matmul(Au, Bu, trans_a=bool(ta), trans_b=bool(tb), threads=16)
     den = np.abs(Au.T if ta else Au).astype(np.float64) @ np.abs(Bu.T if tb else Bu).astype(np.float64)
     assert_gemm_close(got, ref, den, K, f"{dtype} {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+def test_f32_batched_products_on_the_128_tile_ping_pong(hip, oracle, ta, tb):
+    # four 1024^2 x 80 products: one round of 256 tiles of 128 x 128 over the batch
+    bsz, M, N, K = 4, 1024, 1024, 80
+    A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=91 + ta, batch=bsz)
+    got = hip.matmul_batched(hip.from_numpy(A), hip.from_numpy(B), trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    for i in range(bsz):
+        ref = oracle.matmul(Au[i], Bu[i], trans_a=bool(ta), trans_b=bool(tb), threads=16)
+        den = np.abs(Au[i].T if ta else Au[i]).astype(np.float64) @ np.abs(Bu[i].T if tb else Bu[i]).astype(np.float64)
+        assert_gemm_close(got[i], ref, den, K, f"batched 128-tile ping-pong product {i}")
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
