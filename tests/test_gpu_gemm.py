@@ -660,11 +660,13 @@ def test_many_tiny_products_stay_on_the_general_kernel(hip, oracle, dtype):
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [(1024, 4096, 8192), (1024, 2048, 16384), (2048, 2048, 8192),
-                                   (64, 64, 65536), (512, 512, 16384), (192, 320, 8192)])
+                                   (64, 64, 65536), (512, 512, 16384), (192, 320, 8192),
+                                   (1024, 1024, 4096), (768, 768, 8192)])
 def test_f32_k_split_every_entry(hip, oracle, M, N, K, ta, tb):
     # Few tiles and a long K: the product runs as K slices (4 or 8 on the
-    # ping-pong kernel for 256 x 256 tiles; 8 to 128 on the small-product or
-    # 64 x 64 kernels otherwise), then the slices are added in order.
+    # ping-pong kernel for 256 x 256 tiles; 4 to 16 that fill a round of
+    # 128 x 128 tiles; 8 to 128 on the small-product or 64 x 64 kernels
+    # otherwise), then the slices are added in order.
     # Every entry against the loop (its A.B^T form on transposed copies, bit
     # for bit its A.B loop), and bitwise the same on a second call.
     A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=M + N + K + 2 * ta + tb)
