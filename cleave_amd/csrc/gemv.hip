@@ -340,6 +340,7 @@ __global__ __launch_bounds__(kThreads) void outer_kernel(const T* __restrict__ a
 typedef float f4v __attribute__((ext_vector_type(4)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 typedef short s8v __attribute__((ext_vector_type(8)));
+typedef short s4v __attribute__((ext_vector_type(4)));
 typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
 
 template <typename T, int MR>
@@ -416,17 +417,29 @@ __device__ __forceinline__ s8v sk_run_tail(const uint16_t* p, int64_t st, int64_
 
 constexpr int kSkMfmaUnroll = 4;  // blocks of k whose loads are issued together (unstaged X)
 
-// X k-contiguous with 16-byte aligned rows (XS): the wave's 32 rows are staged
-// through its own LDS, F::LINES x 128 bytes of each row at a time, so that each
-// load instruction reads whole 128-byte lines (8 rows of 8 lanes); read
-// straight into the MFMA layout, an instruction took 16-32 rows at 32-64
-// bytes each and the kernel ran at 0.40-0.54 of HBM.  Row r's 16-byte chunk c
-// sits in slot c ^ ((r >> 1) & 7): sixteen lanes reading one chunk of 16
-// consecutive rows, or writing two rows, then cover all 64 banks once.  Only
-// the wave touches its region, and a wave's LDS instructions execute in
+// X staged through the wave's own 4 KiB (or 8) of LDS, so that every load
+// instruction reads whole 16-byte pieces of few lines:
+//   XM 1, X k-contiguous with 16-byte aligned rows: F::LINES x 128 bytes of
+//     each of the wave's 32 rows at a time, 8 rows of 8 lanes per instruction.
+//     Read straight into the MFMA layout, an instruction took 16-32 rows at
+//     32-64 bytes each and the kernel ran at 0.40-0.54 of HBM.  Row r's
+//     16-byte chunk c sits in slot c ^ ((r >> 1) & 7): sixteen lanes reading
+//     one chunk of 16 consecutive rows, or writing two rows, then cover all
+//     64 banks once.
+//   XM 2, X r-contiguous with 16-byte aligned k-rows: the wave's 32 values of
+//     32 (f32) or 64 (bf16) k-rows at a time, 8 (16) k-rows per instruction.
+//     Read as single values, bf16 X took eight 2-byte loads per lane and k
+//     block and ran at 0.45-0.49 of HBM.  f32: k-row kr sits at row
+//     kr ^ ((kr >> 2) & 1), its chunk c in slot c ^ 4*((kr >> 3) & 1), so the
+//     quarter- or half-waves reading k-rows 4 apart use different banks; the
+//     fragments are four ds_read_b32.  bf16: [k-row][32 values], read with
+//     ds_read_b64_tr_b16 (in a 16-lane group, source lane 4j + q points at
+//     k-row kb + j, values c0 + 4q .. c0 + 4q + 3, and result lane i receives
+//     value c0 + i of k-rows kb .. kb + 3), two per fragment.
+// Only the wave touches its region, and a wave's LDS instructions execute in
 // order, so no barrier is needed; the asm statements keep the compiler from
 // moving the reads above the writes (or the next writes above the reads).
-template <typename T, int MR, int RB, bool XS, bool VV>
+template <typename T, int MR, int RB, int XM, bool VV>
 __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
     const T* __restrict__ X, const T* __restrict__ V, float* __restrict__ y, float* __restrict__ part, int64_t R,
     int S, int K, int64_t xs_r, int64_t xs_k, int64_t vs_s, int64_t vs_k, int64_t ys_i, int64_t ys_s,
@@ -435,7 +448,9 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
     using frag = typename F::frag;
     static_assert(MR * RB == 32, "a wave owns 32 rows");
     constexpr int U = kSkMfmaUnroll;
-    __shared__ f4v stage[XS ? kThreads / 64 : 1][XS ? 256 * F::LINES : 1];
+    constexpr bool XS = XM == 1;
+    constexpr int STAGE = XM == 1 ? 256 * F::LINES : XM == 2 ? 256 : 1;  // 16-byte slots per wave
+    __shared__ f4v stage[XM ? kThreads / 64 : 1][STAGE];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int64_t task = (int64_t)blockIdx.x * (kThreads / 64) + wave;
@@ -525,6 +540,87 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
                     const int c = (u % UBL) * CPB + cq;
                     const f4v t = st[(u / UBL) * 256 + rdx[i] + (c ^ ((r >> 1) & 7))];
                     F::mma(__builtin_bit_cast(frag, t), vc[u], acc[i]);
+                }
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int u = 0; u < UB; ++u) vc[u] = vn[u];
+        }
+    } else if constexpr (XM == 2) {
+        constexpr int ESZ = (int)sizeof(T), EPC = 16 / ESZ;  // values per 16-byte chunk
+        constexpr int LPK = 32 / EPC;                         // lanes (chunks) per k-row of the wave's 32 values
+        constexpr int KPI = 64 / LPK;                         // k-rows per load instruction
+        constexpr int GK = 4 * KPI;                           // k-rows per staged group (4 loads per lane)
+        constexpr int UB = GK / F::KBLK;                      // blocks per staged group
+        // copy: instruction j moves k-rows KPI*j + lane/LPK, chunk lane%LPK of
+        // the wave's values (a chunk past R reads the last one, never stored)
+        const int cl = lane % LPK;
+        const int64_t cstart = row0 + (int64_t)cl * EPC <= R - EPC ? row0 + (int64_t)cl * EPC : R - EPC;
+        const T* src0 = X + cstart;
+        int krj[4], dsl[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int kr = KPI * j + lane / LPK;
+            krj[j] = kr;
+            if constexpr (ESZ == 4) dsl[j] = (kr ^ ((kr >> 2) & 1)) * 8 + (cl ^ (((kr >> 3) & 1) << 2));
+            else dsl[j] = kr * 4 + cl;
+        }
+        f4v* st = stage[wave];
+        const int ng = (bf - blk) / UB;
+        f4v data[4];
+        frag vc[UB], vn[UB];
+        auto load_x = [&](int b0) {
+            const int64_t k0 = (int64_t)b0 * F::KBLK;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) data[j] = *reinterpret_cast<const f4v*>(src0 + (k0 + krj[j]) * xs_k);
+        };
+        auto load_v = [&](int b0, frag(&vv)[UB]) {
+#pragma unroll
+            for (int u = 0; u < UB; ++u) {
+                const int64_t k = (int64_t)(b0 + u) * F::KBLK + kq;
+                vv[u] = sk_run<VV>(vr + k * vs_k, vs_k);
+            }
+        };
+        if (ng > 0) {
+            load_x(blk);
+            load_v(blk, vc);
+        }
+        for (int gi = 0; gi < ng; ++gi, blk += UB) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) st[dsl[j]] = data[j];
+            asm volatile("" ::: "memory");
+            if (gi + 1 < ng) {  // the next group's X and V, in flight during this group's math
+                load_x(blk + UB);
+                load_v(blk + UB, vn);
+            }
+#pragma unroll
+            for (int u = 0; u < UB; ++u)
+#pragma unroll
+                for (int i = 0; i < RB; ++i) {
+                    frag a;
+                    if constexpr (ESZ == 4) {
+                        // value r of k-rows u*KBLK + kq + e
+                        const float* sf = reinterpret_cast<const float*>(st);
+                        const int r = i * MR + (lane % MR);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int kr = u * F::KBLK + kq + e;
+                            const int c = (r >> 2) ^ (((kr >> 3) & 1) << 2);
+                            a[e] = sf[((kr ^ ((kr >> 2) & 1)) * 8 + c) * 4 + (r & 3)];
+                        }
+                    } else {
+                        // 16-lane group g: values c0 = 16 (g & 1) .., k-rows
+                        // u*16 + 8 (g >> 1) .. + 7 (two reads of four)
+                        const int gq = lane >> 4, li = lane & 15;
+                        const int kr = u * 16 + 8 * (gq >> 1) + (li >> 2);
+                        const int c0 = 16 * (gq & 1) + 4 * (li & 3);
+                        typedef __attribute__((address_space(3))) s4v lds_s4v;
+                        const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)st;
+                        const uint32_t ad = base + (uint32_t)(kr * 64 + c0 * 2);
+                        const s4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v*)(uintptr_t)ad);
+                        const s4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v*)(uintptr_t)(ad + 4 * 64));
+                        a = __builtin_bit_cast(frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                    }
+                    F::mma(a, vc[u], acc[i]);
                 }
             asm volatile("" ::: "memory");
 #pragma unroll
@@ -694,13 +790,13 @@ int32_t outer(const T* a, const T* b, float* c, int M, int N, int batch) {
     return ch::check_hip(hipGetLastError(), "outer_kernel");
 }
 
-template <typename T, int MR, int RB, bool XS, bool VV>
+template <typename T, int MR, int RB, int XM, bool VV>
 int32_t skinny_mfma_launch(const T* X, const T* V, float* y, float* part, int64_t R, int S, int K, int64_t xs_r,
                            int64_t xs_k, int64_t vs_s, int64_t vs_k, int64_t ys_i, int64_t ys_s, int64_t x_batch,
                            int64_t v_batch, int64_t y_batch, int batch, int64_t nrb, int groups, int bpg) {
     const int64_t waves = nrb * groups;
     const dim3 g((unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64)), (unsigned)batch);
-    skinny_mfma_kernel<T, MR, RB, XS, VV><<<g, kThreads, 0, ch::stream()>>>(
+    skinny_mfma_kernel<T, MR, RB, XM, VV><<<g, kThreads, 0, ch::stream()>>>(
         X, V, y, part, R, S, K, xs_r, xs_k, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch, y_batch, nrb, groups, bpg);
     int32_t st = ch::check_hip(hipGetLastError(), "skinny_mfma_kernel");
     if (st != CLEAVE_HIP_OK || groups == 1) return st;
@@ -717,9 +813,12 @@ int32_t skinny_mfma_mr(const T* X, const T* V, float* y, int64_t R, int S, int K
                        int64_t y_batch, int batch) {
     using F = SkMfma<T, MR>;
     constexpr int64_t esz = sizeof(T);
-    // 16-byte loads along k (X staged through LDS): unit k stride, and every
-    // row (and batch entry) start aligned
+    // X staged through LDS with 16-byte loads (XM 1 along k, 2 along r):
+    // unit stride along one, and every row (k-row) and batch entry aligned.
+    // With r contiguous the k-row pitch is R, so no 16-byte piece straddles R.
     const bool xv = xs_k == 1 && aligned16(X) && (xs_r * esz) % 16 == 0 && (x_batch * esz) % 16 == 0;
+    const bool xt = !xv && xs_r == 1 && xs_k == R && aligned16(X) && (xs_k * esz) % 16 == 0 &&
+                    (x_batch * esz) % 16 == 0;
     const bool vv = vs_k == 1 && aligned16(V) && (vs_s * esz) % 16 == 0 && (v_batch * esz) % 16 == 0;
     const int64_t nrb = (R + MR * RB - 1) / (MR * RB);
     const int nblk = (K + F::KBLK - 1) / F::KBLK;
@@ -727,15 +826,15 @@ int32_t skinny_mfma_mr(const T* X, const T* V, float* y, int64_t R, int S, int K
     // unstaged), each group at least 8 blocks deep, and the partial blocks at
     // most an eighth of X's bytes.
     const int cus = ch::num_cus() > 0 ? ch::num_cus() : 1;
-    const int64_t want = (xv ? 8LL : 16LL) * cus;
+    const int64_t want = (xv || xt ? 8LL : 16LL) * cus;
     int64_t groups = (want + nrb * batch - 1) / (nrb * batch);
     groups = std::min<int64_t>(groups, std::max(1, nblk / 8));
     const int64_t part_per_group = nrb * (int64_t)(MR * RB * MR) * 4;  // bytes per batch entry
     groups = std::min<int64_t>(groups, std::max<int64_t>(1, R * K * esz / 8 / part_per_group));
     if (groups < 1) groups = 1;
     int bpg = (int)((nblk + groups - 1) / groups);
-    if (xv) {  // staged groups start on 128 bytes of the rows
-        constexpr int ub = 128 * F::LINES / (F::KBLK * (int)sizeof(T));
+    if (xv || xt) {  // whole staged groups: 128 bytes of the rows, or 32 (f32) / 64 (bf16) k-rows
+        const int ub = xv ? 128 * F::LINES / (F::KBLK * (int)sizeof(T)) : (int)(128 / esz) / F::KBLK;
         bpg = (bpg + ub - 1) / ub * ub;
     }
     groups = (nblk + bpg - 1) / bpg;
@@ -746,10 +845,11 @@ int32_t skinny_mfma_mr(const T* X, const T* V, float* y, int64_t R, int S, int K
     }
 #define CH_SK_ARGS X, V, y, part, R, S, K, xs_r, xs_k, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch, y_batch, batch, nrb, \
                    (int)groups, bpg
-    if (xv && vv) return skinny_mfma_launch<T, MR, RB, true, true>(CH_SK_ARGS);
-    if (xv) return skinny_mfma_launch<T, MR, RB, true, false>(CH_SK_ARGS);
-    if (vv) return skinny_mfma_launch<T, MR, RB, false, true>(CH_SK_ARGS);
-    return skinny_mfma_launch<T, MR, RB, false, false>(CH_SK_ARGS);
+    if (xv) return vv ? skinny_mfma_launch<T, MR, RB, 1, true>(CH_SK_ARGS)
+                      : skinny_mfma_launch<T, MR, RB, 1, false>(CH_SK_ARGS);
+    if (xt) return vv ? skinny_mfma_launch<T, MR, RB, 2, true>(CH_SK_ARGS)
+                      : skinny_mfma_launch<T, MR, RB, 2, false>(CH_SK_ARGS);
+    return vv ? skinny_mfma_launch<T, MR, RB, 0, true>(CH_SK_ARGS) : skinny_mfma_launch<T, MR, RB, 0, false>(CH_SK_ARGS);
 #undef CH_SK_ARGS
 }
 

@@ -161,7 +161,7 @@ def test_skinny_shapes_misaligned_views(hip, oracle, dtype, off, M, N, K, ta, tb
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-@pytest.mark.parametrize("M,N,K", [(700, 10, 300), (10, 700, 300), (450, 24, 200)])
+@pytest.mark.parametrize("M,N,K", [(700, 10, 300), (10, 700, 300), (450, 24, 200), (712, 12, 300), (20, 712, 260)])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_skinny_clamped_rows_and_columns_stay_apart(hip, oracle, dtype, M, N, K, ta, tb):
     # Rows past the long dimension read its last row, and columns past the
