@@ -325,11 +325,12 @@ int split_count(int M, int N, int K) {
         // the slices must fill the CUs for the ping-pong kernel to take them
         if (tiles * S >= cus) return S;
     }
-    // 128 x 128 tiles: slices of at least 1024 that fill a round of them,
-    // for the 128 x 128 ping-pong kernel (1024^2 x 4096: 66.7 against 77.2
+    // 128 x 128 tiles that one round of the ping-pong kernel would leave
+    // under 77% full: slices of at least 1024 that fill a round of them, for
+    // that kernel (1024^2 x 4096: 66.7 against 77.2
     // us as 64 x 64 tiles; 1024^2 x 8192 121.9 against 152.6; 512^2 x 16384
     // 66.9 against 72.0 as 8 slices of 64 x 64 tiles)
-    if (M % 128 == 0 && N % 128 == 0) {
+    if (M % 128 == 0 && N % 128 == 0 && (double)(M / 128) * (N / 128) < 0.77 * cus) {
         const int64_t tiles = (int64_t)(M / 128) * (N / 128);
         int S = 1;
         while (tiles * S < cus && K % (16 * S * 2) == 0 && K / (S * 2) >= 1024) S *= 2;
@@ -345,6 +346,7 @@ int split_count(int M, int N, int K) {
 
 int32_t dispatch(const float* a, const float* b, float* c, int M, int N, int K, int batch, int ta, int tb,
                  int splits);
+bool try_round_split(const float* a, const float* b, float* c, int M, int N, int K, int ta, int tb, int32_t* st);
 
 }  // namespace
 
@@ -372,6 +374,67 @@ bool try_k_split(const float* a, const float* b, float* c, int M, int N, int K, 
     return true;
 }
 
+template <bool TA, bool TB>
+int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb,
+               int64_t ldc, int batch, int64_t sA, int64_t sB, int64_t sC);
+
+// A product of 128 x 128 tiles (fewer 256 x 256 tiles than CUs) whose last
+// round would be ragged: the first M1 rows of C run whole rounds of tiles,
+// the remaining tile-rows as S K-slices that fill one more round, added in
+// order into their rows (deterministic).  Chosen when a model in units of
+// one full-K tile on the ping-pong kernel (rounds of tiles; the tiled
+// kernels at 0.78 of its rate, as measured at 2176^3 - 3584^3; the slices'
+// extra bytes at 5 TB/s and 4 us for the extra launches) estimates it
+// faster than the unsplit product.  Measured: 3072^3 409 against 451 us,
+// 3584^3 644 against 826, 2304^3 184 against 207, 2176^3 157 against 196,
+// 3072^2 x 1024 151 against 156.  *st is the outcome; false when not split.
+bool try_round_split(const float* a, const float* b, float* c, int M, int N, int K, int ta, int tb, int32_t* st) {
+    const int cus = ch::num_cus() > 0 ? ch::num_cus() : 1;
+    if (M % 128 || N % 128 || K % 16 || ((uintptr_t)a & 15) || ((uintptr_t)b & 15) || ((uintptr_t)c & 15))
+        return false;
+    const int64_t big = (int64_t)(M / 256) * (N / 256);
+    const int tn = N / 128, tm = M / 128;
+    const int64_t T = (int64_t)tm * tn;
+    if (big >= cus || T <= cus) return false;
+    const int64_t full = T / cus;
+    const int t1 = (int)(full * cus / tn);  // tile-rows of whole rounds
+    if (t1 <= 0 || t1 >= tm) return false;
+    const int64_t T1 = (int64_t)t1 * tn, T2 = T - T1;
+    int S = (int)(cus / T2);
+    while (S >= 2 && (K % (16 * S) != 0 || K / S < 256)) --S;
+    if (S < 2) return false;
+    // model, in full-K tile times on the ping-pong kernel
+    const int64_t rounds = (T + cus - 1) / cus;
+    const double fill = (double)T / (double)(rounds * cus);
+    const double unsplit = fill >= 0.77 ? (double)rounds : (double)T / cus / 0.78;
+    const double tile_us = 2.0 * 128 * 128 * K * cus / (157.3e12 * 0.93) * 1e6;  // one tile on one CU
+    const double extra_us = (double)T2 * 128 * 128 * 4 * (2.0 * S + 1.0) / 5e12 * 1e6 + 4.0;
+    const double split =
+        (double)((T1 + cus - 1) / cus) + (double)((T2 * S + cus - 1) / cus) / S + extra_us / tile_us;
+    if (split >= unsplit) return false;
+    const int M1 = t1 * 128, M2 = M - M1;
+    float* part = (float*)ch::scratch_try(9, sizeof(float) * (size_t)S * M2 * N);
+    if (!part) return false;
+    // Rows [0, M1): whole rounds.  Rows [M1, M): S slices of K into part.  A
+    // keeps its full pitch (its rows, or with ta its columns, are offset).
+    const int64_t lda = ta ? M : K, ldb = tb ? K : N;
+    const float* a2 = ta ? a + M1 : a + (int64_t)M1 * K;
+    const int kk = K / S;
+    const int64_t sA = ta ? (int64_t)kk * lda : kk, sB = tb ? kk : (int64_t)kk * ldb, sC = (int64_t)M2 * N;
+    auto run = [&](auto tag) {
+        constexpr bool TA = decltype(tag)::value / 2, TB = decltype(tag)::value % 2;
+        int32_t r = launch<TA, TB>(a, b, c, M1, N, K, lda, ldb, N, 1, (int64_t)M1 * K, (int64_t)K * N, (int64_t)M1 * N);
+        if (r == CLEAVE_HIP_OK) r = launch<TA, TB>(a2, b, part, M2, N, kk, lda, ldb, N, S, sA, sB, sC);
+        return r;
+    };
+    if (!ta && !tb) *st = run(std::integral_constant<int, 0>{});
+    else if (!ta && tb) *st = run(std::integral_constant<int, 1>{});
+    else if (ta && !tb) *st = run(std::integral_constant<int, 2>{});
+    else *st = run(std::integral_constant<int, 3>{});
+    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c + (int64_t)M1 * N, (int64_t)M2 * N, S);
+    return true;
+}
+
 // The aligned kernels; false when none takes the shape.
 template <bool TA, bool TB>
 bool launch_fast(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
@@ -393,27 +456,27 @@ bool launch_fast(const float* a, const float* b, float* c, int M, int N, int K, 
         if (tiles32 <= 2 * cus &&
             launch_small<TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
             return true;
+        // The ping-pong kernel on 128 x 128 tiles (8 waves of 64 x 32, a
+        // 6-deep ring: one workgroup per CU) where its last round of tiles is
+        // at least 77% full.  Against the tiled kernels below: 2048^3 117.6
+        // against 131.2 us, 2048^2 x 4096 229.6 against 256.8, 3072 x 4096 x
+        // 2048 (three rounds) 349.7 against 363.4, 2560^3 (400 tiles, 78%)
+        // 285.0 against 304.1; 3072^3 (576, 75%) 510.4 against 453.8 and
+        // 2304^3 (324, 63%) 256.7 against 208.2 stay tiled.
+        const int64_t tiles128 = (int64_t)(M / 128) * (N / 128) * batch;
+        {
+            const int64_t rounds = (tiles128 + cus - 1) / cus;
+            if (tiles128 > 0 && (double)tiles128 >= 0.77 * (double)(rounds * cus) &&
+                launch_pingpong<TA, TB, 128>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
+                return true;
+        }
         // Fewer 128 x 128 tiles than CUs: 64 x 64 tiles with a 4-deep ring
         // (five workgroups per CU) put the product on 4x the CUs.  1024^3 23.9
         // against 66.7 us on 128 x 128 tiles, 1280^3 49.0 against 84.7,
         // 1536^3 82.9 against 103; a 16-deep ring measured 2-18% slower.
-        const int64_t tiles128 = (int64_t)(M / 128) * (N / 128) * batch;
         if (tiles128 < cus &&
             launch_tiled<64, 64, 16, 2, 2, 4, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
             return true;
-        // From a full round of 128 x 128 tiles, the ping-pong kernel on them
-        // (8 waves of 64 x 32, a 6-deep ring: one workgroup per CU), where its
-        // last round is at least 77% full.  Against the tiled kernels below:
-        // 2048^3 117.6 against 131.2 us, 2048^2 x 4096 229.6 against 256.8,
-        // 3072 x 4096 x 2048 (three rounds) 349.7 against 363.4, 2560^3 (400
-        // tiles, 78%) 285.0 against 304.1; 3072^3 (576, 75%) 510.4 against
-        // 453.8 and 2304^3 (324, 63%) 256.7 against 208.2 stay tiled.
-        if (tiles128 >= cus) {
-            const int64_t rounds = (tiles128 + cus - 1) / cus;
-            if ((double)tiles128 >= 0.77 * (double)(rounds * cus) &&
-                launch_pingpong<TA, TB, 128>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, st))
-                return true;
-        }
         // 128 x 128 tiles run four workgroups per CU, 128 x 64 tiles six.
         // Where the last round of 128 x 128 tiles would fill under 70% of
         // the CUs' slots, the twice as many 128 x 64 tiles balance better:
@@ -482,6 +545,7 @@ int32_t dispatch(const float* a, const float* b, float* c, int M, int N, int K, 
     if (splits <= 1 && (M == 1 || N == 1 || K == 1)) return ch::matmul_vector_f32(a, b, c, M, N, K, batch, ta, tb);
     int32_t st = CLEAVE_HIP_OK;
     if (splits <= 1 && batch == 1 && try_k_split(a, b, c, M, N, K, ta, tb, &st)) return st;
+    if (splits <= 1 && batch == 1 && try_round_split(a, b, c, M, N, K, ta, tb, &st)) return st;
     const int64_t lda = ta ? M : K, ldb = tb ? K : N, ldc = N;
     int64_t sA = (int64_t)M * K, sB = (int64_t)K * N, sC = (int64_t)M * N;
     int kk = K;

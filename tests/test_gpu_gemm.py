@@ -607,10 +607,10 @@ def test_padded_infinities_and_nans(hip, oracle, dtype):
 # The aligned kernels are chosen by tile count (on a 256-CU MI355X): f32 runs
 # the small kernel up to 512 tiles of 32 x 32 (640^3), 64 x 64 tiles below
 # 256 tiles of 128 x 128 (1024^2 x 512, 1280^2 x 256), the ping-pong kernel on
-# 128 x 128 tiles from one full round of them whose last round is at least
-# 77% full (2048^2 x 128; x 16, one k-tile; 2048 x 4096 x 48; 2560^2 x 64;
-# three rounds at 3072 x 4096 x 32), 128 x 64 tiles where the last round of
-# four workgroups per CU would be under 70% full (2304^2 x 128); bf16 runs 64 x 128
+# 128 x 128 tiles where their last round is at least 77% full (2048^2 x 128;
+# x 16, one k-tile; 2048 x 4096 x 48; 2560^2 x 64; three rounds at 3072 x 4096
+# x 32), 128 x 64 tiles where the last round of four workgroups per CU would
+# be under 70% full and K is too short to split it (2304^2 x 128); bf16 runs 64 x 128
 # tiles for up to a round of 128 x 128 (1024^2 x 512; 128 x 128 with an
 # m-contiguous A), two-stage 128 x 128 tiles for several rounds
 # (2304^2 x 128), and 256 x 256 tiles from 128 of them (3072^2 x 128 tiled,
@@ -679,6 +679,25 @@ def test_f32_k_split_every_entry(hip, oracle, M, N, K, ta, tb):
     ref = oracle.matmul(Ak, Bk, trans_b=True, threads=16)
     den = np.abs(Ak) @ np.abs(Bk).T
     assert_gemm_close(got, ref, den, K, f"k-split {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_f32_ragged_round_split_every_entry(hip, oracle, ta, tb):
+    # 324 tiles of 128 x 128 (one round and 68 left): rows 0-1919 run a whole
+    # round on the ping-pong kernel, rows 1920-2303 as 3 K-slices added in
+    # order into their rows.  Every entry against the loop (A.B^T form on
+    # transposed copies), and bitwise the same on a second call.
+    M, N, K = 2304, 2304, 768
+    A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=5 + 2 * ta + tb)
+    a, b = hip.from_numpy(A), hip.from_numpy(B)
+    got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    again = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    Ak = np.ascontiguousarray(Au.T if ta else Au)
+    Bk = np.ascontiguousarray(Bu if tb else Bu.T)
+    ref = oracle.matmul(Ak, Bk, trans_b=True, threads=16)
+    den = np.abs(Ak).astype(np.float64) @ np.abs(Bk).astype(np.float64).T
+    assert_gemm_close(got, ref, den, K, f"round split {M}x{N}x{K} ta={ta} tb={tb}")
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
