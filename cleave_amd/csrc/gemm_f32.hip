@@ -332,6 +332,14 @@ int split_count(int M, int N, int K) {
     // 66.9 against 72.0 as 8 slices of 64 x 64 tiles)
     if (M % 128 == 0 && N % 128 == 0 && (double)(M / 128) * (N / 128) < 0.77 * cus) {
         const int64_t tiles = (int64_t)(M / 128) * (N / 128);
+        // as many slices, at least 512 deep, as fit one round, if that round
+        // is at least 77% full (384 x 3072^2: 3 slices, 216 tiles)
+        for (int S = (int)(cus / tiles); S >= 2; --S)
+            if (K % (16 * S) == 0 && K / S >= 512) {
+                if (tiles * S >= 0.77 * cus) return S;
+                break;
+            }
+        // else a power of two that fills at least a round
         int S = 1;
         while (tiles * S < cus && K % (16 * S * 2) == 0 && K / (S * 2) >= 1024) S *= 2;
         if (S > 1 && tiles * S >= cus) return S;
@@ -346,7 +354,6 @@ int split_count(int M, int N, int K) {
 
 int32_t dispatch(const float* a, const float* b, float* c, int M, int N, int K, int batch, int ta, int tb,
                  int splits);
-bool try_round_split(const float* a, const float* b, float* c, int M, int N, int K, int ta, int tb, int32_t* st);
 
 }  // namespace
 
@@ -362,77 +369,100 @@ int32_t sum_slices_f32(const float* part, float* c, int64_t n, int S) {
 
 namespace {
 
-// One product (batch 1) as split_count's K slices, when it asks for more than
-// one and the slice buffer can be had: *st is the outcome; false when not split.
-bool try_k_split(const float* a, const float* b, float* c, int M, int N, int K, int ta, int tb, int32_t* st) {
-    if (((uintptr_t)c & 15) != 0) return false;
-    const int S = split_count(M, N, K);
-    float* part = S > 1 ? (float*)ch::scratch_try(9, sizeof(float) * (size_t)S * M * N) : nullptr;
-    if (!part) return false;
-    *st = dispatch(a, b, part, M, N, K, 1, ta, tb, S);
-    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, (int64_t)M * N, S);
-    return true;
-}
-
 template <bool TA, bool TB>
 int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb,
                int64_t ldc, int batch, int64_t sA, int64_t sB, int64_t sC);
 
-// A product of 128 x 128 tiles (fewer 256 x 256 tiles than CUs) whose last
-// round would be ragged: the first M1 rows of C run whole rounds of tiles,
-// the remaining tile-rows as S K-slices that fill one more round, added in
-// order into their rows (deterministic).  Chosen when a model in units of
-// one full-K tile on the ping-pong kernel (rounds of tiles; the tiled
-// kernels at 0.78 of its rate, as measured at 2176^3 - 3584^3; the slices'
-// extra bytes at 5 TB/s and 4 us for the extra launches) estimates it
-// faster than the unsplit product.  Measured: 3072^3 409 against 451 us,
-// 3584^3 644 against 826, 2304^3 184 against 207, 2176^3 157 against 196,
-// 3072^2 x 1024 151 against 156.  *st is the outcome; false when not split.
-bool try_round_split(const float* a, const float* b, float* c, int M, int N, int K, int ta, int tb, int32_t* st) {
-    const int cus = ch::num_cus() > 0 ? ch::num_cus() : 1;
-    if (M % 128 || N % 128 || K % 16 || ((uintptr_t)a & 15) || ((uintptr_t)b & 15) || ((uintptr_t)c & 15))
-        return false;
-    const int64_t big = (int64_t)(M / 256) * (N / 256);
-    const int tn = N / 128, tm = M / 128;
-    const int64_t T = (int64_t)tm * tn;
-    if (big >= cus || T <= cus) return false;
-    const int64_t full = T / cus;
-    const int t1 = (int)(full * cus / tn);  // tile-rows of whole rounds
-    if (t1 <= 0 || t1 >= tm) return false;
-    const int64_t T1 = (int64_t)t1 * tn, T2 = T - T1;
-    int S = (int)(cus / T2);
-    while (S >= 2 && (K % (16 * S) != 0 || K / S < 256)) --S;
-    if (S < 2) return false;
-    // model, in full-K tile times on the ping-pong kernel
-    const int64_t rounds = (T + cus - 1) / cus;
-    const double fill = (double)T / (double)(rounds * cus);
-    const double unsplit = fill >= 0.77 ? (double)rounds : (double)T / cus / 0.78;
-    const double tile_us = 2.0 * 128 * 128 * K * cus / (157.3e12 * 0.93) * 1e6;  // one tile on one CU
-    const double extra_us = (double)T2 * 128 * 128 * 4 * (2.0 * S + 1.0) / 5e12 * 1e6 + 4.0;
-    const double split =
-        (double)((T1 + cus - 1) / cus) + (double)((T2 * S + cus - 1) / cus) / S + extra_us / tile_us;
-    if (split >= unsplit) return false;
-    const int M1 = t1 * 128, M2 = M - M1;
-    float* part = (float*)ch::scratch_try(9, sizeof(float) * (size_t)S * M2 * N);
+// launch<TA, TB> for run-time flags.
+int32_t launch_layout(int ta, int tb, const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
+                      int64_t ldb, int64_t ldc, int batch, int64_t sA, int64_t sB, int64_t sC) {
+    if (!ta && !tb) return launch<false, false>(a, b, c, M, N, K, lda, ldb, ldc, batch, sA, sB, sC);
+    if (!ta && tb) return launch<false, true>(a, b, c, M, N, K, lda, ldb, ldc, batch, sA, sB, sC);
+    if (ta && !tb) return launch<true, false>(a, b, c, M, N, K, lda, ldb, ldc, batch, sA, sB, sC);
+    return launch<true, true>(a, b, c, M, N, K, lda, ldb, ldc, batch, sA, sB, sC);
+}
+
+// One product (batch 1, C of pitch N; A and B of pitches lda and ldb, so that
+// a band of a larger product's rows keeps its operand pitches) as
+// split_count's K slices, when it asks for more than one and the slice
+// buffer can be had: *st is the outcome; false when not split.
+bool try_k_split(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb, int ta,
+                 int tb, int32_t* st) {
+    if (((uintptr_t)c & 15) != 0) return false;
+    const int S = split_count(M, N, K);
+    float* part = S > 1 ? (float*)ch::scratch_try(9, sizeof(float) * (size_t)S * M * N) : nullptr;
     if (!part) return false;
-    // Rows [0, M1): whole rounds.  Rows [M1, M): S slices of K into part.  A
-    // keeps its full pitch (its rows, or with ta its columns, are offset).
-    const int64_t lda = ta ? M : K, ldb = tb ? K : N;
-    const float* a2 = ta ? a + M1 : a + (int64_t)M1 * K;
     const int kk = K / S;
-    const int64_t sA = ta ? (int64_t)kk * lda : kk, sB = tb ? kk : (int64_t)kk * ldb, sC = (int64_t)M2 * N;
-    auto run = [&](auto tag) {
-        constexpr bool TA = decltype(tag)::value / 2, TB = decltype(tag)::value % 2;
-        int32_t r = launch<TA, TB>(a, b, c, M1, N, K, lda, ldb, N, 1, (int64_t)M1 * K, (int64_t)K * N, (int64_t)M1 * N);
-        if (r == CLEAVE_HIP_OK) r = launch<TA, TB>(a2, b, part, M2, N, kk, lda, ldb, N, S, sA, sB, sC);
-        return r;
-    };
-    if (!ta && !tb) *st = run(std::integral_constant<int, 0>{});
-    else if (!ta && tb) *st = run(std::integral_constant<int, 1>{});
-    else if (ta && !tb) *st = run(std::integral_constant<int, 2>{});
-    else *st = run(std::integral_constant<int, 3>{});
-    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c + (int64_t)M1 * N, (int64_t)M2 * N, S);
+    const int64_t sA = ta ? (int64_t)kk * lda : kk, sB = tb ? kk : (int64_t)kk * ldb;
+    *st = launch_layout(ta, tb, a, b, part, M, N, kk, lda, ldb, N, S, sA, sB, (int64_t)M * N);
+    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, (int64_t)M * N, S);
     return true;
+}
+
+// Rough time of an aligned product, in us, by the kernel the launchers pick:
+// rounds of 256 x 256 tiles (0.96 of peak per tile), rounds of 128 x 128
+// tiles on the ping-pong kernel (0.93) when the last is at least 77% full,
+// the tiled kernels (0.78 of that, as measured at 2176^3 - 3584^3), or, below
+// a round, K slices and small tiles (0.70).
+double est_us(int M, int N, int K) {
+    const double cus = ch::num_cus() > 0 ? ch::num_cus() : 1, peak = 157.3e12;
+    const int64_t big = (int64_t)(M / 256) * (N / 256), t128 = (int64_t)(M / 128) * (N / 128);
+    if (M % 256 == 0 && N % 256 == 0 && big >= cus)
+        return std::ceil(big / cus) * cus * 2.0 * 256 * 256 * K / (peak * 0.96) * 1e6;
+    const double flops = 2.0 * M * N * K;
+    if (M % 128 == 0 && N % 128 == 0 && t128 >= 0.77 * cus) {
+        const double rounds = std::ceil(t128 / cus);
+        if (t128 >= 0.77 * rounds * cus) return rounds * cus * 2.0 * 128 * 128 * K / (peak * 0.93) * 1e6;
+        return flops / (peak * 0.93 * 0.78) * 1e6;
+    }
+    return flops / (peak * 0.70) * 1e6;
+}
+
+int32_t product(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb, int ta,
+                int tb, int depth);
+
+// A product whose tiles (256 x 256 from a round of them, else 128 x 128 from
+// more than a round) end in a ragged round: the first M1 rows of C, the
+// whole rounds, run as one product and the remaining rows as another, which
+// takes its own kernel (K slices, 128 x 128 tiles, or a split of its own).
+// Chosen when est_us gives the two, plus 4 us for the extra launches, at
+// least 3% under the whole.  Measured (128 x 128 tiles; the rest as K slices
+// that fill one more round, added in order into their rows): 3072^3 409
+// against 451 us, 3584^3 644 against 826, 2304^3 184 against 207, 2176^3 157
+// against 196, 3072^2 x 1024 151 against 156.  Deterministic: each part's
+// kernels are chosen by its shape alone.  *st is the outcome; false when not
+// split.
+bool try_round_split(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb,
+                     int ta, int tb, int depth, int32_t* st) {
+    const int cus = ch::num_cus() > 0 ? ch::num_cus() : 1;
+    if (depth >= 3 || K % 16 || ((uintptr_t)a & 15) || ((uintptr_t)b & 15) || ((uintptr_t)c & 15)) return false;
+    const int64_t big = (int64_t)(M / 256) * (N / 256), t128 = (int64_t)(M / 128) * (N / 128);
+    int tile;
+    int64_t T;
+    if (M % 256 == 0 && N % 256 == 0 && big >= cus) tile = 256, T = big;
+    else if (M % 128 == 0 && N % 128 == 0 && t128 > cus) tile = 128, T = t128;
+    else return false;
+    const int tn = N / tile, tm = M / tile;
+    const int t1 = (int)(T / cus * cus / tn);  // tile-rows of whole rounds
+    if (t1 <= 0 || t1 >= tm) return false;
+    const int M1 = t1 * tile, M2 = M - M1;
+    if (est_us(M1, N, K) + est_us(M2, N, K) + 4.0 >= 0.97 * est_us(M, N, K)) return false;
+    // A keeps its full pitch (its rows, or with ta its columns, are offset)
+    const float* a2 = ta ? a + M1 : a + (int64_t)M1 * lda;
+    *st = product(a, b, c, M1, N, K, lda, ldb, ta, tb, depth + 1);
+    if (*st == CLEAVE_HIP_OK) *st = product(a2, b, c + (int64_t)M1 * N, M2, N, K, lda, ldb, ta, tb, depth + 1);
+    return true;
+}
+
+// One product (batch 1, C of pitch N): K slices, a split at a ragged round,
+// or the launchers.
+int32_t product(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb, int ta,
+                int tb, int depth) {
+    int32_t st = CLEAVE_HIP_OK;
+    if (try_k_split(a, b, c, M, N, K, lda, ldb, ta, tb, &st)) return st;
+    if (try_round_split(a, b, c, M, N, K, lda, ldb, ta, tb, depth, &st)) return st;
+    return launch_layout(ta, tb, a, b, c, M, N, K, lda, ldb, N, 1, (int64_t)M * K, (int64_t)K * N,
+                         (int64_t)M * N);
 }
 
 // The aligned kernels; false when none takes the shape.
@@ -527,7 +557,7 @@ int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, in
             const int64_t plda = TA ? Mp : Kp, pldb = TB ? Kp : Np;
             const int64_t psA = (int64_t)Mp * Kp, psB = (int64_t)Kp * Np, psC = (int64_t)Mp * Np;
             int32_t s = CLEAVE_HIP_OK;
-            if (batch == 1 && try_k_split(pa, pb, pc, Mp, Np, Kp, TA, TB, &s)) return s;
+            if (batch == 1) return product(pa, pb, pc, Mp, Np, Kp, plda, pldb, TA, TB, 0);
             if (launch_fast<TA, TB>(pa, pb, pc, Mp, Np, Kp, plda, pldb, Np, batch, psA, psB, psC, &s)) return s;
             return launch_general<TA, TB>(pa, pb, pc, Mp, Np, Kp, plda, pldb, Np, batch, psA, psB, psC);
         };
@@ -543,10 +573,8 @@ int32_t dispatch(const float* a, const float* b, float* c, int M, int N, int K, 
                  int ta, int tb, int splits) {
     // a dimension of 1: matrix-vector or outer products (gemv.hip)
     if (splits <= 1 && (M == 1 || N == 1 || K == 1)) return ch::matmul_vector_f32(a, b, c, M, N, K, batch, ta, tb);
-    int32_t st = CLEAVE_HIP_OK;
-    if (splits <= 1 && batch == 1 && try_k_split(a, b, c, M, N, K, ta, tb, &st)) return st;
-    if (splits <= 1 && batch == 1 && try_round_split(a, b, c, M, N, K, ta, tb, &st)) return st;
     const int64_t lda = ta ? M : K, ldb = tb ? K : N, ldc = N;
+    if (splits <= 1 && batch == 1) return product(a, b, c, M, N, K, lda, ldb, ta, tb, 0);
     int64_t sA = (int64_t)M * K, sB = (int64_t)K * N, sC = (int64_t)M * N;
     int kk = K;
     if (splits > 1) {

@@ -681,13 +681,22 @@ def test_f32_k_split_every_entry(hip, oracle, M, N, K, ta, tb):
     assert_gemm_close(got, ref, den, K, f"k-split {M}x{N}x{K} ta={ta} tb={tb}")
 
 
-@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-def test_f32_ragged_round_split_every_entry(hip, oracle, ta, tb):
-    # 324 tiles of 128 x 128 (one round and 68 left): rows 0-1919 run a whole
-    # round on the ping-pong kernel, rows 1920-2303 as 3 K-slices added in
-    # order into their rows.  Every entry against the loop (A.B^T form on
-    # transposed copies), and bitwise the same on a second call.
-    M, N, K = 2304, 2304, 768
+@pytest.mark.parametrize("M,N,K,ta,tb", [
+    # 324 tiles of 128 x 128: rows 0-1791 a whole round on the ping-pong
+    # kernel, rows 1792-2303 a product of their own
+    *[(2304, 2304, 768, ta, tb) for ta in (0, 1) for tb in (0, 1)],
+    # 272 tiles of 256 x 256: rows 0-4095 a round of them, rows 4096-4351 on
+    # 64 x 64 tiles
+    *[(4352, 4096, 256, ta, tb) for ta in (0, 1) for tb in (0, 1)],
+    # 352 tiles of 256 x 256, whose remaining 768 rows (384 tiles of 128 x
+    # 128) split again: rows 0-2047, 2048-2559, 2560-2815
+    (2816, 8192, 512, 0, 0), (2816, 8192, 512, 1, 1),
+])
+def test_f32_ragged_round_split_every_entry(hip, oracle, M, N, K, ta, tb):
+    # A product whose last round of tiles is ragged runs as bands of rows:
+    # whole rounds, then the rest on its own kernels.  Every entry against the
+    # loop (A.B^T form on transposed copies), and bitwise the same on a second
+    # call.
     A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=5 + 2 * ta + tb)
     a, b = hip.from_numpy(A), hip.from_numpy(B)
     got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
