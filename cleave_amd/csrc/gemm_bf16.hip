@@ -350,23 +350,35 @@ bool launch_fast(const uint16_t* a, const uint16_t* b, float* c, int M, int N, i
 int split_count(int M, int N, int K) {
     const int cus = ch::num_cus();
     const int64_t tiles = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
-    if (tiles * 2 > cus) return 1;
+    if (tiles * 2 > cus) {
+        // Fewer 256 x 256 tiles than half a round (the band left by a split at
+        // a ragged round, 256 x 9216^2): as many slices, at least 1024 deep,
+        // as fit a round, if they make half a round, for those kernels.
+        const int64_t big = (M % 256 == 0 && N % 256 == 0) ? (int64_t)(M / 256) * (N / 256) : 0;
+        if (big > 0 && big * 2 < cus)
+            for (int S = (int)(cus / big); S >= 2; --S)
+                if (K % (64 * S) == 0 && K / S >= 1024) return big * S * 2 >= cus ? S : 1;
+        return 1;
+    }
     int S = 1;
     while (tiles * S * 2 <= cus && K % (64 * S * 2) == 0 && K / (S * 2) >= 1024) S *= 2;
     return S;
 }
 
-// One product as split_count's K slices into a scratch buffer, added in
-// order (ch::sum_slices_f32, deterministic); false when not split.
+// One product (C of pitch N; A and B of pitches lda and ldb, so that a band
+// of a larger product's rows keeps its operand pitches) as split_count's K
+// slices into a scratch buffer, added in order (ch::sum_slices_f32,
+// deterministic); false when not split.
 template <bool TA, bool TB>
-bool try_k_split(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int32_t* st) {
+bool try_k_split(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb,
+                 int32_t* st) {
     const int64_t n = (int64_t)M * N;
     if (((uintptr_t)c & 15) != 0 || n % 4 != 0) return false;
     const int S = split_count(M, N, K);
     float* part = S > 1 ? (float*)ch::scratch_try(10, sizeof(float) * (size_t)(S * n)) : nullptr;
     if (!part) return false;
     const int kk = K / S;
-    const Strides sl{TA ? M : K, TB ? K : N, TA ? (int64_t)kk * M : kk, TB ? kk : (int64_t)kk * N, n};
+    const Strides sl{lda, ldb, TA ? (int64_t)kk * lda : kk, TB ? kk : (int64_t)kk * ldb, n};
     if (!launch_fast<TA, TB>(a, b, part, M, N, kk, S, sl, st)) *st = launch<TA, TB>(a, b, part, M, N, kk, S, sl);
     if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, n, S);
     return true;
@@ -394,7 +406,7 @@ int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N,
         const ch::PadPlan p = ch::pad_plan(M, N, K, batch, TA, TB, a, b, 2, ch::num_cus(), kPadModel);
         auto gemm = [batch](const uint16_t* pa, const uint16_t* pb, float* pc, int Mp, int Np, int Kp) {
             int32_t s = CLEAVE_HIP_OK;
-            if (batch == 1 && try_k_split<TA, TB>(pa, pb, pc, Mp, Np, Kp, &s)) return s;
+            if (batch == 1 && try_k_split<TA, TB>(pa, pb, pc, Mp, Np, Kp, TA ? Mp : Kp, TB ? Kp : Np, &s)) return s;
             if (launch_fast<TA, TB>(pa, pb, pc, Mp, Np, Kp, batch, packed<TA, TB>(Mp, Np, Kp), &s)) return s;
             return launch<TA, TB>(pa, pb, pc, Mp, Np, Kp, batch, packed<TA, TB>(Mp, Np, Kp));
         };
@@ -403,18 +415,72 @@ int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N,
     return launch<TA, TB>(a, b, c, M, N, K, batch, packed<TA, TB>(M, N, K));
 }
 
+// Rough time of an aligned product, in us: rounds of 256 x 256 tiles (0.58
+// of the dense peak per tile, as 8192^3 runs) from half a round of them, else
+// 0.26 (1024^3 - 2048^3 on 128 x 128 or 64 x 128 tiles, and K slices).
+double est_us(int M, int N, int K) {
+    const double cus = ch::num_cus() > 0 ? ch::num_cus() : 1, peak = 2516e12;
+    const int64_t big = (M % 256 == 0 && N % 256 == 0) ? (int64_t)(M / 256) * (N / 256) : 0;
+    if (big * 2 >= cus) return std::ceil(big / cus) * cus * 2.0 * 256 * 256 * K / (peak * 0.58) * 1e6;
+    return 2.0 * M * N * K / (peak * 0.26) * 1e6;
+}
+
+template <bool TA, bool TB>
+int32_t product(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb,
+                int depth);
+
+// More than a round of 256 x 256 tiles ending in a ragged round: the first M1
+// rows of C, the whole rounds, run as one product and the remaining rows as
+// another, which takes its own kernel (K slices, smaller tiles, or a split of
+// its own), when est_us gives the two, plus 4 us for the extra launches, at
+// least 3% under the whole.  Deterministic: each part's kernels are chosen by
+// its shape alone.  *st is the outcome; false when not split.
+template <bool TA, bool TB>
+bool try_round_split(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb,
+                     int depth, int32_t* st) {
+    const int cus = ch::num_cus() > 0 ? ch::num_cus() : 1;
+    if (depth >= 3 || M % 256 || N % 256 || K % 64 || ((uintptr_t)a & 15) || ((uintptr_t)b & 15) ||
+        ((uintptr_t)c & 15))
+        return false;
+    const int64_t T = (int64_t)(M / 256) * (N / 256);
+    if (T <= cus) return false;
+    const int tn = N / 256, tm = M / 256;
+    const int t1 = (int)(T / cus * cus / tn);  // tile-rows of whole rounds
+    if (t1 <= 0 || t1 >= tm) return false;
+    const int M1 = t1 * 256, M2 = M - M1;
+    if (est_us(M1, N, K) + est_us(M2, N, K) + 4.0 >= 0.97 * est_us(M, N, K)) return false;
+    // A keeps its full pitch (its rows, or with TA its columns, are offset)
+    const uint16_t* a2 = TA ? a + M1 : a + (int64_t)M1 * lda;
+    *st = product<TA, TB>(a, b, c, M1, N, K, lda, ldb, depth + 1);
+    if (*st == CLEAVE_HIP_OK) *st = product<TA, TB>(a2, b, c + (int64_t)M1 * N, M2, N, K, lda, ldb, depth + 1);
+    return true;
+}
+
+// One product (C of pitch N): K slices for few tiles and a long K (an output
+// dimension of at most 32 streams its long operand instead, in launch_any), a
+// split at a ragged round, or the launchers.
+template <bool TA, bool TB>
+int32_t product(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb,
+                int depth) {
+    int32_t st = CLEAVE_HIP_OK;
+    if (M > 32 && N > 32 && try_k_split<TA, TB>(a, b, c, M, N, K, lda, ldb, &st)) return st;
+    if (try_round_split<TA, TB>(a, b, c, M, N, K, lda, ldb, depth, &st)) return st;
+    if (lda == (TA ? M : K) && ldb == (TB ? K : N)) return launch_any<TA, TB>(a, b, c, M, N, K, 1);
+    // a band of rows of a larger product (aligned: 256-row bands)
+    const Strides s{lda, ldb, (int64_t)M * K, (int64_t)K * N, (int64_t)M * N};
+    if (launch_fast<TA, TB>(a, b, c, M, N, K, 1, s, &st)) return st;
+    return launch<TA, TB>(a, b, c, M, N, K, 1, s);
+}
+
 int32_t dispatch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
                  int ta, int tb) {
     // a dimension of 1: matrix-vector or outer products (gemv.hip)
     if (M == 1 || N == 1 || K == 1) return ch::matmul_vector_bf16(a, b, c, M, N, K, batch, ta, tb);
-    // few tiles and a long K: K slices (an output dimension of at most 32
-    // streams its long operand instead, in launch_any)
-    int32_t st = CLEAVE_HIP_OK;
-    if (batch == 1 && M > 32 && N > 32) {
-        if (!ta && !tb && try_k_split<false, false>(a, b, c, M, N, K, &st)) return st;
-        if (!ta && tb && try_k_split<false, true>(a, b, c, M, N, K, &st)) return st;
-        if (ta && !tb && try_k_split<true, false>(a, b, c, M, N, K, &st)) return st;
-        if (ta && tb && try_k_split<true, true>(a, b, c, M, N, K, &st)) return st;
+    if (batch == 1) {
+        if (!ta && !tb) return product<false, false>(a, b, c, M, N, K, K, N, 0);
+        if (!ta && tb) return product<false, true>(a, b, c, M, N, K, K, K, 0);
+        if (ta && !tb) return product<true, false>(a, b, c, M, N, K, M, N, 0);
+        return product<true, true>(a, b, c, M, N, K, M, K, 0);
     }
     if (!ta && !tb) return launch_any<false, false>(a, b, c, M, N, K, batch);
     if (!ta && tb) return launch_any<false, true>(a, b, c, M, N, K, batch);

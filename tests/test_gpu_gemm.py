@@ -709,6 +709,24 @@ def test_f32_ragged_round_split_every_entry(hip, oracle, M, N, K, ta, tb):
     assert_gemm_close(got, ref, den, K, f"round split {M}x{N}x{K} ta={ta} tb={tb}")
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_bf16_ragged_round_split_every_entry(hip, oracle, ta, tb):
+    # 272 tiles of 256 x 256: rows 0-4095 a round of them, rows 4096-4351 a
+    # product of their own.  Every entry against the loop on the upcast values,
+    # and bitwise the same on a second call.
+    M, N, K = 4352, 4096, 512
+    A, B, Au, Bu = _operands(oracle, "bf16", M, N, K, ta, tb, seed=31 + 2 * ta + tb)
+    a, b = hip.from_numpy(A, "bf16"), hip.from_numpy(B, "bf16")
+    got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    again = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    Ak = np.ascontiguousarray(Au.T if ta else Au)
+    Bk = np.ascontiguousarray(Bu if tb else Bu.T)
+    ref = oracle.matmul(Ak, Bk, trans_b=True, threads=16)
+    den = np.abs(Ak).astype(np.float64) @ np.abs(Bk).astype(np.float64).T
+    assert_gemm_close(got, ref, den, K, f"bf16 round split {M}x{N}x{K} ta={ta} tb={tb}")
+
+
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [(100, 100, 100000), (70, 300, 30000)])
 def test_f32_ragged_long_k_every_entry(hip, oracle, M, N, K, ta, tb):
@@ -724,12 +742,15 @@ def test_f32_ragged_long_k_every_entry(hip, oracle, M, N, K, ta, tb):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-@pytest.mark.parametrize("M,N,K", [(64, 64, 65536), (128, 128, 65536), (512, 1024, 16384), (100, 100, 100000)])
+@pytest.mark.parametrize("M,N,K", [(64, 64, 65536), (128, 128, 65536), (512, 1024, 16384), (100, 100, 100000),
+                                   (256, 8448, 4096)])
 def test_bf16_k_split_every_entry(hip, oracle, M, N, K, ta, tb):
     # bf16 products with few 128 x 128 tiles and a long K run as K slices
     # (on the tiled kernels, on the general kernel for 64 x 64, and on the
-    # padded copies for 100 x 100), added in order; every entry against the
-    # f32 loop on the upcast values, and a second call gives the same bits.
+    # padded copies for 100 x 100), and with fewer 256 x 256 tiles than half a
+    # round as slices of those (256 x 8448: 33 tiles, 4 slices); added in
+    # order; every entry against the f32 loop on the upcast values, and a
+    # second call gives the same bits.
     A, B, Au, Bu = _operands(oracle, "bf16", M, N, K, ta, tb, seed=M + N + K + 2 * ta + tb)
     a, b = hip.from_numpy(A, "bf16"), hip.from_numpy(B, "bf16")
     got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
