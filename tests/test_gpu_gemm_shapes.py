@@ -1,0 +1,68 @@
+"""Matmul dispatch over many shapes on the GPU, through the C ABI.
+
+The aligned kernels are chosen by shape: the small-product kernel, 64 x 64 and
+128 x 128 tiles, the 128 x 128 and 256 x 256 ping-pong kernels, K slices,
+bands of rows at a ragged round of tiles, zero-padded copies for ragged
+shapes, the skinny kernels (an output dimension of 2-32), matrix-vector and
+outer products, and the guarded general kernel.  This file draws shapes
+around those thresholds (tile multiples and their neighbours, short and long
+K, one-row outputs) from a fixed seed, in both dtypes and random layouts, and
+checks every entry against the oracle's loop (oracle/oracle.c, linalg.matmul
+of /root/reference/stdlib/linalg/matrix.cleave:27-61) under the GEMM bound
+|C - C_ref| <= 1e-5 sqrt(K) sum|A||B|, and that a second call repeats bit for
+bit (every path sums in an order fixed by the shape).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import assert_gemm_close
+
+pytestmark = pytest.mark.gpu
+
+_DIMS = [1, 2, 17, 31, 32, 33, 64, 100, 127, 128, 129, 255, 256, 257, 384, 512, 640, 1000, 1024,
+         1536, 1920, 2048, 2304, 2816, 3072, 4352]
+_KS = [1, 2, 15, 16, 17, 48, 64, 100, 256, 512, 768, 1024, 2048, 4100]
+_MAX_MAC = 4e9  # oracle work per case
+
+
+def _cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        M, N = int(rng.choice(_DIMS)), int(rng.choice(_DIMS))
+        K = int(rng.choice(_KS))
+        if M * N * K > _MAX_MAC:
+            continue
+        dtype = "bf16" if rng.random() < 0.4 else "f32"
+        out.append((dtype, M, N, K, int(rng.integers(2)), int(rng.integers(2))))
+    return out
+
+
+def _operands(oracle, dtype, M, N, K, ta, tb, seed):
+    rng = np.random.default_rng(seed)
+    A32 = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B32 = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    if dtype == "bf16":
+        A, B = oracle.to_bf16(A32), oracle.to_bf16(B32)
+        return A, B, oracle.bf16_to_f32(A).reshape(A.shape), oracle.bf16_to_f32(B).reshape(B.shape)
+    return A32, B32, A32, B32
+
+
+@pytest.mark.parametrize("dtype,M,N,K,ta,tb", _cases(160, seed=2024))
+def test_shape_every_entry(hip, oracle, dtype, M, N, K, ta, tb):
+    A, B, Au, Bu = _operands(oracle, dtype, M, N, K, ta, tb, seed=M * 7 + N * 3 + K + 2 * ta + tb)
+    a, b = hip.from_numpy(A, dtype), hip.from_numpy(B, dtype)
+    got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    again = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert got.shape == (M, N)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "repeat"
+    Ak = np.ascontiguousarray(Au.T if ta else Au)
+    Bk = np.ascontiguousarray(Bu if tb else Bu.T)
+    ref = oracle.matmul(Ak, Bk, trans_b=True, threads=16)
+    den = np.abs(Ak).astype(np.float64) @ np.abs(Bk).astype(np.float64).T
+    if K == 1:  # one product added to a zero: exact
+        assert np.array_equal(got.view(np.uint32), ref.astype(np.float32).view(np.uint32))
+    else:
+        assert_gemm_close(got, ref, den, K, f"{dtype} {M}x{N}x{K} ta={ta} tb={tb}")
