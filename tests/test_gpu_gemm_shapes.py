@@ -66,3 +66,43 @@ def test_shape_every_entry(hip, oracle, dtype, M, N, K, ta, tb):
         assert np.array_equal(got.view(np.uint32), ref.astype(np.float32).view(np.uint32))
     else:
         assert_gemm_close(got, ref, den, K, f"{dtype} {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+def _batched_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        M, N = int(rng.choice(_DIMS[:19])), int(rng.choice(_DIMS[:19]))
+        K = int(rng.choice(_KS[:12]))
+        bsz = int(rng.choice([2, 3, 7, 16, 64]))
+        if bsz * M * N * K > _MAX_MAC / 2:
+            continue
+        dtype = "bf16" if rng.random() < 0.4 else "f32"
+        out.append((dtype, bsz, M, N, K, int(rng.integers(2)), int(rng.integers(2))))
+    return out
+
+
+@pytest.mark.parametrize("dtype,bsz,M,N,K,ta,tb", _batched_cases(48, seed=7))
+def test_batched_shape_every_entry(hip, oracle, dtype, bsz, M, N, K, ta, tb):
+    rng = np.random.default_rng(bsz * 1000 + M + N + K)
+    A32 = rng.standard_normal((bsz,) + ((K, M) if ta else (M, K))).astype(np.float32)
+    B32 = rng.standard_normal((bsz,) + ((N, K) if tb else (K, N))).astype(np.float32)
+    if dtype == "bf16":
+        A, B = oracle.to_bf16(A32), oracle.to_bf16(B32)
+        Au, Bu = oracle.bf16_to_f32(A).reshape(A.shape), oracle.bf16_to_f32(B).reshape(B.shape)
+    else:
+        A, B, Au, Bu = A32, B32, A32, B32
+    a, b = hip.from_numpy(A, dtype), hip.from_numpy(B, dtype)
+    got = hip.matmul_batched(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    again = hip.matmul_batched(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert got.shape == (bsz, M, N)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "repeat"
+    for i in range(bsz):
+        Ak = np.ascontiguousarray(Au[i].T if ta else Au[i])
+        Bk = np.ascontiguousarray(Bu[i] if tb else Bu[i].T)
+        ref = oracle.matmul(Ak, Bk, trans_b=True, threads=16)
+        if K == 1:
+            assert np.array_equal(got[i].view(np.uint32), ref.astype(np.float32).view(np.uint32))
+        else:
+            den = np.abs(Ak).astype(np.float64) @ np.abs(Bk).astype(np.float64).T
+            assert_gemm_close(got[i], ref, den, K, f"{dtype} batch {i}/{bsz} {M}x{N}x{K} ta={ta} tb={tb}")
