@@ -325,11 +325,10 @@ int split_count(int M, int N, int K) {
         // the slices must fill the CUs for the ping-pong kernel to take them
         if (tiles * S >= cus) return S;
     }
-    // 128 x 128 tiles that one round of the ping-pong kernel would leave
-    // under 77% full: slices of at least 1024 that fill a round of them, for
-    // that kernel (1024^2 x 4096: 66.7 against 77.2
-    // us as 64 x 64 tiles; 1024^2 x 8192 121.9 against 152.6; 512^2 x 16384
-    // 66.9 against 72.0 as 8 slices of 64 x 64 tiles)
+    // 128 x 128 tiles that one round of their ping-pong kernel would leave
+    // under 77% full: K slices for that kernel (1024^2 x 4096: 66.7 against
+    // 77.2 us as 64 x 64 tiles; 1024^2 x 8192 121.9 against 152.6; 512^2 x
+    // 16384 66.9 against 72.0 as 8 slices of 64 x 64 tiles)
     if (M % 128 == 0 && N % 128 == 0 && (double)(M / 128) * (N / 128) < 0.77 * cus) {
         const int64_t tiles = (int64_t)(M / 128) * (N / 128);
         // as many slices, at least 512 deep, as fit one round, if that round
