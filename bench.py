@@ -386,6 +386,34 @@ def gemm_bf16_batched_layouts(ca, layouts, steps):
     return out
 
 
+def gemm_shapes(ca, specs, steps):
+    """One product per spec "dtype:MxNxK:layout" (dtype f32 or bf16, layout
+    nn/nt/tn/tt for op(A) op(B)), timed with HIP events after a 0.3 s warm-up.
+    Reports TFLOP/s and the compulsory HBM bytes (A and B read once, f32 C
+    written once) as a fraction of peak.  For comparing kernels and for
+    kernel traces of one shape at a time."""
+    out = {}
+    for spec in specs:
+        dt, dims, lay = spec.split(":")
+        m, n, k = (int(x) for x in dims.split("x"))
+        ta, tb = lay[0] == "t", lay[1] == "t"
+        a = ca.fill_normal(ca.empty((k, m) if ta else (m, k)), seed=11)
+        b = ca.fill_normal(ca.empty((n, k) if tb else (k, n)), seed=12)
+        if dt == "bf16":
+            a, b = ca.to_bf16(a), ca.to_bf16(b)
+        elif dt != "f32":
+            raise ValueError(f"unknown dtype in {spec!r}")
+        c = ca.empty((m, n))
+        esz = 2 if dt == "bf16" else 4
+        hbm = (m * k + k * n) * esz + m * n * 4
+        _, ev = timed(ca, lambda: ca.matmul(a, b, trans_a=ta, trans_b=tb, out=c), steps, 3, 0.3)
+        out[spec] = {"kernel_ms": round(ev, 5), "TFLOP/s": round(2.0 * m * n * k / (ev * 1e-3) / 1e12, 2),
+                     "frac_hbm": round(hbm / (ev * 1e-3) / 1e9 / PEAK_HBM, 4)}
+        log(f"gemm {spec}: {ev * 1e3:.1f} us")
+        del a, b, c
+    return out
+
+
 COPY_ELEMS = 1 << 26  # 256 MiB of f32 read, 256 MiB written per launch
 
 
@@ -419,6 +447,8 @@ def main():
                     help="only time the bf16 8192^3 product in the comma-separated layouts (nn,nt,tn,tt)")
     ap.add_argument("--gemm-bf16-batched", metavar="LAYOUTS", default=None,
                     help="only time the batched bf16 64 x 512^3 product in the given layouts")
+    ap.add_argument("--gemm", metavar="SPECS", default=None,
+                    help="only time the comma-separated products dtype:MxNxK:layout (e.g. f32:2048x2048x2048:nn)")
     ap.add_argument("--host-boundary", action="store_true",
                     help="only time the _host entry points (host arrays across the C ABI, PCIe included)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -451,6 +481,10 @@ def main():
     if args.gemm_bf16_batched:
         print(json.dumps({"gemm_bf16_batched_64x512": gemm_bf16_batched_layouts(
             ca, args.gemm_bf16_batched.split(","), steps), "library": str(ca._lib.LIB_PATH)}), flush=True)
+        return
+    if args.gemm:
+        print(json.dumps({"gemm": gemm_shapes(ca, args.gemm.split(","), steps),
+                          "library": str(ca._lib.LIB_PATH)}), flush=True)
         return
     if args.host_boundary:
         print(json.dumps({"host_boundary": host_boundary(steps)}), flush=True)
