@@ -382,13 +382,13 @@ int32_t launch_layout(int ta, int tb, const float* a, const float* b, float* c, 
 }
 
 // One product (batch 1, C of pitch N; A and B of pitches lda and ldb, so that
-// a band of a larger product's rows keeps its operand pitches) as
-// split_count's K slices, when it asks for more than one and the slice
-// buffer can be had: *st is the outcome; false when not split.
-bool try_k_split(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb, int ta,
-                 int tb, int32_t* st) {
+// a band of a larger product's rows keeps its operand pitches) as S > 1 K
+// slices (K a multiple of 16 S) computed into the slice buffer and added in
+// order, when that buffer can be had: *st is the outcome; false when not
+// split.
+bool run_k_slices(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb, int ta,
+                  int tb, int S, int32_t* st) {
     if (((uintptr_t)c & 15) != 0) return false;
-    const int S = split_count(M, N, K);
     float* part = S > 1 ? (float*)ch::scratch_try(9, sizeof(float) * (size_t)S * M * N) : nullptr;
     if (!part) return false;
     const int kk = K / S;
@@ -398,23 +398,41 @@ bool try_k_split(const float* a, const float* b, float* c, int M, int N, int K, 
     return true;
 }
 
-// Rough time of an aligned product, in us, by the kernel the launchers pick:
-// rounds of 256 x 256 tiles (0.96 of peak per tile), rounds of 128 x 128
-// tiles on the ping-pong kernel (0.93) when the last is at least 77% full,
-// the tiled kernels (0.78 of that, as measured at 2176^3 - 3584^3), or, below
-// a round, K slices and small tiles (0.70).
-double est_us(int M, int N, int K) {
+// split_count's K slices, when it asks for more than one.
+bool try_k_split(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb, int ta,
+                 int tb, int32_t* st) {
+    return run_k_slices(a, b, c, M, N, K, lda, ldb, ta, tb, split_count(M, N, K), st);
+}
+
+// Rough time of `batch` aligned products launched together, in us, by the
+// kernel the launchers pick: rounds of 256 x 256 tiles (0.96 of peak per
+// tile), rounds of 128 x 128 tiles on the ping-pong kernel (0.93) when the
+// last is at least 77% full, the tiled kernels (0.78 of that, as measured at
+// 2176^3 - 3584^3), or, below a round, small tiles (0.70).
+double est_launch_us(int M, int N, int K, int batch) {
     const double cus = ch::num_cus() > 0 ? ch::num_cus() : 1, peak = 157.3e12;
-    const int64_t big = (int64_t)(M / 256) * (N / 256), t128 = (int64_t)(M / 128) * (N / 128);
+    const int64_t big = (int64_t)(M / 256) * (N / 256) * batch, t128 = (int64_t)(M / 128) * (N / 128) * batch;
     if (M % 256 == 0 && N % 256 == 0 && big >= cus)
         return std::ceil(big / cus) * cus * 2.0 * 256 * 256 * K / (peak * 0.96) * 1e6;
-    const double flops = 2.0 * M * N * K;
+    const double flops = 2.0 * M * N * K * batch;
     if (M % 128 == 0 && N % 128 == 0 && t128 >= 0.77 * cus) {
         const double rounds = std::ceil(t128 / cus);
         if (t128 >= 0.77 * rounds * cus) return rounds * cus * 2.0 * 128 * 128 * K / (peak * 0.93) * 1e6;
         return flops / (peak * 0.93 * 0.78) * 1e6;
     }
     return flops / (peak * 0.70) * 1e6;
+}
+
+// The slice sum's S + 1 passes over an M x N C at 6.5 TB/s, plus 4 us of
+// launches.
+double est_sum_us(int M, int N, int S) { return (S + 1) * 4.0 * M * N / 6.5e12 * 1e6 + 4.0; }
+
+// Rough time of one aligned product as launched: split_count's K slices
+// when it asks for them, else one launch.
+double est_us(int M, int N, int K) {
+    const int S = split_count(M, N, K);
+    if (S > 1) return est_launch_us(M, N, K / S, S) + est_sum_us(M, N, S);
+    return est_launch_us(M, N, K, 1);
 }
 
 int32_t product(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb, int ta,
@@ -424,42 +442,84 @@ int32_t product(const float* a, const float* b, float* c, int M, int N, int K, i
 // more than a round) end in a ragged round: the first M1 rows of C, the
 // whole rounds, run as one product and the remaining rows as another, which
 // takes its own kernel (K slices, 128 x 128 tiles, or a split of its own).
-// Chosen when est_us gives the two, plus 4 us for the extra launches, at
-// least 3% under the whole.  Measured (128 x 128 tiles; the rest as K slices
-// that fill one more round, added in order into their rows): 3072^3 409
-// against 451 us, 3584^3 644 against 826, 2304^3 184 against 207, 2176^3 157
-// against 196, 3072^2 x 1024 151 against 156.  Deterministic: each part's
-// kernels are chosen by its shape alone.  *st is the outcome; false when not
-// split.
-bool try_round_split(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb,
-                     int ta, int tb, int depth, int32_t* st) {
+// Returns M1 (0: no such split) and, in *us, est_us of the two parts plus
+// 4 us for the extra launches.  Measured (128 x 128 tiles; the rest as K
+// slices that fill one more round, added in order into their rows): 3072^3
+// 409 against 451 us, 3584^3 644 against 826, 2304^3 184 against 207, 2176^3
+// 157 against 196, 3072^2 x 1024 151 against 156.
+int round_split_rows(int M, int N, int K, double* us) {
     const int cus = ch::num_cus() > 0 ? ch::num_cus() : 1;
-    if (depth >= 3 || K % 16 || ((uintptr_t)a & 15) || ((uintptr_t)b & 15) || ((uintptr_t)c & 15)) return false;
+    if (K % 16) return 0;
     const int64_t big = (int64_t)(M / 256) * (N / 256), t128 = (int64_t)(M / 128) * (N / 128);
     int tile;
     int64_t T;
     if (M % 256 == 0 && N % 256 == 0 && big >= cus) tile = 256, T = big;
     else if (M % 128 == 0 && N % 128 == 0 && t128 > cus) tile = 128, T = t128;
-    else return false;
+    else return 0;
     const int tn = N / tile, tm = M / tile;
     const int t1 = (int)(T / cus * cus / tn);  // tile-rows of whole rounds
-    if (t1 <= 0 || t1 >= tm) return false;
-    const int M1 = t1 * tile, M2 = M - M1;
-    if (est_us(M1, N, K) + est_us(M2, N, K) + 4.0 >= 0.97 * est_us(M, N, K)) return false;
-    // A keeps its full pitch (its rows, or with ta its columns, are offset)
-    const float* a2 = ta ? a + M1 : a + (int64_t)M1 * lda;
-    *st = product(a, b, c, M1, N, K, lda, ldb, ta, tb, depth + 1);
-    if (*st == CLEAVE_HIP_OK) *st = product(a2, b, c + (int64_t)M1 * N, M2, N, K, lda, ldb, ta, tb, depth + 1);
-    return true;
+    if (t1 <= 0 || t1 >= tm) return 0;
+    const int M1 = t1 * tile;
+    *us = est_us(M1, N, K) + est_us(M - M1, N, K) + 4.0;
+    return M1;
 }
 
-// One product (batch 1, C of pitch N): K slices, a split at a ragged round,
-// or the launchers.
+// K slices of a product of more than a round of 128 x 128 tiles, S of them
+// (2-8, each at least 1024 deep, too few 256 x 256 tiles for that kernel to
+// take them) so that the slices' tiles fill at least 90% of their last
+// round: est_launch_us of the slices (rounds of the 128 x 128 ping-pong
+// kernel) plus the slice sum.  Returns the cheapest S (0: none) and its time
+// in *us.
+int round_slices(int M, int N, int K, double* us) {
+    const int cus = ch::num_cus() > 0 ? ch::num_cus() : 1;
+    if (M % 128 || N % 128) return 0;
+    const int64_t t = (int64_t)(M / 128) * (N / 128);
+    const int64_t big = (M % 256 == 0 && N % 256 == 0) ? (int64_t)(M / 256) * (N / 256) : 0;
+    if (t <= cus) return 0;
+    int best = 0;
+    for (int S = 2; S <= 8; ++S) {
+        if (K % (16 * S) || K / S < 1024 || big * S >= cus) continue;
+        const double rounds = std::ceil((double)(t * S) / cus);
+        if ((double)(t * S) < 0.9 * rounds * cus) continue;
+        const double u = est_launch_us(M, N, K / S, S) + est_sum_us(M, N, S);
+        if (!best || u < *us) best = S, *us = u;
+    }
+    return best;
+}
+
+// One product (batch 1, C of pitch N; A and B of pitches lda and ldb, so that
+// a band of a larger product's rows keeps its operand pitches): K slices
+// for few tiles; at a ragged round, a band of rows or K slices that fill
+// whole rounds, where the estimate is at least 3% under the whole's, and
+// the slices only 8% under the band's (the estimate prices the band's tiled
+// kernels low where all their tiles are resident at once: 1024 x 5632 x 2048
+// ran 185 us as a band, 189 as slices).  Measured: 2048 x
+// 3072 x 4032 (384 tiles) as 2 slices in 3 full rounds 352 us against 411 as
+// a band of 768 rows; 896 x 5632 x 4096 (308) as 4 slices in 5 rounds 310
+// against 330; 1536 x 4096^2 (384) stays a band of 512 rows, 351 against 358
+// as slices; else the launchers.  Deterministic: the kernels are chosen by
+// the shape alone, and slices are added in order.
 int32_t product(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb, int ta,
                 int tb, int depth) {
     int32_t st = CLEAVE_HIP_OK;
     if (try_k_split(a, b, c, M, N, K, lda, ldb, ta, tb, &st)) return st;
-    if (try_round_split(a, b, c, M, N, K, lda, ldb, ta, tb, depth, &st)) return st;
+    const bool aligned = ((uintptr_t)a & 15) == 0 && ((uintptr_t)b & 15) == 0 && ((uintptr_t)c & 15) == 0;
+    if (depth < 3 && aligned) {
+        const double whole = est_us(M, N, K);
+        double us_rows = 0, us_sl = 0;
+        const int M1 = round_split_rows(M, N, K, &us_rows);
+        const int S = round_slices(M, N, K, &us_sl);
+        if (S && us_sl < 0.97 * whole && (!M1 || us_sl < 0.92 * us_rows) &&
+            run_k_slices(a, b, c, M, N, K, lda, ldb, ta, tb, S, &st))
+            return st;
+        if (M1 && us_rows < 0.97 * whole) {
+            // A keeps its full pitch (its rows, or with ta its columns, are offset)
+            const float* a2 = ta ? a + M1 : a + (int64_t)M1 * lda;
+            st = product(a, b, c, M1, N, K, lda, ldb, ta, tb, depth + 1);
+            if (st == CLEAVE_HIP_OK) st = product(a2, b, c + (int64_t)M1 * N, M - M1, N, K, lda, ldb, ta, tb, depth + 1);
+            return st;
+        }
+    }
     return launch_layout(ta, tb, a, b, c, M, N, K, lda, ldb, N, 1, (int64_t)M * K, (int64_t)K * N,
                          (int64_t)M * N);
 }

@@ -709,6 +709,28 @@ def test_f32_ragged_round_split_every_entry(hip, oracle, M, N, K, ta, tb):
     assert_gemm_close(got, ref, den, K, f"round split {M}x{N}x{K} ta={ta} tb={tb}")
 
 
+@pytest.mark.parametrize("M,N,K,ta,tb", [
+    # 384 tiles of 128 x 128 (a round and a half): two K slices of 1024 fill
+    # three whole rounds on the ping-pong kernel, added in order
+    *[(2048, 3072, 2048, ta, tb) for ta in (0, 1) for tb in (0, 1)],
+    # the same on zero-padded copies (2048 x 3072 x 2048)
+    (2000, 3000, 2040, 0, 0),
+])
+def test_f32_k_slices_at_ragged_round_every_entry(hip, oracle, M, N, K, ta, tb):
+    # Every entry against the loop (A.B^T form on transposed copies), and
+    # bitwise the same on a second call.
+    A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=41 + 2 * ta + tb)
+    a, b = hip.from_numpy(A), hip.from_numpy(B)
+    got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    again = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    Ak = np.ascontiguousarray(Au.T if ta else Au)
+    Bk = np.ascontiguousarray(Bu if tb else Bu.T)
+    ref = oracle.matmul(Ak, Bk, trans_b=True, threads=16)
+    den = np.abs(Ak).astype(np.float64) @ np.abs(Bk).astype(np.float64).T
+    assert_gemm_close(got, ref, den, K, f"K slices {M}x{N}x{K} ta={ta} tb={tb}")
+
+
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_bf16_ragged_round_split_every_entry(hip, oracle, ta, tb):
     # 272 tiles of 256 x 256: rows 0-4095 a round of them, rows 4096-4351 a
