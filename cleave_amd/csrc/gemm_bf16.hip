@@ -386,8 +386,8 @@ bool try_k_split(const uint16_t* a, const uint16_t* b, float* c, int M, int N, i
 
 // Products of at least this many flops (2 M N K per product) that no aligned
 // kernel takes run on zero-padded copies (gemm_pad.hpp); smaller ones run
-// the general kernel, one launch against the padded route's four (~12 us
-// together).  Measured crossing: ~115^3 (100^3 11.1 us general, 12.1 padded;
+// the general kernel, one launch against the padded route's three (~10 us
+// together; measured when it was four).  Measured crossing: ~115^3 (100^3 11.1 us general, 12.1 padded;
 // 127 x 129 x 131 14.1 against 12.0).
 constexpr double kPadMinFlops = 1u << 22;
 // 256 x 256 tiles (8192^3) 0.55 of peak, also from half a round of them;

@@ -586,8 +586,8 @@ bool launch_fast(const float* a, const float* b, float* c, int M, int N, int K, 
 
 // Products of at least this many flops (2 M N K per product) that no aligned
 // kernel takes run on zero-padded copies (gemm_pad.hpp); smaller ones run
-// the general kernel, one launch against the padded route's four (~12 us
-// together).  Measured crossing: ~80^3 (64 x 64 x 63 10.2 us general, 12.4
+// the general kernel, one launch against the padded route's three (~10 us
+// together; measured when it was four).  Measured crossing: ~80^3 (64 x 64 x 63 10.2 us general, 12.4
 // padded; 100^3 15.9 against 12.5).
 constexpr double kPadMinFlops = 1u << 20;
 // Skinny products (gemv.hip) from the same size: 3 x 5 x 7 took 7.2 us there

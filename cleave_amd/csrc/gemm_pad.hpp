@@ -82,36 +82,54 @@ inline PadPlan pad_plan(int M, int N, int K, int batch, bool ta, bool tb, const 
     return p;
 }
 
-// dst (batch matrices of rows_p x cols_p, row pitch cols_p) = src (batch
-// matrices of rows x cols, row pitch cols), zeros past row `rows` and
-// column `cols`.  One workgroup per destination row (grid-strided), each
-// thread 8 consecutive elements; cols_p % 8 == 0 and dst 16-byte aligned.
-// vec_src: src rows are 16-byte aligned, so whole chunks load as vectors.
+// One padded copy: dst (batch matrices of rows_p x cols_p, row pitch cols_p)
+// = src (batch matrices of rows x cols, row pitch cols), zeros past row
+// `rows` and column `cols`; total_rows = batch * rows_p (0: nothing to copy).
+// cols_p % 8 == 0 and dst 16-byte aligned.  vec_src: src rows are 16-byte
+// aligned, so whole chunks load as vectors.
 template <typename T>
-__global__ __launch_bounds__(256) void pad_copy_kernel(const T* __restrict__ src, T* __restrict__ dst, int rows,
-                                                       int cols, int rows_p, int cols_p, int64_t total_rows,
-                                                       bool vec_src) {
+struct PadCopy {
+    const T* src;
+    T* dst;
+    int rows, cols, rows_p, cols_p;
+    int64_t total_rows;
+    bool vec_src;
+};
+
+// Destination row rr of one padded copy, each thread 8 consecutive elements.
+template <typename T>
+__device__ __forceinline__ void pad_copy_row(const PadCopy<T>& j, int64_t rr) {
     typedef T v8 __attribute__((ext_vector_type(8), aligned(16)));  // 16-byte alignment is all that is checked
-    for (int64_t rr = blockIdx.x; rr < total_rows; rr += gridDim.x) {
-        const int64_t bt = rr / rows_p;
-        const int r = (int)(rr - bt * rows_p);
-        const T* s = src + (bt * rows + r) * (int64_t)cols;
-        T* d = dst + rr * (int64_t)cols_p;
-        for (int c0 = threadIdx.x * 8; c0 < cols_p; c0 += 256 * 8) {
-            v8 v;
-            if (r < rows && c0 + 8 <= cols) {
-                if (vec_src) {
-                    v = *reinterpret_cast<const v8*>(s + c0);
-                } else {
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) v[t] = s[c0 + t];
-                }
+    const int64_t bt = rr / j.rows_p;
+    const int r = (int)(rr - bt * j.rows_p);
+    const T* s = j.src + (bt * j.rows + r) * (int64_t)j.cols;
+    T* d = j.dst + rr * (int64_t)j.cols_p;
+    for (int c0 = threadIdx.x * 8; c0 < j.cols_p; c0 += 256 * 8) {
+        v8 v;
+        if (r < j.rows && c0 + 8 <= j.cols) {
+            if (j.vec_src) {
+                v = *reinterpret_cast<const v8*>(s + c0);
             } else {
 #pragma unroll
-                for (int t = 0; t < 8; ++t) v[t] = (r < rows && c0 + t < cols) ? s[c0 + t] : (T)0;
+                for (int t = 0; t < 8; ++t) v[t] = s[c0 + t];
             }
-            *reinterpret_cast<v8*>(d + c0) = v;
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) v[t] = (r < j.rows && c0 + t < j.cols) ? s[c0 + t] : (T)0;
         }
+        *reinterpret_cast<v8*>(d + c0) = v;
+    }
+}
+
+// Both operands' padded copies in one launch: destination rows 0 ..
+// a.total_rows - 1 are a's, the next b.total_rows are b's.  One workgroup
+// per destination row, grid-strided.
+template <typename T>
+__global__ __launch_bounds__(256) void pad_copy_kernel(PadCopy<T> a, PadCopy<T> b) {
+    const int64_t total = a.total_rows + b.total_rows;
+    for (int64_t rr = blockIdx.x; rr < total; rr += gridDim.x) {
+        if (rr < a.total_rows) pad_copy_row(a, rr);
+        else pad_copy_row(b, rr - a.total_rows);
     }
 }
 
@@ -162,26 +180,29 @@ bool run_padded(const PadPlan& p, const T* a, const T* b, float* c, int batch, b
     const T* pa = a;
     const T* pb = b;
     float* pc = c;
+    PadCopy<T> ja{}, jb{};
     if (p.copy_a) {
         T* d = (T*)base;
         const int rows = ta ? p.K : p.M, cols = ta ? p.M : p.K;
         const int rows_p = ta ? p.Kp : p.Mp, cols_p = ta ? p.Mp : p.Kp;
-        const int64_t tr = (int64_t)batch * rows_p;
         const bool vec = ((uintptr_t)a & 15) == 0 && ((int64_t)cols * sizeof(T)) % 16 == 0;
-        pad_copy_kernel<T><<<pad_grid(tr, cus), 256, 0, stream()>>>(a, d, rows, cols, rows_p, cols_p, tr, vec);
+        ja = PadCopy<T>{a, d, rows, cols, rows_p, cols_p, (int64_t)batch * rows_p, vec};
         pa = d;
     }
     if (p.copy_b) {
         T* d = (T*)(base + p.bytes_a);
         const int rows = tb ? p.N : p.K, cols = tb ? p.K : p.N;
         const int rows_p = tb ? p.Np : p.Kp, cols_p = tb ? p.Kp : p.Np;
-        const int64_t tr = (int64_t)batch * rows_p;
         const bool vec = ((uintptr_t)b & 15) == 0 && ((int64_t)cols * sizeof(T)) % 16 == 0;
-        pad_copy_kernel<T><<<pad_grid(tr, cus), 256, 0, stream()>>>(b, d, rows, cols, rows_p, cols_p, tr, vec);
+        jb = PadCopy<T>{b, d, rows, cols, rows_p, cols_p, (int64_t)batch * rows_p, vec};
         pb = d;
     }
+    int32_t st = CLEAVE_HIP_OK;
+    if (ja.total_rows + jb.total_rows > 0) {
+        pad_copy_kernel<T><<<pad_grid(ja.total_rows + jb.total_rows, cus), 256, 0, stream()>>>(ja, jb);
+        st = check_hip(hipGetLastError(), "pad_copy_kernel");
+    }
     if (p.crop_c) pc = (float*)(base + p.bytes_a + p.bytes_b);
-    int32_t st = check_hip(hipGetLastError(), "pad_copy_kernel");
     if (st == CLEAVE_HIP_OK) st = gemm(pa, pb, pc, p.Mp, p.Np, p.Kp);
     if (st == CLEAVE_HIP_OK && p.crop_c) {
         const int64_t tr = (int64_t)batch * p.M;
