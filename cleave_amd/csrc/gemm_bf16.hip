@@ -320,6 +320,16 @@ bool launch_fast(const uint16_t* a, const uint16_t* b, float* c, int M, int N, i
     // 45.9 us; 2048^3, 64 tiles: 39.6 against 26.1 us).
     const int cus = ch::num_cus();
     const int64_t big_tiles = (int64_t)(M / 256) * (N / 256) * batch;
+    // A short K over more than a round of tiles: the products are bound by
+    // their f32 C stores, which two workgroups per CU on 128 x 128 tiles
+    // overlap with each other's loads and math.  Against the 256 x 256
+    // kernels, one box, same run: 16384^2 x 256 314 against 355 us (A·Bᵀ 315
+    // against 398), 10240^2 x 256 103 against 129, 6144^2 x 256 38 against 47,
+    // 65536 x 1024 x 256 78 against 85, 8192^2 x 128 Aᵀ·B 51 against 60; but
+    // 8192^2 x 256 71-77 against 69-72 (four rounds exactly).
+    if (K <= 256 && K % 64 == 0 && big_tiles > cus &&
+        launch_tiled<128, 128, 64, 2, 2, 2, 32, TA, TB>(a, b, c, M, N, K, batch, s, st))
+        return true;
     if (big_tiles * 2 >= cus) {
         const bool short_single_round = big_tiles <= cus && K <= 512;
         if (!short_single_round && launch_pairs<TA, TB>(a, b, c, M, N, K, batch, s, st)) return true;

@@ -378,15 +378,16 @@ def test_f32_batched_through_pingpong(hip, oracle):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-@pytest.mark.parametrize("M,N,K", [(4096, 8192, 128), (3840, 5120, 128)])
+@pytest.mark.parametrize("M,N,K", [(4096, 8192, 320), (3840, 5120, 320), (4096, 8192, 128), (3840, 5120, 128)])
 def test_bf16_pingpong_every_entry(hip, oracle, M, N, K, ta, tb):
     # Two rounds of 256 x 256 tiles (512, or 300: 44 workgroups of 256 take a
-    # second tile) go to a ping-pong kernel (the paired-copy one, which keeps
-    # one workgroup per CU looping over its tiles, for A·B, A·Bᵀ and Aᵀ·Bᵀ).
-    # Its epilogue swaps 16-lane rows between accumulator blocks to store
-    # whole 128-byte rows; every entry of C is checked, since a value stored
-    # in the wrong column of its row would keep the row sums the sampled
-    # tests also check.
+    # second tile) with K = 320 go to a ping-pong kernel (the paired-copy one,
+    # which keeps one workgroup per CU looping over its tiles, for A·B, A·Bᵀ
+    # and Aᵀ·Bᵀ).  Its epilogue swaps 16-lane rows between accumulator blocks
+    # to store whole 128-byte rows; every entry of C is checked, since a value
+    # stored in the wrong column of its row would keep the row sums the
+    # sampled tests also check.  With K = 128 the same shapes go to 128 x 128
+    # tiles, two workgroups per CU (a short K over several rounds).
     rng = np.random.default_rng(40 + 2 * ta + tb + M)
     A = oracle.to_bf16(rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32))
     B = oracle.to_bf16(rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32))
@@ -403,13 +404,15 @@ def test_bf16_pingpong_every_entry(hip, oracle, M, N, K, ta, tb):
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("K", [32, 64, 128, 160, 192, 352, 384, 832])
 def test_bf16_pingpong_ring_depths(hip, oracle, K, ta, tb):
-    # 4096 x 8192 outputs are two rounds of 256 x 256 tiles, which the
-    # dispatch gives to a ping-pong kernel.  With K a multiple of 64, A·B and
-    # Aᵀ·Bᵀ take the kernel that copies the k-contiguous operand in pairs of
-    # k-tiles (a ring of 3 pairs beside a ring of 4 single k-tiles): K = 64,
-    # 128, 192, 384, 832 are 1, 2, 3, 6 and 13 pairs (never filled, filled,
-    # wrapping).  The other K, and the other layouts, take the kernel with a
-    # ring of five single k-tiles: 1, 5 and 11 k-tiles for K = 32, 160, 352.
+    # 4096 x 8192 outputs are two rounds of 256 x 256 tiles.  From K = 320
+    # the dispatch gives them to a ping-pong kernel: with K a multiple of 64,
+    # A·B and Aᵀ·Bᵀ take the kernel that copies the k-contiguous operand in
+    # pairs of k-tiles (a ring of 3 pairs beside a ring of 4 single k-tiles):
+    # K = 384 and 832 are 6 and 13 pairs (filled, wrapping).  The other K, and
+    # the other layouts, take the kernel with a ring of five single k-tiles:
+    # 1, 5 and 11 k-tiles for K = 32, 160, 352.  K = 64, 128 and 192 (a short
+    # K over several rounds) go to 128 x 128 tiles, two workgroups per CU,
+    # with 1 - 3 k-tiles of 64.
     M, N = 4096, 8192
     a = hip.to_bf16(hip.fill_normal(hip.empty((K, M) if ta else (M, K)), seed=101 + K + 2 * ta + tb, std=0.02))
     b = hip.to_bf16(hip.fill_normal(hip.empty((N, K) if tb else (K, N)), seed=111 + K + 2 * ta + tb, std=0.02))
