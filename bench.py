@@ -387,27 +387,31 @@ def gemm_bf16_batched_layouts(ca, layouts, steps):
 
 
 def gemm_shapes(ca, specs, steps):
-    """One product per spec "dtype:MxNxK:layout" (dtype f32 or bf16, layout
-    nn/nt/tn/tt for op(A) op(B)), timed with HIP events after a 0.3 s warm-up.
-    Reports TFLOP/s and the compulsory HBM bytes (A and B read once, f32 C
-    written once) as a fraction of peak.  For comparing kernels and for
-    kernel traces of one shape at a time."""
+    """One product per spec "dtype:MxNxK:layout", or a batch of them as
+    "dtype:BxMxNxK:layout" (dtype f32 or bf16, layout nn/nt/tn/tt for op(A)
+    op(B)), timed with HIP events after a 0.3 s warm-up.  Reports TFLOP/s and
+    the compulsory HBM bytes (A and B read once, f32 C written once) as a
+    fraction of peak.  For comparing kernels and for kernel traces of one
+    shape at a time."""
     out = {}
     for spec in specs:
         dt, dims, lay = spec.split(":")
-        m, n, k = (int(x) for x in dims.split("x"))
+        d = [int(x) for x in dims.split("x")]
+        bs, (m, n, k) = (d[0], d[1:]) if len(d) == 4 else (1, d)
+        lead = (bs,) if len(d) == 4 else ()
         ta, tb = lay[0] == "t", lay[1] == "t"
-        a = ca.fill_normal(ca.empty((k, m) if ta else (m, k)), seed=11)
-        b = ca.fill_normal(ca.empty((n, k) if tb else (k, n)), seed=12)
+        a = ca.fill_normal(ca.empty(lead + ((k, m) if ta else (m, k))), seed=11)
+        b = ca.fill_normal(ca.empty(lead + ((n, k) if tb else (k, n))), seed=12)
         if dt == "bf16":
             a, b = ca.to_bf16(a), ca.to_bf16(b)
         elif dt != "f32":
             raise ValueError(f"unknown dtype in {spec!r}")
-        c = ca.empty((m, n))
+        c = ca.empty(lead + (m, n))
         esz = 2 if dt == "bf16" else 4
-        hbm = (m * k + k * n) * esz + m * n * 4
-        _, ev = timed(ca, lambda: ca.matmul(a, b, trans_a=ta, trans_b=tb, out=c), steps, 3, 0.3)
-        out[spec] = {"kernel_ms": round(ev, 5), "TFLOP/s": round(2.0 * m * n * k / (ev * 1e-3) / 1e12, 2),
+        hbm = bs * ((m * k + k * n) * esz + m * n * 4)
+        mm = ca.matmul_batched if lead else ca.matmul
+        _, ev = timed(ca, lambda: mm(a, b, trans_a=ta, trans_b=tb, out=c), steps, 3, 0.3)
+        out[spec] = {"kernel_ms": round(ev, 5), "TFLOP/s": round(2.0 * bs * m * n * k / (ev * 1e-3) / 1e12, 2),
                      "frac_hbm": round(hbm / (ev * 1e-3) / 1e9 / PEAK_HBM, 4)}
         log(f"gemm {spec}: {ev * 1e3:.1f} us")
         del a, b, c
@@ -448,7 +452,8 @@ def main():
     ap.add_argument("--gemm-bf16-batched", metavar="LAYOUTS", default=None,
                     help="only time the batched bf16 64 x 512^3 product in the given layouts")
     ap.add_argument("--gemm", metavar="SPECS", default=None,
-                    help="only time the comma-separated products dtype:MxNxK:layout (e.g. f32:2048x2048x2048:nn)")
+                    help="only time the comma-separated products dtype:MxNxK:layout or batches dtype:BxMxNxK:layout "
+                         "(e.g. f32:2048x2048x2048:nn)")
     ap.add_argument("--host-boundary", action="store_true",
                     help="only time the _host entry points (host arrays across the C ABI, PCIe included)")
     ap.add_argument("--calibrate-copy", action="store_true",

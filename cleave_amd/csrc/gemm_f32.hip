@@ -273,10 +273,13 @@ bool launch_small(const float* a, const float* b, float* c, int M, int N, int K,
 }
 
 // Ping-pong kernel (gemm_f32_pingpong.hpp) when the shape divides its
-// TILE x TILE x 16 tile; false when it does not.
+// TILE x TILE x 16 tile; false when it does not.  kslices > 1: the batch is
+// that many K slices of each of batch / kslices products (the kernel's
+// kslices form).
 template <bool TA, bool TB, int TILE = 256>
 bool launch_pingpong(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
-                     int64_t ldb, int batch, int64_t sA, int64_t sB, int64_t sC, int32_t* status) {
+                     int64_t ldb, int batch, int64_t sA, int64_t sB, int64_t sC, int32_t* status,
+                     int kslices = 1) {
     using P = ch::F32PingPong<!TA, TB, 0, TILE>;
     if (!P::fits(M, N, K, lda, ldb) || ((uintptr_t)a & 15) || ((uintptr_t)b & 15) || (sA % 4) || (sB % 4))
         return false;
@@ -284,7 +287,7 @@ bool launch_pingpong(const float* a, const float* b, float* c, int M, int N, int
     if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
     dim3 grid((unsigned)(tiles_m * tiles_n * batch));
     ch::gemm_f32_pingpong_kernel<!TA, TB, 0, TILE><<<grid, P::THREADS, 0, ch::stream()>>>(
-        a, b, c, M, N, K, lda, ldb, sA, sB, sC, tiles_m, tiles_n, batch, ch::MlpFuse{});
+        a, b, c, M, N, K, lda, ldb, sA, sB, sC, tiles_m, tiles_n, batch, kslices, ch::MlpFuse{});
     *status = ch::check_hip(hipGetLastError(), "gemm_f32_pingpong_kernel");
     return true;
 }
@@ -625,6 +628,35 @@ int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, in
     return launch_general<TA, TB>(a, b, c, M, N, K, lda, ldb, ldc, batch, sA, sB, sC);
 }
 
+// A batch of packed products with fewer 128 x 128 tiles than 77% of a round
+// and a long K: S K slices of each product, at least 512 deep, whose tiles
+// fill one round at least 77%, in one launch of the 128 x 128 ping-pong
+// kernel, then added in order (deterministic).  *st is the outcome; false
+// when not split.
+template <bool TA, bool TB>
+bool try_batched_k_slices(const float* a, const float* b, float* c, int M, int N, int K, int batch, int32_t* st) {
+    const int cus = ch::num_cus() > 0 ? ch::num_cus() : 1;
+    if (M % 128 || N % 128 || ((uintptr_t)c & 15)) return false;
+    const int64_t t = (int64_t)(M / 128) * (N / 128) * batch;
+    if (t >= 0.77 * cus) return false;
+    int S = 0;
+    for (int s = (int)(cus / t); s >= 2; --s)
+        if (K % (16 * s) == 0 && K / s >= 512) {
+            if (t * s >= 0.77 * cus) S = s;
+            break;
+        }
+    if (S == 0 || (int64_t)batch * S > 0x7FFFFFFF) return false;
+    const int64_t n = (int64_t)batch * M * N;
+    float* part = (float*)ch::scratch_try(9, sizeof(float) * (size_t)S * n);
+    if (!part) return false;
+    const int64_t lda = TA ? M : K, ldb = TB ? K : N;
+    if (!launch_pingpong<TA, TB, 128>(a, b, part, M, N, K / S, lda, ldb, batch * S, (int64_t)M * K,
+                                      (int64_t)K * N, (int64_t)M * N, st, S))
+        return false;
+    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, n, S);
+    return true;
+}
+
 // batch >= 1 independent products packed back to back, or (splits > 1, batch
 // must be 1) one product whose K range is cut into `splits` equal slices,
 // slice s writing its partial sum to c + s*M*N.
@@ -634,6 +666,15 @@ int32_t dispatch(const float* a, const float* b, float* c, int M, int N, int K, 
     if (splits <= 1 && (M == 1 || N == 1 || K == 1)) return ch::matmul_vector_f32(a, b, c, M, N, K, batch, ta, tb);
     const int64_t lda = ta ? M : K, ldb = tb ? K : N, ldc = N;
     if (splits <= 1 && batch == 1) return product(a, b, c, M, N, K, lda, ldb, ta, tb, 0);
+    if (splits <= 1) {
+        int32_t st = CLEAVE_HIP_OK;
+        bool done;
+        if (!ta && !tb) done = try_batched_k_slices<false, false>(a, b, c, M, N, K, batch, &st);
+        else if (!ta && tb) done = try_batched_k_slices<false, true>(a, b, c, M, N, K, batch, &st);
+        else if (ta && !tb) done = try_batched_k_slices<true, false>(a, b, c, M, N, K, batch, &st);
+        else done = try_batched_k_slices<true, true>(a, b, c, M, N, K, batch, &st);
+        if (done) return st;
+    }
     int64_t sA = (int64_t)M * K, sB = (int64_t)K * N, sC = (int64_t)M * N;
     int kk = K;
     if (splits > 1) {

@@ -198,11 +198,16 @@ struct Direct {
 
 }  // namespace f32pp
 
+// `batch` products of M x N x K, product z at A + z strideA, B + z strideB,
+// C + z strideC.  With kslices > 1 (batch a multiple of it) the products are
+// the K slices of batch / kslices products of depth K * kslices: z = s nb + b
+// (nb = batch / kslices) is slice s of product b, at A + b strideA plus s K
+// columns (k-contiguous A) or s K rows of A (likewise B), and C + z strideC.
 template <bool AKC, bool BKC, int MODE = 0, int TILE = 256>
 __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
     int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC, int tiles_m, int tiles_n,
-    int batch, MlpFuse fuse) {
+    int batch, int kslices, MlpFuse fuse) {
     using namespace ch::tiles;
     using namespace ch::f32pp;
     using P = F32PingPong<AKC, BKC, MODE, TILE>;
@@ -217,8 +222,14 @@ __global__ __launch_bounds__(512) void gemm_f32_pingpong_kernel(
     int bt, tm, tn;
     ch::block_coords(blockIdx.x, tiles_m, tiles_n, batch, bt, tm, tn);
     const int m0 = tm * P::BM, n0 = tn * P::BN;
-    A += (int64_t)bt * strideA;
-    B += (int64_t)bt * strideB;
+    if (kslices > 1) {
+        const int nb = batch / kslices, sl = bt / nb, pb = bt - sl * nb;
+        A += (int64_t)pb * strideA + (AKC ? (int64_t)sl * K : (int64_t)sl * K * lda);
+        B += (int64_t)pb * strideB + (BKC ? (int64_t)sl * K : (int64_t)sl * K * ldb);
+    } else {
+        A += (int64_t)bt * strideA;
+        B += (int64_t)bt * strideB;
+    }
     C += (int64_t)bt * strideC;
     const uint32_t lds0 = lds_addr(smem);
     const int nk = K / BK;

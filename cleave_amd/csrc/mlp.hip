@@ -279,7 +279,7 @@ int32_t fused_step(const float* x, const float* y, float* w1, float* w2, float* 
     f1.zpart = zpart;
     ch::gemm_f32_pingpong_kernel<true, false, 1>
         <<<dim3((unsigned)((B / 256) * (Hd / 256))), FusedTile1::THREADS, 0, st>>>(
-            x, w1, H, B, Hd, D, D, Hd, 0, 0, 0, B / 256, Hd / 256, 1, f1);
+            x, w1, H, B, Hd, D, D, Hd, 0, 0, 0, B / 256, Hd / 256, 1, 1, f1);
     CH_LAUNCHED("gemm_f32_pingpong_kernel(MODE 1)");
     row_finish_kernel<<<row_blocks, kThreads, 0, st>>>(zpart, P, y, B, sq, d2);
     CH_LAUNCHED("row_finish_kernel");
@@ -293,7 +293,7 @@ int32_t fused_step(const float* x, const float* y, float* w1, float* w2, float* 
     ch::gemm_f32_pingpong_kernel<false, false, 2>
         <<<dim3((unsigned)((D / 256) * (Hd / 256) * splits)), FusedTile2::THREADS, 0, st>>>(
             x, H, slices, D, Hd, kk, D, Hd, (int64_t)kk * D, (int64_t)kk * Hd, (int64_t)D * Hd, D / 256,
-            Hd / 256, splits, f2);
+            Hd / 256, splits, 1, f2);
     CH_LAUNCHED("gemm_f32_pingpong_kernel(MODE 2)");
     dw1_finish_kernel<<<dim3((unsigned)((Hd + kThreads - 1) / kThreads), (unsigned)(D < 1024 ? D : 1024)),
                         kThreads, 0, st>>>(slices, splits, D, Hd, w2, dw1, w1, lr);

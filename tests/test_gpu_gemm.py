@@ -647,6 +647,32 @@ def test_f32_batched_products_on_the_128_tile_ping_pong(hip, oracle, ta, tb):
         assert_gemm_close(got[i], ref, den, K, f"batched 128-tile ping-pong product {i}")
 
 
+@pytest.mark.parametrize("bsz,M,N,K,ta,tb", [
+    # 64 tiles of 128 x 128 over the batch: 4 K slices of 512 (a round of 256
+    # tiles on the 128 x 128 ping-pong kernel, each slice at its product's
+    # k-offset), added in order
+    *[(16, 256, 256, 2048, ta, tb) for ta in (0, 1) for tb in (0, 1)],
+    # 64 products of one tile: 4 slices of 1024
+    (64, 128, 128, 4096, 0, 0),
+    # 48 tiles: 5 slices of 768 (240 tiles)
+    (3, 512, 512, 3840, 1, 0),
+])
+def test_f32_batched_k_slices_every_entry(hip, oracle, bsz, M, N, K, ta, tb):
+    # Every entry of every product against the loop, and bitwise the same on
+    # a second call.
+    A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=97 + 2 * ta + tb, batch=bsz)
+    a, b = hip.from_numpy(A), hip.from_numpy(B)
+    got = hip.matmul_batched(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    again = hip.matmul_batched(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    for i in range(bsz):
+        Ak = np.ascontiguousarray(Au[i].T if ta else Au[i])
+        Bk = np.ascontiguousarray(Bu[i] if tb else Bu[i].T)
+        ref = oracle.matmul(Ak, Bk, trans_b=True, threads=16)
+        den = np.abs(Ak).astype(np.float64) @ np.abs(Bk).astype(np.float64).T
+        assert_gemm_close(got[i], ref, den, K, f"batched K slices {i}/{bsz} {M}x{N}x{K} ta={ta} tb={tb}")
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_many_tiny_products_stay_on_the_general_kernel(hip, oracle, dtype):
     # 2048 products of 16 x 24 x 20: above the padded route's size threshold
