@@ -233,7 +233,7 @@ int32_t launch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int
 // Returns false when the shape or alignment does not fit.
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int MI, bool TA, bool TB>
 bool launch_tiled(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch, const Strides& s,
-                  int32_t* status) {
+                  int32_t* status, int kslices = 1) {
     using P = ch::Bf16Tiled<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI>;
     const int64_t lda = s.lda, ldb = s.ldb;
     if (!P::fits(M, N, K, lda, ldb) || !bases_aligned(a, b, s)) return false;
@@ -241,7 +241,7 @@ bool launch_tiled(const uint16_t* a, const uint16_t* b, float* c, int M, int N, 
     if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
     dim3 grid((unsigned)(tiles_m * tiles_n * batch));
     ch::gemm_bf16_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI><<<grid, P::THREADS, 0, ch::stream()>>>(
-        a, b, c, M, N, K, lda, ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch);
+        a, b, c, M, N, K, lda, ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch, kslices);
     *status = ch::check_hip(hipGetLastError(), "gemm_bf16_tiled_kernel");
     return true;
 }
@@ -482,6 +482,35 @@ int32_t product(const uint16_t* a, const uint16_t* b, float* c, int M, int N, in
     return launch<TA, TB>(a, b, c, M, N, K, 1, s);
 }
 
+// A batch of packed products with at most half a round of 128 x 128 tiles,
+// over all its products, and a long K: S K slices of each product, at least
+// 1024 deep, whose tiles fill at least half a round, in one launch of the
+// 128 x 128 tiled kernel (its kslices form), then added in order
+// (deterministic).  *st is the outcome; false when not split.
+template <bool TA, bool TB>
+bool try_batched_k_slices(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
+                          int32_t* st) {
+    const int cus = ch::num_cus() > 0 ? ch::num_cus() : 1;
+    if (M % 128 || N % 128 || ((uintptr_t)c & 15)) return false;
+    const int64_t t = (int64_t)(M / 128) * (N / 128) * batch;
+    if (t * 2 > cus) return false;
+    int S = 0;
+    for (int s = (int)(cus / t); s >= 2; --s)
+        if (K % (64 * s) == 0 && K / s >= 1024) {
+            if (t * s * 2 >= cus) S = s;
+            break;
+        }
+    if (S == 0) return false;
+    const int64_t n = (int64_t)batch * M * N;
+    float* part = (float*)ch::scratch_try(10, sizeof(float) * (size_t)S * n);
+    if (!part) return false;
+    if (!launch_tiled<128, 128, 64, 2, 2, 3, 32, TA, TB>(a, b, part, M, N, K / S, batch * S, packed<TA, TB>(M, N, K),
+                                                         st, S))
+        return false;
+    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, n, S);
+    return true;
+}
+
 int32_t dispatch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
                  int ta, int tb) {
     // a dimension of 1: matrix-vector or outer products (gemv.hip)
@@ -492,6 +521,13 @@ int32_t dispatch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, i
         if (ta && !tb) return product<true, false>(a, b, c, M, N, K, M, N, 0);
         return product<true, true>(a, b, c, M, N, K, M, K, 0);
     }
+    int32_t st = CLEAVE_HIP_OK;
+    bool done;
+    if (!ta && !tb) done = try_batched_k_slices<false, false>(a, b, c, M, N, K, batch, &st);
+    else if (!ta && tb) done = try_batched_k_slices<false, true>(a, b, c, M, N, K, batch, &st);
+    else if (ta && !tb) done = try_batched_k_slices<true, false>(a, b, c, M, N, K, batch, &st);
+    else done = try_batched_k_slices<true, true>(a, b, c, M, N, K, batch, &st);
+    if (done) return st;
     if (!ta && !tb) return launch_any<false, false>(a, b, c, M, N, K, batch);
     if (!ta && tb) return launch_any<false, true>(a, b, c, M, N, K, batch);
     if (ta && !tb) return launch_any<true, false>(a, b, c, M, N, K, batch);

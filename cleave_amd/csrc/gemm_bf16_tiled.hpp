@@ -57,11 +57,16 @@ struct Bf16Tiled {
         return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
     }};
 
+// `batch` products of M x N x K, product z at A + z strideA, B + z strideB,
+// C + z strideC.  With kslices > 1 (batch a multiple of it) the products are
+// the K slices of batch / kslices products of depth K * kslices: z = s nb + b
+// (nb = batch / kslices) is slice s of product b, at A + b strideA plus s K
+// columns (k-contiguous A) or s K rows of A (likewise B), and C + z strideC.
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC, int MI = 32>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC,
-    int tiles_m, int tiles_n, int batch) {
+    int tiles_m, int tiles_n, int batch, int kslices) {
     using namespace ch::tiles;
     using P = Bf16Tiled<BM, BN, BK, WM, WN, STAGES, AKC, BKC, MI>;
     typedef float vacc __attribute__((ext_vector_type(MI == 32 ? 16 : 4)));
@@ -74,8 +79,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
     int bt, tm, tn;  // product (batch entry or K-slice) and tile of this workgroup
     ch::block_coords(blockIdx.x, tiles_m, tiles_n, batch, bt, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    A += (int64_t)bt * strideA;
-    B += (int64_t)bt * strideB;
+    if (kslices > 1) {
+        const int nb = batch / kslices, sl = bt / nb, pb = bt - sl * nb;
+        A += (int64_t)pb * strideA + (AKC ? (int64_t)sl * K : (int64_t)sl * K * lda);
+        B += (int64_t)pb * strideB + (BKC ? (int64_t)sl * K : (int64_t)sl * K * ldb);
+    } else {
+        A += (int64_t)bt * strideA;
+        B += (int64_t)bt * strideB;
+    }
     C += (int64_t)bt * strideC;
 
     TileCopy<AKC, BM, BK, NW> copy_a;

@@ -647,21 +647,25 @@ def test_f32_batched_products_on_the_128_tile_ping_pong(hip, oracle, ta, tb):
         assert_gemm_close(got[i], ref, den, K, f"batched 128-tile ping-pong product {i}")
 
 
-@pytest.mark.parametrize("bsz,M,N,K,ta,tb", [
-    # 64 tiles of 128 x 128 over the batch: 4 K slices of 512 (a round of 256
-    # tiles on the 128 x 128 ping-pong kernel, each slice at its product's
-    # k-offset), added in order
-    *[(16, 256, 256, 2048, ta, tb) for ta in (0, 1) for tb in (0, 1)],
+@pytest.mark.parametrize("dtype,bsz,M,N,K,ta,tb", [
+    # f32, 64 tiles of 128 x 128 over the batch: 4 K slices of 512 (a round
+    # of 256 tiles on the 128 x 128 ping-pong kernel, each slice at its
+    # product's k-offset), added in order
+    *[("f32", 16, 256, 256, 2048, ta, tb) for ta in (0, 1) for tb in (0, 1)],
     # 64 products of one tile: 4 slices of 1024
-    (64, 128, 128, 4096, 0, 0),
+    ("f32", 64, 128, 128, 4096, 0, 0),
     # 48 tiles: 5 slices of 768 (240 tiles)
-    (3, 512, 512, 3840, 1, 0),
+    ("f32", 3, 512, 512, 3840, 1, 0),
+    # bf16 on the 128 x 128 tiled kernel: 64 tiles as 4 slices of 1024
+    *[("bf16", 16, 256, 256, 4096, ta, tb) for ta in (0, 1) for tb in (0, 1)],
+    # 32 tiles as 8 slices of 1024
+    ("bf16", 2, 512, 512, 8192, 0, 1),
 ])
-def test_f32_batched_k_slices_every_entry(hip, oracle, bsz, M, N, K, ta, tb):
+def test_batched_k_slices_every_entry(hip, oracle, dtype, bsz, M, N, K, ta, tb):
     # Every entry of every product against the loop, and bitwise the same on
     # a second call.
-    A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=97 + 2 * ta + tb, batch=bsz)
-    a, b = hip.from_numpy(A), hip.from_numpy(B)
+    A, B, Au, Bu = _operands(oracle, dtype, M, N, K, ta, tb, seed=97 + 2 * ta + tb, batch=bsz)
+    a, b = hip.from_numpy(A, dtype), hip.from_numpy(B, dtype)
     got = hip.matmul_batched(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
     again = hip.matmul_batched(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
@@ -670,7 +674,7 @@ def test_f32_batched_k_slices_every_entry(hip, oracle, bsz, M, N, K, ta, tb):
         Bk = np.ascontiguousarray(Bu[i] if tb else Bu[i].T)
         ref = oracle.matmul(Ak, Bk, trans_b=True, threads=16)
         den = np.abs(Ak).astype(np.float64) @ np.abs(Bk).astype(np.float64).T
-        assert_gemm_close(got[i], ref, den, K, f"batched K slices {i}/{bsz} {M}x{N}x{K} ta={ta} tb={tb}")
+        assert_gemm_close(got[i], ref, den, K, f"{dtype} batched K slices {i}/{bsz} {M}x{N}x{K} ta={ta} tb={tb}")
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
