@@ -46,6 +46,8 @@ SIGNATURES: dict[str, tuple] = {
     "cleave_hip_device_available": (i32, []),
     "cleave_hip_buf_alloc": (vp, [i64]),
     "cleave_hip_buf_free": (None, [vp]),
+    "cleave_hip_buf_trim": (i64, []),
+    "cleave_hip_buf_cached_bytes": (i64, []),
     "cleave_hip_upload": (i64, [vp, vp, i64]),
     "cleave_hip_download": (i64, [vp, vp, i64]),
     "cleave_hip_sync": (i32, []),
@@ -126,6 +128,22 @@ SIGNATURES: dict[str, tuple] = {
     "cleave_hip_mandelbrot_u32_host": (i32, [vp, i64, i32, i32, f32, f32, f32, f32, i32]),
     "cleave_hip_mlp_step_f32_host": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64,
                                            vp, i32, i32, i32, f32]),
+    "cleave_hip_reduce_sum_i32_i64": (i32, [vp, i64, vp]),
+    "cleave_hip_sum_i32_i64": (i64, [vp, i64]),
+    "cleave_hip_sum_i32_i64_host": (i64, [vp, i64]),
+    "cleave_hip_matmul_f32_into": (i64, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, i32]),
+    "cleave_hip_add_f32_into": (i64, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_sub_f32_into": (i64, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_mul_f32_into": (i64, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_div_f32_into": (i64, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_neg_f32_into": (i64, [vp, i64, vp, i64]),
+    "cleave_hip_relu_f32_into": (i64, [vp, i64, vp, i64]),
+    "cleave_hip_sigmoid_f32_into": (i64, [vp, i64, vp, i64]),
+    "cleave_hip_tanh_f32_into": (i64, [vp, i64, vp, i64]),
+    "cleave_hip_sigmoid_bwd_f32_into": (i64, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_tanh_bwd_f32_into": (i64, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_relu_bwd_f32_into": (i64, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_escape_grid_i32": (i64, [vp, i64, i32, i32, f32, f32, f32, f32, i32]),
     # memref-descriptor forms: every tensor argument is a pointer to an
     # unranked descriptor {int64 rank; void* ranked descriptor}
     "_mlir_ciface_cleave_hip_matmul_f32": (i32, [vp, vp, vp]),

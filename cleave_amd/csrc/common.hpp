@@ -31,6 +31,9 @@ int32_t check_hip(hipError_t e, const char* what);
 // blocks in runtime.hip).
 void* buf_alloc(uint64_t bytes);
 void buf_free(void* buf);
+// Returns every cached free block to the device; the bytes released.
+size_t buf_trim();
+size_t buf_cached_bytes();
 
 // Scratch device memory owned by the library (grown on demand, never shrunk).
 // `slot` (0 .. kScratchSlots-1) selects an independent buffer.

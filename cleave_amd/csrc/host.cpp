@@ -31,6 +31,7 @@
 #include <unistd.h>
 
 #include "common.hpp"
+#include "copy_split.hpp"
 
 namespace {
 
@@ -89,18 +90,19 @@ class CopyPool {
         }
         return th_.size();
     }
-    // memcpy of n bytes, split over the workers and the calling thread.
+    // memcpy of n bytes, split over the workers and the calling thread
+    // (ranges from copy_split.hpp: together they cover all n bytes).
     void copy(void* dst, const void* src, size_t n) {
-        const size_t parts = std::min<size_t>(workers() + 1, std::max<size_t>(1, n / kCopySlice));
-        if (parts <= 1) {
+        const ch::CopySplit s = ch::copy_split(n, workers() + 1, kCopySlice);
+        if (s.parts <= 1) {
             memcpy(dst, src, n);
             return;
         }
-        const size_t step = (n / parts + 63) & ~size_t(63);
         {
             std::lock_guard<std::mutex> lk(mu_);
-            for (size_t p = 1; p < parts; ++p) {
-                const size_t off = std::min(n, p * step), len = std::min(n, off + step) - off;
+            for (size_t p = 1; p < s.parts; ++p) {
+                size_t off, len;
+                ch::copy_range(s, n, p, &off, &len);
                 if (len) {
                     tasks_.push_back(Task{(char*)dst + off, (const char*)src + off, len});
                     ++pending_;
@@ -108,7 +110,9 @@ class CopyPool {
             }
         }
         work_.notify_all();
-        memcpy(dst, src, std::min(step, n));
+        size_t off0, len0;
+        ch::copy_range(s, n, 0, &off0, &len0);
+        memcpy(dst, src, len0);
         std::unique_lock<std::mutex> lk(mu_);
         done_.wait(lk, [this] { return pending_ == 0; });
     }
@@ -478,6 +482,10 @@ uint64_t cleave_hip_sum_u32_u64_host(const uint32_t* x, int64_t len) {
     return reduce_host<uint64_t, uint32_t>("cleave_hip_sum_u32_u64_host", &cleave_hip_sum_u32_u64, x, len, 0);
 }
 
+int64_t cleave_hip_sum_i32_i64_host(const int32_t* x, int64_t len) {
+    return reduce_host<int64_t, int32_t>("cleave_hip_sum_i32_i64_host", &cleave_hip_sum_i32_i64, x, len, 0);
+}
+
 // ---- Index<Tensor> ---------------------------------------------------------------
 
 float cleave_hip_index_f32_host(const float* t, int64_t len, const int32_t* dims, int64_t ndims,
@@ -530,6 +538,58 @@ int32_t cleave_hip_mlp_step_f32_host(const float* x, int64_t xlen, const float* 
         s.dev<float>(ix), xlen, s.dev<float>(iy), ylen, s.dev<float>(iw1), w1len, s.dev<float>(iw2), w2len,
         idw1 >= 0 ? s.dev<float>(idw1) : nullptr, dw1len, idw2 >= 0 ? s.dev<float>(idw2) : nullptr, dw2len,
         il >= 0 ? s.dev<float>(il) : nullptr, B, D, Hd, lr));
+}
+
+// ---- output-first forms for cleave's array-return identity ----------------------
+// An extern whose cleave result is an array returns i64 at the C level and
+// hands back its first array argument (cleave/src/mlir_lower.rs:1062-1075,
+// :1123-1124).  These forms put the output array first and return its
+// element count on success (like print_bytes returning its length,
+// cleave-rt/src/lib.rs:114-122), or the negative status of the `_host` call
+// they forward to.
+
+#define CH_INTO_RESULT(call, outlen)                      \
+    do {                                                  \
+        const int32_t _st = (call);                       \
+        return _st == CLEAVE_HIP_OK ? (outlen) : (int64_t)_st; \
+    } while (0)
+
+int64_t cleave_hip_matmul_f32_into(float* c, int64_t clen, const float* a, int64_t alen, const float* b,
+                                   int64_t blen, int32_t M, int32_t N, int32_t K, int32_t trans_a,
+                                   int32_t trans_b) {
+    CH_INTO_RESULT(cleave_hip_matmul_f32_host(a, alen, b, blen, c, clen, M, N, K, trans_a, trans_b), clen);
+}
+
+#define CH_MAP2_INTO(op)                                                                                  \
+    int64_t cleave_hip_##op##_f32_into(float* out, int64_t outlen, const float* a, int64_t alen,       \
+                                       const float* b, int64_t blen) {                                  \
+        CH_INTO_RESULT(cleave_hip_##op##_f32_host(a, alen, b, blen, out, outlen), outlen);             \
+    }
+#define CH_MAP1_INTO(op)                                                                                  \
+    int64_t cleave_hip_##op##_f32_into(float* out, int64_t outlen, const float* x, int64_t xlen) {      \
+        CH_INTO_RESULT(cleave_hip_##op##_f32_host(x, xlen, out, outlen), outlen);                      \
+    }
+
+CH_MAP2_INTO(add)
+CH_MAP2_INTO(sub)
+CH_MAP2_INTO(mul)
+CH_MAP2_INTO(div)
+CH_MAP1_INTO(neg)
+CH_MAP1_INTO(relu)
+CH_MAP1_INTO(sigmoid)
+CH_MAP1_INTO(tanh)
+CH_MAP2_INTO(sigmoid_bwd)
+CH_MAP2_INTO(tanh_bwd)
+CH_MAP2_INTO(relu_bwd)
+
+// Escape counts as cleave's i32 (escape_count returns i32,
+// examples/mandelbrot.cleave:14): counts are at most max_iter < 2^31, so the
+// u32 counts of the same grid have the same bits.
+int64_t cleave_hip_escape_grid_i32(int32_t* out, int64_t outlen, int32_t width, int32_t height, float x0,
+                                   float y0, float dx, float dy, int32_t max_iter) {
+    CH_INTO_RESULT(cleave_hip_mandelbrot_u32_host(reinterpret_cast<uint32_t*>(out), outlen, width, height, x0, y0,
+                                                  dx, dy, max_iter),
+                   outlen);
 }
 
 }  // extern "C"

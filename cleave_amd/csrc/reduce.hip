@@ -1,5 +1,6 @@
-// reduce.hip -- Sum / Mean / Max (stdlib/nn/nn.cleave:111-149) and the exact
-// u64 sum of u32 escape counts.
+// reduce.hip -- Sum / Mean / Max (stdlib/nn/nn.cleave:111-149), the exact
+// u64 sum of u32 escape counts, and the exact i64 sum of i32 arrays (the
+// same counts as cleave's i32 type carries them).
 //
 // Two stages, both deterministic for a given length: stage 1 runs a fixed
 // grid (a function of the length and the CU count only); each thread folds
@@ -233,6 +234,14 @@ __device__ uint64_t block_sum_u64(uint64_t v) {
     return r;
 }
 
+// Signed: each element is sign-extended to 64 bits, so the u64 total is the
+// two's-complement bits of the exact i64 sum (stage 2 is the same add).
+template <bool Signed>
+__device__ __forceinline__ uint64_t widen(uint32_t v) {
+    return Signed ? (uint64_t)(int64_t)(int32_t)v : (uint64_t)v;
+}
+
+template <bool Signed>
 __global__ __launch_bounds__(kThreads) void sum_u32_stage1(const uint32_t* __restrict__ x, int64_t n,
                                                            uint64_t* __restrict__ partial,
                                                            int aligned) {
@@ -247,15 +256,16 @@ __global__ __launch_bounds__(kThreads) void sum_u32_stage1(const uint32_t* __res
                 int64_t i = base + (int64_t)u * kThreads;
                 v[u] = i < nv ? __builtin_nontemporal_load(reinterpret_cast<const u4*>(x) + i) : u4{0, 0, 0, 0};
             }
-            // Four u32 fit in u64 without overflow; add pairs in 64 bits.
+            // Add in 64 bits (mod 2^64, exact for both forms).
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u)
-                acc += ((uint64_t)v[u][0] + v[u][1]) + ((uint64_t)v[u][2] + v[u][3]);
+                acc += (widen<Signed>(v[u][0]) + widen<Signed>(v[u][1])) +
+                       (widen<Signed>(v[u][2]) + widen<Signed>(v[u][3]));
         }
-        if (blockIdx.x == 0 && threadIdx.x < (n & 3)) acc += x[nv * 4 + threadIdx.x];
+        if (blockIdx.x == 0 && threadIdx.x < (n & 3)) acc += widen<Signed>(x[nv * 4 + threadIdx.x]);
     } else {
         for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
-            acc += x[i];
+            acc += widen<Signed>(x[i]);
     }
     uint64_t r = block_sum_u64(acc);
     if (threadIdx.x == 0) partial[blockIdx.x] = r;
@@ -355,9 +365,28 @@ int32_t cleave_hip_reduce_sum_u32_u64(const uint32_t* x, int64_t len, uint64_t* 
     unsigned blocks = stage1_blocks(aligned ? len / 4 + 1 : len / kUnroll + 1);
     uint64_t* part = (uint64_t*)ch::scratch(2, sizeof(uint64_t) * blocks);
     if (!part) return CLEAVE_HIP_ERR_OOM;
-    sum_u32_stage1<<<blocks, kThreads, 0, ch::stream()>>>(x, len, part, aligned);
+    sum_u32_stage1<false><<<blocks, kThreads, 0, ch::stream()>>>(x, len, part, aligned);
     CH_LAUNCHED("sum_u32_stage1");
     sum_u64_stage2<<<1, kThreads, 0, ch::stream()>>>(part, (int)blocks, out_dev);
+    CH_LAUNCHED("sum_u64_stage2");
+    return CLEAVE_HIP_OK;
+}
+
+int32_t cleave_hip_reduce_sum_i32_i64(const int32_t* x, int64_t len, int64_t* out_dev) {
+    const char* fn = "cleave_hip_reduce_sum_i32_i64";
+    CH_REQUIRE(len >= 0, "%s: negative length", fn);
+    CH_REQUIRE(x && out_dev, "%s: null buffer", fn);
+    CH_INIT_OR_RETURN();
+    CH_DEVICE(fn, x, len * 4);
+    CH_DEVICE(fn, out_dev, 8);
+    const int aligned = aligned16(x);
+    unsigned blocks = stage1_blocks(aligned ? len / 4 + 1 : len / kUnroll + 1);
+    uint64_t* part = (uint64_t*)ch::scratch(2, sizeof(uint64_t) * blocks);
+    if (!part) return CLEAVE_HIP_ERR_OOM;
+    sum_u32_stage1<true><<<blocks, kThreads, 0, ch::stream()>>>(reinterpret_cast<const uint32_t*>(x), len, part,
+                                                                 aligned);
+    CH_LAUNCHED("sum_i32_stage1");
+    sum_u64_stage2<<<1, kThreads, 0, ch::stream()>>>(part, (int)blocks, reinterpret_cast<uint64_t*>(out_dev));
     CH_LAUNCHED("sum_u64_stage2");
     return CLEAVE_HIP_OK;
 }
@@ -399,6 +428,17 @@ int64_t cleave_hip_argmax_f32(const float* x, int64_t len) {
     if (cleave_hip_reduce_max_f32(x, len, nullptr, d) != CLEAVE_HIP_OK) return -1;
     int64_t r = -1;
     if (cleave_hip_download(&r, d, sizeof(int64_t)) != (int64_t)sizeof(int64_t)) return -1;
+    return r;
+}
+
+int64_t cleave_hip_sum_i32_i64(const int32_t* x, int64_t len) {
+    ch::clear_error();
+    if (ch::ensure_init() != CLEAVE_HIP_OK) return 0;
+    int64_t* d = (int64_t*)ch::scratch(3, 64);
+    if (!d) return 0;
+    if (cleave_hip_reduce_sum_i32_i64(x, len, d) != CLEAVE_HIP_OK) return 0;
+    int64_t r = 0;
+    if (cleave_hip_download(&r, d, sizeof(int64_t)) != (int64_t)sizeof(int64_t)) return 0;
     return r;
 }
 

@@ -100,6 +100,10 @@ void* scratch(int slot, size_t bytes) {
     return p;
 }
 
+namespace {
+size_t release_cached();
+}  // namespace
+
 void* scratch_try(int slot, size_t bytes) {
     if (slot < 0 || slot >= kScratchSlots) return nullptr;
     if (g.scratch_bytes[slot] >= bytes && g.scratch[slot]) return g.scratch[slot];
@@ -113,7 +117,12 @@ void* scratch_try(int slot, size_t bytes) {
     void* p = nullptr;
     if (hipMalloc(&p, bytes) != hipSuccess) {
         (void)hipGetLastError();
-        return nullptr;
+        // The cache of freed buffers may hold the memory: return it to the
+        // device and try once more, as buf_alloc does.
+        if (release_cached() == 0 || hipMalloc(&p, bytes) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
     }
     g.scratch[slot] = p;
     g.scratch_bytes[slot] = bytes;
@@ -134,6 +143,7 @@ struct BufPool {
     std::mutex mu;
     std::map<uintptr_t, std::pair<uint64_t, size_t>> live;  // base -> (bytes asked for, block size)
     std::multimap<size_t, void*> cached;                     // block size -> free block
+    std::map<uintptr_t, size_t> cached_at;                   // base -> block size, the same free blocks
     size_t cached_bytes = 0;
 };
 BufPool g_pool;
@@ -144,18 +154,34 @@ size_t block_size(uint64_t bytes) {
     return (size_t)((bytes + q - 1) / q * q);
 }
 
-void release_cached() {
+// Returns every cached block to the device; the bytes released.
+size_t release_cached() {
     std::vector<void*> blocks;
+    size_t bytes = 0;
     {
         std::lock_guard<std::mutex> lk(g_pool.mu);
         for (auto& kv : g_pool.cached) blocks.push_back(kv.second);
+        bytes = g_pool.cached_bytes;
         g_pool.cached.clear();
+        g_pool.cached_at.clear();
         g_pool.cached_bytes = 0;
     }
-    if (blocks.empty()) return;
+    if (blocks.empty()) return 0;
     (void)hipStreamSynchronize(g.stream);
     for (void* b : blocks) (void)hipFree(b);
     (void)hipGetLastError();
+    return bytes;
+}
+
+// True when p lies in a freed block that waits in the cache: a pointer into
+// a buffer its owner already released.
+bool in_cached_block(const void* p) {
+    const uintptr_t q = (uintptr_t)p;
+    std::lock_guard<std::mutex> lk(g_pool.mu);
+    auto it = g_pool.cached_at.upper_bound(q);
+    if (it == g_pool.cached_at.begin()) return false;
+    --it;
+    return q < it->first + it->second;
 }
 
 // The bytes from p to the end of the library buffer holding it (what its
@@ -182,6 +208,7 @@ void* buf_alloc(uint64_t bytes) {
         if (it != g_pool.cached.end()) {
             p = it->second;
             g_pool.cached.erase(it);
+            g_pool.cached_at.erase((uintptr_t)p);
             g_pool.cached_bytes -= sz;
         }
     }
@@ -211,6 +238,7 @@ void buf_free(void* buf) {
             g_pool.live.erase(it);
             if (g_pool.cached_bytes + sz <= kPoolCap) {
                 g_pool.cached.emplace(sz, buf);
+                g_pool.cached_at[(uintptr_t)buf] = sz;
                 g_pool.cached_bytes += sz;
                 return;
             }
@@ -220,6 +248,13 @@ void buf_free(void* buf) {
     // queued work may still use it.
     if (check_hip(hipStreamSynchronize(g.stream), "hipStreamSynchronize") != CLEAVE_HIP_OK) return;
     check_hip(hipFree(buf), "hipFree");
+}
+
+size_t buf_trim() { return release_cached(); }
+
+size_t buf_cached_bytes() {
+    std::lock_guard<std::mutex> lk(g_pool.mu);
+    return g_pool.cached_bytes;
 }
 
 int32_t require_device(const char* fn, const char* what, const void* p, uint64_t bytes) {
@@ -237,6 +272,10 @@ int32_t require_device(const char* fn, const char* what, const void* p, uint64_t
         return fail(CLEAVE_HIP_ERR_ARG,
                     "%s: %s (%p) is not device memory (memory type %d); pass a buffer from "
                     "cleave_hip_buf_alloc (the _host entry points take host arrays)", fn, what, p, (int)at.type);
+    if (in_cached_block(p))
+        return fail(CLEAVE_HIP_ERR_ARG,
+                    "%s: %s (%p) points into a buffer that was freed (cleave_hip_buf_free); allocate a new one",
+                    fn, what, p);
     uint64_t avail = 0;
     if (pool_extent(p, &avail)) {
         if (bytes > avail)
@@ -357,6 +396,16 @@ void cleave_hip_buf_free(void* buf) {
     if (!buf) return;
     if (ch::ensure_init() != CLEAVE_HIP_OK) return;
     ch::buf_free(buf);
+}
+
+int64_t cleave_hip_buf_trim(void) {
+    CH_INIT_OR_RETURN();
+    return (int64_t)ch::buf_trim();
+}
+
+int64_t cleave_hip_buf_cached_bytes(void) {
+    CH_INIT_OR_RETURN();
+    return (int64_t)ch::buf_cached_bytes();
 }
 
 int64_t cleave_hip_upload(void* dst_dev, const void* src_host, int64_t bytes) {

@@ -162,6 +162,12 @@ def sum_u64(x) -> int:
     return int(_scalar("cleave_hip_sum_u32_u64_host", _p(x), x.size))
 
 
+def sum_i64(x) -> int:
+    """Exact i64 sum of an i32 array (cleave's Sum<[i32; N], i64> binding)."""
+    x = _arr(x, np.int32)
+    return int(_scalar("cleave_hip_sum_i32_i64_host", _p(x), x.size))
+
+
 # ---- Index<Tensor> (stdlib/linalg/tensor.cleave:113-133) ----------------------------------
 
 def index(t: np.ndarray, idx) -> float:
@@ -209,3 +215,28 @@ def mlp_step(x, y, w1: np.ndarray, w2: np.ndarray, lr: float, want_grads: bool =
          _p(dw1) if want_grads else None, dw1.size if want_grads else 0,
          _p(dw2) if want_grads else None, dw2.size if want_grads else 0, _p(loss), B, D, Hd, float(lr))
     return float(loss[0]), dw1, dw2
+
+
+# ---- output-first forms (cleave's array-return identity) -----------------------------------
+
+def into(fn: str, out: np.ndarray, *args) -> np.ndarray:
+    """Calls a `cleave_hip_*_into` entry point the way cleave's extern lowering
+    does (/root/reference/cleave/src/mlir_lower.rs:1062-1130): every array
+    argument, `out` first, becomes (pointer, length); the C result is an i64
+    (the output length, or a negative status); the value handed back is `out`
+    itself, filled in place."""
+    if not out.flags["C_CONTIGUOUS"]:
+        raise TypeError(f"{fn}: out must be C-contiguous (written in place)")
+    flat = [_p(out), out.size]
+    for a in args:
+        if isinstance(a, np.ndarray):
+            flat += [_p(a), a.size]
+        else:
+            flat.append(a)
+    n = getattr(load(), fn)(*flat)
+    if n < 0:
+        code, msg = _lib.last_error()
+        raise CleaveHipError(int(n), msg)
+    if n != out.size:
+        raise CleaveHipError(_lib.ERR_RUNTIME, f"{fn} returned {n}, expected the output length {out.size}")
+    return out

@@ -74,10 +74,19 @@ CLEAVE_HIP_API int32_t cleave_hip_device_available(void);
  * a cache of free blocks that later allocations of the same size reuse
  * without a device synchronisation (work on the library stream is ordered).
  * The cache holds at most 32 GiB and is returned to the device when an
- * allocation would otherwise fail.  A device entry point refuses an operand
- * that runs past the bytes its buffer was allocated with. */
+ * allocation (a buffer, or library scratch) would otherwise fail.  A device
+ * entry point refuses an operand that runs past the bytes its buffer was
+ * allocated with, and a pointer into a freed block still in the cache. */
 CLEAVE_HIP_API void* cleave_hip_buf_alloc(int64_t bytes);
 CLEAVE_HIP_API void cleave_hip_buf_free(void* buf);
+/* Returns every cached free block to the device (after the library stream
+ * drains) and the bytes released, for a host that needs the memory for
+ * something outside this library.  The library's own allocations (buffers
+ * and scratch) already do this before they fail.  (No reference
+ * counterpart: cleave_alloc never frees, cleave-rt/src/lib.rs:56-71.) */
+CLEAVE_HIP_API int64_t cleave_hip_buf_trim(void);
+/* Bytes held by the cache of freed blocks. */
+CLEAVE_HIP_API int64_t cleave_hip_buf_cached_bytes(void);
 /* Host <-> device copies on the library stream; both return the byte count
  * (like print_bytes' "returns len", cleave-rt/src/lib.rs:114-122) after the
  * stream has drained, so the host buffer may be reused at once. */
@@ -226,6 +235,10 @@ CLEAVE_HIP_API int32_t cleave_hip_reduce_sum_f32(const float* x, int64_t len, fl
 CLEAVE_HIP_API int32_t cleave_hip_reduce_max_f32(const float* x, int64_t len, float* max_dev,
                                   int64_t* argmax_dev);
 CLEAVE_HIP_API int32_t cleave_hip_reduce_sum_u32_u64(const uint32_t* x, int64_t len, uint64_t* out_dev);
+/* Exact i64 sum of an i32 array: the escape counts as cleave's i32 type holds
+ * them (escape_count returns i32, examples/mandelbrot.cleave:14).  Extension:
+ * the reference's Sum is over Float elements (stdlib/nn/nn.cleave:111-117). */
+CLEAVE_HIP_API int32_t cleave_hip_reduce_sum_i32_i64(const int32_t* x, int64_t len, int64_t* out_dev);
 /* cleave_hip_reduce_sum_f32 that allocates nothing.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
@@ -243,6 +256,7 @@ CLEAVE_HIP_API float cleave_hip_max_of_f32(const float* x, int64_t len);
 /* First index of the value max_of returns (extension; the reference has no argmax). */
 CLEAVE_HIP_API int64_t cleave_hip_argmax_f32(const float* x, int64_t len);
 CLEAVE_HIP_API uint64_t cleave_hip_sum_u32_u64(const uint32_t* x, int64_t len);
+CLEAVE_HIP_API int64_t cleave_hip_sum_i32_i64(const int32_t* x, int64_t len); /* 0 after an error */
 
 /* ---------------------------------------------------------------------- */
 /* Index<Tensor> (stdlib/linalg/tensor.cleave:113-133)                      */
@@ -356,6 +370,7 @@ CLEAVE_HIP_API float cleave_hip_mean_f32_host(const float* x, int64_t len);
 CLEAVE_HIP_API float cleave_hip_max_of_f32_host(const float* x, int64_t len);
 CLEAVE_HIP_API int64_t cleave_hip_argmax_f32_host(const float* x, int64_t len);
 CLEAVE_HIP_API uint64_t cleave_hip_sum_u32_u64_host(const uint32_t* x, int64_t len);
+CLEAVE_HIP_API int64_t cleave_hip_sum_i32_i64_host(const int32_t* x, int64_t len);
 
 /* Index<Tensor> (stdlib/linalg/tensor.cleave:113-133). */
 CLEAVE_HIP_API float cleave_hip_index_f32_host(const float* t, int64_t len, const int32_t* dims, int64_t ndims,
@@ -374,6 +389,50 @@ CLEAVE_HIP_API int32_t cleave_hip_mlp_step_f32_host(const float* x, int64_t xlen
                                                     float* w1, int64_t w1len, float* w2, int64_t w2len,
                                                     float* dw1, int64_t dw1len, float* dw2, int64_t dw2len,
                                                     float* loss, int32_t B, int32_t D, int32_t Hd, float lr);
+
+/* ---------------------------------------------------------------------- */
+/* Output-first forms, for cleave's array-return identity                   */
+/* ---------------------------------------------------------------------- */
+/* A cleave `extern` whose result type is an array is declared at the C level
+ * as returning i64, and the call's cleave result is its FIRST array argument
+ * (cleave/src/mlir_lower.rs:1062-1075, :1123-1124; print_bytes,
+ * stdlib/io/io.cleave:35).  So an extern that fills an array takes that array
+ * first: each `_into` form below is the `_host` form of the same operator
+ * with the output array moved to the front and an int64_t result, the output
+ * length on success or the `_host` call's negative status.  All arrays are
+ * host arrays, as for the `_host` forms; the output is written in place, so
+ * the cleave result (the same array) holds it. */
+
+/* c = op(a) * op(b) (stdlib/linalg/matrix.cleave:22-61). */
+CLEAVE_HIP_API int64_t cleave_hip_matmul_f32_into(float* c, int64_t clen, const float* a, int64_t alen,
+                                                  const float* b, int64_t blen, int32_t M, int32_t N, int32_t K,
+                                                  int32_t trans_a, int32_t trans_b);
+/* Ring<Tensor> (stdlib/linalg/tensor.cleave:66-71). */
+CLEAVE_HIP_API int64_t cleave_hip_add_f32_into(float* out, int64_t outlen, const float* a, int64_t alen,
+                                               const float* b, int64_t blen);
+CLEAVE_HIP_API int64_t cleave_hip_sub_f32_into(float* out, int64_t outlen, const float* a, int64_t alen,
+                                               const float* b, int64_t blen);
+CLEAVE_HIP_API int64_t cleave_hip_mul_f32_into(float* out, int64_t outlen, const float* a, int64_t alen,
+                                               const float* b, int64_t blen);
+CLEAVE_HIP_API int64_t cleave_hip_div_f32_into(float* out, int64_t outlen, const float* a, int64_t alen,
+                                               const float* b, int64_t blen);
+CLEAVE_HIP_API int64_t cleave_hip_neg_f32_into(float* out, int64_t outlen, const float* x, int64_t xlen);
+/* Activation<Tensor> (stdlib/nn/nn.cleave:82-95). */
+CLEAVE_HIP_API int64_t cleave_hip_relu_f32_into(float* out, int64_t outlen, const float* x, int64_t xlen);
+CLEAVE_HIP_API int64_t cleave_hip_sigmoid_f32_into(float* out, int64_t outlen, const float* x, int64_t xlen);
+CLEAVE_HIP_API int64_t cleave_hip_tanh_f32_into(float* out, int64_t outlen, const float* x, int64_t xlen);
+/* Backward maps (stdlib/num/num.cleave:123-136, :222-223). */
+CLEAVE_HIP_API int64_t cleave_hip_sigmoid_bwd_f32_into(float* out, int64_t outlen, const float* s, int64_t slen,
+                                                       const float* g, int64_t glen);
+CLEAVE_HIP_API int64_t cleave_hip_tanh_bwd_f32_into(float* out, int64_t outlen, const float* t, int64_t tlen,
+                                                    const float* g, int64_t glen);
+CLEAVE_HIP_API int64_t cleave_hip_relu_bwd_f32_into(float* out, int64_t outlen, const float* x, int64_t xlen,
+                                                    const float* g, int64_t glen);
+/* escape_count over a grid (examples/mandelbrot.cleave:14-26) as i32 counts,
+ * escape_count's own return type: the counts of cleave_hip_mandelbrot_u32,
+ * which never exceed max_iter, so the bits are the same. */
+CLEAVE_HIP_API int64_t cleave_hip_escape_grid_i32(int32_t* out, int64_t outlen, int32_t width, int32_t height,
+                                                  float x0, float y0, float dx, float dy, int32_t max_iter);
 
 #ifdef __cplusplus
 }

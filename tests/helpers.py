@@ -53,3 +53,34 @@ def view(t, offset_elems, n):
 
     esize = {"f32": 4, "u32": 4, "bf16": 2}[t.dtype]
     return ca.Tensor(t.ptr + offset_elems * esize, (n,), t.dtype, owned=False)
+
+
+def mlp_grad_scales(X, y, W1, W2):
+    """Per-entry scales of the MLP step's gradient contractions, in float64.
+
+    dW1 = X^T d1 and dW2 = H^T d2 are K = B contractions, so each entry gets
+    the GEMM bound 1e-5 * sqrt(B) * sum_m |a_m||b_m|; these are those sums:
+    |X|^T |d1| with |d1| = |W2| * H(1-H) * |d2|, and |H|^T |d2|, where
+    d2 = (2/B)(yhat - y) yhat (1 - yhat) from a float64 forward pass (ample for
+    a tolerance's scale)."""
+    X64 = np.asarray(X, np.float64)
+    B = X64.shape[0]
+    H = 1.0 / (1.0 + np.exp(-(X64 @ np.asarray(W1, np.float64))))
+    W2v = np.asarray(W2, np.float64).ravel()
+    yh = 1.0 / (1.0 + np.exp(-(H @ W2v)))
+    d2 = np.abs((2.0 / B) * (yh - np.asarray(y, np.float64).ravel()) * yh * (1.0 - yh))
+    a1 = np.abs(X64).T @ (np.abs(W2v)[None, :] * (H * (1.0 - H)) * d2[:, None])
+    a2 = np.abs(H).T @ d2
+    return a1, a2
+
+
+def assert_mlp_grads_close(got1, got2, ref1, ref2, X, y, W1, W2, what=""):
+    """Every dW1 / dW2 entry within the GEMM bound of the oracle's entry."""
+    B = np.asarray(X).shape[0]
+    a1, a2 = mlp_grad_scales(X, y, W1, W2)
+    tol = 1e-5 * np.sqrt(B)
+    e1 = gemm_normalised_error(np.asarray(got1).reshape(a1.shape), np.asarray(ref1).reshape(a1.shape), a1)
+    e2 = gemm_normalised_error(np.asarray(got2).reshape(a2.shape), np.asarray(ref2).reshape(a2.shape), a2)
+    assert e1 <= tol, f"{what} dW1 normalised error {e1:.3e} > {tol:.3e}"
+    assert e2 <= tol, f"{what} dW2 normalised error {e2:.3e} > {tol:.3e}"
+    return e1, e2

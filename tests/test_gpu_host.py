@@ -14,7 +14,7 @@ import ctypes as C
 import numpy as np
 import pytest
 
-from helpers import assert_gemm_close, rel_close
+from helpers import assert_gemm_close, assert_mlp_grads_close, rel_close
 
 pytestmark = pytest.mark.gpu
 
@@ -159,10 +159,9 @@ def test_mlp_step_host(host, oracle):
     w1, w2 = W1.copy(), W2.copy()
     loss, dw1, dw2 = host.mlp_step(X, y, w1, w2, 0.01)
     assert abs(loss - lossr) <= 1e-5 * abs(lossr)
-    g1 = np.abs(dW1r).max()
-    assert np.max(np.abs(dw1 - dW1r)) <= 1e-4 * g1
-    assert np.max(np.abs(dw2 - dW2r)) <= 1e-4 * np.abs(dW2r).max()
-    assert np.allclose(w1, W1r, rtol=1e-6, atol=1e-8) and np.allclose(w2, W2r, rtol=1e-6, atol=1e-8)
+    assert_mlp_grads_close(dw1, dw2, dW1r, dW2r, X, y, W1, W2, "host")
+    assert np.array_equal(w1, W1 - np.float32(0.01) * dw1)
+    assert np.array_equal(w2, W2 - np.float32(0.01) * dw2)
 
 
 def test_large_host_arrays_through_the_bounce_buffers(host, oracle):
@@ -192,6 +191,25 @@ def test_large_host_arrays_through_the_bounce_buffers(host, oracle):
     cnt = host.escape_counts(w_, h_, -2.0, -1.5, 3.0 / w_, 3.0 / h_, 64)
     ref = oracle.mandelbrot(w_, h_, -2.0, -1.5, np.float32(3.0 / w_), np.float32(3.0 / h_), 64, threads=16)
     assert np.array_equal(cnt.reshape(h_, w_), ref)
+
+
+def test_host_copies_whose_split_leaves_a_tail(host, oracle):
+    # 2,621,441 floats = 10,485,764 bytes: one bounce chunk split over up to 5
+    # copying threads.  A split that rounded n / parts down to 64 bytes left
+    # the last 4 bytes uncopied here (stale input on the way in, an unwritten
+    # output element on the way out).
+    rng = np.random.default_rng(321)
+    n = 2621441
+    a = rng.standard_normal(n, dtype=np.float32)
+    b = rng.standard_normal(n, dtype=np.float32)
+    got = host.add(a, b)
+    assert np.array_equal(got, oracle.add(a, b))
+    assert got[-1] == a[-1] + b[-1]
+    s = host.sum(a)
+    assert abs(s - oracle.sum_f32(a)) <= 1e-5 * float(np.sum(np.abs(a), dtype=np.float64))
+    for m in (n - 1, n + 1, 3 * 1048576 + 5, 4 * 1048576 - 3):  # other ragged splits around it
+        x = rng.standard_normal(m, dtype=np.float32)
+        assert np.array_equal(host.neg(x), -x), m
 
 
 def test_host_forms_take_empty_arrays(host):

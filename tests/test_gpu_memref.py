@@ -8,7 +8,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from helpers import assert_gemm_close, rel_close
+from helpers import assert_gemm_close, assert_mlp_grads_close, rel_close
 
 pytestmark = pytest.mark.gpu
 
@@ -168,7 +168,7 @@ def test_mlp_step(hip, mr, oracle, B, D, H):
     mr.call("cleave_hip_mlp_step_f32", mr.of(x), mr.of(y), mr.of(w1), mr.of(w2), mr.of(dw1), mr.of(dw2),
             mr.of(loss), lr)
     assert abs(loss.numpy()[0] - loss_r) <= 1e-5 * abs(loss_r)
-    assert np.max(np.abs(dw1.numpy() - dW1_r)) <= 1e-4 * np.abs(dW1_r).max()
-    assert np.max(np.abs(dw2.numpy() - dW2_r)) <= 1e-4 * np.abs(dW2_r).max()
-    assert np.max(np.abs(w1.numpy() - W1_r)) <= 1e-6 * max(1.0, np.abs(W1_r).max())
-    assert np.max(np.abs(w2.numpy() - W2_r)) <= 1e-6 * max(1.0, np.abs(W2_r).max())
+    g1, g2 = dw1.numpy(), dw2.numpy()
+    assert_mlp_grads_close(g1, g2, dW1_r, dW2_r, X, Y, W1, W2, f"memref B={B}")
+    assert np.array_equal(w1.numpy(), W1 - np.float32(lr) * g1)
+    assert np.array_equal(w2.numpy(), W2 - np.float32(lr) * g2)
