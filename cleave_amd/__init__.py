@@ -6,6 +6,7 @@ program calls (/root/reference/stdlib/linalg/{tensor,matrix}.cleave,
 /root/reference/stdlib/nn/nn.cleave), over device-resident tensors:
 
     matmul(a, b)                     MatMul::matmul          matrix.cleave:27-61
+    (every Float operator takes f32 tensors, or f64 ones for Tensor<f64, ...>)
     add/sub/mul/div/neg, zero        Ring<Tensor>            tensor.cleave:66-80
     relu/sigmoid/tanh                Activation<Tensor>      nn.cleave:82-95
     sum/mean/max_of                  Sum/Mean/Max            nn.cleave:111-149
@@ -33,7 +34,7 @@ __all__ = [
     "fill_bernoulli", "to_bf16", "Timer", "symbol_table",
 ]
 
-_DTYPES = {"f32": (np.float32, 4), "bf16": (np.uint16, 2), "u32": (np.uint32, 4),
+_DTYPES = {"f32": (np.float32, 4), "f64": (np.float64, 8), "bf16": (np.uint16, 2), "u32": (np.uint32, 4),
            "u64": (np.uint64, 8), "i64": (np.int64, 8)}
 
 
@@ -134,7 +135,7 @@ def empty(shape, dtype: str = "f32") -> Tensor:
 
 def from_numpy(arr: np.ndarray, dtype: str | None = None) -> Tensor:
     if dtype is None:
-        dtype = {np.dtype(np.float32): "f32", np.dtype(np.uint16): "bf16",
+        dtype = {np.dtype(np.float32): "f32", np.dtype(np.float64): "f64", np.dtype(np.uint16): "bf16",
                  np.dtype(np.uint32): "u32"}[np.dtype(arr.dtype)]
     t = empty(arr.shape, dtype)
     return t.upload(arr)
@@ -145,11 +146,19 @@ def _need(t: Tensor, dtype: str, what: str) -> None:
         raise TypeError(f"{what}: expected {dtype} tensor, got {t.dtype}")
 
 
+def _float_sfx(t: Tensor, what: str) -> str:
+    """The entry-point suffix of a Float tensor: f32, or f64 for Tensor<f64, ...>."""
+    if t.dtype not in ("f32", "f64"):
+        raise TypeError(f"{what}: expected an f32 or f64 tensor, got {t.dtype}")
+    return t.dtype
+
+
 # ---- MatMul (stdlib/linalg/matrix.cleave:22-61) ------------------------------
 
 def matmul(a: Tensor, b: Tensor, trans_a: bool = False, trans_b: bool = False,
            out: Tensor | None = None) -> Tensor:
-    """C = op(A) op(B) with fp32 accumulation; A/B f32 or bf16 (both the same)."""
+    """C = op(A) op(B): f32 or bf16 operands give an f32 product (f32
+    accumulation), f64 operands an f64 one."""
     if len(a.shape) != 2 or len(b.shape) != 2:
         raise ValueError("matmul: rank-2 operands required")
     M, K = (a.shape[1], a.shape[0]) if trans_a else a.shape
@@ -158,8 +167,8 @@ def matmul(a: Tensor, b: Tensor, trans_a: bool = False, trans_b: bool = False,
         raise ValueError(f"matmul: inner dimensions differ ({K} vs {Kb})")
     if a.dtype != b.dtype:
         raise TypeError("matmul: operands must share a dtype")
-    out = out if out is not None else empty((M, N), "f32")
-    fn = "cleave_hip_matmul_f32" if a.dtype == "f32" else "cleave_hip_matmul_bf16"
+    out = out if out is not None else empty((M, N), "f64" if a.dtype == "f64" else "f32")
+    fn = {"f32": "cleave_hip_matmul_f32", "bf16": "cleave_hip_matmul_bf16", "f64": "cleave_hip_matmul_f64"}[a.dtype]
     call(fn, a.ptr, a.size, b.ptr, b.size, out.ptr, out.size, M, N, K, int(trans_a), int(trans_b))
     return out
 
@@ -173,98 +182,95 @@ def matmul_batched(a: Tensor, b: Tensor, out: Tensor | None = None, trans_a: boo
         M, K = K, M
     if trans_b:
         Kb, N = N, Kb
-    out = out if out is not None else empty((batch, M, N), "f32")
-    if a.dtype == "f32":
-        call("cleave_hip_matmul_batched_f32", a.ptr, a.size, b.ptr, b.size, out.ptr, out.size,
-             batch, M, N, K, int(trans_a), int(trans_b))
-    else:
-        call("cleave_hip_matmul_batched_bf16", a.ptr, a.size, b.ptr, b.size, out.ptr, out.size,
-             batch, M, N, K, int(trans_a), int(trans_b))
+    out = out if out is not None else empty((batch, M, N), "f64" if a.dtype == "f64" else "f32")
+    call(f"cleave_hip_matmul_batched_{a.dtype}", a.ptr, a.size, b.ptr, b.size, out.ptr, out.size,
+         batch, M, N, K, int(trans_a), int(trans_b))
     return out
 
 
 # ---- Ring<Tensor> / Activation<Tensor> ------------------------------------------
 
-def _binary(fn: str, a: Tensor, b: Tensor, out: Tensor | None) -> Tensor:
-    out = out if out is not None else empty(a.shape, "f32")
-    call(fn, a.ptr, a.size, b.ptr, b.size, out.ptr, out.size)
+def _binary(op: str, a: Tensor, b: Tensor, out: Tensor | None) -> Tensor:
+    sfx = _float_sfx(a, op)
+    out = out if out is not None else empty(a.shape, sfx)
+    call(f"cleave_hip_{op}_{sfx}", a.ptr, a.size, b.ptr, b.size, out.ptr, out.size)
     return out
 
 
-def _unary(fn: str, a: Tensor, out: Tensor | None) -> Tensor:
-    out = out if out is not None else empty(a.shape, "f32")
-    call(fn, a.ptr, a.size, out.ptr, out.size)
+def _unary(op: str, a: Tensor, out: Tensor | None) -> Tensor:
+    sfx = _float_sfx(a, op)
+    out = out if out is not None else empty(a.shape, sfx)
+    call(f"cleave_hip_{op}_{sfx}", a.ptr, a.size, out.ptr, out.size)
     return out
 
 
-def add(a, b, out=None): return _binary("cleave_hip_add_f32", a, b, out)
-def sub(a, b, out=None): return _binary("cleave_hip_sub_f32", a, b, out)
-def mul(a, b, out=None): return _binary("cleave_hip_mul_f32", a, b, out)
-def div(a, b, out=None): return _binary("cleave_hip_div_f32", a, b, out)
-def neg(a, out=None): return _unary("cleave_hip_neg_f32", a, out)
-def relu(x, out=None): return _unary("cleave_hip_relu_f32", x, out)
-def sigmoid(x, out=None): return _unary("cleave_hip_sigmoid_f32", x, out)
-def tanh(x, out=None): return _unary("cleave_hip_tanh_f32", x, out)
-def sigmoid_bwd(s, g, out=None): return _binary("cleave_hip_sigmoid_bwd_f32", s, g, out)
-def tanh_bwd(t, g, out=None): return _binary("cleave_hip_tanh_bwd_f32", t, g, out)
-def relu_bwd(x, g, out=None): return _binary("cleave_hip_relu_bwd_f32", x, g, out)
+def add(a, b, out=None): return _binary("add", a, b, out)
+def sub(a, b, out=None): return _binary("sub", a, b, out)
+def mul(a, b, out=None): return _binary("mul", a, b, out)
+def div(a, b, out=None): return _binary("div", a, b, out)
+def neg(a, out=None): return _unary("neg", a, out)
+def relu(x, out=None): return _unary("relu", x, out)
+def sigmoid(x, out=None): return _unary("sigmoid", x, out)
+def tanh(x, out=None): return _unary("tanh", x, out)
+def sigmoid_bwd(s, g, out=None): return _binary("sigmoid_bwd", s, g, out)
+def tanh_bwd(t, g, out=None): return _binary("tanh_bwd", t, g, out)
+def relu_bwd(x, g, out=None): return _binary("relu_bwd", x, g, out)
 
 
 def add_row_bias(a: Tensor, bias: Tensor, out: Tensor | None = None) -> Tensor:
     """out[i, j] = a[i, j] + bias[j]: a bias shared by every row of a batch."""
     rows, cols = a.shape
-    out = out if out is not None else empty(a.shape, "f32")
-    call("cleave_hip_add_row_bias_f32", a.ptr, a.size, bias.ptr, bias.size, out.ptr, out.size, rows, cols)
+    sfx = _float_sfx(a, "add_row_bias")
+    out = out if out is not None else empty(a.shape, sfx)
+    call(f"cleave_hip_add_row_bias_{sfx}", a.ptr, a.size, bias.ptr, bias.size, out.ptr, out.size, rows, cols)
     return out
 
 
 def sum_rows(g: Tensor, out: Tensor | None = None) -> Tensor:
     """out[j] = sum_i g[i, j]: the reverse rule of add_row_bias."""
     rows, cols = g.shape
-    out = out if out is not None else empty((cols,), "f32")
-    call("cleave_hip_sum_rows_f32", g.ptr, g.size, out.ptr, out.size, rows, cols)
+    sfx = _float_sfx(g, "sum_rows")
+    out = out if out is not None else empty((cols,), sfx)
+    call(f"cleave_hip_sum_rows_{sfx}", g.ptr, g.size, out.ptr, out.size, rows, cols)
     return out
 
 
 def zero(shape_or_tensor) -> Tensor:
     """Ring::zero (stdlib/linalg/tensor.cleave:79)."""
     t = shape_or_tensor if isinstance(shape_or_tensor, Tensor) else empty(shape_or_tensor, "f32")
-    call("cleave_hip_zero_f32", t.ptr, t.size)
+    call(f"cleave_hip_zero_{_float_sfx(t, 'zero')}", t.ptr, t.size)
     return t
 
 
 def div_bwd(a: Tensor, b: Tensor, g: Tensor) -> tuple[Tensor, Tensor]:
-    da, db = empty(a.shape), empty(a.shape)
-    call("cleave_hip_div_bwd_f32", a.ptr, a.size, b.ptr, b.size, g.ptr, g.size, da.ptr, da.size,
+    sfx = _float_sfx(a, "div_bwd")
+    da, db = empty(a.shape, sfx), empty(a.shape, sfx)
+    call(f"cleave_hip_div_bwd_{sfx}", a.ptr, a.size, b.ptr, b.size, g.ptr, g.size, da.ptr, da.size,
          db.ptr, db.size)
     return da, db
 
 
 def sgd_update(w: Tensor, g: Tensor, lr: float) -> Tensor:
-    call("cleave_hip_sgd_update_f32", w.ptr, w.size, g.ptr, g.size, float(lr))
+    call(f"cleave_hip_sgd_update_{_float_sfx(w, 'sgd_update')}", w.ptr, w.size, g.ptr, g.size, float(lr))
     return w
 
 
 # ---- Sum / Mean / Max ----------------------------------------------------------
 
 def sum(t: Tensor) -> float:  # noqa: A001 - mirrors the stdlib name
-    _need(t, "f32", "sum")
-    return _checked_scalar("cleave_hip_sum_f32", t)
+    return _checked_scalar(f"cleave_hip_sum_{_float_sfx(t, 'sum')}", t)
 
 
 def mean(t: Tensor) -> float:
-    _need(t, "f32", "mean")
-    return _checked_scalar("cleave_hip_mean_f32", t)
+    return _checked_scalar(f"cleave_hip_mean_{_float_sfx(t, 'mean')}", t)
 
 
 def max_of(t: Tensor) -> float:
-    _need(t, "f32", "max_of")
-    return _checked_scalar("cleave_hip_max_of_f32", t)
+    return _checked_scalar(f"cleave_hip_max_of_{_float_sfx(t, 'max_of')}", t)
 
 
 def argmax(t: Tensor) -> int:
-    _need(t, "f32", "argmax")
-    return int(_checked_scalar("cleave_hip_argmax_f32", t))
+    return int(_checked_scalar(f"cleave_hip_argmax_{_float_sfx(t, 'argmax')}", t))
 
 
 def sum_u64(t: Tensor) -> int:
@@ -274,15 +280,13 @@ def sum_u64(t: Tensor) -> int:
 
 def reduce_sum(t: Tensor, out: Tensor) -> Tensor:
     """Queued sum into a device scalar (no synchronisation)."""
-    _need(t, "f32", "reduce_sum")
-    call("cleave_hip_reduce_sum_f32", t.ptr, t.size, out.ptr)
+    call(f"cleave_hip_reduce_sum_{_float_sfx(t, 'reduce_sum')}", t.ptr, t.size, out.ptr)
     return out
 
 
 def reduce_max(t: Tensor, out_max: Tensor | None, out_argmax: Tensor | None) -> None:
     """Queued max_of / argmax into device scalars (no synchronisation)."""
-    _need(t, "f32", "reduce_max")
-    call("cleave_hip_reduce_max_f32", t.ptr, t.size, out_max.ptr if out_max else None,
+    call(f"cleave_hip_reduce_max_{_float_sfx(t, 'reduce_max')}", t.ptr, t.size, out_max.ptr if out_max else None,
          out_argmax.ptr if out_argmax else None)
 
 
@@ -313,9 +317,10 @@ def _dims_idx(t: Tensor, idx):
 
 def index(t: Tensor, idx) -> float:
     """t[idx]: one index per dimension of t, row-major (Index::index)."""
-    _need(t, "f32", "index")
+    sfx = _float_sfx(t, "index")
     dims, ix = _dims_idx(t, idx)
-    v = load().cleave_hip_index_f32(t.ptr, t.size, dims.ctypes.data, dims.size, ix.ctypes.data, ix.size)
+    v = getattr(load(), f"cleave_hip_index_{sfx}")(t.ptr, t.size, dims.ctypes.data, dims.size, ix.ctypes.data,
+                                                     ix.size)
     code, msg = _lib.last_error()
     if code < 0:
         raise CleaveHipError(code, msg)
@@ -324,9 +329,9 @@ def index(t: Tensor, idx) -> float:
 
 def index_bwd(g: float, dt: Tensor, idx) -> Tensor:
     """Reverse mode of `derivative index(c, idx): index(d(c), idx)`: dt[idx] += g."""
-    _need(dt, "f32", "index_bwd")
+    sfx = _float_sfx(dt, "index_bwd")
     dims, ix = _dims_idx(dt, idx)
-    call("cleave_hip_index_bwd_f32", float(g), dt.ptr, dt.size, dims.ctypes.data, dims.size,
+    call(f"cleave_hip_index_bwd_{sfx}", float(g), dt.ptr, dt.size, dims.ctypes.data, dims.size,
          ix.ctypes.data, ix.size)
     return dt
 

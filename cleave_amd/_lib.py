@@ -33,7 +33,7 @@ u32p = C.POINTER(C.c_uint32)
 u64p = C.POINTER(C.c_uint64)
 i64p = C.POINTER(C.c_int64)
 vp = C.c_void_p
-i32, i64, u64, f32 = C.c_int32, C.c_int64, C.c_uint64, C.c_float
+i32, i64, u64, f32, f64 = C.c_int32, C.c_int64, C.c_uint64, C.c_float, C.c_double
 
 
 class Symbol(C.Structure):
@@ -144,6 +144,68 @@ SIGNATURES: dict[str, tuple] = {
     "cleave_hip_tanh_bwd_f32_into": (i64, [vp, i64, vp, i64, vp, i64]),
     "cleave_hip_relu_bwd_f32_into": (i64, [vp, i64, vp, i64, vp, i64]),
     "cleave_hip_escape_grid_i32": (i64, [vp, i64, i32, i32, f32, f32, f32, f32, i32]),
+    "cleave_hip_matmul_f64": (i32, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, i32]),
+    "cleave_hip_matmul_batched_f64": (i32, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, i32, i32]),
+    "cleave_hip_add_f64": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_sub_f64": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_mul_f64": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_div_f64": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_neg_f64": (i32, [vp, i64, vp, i64]),
+    "cleave_hip_zero_f64": (i32, [vp, i64]),
+    "cleave_hip_relu_f64": (i32, [vp, i64, vp, i64]),
+    "cleave_hip_sigmoid_f64": (i32, [vp, i64, vp, i64]),
+    "cleave_hip_tanh_f64": (i32, [vp, i64, vp, i64]),
+    "cleave_hip_sigmoid_bwd_f64": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_tanh_bwd_f64": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_relu_bwd_f64": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_div_bwd_f64": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_sgd_update_f64": (i32, [vp, i64, vp, i64, f64]),
+    "cleave_hip_add_row_bias_f64": (i32, [vp, i64, vp, i64, vp, i64, i32, i32]),
+    "cleave_hip_sum_rows_f64": (i32, [vp, i64, vp, i64, i32, i32]),
+    "cleave_hip_reduce_sum_f64": (i32, [vp, i64, vp]),
+    "cleave_hip_reduce_max_f64": (i32, [vp, i64, vp, vp]),
+    "cleave_hip_sum_f64": (f64, [vp, i64]),
+    "cleave_hip_mean_f64": (f64, [vp, i64]),
+    "cleave_hip_max_of_f64": (f64, [vp, i64]),
+    "cleave_hip_argmax_f64": (i64, [vp, i64]),
+    "cleave_hip_index_f64": (f64, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_index_bwd_f64": (i32, [f64, vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_matmul_f64_host": (i32, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, i32]),
+    "cleave_hip_matmul_batched_f64_host": (i32, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, i32, i32]),
+    "cleave_hip_add_f64_host": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_sub_f64_host": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_mul_f64_host": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_div_f64_host": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_neg_f64_host": (i32, [vp, i64, vp, i64]),
+    "cleave_hip_zero_f64_host": (i32, [vp, i64]),
+    "cleave_hip_relu_f64_host": (i32, [vp, i64, vp, i64]),
+    "cleave_hip_sigmoid_f64_host": (i32, [vp, i64, vp, i64]),
+    "cleave_hip_tanh_f64_host": (i32, [vp, i64, vp, i64]),
+    "cleave_hip_sigmoid_bwd_f64_host": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_tanh_bwd_f64_host": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_relu_bwd_f64_host": (i32, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_div_bwd_f64_host": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_sgd_update_f64_host": (i32, [vp, i64, vp, i64, f64]),
+    "cleave_hip_add_row_bias_f64_host": (i32, [vp, i64, vp, i64, vp, i64, i32, i32]),
+    "cleave_hip_sum_rows_f64_host": (i32, [vp, i64, vp, i64, i32, i32]),
+    "cleave_hip_sum_f64_host": (f64, [vp, i64]),
+    "cleave_hip_mean_f64_host": (f64, [vp, i64]),
+    "cleave_hip_max_of_f64_host": (f64, [vp, i64]),
+    "cleave_hip_argmax_f64_host": (i64, [vp, i64]),
+    "cleave_hip_index_f64_host": (f64, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_index_bwd_f64_host": (i32, [f64, vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_matmul_f64_into": (i64, [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, i32]),
+    "cleave_hip_add_f64_into": (i64, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_sub_f64_into": (i64, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_mul_f64_into": (i64, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_div_f64_into": (i64, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_neg_f64_into": (i64, [vp, i64, vp, i64]),
+    "cleave_hip_relu_f64_into": (i64, [vp, i64, vp, i64]),
+    "cleave_hip_sigmoid_f64_into": (i64, [vp, i64, vp, i64]),
+    "cleave_hip_tanh_f64_into": (i64, [vp, i64, vp, i64]),
+    "cleave_hip_sigmoid_bwd_f64_into": (i64, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_tanh_bwd_f64_into": (i64, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_relu_bwd_f64_into": (i64, [vp, i64, vp, i64, vp, i64]),
     # memref-descriptor forms: every tensor argument is a pointer to an
     # unranked descriptor {int64 rank; void* ranked descriptor}
     "_mlir_ciface_cleave_hip_matmul_f32": (i32, [vp, vp, vp]),
@@ -173,6 +235,24 @@ SIGNATURES: dict[str, tuple] = {
     "_mlir_ciface_cleave_hip_index_bwd_f32": (i32, [f32, vp, vp]),
     "_mlir_ciface_cleave_hip_mandelbrot_u32": (i32, [vp, f32, f32, f32, f32, i32]),
     "_mlir_ciface_cleave_hip_mlp_step_f32": (i32, [vp, vp, vp, vp, vp, vp, vp, f32]),
+    "_mlir_ciface_cleave_hip_matmul_f64": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_add_f64": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_sub_f64": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_mul_f64": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_div_f64": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_neg_f64": (i32, [vp, vp]),
+    "_mlir_ciface_cleave_hip_relu_f64": (i32, [vp, vp]),
+    "_mlir_ciface_cleave_hip_sigmoid_f64": (i32, [vp, vp]),
+    "_mlir_ciface_cleave_hip_tanh_f64": (i32, [vp, vp]),
+    "_mlir_ciface_cleave_hip_sigmoid_bwd_f64": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_tanh_bwd_f64": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_relu_bwd_f64": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_sum_f64": (f64, [vp]),
+    "_mlir_ciface_cleave_hip_mean_f64": (f64, [vp]),
+    "_mlir_ciface_cleave_hip_max_of_f64": (f64, [vp]),
+    "_mlir_ciface_cleave_hip_argmax_f64": (i64, [vp]),
+    "_mlir_ciface_cleave_hip_index_f64": (f64, [vp, vp]),
+    "_mlir_ciface_cleave_hip_index_bwd_f64": (i32, [f64, vp, vp]),
 }
 
 # Functions whose int32 return is a status code.

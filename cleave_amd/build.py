@@ -47,7 +47,7 @@ HIP_FLAGS = [
     "-Wno-unused-function",
     "-fvisibility=hidden",
 ]
-SOURCES = ["runtime.hip", "gemm_f32.hip", "gemm_bf16.hip", "gemv.hip", "elementwise.hip", "reduce.hip",
+SOURCES = ["runtime.hip", "gemm_f32.hip", "gemm_bf16.hip", "gemm_f64.hip", "gemv.hip", "elementwise.hip", "reduce.hip",
            "mandelbrot.hip", "mlp.hip", "index.hip", "broadcast.hip", "memref.cpp",
            "host.cpp", "symbols.cpp"]
 

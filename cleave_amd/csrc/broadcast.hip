@@ -1,4 +1,4 @@
-// broadcast.hip -- a bias shared by every row of a batch, and its reverse rule.
+// broadcast.hip -- a bias shared by every row of a batch, and its reverse rule (f32, f64).
 //
 // The reference adds a bias of the operand's own shape (examples/xor_tensor.cleave:44-49,
 // one example at a time: matmul(x, w) + b1 with both 1 x n), because Ring<Tensor>::add
@@ -17,23 +17,34 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kRowUnroll = 4;
-typedef float f4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ f4 ld4nt(const float* p) { return __builtin_nontemporal_load(reinterpret_cast<const f4*>(p)); }
-__device__ __forceinline__ void st4nt(float* p, f4 v) { __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p)); }
+// A 16-byte column chunk: 4 floats or 2 doubles.
+template <class T>
+struct Chunk {
+    static constexpr int kN = 16 / sizeof(T);
+    typedef T type __attribute__((ext_vector_type(kN)));
+};
+template <class T>
+__device__ __forceinline__ typename Chunk<T>::type ldnt(const T* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const typename Chunk<T>::type*>(p));
+}
+template <class T>
+__device__ __forceinline__ void stnt(T* p, typename Chunk<T>::type v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<typename Chunk<T>::type*>(p));
+}
 
 // Launch shape of both kernels: blockIdx.x = group * nseg + seg, where seg
 // picks kThreads column chunks and group a run of rows_per_group rows.
 struct Tiling {
-    int64_t cv = 0;          // 16-byte column chunks per row (cols / 4)
+    int64_t cv = 0;          // 16-byte column chunks per row (cols / elements per chunk)
     int64_t nseg = 0;        // column segments of kThreads chunks
     int64_t groups = 0;      // row groups
     int64_t rows_per_group = 0;
 };
 
-Tiling tiling_rows(int64_t rows, int64_t cols, int64_t rows_per_group) {
+Tiling tiling_rows(int64_t rows, int64_t cols, int64_t rows_per_group, int per_chunk) {
     Tiling t;
-    t.cv = cols / 4;
+    t.cv = cols / per_chunk;
     t.nseg = (t.cv + kThreads - 1) / kThreads;
     t.rows_per_group = rows_per_group < rows ? rows_per_group : rows;
     t.groups = (rows + t.rows_per_group - 1) / t.rows_per_group;
@@ -42,57 +53,60 @@ Tiling tiling_rows(int64_t rows, int64_t cols, int64_t rows_per_group) {
 // The bias add moves every element once, so short row groups (many blocks, as a
 // one-shot map) keep the most bytes in flight: 8 rows per block measured
 // 6.6 TB/s at 65536 x 4096 against 4.8 TB/s for 128.
-Tiling tiling_bias(int64_t rows, int64_t cols) { return tiling_rows(rows, cols, 8); }
+Tiling tiling_bias(int64_t rows, int64_t cols, int per_chunk) { return tiling_rows(rows, cols, 8, per_chunk); }
 // The column sums write one partial row per group, which the second stage
 // reads back; about four blocks per CU in the first stage measured best
 // (6.75 TB/s at 65536 x 4096, 256 groups).
-Tiling tiling_sum(int64_t rows, int64_t cols) {
-    const int64_t nseg = (cols / 4 + kThreads - 1) / kThreads;
+Tiling tiling_sum(int64_t rows, int64_t cols, int per_chunk) {
+    const int64_t nseg = (cols / per_chunk + kThreads - 1) / kThreads;
     int64_t groups = 4LL * ch::num_cus() / nseg;
     if (groups < 1) groups = 1;
     if (groups > rows) groups = rows;
-    return tiling_rows(rows, cols, (rows + groups - 1) / groups);
+    return tiling_rows(rows, cols, (rows + groups - 1) / groups, per_chunk);
 }
 
-__global__ __launch_bounds__(kThreads) void add_row_bias_kernel(const float* __restrict__ a,
-                                                                const float* __restrict__ bias,
-                                                                float* __restrict__ out, int64_t rows,
-                                                                int64_t cols, int64_t nseg, int64_t rpg) {
+template <class T>
+__global__ __launch_bounds__(kThreads) void add_row_bias_kernel(const T* __restrict__ a, const T* __restrict__ bias,
+                                                                T* __restrict__ out, int64_t rows, int64_t cols,
+                                                                int64_t nseg, int64_t rpg) {
+    typedef typename Chunk<T>::type V;
     const int64_t seg = blockIdx.x % nseg, group = blockIdx.x / nseg;
-    const int64_t c = (seg * kThreads + threadIdx.x) * 4;
+    const int64_t c = (seg * kThreads + threadIdx.x) * Chunk<T>::kN;
     if (c >= cols) return;
-    const f4 b = *reinterpret_cast<const f4*>(bias + c);
+    const V b = *reinterpret_cast<const V*>(bias + c);
     const int64_t r0 = group * rpg;
     const int64_t r1 = r0 + rpg < rows ? r0 + rpg : rows;
     int64_t r = r0;
     for (; r + kRowUnroll <= r1; r += kRowUnroll) {
-        f4 v[kRowUnroll];
+        V v[kRowUnroll];
 #pragma unroll
-        for (int u = 0; u < kRowUnroll; ++u) v[u] = ld4nt(a + (r + u) * cols + c);
+        for (int u = 0; u < kRowUnroll; ++u) v[u] = ldnt(a + (r + u) * cols + c);
 #pragma unroll
-        for (int u = 0; u < kRowUnroll; ++u) st4nt(out + (r + u) * cols + c, v[u] + b);
+        for (int u = 0; u < kRowUnroll; ++u) stnt(out + (r + u) * cols + c, v[u] + b);
     }
-    for (; r < r1; ++r) st4nt(out + r * cols + c, ld4nt(a + r * cols + c) + b);
+    for (; r < r1; ++r) stnt(out + r * cols + c, ldnt(a + r * cols + c) + b);
 }
 
-__global__ __launch_bounds__(kThreads) void sum_rows_stage1(const float* __restrict__ g, float* __restrict__ part,
+template <class T>
+__global__ __launch_bounds__(kThreads) void sum_rows_stage1(const T* __restrict__ g, T* __restrict__ part,
                                                             int64_t rows, int64_t cols, int64_t nseg, int64_t rpg) {
+    typedef typename Chunk<T>::type V;
     const int64_t seg = blockIdx.x % nseg, group = blockIdx.x / nseg;
-    const int64_t c = (seg * kThreads + threadIdx.x) * 4;
+    const int64_t c = (seg * kThreads + threadIdx.x) * Chunk<T>::kN;
     if (c >= cols) return;
     const int64_t r0 = group * rpg;
     const int64_t r1 = r0 + rpg < rows ? r0 + rpg : rows;
-    f4 acc = ld4nt(g + r0 * cols + c);
+    V acc = ldnt(g + r0 * cols + c);
     int64_t r = r0 + 1;
     for (; r + kRowUnroll <= r1; r += kRowUnroll) {
-        f4 v[kRowUnroll];
+        V v[kRowUnroll];
 #pragma unroll
-        for (int u = 0; u < kRowUnroll; ++u) v[u] = ld4nt(g + (r + u) * cols + c);
+        for (int u = 0; u < kRowUnroll; ++u) v[u] = ldnt(g + (r + u) * cols + c);
 #pragma unroll
         for (int u = 0; u < kRowUnroll; ++u) acc = acc + v[u];
     }
-    for (; r < r1; ++r) acc = acc + ld4nt(g + r * cols + c);
-    *reinterpret_cast<f4*>(part + group * cols + c) = acc;
+    for (; r < r1; ++r) acc = acc + ldnt(g + r * cols + c);
+    *reinterpret_cast<V*>(part + group * cols + c) = acc;
 }
 
 // out[j] = the sum of part[0..groups)[j].  Eight threads share a column:
@@ -104,18 +118,19 @@ __global__ __launch_bounds__(kThreads) void sum_rows_stage1(const float* __restr
 // per column, folding all 256 groups itself, left 16 blocks and took 12.4 us.
 constexpr int kGroupUnroll = 8;
 constexpr int kStage2Split = 8, kStage2Cols = kThreads / kStage2Split;
-__global__ __launch_bounds__(kThreads) void sum_rows_stage2(const float* __restrict__ part, float* __restrict__ out,
+template <class T>
+__global__ __launch_bounds__(kThreads) void sum_rows_stage2(const T* __restrict__ part, T* __restrict__ out,
                                                             int64_t groups, int64_t cols) {
-    __shared__ float red[kStage2Split][kStage2Cols];
+    __shared__ T red[kStage2Split][kStage2Cols];
     const int jj = threadIdx.x % kStage2Cols, s = threadIdx.x / kStage2Cols;
     const int64_t j = (int64_t)blockIdx.x * kStage2Cols + jj;
     const int64_t q0 = groups * s / kStage2Split, q1 = groups * (s + 1) / kStage2Split;
-    float acc = 0.0f;
+    T acc = T(0);
     if (j < cols && q0 < q1) {
         acc = part[q0 * cols + j];
         int64_t q = q0 + 1;
         for (; q + kGroupUnroll <= q1; q += kGroupUnroll) {
-            float v[kGroupUnroll];
+            T v[kGroupUnroll];
 #pragma unroll
             for (int u = 0; u < kGroupUnroll; ++u) v[u] = part[(q + u) * cols + j];
 #pragma unroll
@@ -130,7 +145,7 @@ __global__ __launch_bounds__(kThreads) void sum_rows_stage2(const float* __restr
         // groups < 8; the last one never is)
         int t = 0;
         while (groups * (t + 1) / kStage2Split == groups * t / kStage2Split) ++t;
-        float r = red[t][jj];
+        T r = red[t][jj];
         for (++t; t < kStage2Split; ++t)
             if (groups * (t + 1) / kStage2Split > groups * t / kStage2Split) r = r + red[t][jj];
         out[j] = r;
@@ -138,14 +153,16 @@ __global__ __launch_bounds__(kThreads) void sum_rows_stage2(const float* __restr
 }
 
 // Scalar forms for widths that are not a multiple of 4 or unaligned pointers.
-__global__ void add_row_bias_scalar(const float* a, const float* bias, float* out, int64_t rows, int64_t cols) {
+template <class T>
+__global__ void add_row_bias_scalar(const T* a, const T* bias, T* out, int64_t rows, int64_t cols) {
     const int64_t n = rows * cols;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
         out[i] = a[i] + bias[i % cols];
 }
-__global__ void sum_rows_scalar(const float* g, float* out, int64_t rows, int64_t cols) {
+template <class T>
+__global__ void sum_rows_scalar(const T* g, T* out, int64_t rows, int64_t cols) {
     for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < cols; j += (int64_t)gridDim.x * blockDim.x) {
-        float acc = g[j];
+        T acc = g[j];
         for (int64_t r = 1; r < rows; ++r) acc = acc + g[r * cols + j];
         out[j] = acc;
     }
@@ -159,13 +176,10 @@ unsigned blocks_for(int64_t n) {
     return (unsigned)(b < 1 ? 1 : b);
 }
 
-}  // namespace
-
-extern "C" {
-
-int32_t cleave_hip_add_row_bias_f32(const float* a, int64_t alen, const float* bias, int64_t blen, float* out,
-                                    int64_t outlen, int32_t rows, int32_t cols) {
-    const char* fn = "cleave_hip_add_row_bias_f32";
+template <class T>
+int32_t run_add_row_bias(const char* fn, const T* a, int64_t alen, const T* bias, int64_t blen, T* out,
+                         int64_t outlen, int32_t rows, int32_t cols) {
+    constexpr int V = Chunk<T>::kN;
     CH_REQUIRE(rows >= 0 && cols >= 0, "%s: negative shape (%d x %d)", fn, rows, cols);
     CH_REQUIRE(alen == (int64_t)rows * cols && outlen == alen, "%s: a/out lengths (%lld, %lld) != rows*cols %lld",
                fn, (long long)alen, (long long)outlen, (long long)rows * cols);
@@ -173,23 +187,23 @@ int32_t cleave_hip_add_row_bias_f32(const float* a, int64_t alen, const float* b
     if (alen == 0) return CLEAVE_HIP_OK;
     CH_REQUIRE(a && bias && out, "%s: null buffer", fn);
     CH_INIT_OR_RETURN();
-    CH_DEVICE(fn, a, alen * 4);
-    CH_DEVICE(fn, bias, blen * 4);
-    CH_DEVICE(fn, out, outlen * 4);
-    if (cols % 4 == 0 && aligned16(a) && aligned16(bias) && aligned16(out)) {
-        const Tiling t = tiling_bias(rows, cols);
-        add_row_bias_kernel<<<(unsigned)(t.nseg * t.groups), kThreads, 0, ch::stream()>>>(
+    CH_DEVICE(fn, a, alen * sizeof(T));
+    CH_DEVICE(fn, bias, blen * sizeof(T));
+    CH_DEVICE(fn, out, outlen * sizeof(T));
+    if (cols % V == 0 && aligned16(a) && aligned16(bias) && aligned16(out)) {
+        const Tiling t = tiling_bias(rows, cols, V);
+        add_row_bias_kernel<T><<<(unsigned)(t.nseg * t.groups), kThreads, 0, ch::stream()>>>(
             a, bias, out, rows, cols, t.nseg, t.rows_per_group);
     } else {
-        add_row_bias_scalar<<<blocks_for(alen), kThreads, 0, ch::stream()>>>(a, bias, out, rows, cols);
+        add_row_bias_scalar<T><<<blocks_for(alen), kThreads, 0, ch::stream()>>>(a, bias, out, rows, cols);
     }
     CH_LAUNCHED(fn);
     return CLEAVE_HIP_OK;
 }
 
-int32_t cleave_hip_sum_rows_f32(const float* g, int64_t glen, float* out, int64_t outlen, int32_t rows,
-                                int32_t cols) {
-    const char* fn = "cleave_hip_sum_rows_f32";
+template <class T>
+int32_t run_sum_rows(const char* fn, const T* g, int64_t glen, T* out, int64_t outlen, int32_t rows, int32_t cols) {
+    constexpr int V = Chunk<T>::kN;
     CH_REQUIRE(rows >= 1 && cols >= 0, "%s: need at least one row (%d x %d)", fn, rows, cols);
     CH_REQUIRE(glen == (int64_t)rows * cols, "%s: g length %lld != rows*cols %lld", fn, (long long)glen,
                (long long)rows * cols);
@@ -197,22 +211,46 @@ int32_t cleave_hip_sum_rows_f32(const float* g, int64_t glen, float* out, int64_
     if (cols == 0) return CLEAVE_HIP_OK;
     CH_REQUIRE(g && out, "%s: null buffer", fn);
     CH_INIT_OR_RETURN();
-    CH_DEVICE(fn, g, glen * 4);
-    CH_DEVICE(fn, out, outlen * 4);
-    if (cols % 4 == 0 && aligned16(g)) {
-        const Tiling t = tiling_sum(rows, cols);
-        float* part = (float*)ch::scratch(5, sizeof(float) * (size_t)(t.groups * cols));
-        if (!part) return ch::fail(CLEAVE_HIP_ERR_OOM, "%s: scratch of %lld floats", fn, (long long)(t.groups * cols));
-        sum_rows_stage1<<<(unsigned)(t.nseg * t.groups), kThreads, 0, ch::stream()>>>(g, part, rows, cols, t.nseg,
-                                                                                       t.rows_per_group);
+    CH_DEVICE(fn, g, glen * sizeof(T));
+    CH_DEVICE(fn, out, outlen * sizeof(T));
+    if (cols % V == 0 && aligned16(g)) {
+        const Tiling t = tiling_sum(rows, cols, V);
+        T* part = (T*)ch::scratch(5, sizeof(T) * (size_t)(t.groups * cols));
+        if (!part) return ch::fail(CLEAVE_HIP_ERR_OOM, "%s: scratch of %lld elements", fn, (long long)(t.groups * cols));
+        sum_rows_stage1<T><<<(unsigned)(t.nseg * t.groups), kThreads, 0, ch::stream()>>>(g, part, rows, cols, t.nseg,
+                                                                                          t.rows_per_group);
         CH_LAUNCHED(fn);
-        sum_rows_stage2<<<(unsigned)((cols + kStage2Cols - 1) / kStage2Cols), kThreads, 0, ch::stream()>>>(
+        sum_rows_stage2<T><<<(unsigned)((cols + kStage2Cols - 1) / kStage2Cols), kThreads, 0, ch::stream()>>>(
             part, out, t.groups, cols);
     } else {
-        sum_rows_scalar<<<blocks_for(cols), kThreads, 0, ch::stream()>>>(g, out, rows, cols);
+        sum_rows_scalar<T><<<blocks_for(cols), kThreads, 0, ch::stream()>>>(g, out, rows, cols);
     }
     CH_LAUNCHED(fn);
     return CLEAVE_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t cleave_hip_add_row_bias_f32(const float* a, int64_t alen, const float* bias, int64_t blen, float* out,
+                                    int64_t outlen, int32_t rows, int32_t cols) {
+    return run_add_row_bias<float>("cleave_hip_add_row_bias_f32", a, alen, bias, blen, out, outlen, rows, cols);
+}
+
+int32_t cleave_hip_sum_rows_f32(const float* g, int64_t glen, float* out, int64_t outlen, int32_t rows,
+                                int32_t cols) {
+    return run_sum_rows<float>("cleave_hip_sum_rows_f32", g, glen, out, outlen, rows, cols);
+}
+
+int32_t cleave_hip_add_row_bias_f64(const double* a, int64_t alen, const double* bias, int64_t blen, double* out,
+                                    int64_t outlen, int32_t rows, int32_t cols) {
+    return run_add_row_bias<double>("cleave_hip_add_row_bias_f64", a, alen, bias, blen, out, outlen, rows, cols);
+}
+
+int32_t cleave_hip_sum_rows_f64(const double* g, int64_t glen, double* out, int64_t outlen, int32_t rows,
+                                int32_t cols) {
+    return run_sum_rows<double>("cleave_hip_sum_rows_f64", g, glen, out, outlen, rows, cols);
 }
 
 }  // extern "C"

@@ -306,24 +306,38 @@ class Staged {
     bool staged_ = false;
 };
 
-using Map1 = int32_t (*)(const float*, int64_t, float*, int64_t);
-using Map2 = int32_t (*)(const float*, int64_t, const float*, int64_t, float*, int64_t);
-
-int32_t map1_host(const char* fn, Map1 f, const float* a, int64_t alen, float* out, int64_t outlen) {
-    Staged s(fn);
-    const int ia = s.in(a, alen, 4), io = s.out(out, outlen, 4);
-    int32_t st = s.stage();
-    if (st != CLEAVE_HIP_OK) return st;
-    return s.finish(f(s.dev<float>(ia), alen, s.dev<float>(io), outlen));
-}
-
-int32_t map2_host(const char* fn, Map2 f, const float* a, int64_t alen, const float* b, int64_t blen, float* out,
+template <class T>
+int32_t map1_host(const char* fn, int32_t (*f)(const T*, int64_t, T*, int64_t), const T* a, int64_t alen, T* out,
                   int64_t outlen) {
     Staged s(fn);
-    const int ia = s.in(a, alen, 4), ib = s.in(b, blen, 4), io = s.out(out, outlen, 4);
+    const int ia = s.in(a, alen, sizeof(T)), io = s.out(out, outlen, sizeof(T));
     int32_t st = s.stage();
     if (st != CLEAVE_HIP_OK) return st;
-    return s.finish(f(s.dev<float>(ia), alen, s.dev<float>(ib), blen, s.dev<float>(io), outlen));
+    return s.finish(f(s.dev<T>(ia), alen, s.dev<T>(io), outlen));
+}
+
+template <class T>
+int32_t map2_host(const char* fn, int32_t (*f)(const T*, int64_t, const T*, int64_t, T*, int64_t), const T* a,
+                  int64_t alen, const T* b, int64_t blen, T* out, int64_t outlen) {
+    Staged s(fn);
+    const int ia = s.in(a, alen, sizeof(T)), ib = s.in(b, blen, sizeof(T)), io = s.out(out, outlen, sizeof(T));
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(f(s.dev<T>(ia), alen, s.dev<T>(ib), blen, s.dev<T>(io), outlen));
+}
+
+// The matmul host forms: A and B staged in, C staged out.
+template <class TA, class TC>
+int32_t matmul_host(const char* fn,
+                    int32_t (*f)(const TA*, int64_t, const TA*, int64_t, TC*, int64_t, int32_t, int32_t, int32_t,
+                                 int32_t, int32_t, int32_t),
+                    const TA* a, int64_t alen, const TA* b, int64_t blen, TC* c, int64_t clen, int32_t batch,
+                    int32_t M, int32_t N, int32_t K, int32_t trans_a, int32_t trans_b) {
+    Staged s(fn);
+    const int ia = s.in(a, alen, sizeof(TA)), ib = s.in(b, blen, sizeof(TA)), ic = s.out(c, clen, sizeof(TC));
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(f(s.dev<TA>(ia), alen, s.dev<TA>(ib), blen, s.dev<TC>(ic), clen, batch, M, N, K, trans_a, trans_b));
 }
 
 // Scalar-returning reductions: stage x, then call the device form (which
@@ -360,12 +374,8 @@ int32_t cleave_hip_matmul_f32_host(const float* a, int64_t alen, const float* b,
 int32_t cleave_hip_matmul_batched_f32_host(const float* a, int64_t alen, const float* b, int64_t blen, float* c,
                                            int64_t clen, int32_t batch, int32_t M, int32_t N, int32_t K,
                                            int32_t trans_a, int32_t trans_b) {
-    Staged s("cleave_hip_matmul_batched_f32_host");
-    const int ia = s.in(a, alen, 4), ib = s.in(b, blen, 4), ic = s.out(c, clen, 4);
-    int32_t st = s.stage();
-    if (st != CLEAVE_HIP_OK) return st;
-    return s.finish(cleave_hip_matmul_batched_f32(s.dev<float>(ia), alen, s.dev<float>(ib), blen,
-                                                  s.dev<float>(ic), clen, batch, M, N, K, trans_a, trans_b));
+    return matmul_host<float, float>("cleave_hip_matmul_batched_f32_host", &cleave_hip_matmul_batched_f32, a, alen, b,
+                                     blen, c, clen, batch, M, N, K, trans_a, trans_b);
 }
 
 int32_t cleave_hip_matmul_bf16_host(const uint16_t* a, int64_t alen, const uint16_t* b, int64_t blen, float* c,
@@ -382,37 +392,56 @@ int32_t cleave_hip_matmul_bf16_host(const uint16_t* a, int64_t alen, const uint1
 int32_t cleave_hip_matmul_batched_bf16_host(const uint16_t* a, int64_t alen, const uint16_t* b, int64_t blen,
                                             float* c, int64_t clen, int32_t batch, int32_t M, int32_t N,
                                             int32_t K, int32_t trans_a, int32_t trans_b) {
-    Staged s("cleave_hip_matmul_batched_bf16_host");
-    const int ia = s.in(a, alen, 2), ib = s.in(b, blen, 2), ic = s.out(c, clen, 4);
-    int32_t st = s.stage();
-    if (st != CLEAVE_HIP_OK) return st;
-    return s.finish(cleave_hip_matmul_batched_bf16(s.dev<uint16_t>(ia), alen, s.dev<uint16_t>(ib), blen,
-                                                   s.dev<float>(ic), clen, batch, M, N, K, trans_a, trans_b));
+    return matmul_host<uint16_t, float>("cleave_hip_matmul_batched_bf16_host", &cleave_hip_matmul_batched_bf16, a,
+                                        alen, b, blen, c, clen, batch, M, N, K, trans_a, trans_b);
+}
+
+int32_t cleave_hip_matmul_f64_host(const double* a, int64_t alen, const double* b, int64_t blen, double* c,
+                                   int64_t clen, int32_t M, int32_t N, int32_t K, int32_t trans_a, int32_t trans_b) {
+    return matmul_host<double, double>("cleave_hip_matmul_f64_host", &cleave_hip_matmul_batched_f64, a, alen, b, blen,
+                                       c, clen, 1, M, N, K, trans_a, trans_b);
+}
+
+int32_t cleave_hip_matmul_batched_f64_host(const double* a, int64_t alen, const double* b, int64_t blen, double* c,
+                                           int64_t clen, int32_t batch, int32_t M, int32_t N, int32_t K,
+                                           int32_t trans_a, int32_t trans_b) {
+    return matmul_host<double, double>("cleave_hip_matmul_batched_f64_host", &cleave_hip_matmul_batched_f64, a, alen,
+                                       b, blen, c, clen, batch, M, N, K, trans_a, trans_b);
 }
 
 // ---- Ring<Tensor>, Activation<Tensor>, backward maps ------------------------------
 
-#define CH_MAP2_HOST(name)                                                                                   \
-    int32_t name##_host(const float* a, int64_t alen, const float* b, int64_t blen, float* out,          \
-                        int64_t outlen) {                                                                 \
-        return map2_host(#name "_host", &name, a, alen, b, blen, out, outlen);                            \
+#define CH_MAP2_HOST(name, T)                                                                                \
+    int32_t name##_host(const T* a, int64_t alen, const T* b, int64_t blen, T* out, int64_t outlen) {     \
+        return map2_host<T>(#name "_host", &name, a, alen, b, blen, out, outlen);                          \
     }
-#define CH_MAP1_HOST(name)                                                                                   \
-    int32_t name##_host(const float* a, int64_t alen, float* out, int64_t outlen) {                       \
-        return map1_host(#name "_host", &name, a, alen, out, outlen);                                     \
+#define CH_MAP1_HOST(name, T)                                                                                \
+    int32_t name##_host(const T* a, int64_t alen, T* out, int64_t outlen) {                                \
+        return map1_host<T>(#name "_host", &name, a, alen, out, outlen);                                   \
     }
 
-CH_MAP2_HOST(cleave_hip_add_f32)
-CH_MAP2_HOST(cleave_hip_sub_f32)
-CH_MAP2_HOST(cleave_hip_mul_f32)
-CH_MAP2_HOST(cleave_hip_div_f32)
-CH_MAP1_HOST(cleave_hip_neg_f32)
-CH_MAP1_HOST(cleave_hip_relu_f32)
-CH_MAP1_HOST(cleave_hip_sigmoid_f32)
-CH_MAP1_HOST(cleave_hip_tanh_f32)
-CH_MAP2_HOST(cleave_hip_sigmoid_bwd_f32)
-CH_MAP2_HOST(cleave_hip_tanh_bwd_f32)
-CH_MAP2_HOST(cleave_hip_relu_bwd_f32)
+CH_MAP2_HOST(cleave_hip_add_f32, float)
+CH_MAP2_HOST(cleave_hip_sub_f32, float)
+CH_MAP2_HOST(cleave_hip_mul_f32, float)
+CH_MAP2_HOST(cleave_hip_div_f32, float)
+CH_MAP1_HOST(cleave_hip_neg_f32, float)
+CH_MAP1_HOST(cleave_hip_relu_f32, float)
+CH_MAP1_HOST(cleave_hip_sigmoid_f32, float)
+CH_MAP1_HOST(cleave_hip_tanh_f32, float)
+CH_MAP2_HOST(cleave_hip_sigmoid_bwd_f32, float)
+CH_MAP2_HOST(cleave_hip_tanh_bwd_f32, float)
+CH_MAP2_HOST(cleave_hip_relu_bwd_f32, float)
+CH_MAP2_HOST(cleave_hip_add_f64, double)
+CH_MAP2_HOST(cleave_hip_sub_f64, double)
+CH_MAP2_HOST(cleave_hip_mul_f64, double)
+CH_MAP2_HOST(cleave_hip_div_f64, double)
+CH_MAP1_HOST(cleave_hip_neg_f64, double)
+CH_MAP1_HOST(cleave_hip_relu_f64, double)
+CH_MAP1_HOST(cleave_hip_sigmoid_f64, double)
+CH_MAP1_HOST(cleave_hip_tanh_f64, double)
+CH_MAP2_HOST(cleave_hip_sigmoid_bwd_f64, double)
+CH_MAP2_HOST(cleave_hip_tanh_bwd_f64, double)
+CH_MAP2_HOST(cleave_hip_relu_bwd_f64, double)
 
 int32_t cleave_hip_zero_f32_host(float* out, int64_t outlen) {
     Staged s("cleave_hip_zero_f32_host");
@@ -460,6 +489,52 @@ int32_t cleave_hip_sum_rows_f32_host(const float* g, int64_t glen, float* out, i
     return s.finish(cleave_hip_sum_rows_f32(s.dev<float>(ig), glen, s.dev<float>(io), outlen, rows, cols));
 }
 
+int32_t cleave_hip_zero_f64_host(double* out, int64_t outlen) {
+    Staged s("cleave_hip_zero_f64_host");
+    const int io = s.out(out, outlen, 8);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_zero_f64(s.dev<double>(io), outlen));
+}
+
+int32_t cleave_hip_div_bwd_f64_host(const double* a, int64_t alen, const double* b, int64_t blen, const double* g,
+                                    int64_t glen, double* da, int64_t dalen, double* db, int64_t dblen) {
+    Staged s("cleave_hip_div_bwd_f64_host");
+    const int ia = s.in(a, alen, 8), ib = s.in(b, blen, 8), ig = s.in(g, glen, 8);
+    const int ida = s.out(da, dalen, 8), idb = s.out(db, dblen, 8);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_div_bwd_f64(s.dev<double>(ia), alen, s.dev<double>(ib), blen, s.dev<double>(ig), glen,
+                                           s.dev<double>(ida), dalen, s.dev<double>(idb), dblen));
+}
+
+int32_t cleave_hip_sgd_update_f64_host(double* w, int64_t wlen, const double* g, int64_t glen, double lr) {
+    Staged s("cleave_hip_sgd_update_f64_host");
+    const int iw = s.inout(w, wlen, 8), ig = s.in(g, glen, 8);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_sgd_update_f64(s.dev<double>(iw), wlen, s.dev<double>(ig), glen, lr));
+}
+
+int32_t cleave_hip_add_row_bias_f64_host(const double* a, int64_t alen, const double* bias, int64_t blen,
+                                         double* out, int64_t outlen, int32_t rows, int32_t cols) {
+    Staged s("cleave_hip_add_row_bias_f64_host");
+    const int ia = s.in(a, alen, 8), ib = s.in(bias, blen, 8), io = s.out(out, outlen, 8);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_add_row_bias_f64(s.dev<double>(ia), alen, s.dev<double>(ib), blen,
+                                                s.dev<double>(io), outlen, rows, cols));
+}
+
+int32_t cleave_hip_sum_rows_f64_host(const double* g, int64_t glen, double* out, int64_t outlen, int32_t rows,
+                                     int32_t cols) {
+    Staged s("cleave_hip_sum_rows_f64_host");
+    const int ig = s.in(g, glen, 8), io = s.out(out, outlen, 8);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_sum_rows_f64(s.dev<double>(ig), glen, s.dev<double>(io), outlen, rows, cols));
+}
+
 // ---- Sum / Mean / Max ----------------------------------------------------------
 
 float cleave_hip_sum_f32_host(const float* x, int64_t len) {
@@ -486,6 +561,22 @@ int64_t cleave_hip_sum_i32_i64_host(const int32_t* x, int64_t len) {
     return reduce_host<int64_t, int32_t>("cleave_hip_sum_i32_i64_host", &cleave_hip_sum_i32_i64, x, len, 0);
 }
 
+double cleave_hip_sum_f64_host(const double* x, int64_t len) {
+    return reduce_host<double, double>("cleave_hip_sum_f64_host", &cleave_hip_sum_f64, x, len, NAN);
+}
+
+double cleave_hip_mean_f64_host(const double* x, int64_t len) {
+    return reduce_host<double, double>("cleave_hip_mean_f64_host", &cleave_hip_mean_f64, x, len, NAN);
+}
+
+double cleave_hip_max_of_f64_host(const double* x, int64_t len) {
+    return reduce_host<double, double>("cleave_hip_max_of_f64_host", &cleave_hip_max_of_f64, x, len, NAN);
+}
+
+int64_t cleave_hip_argmax_f64_host(const double* x, int64_t len) {
+    return reduce_host<int64_t, double>("cleave_hip_argmax_f64_host", &cleave_hip_argmax_f64, x, len, -1);
+}
+
 // ---- Index<Tensor> ---------------------------------------------------------------
 
 float cleave_hip_index_f32_host(const float* t, int64_t len, const int32_t* dims, int64_t ndims,
@@ -507,6 +598,27 @@ int32_t cleave_hip_index_bwd_f32_host(float g, float* dt, int64_t len, const int
     int32_t st = s.stage();
     if (st != CLEAVE_HIP_OK) return st;
     return s.finish(cleave_hip_index_bwd_f32(g, s.dev<float>(it), len, dims, ndims, idx, nidx));
+}
+
+double cleave_hip_index_f64_host(const double* t, int64_t len, const int32_t* dims, int64_t ndims,
+                                 const int32_t* idx, int64_t nidx) {
+    ch::clear_error();
+    Staged s("cleave_hip_index_f64_host");
+    const int it = s.in(t, len, 8);
+    if (s.stage() != CLEAVE_HIP_OK) return NAN;
+    const double v = cleave_hip_index_f64(s.dev<double>(it), len, dims, ndims, idx, nidx);
+    const int32_t err = cleave_hip_last_error();
+    if (s.finish(CLEAVE_HIP_OK) != CLEAVE_HIP_OK || err != CLEAVE_HIP_OK) return NAN;
+    return v;
+}
+
+int32_t cleave_hip_index_bwd_f64_host(double g, double* dt, int64_t len, const int32_t* dims, int64_t ndims,
+                                      const int32_t* idx, int64_t nidx) {
+    Staged s("cleave_hip_index_bwd_f64_host");
+    const int it = s.inout(dt, len, 8);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_index_bwd_f64(g, s.dev<double>(it), len, dims, ndims, idx, nidx));
 }
 
 // ---- escape_count map ---------------------------------------------------------------
@@ -560,27 +672,36 @@ int64_t cleave_hip_matmul_f32_into(float* c, int64_t clen, const float* a, int64
     CH_INTO_RESULT(cleave_hip_matmul_f32_host(a, alen, b, blen, c, clen, M, N, K, trans_a, trans_b), clen);
 }
 
-#define CH_MAP2_INTO(op)                                                                                  \
-    int64_t cleave_hip_##op##_f32_into(float* out, int64_t outlen, const float* a, int64_t alen,       \
-                                       const float* b, int64_t blen) {                                  \
-        CH_INTO_RESULT(cleave_hip_##op##_f32_host(a, alen, b, blen, out, outlen), outlen);             \
-    }
-#define CH_MAP1_INTO(op)                                                                                  \
-    int64_t cleave_hip_##op##_f32_into(float* out, int64_t outlen, const float* x, int64_t xlen) {      \
-        CH_INTO_RESULT(cleave_hip_##op##_f32_host(x, xlen, out, outlen), outlen);                      \
-    }
+int64_t cleave_hip_matmul_f64_into(double* c, int64_t clen, const double* a, int64_t alen, const double* b,
+                                   int64_t blen, int32_t M, int32_t N, int32_t K, int32_t trans_a,
+                                   int32_t trans_b) {
+    CH_INTO_RESULT(cleave_hip_matmul_f64_host(a, alen, b, blen, c, clen, M, N, K, trans_a, trans_b), clen);
+}
 
-CH_MAP2_INTO(add)
-CH_MAP2_INTO(sub)
-CH_MAP2_INTO(mul)
-CH_MAP2_INTO(div)
-CH_MAP1_INTO(neg)
-CH_MAP1_INTO(relu)
-CH_MAP1_INTO(sigmoid)
-CH_MAP1_INTO(tanh)
-CH_MAP2_INTO(sigmoid_bwd)
-CH_MAP2_INTO(tanh_bwd)
-CH_MAP2_INTO(relu_bwd)
+#define CH_MAP2_INTO(op, T, sfx)                                                                          \
+    int64_t cleave_hip_##op##_##sfx##_into(T* out, int64_t outlen, const T* a, int64_t alen, const T* b, \
+                                           int64_t blen) {                                              \
+        CH_INTO_RESULT(cleave_hip_##op##_##sfx##_host(a, alen, b, blen, out, outlen), outlen);         \
+    }
+#define CH_MAP1_INTO(op, T, sfx)                                                                          \
+    int64_t cleave_hip_##op##_##sfx##_into(T* out, int64_t outlen, const T* x, int64_t xlen) {          \
+        CH_INTO_RESULT(cleave_hip_##op##_##sfx##_host(x, xlen, out, outlen), outlen);                  \
+    }
+#define CH_INTO_ENTRIES(T, sfx) \
+    CH_MAP2_INTO(add, T, sfx)   \
+    CH_MAP2_INTO(sub, T, sfx)   \
+    CH_MAP2_INTO(mul, T, sfx)   \
+    CH_MAP2_INTO(div, T, sfx)   \
+    CH_MAP1_INTO(neg, T, sfx)   \
+    CH_MAP1_INTO(relu, T, sfx)  \
+    CH_MAP1_INTO(sigmoid, T, sfx) \
+    CH_MAP1_INTO(tanh, T, sfx)  \
+    CH_MAP2_INTO(sigmoid_bwd, T, sfx) \
+    CH_MAP2_INTO(tanh_bwd, T, sfx) \
+    CH_MAP2_INTO(relu_bwd, T, sfx)
+
+CH_INTO_ENTRIES(float, f32)
+CH_INTO_ENTRIES(double, f64)
 
 // Escape counts as cleave's i32 (escape_count returns i32,
 // examples/mandelbrot.cleave:14): counts are at most max_iter < 2^31, so the

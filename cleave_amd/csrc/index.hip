@@ -1,4 +1,4 @@
-// index.hip -- Index<Tensor>::index (stdlib/linalg/tensor.cleave:113-133) and
+// index.hip -- Index<Tensor>::index (stdlib/linalg/tensor.cleave:113-133), f32 and f64, and
 // the reverse-mode form of its derivative rule `index(d(c), idx)`.
 //
 // `idx` and the tensor's `dims` arrive as (pointer, length) pairs of host
@@ -31,7 +31,39 @@ int32_t flat_offset(const char* fn, int64_t len, const int32_t* dims, int64_t nd
     return CLEAVE_HIP_OK;
 }
 
-__global__ void scatter_add_kernel(float* __restrict__ dt, int64_t off, float g) { dt[off] = dt[off] + g; }
+template <class T>
+__global__ void scatter_add_kernel(T* __restrict__ dt, int64_t off, T g) { dt[off] = dt[off] + g; }
+
+template <class T>
+T run_index(const char* fn, const T* t, int64_t len, const int32_t* dims, int64_t ndims, const int32_t* idx,
+            int64_t nidx) {
+    ch::clear_error();
+    int64_t off = 0;
+    if (!t) {
+        ch::fail(CLEAVE_HIP_ERR_ARG, "%s: null tensor", fn);
+        return NAN;
+    }
+    if (flat_offset(fn, len, dims, ndims, idx, nidx, &off) != CLEAVE_HIP_OK) return NAN;
+    if (ch::ensure_init() != CLEAVE_HIP_OK) return NAN;
+    if (ch::require_device(fn, "t", t, (uint64_t)len * sizeof(T)) != CLEAVE_HIP_OK) return NAN;
+    T v = NAN;
+    if (cleave_hip_download(&v, t + off, sizeof(T)) != (int64_t)sizeof(T)) return NAN;
+    return v;
+}
+
+template <class T>
+int32_t run_index_bwd(const char* fn, T g, T* dt, int64_t len, const int32_t* dims, int64_t ndims,
+                      const int32_t* idx, int64_t nidx) {
+    CH_REQUIRE(dt != nullptr, "%s: null gradient buffer", fn);
+    int64_t off = 0;
+    const int32_t st = flat_offset(fn, len, dims, ndims, idx, nidx, &off);
+    if (st != CLEAVE_HIP_OK) return st;
+    CH_INIT_OR_RETURN();
+    CH_DEVICE(fn, dt, len * sizeof(T));
+    scatter_add_kernel<T><<<1, 1, 0, ch::stream()>>>(dt, off, g);
+    CH_LAUNCHED("scatter_add_kernel");
+    return CLEAVE_HIP_OK;
+}
 
 }  // namespace
 
@@ -39,31 +71,22 @@ extern "C" {
 
 float cleave_hip_index_f32(const float* t, int64_t len, const int32_t* dims, int64_t ndims,
                            const int32_t* idx, int64_t nidx) {
-    ch::clear_error();
-    int64_t off = 0;
-    if (!t) {
-        ch::fail(CLEAVE_HIP_ERR_ARG, "cleave_hip_index_f32: null tensor");
-        return NAN;
-    }
-    if (flat_offset("cleave_hip_index_f32", len, dims, ndims, idx, nidx, &off) != CLEAVE_HIP_OK) return NAN;
-    if (ch::ensure_init() != CLEAVE_HIP_OK) return NAN;
-    if (ch::require_device("cleave_hip_index_f32", "t", t, (uint64_t)len * 4) != CLEAVE_HIP_OK) return NAN;
-    float v = NAN;
-    if (cleave_hip_download(&v, t + off, sizeof(float)) != (int64_t)sizeof(float)) return NAN;
-    return v;
+    return run_index<float>("cleave_hip_index_f32", t, len, dims, ndims, idx, nidx);
 }
 
 int32_t cleave_hip_index_bwd_f32(float g, float* dt, int64_t len, const int32_t* dims, int64_t ndims,
                                  const int32_t* idx, int64_t nidx) {
-    CH_REQUIRE(dt != nullptr, "cleave_hip_index_bwd_f32: null gradient buffer");
-    int64_t off = 0;
-    const int32_t st = flat_offset("cleave_hip_index_bwd_f32", len, dims, ndims, idx, nidx, &off);
-    if (st != CLEAVE_HIP_OK) return st;
-    CH_INIT_OR_RETURN();
-    CH_DEVICE("cleave_hip_index_bwd_f32", dt, len * 4);
-    scatter_add_kernel<<<1, 1, 0, ch::stream()>>>(dt, off, g);
-    CH_LAUNCHED("scatter_add_kernel");
-    return CLEAVE_HIP_OK;
+    return run_index_bwd<float>("cleave_hip_index_bwd_f32", g, dt, len, dims, ndims, idx, nidx);
+}
+
+double cleave_hip_index_f64(const double* t, int64_t len, const int32_t* dims, int64_t ndims,
+                            const int32_t* idx, int64_t nidx) {
+    return run_index<double>("cleave_hip_index_f64", t, len, dims, ndims, idx, nidx);
+}
+
+int32_t cleave_hip_index_bwd_f64(double g, double* dt, int64_t len, const int32_t* dims, int64_t ndims,
+                                 const int32_t* idx, int64_t nidx) {
+    return run_index_bwd<double>("cleave_hip_index_bwd_f64", g, dt, len, dims, ndims, idx, nidx);
 }
 
 }  // extern "C"

@@ -106,14 +106,22 @@ int32_t narrow(int64_t x, const char* fn, const char* what, int32_t* out) {
         if (_st != CLEAVE_HIP_OK) return _st;         \
     } while (0)
 
-template <bool BF16>
-int32_t matmul_mr(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr c, const char* fn) {
-    const int esz = BF16 ? 2 : 4;
+// Pointer forms of one product element type: the single and the batched one.
+template <class TA, class TC>
+struct MatmulFns {
+    int32_t (*single)(const TA*, int64_t, const TA*, int64_t, TC*, int64_t, int32_t, int32_t, int32_t, int32_t,
+                      int32_t);
+    int32_t (*batched)(const TA*, int64_t, const TA*, int64_t, TC*, int64_t, int32_t, int32_t, int32_t, int32_t,
+                       int32_t, int32_t);
+};
+
+template <class TA, class TC>
+int32_t matmul_mr(MatmulFns<TA, TC> f, cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr c, const char* fn) {
     View A, B, C;
     int ta = 0, tb = 0, tc = 0;
-    CH_TRY(mat_view(a, esz, fn, "a", &A, &ta));
-    CH_TRY(mat_view(b, esz, fn, "b", &B, &tb));
-    CH_TRY(mat_view(c, 4, fn, "c", &C, &tc));
+    CH_TRY(mat_view(a, sizeof(TA), fn, "a", &A, &ta));
+    CH_TRY(mat_view(b, sizeof(TA), fn, "b", &B, &tb));
+    CH_TRY(mat_view(c, sizeof(TC), fn, "c", &C, &tc));
     CH_REQUIRE(A.rank == B.rank && B.rank == C.rank, "%s: operand ranks differ (%lld, %lld, %lld)", fn,
                (long long)A.rank, (long long)B.rank, (long long)C.rank);
     CH_REQUIRE(tc == 0, "%s: c must be row-major", fn);
@@ -127,46 +135,41 @@ int32_t matmul_mr(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr c, const char*
     CH_TRY(narrow(M, fn, "M", &m32));
     CH_TRY(narrow(N, fn, "N", &n32));
     CH_TRY(narrow(K, fn, "K", &k32));
-    if (r == 2) {
-        if (BF16)
-            return cleave_hip_matmul_bf16(reinterpret_cast<const uint16_t*>(A.data), A.count,
-                                          reinterpret_cast<const uint16_t*>(B.data), B.count,
-                                          reinterpret_cast<float*>(C.data), C.count, m32, n32, k32, ta, tb);
-        return cleave_hip_matmul_f32(reinterpret_cast<const float*>(A.data), A.count,
-                                     reinterpret_cast<const float*>(B.data), B.count,
-                                     reinterpret_cast<float*>(C.data), C.count, m32, n32, k32, ta, tb);
-    }
+    const TA* ap = reinterpret_cast<const TA*>(A.data);
+    const TA* bp = reinterpret_cast<const TA*>(B.data);
+    TC* cp = reinterpret_cast<TC*>(C.data);
+    if (r == 2) return f.single(ap, A.count, bp, B.count, cp, C.count, m32, n32, k32, ta, tb);
     CH_REQUIRE(A.sizes[0] == B.sizes[0] && B.sizes[0] == C.sizes[0], "%s: batch sizes differ", fn);
     int32_t batch;
     CH_TRY(narrow(A.sizes[0], fn, "batch", &batch));
-    if (BF16) {
-        return cleave_hip_matmul_batched_bf16(reinterpret_cast<const uint16_t*>(A.data), A.count,
-                                              reinterpret_cast<const uint16_t*>(B.data), B.count,
-                                              reinterpret_cast<float*>(C.data), C.count, batch, m32, n32, k32,
-                                              ta, tb);
-    }
-    return cleave_hip_matmul_batched_f32(reinterpret_cast<const float*>(A.data), A.count,
-                                         reinterpret_cast<const float*>(B.data), B.count,
-                                         reinterpret_cast<float*>(C.data), C.count, batch, m32, n32, k32, ta, tb);
+    return f.batched(ap, A.count, bp, B.count, cp, C.count, batch, m32, n32, k32, ta, tb);
 }
 
-using Map1 = int32_t (*)(const float*, int64_t, float*, int64_t);
-using Map2 = int32_t (*)(const float*, int64_t, const float*, int64_t, float*, int64_t);
-
-int32_t map1_mr(Map1 f, cleave_hip_mr x, cleave_hip_mr out, const char* fn) {
+template <class T>
+int32_t map1_mr(int32_t (*f)(const T*, int64_t, T*, int64_t), cleave_hip_mr x, cleave_hip_mr out, const char* fn) {
     View X, O;
-    CH_TRY(flat_view(x, 4, fn, "x", nullptr, &X));
-    CH_TRY(flat_view(out, 4, fn, "out", &X, &O));
-    return f(reinterpret_cast<const float*>(X.data), X.count, reinterpret_cast<float*>(O.data), O.count);
+    CH_TRY(flat_view(x, sizeof(T), fn, "x", nullptr, &X));
+    CH_TRY(flat_view(out, sizeof(T), fn, "out", &X, &O));
+    return f(reinterpret_cast<const T*>(X.data), X.count, reinterpret_cast<T*>(O.data), O.count);
 }
 
-int32_t map2_mr(Map2 f, cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out, const char* fn) {
+template <class T>
+int32_t map2_mr(int32_t (*f)(const T*, int64_t, const T*, int64_t, T*, int64_t), cleave_hip_mr a, cleave_hip_mr b,
+                cleave_hip_mr out, const char* fn) {
     View A, B, O;
-    CH_TRY(flat_view(a, 4, fn, "a", nullptr, &A));
-    CH_TRY(flat_view(b, 4, fn, "b", &A, &B));
-    CH_TRY(flat_view(out, 4, fn, "out", &A, &O));
-    return f(reinterpret_cast<const float*>(A.data), A.count, reinterpret_cast<const float*>(B.data), B.count,
-             reinterpret_cast<float*>(O.data), O.count);
+    CH_TRY(flat_view(a, sizeof(T), fn, "a", nullptr, &A));
+    CH_TRY(flat_view(b, sizeof(T), fn, "b", &A, &B));
+    CH_TRY(flat_view(out, sizeof(T), fn, "out", &A, &O));
+    return f(reinterpret_cast<const T*>(A.data), A.count, reinterpret_cast<const T*>(B.data), B.count,
+             reinterpret_cast<T*>(O.data), O.count);
+}
+
+// A host-returning reduction over a contiguous operand; `bad` after an error.
+template <class R, class T>
+R reduce_mr(R (*f)(const T*, int64_t), cleave_hip_mr x, const char* fn, R bad) {
+    View X;
+    if (flat_view(x, sizeof(T), fn, "x", nullptr, &X) != CLEAVE_HIP_OK) return bad;
+    return f(reinterpret_cast<const T*>(X.data), X.count);
 }
 
 // idx: host memref<K x i32>, K = rank of the tensor; copied to int32 arrays of dims/idx.
@@ -188,31 +191,40 @@ int32_t index_args(const View& t, cleave_hip_mr idx, const char* fn, int32_t* di
 extern "C" {
 
 int32_t _mlir_ciface_cleave_hip_matmul_f32(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr c) {
-    return matmul_mr<false>(a, b, c, "_mlir_ciface_cleave_hip_matmul_f32");
+    return matmul_mr<float, float>({cleave_hip_matmul_f32, cleave_hip_matmul_batched_f32}, a, b, c,
+                                   "_mlir_ciface_cleave_hip_matmul_f32");
 }
 int32_t _mlir_ciface_cleave_hip_matmul_bf16(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr c) {
-    return matmul_mr<true>(a, b, c, "_mlir_ciface_cleave_hip_matmul_bf16");
+    return matmul_mr<uint16_t, float>({cleave_hip_matmul_bf16, cleave_hip_matmul_batched_bf16}, a, b, c,
+                                      "_mlir_ciface_cleave_hip_matmul_bf16");
+}
+int32_t _mlir_ciface_cleave_hip_matmul_f64(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr c) {
+    return matmul_mr<double, double>({cleave_hip_matmul_f64, cleave_hip_matmul_batched_f64}, a, b, c,
+                                     "_mlir_ciface_cleave_hip_matmul_f64");
 }
 
-#define CH_MAP2(name)                                                                             \
-    int32_t _mlir_ciface_cleave_hip_##name##_f32(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out) { \
-        return map2_mr(cleave_hip_##name##_f32, a, b, out, "_mlir_ciface_cleave_hip_" #name "_f32");  \
+#define CH_MAP2(name, T, sfx)                                                                                 \
+    int32_t _mlir_ciface_cleave_hip_##name##_##sfx(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out) {   \
+        return map2_mr<T>(cleave_hip_##name##_##sfx, a, b, out, "_mlir_ciface_cleave_hip_" #name "_" #sfx); \
     }
-#define CH_MAP1(name)                                                                    \
-    int32_t _mlir_ciface_cleave_hip_##name##_f32(cleave_hip_mr x, cleave_hip_mr out) {     \
-        return map1_mr(cleave_hip_##name##_f32, x, out, "_mlir_ciface_cleave_hip_" #name "_f32"); \
+#define CH_MAP1(name, T, sfx)                                                                                 \
+    int32_t _mlir_ciface_cleave_hip_##name##_##sfx(cleave_hip_mr x, cleave_hip_mr out) {                    \
+        return map1_mr<T>(cleave_hip_##name##_##sfx, x, out, "_mlir_ciface_cleave_hip_" #name "_" #sfx);    \
     }
-CH_MAP2(add)
-CH_MAP2(sub)
-CH_MAP2(mul)
-CH_MAP2(div)
-CH_MAP1(neg)
-CH_MAP1(relu)
-CH_MAP1(sigmoid)
-CH_MAP1(tanh)
-CH_MAP2(sigmoid_bwd)
-CH_MAP2(tanh_bwd)
-CH_MAP2(relu_bwd)
+#define CH_MAPS(T, sfx)            \
+    CH_MAP2(add, T, sfx)           \
+    CH_MAP2(sub, T, sfx)           \
+    CH_MAP2(mul, T, sfx)           \
+    CH_MAP2(div, T, sfx)           \
+    CH_MAP1(neg, T, sfx)           \
+    CH_MAP1(relu, T, sfx)          \
+    CH_MAP1(sigmoid, T, sfx)       \
+    CH_MAP1(tanh, T, sfx)          \
+    CH_MAP2(sigmoid_bwd, T, sfx)   \
+    CH_MAP2(tanh_bwd, T, sfx)      \
+    CH_MAP2(relu_bwd, T, sfx)
+CH_MAPS(float, f32)
+CH_MAPS(double, f64)
 
 int32_t _mlir_ciface_cleave_hip_zero_f32(cleave_hip_mr out) {
     const char* fn = "_mlir_ciface_cleave_hip_zero_f32";
@@ -277,29 +289,31 @@ int32_t _mlir_ciface_cleave_hip_sum_rows_f32(cleave_hip_mr g, cleave_hip_mr out)
 }
 
 float _mlir_ciface_cleave_hip_sum_f32(cleave_hip_mr x) {
-    View X;
-    if (flat_view(x, 4, "_mlir_ciface_cleave_hip_sum_f32", "x", nullptr, &X) != CLEAVE_HIP_OK) return NAN;
-    return cleave_hip_sum_f32(reinterpret_cast<const float*>(X.data), X.count);
+    return reduce_mr<float, float>(cleave_hip_sum_f32, x, "_mlir_ciface_cleave_hip_sum_f32", NAN);
 }
 float _mlir_ciface_cleave_hip_mean_f32(cleave_hip_mr x) {
-    View X;
-    if (flat_view(x, 4, "_mlir_ciface_cleave_hip_mean_f32", "x", nullptr, &X) != CLEAVE_HIP_OK) return NAN;
-    return cleave_hip_mean_f32(reinterpret_cast<const float*>(X.data), X.count);
+    return reduce_mr<float, float>(cleave_hip_mean_f32, x, "_mlir_ciface_cleave_hip_mean_f32", NAN);
 }
 float _mlir_ciface_cleave_hip_max_of_f32(cleave_hip_mr x) {
-    View X;
-    if (flat_view(x, 4, "_mlir_ciface_cleave_hip_max_of_f32", "x", nullptr, &X) != CLEAVE_HIP_OK) return NAN;
-    return cleave_hip_max_of_f32(reinterpret_cast<const float*>(X.data), X.count);
+    return reduce_mr<float, float>(cleave_hip_max_of_f32, x, "_mlir_ciface_cleave_hip_max_of_f32", NAN);
 }
 int64_t _mlir_ciface_cleave_hip_argmax_f32(cleave_hip_mr x) {
-    View X;
-    if (flat_view(x, 4, "_mlir_ciface_cleave_hip_argmax_f32", "x", nullptr, &X) != CLEAVE_HIP_OK) return -1;
-    return cleave_hip_argmax_f32(reinterpret_cast<const float*>(X.data), X.count);
+    return reduce_mr<int64_t, float>(cleave_hip_argmax_f32, x, "_mlir_ciface_cleave_hip_argmax_f32", -1);
 }
 uint64_t _mlir_ciface_cleave_hip_sum_u32_u64(cleave_hip_mr x) {
-    View X;
-    if (flat_view(x, 4, "_mlir_ciface_cleave_hip_sum_u32_u64", "x", nullptr, &X) != CLEAVE_HIP_OK) return 0;
-    return cleave_hip_sum_u32_u64(reinterpret_cast<const uint32_t*>(X.data), X.count);
+    return reduce_mr<uint64_t, uint32_t>(cleave_hip_sum_u32_u64, x, "_mlir_ciface_cleave_hip_sum_u32_u64", 0);
+}
+double _mlir_ciface_cleave_hip_sum_f64(cleave_hip_mr x) {
+    return reduce_mr<double, double>(cleave_hip_sum_f64, x, "_mlir_ciface_cleave_hip_sum_f64", NAN);
+}
+double _mlir_ciface_cleave_hip_mean_f64(cleave_hip_mr x) {
+    return reduce_mr<double, double>(cleave_hip_mean_f64, x, "_mlir_ciface_cleave_hip_mean_f64", NAN);
+}
+double _mlir_ciface_cleave_hip_max_of_f64(cleave_hip_mr x) {
+    return reduce_mr<double, double>(cleave_hip_max_of_f64, x, "_mlir_ciface_cleave_hip_max_of_f64", NAN);
+}
+int64_t _mlir_ciface_cleave_hip_argmax_f64(cleave_hip_mr x) {
+    return reduce_mr<int64_t, double>(cleave_hip_argmax_f64, x, "_mlir_ciface_cleave_hip_argmax_f64", -1);
 }
 
 float _mlir_ciface_cleave_hip_index_f32(cleave_hip_mr t, cleave_hip_mr idx) {
@@ -317,6 +331,22 @@ int32_t _mlir_ciface_cleave_hip_index_bwd_f32(float g, cleave_hip_mr dt, cleave_
     CH_TRY(flat_view(dt, 4, fn, "dt", nullptr, &T));
     CH_TRY(index_args(T, idx, fn, dims, ix));
     return cleave_hip_index_bwd_f32(g, reinterpret_cast<float*>(T.data), T.count, dims, T.rank, ix, T.rank);
+}
+double _mlir_ciface_cleave_hip_index_f64(cleave_hip_mr t, cleave_hip_mr idx) {
+    const char* fn = "_mlir_ciface_cleave_hip_index_f64";
+    View T;
+    int32_t dims[kMaxRank], ix[kMaxRank];
+    if (flat_view(t, 8, fn, "t", nullptr, &T) != CLEAVE_HIP_OK) return NAN;
+    if (index_args(T, idx, fn, dims, ix) != CLEAVE_HIP_OK) return NAN;
+    return cleave_hip_index_f64(reinterpret_cast<const double*>(T.data), T.count, dims, T.rank, ix, T.rank);
+}
+int32_t _mlir_ciface_cleave_hip_index_bwd_f64(double g, cleave_hip_mr dt, cleave_hip_mr idx) {
+    const char* fn = "_mlir_ciface_cleave_hip_index_bwd_f64";
+    View T;
+    int32_t dims[kMaxRank], ix[kMaxRank];
+    CH_TRY(flat_view(dt, 8, fn, "dt", nullptr, &T));
+    CH_TRY(index_args(T, idx, fn, dims, ix));
+    return cleave_hip_index_bwd_f64(g, reinterpret_cast<double*>(T.data), T.count, dims, T.rank, ix, T.rank);
 }
 
 int32_t _mlir_ciface_cleave_hip_mandelbrot_u32(cleave_hip_mr out, float x0, float y0, float dx, float dy,

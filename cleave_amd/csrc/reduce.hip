@@ -25,7 +25,6 @@ constexpr int kUnroll = 4;
 
 // Native clang vectors (register-promoted; HIP's float4/uint4 structs are not
 // always) loaded with non-temporal hints: the data is streamed once.
-typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
 // Stage-1 grid: enough blocks for 16 per CU (a function of the length and the
@@ -37,52 +36,67 @@ unsigned stage1_blocks(int64_t nvec) {
     return (unsigned)(want < 1 ? 1 : want);
 }
 
-// ---- sum f32 --------------------------------------------------------------
-__device__ __forceinline__ float wave_sum(float v) {
+// ---- sum f32 / f64 ------------------------------------------------------------
+// One 16-byte vector per load: 4 floats or 2 doubles.
+template <class T>
+struct Vec16 {
+    static constexpr int kN = 16 / sizeof(T);
+    typedef T type __attribute__((ext_vector_type(kN)));
+};
+
+template <class T>
+__device__ __forceinline__ T wave_sum(T v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
     return v;
 }
 
-__device__ float block_sum(float v) {
-    __shared__ float part[kThreads / 64];
+template <class T>
+__device__ T block_sum(T v) {
+    __shared__ T part[kThreads / 64];
     v = wave_sum(v);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
     __syncthreads();
-    float r = 0.0f;
+    T r = T(0);
     if (threadIdx.x == 0)
         for (int w = 0; w < kThreads / 64; ++w) r += part[w];
     return r;  // valid in thread 0
 }
 
-__global__ __launch_bounds__(kThreads) void sum_f32_stage1(const float* __restrict__ x,
-                                                           int64_t n, float* __restrict__ partial,
-                                                           int aligned) {
-    float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+// Each lane keeps one accumulator per vector element and adds them in a
+// fixed tree at the end: (a0 + a1) + (a2 + a3) for f32, a0 + a1 for f64.
+template <class T>
+__global__ __launch_bounds__(kThreads) void sum_stage1(const T* __restrict__ x, int64_t n, T* __restrict__ partial,
+                                                       int aligned) {
+    constexpr int V = Vec16<T>::kN;
+    typedef typename Vec16<T>::type VT;
+    T acc[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc[e] = T(0);
     if (aligned) {
-        const int64_t nv = n / 4;
+        const int64_t nv = n / V;
         const int64_t step = (int64_t)gridDim.x * kThreads * kUnroll;
         for (int64_t base = (int64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x; base < nv; base += step) {
-            f4 v[kUnroll];
+            VT v[kUnroll];
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) {
                 int64_t i = base + (int64_t)u * kThreads;
-                v[u] = i < nv ? __builtin_nontemporal_load(reinterpret_cast<const f4*>(x) + i) : f4{0.f, 0.f, 0.f, 0.f};
+                v[u] = i < nv ? __builtin_nontemporal_load(reinterpret_cast<const VT*>(x) + i) : VT(T(0));
             }
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
-                acc0 += v[u][0];
-                acc1 += v[u][1];
-                acc2 += v[u][2];
-                acc3 += v[u][3];
-            }
+            for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+                for (int e = 0; e < V; ++e) acc[e] += v[u][e];
         }
-        if (blockIdx.x == 0 && threadIdx.x < (n & 3)) acc0 += x[nv * 4 + threadIdx.x];
+        if (blockIdx.x == 0 && threadIdx.x < (n % V)) acc[0] += x[nv * V + threadIdx.x];
     } else {
         for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
-            acc0 += x[i];
+            acc[0] += x[i];
     }
-    float r = block_sum((acc0 + acc1) + (acc2 + acc3));
+    T lane;
+    if constexpr (V == 4) lane = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    else lane = acc[0] + acc[1];
+    T r = block_sum(lane);
     if (threadIdx.x == 0) partial[blockIdx.x] = r;
 }
 
@@ -92,47 +106,51 @@ __global__ __launch_bounds__(kThreads) void sum_f32_stage1(const float* __restri
 // partials; the order, and so the result, is unchanged).
 constexpr int kStage2Loads = 16;
 
-__global__ __launch_bounds__(kThreads) void sum_f32_stage2(const float* __restrict__ partial,
-                                                           int nparts, float* __restrict__ out) {
-    float acc = 0.f;
+template <class T>
+__global__ __launch_bounds__(kThreads) void sum_stage2(const T* __restrict__ partial, int nparts, T* __restrict__ out) {
+    T acc = T(0);
     for (int i0 = threadIdx.x; i0 < nparts; i0 += kThreads * kStage2Loads) {
-        float v[kStage2Loads];
+        T v[kStage2Loads];
 #pragma unroll
         for (int u = 0; u < kStage2Loads; ++u) {
             const int i = i0 + u * kThreads;
-            v[u] = i < nparts ? partial[i] : 0.f;
+            v[u] = i < nparts ? partial[i] : T(0);
         }
 #pragma unroll
         for (int u = 0; u < kStage2Loads; ++u)
             if (i0 + u * kThreads < nparts) acc += v[u];
     }
-    float r = block_sum(acc);
+    T r = block_sum(acc);
     if (threadIdx.x == 0) *out = r;
 }
 
-// ---- max / argmax f32 -------------------------------------------------------
+// ---- max / argmax f32 / f64 -------------------------------------------------
+template <class T>
 struct Best {
-    float v;
+    T v;
     int64_t i;
 };
-__device__ __forceinline__ void take_better(Best& a, float v, int64_t i) {
+template <class T>
+__device__ __forceinline__ void take_better(Best<T>& a, T v, int64_t i) {
     // Comparisons involving NaN are false, so a NaN candidate never wins.
     if (v > a.v || (v == a.v && i < a.i)) {
         a.v = v;
         a.i = i;
     }
 }
-__device__ __forceinline__ Best wave_best(Best b) {
+template <class T>
+__device__ __forceinline__ Best<T> wave_best(Best<T> b) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
-        float v = __shfl_xor(b.v, o);
+        T v = __shfl_xor(b.v, o);
         int64_t i = __shfl_xor(b.i, o);
         take_better(b, v, i);
     }
     return b;
 }
-__device__ Best block_best(Best b) {
-    __shared__ float pv[kThreads / 64];
+template <class T>
+__device__ Best<T> block_best(Best<T> b) {
+    __shared__ T pv[kThreads / 64];
     __shared__ int64_t pi[kThreads / 64];
     b = wave_best(b);
     if ((threadIdx.x & 63) == 0) {
@@ -140,71 +158,70 @@ __device__ Best block_best(Best b) {
         pi[threadIdx.x >> 6] = b.i;
     }
     __syncthreads();
-    Best r{-INFINITY, INT64_MAX};
+    Best<T> r{-INFINITY, INT64_MAX};
     if (threadIdx.x == 0)
         for (int w = 0; w < kThreads / 64; ++w) take_better(r, pv[w], pi[w]);
     return r;
 }
 
-__global__ __launch_bounds__(kThreads) void max_f32_stage1(const float* __restrict__ x, int64_t n,
-                                                           float* __restrict__ pv,
-                                                           int64_t* __restrict__ pi, int aligned) {
-    Best b{-INFINITY, INT64_MAX};
+template <class T>
+__global__ __launch_bounds__(kThreads) void max_stage1(const T* __restrict__ x, int64_t n, T* __restrict__ pv,
+                                                       int64_t* __restrict__ pi, int aligned) {
+    constexpr int V = Vec16<T>::kN;
+    typedef typename Vec16<T>::type VT;
+    Best<T> b{-INFINITY, INT64_MAX};
     if (aligned) {
-        const int64_t nv = n / 4;
+        const int64_t nv = n / V;
         const int64_t step = (int64_t)gridDim.x * kThreads * kUnroll;
         for (int64_t base = (int64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x; base < nv; base += step) {
-            f4 v[kUnroll];
+            VT v[kUnroll];
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) {
                 int64_t i = base + (int64_t)u * kThreads;
-                if (i < nv) v[u] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(x) + i);
+                if (i < nv) v[u] = __builtin_nontemporal_load(reinterpret_cast<const VT*>(x) + i);
             }
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) {
                 int64_t i = base + (int64_t)u * kThreads;
                 if (i < nv) {
-                    take_better(b, v[u][0], 4 * i + 0);
-                    take_better(b, v[u][1], 4 * i + 1);
-                    take_better(b, v[u][2], 4 * i + 2);
-                    take_better(b, v[u][3], 4 * i + 3);
+#pragma unroll
+                    for (int e = 0; e < V; ++e) take_better(b, v[u][e], V * i + e);
                 }
             }
         }
-        if (blockIdx.x == 0 && threadIdx.x < (n & 3)) take_better(b, x[nv * 4 + threadIdx.x], nv * 4 + threadIdx.x);
+        if (blockIdx.x == 0 && threadIdx.x < (n % V)) take_better(b, x[nv * V + threadIdx.x], nv * V + threadIdx.x);
     } else {
         for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
             take_better(b, x[i], i);
     }
-    Best r = block_best(b);
+    Best<T> r = block_best(b);
     if (threadIdx.x == 0) {
         pv[blockIdx.x] = r.v;
         pi[blockIdx.x] = r.i;
     }
 }
 
-__global__ __launch_bounds__(kThreads) void max_f32_stage2(const float* __restrict__ x,
-                                                           const float* __restrict__ pv,
-                                                           const int64_t* __restrict__ pi,
-                                                           int nparts, float* __restrict__ out_v,
-                                                           int64_t* __restrict__ out_i) {
-    Best b{-INFINITY, INT64_MAX};
+template <class T>
+__global__ __launch_bounds__(kThreads) void max_stage2(const T* __restrict__ x, const T* __restrict__ pv,
+                                                       const int64_t* __restrict__ pi, int nparts,
+                                                       T* __restrict__ out_v, int64_t* __restrict__ out_i) {
+    Best<T> b{-INFINITY, INT64_MAX};
     for (int i0 = threadIdx.x; i0 < nparts; i0 += kThreads * kStage2Loads) {
-        float v[kStage2Loads];
+        T v[kStage2Loads];
         int64_t ix[kStage2Loads];
 #pragma unroll
         for (int u = 0; u < kStage2Loads; ++u) {
             const int i = i0 + u * kThreads;
-            v[u] = i < nparts ? pv[i] : -INFINITY;
+            v[u] = i < nparts ? pv[i] : T(-INFINITY);
             ix[u] = i < nparts ? pi[i] : INT64_MAX;
         }
 #pragma unroll
         for (int u = 0; u < kStage2Loads; ++u)
             if (i0 + u * kThreads < nparts) take_better(b, v[u], ix[u]);
     }
-    Best r = block_best(b);
+    Best<T> r = block_best(b);
     if (threadIdx.x == 0) {
-        float x0 = x[0];
+        T x0 = x[0];
         if (x0 != x0) {  // nothing compares > NaN, so the fold keeps a NaN v[0]
             r.v = x0;
             r.i = 0;
@@ -290,25 +307,74 @@ __global__ __launch_bounds__(kThreads) void sum_u64_stage2(const uint64_t* __res
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// Sum into a device scalar: stage-1 partials in scratch slot 0.
+template <class T>
+int32_t run_reduce_sum(const char* fn, const T* x, int64_t len, T* out_dev) {
+    constexpr int V = Vec16<T>::kN;
+    CH_REQUIRE(len >= 1, "%s: length must be >= 1 (sum reads v[0])", fn);
+    CH_REQUIRE(x && out_dev, "%s: null buffer", fn);
+    CH_INIT_OR_RETURN();
+    CH_DEVICE(fn, x, len * sizeof(T));
+    CH_DEVICE(fn, out_dev, sizeof(T));
+    const int aligned = aligned16(x);
+    unsigned blocks = stage1_blocks(aligned ? len / V + 1 : len / kUnroll + 1);
+    T* part = (T*)ch::scratch(0, sizeof(T) * blocks);
+    if (!part) return CLEAVE_HIP_ERR_OOM;
+    sum_stage1<T><<<blocks, kThreads, 0, ch::stream()>>>(x, len, part, aligned);
+    CH_LAUNCHED("sum_stage1");
+    sum_stage2<T><<<1, kThreads, 0, ch::stream()>>>(part, (int)blocks, out_dev);
+    CH_LAUNCHED("sum_stage2");
+    return CLEAVE_HIP_OK;
+}
+
+// max_of / argmax into device scalars: partial indices then values in slot 1.
+template <class T>
+int32_t run_reduce_max(const char* fn, const T* x, int64_t len, T* max_dev, int64_t* argmax_dev) {
+    constexpr int V = Vec16<T>::kN;
+    CH_REQUIRE(len >= 1, "%s: length must be >= 1 (max_of reads v[0])", fn);
+    CH_REQUIRE(x && (max_dev || argmax_dev), "%s: null buffer", fn);
+    CH_INIT_OR_RETURN();
+    CH_DEVICE(fn, x, len * sizeof(T));
+    if (max_dev) CH_DEVICE(fn, max_dev, sizeof(T));
+    if (argmax_dev) CH_DEVICE(fn, argmax_dev, 8);
+    const int aligned = aligned16(x);
+    unsigned blocks = stage1_blocks(aligned ? len / V + 1 : len / kUnroll + 1);
+    char* base = (char*)ch::scratch(1, (sizeof(T) + sizeof(int64_t)) * blocks + 64);
+    if (!base) return CLEAVE_HIP_ERR_OOM;
+    int64_t* pi = (int64_t*)base;
+    T* pv = (T*)(base + sizeof(int64_t) * blocks);
+    max_stage1<T><<<blocks, kThreads, 0, ch::stream()>>>(x, len, pv, pi, aligned);
+    CH_LAUNCHED("max_stage1");
+    max_stage2<T><<<1, kThreads, 0, ch::stream()>>>(x, pv, pi, (int)blocks, max_dev, argmax_dev);
+    CH_LAUNCHED("max_stage2");
+    return CLEAVE_HIP_OK;
+}
+
+// Host-returning forms: queue the reduction into a library-owned device word,
+// then copy it back (synchronising the stream).  `bad` comes back after an
+// error (NaN, or -1 for an index).
+template <class R, class Queue>
+R reduce_to_host(Queue queue, R bad) {
+    ch::clear_error();
+    if (ch::ensure_init() != CLEAVE_HIP_OK) return bad;
+    R* d = (R*)ch::scratch(3, 64);
+    if (!d) return bad;
+    if (queue(d) != CLEAVE_HIP_OK) return bad;
+    R r = bad;
+    if (cleave_hip_download(&r, d, sizeof(R)) != (int64_t)sizeof(R)) return bad;
+    return r;
+}
+
 }  // namespace
 
 extern "C" {
 
 int32_t cleave_hip_reduce_sum_f32(const float* x, int64_t len, float* out_dev) {
-    CH_REQUIRE(len >= 1, "cleave_hip_reduce_sum_f32: length must be >= 1 (sum reads v[0])");
-    CH_REQUIRE(x && out_dev, "cleave_hip_reduce_sum_f32: null buffer");
-    CH_INIT_OR_RETURN();
-    CH_DEVICE("cleave_hip_reduce_sum_f32", x, len * 4);
-    CH_DEVICE("cleave_hip_reduce_sum_f32", out_dev, 4);
-    const int aligned = aligned16(x);
-    unsigned blocks = stage1_blocks(aligned ? len / 4 + 1 : len / kUnroll + 1);
-    float* part = (float*)ch::scratch(0, sizeof(float) * blocks);
-    if (!part) return CLEAVE_HIP_ERR_OOM;
-    sum_f32_stage1<<<blocks, kThreads, 0, ch::stream()>>>(x, len, part, aligned);
-    CH_LAUNCHED("sum_f32_stage1");
-    sum_f32_stage2<<<1, kThreads, 0, ch::stream()>>>(part, (int)blocks, out_dev);
-    CH_LAUNCHED("sum_f32_stage2");
-    return CLEAVE_HIP_OK;
+    return run_reduce_sum<float>("cleave_hip_reduce_sum_f32", x, len, out_dev);
+}
+
+int32_t cleave_hip_reduce_sum_f64(const double* x, int64_t len, double* out_dev) {
+    return run_reduce_sum<double>("cleave_hip_reduce_sum_f64", x, len, out_dev);
 }
 
 // cleave_hip_reduce_sum_f32 with its stage-1 partials in the library's static
@@ -328,31 +394,19 @@ int32_t cleave_hip_reduce_sum_f32_noalloc(const float* x, int64_t len, float* ou
     unsigned blocks = stage1_blocks(aligned ? len / 4 + 1 : len / kUnroll + 1);
     CH_REQUIRE(blocks <= (unsigned)ch::kNoAllocFloats,
                "%s: %u partial sums exceed the static workspace of %d floats", fn, blocks, ch::kNoAllocFloats);
-    sum_f32_stage1<<<blocks, kThreads, 0, ch::stream()>>>(x, len, part, aligned);
-    CH_LAUNCHED("sum_f32_stage1");
-    sum_f32_stage2<<<1, kThreads, 0, ch::stream()>>>(part, (int)blocks, out_dev);
-    CH_LAUNCHED("sum_f32_stage2");
+    sum_stage1<float><<<blocks, kThreads, 0, ch::stream()>>>(x, len, part, aligned);
+    CH_LAUNCHED("sum_stage1");
+    sum_stage2<float><<<1, kThreads, 0, ch::stream()>>>(part, (int)blocks, out_dev);
+    CH_LAUNCHED("sum_stage2");
     return CLEAVE_HIP_OK;
 }
 
 int32_t cleave_hip_reduce_max_f32(const float* x, int64_t len, float* max_dev, int64_t* argmax_dev) {
-    CH_REQUIRE(len >= 1, "cleave_hip_reduce_max_f32: length must be >= 1 (max_of reads v[0])");
-    CH_REQUIRE(x && (max_dev || argmax_dev), "cleave_hip_reduce_max_f32: null buffer");
-    CH_INIT_OR_RETURN();
-    CH_DEVICE("cleave_hip_reduce_max_f32", x, len * 4);
-    if (max_dev) CH_DEVICE("cleave_hip_reduce_max_f32", max_dev, 4);
-    if (argmax_dev) CH_DEVICE("cleave_hip_reduce_max_f32", argmax_dev, 8);
-    const int aligned = aligned16(x);
-    unsigned blocks = stage1_blocks(aligned ? len / 4 + 1 : len / kUnroll + 1);
-    char* base = (char*)ch::scratch(1, (sizeof(float) + sizeof(int64_t)) * blocks + 64);
-    if (!base) return CLEAVE_HIP_ERR_OOM;
-    int64_t* pi = (int64_t*)base;
-    float* pv = (float*)(base + sizeof(int64_t) * blocks);
-    max_f32_stage1<<<blocks, kThreads, 0, ch::stream()>>>(x, len, pv, pi, aligned);
-    CH_LAUNCHED("max_f32_stage1");
-    max_f32_stage2<<<1, kThreads, 0, ch::stream()>>>(x, pv, pi, (int)blocks, max_dev, argmax_dev);
-    CH_LAUNCHED("max_f32_stage2");
-    return CLEAVE_HIP_OK;
+    return run_reduce_max<float>("cleave_hip_reduce_max_f32", x, len, max_dev, argmax_dev);
+}
+
+int32_t cleave_hip_reduce_max_f64(const double* x, int64_t len, double* max_dev, int64_t* argmax_dev) {
+    return run_reduce_max<double>("cleave_hip_reduce_max_f64", x, len, max_dev, argmax_dev);
 }
 
 int32_t cleave_hip_reduce_sum_u32_u64(const uint32_t* x, int64_t len, uint64_t* out_dev) {
@@ -391,17 +445,10 @@ int32_t cleave_hip_reduce_sum_i32_i64(const int32_t* x, int64_t len, int64_t* ou
     return CLEAVE_HIP_OK;
 }
 
-// Host-returning forms: queue the reduction into a library-owned device word,
-// then copy it back (synchronising the stream).
+// Host-returning forms (synchronise): the reduction lands in a library-owned
+// device word that is copied back.
 float cleave_hip_sum_f32(const float* x, int64_t len) {
-    ch::clear_error();
-    if (ch::ensure_init() != CLEAVE_HIP_OK) return NAN;
-    float* d = (float*)ch::scratch(3, 64);
-    if (!d) return NAN;
-    if (cleave_hip_reduce_sum_f32(x, len, d) != CLEAVE_HIP_OK) return NAN;
-    float r = NAN;
-    if (cleave_hip_download(&r, d, sizeof(float)) != (int64_t)sizeof(float)) return NAN;
-    return r;
+    return reduce_to_host<float>([&](float* d) { return cleave_hip_reduce_sum_f32(x, len, d); }, NAN);
 }
 
 float cleave_hip_mean_f32(const float* x, int64_t len) {
@@ -410,47 +457,36 @@ float cleave_hip_mean_f32(const float* x, int64_t len) {
 }
 
 float cleave_hip_max_of_f32(const float* x, int64_t len) {
-    ch::clear_error();
-    if (ch::ensure_init() != CLEAVE_HIP_OK) return NAN;
-    float* d = (float*)ch::scratch(3, 64);
-    if (!d) return NAN;
-    if (cleave_hip_reduce_max_f32(x, len, d, nullptr) != CLEAVE_HIP_OK) return NAN;
-    float r = NAN;
-    if (cleave_hip_download(&r, d, sizeof(float)) != (int64_t)sizeof(float)) return NAN;
-    return r;
+    return reduce_to_host<float>([&](float* d) { return cleave_hip_reduce_max_f32(x, len, d, nullptr); }, NAN);
 }
 
 int64_t cleave_hip_argmax_f32(const float* x, int64_t len) {
-    ch::clear_error();
-    if (ch::ensure_init() != CLEAVE_HIP_OK) return -1;
-    int64_t* d = (int64_t*)ch::scratch(3, 64);
-    if (!d) return -1;
-    if (cleave_hip_reduce_max_f32(x, len, nullptr, d) != CLEAVE_HIP_OK) return -1;
-    int64_t r = -1;
-    if (cleave_hip_download(&r, d, sizeof(int64_t)) != (int64_t)sizeof(int64_t)) return -1;
-    return r;
+    return reduce_to_host<int64_t>([&](int64_t* d) { return cleave_hip_reduce_max_f32(x, len, nullptr, d); }, -1);
+}
+
+double cleave_hip_sum_f64(const double* x, int64_t len) {
+    return reduce_to_host<double>([&](double* d) { return cleave_hip_reduce_sum_f64(x, len, d); }, NAN);
+}
+
+double cleave_hip_mean_f64(const double* x, int64_t len) {
+    double s = cleave_hip_sum_f64(x, len);
+    return s / (double)len;  // sum(v) / N.to() on f64, stdlib/nn/nn.cleave:135-138
+}
+
+double cleave_hip_max_of_f64(const double* x, int64_t len) {
+    return reduce_to_host<double>([&](double* d) { return cleave_hip_reduce_max_f64(x, len, d, nullptr); }, NAN);
+}
+
+int64_t cleave_hip_argmax_f64(const double* x, int64_t len) {
+    return reduce_to_host<int64_t>([&](int64_t* d) { return cleave_hip_reduce_max_f64(x, len, nullptr, d); }, -1);
 }
 
 int64_t cleave_hip_sum_i32_i64(const int32_t* x, int64_t len) {
-    ch::clear_error();
-    if (ch::ensure_init() != CLEAVE_HIP_OK) return 0;
-    int64_t* d = (int64_t*)ch::scratch(3, 64);
-    if (!d) return 0;
-    if (cleave_hip_reduce_sum_i32_i64(x, len, d) != CLEAVE_HIP_OK) return 0;
-    int64_t r = 0;
-    if (cleave_hip_download(&r, d, sizeof(int64_t)) != (int64_t)sizeof(int64_t)) return 0;
-    return r;
+    return reduce_to_host<int64_t>([&](int64_t* d) { return cleave_hip_reduce_sum_i32_i64(x, len, d); }, 0);
 }
 
 uint64_t cleave_hip_sum_u32_u64(const uint32_t* x, int64_t len) {
-    ch::clear_error();
-    if (ch::ensure_init() != CLEAVE_HIP_OK) return 0;
-    uint64_t* d = (uint64_t*)ch::scratch(3, 64);
-    if (!d) return 0;
-    if (cleave_hip_reduce_sum_u32_u64(x, len, d) != CLEAVE_HIP_OK) return 0;
-    uint64_t r = 0;
-    if (cleave_hip_download(&r, d, sizeof(uint64_t)) != (int64_t)sizeof(uint64_t)) return 0;
-    return r;
+    return reduce_to_host<uint64_t>([&](uint64_t* d) { return cleave_hip_reduce_sum_u32_u64(x, len, d); }, 0);
 }
 
 }  // extern "C"

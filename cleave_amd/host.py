@@ -7,7 +7,8 @@ arrays are host memory passed as (aligned pointer, i64 length) pairs
 through HBM, runs the HIP kernels and copies the results back before it
 returns.  Names follow the stdlib (/root/reference/stdlib/linalg/matrix.cleave,
 tensor.cleave, /root/reference/stdlib/nn/nn.cleave); device-resident work uses
-the functions of the package itself instead.
+the functions of the package itself instead.  float64 arrays take the f64
+entry points (Tensor<f64, ...>); other float arrays are converted to f32.
 """
 from __future__ import annotations
 
@@ -35,65 +36,80 @@ def _scalar(fn: str, *args):
 
 # ---- MatMul (stdlib/linalg/matrix.cleave:22-61) --------------------------------------
 
+def _kind(a) -> str:
+    """Operand element type: bf16 bit patterns (uint16), f64 (float64), else f32."""
+    dt = np.asarray(a).dtype
+    return "bf16" if dt == np.uint16 else ("f64" if dt == np.float64 else "f32")
+
+
+_NP = {"f32": np.float32, "f64": np.float64, "bf16": np.uint16}
+
+
 def matmul(a: np.ndarray, b: np.ndarray, trans_a: bool = False, trans_b: bool = False) -> np.ndarray:
-    """C = op(A) op(B), f32 accumulate and output.  float32 operands run the f32
-    product; uint16 operands are bf16 bit patterns and run the bf16 product."""
-    bf16 = np.asarray(a).dtype == np.uint16
-    dt = np.uint16 if bf16 else np.float32
-    a, b = _arr(a, dt), _arr(b, dt)
+    """C = op(A) op(B).  float32 operands run the f32 product, uint16 operands
+    (bf16 bit patterns) the bf16 one, both with an f32 result; float64
+    operands run the f64 product."""
+    kind = _kind(a)
+    a, b = _arr(a, _NP[kind]), _arr(b, _NP[kind])
     M, K = (a.shape[1], a.shape[0]) if trans_a else a.shape
     Kb, N = (b.shape[1], b.shape[0]) if trans_b else b.shape
     if K != Kb:
         raise ValueError(f"matmul: inner dimensions differ ({K} vs {Kb})")
-    c = np.empty((M, N), np.float32)
-    fn = "cleave_hip_matmul_bf16_host" if bf16 else "cleave_hip_matmul_f32_host"
-    call(fn, _p(a), a.size, _p(b), b.size, _p(c), c.size, M, N, K, int(trans_a), int(trans_b))
+    c = np.empty((M, N), np.float64 if kind == "f64" else np.float32)
+    call(f"cleave_hip_matmul_{kind}_host", _p(a), a.size, _p(b), b.size, _p(c), c.size, M, N, K, int(trans_a),
+         int(trans_b))
     return c
 
 
 def matmul_batched(a: np.ndarray, b: np.ndarray, trans_a: bool = False, trans_b: bool = False) -> np.ndarray:
-    bf16 = np.asarray(a).dtype == np.uint16
-    dt = np.uint16 if bf16 else np.float32
-    a, b = _arr(a, dt), _arr(b, dt)
+    kind = _kind(a)
+    a, b = _arr(a, _NP[kind]), _arr(b, _NP[kind])
     batch, M, K = a.shape
     _, Kb, N = b.shape
     if trans_a:
         M, K = K, M
     if trans_b:
         Kb, N = N, Kb
-    c = np.empty((batch, M, N), np.float32)
-    fn = "cleave_hip_matmul_batched_bf16_host" if bf16 else "cleave_hip_matmul_batched_f32_host"
-    call(fn, _p(a), a.size, _p(b), b.size, _p(c), c.size, batch, M, N, K, int(trans_a), int(trans_b))
+    c = np.empty((batch, M, N), np.float64 if kind == "f64" else np.float32)
+    call(f"cleave_hip_matmul_batched_{kind}_host", _p(a), a.size, _p(b), b.size, _p(c), c.size, batch, M, N, K,
+         int(trans_a), int(trans_b))
     return c
 
 
 # ---- Ring<Tensor>, Activation<Tensor>, backward maps -------------------------------------
 
-def _map1(fn: str, x) -> np.ndarray:
-    x = _arr(x, np.float32)
+def _fkind(a) -> str:
+    """f64 for float64 arrays, f32 for everything else (converted)."""
+    return "f64" if np.asarray(a).dtype == np.float64 else "f32"
+
+
+def _map1(op: str, x) -> np.ndarray:
+    kind = _fkind(x)
+    x = _arr(x, _NP[kind])
     out = np.empty_like(x)
-    call(fn, _p(x), x.size, _p(out), out.size)
+    call(f"cleave_hip_{op}_{kind}_host", _p(x), x.size, _p(out), out.size)
     return out
 
 
-def _map2(fn: str, a, b) -> np.ndarray:
-    a, b = _arr(a, np.float32), _arr(b, np.float32)
+def _map2(op: str, a, b) -> np.ndarray:
+    kind = _fkind(a)
+    a, b = _arr(a, _NP[kind]), _arr(b, _NP[kind])
     out = np.empty_like(a)
-    call(fn, _p(a), a.size, _p(b), b.size, _p(out), out.size)
+    call(f"cleave_hip_{op}_{kind}_host", _p(a), a.size, _p(b), b.size, _p(out), out.size)
     return out
 
 
-def add(a, b): return _map2("cleave_hip_add_f32_host", a, b)
-def sub(a, b): return _map2("cleave_hip_sub_f32_host", a, b)
-def mul(a, b): return _map2("cleave_hip_mul_f32_host", a, b)
-def div(a, b): return _map2("cleave_hip_div_f32_host", a, b)
-def neg(a): return _map1("cleave_hip_neg_f32_host", a)
-def relu(x): return _map1("cleave_hip_relu_f32_host", x)
-def sigmoid(x): return _map1("cleave_hip_sigmoid_f32_host", x)
-def tanh(x): return _map1("cleave_hip_tanh_f32_host", x)
-def sigmoid_bwd(s, g): return _map2("cleave_hip_sigmoid_bwd_f32_host", s, g)
-def tanh_bwd(t, g): return _map2("cleave_hip_tanh_bwd_f32_host", t, g)
-def relu_bwd(x, g): return _map2("cleave_hip_relu_bwd_f32_host", x, g)
+def add(a, b): return _map2("add", a, b)
+def sub(a, b): return _map2("sub", a, b)
+def mul(a, b): return _map2("mul", a, b)
+def div(a, b): return _map2("div", a, b)
+def neg(a): return _map1("neg", a)
+def relu(x): return _map1("relu", x)
+def sigmoid(x): return _map1("sigmoid", x)
+def tanh(x): return _map1("tanh", x)
+def sigmoid_bwd(s, g): return _map2("sigmoid_bwd", s, g)
+def tanh_bwd(t, g): return _map2("tanh_bwd", t, g)
+def relu_bwd(x, g): return _map2("relu_bwd", x, g)
 
 
 def zero(shape) -> np.ndarray:
@@ -137,24 +153,26 @@ def sum_rows(g) -> np.ndarray:
 
 # ---- Sum / Mean / Max (stdlib/nn/nn.cleave:111-149) -------------------------------------
 
+def _reduce(op: str, x):
+    kind = _fkind(x)
+    x = _arr(x, _NP[kind])
+    return _scalar(f"cleave_hip_{op}_{kind}_host", _p(x), x.size)
+
+
 def sum(x) -> float:  # noqa: A001 - mirrors the stdlib name
-    x = _arr(x, np.float32)
-    return float(_scalar("cleave_hip_sum_f32_host", _p(x), x.size))
+    return float(_reduce("sum", x))
 
 
 def mean(x) -> float:
-    x = _arr(x, np.float32)
-    return float(_scalar("cleave_hip_mean_f32_host", _p(x), x.size))
+    return float(_reduce("mean", x))
 
 
 def max_of(x) -> float:
-    x = _arr(x, np.float32)
-    return float(_scalar("cleave_hip_max_of_f32_host", _p(x), x.size))
+    return float(_reduce("max_of", x))
 
 
 def argmax(x) -> int:
-    x = _arr(x, np.float32)
-    return int(_scalar("cleave_hip_argmax_f32_host", _p(x), x.size))
+    return int(_reduce("argmax", x))
 
 
 def sum_u64(x) -> int:
@@ -171,10 +189,11 @@ def sum_i64(x) -> int:
 # ---- Index<Tensor> (stdlib/linalg/tensor.cleave:113-133) ----------------------------------
 
 def index(t: np.ndarray, idx) -> float:
-    t = _arr(t, np.float32)
+    kind = _fkind(t)
+    t = _arr(t, _NP[kind])
     dims = _arr(t.shape, np.int32)
     ix = _arr(np.atleast_1d(idx), np.int32)
-    return float(_scalar("cleave_hip_index_f32_host", _p(t), t.size, _p(dims), dims.size, _p(ix), ix.size))
+    return float(_scalar(f"cleave_hip_index_{kind}_host", _p(t), t.size, _p(dims), dims.size, _p(ix), ix.size))
 
 
 def index_bwd(g: float, dt: np.ndarray, idx) -> np.ndarray:

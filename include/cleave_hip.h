@@ -298,6 +298,65 @@ CLEAVE_HIP_API int32_t cleave_hip_mlp_step_f32(const float* x, int64_t xlen, con
                                 float* loss_dev, int32_t B, int32_t D, int32_t Hd, float lr);
 
 /* ---------------------------------------------------------------------- */
+/* Tensor<f64, ...>                                                         */
+/* ---------------------------------------------------------------------- */
+/* Every tensor impl of the stdlib is generic over T: Float
+ * (stdlib/linalg/tensor.cleave:40, :66-71; stdlib/nn/nn.cleave:82, :111,
+ * :119, :141; stdlib/linalg/matrix.cleave:27), and Float covers f64
+ * (stdlib/num/num.cleave:50-51, Ring<f64> :189-196).  These are the f32
+ * operators above on double operands, with the same argument meaning,
+ * lengths in elements, checks and error behaviour; they compute in double
+ * throughout (math.exp / math.tanh are the device's double exp / tanh). */
+
+/* C = op(A) op(B) in f64 on the f64 matrix cores (v_mfma_f64_16x16x4f64). */
+CLEAVE_HIP_API int32_t cleave_hip_matmul_f64(const double* a, int64_t alen, const double* b, int64_t blen,
+                                             double* c, int64_t clen, int32_t M, int32_t N, int32_t K,
+                                             int32_t trans_a, int32_t trans_b);
+CLEAVE_HIP_API int32_t cleave_hip_matmul_batched_f64(const double* a, int64_t alen, const double* b,
+                                                     int64_t blen, double* c, int64_t clen, int32_t batch,
+                                                     int32_t M, int32_t N, int32_t K, int32_t trans_a,
+                                                     int32_t trans_b);
+CLEAVE_HIP_API int32_t cleave_hip_add_f64(const double* a, int64_t alen, const double* b, int64_t blen,
+                                          double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_sub_f64(const double* a, int64_t alen, const double* b, int64_t blen,
+                                          double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_mul_f64(const double* a, int64_t alen, const double* b, int64_t blen,
+                                          double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_div_f64(const double* a, int64_t alen, const double* b, int64_t blen,
+                                          double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_neg_f64(const double* a, int64_t alen, double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_zero_f64(double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_relu_f64(const double* x, int64_t xlen, double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_sigmoid_f64(const double* x, int64_t xlen, double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_tanh_f64(const double* x, int64_t xlen, double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_sigmoid_bwd_f64(const double* s, int64_t slen, const double* g, int64_t glen,
+                                                  double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_tanh_bwd_f64(const double* t, int64_t tlen, const double* g, int64_t glen,
+                                               double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_relu_bwd_f64(const double* x, int64_t xlen, const double* g, int64_t glen,
+                                               double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_div_bwd_f64(const double* a, int64_t alen, const double* b, int64_t blen,
+                                              const double* g, int64_t glen, double* da, int64_t dalen,
+                                              double* db, int64_t dblen);
+CLEAVE_HIP_API int32_t cleave_hip_sgd_update_f64(double* w, int64_t wlen, const double* g, int64_t glen,
+                                                 double lr);
+CLEAVE_HIP_API int32_t cleave_hip_add_row_bias_f64(const double* a, int64_t alen, const double* bias, int64_t blen,
+                                                   double* out, int64_t outlen, int32_t rows, int32_t cols);
+CLEAVE_HIP_API int32_t cleave_hip_sum_rows_f64(const double* g, int64_t glen, double* out, int64_t outlen,
+                                               int32_t rows, int32_t cols);
+CLEAVE_HIP_API int32_t cleave_hip_reduce_sum_f64(const double* x, int64_t len, double* out_dev);
+CLEAVE_HIP_API int32_t cleave_hip_reduce_max_f64(const double* x, int64_t len, double* max_dev,
+                                                 int64_t* argmax_dev);
+CLEAVE_HIP_API double cleave_hip_sum_f64(const double* x, int64_t len);
+CLEAVE_HIP_API double cleave_hip_mean_f64(const double* x, int64_t len);
+CLEAVE_HIP_API double cleave_hip_max_of_f64(const double* x, int64_t len);
+CLEAVE_HIP_API int64_t cleave_hip_argmax_f64(const double* x, int64_t len);
+CLEAVE_HIP_API double cleave_hip_index_f64(const double* t, int64_t len, const int32_t* dims, int64_t ndims,
+                                           const int32_t* idx, int64_t nidx);
+CLEAVE_HIP_API int32_t cleave_hip_index_bwd_f64(double g, double* dt, int64_t len, const int32_t* dims,
+                                                int64_t ndims, const int32_t* idx, int64_t nidx);
+
+/* ---------------------------------------------------------------------- */
 /* Host-array forms                                                         */
 /* ---------------------------------------------------------------------- */
 /* cleave's extern lowering passes an [T; N] argument as the aligned pointer
@@ -378,6 +437,52 @@ CLEAVE_HIP_API float cleave_hip_index_f32_host(const float* t, int64_t len, cons
 CLEAVE_HIP_API int32_t cleave_hip_index_bwd_f32_host(float g, float* dt, int64_t len, const int32_t* dims,
                                                      int64_t ndims, const int32_t* idx, int64_t nidx);
 
+/* Tensor<f64, ...> operators on host arrays. */
+CLEAVE_HIP_API int32_t cleave_hip_matmul_f64_host(const double* a, int64_t alen, const double* b, int64_t blen,
+                                                  double* c, int64_t clen, int32_t M, int32_t N, int32_t K,
+                                                  int32_t trans_a, int32_t trans_b);
+CLEAVE_HIP_API int32_t cleave_hip_matmul_batched_f64_host(const double* a, int64_t alen, const double* b,
+                                                          int64_t blen, double* c, int64_t clen, int32_t batch,
+                                                          int32_t M, int32_t N, int32_t K, int32_t trans_a,
+                                                          int32_t trans_b);
+CLEAVE_HIP_API int32_t cleave_hip_add_f64_host(const double* a, int64_t alen, const double* b, int64_t blen,
+                                               double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_sub_f64_host(const double* a, int64_t alen, const double* b, int64_t blen,
+                                               double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_mul_f64_host(const double* a, int64_t alen, const double* b, int64_t blen,
+                                               double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_div_f64_host(const double* a, int64_t alen, const double* b, int64_t blen,
+                                               double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_neg_f64_host(const double* a, int64_t alen, double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_zero_f64_host(double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_relu_f64_host(const double* x, int64_t xlen, double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_sigmoid_f64_host(const double* x, int64_t xlen, double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_tanh_f64_host(const double* x, int64_t xlen, double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_sigmoid_bwd_f64_host(const double* s, int64_t slen, const double* g,
+                                                       int64_t glen, double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_tanh_bwd_f64_host(const double* t, int64_t tlen, const double* g, int64_t glen,
+                                                    double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_relu_bwd_f64_host(const double* x, int64_t xlen, const double* g, int64_t glen,
+                                                    double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_div_bwd_f64_host(const double* a, int64_t alen, const double* b, int64_t blen,
+                                                   const double* g, int64_t glen, double* da, int64_t dalen,
+                                                   double* db, int64_t dblen);
+CLEAVE_HIP_API int32_t cleave_hip_sgd_update_f64_host(double* w, int64_t wlen, const double* g, int64_t glen,
+                                                      double lr);
+CLEAVE_HIP_API int32_t cleave_hip_add_row_bias_f64_host(const double* a, int64_t alen, const double* bias,
+                                                        int64_t blen, double* out, int64_t outlen, int32_t rows,
+                                                        int32_t cols);
+CLEAVE_HIP_API int32_t cleave_hip_sum_rows_f64_host(const double* g, int64_t glen, double* out, int64_t outlen,
+                                                    int32_t rows, int32_t cols);
+CLEAVE_HIP_API double cleave_hip_sum_f64_host(const double* x, int64_t len);
+CLEAVE_HIP_API double cleave_hip_mean_f64_host(const double* x, int64_t len);
+CLEAVE_HIP_API double cleave_hip_max_of_f64_host(const double* x, int64_t len);
+CLEAVE_HIP_API int64_t cleave_hip_argmax_f64_host(const double* x, int64_t len);
+CLEAVE_HIP_API double cleave_hip_index_f64_host(const double* t, int64_t len, const int32_t* dims, int64_t ndims,
+                                                const int32_t* idx, int64_t nidx);
+CLEAVE_HIP_API int32_t cleave_hip_index_bwd_f64_host(double g, double* dt, int64_t len, const int32_t* dims,
+                                                     int64_t ndims, const int32_t* idx, int64_t nidx);
+
 /* escape_count map (examples/mandelbrot.cleave:14-26). */
 CLEAVE_HIP_API int32_t cleave_hip_mandelbrot_u32_host(uint32_t* out, int64_t outlen, int32_t width,
                                                       int32_t height, float x0, float y0, float dx, float dy,
@@ -428,6 +533,28 @@ CLEAVE_HIP_API int64_t cleave_hip_tanh_bwd_f32_into(float* out, int64_t outlen, 
                                                     const float* g, int64_t glen);
 CLEAVE_HIP_API int64_t cleave_hip_relu_bwd_f32_into(float* out, int64_t outlen, const float* x, int64_t xlen,
                                                     const float* g, int64_t glen);
+/* The same on f64 arrays. */
+CLEAVE_HIP_API int64_t cleave_hip_matmul_f64_into(double* c, int64_t clen, const double* a, int64_t alen,
+                                                  const double* b, int64_t blen, int32_t M, int32_t N, int32_t K,
+                                                  int32_t trans_a, int32_t trans_b);
+CLEAVE_HIP_API int64_t cleave_hip_add_f64_into(double* out, int64_t outlen, const double* a, int64_t alen,
+                                               const double* b, int64_t blen);
+CLEAVE_HIP_API int64_t cleave_hip_sub_f64_into(double* out, int64_t outlen, const double* a, int64_t alen,
+                                               const double* b, int64_t blen);
+CLEAVE_HIP_API int64_t cleave_hip_mul_f64_into(double* out, int64_t outlen, const double* a, int64_t alen,
+                                               const double* b, int64_t blen);
+CLEAVE_HIP_API int64_t cleave_hip_div_f64_into(double* out, int64_t outlen, const double* a, int64_t alen,
+                                               const double* b, int64_t blen);
+CLEAVE_HIP_API int64_t cleave_hip_neg_f64_into(double* out, int64_t outlen, const double* x, int64_t xlen);
+CLEAVE_HIP_API int64_t cleave_hip_relu_f64_into(double* out, int64_t outlen, const double* x, int64_t xlen);
+CLEAVE_HIP_API int64_t cleave_hip_sigmoid_f64_into(double* out, int64_t outlen, const double* x, int64_t xlen);
+CLEAVE_HIP_API int64_t cleave_hip_tanh_f64_into(double* out, int64_t outlen, const double* x, int64_t xlen);
+CLEAVE_HIP_API int64_t cleave_hip_sigmoid_bwd_f64_into(double* out, int64_t outlen, const double* s, int64_t slen,
+                                                       const double* g, int64_t glen);
+CLEAVE_HIP_API int64_t cleave_hip_tanh_bwd_f64_into(double* out, int64_t outlen, const double* t, int64_t tlen,
+                                                    const double* g, int64_t glen);
+CLEAVE_HIP_API int64_t cleave_hip_relu_bwd_f64_into(double* out, int64_t outlen, const double* x, int64_t xlen,
+                                                    const double* g, int64_t glen);
 /* escape_count over a grid (examples/mandelbrot.cleave:14-26) as i32 counts,
  * escape_count's own return type: the counts of cleave_hip_mandelbrot_u32,
  * which never exceed max_iter, so the bits are the same. */

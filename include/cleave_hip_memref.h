@@ -117,6 +117,26 @@ CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_mlp_step_f32(cleave_hip_mr x, cle
                                                            cleave_hip_mr w2, cleave_hip_mr dw1, cleave_hip_mr dw2,
                                                            cleave_hip_mr loss, float lr);
 
+/* Tensor<f64, ...> forms of the above (memref<... x f64>), same rules. */
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_matmul_f64(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr c);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_add_f64(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_sub_f64(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_mul_f64(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_div_f64(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_neg_f64(cleave_hip_mr a, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_relu_f64(cleave_hip_mr x, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_sigmoid_f64(cleave_hip_mr x, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_tanh_f64(cleave_hip_mr x, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_sigmoid_bwd_f64(cleave_hip_mr s, cleave_hip_mr g, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_tanh_bwd_f64(cleave_hip_mr t, cleave_hip_mr g, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_relu_bwd_f64(cleave_hip_mr x, cleave_hip_mr g, cleave_hip_mr out);
+CLEAVE_HIP_API double _mlir_ciface_cleave_hip_sum_f64(cleave_hip_mr x);
+CLEAVE_HIP_API double _mlir_ciface_cleave_hip_mean_f64(cleave_hip_mr x);
+CLEAVE_HIP_API double _mlir_ciface_cleave_hip_max_of_f64(cleave_hip_mr x);
+CLEAVE_HIP_API int64_t _mlir_ciface_cleave_hip_argmax_f64(cleave_hip_mr x);
+CLEAVE_HIP_API double _mlir_ciface_cleave_hip_index_f64(cleave_hip_mr t, cleave_hip_mr idx);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_index_bwd_f64(double g, cleave_hip_mr dt, cleave_hip_mr idx);
+
 #ifdef __cplusplus
 }
 #endif

@@ -650,3 +650,142 @@ void or_xor_tensor_train(int32_t steps, float lr, float* preds4) {
         preds4[r] = xor_forward(&p, xs1[r], xs2[r], &h0, &h1);
     }
 }
+
+/* ======================================================================== */
+/* f64: the same operators on Tensor<f64, ...>.  Every tensor impl is       */
+/* generic over T: Float (stdlib/linalg/tensor.cleave:40, :66-71;           */
+/* stdlib/nn/nn.cleave:82, :111, :119, :141; stdlib/linalg/matrix.cleave:27) */
+/* and Float covers f64 (stdlib/num/num.cleave:50-51, Ring<f64> :189-196),  */
+/* so the lowered ops are the f32 ones above in double: addf/mulf/... on    */
+/* f64, math.exp / math.tanh through libm's exp / tanh.                     */
+/* ======================================================================== */
+
+static inline double a_at64(const double* A, int32_t M, int32_t K, int32_t ta, int32_t i, int32_t k) {
+    return ta ? A[(int64_t)k * M + i] : A[(int64_t)i * K + k];
+}
+static inline double b_at64(const double* B, int32_t N, int32_t K, int32_t tb, int32_t k, int32_t j) {
+    return tb ? B[(int64_t)j * K + k] : B[(int64_t)k * N + j];
+}
+
+/* linalg.matmul on f64 (matrix.cleave:59-60, region mlir_lower.rs:2089-2120):
+ * C = 0, then for k ascending C = C + (a * b), each op rounded. */
+void or_matmul_f64_rows(const double* A, const double* B, double* C, int32_t M, int32_t N, int32_t K,
+                        int32_t trans_a, int32_t trans_b, int32_t row0, int32_t row1) {
+    for (int32_t i = row0; i < row1; ++i)
+        for (int32_t j = 0; j < N; ++j) {
+            double c = 0.0;
+            for (int32_t k = 0; k < K; ++k) {
+                double p = a_at64(A, M, K, trans_a, i, k) * b_at64(B, N, K, trans_b, k, j);
+                c = c + p;
+            }
+            C[(int64_t)i * N + j] = c;
+        }
+}
+
+void or_matmul_f64_mt(const double* A, const double* B, double* C, int32_t M, int32_t N, int32_t K,
+                      int32_t trans_a, int32_t trans_b, int32_t threads) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)
+#endif
+    for (int32_t i = 0; i < M; ++i) or_matmul_f64_rows(A, B, C, M, N, K, trans_a, trans_b, i, i + 1);
+    (void)threads;
+}
+
+void or_add_f64(const double* a, const double* b, double* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = a[i] + b[i];
+}
+void or_sub_f64(const double* a, const double* b, double* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = a[i] - b[i];
+}
+void or_mul_f64(const double* a, const double* b, double* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = a[i] * b[i];
+}
+void or_div_f64(const double* a, const double* b, double* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = a[i] / b[i];
+}
+void or_neg_f64(const double* a, double* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = -a[i];
+}
+/* arith.maximumf on f64 (nn.cleave:83-85). */
+static inline double ieee_maximum64(double x, double y) {
+    if (isnan(x) || isnan(y)) return x + y;
+    if (x == y) return signbit(x) ? y : x;
+    return x > y ? x : y;
+}
+void or_relu_f64(const double* a, double* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = ieee_maximum64(a[i], 0.0);
+}
+/* nn.cleave:87-93 on f64: negf, math.exp (libm exp), addf(1, e), divf(1, .). */
+double or_sigmoid_f64_scalar(double x) {
+    double e = exp(-x);
+    double denom = 1.0 + e;
+    return 1.0 / denom;
+}
+void or_sigmoid_f64(const double* a, double* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = or_sigmoid_f64_scalar(a[i]);
+}
+void or_tanh_f64(const double* a, double* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = tanh(a[i]);
+}
+void or_sigmoid_bwd_f64(const double* s, const double* g, double* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = g[i] * s[i] * (1.0 - s[i]);
+}
+void or_tanh_bwd_f64(const double* t, const double* g, double* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = g[i] * (1.0 - t[i] * t[i]);
+}
+void or_relu_bwd_f64(const double* x, const double* g, double* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = x[i] > 0.0 ? g[i] : 0.0;
+}
+void or_div_bwd_f64(const double* a, const double* b, const double* g, double* da, double* db, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        da[i] = g[i] / b[i];
+        db[i] = -(g[i] * a[i]) / (b[i] * b[i]);
+    }
+}
+void or_add_row_bias_f64(const double* a, const double* bias, double* out, int32_t rows, int32_t cols) {
+    for (int64_t i = 0; i < rows; ++i)
+        for (int64_t j = 0; j < cols; ++j) out[i * cols + j] = a[i * cols + j] + bias[j];
+}
+void or_sum_rows_f64(const double* g, double* out, int32_t rows, int32_t cols) {
+    for (int64_t j = 0; j < cols; ++j) {
+        double acc = g[j];
+        for (int64_t i = 1; i < rows; ++i) acc = acc + g[i * cols + j];
+        out[j] = acc;
+    }
+}
+int32_t or_index_f64(const double* t, const int32_t* dims, int32_t ndims, const int32_t* idx, double* out) {
+    const int64_t off = or_flat_offset(dims, ndims, idx);
+    if (off < 0) return -1;
+    *out = t[off];
+    return 0;
+}
+int32_t or_index_bwd_f64(double g, double* dt, const int32_t* dims, int32_t ndims, const int32_t* idx) {
+    const int64_t off = or_flat_offset(dims, ndims, idx);
+    if (off < 0) return -1;
+    dt[off] = dt[off] + g;
+    return 0;
+}
+/* Sum / Mean / Max on f64 (nn.cleave:111-149): left fold from v[0];
+ * mean = sum / N.to() (sitofp to f64); strict-> first-wins max. */
+double or_sum_f64(const double* v, int64_t n) {
+    double acc = v[0];
+    for (int64_t i = 1; i < n; ++i) acc = acc + v[i];
+    return acc;
+}
+double or_mean_f64(const double* v, int64_t n) { return or_sum_f64(v, n) / (double)n; }
+double or_max_of_f64(const double* v, int64_t n) {
+    double acc = v[0];
+    for (int64_t i = 1; i < n; ++i)
+        if (v[i] > acc) acc = v[i];
+    return acc;
+}
+int64_t or_argmax_f64(const double* v, int64_t n) {
+    double acc = v[0];
+    int64_t idx = 0;
+    for (int64_t i = 1; i < n; ++i)
+        if (v[i] > acc) {
+            acc = v[i];
+            idx = i;
+        }
+    return idx;
+}

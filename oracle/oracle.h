@@ -172,6 +172,38 @@ double or_mlp_loss_f64(const float* X, const float* y, const float* W1, const fl
  * predictions (forward of rows 00, 01, 10, 11).  Pinned: doc/backlog.md:142. */
 void or_xor_tensor_train(int32_t steps, float lr, float* preds4);
 
+
+/* f64: the same operators on Tensor<f64, ...> (every tensor impl is generic
+ * over T: Float, and Float covers f64, stdlib/num/num.cleave:50-51).
+ * Pinned: the reference's golden vectors in f64, exact identities (A*0 = 0,
+ * A*I = A, transpose forms against explicit transposes), brute force in
+ * long double, libm closed forms and special values, bitwise order checks. */
+void or_matmul_f64_rows(const double* A, const double* B, double* C, int32_t M, int32_t N, int32_t K,
+                        int32_t trans_a, int32_t trans_b, int32_t row0, int32_t row1);
+void or_matmul_f64_mt(const double* A, const double* B, double* C, int32_t M, int32_t N, int32_t K,
+                      int32_t trans_a, int32_t trans_b, int32_t threads);
+void or_add_f64(const double* a, const double* b, double* out, int64_t n);
+void or_sub_f64(const double* a, const double* b, double* out, int64_t n);
+void or_mul_f64(const double* a, const double* b, double* out, int64_t n);
+void or_div_f64(const double* a, const double* b, double* out, int64_t n);
+void or_neg_f64(const double* a, double* out, int64_t n);
+void or_relu_f64(const double* a, double* out, int64_t n);
+double or_sigmoid_f64_scalar(double x);
+void or_sigmoid_f64(const double* a, double* out, int64_t n);
+void or_tanh_f64(const double* a, double* out, int64_t n);
+void or_sigmoid_bwd_f64(const double* s, const double* g, double* out, int64_t n);
+void or_tanh_bwd_f64(const double* t, const double* g, double* out, int64_t n);
+void or_relu_bwd_f64(const double* x, const double* g, double* out, int64_t n);
+void or_div_bwd_f64(const double* a, const double* b, const double* g, double* da, double* db, int64_t n);
+void or_add_row_bias_f64(const double* a, const double* bias, double* out, int32_t rows, int32_t cols);
+void or_sum_rows_f64(const double* g, double* out, int32_t rows, int32_t cols);
+int32_t or_index_f64(const double* t, const int32_t* dims, int32_t ndims, const int32_t* idx, double* out);
+int32_t or_index_bwd_f64(double g, double* dt, const int32_t* dims, int32_t ndims, const int32_t* idx);
+double or_sum_f64(const double* v, int64_t n);
+double or_mean_f64(const double* v, int64_t n);
+double or_max_of_f64(const double* v, int64_t n);
+int64_t or_argmax_f64(const double* v, int64_t n);
+
 #ifdef __cplusplus
 }
 #endif

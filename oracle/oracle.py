@@ -67,6 +67,30 @@ _SIGS = {
                                  _i32]),
     "or_mandelbrot_rows_mt": (None, [_p, _i32, _i32, _f, _f, _f, _f, _i32, _i32, _i32, _i32]),
     "or_xor_tensor_train": (None, [_i32, _f, _p]),
+    # f64 forms
+    "or_matmul_f64_rows": (None, [_p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "or_matmul_f64_mt": (None, [_p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "or_add_f64": (None, [_p, _p, _p, _i64]),
+    "or_sub_f64": (None, [_p, _p, _p, _i64]),
+    "or_mul_f64": (None, [_p, _p, _p, _i64]),
+    "or_div_f64": (None, [_p, _p, _p, _i64]),
+    "or_neg_f64": (None, [_p, _p, _i64]),
+    "or_relu_f64": (None, [_p, _p, _i64]),
+    "or_sigmoid_f64": (None, [_p, _p, _i64]),
+    "or_sigmoid_f64_scalar": (C.c_double, [C.c_double]),
+    "or_tanh_f64": (None, [_p, _p, _i64]),
+    "or_sigmoid_bwd_f64": (None, [_p, _p, _p, _i64]),
+    "or_tanh_bwd_f64": (None, [_p, _p, _p, _i64]),
+    "or_relu_bwd_f64": (None, [_p, _p, _p, _i64]),
+    "or_div_bwd_f64": (None, [_p, _p, _p, _p, _p, _i64]),
+    "or_add_row_bias_f64": (None, [_p, _p, _p, _i32, _i32]),
+    "or_sum_rows_f64": (None, [_p, _p, _i32, _i32]),
+    "or_index_f64": (_i32, [_p, _p, _i32, _p, _p]),
+    "or_index_bwd_f64": (_i32, [C.c_double, _p, _p, _i32, _p]),
+    "or_sum_f64": (C.c_double, [_p, _i64]),
+    "or_mean_f64": (C.c_double, [_p, _i64]),
+    "or_max_of_f64": (C.c_double, [_p, _i64]),
+    "or_argmax_f64": (_i64, [_p, _i64]),
 }
 
 _lib = None
@@ -355,3 +379,110 @@ def xor_tensor_train(steps: int = 4000, lr: float = 1.0) -> np.ndarray:
     out = np.empty(4, np.float32)
     lib().or_xor_tensor_train(steps, lr, _ptr(out))
     return out
+
+
+# ---- f64 forms (Tensor<f64, ...>) --------------------------------------------------
+
+def _f64(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float64)
+
+
+def matmul_f64(A, B, trans_a=False, trans_b=False, threads: int = 1) -> np.ndarray:
+    A, B = _f64(A), _f64(B)
+    M, K = (A.shape[1], A.shape[0]) if trans_a else A.shape
+    N = B.shape[0] if trans_b else B.shape[1]
+    C_ = np.empty((M, N), np.float64)
+    lib().or_matmul_f64_mt(_ptr(A), _ptr(B), _ptr(C_), M, N, K, int(trans_a), int(trans_b), max(1, threads))
+    return C_
+
+
+def matmul_f64_rows(A, B, M, N, K, row0, row1, trans_a=False, trans_b=False) -> np.ndarray:
+    """Rows [row0,row1) of the f64 product."""
+    A, B = _f64(A), _f64(B)
+    C_ = np.empty((M, N), np.float64)
+    lib().or_matmul_f64_rows(_ptr(A), _ptr(B), _ptr(C_), M, N, K, int(trans_a), int(trans_b), row0, row1)
+    return C_[row0:row1]
+
+
+def _map1_64(name, a):
+    a = _f64(a)
+    out = np.empty_like(a)
+    getattr(lib(), name)(_ptr(a), _ptr(out), a.size)
+    return out
+
+
+def _map2_64(name, a, b):
+    a, b = _f64(a), _f64(b)
+    out = np.empty_like(a)
+    getattr(lib(), name)(_ptr(a), _ptr(b), _ptr(out), a.size)
+    return out
+
+
+def add_f64(a, b): return _map2_64("or_add_f64", a, b)
+def sub_f64(a, b): return _map2_64("or_sub_f64", a, b)
+def mul_f64(a, b): return _map2_64("or_mul_f64", a, b)
+def div_f64(a, b): return _map2_64("or_div_f64", a, b)
+def neg_f64(a): return _map1_64("or_neg_f64", a)
+def relu_f64(a): return _map1_64("or_relu_f64", a)
+def sigmoid_f64(a): return _map1_64("or_sigmoid_f64", a)
+def tanh_f64(a): return _map1_64("or_tanh_f64", a)
+def sigmoid_bwd_f64(s, g): return _map2_64("or_sigmoid_bwd_f64", s, g)
+def tanh_bwd_f64(t, g): return _map2_64("or_tanh_bwd_f64", t, g)
+def relu_bwd_f64(x, g): return _map2_64("or_relu_bwd_f64", x, g)
+
+
+def div_bwd_f64(a, b, g):
+    a, b, g = _f64(a), _f64(b), _f64(g)
+    da, db = np.empty_like(a), np.empty_like(a)
+    lib().or_div_bwd_f64(_ptr(a), _ptr(b), _ptr(g), _ptr(da), _ptr(db), a.size)
+    return da, db
+
+
+def add_row_bias_f64(a, bias) -> np.ndarray:
+    a, bias = _f64(a), _f64(bias)
+    out = np.empty_like(a)
+    lib().or_add_row_bias_f64(_ptr(a), _ptr(bias), _ptr(out), a.shape[0], a.shape[1])
+    return out
+
+
+def sum_rows_f64(g) -> np.ndarray:
+    g = _f64(g)
+    out = np.empty(g.shape[1], np.float64)
+    lib().or_sum_rows_f64(_ptr(g), _ptr(out), g.shape[0], g.shape[1])
+    return out
+
+
+def index_f64(t, idx) -> float:
+    t = _f64(t)
+    dims, ix = _dims_idx(t.shape, idx)
+    out = np.zeros(1, np.float64)
+    if lib().or_index_f64(_ptr(t), _ptr(dims), dims.size, _ptr(ix), _ptr(out)) != 0:
+        raise IndexError(f"index {tuple(idx)} outside shape {t.shape}")
+    return float(out[0])
+
+
+def index_bwd_f64(g: float, dt: np.ndarray, idx) -> None:
+    assert dt.dtype == np.float64 and dt.flags["C_CONTIGUOUS"]
+    dims, ix = _dims_idx(dt.shape, idx)
+    if lib().or_index_bwd_f64(g, _ptr(dt), _ptr(dims), dims.size, _ptr(ix)) != 0:
+        raise IndexError(f"index {tuple(idx)} outside shape {dt.shape}")
+
+
+def sum_f64(v) -> float:
+    v = _f64(v)
+    return float(lib().or_sum_f64(_ptr(v), v.size))
+
+
+def mean_f64(v) -> float:
+    v = _f64(v)
+    return float(lib().or_mean_f64(_ptr(v), v.size))
+
+
+def max_of_f64(v) -> float:
+    v = _f64(v)
+    return float(lib().or_max_of_f64(_ptr(v), v.size))
+
+
+def argmax_f64(v) -> int:
+    v = _f64(v)
+    return int(lib().or_argmax_f64(_ptr(v), v.size))

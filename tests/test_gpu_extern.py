@@ -130,3 +130,33 @@ def test_escape_grid(externs, oracle):
         assert out is out0 and np.array_equal(out.reshape(h, w), ref.astype(np.int32))
         total = call_lowered(externs["cleave_hip_sum_i32_i64_host"], [out])
         assert total == int(ref.sum(dtype=np.int64))
+
+
+def test_f64_declarations(externs, oracle):
+    # the Tensor<f64> impls of the same blocks: reductions, IndexAt, MatMulInto, MapInto
+    rng = np.random.default_rng(93)
+    x = rng.standard_normal(20011) * 2 + 0.1
+    tol = 2e-14 * np.sqrt(x.size) * np.abs(x).sum()
+    assert abs(call_lowered(externs["cleave_hip_sum_f64_host"], [x]) - oracle.sum_f64(x)) <= tol
+    assert abs(call_lowered(externs["cleave_hip_mean_f64_host"], [x]) - oracle.mean_f64(x)) <= tol / x.size
+    assert call_lowered(externs["cleave_hip_max_of_f64_host"], [x]) == oracle.max_of_f64(x)
+    assert call_lowered(externs["cleave_hip_argmax_f64_host"], [x]) == oracle.argmax_f64(x)
+    t = rng.standard_normal((4, 3, 5))
+    got = call_lowered(externs["cleave_hip_index_f64_host"], [t.ravel(), np.array([4, 3, 5], np.int32),
+                                                              np.array([3, 1, 4], np.int32)])
+    assert got == t[3, 1, 4]
+    M, N, K = 45, 70, 33
+    A, B = rng.standard_normal((M, K)), rng.standard_normal((K, N))
+    c0 = np.zeros(M * N)
+    c = call_lowered(externs["cleave_hip_matmul_f64_into"], [c0, A.ravel(), B.ravel(), M, N, K, 0, 0])
+    assert c is c0
+    ref = oracle.matmul_f64(A, B)
+    err = np.max(np.abs(c.reshape(M, N) - ref) / (np.abs(A) @ np.abs(B)))
+    assert err <= 2e-14 * np.sqrt(K)
+    a, b = rng.standard_normal(999), rng.standard_normal(999) + 3
+    for op, f in {"add": oracle.add_f64, "sub": oracle.sub_f64, "mul": oracle.mul_f64, "div": oracle.div_f64,
+                  "relu_bwd": oracle.relu_bwd_f64}.items():
+        out = call_lowered(externs[f"cleave_hip_{op}_f64_into"], [np.zeros(999), a, b])
+        assert np.array_equal(out, f(a, b)), op
+    out = call_lowered(externs["cleave_hip_sigmoid_f64_into"], [np.zeros(999), a])
+    assert rel_close(out, oracle.sigmoid_f64(a), rtol=1e-14)
