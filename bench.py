@@ -13,6 +13,7 @@ Prints ONE JSON line on stdout:
                of the same product, extrapolated to GFLOP/s
   secondary    the other BASELINE configs (f32 256^3, bf16 8192^3, batched bf16,
                f32 A B^T / A^T B, MLP steps/s, escape-count map, u64 count sum), the
+               config-2 product on Tensor<f64> (vs 78.6 TFLOP/s FP64 MFMA), the
                MLP step through the reverse-mode tape, a matrix-vector product, and
                the maps, reductions and row-broadcast bias, each with its own
                HIP-event roofline figure and (unless --no-cpu) a single-core CPU
@@ -38,6 +39,7 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense FP32 matrix
 PEAK_BF16_MFMA = 2516.6  # TFLOP/s, MI355X dense BF16 matrix
+PEAK_FP64_MFMA = 78.6  # TFLOP/s, MI355X dense FP64 matrix
 MANDEL_VALU_PER_ITER = 8  # 7 arithmetic (2p + ci as one exact fma) + the escape compare, per iteration
 PEAK_FP32_VALU_NOFMA = 78.6  # T op/s: MI355X FP32 vector peak 157.3 TFLOP/s counts an FMA as 2; one non-FMA op per lane-cycle is half
 PEAK_HBM = 8000.0  # GB/s
@@ -216,6 +218,11 @@ def cpu_secondary(orc, name, budget_s, **kw):
         rows, dt = cpu_rows(lambda r0, r1: orc.matmul_rows(A, B, n, n, n, r0, r1, ta, tb), n, budget_s)
         return _cpu_entry(round(2.0 * rows * n * n / dt / 1e9, 4), "GFLOP/s",
                           f"rows 1..{rows} of the {n}^3 product, restated k-ascending loop, {dt:.1f} s")
+    if name == "gemm_f64_4096":
+        A, B, n = kw["A"], kw["B"], kw["n"]
+        rows, dt = cpu_rows(lambda r0, r1: orc.matmul_f64_rows(A, B, n, n, n, r0, r1), n, budget_s)
+        return _cpu_entry(round(2.0 * rows * n * n / dt / 1e9, 4), "GFLOP/s",
+                          f"rows 1..{rows} of the {n}^3 f64 product, restated k-ascending loop, {dt:.1f} s")
     if name == "gemm_bf16_8192":
         A, B, m = kw["A"], kw["B"], kw["m"]
         rows, dt = cpu_rows(lambda r0, r1: orc.matmul_bf16_rows(A, B, m, m, m, r0, r1), m, budget_s)
@@ -388,11 +395,13 @@ def gemm_bf16_batched_layouts(ca, layouts, steps):
 
 def gemm_shapes(ca, specs, steps):
     """One product per spec "dtype:MxNxK:layout", or a batch of them as
-    "dtype:BxMxNxK:layout" (dtype f32 or bf16, layout nn/nt/tn/tt for op(A)
+    "dtype:BxMxNxK:layout" (dtype f32, bf16 or f64, layout nn/nt/tn/tt for op(A)
     op(B)), timed with HIP events after a 0.3 s warm-up.  Reports TFLOP/s and
     the compulsory HBM bytes (A and B read once, f32 C written once) as a
     fraction of peak.  For comparing kernels and for kernel traces of one
     shape at a time."""
+    import numpy as np
+
     out = {}
     for spec in specs:
         dt, dims, lay = spec.split(":")
@@ -400,15 +409,20 @@ def gemm_shapes(ca, specs, steps):
         bs, (m, n, k) = (d[0], d[1:]) if len(d) == 4 else (1, d)
         lead = (bs,) if len(d) == 4 else ()
         ta, tb = lay[0] == "t", lay[1] == "t"
-        a = ca.fill_normal(ca.empty(lead + ((k, m) if ta else (m, k))), seed=11)
-        b = ca.fill_normal(ca.empty(lead + ((n, k) if tb else (k, n))), seed=12)
+        if dt == "f64":
+            rng = np.random.default_rng(11)
+            a = ca.from_numpy(rng.standard_normal(lead + ((k, m) if ta else (m, k))))
+            b = ca.from_numpy(rng.standard_normal(lead + ((n, k) if tb else (k, n))))
+        else:
+            a = ca.fill_normal(ca.empty(lead + ((k, m) if ta else (m, k))), seed=11)
+            b = ca.fill_normal(ca.empty(lead + ((n, k) if tb else (k, n))), seed=12)
         if dt == "bf16":
             a, b = ca.to_bf16(a), ca.to_bf16(b)
-        elif dt != "f32":
+        elif dt not in ("f32", "f64"):
             raise ValueError(f"unknown dtype in {spec!r}")
-        c = ca.empty(lead + (m, n))
-        esz = 2 if dt == "bf16" else 4
-        hbm = bs * ((m * k + k * n) * esz + m * n * 4)
+        c = ca.empty(lead + (m, n), "f64" if dt == "f64" else "f32")
+        esz = {"bf16": 2, "f32": 4, "f64": 8}[dt]
+        hbm = bs * ((m * k + k * n) * esz + m * n * (8 if dt == "f64" else 4))
         mm = ca.matmul_batched if lead else ca.matmul
         _, ev = timed(ca, lambda: mm(a, b, trans_a=ta, trans_b=tb, out=c), steps, 3, 0.3)
         out[spec] = {"kernel_ms": round(ev, 5), "TFLOP/s": round(2.0 * bs * m * n * k / (ev * 1e-3) / 1e12, 2),
@@ -569,6 +583,20 @@ def main():
             if want_cpu:
                 secondary[name]["cpu_baseline"] = cpu_secondary(orc, name, cb, A=A_host, B=B_host, n=n, ta=ta, tb=tb)
         del c
+        # Tensor<f64>: the config-2 product in f64 on the f64 matrix cores
+        rng64 = np.random.default_rng(103)
+        a64 = ca.from_numpy(rng64.standard_normal((n, n)))
+        b64 = ca.from_numpy(rng64.standard_normal((n, n)))
+        c64 = ca.empty((n, n), "f64")
+        wall_s, ev = timed(ca, lambda: ca.matmul(a64, b64, out=c64), max(10, sec_steps // 2), 2, 0.3)
+        ach = flop / (ev * 1e-3) / 1e12
+        secondary["gemm_f64_4096"] = {"GFLOP/s": round(flop * max(10, sec_steps // 2) / wall_s / 1e9, 1),
+                                      "kernel_ms": round(ev, 4), "frac_fp64_mfma": round(ach / PEAK_FP64_MFMA, 4)}
+        log(f"gemm_f64_4096: {ach:.1f} TFLOP/s")
+        if want_cpu:
+            secondary["gemm_f64_4096"]["cpu_baseline"] = cpu_secondary(orc, "gemm_f64_4096", cb, A=a64.numpy(),
+                                                                       B=b64.numpy(), n=n)
+        del a64, b64, c64
         # bf16 8192^3
         m = 8192
         a32 = ca.fill_normal(ca.empty((m, m)), seed=201, std=0.02)

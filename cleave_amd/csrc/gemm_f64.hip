@@ -20,7 +20,8 @@
 // loads are issued before the current tile's MFMAs and written to the other
 // stage after them, one barrier per tile.  Both operands sit in LDS k-major
 // ([k][m] and [k][n], rows padded to 144 doubles so the two 16-lane row
-// groups of a half-wave read opposite bank halves).  Global loads are 16-byte
+// groups of a half-wave read opposite bank halves, columns swizzled per k-row
+// pair, lds_col).  Global loads are 16-byte
 // vectors along whichever index is contiguous in memory when that extent is
 // even, single doubles otherwise; out-of-range elements load as zero, so any
 // M, N, K (K = 0 included: C = 0, the zero-filled accumulator of
@@ -36,6 +37,17 @@ typedef double d2 __attribute__((ext_vector_type(2)));
 constexpr int kThreads = 256;
 constexpr int BM = 128, BN = 128, BK = 16;
 constexpr int kPitch = 144;  // LDS row pitch in doubles: 1152 B, 128 B mod 256
+
+// LDS column of output index r in k-row k.  A k-contiguous operand is stored
+// transposed: the 64 lanes of one store instruction cover 8 k-rows (8 lanes
+// each) at 8 columns, and with a 144-double pitch every even k-row starts on
+// the same bank, an 8-way conflict.  XOR-ing the column with 8 * ((k / 2) % 8)
+// spreads those lanes over all 32 double slots of a 256-byte bank cycle (2
+// passes for 512 bytes).  The XOR only moves 8-double groups, so the 16 lanes
+// of an MFMA operand read still see one aligned 128-byte block per k-row, and
+// k-rows 2j and 2j + 1 (one half-wave) share the XOR and stay 128 bytes apart
+// modulo 256.  A 16-byte pair (r, r + 1), r even, stays adjacent.
+__device__ __forceinline__ int lds_col(int k, int r) { return r ^ (((k >> 1) & 7) << 3); }
 
 // Global -> register staging of one operand tile (R rows of the output
 // dimension by BK along k).  KC: the operand is k-contiguous in memory (A
@@ -79,13 +91,13 @@ struct TileLoad {
             if constexpr (KC) {
                 const int r = c / (BK / V), k = (c % (BK / V)) * V;
 #pragma unroll
-                for (int e = 0; e < V; ++e) s[(k + e) * kPitch + r] = v[V * i + e];
+                for (int e = 0; e < V; ++e) s[(k + e) * kPitch + lds_col(k + e, r)] = v[V * i + e];
             } else {
                 const int k = c / (BM / V), r = (c % (BM / V)) * V;
                 if constexpr (V == 2)
-                    *reinterpret_cast<d2*>(s + k * kPitch + r) = d2{v[2 * i], v[2 * i + 1]};
+                    *reinterpret_cast<d2*>(s + k * kPitch + lds_col(k, r)) = d2{v[2 * i], v[2 * i + 1]};
                 else
-                    s[k * kPitch + r] = v[i];
+                    s[k * kPitch + lds_col(k, r)] = v[i];
             }
         }
     }
@@ -143,9 +155,9 @@ __global__ __launch_bounds__(kThreads) void gemm_f64_kernel(const double* __rest
         for (int ks = 0; ks < BK; ks += 4) {
             double a[4], bv[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = as[(ks + lk) * kPitch + wm + 16 * i + lr];
+            for (int i = 0; i < 4; ++i) a[i] = as[(ks + lk) * kPitch + lds_col(ks + lk, wm + 16 * i + lr)];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) bv[j] = bs[(ks + lk) * kPitch + wn + 16 * j + lr];
+            for (int j = 0; j < 4; ++j) bv[j] = bs[(ks + lk) * kPitch + lds_col(ks + lk, wn + 16 * j + lr)];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
