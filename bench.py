@@ -448,6 +448,60 @@ def calibrate_copy(ca, steps):
                       "kernel_ms": round(ev, 4), "GB/s": round(gbs, 1)}), flush=True)
 
 
+def mlp_lines(ca, steps, secondary, want_cpu, cb, orc):
+    """the fused MLP step and the same step through the
+    reverse-mode tape, into `secondary`."""
+    import numpy as np
+
+    # MLP step (config 4)
+    B_, D_, H_ = 65536, 1024, 4096
+    x = ca.fill_normal(ca.empty((B_, D_)), seed=401)
+    yv = ca.fill_bernoulli(ca.empty(B_), seed=402)
+    lim1 = float(np.sqrt(6.0 / (D_ + H_)))
+    lim2 = float(np.sqrt(6.0 / (H_ + 1)))
+    w1 = ca.fill_uniform(ca.empty((D_, H_)), seed=403, lo=-lim1, hi=lim1)
+    w2 = ca.fill_uniform(ca.empty(H_), seed=404, lo=-lim2, hi=lim2)
+    loss = ca.empty(1)
+    mlp_steps = max(5, steps // 5)
+    wall_s, ev = timed(ca, lambda: ca.mlp_step(x, yv, w1, w2, 0.01, loss=loss), mlp_steps, 2, 0.3)
+    gemm_fl = 2.0 * B_ * D_ * H_ * 2 + 4.0 * B_ * H_
+    secondary["mlp_step_65536x1024x4096"] = {
+        "steps_per_s": round(mlp_steps / wall_s, 3), "ms_per_step": round(ev, 3),
+        "gemm_TFLOP/s": round(gemm_fl / (ev * 1e-3) / 1e12, 2),
+        "loss_after": float(loss.numpy()[0])}
+    log(f"mlp step: {mlp_steps / wall_s:.2f} steps/s ({ev:.2f} ms)")
+    if want_cpu:
+        secondary["mlp_step_65536x1024x4096"]["cpu_baseline"] = cpu_secondary(
+            orc, "mlp_step_65536x1024x4096", cb, X=x.numpy(), y=yv.numpy(), W1=w1.numpy(), W2=w2.numpy(), B=B_)
+    # The same step written as a program of the library's operators and
+    # differentiated by the reverse-mode tape (cleave_amd.autograd).  The tape
+    # runs the hidden layer sigmoid(X W1) w2 and its reverse rule as the fused
+    # step's kernels; the output sigmoid, the error, the mean, their rules and
+    # the two SGD updates are separate launches.
+    from cleave_amd import autograd as ad
+    fused_ms = ev
+    X_, Y_ = ad.const(x), ad.const(yv.view((B_, 1)))
+    w2c = w2.view((H_, 1))
+
+    def tape_step():
+        W1, W2 = ad.param(w1), ad.param(w2c)
+        e = ad.sigmoid(ad.sigmoid(X_ @ W1) @ W2) - Y_
+        ad.backward(ad.mean(e * e))
+        ca.sgd_update(w1, W1.grad, 0.01)
+        ca.sgd_update(w2c, W2.grad, 0.01)
+
+    wall_s, ev = timed(ca, tape_step, mlp_steps, 2, 0.3)
+    secondary["mlp_step_tape_65536x1024x4096"] = {
+        "steps_per_s": round(mlp_steps / wall_s, 3), "ms_per_step": round(ev, 3),
+        "gemm_TFLOP/s": round(gemm_fl / (ev * 1e-3) / 1e12, 2),
+        "fused_over_tape": round(fused_ms / ev, 3),
+        "note": "reverse-mode derive() over a tape (cleave_amd.autograd), its hidden layer on the fused "
+                "kernels; the CPU baseline is mlp_step_65536x1024x4096's, the same step"}
+    log(f"mlp step through the tape: {mlp_steps / wall_s:.2f} steps/s ({ev:.2f} ms)")
+    del X_, Y_, w2c
+    del x, yv, w1, w2
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -470,6 +524,7 @@ def main():
                          "(e.g. f32:2048x2048x2048:nn)")
     ap.add_argument("--host-boundary", action="store_true",
                     help="only time the _host entry points (host arrays across the C ABI, PCIe included)")
+    ap.add_argument("--mlp", action="store_true", help="only time the MLP step, fused and through the tape")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run the copy kernel used to scale rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
@@ -507,6 +562,11 @@ def main():
         return
     if args.host_boundary:
         print(json.dumps({"host_boundary": host_boundary(steps)}), flush=True)
+        return
+    if args.mlp:
+        out = {}
+        mlp_lines(ca, steps, out, False, 0.0, None)
+        print(json.dumps({"mlp": out}), flush=True)
         return
 
     # ---- headline: f32 4096^3 NN --------------------------------------------
@@ -645,53 +705,7 @@ def main():
             secondary["gemm_bf16_batched_64x512"]["cpu_baseline"] = cpu_secondary(
                 orc, "gemm_bf16_batched_64x512", cb, A=xb.numpy()[0], B=yb.numpy()[0], bs=bs, k=k)
         del xb, yb, zb
-        # MLP step (config 4)
-        B_, D_, H_ = 65536, 1024, 4096
-        x = ca.fill_normal(ca.empty((B_, D_)), seed=401)
-        yv = ca.fill_bernoulli(ca.empty(B_), seed=402)
-        lim1 = float(np.sqrt(6.0 / (D_ + H_)))
-        lim2 = float(np.sqrt(6.0 / (H_ + 1)))
-        w1 = ca.fill_uniform(ca.empty((D_, H_)), seed=403, lo=-lim1, hi=lim1)
-        w2 = ca.fill_uniform(ca.empty(H_), seed=404, lo=-lim2, hi=lim2)
-        loss = ca.empty(1)
-        mlp_steps = max(5, steps // 5)
-        wall_s, ev = timed(ca, lambda: ca.mlp_step(x, yv, w1, w2, 0.01, loss=loss), mlp_steps, 2, 0.3)
-        gemm_fl = 2.0 * B_ * D_ * H_ * 2 + 4.0 * B_ * H_
-        secondary["mlp_step_65536x1024x4096"] = {
-            "steps_per_s": round(mlp_steps / wall_s, 3), "ms_per_step": round(ev, 3),
-            "gemm_TFLOP/s": round(gemm_fl / (ev * 1e-3) / 1e12, 2),
-            "loss_after": float(loss.numpy()[0])}
-        log(f"mlp step: {mlp_steps / wall_s:.2f} steps/s ({ev:.2f} ms)")
-        if want_cpu:
-            secondary["mlp_step_65536x1024x4096"]["cpu_baseline"] = cpu_secondary(
-                orc, "mlp_step_65536x1024x4096", cb, X=x.numpy(), y=yv.numpy(), W1=w1.numpy(), W2=w2.numpy(), B=B_)
-        # The same step written as a program of the library's operators and
-        # differentiated by the reverse-mode tape (cleave_amd.autograd): the
-        # GEMMs, sigmoid maps and their reverse rules, the N = 1 and K = 1
-        # products of the second layer, the mean, and two SGD updates, each a
-        # separate launch.
-        from cleave_amd import autograd as ad
-        fused_ms = ev
-        X_, Y_ = ad.const(x), ad.const(yv.view((B_, 1)))
-        w2c = w2.view((H_, 1))
-
-        def tape_step():
-            W1, W2 = ad.param(w1), ad.param(w2c)
-            e = ad.sigmoid(ad.sigmoid(X_ @ W1) @ W2) - Y_
-            ad.backward(ad.mean(e * e))
-            ca.sgd_update(w1, W1.grad, 0.01)
-            ca.sgd_update(w2c, W2.grad, 0.01)
-
-        wall_s, ev = timed(ca, tape_step, mlp_steps, 2, 0.3)
-        secondary["mlp_step_tape_65536x1024x4096"] = {
-            "steps_per_s": round(mlp_steps / wall_s, 3), "ms_per_step": round(ev, 3),
-            "gemm_TFLOP/s": round(gemm_fl / (ev * 1e-3) / 1e12, 2),
-            "fused_over_tape": round(fused_ms / ev, 3),
-            "note": "reverse-mode derive() over a tape of separate launches (cleave_amd.autograd); the CPU "
-                    "baseline is mlp_step_65536x1024x4096's, the same step"}
-        log(f"mlp step through the tape: {mlp_steps / wall_s:.2f} steps/s ({ev:.2f} ms)")
-        del X_, Y_, w2c
-        del x, yv, w1, w2
+        mlp_lines(ca, steps, secondary, want_cpu, cb, orc if want_cpu else None)
         # a matrix-vector product (a2 at N = 1: the reference's matmul by a
         # column vector, gemv.hip), HBM-bound on the matrix
         mv_m, mv_k = 65536, 4096

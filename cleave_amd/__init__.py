@@ -13,6 +13,7 @@ program calls (/root/reference/stdlib/linalg/{tensor,matrix}.cleave,
     index, index_bwd                 Index + its derivative  tensor.cleave:113-133
     escape_counts                    escape_count over a grid, examples/mandelbrot.cleave:14-26
     mlp_step                         SGD step, examples/xor_tensor.cleave:38-92 style
+    sigmoid_hidden_fwd / _bwd        that step's hidden layer, z = sigmoid(X W1) w2, and its rule
 
 Errors raise CleaveHipError (the ABI returns a negative status instead of
 aborting once the binding switches abort-on-error off).
@@ -31,7 +32,7 @@ __all__ = [
     "matmul", "matmul_batched", "add", "sub", "mul", "div", "neg", "zero", "relu", "sigmoid",
     "tanh", "sigmoid_bwd", "tanh_bwd", "relu_bwd", "div_bwd", "sgd_update", "sum", "mean",
     "max_of", "argmax", "sum_u64", "index", "index_bwd", "reduce_sum", "reduce_max", "reduce_sum_u64", "escape_counts", "mlp_step", "fill_uniform", "fill_normal",
-    "fill_bernoulli", "to_bf16", "Timer", "symbol_table",
+    "fill_bernoulli", "to_bf16", "Timer", "symbol_table", "sigmoid_hidden_fwd", "sigmoid_hidden_bwd",
 ]
 
 _DTYPES = {"f32": (np.float32, 4), "f64": (np.float64, 8), "bf16": (np.uint16, 2), "u32": (np.uint32, 4),
@@ -357,6 +358,30 @@ def mlp_step(x: Tensor, y: Tensor, w1: Tensor, w2: Tensor, lr: float,
          w2.size, dw1.ptr if dw1 else None, dw1.size if dw1 else 0,
          dw2.ptr if dw2 else None, dw2.size if dw2 else 0, loss.ptr if loss else None,
          B, D, Hd, float(lr))
+
+
+def sigmoid_hidden_fwd(x: Tensor, w1: Tensor, w2: Tensor, h: Tensor | None = None,
+                       z: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """H = sigmoid(X W1) and z = H w2 (w2 a column of Hd): the MLP step's fused
+    forward kernels as one layer.  Returns (H, z)."""
+    B, D = x.shape
+    Hd = w1.shape[1]
+    h = h if h is not None else empty((B, Hd))
+    z = z if z is not None else empty((B, 1))
+    call("cleave_hip_sigmoid_hidden_fwd_f32", x.ptr, x.size, w1.ptr, w1.size, w2.ptr, w2.size, h.ptr, h.size,
+         z.ptr, z.size, B, D, Hd)
+    return h, z
+
+
+def sigmoid_hidden_bwd(x: Tensor, h: Tensor, w2: Tensor, g: Tensor, dw1: Tensor | None = None,
+                       dw2: Tensor | None = None) -> None:
+    """Reverse rule of z = sigmoid(X W1) w2 given H and g = dL/dz: dW1 = X^T d1 and
+    dW2 = H^T g, d1 = (g w2^T) H(1 - H).  Either output may be None."""
+    B, D = x.shape
+    Hd = h.shape[1]
+    call("cleave_hip_sigmoid_hidden_bwd_f32", x.ptr, x.size, h.ptr, h.size, w2.ptr, w2.size, g.ptr, g.size,
+         dw1.ptr if dw1 else None, dw1.size if dw1 else 0, dw2.ptr if dw2 else None, dw2.size if dw2 else 0,
+         B, D, Hd)
 
 
 # ---- synthetic inputs ------------------------------------------------------------

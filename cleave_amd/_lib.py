@@ -206,6 +206,8 @@ SIGNATURES: dict[str, tuple] = {
     "cleave_hip_sigmoid_bwd_f64_into": (i64, [vp, i64, vp, i64, vp, i64]),
     "cleave_hip_tanh_bwd_f64_into": (i64, [vp, i64, vp, i64, vp, i64]),
     "cleave_hip_relu_bwd_f64_into": (i64, [vp, i64, vp, i64, vp, i64]),
+    "cleave_hip_sigmoid_hidden_fwd_f32": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32]),
+    "cleave_hip_sigmoid_hidden_bwd_f32": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32]),
     # memref-descriptor forms: every tensor argument is a pointer to an
     # unranked descriptor {int64 rank; void* ranked descriptor}
     "_mlir_ciface_cleave_hip_matmul_f32": (i32, [vp, vp, vp]),

@@ -44,16 +44,9 @@ __global__ __launch_bounds__(kThreads) void sigmoid_inplace_kernel(float* __rest
     if (blockIdx.x == 0 && threadIdx.x < (n & 3)) h[nv * 4 + threadIdx.x] = sigmoidf_ref(h[nv * 4 + threadIdx.x]);
 }
 
-// One wave per row: z2 = H[m,:] . W2, then the per-row loss pieces.
-__global__ __launch_bounds__(kThreads) void row_pass_kernel(const float* __restrict__ H,
-                                                            const float* __restrict__ W2,
-                                                            const float* __restrict__ y, int B,
-                                                            int Hd, float* __restrict__ sq,
-                                                            float* __restrict__ d2) {
+// H[row,:] . W2 by one wave (every lane returns the sum).
+__device__ __forceinline__ float row_dot(const float* __restrict__ h, const float* __restrict__ W2, int Hd) {
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-    if (row >= B) return;
-    const float* h = H + (int64_t)row * Hd;
     float acc = 0.0f;
     if ((Hd & 3) == 0) {
         for (int c = lane * 4; c < Hd; c += 256) {
@@ -66,6 +59,19 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(const float* __restr
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+    return acc;
+}
+
+// One wave per row: z2 = H[m,:] . W2, then the per-row loss pieces.
+__global__ __launch_bounds__(kThreads) void row_pass_kernel(const float* __restrict__ H,
+                                                            const float* __restrict__ W2,
+                                                            const float* __restrict__ y, int B,
+                                                            int Hd, float* __restrict__ sq,
+                                                            float* __restrict__ d2) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (row >= B) return;
+    const float acc = row_dot(H + (int64_t)row * Hd, W2, Hd);
     if (lane == 0) {
         float yh = sigmoidf_ref(acc);
         float e = yh - y[row];
@@ -81,6 +87,22 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(const float* __restr
 // errors into sqpart[block] (wave shuffles, then the 4 wave sums in order),
 // which loss_kernel adds up.
 constexpr int kPartUnroll = 8;
+
+// The P partials of row `row` of H W2, added in order (eight loads in flight).
+__device__ __forceinline__ float sum_row_partials(const float* __restrict__ zpart, int P, int B, int row) {
+    float z = zpart[row];
+    int p = 1;
+    for (; p + kPartUnroll <= P; p += kPartUnroll) {
+        float v[kPartUnroll];
+#pragma unroll
+        for (int u = 0; u < kPartUnroll; ++u) v[u] = zpart[(int64_t)(p + u) * B + row];
+#pragma unroll
+        for (int u = 0; u < kPartUnroll; ++u) z += v[u];
+    }
+    for (; p < P; ++p) z += zpart[(int64_t)p * B + row];
+    return z;
+}
+
 __global__ __launch_bounds__(kThreads) void row_finish_kernel(const float* __restrict__ zpart, int P,
                                                               const float* __restrict__ y, int B,
                                                               float* __restrict__ sqpart,
@@ -89,16 +111,7 @@ __global__ __launch_bounds__(kThreads) void row_finish_kernel(const float* __res
     const int row = blockIdx.x * kThreads + threadIdx.x;
     float sq = 0.0f;
     if (row < B) {
-        float z = zpart[row];
-        int p = 1;
-        for (; p + kPartUnroll <= P; p += kPartUnroll) {
-            float v[kPartUnroll];
-#pragma unroll
-            for (int u = 0; u < kPartUnroll; ++u) v[u] = zpart[(int64_t)(p + u) * B + row];
-#pragma unroll
-            for (int u = 0; u < kPartUnroll; ++u) z += v[u];
-        }
-        for (; p < P; ++p) z += zpart[(int64_t)p * B + row];
+        const float z = sum_row_partials(zpart, P, B, row);
         const float yh = sigmoidf_ref(z);
         const float e = yh - y[row];
         sq = e * e;
@@ -116,10 +129,26 @@ __global__ __launch_bounds__(kThreads) void row_finish_kernel(const float* __res
     }
 }
 
+// The hidden layer's z = H W2 alone: from the fused GEMM's partials (the z of
+// row_finish_kernel), or one wave per row (the z of row_pass_kernel).
+__global__ __launch_bounds__(kThreads) void z_finish_kernel(const float* __restrict__ zpart, int P, int B,
+                                                            float* __restrict__ z) {
+    const int row = blockIdx.x * kThreads + threadIdx.x;
+    if (row < B) z[row] = sum_row_partials(zpart, P, B, row);
+}
+
+__global__ __launch_bounds__(kThreads) void row_dot_kernel(const float* __restrict__ H, const float* __restrict__ W2,
+                                                           int B, int Hd, float* __restrict__ z) {
+    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (row >= B) return;
+    const float acc = row_dot(H + (int64_t)row * Hd, W2, Hd);
+    if ((threadIdx.x & 63) == 0) z[row] = acc;
+}
+
 // Column pass: each thread owns 4 consecutive columns of a band of rows.
-// Writes d1 over H and one dW2 partial per (row band, column).
+// Writes d1 (over H when D1 is H) and one dW2 partial per (row band, column).
 constexpr int kRowsPerBand = 256;
-__global__ __launch_bounds__(kThreads) void col_pass_kernel(float* __restrict__ H,
+__global__ __launch_bounds__(kThreads) void col_pass_kernel(const float* H, float* D1,
                                                             const float* __restrict__ W2,
                                                             const float* __restrict__ d2, int B,
                                                             int Hd, float* __restrict__ part) {
@@ -131,13 +160,14 @@ __global__ __launch_bounds__(kThreads) void col_pass_kernel(float* __restrict__ 
     float w[4], s[4] = {0.f, 0.f, 0.f, 0.f};
     for (int j = 0; j < 4; ++j) w[j] = j < nc ? W2[c + j] : 0.0f;
     for (int r = r0; r < r1; ++r) {
-        float* h = H + (int64_t)r * Hd + c;
+        const float* h = H + (int64_t)r * Hd + c;
+        float* d1 = D1 + (int64_t)r * Hd + c;
         const float dm = d2[r];
         for (int j = 0; j < nc; ++j) {
             float hv = h[j];
             s[j] += hv * dm;
             float g = dm * w[j];
-            h[j] = g * hv * (1.0f - hv);
+            d1[j] = g * hv * (1.0f - hv);
         }
     }
     for (int j = 0; j < nc; ++j) part[(int64_t)blockIdx.y * Hd + c + j] = s[j];
@@ -303,6 +333,103 @@ int32_t fused_step(const float* x, const float* y, float* w1, float* w2, float* 
     return CLEAVE_HIP_OK;
 }
 
+// ---- the hidden layer alone: z = sigmoid(X W1) w2 and its reverse rule ----------
+// The same kernels as the step, for a host (the reverse-mode tape) that meets
+// this subgraph in a program: forward writes H and z; backward takes H and
+// g = dL/dz and writes dW1 = X^T d1, dW2 = H^T g with d1 = (g w2^T) H(1-H).
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+bool layer_fwd_fits(const float* x, const float* w1, const float* h, int B, int D, int Hd) {
+    return B % 256 == 0 && D % 256 == 0 && Hd % 256 == 0 && aligned16(x) && aligned16(w1) && aligned16(h) &&
+           FusedTile1::fits(B, Hd, D, D, Hd);
+}
+
+bool layer_bwd_fits(const float* x, const float* h, int B, int D, int Hd) {
+    return B % 256 == 0 && D % 256 == 0 && Hd % 256 == 0 && aligned16(x) && aligned16(h) &&
+           FusedTile2::fits(D, Hd, B / fused_splits(B, D, Hd), D, Hd);
+}
+
+int32_t hidden_fwd(const float* x, const float* w1, const float* w2, float* h, float* z, int B, int D, int Hd,
+                   hipStream_t st) {
+    if (layer_fwd_fits(x, w1, h, B, D, Hd)) {
+        const int P = (Hd / 256) * 4;
+        float* zpart = (float*)ch::scratch(4, sizeof(float) * (size_t)P * B);
+        if (!zpart) return CLEAVE_HIP_ERR_OOM;
+        ch::MlpFuse f1;
+        f1.w2 = w2;
+        f1.zpart = zpart;
+        ch::gemm_f32_pingpong_kernel<true, false, 1>
+            <<<dim3((unsigned)((B / 256) * (Hd / 256))), FusedTile1::THREADS, 0, st>>>(
+                x, w1, h, B, Hd, D, D, Hd, 0, 0, 0, B / 256, Hd / 256, 1, 1, f1);
+        CH_LAUNCHED("gemm_f32_pingpong_kernel(MODE 1)");
+        z_finish_kernel<<<(B + kThreads - 1) / kThreads, kThreads, 0, st>>>(zpart, P, B, z);
+        CH_LAUNCHED("z_finish_kernel");
+        return CLEAVE_HIP_OK;
+    }
+    int32_t rc = ch::gemm_f32_device(x, w1, h, B, Hd, D, 0, 0, 1);
+    if (rc != CLEAVE_HIP_OK) return rc;
+    const int64_t nH = (int64_t)B * Hd;
+    sigmoid_inplace_kernel<<<capped_grid(nH / 4 + 1), kThreads, 0, st>>>(h, nH);
+    CH_LAUNCHED("sigmoid_inplace_kernel");
+    row_dot_kernel<<<(B + 3) / 4, kThreads, 0, st>>>(h, w2, B, Hd, z);
+    CH_LAUNCHED("row_dot_kernel");
+    return CLEAVE_HIP_OK;
+}
+
+int32_t hidden_bwd(const float* x, const float* h, const float* w2, const float* g, float* dw1, float* dw2, int B,
+                   int D, int Hd, hipStream_t st) {
+    auto up = [](size_t n) { return (n + 63) & ~(size_t)63; };
+    if (layer_bwd_fits(x, h, B, D, Hd)) {
+        const int splits = fused_splits(B, D, Hd);
+        const int dw2_slices = splits * (D / 256) * 2;
+        const size_t nPart = (size_t)dw2_slices * Hd, nSl = (size_t)splits * D * Hd;
+        float* part = (float*)ch::scratch(4, sizeof(float) * (up(nPart) + up(nSl)));
+        if (!part) return CLEAVE_HIP_ERR_OOM;
+        float* slices = part + up(nPart);
+        const int kk = B / splits;
+        ch::MlpFuse f2;
+        f2.d2 = g;
+        f2.dw2part = part;
+        ch::gemm_f32_pingpong_kernel<false, false, 2>
+            <<<dim3((unsigned)((D / 256) * (Hd / 256) * splits)), FusedTile2::THREADS, 0, st>>>(
+                x, h, slices, D, Hd, kk, D, Hd, (int64_t)kk * D, (int64_t)kk * Hd, (int64_t)D * Hd, D / 256,
+                Hd / 256, splits, 1, f2);
+        CH_LAUNCHED("gemm_f32_pingpong_kernel(MODE 2)");
+        if (dw1) {
+            dw1_finish_kernel<<<dim3((unsigned)((Hd + kThreads - 1) / kThreads), (unsigned)(D < 1024 ? D : 1024)),
+                                kThreads, 0, st>>>(slices, splits, D, Hd, w2, dw1, nullptr, 0.0f);
+            CH_LAUNCHED("dw1_finish_kernel");
+        }
+        if (dw2) {
+            sum_slices_sgd_kernel<<<capped_grid(Hd), kThreads, 0, st>>>(part, dw2_slices, Hd, dw2, nullptr, 0.0f);
+            CH_LAUNCHED("sum_slices_sgd_kernel(dW2)");
+        }
+        return CLEAVE_HIP_OK;
+    }
+    const int splits = choose_splits(D, Hd, B);
+    const int bands = (B + kRowsPerBand - 1) / kRowsPerBand;
+    const size_t nH = (size_t)B * Hd, nPart = (size_t)bands * Hd, nSl = (size_t)splits * D * Hd;
+    float* d1 = (float*)ch::scratch(4, sizeof(float) * (up(nH) + up(nPart) + up(nSl)));
+    if (!d1) return CLEAVE_HIP_ERR_OOM;
+    float* part = d1 + up(nH);
+    float* slices = part + up(nPart);
+    dim3 cgrid((unsigned)((Hd + 4 * kThreads - 1) / (4 * kThreads)), (unsigned)bands);
+    col_pass_kernel<<<cgrid, kThreads, 0, st>>>(h, d1, w2, g, B, Hd, part);
+    CH_LAUNCHED("col_pass_kernel");
+    if (dw2) {
+        sum_slices_sgd_kernel<<<capped_grid(Hd), kThreads, 0, st>>>(part, bands, Hd, dw2, nullptr, 0.0f);
+        CH_LAUNCHED("sum_slices_sgd_kernel(dW2)");
+    }
+    if (dw1) {
+        int32_t rc = ch::gemm_f32_device(x, d1, slices, D, Hd, B, 1, 0, splits);
+        if (rc != CLEAVE_HIP_OK) return rc;
+        sum_slices_sgd_kernel<<<capped_grid((int64_t)D * Hd), kThreads, 0, st>>>(slices, splits, (int64_t)D * Hd,
+                                                                                  dw1, nullptr, 0.0f);
+        CH_LAUNCHED("sum_slices_sgd_kernel(dW1)");
+    }
+    return CLEAVE_HIP_OK;
+}
+
 }  // namespace
 
 extern "C" int32_t cleave_hip_mlp_step_f32(const float* x, int64_t xlen, const float* y,
@@ -356,7 +483,7 @@ extern "C" int32_t cleave_hip_mlp_step_f32(const float* x, int64_t xlen, const f
     loss_kernel<<<1, kThreads, 0, st>>>(sq, B, (float)B, loss_dev ? loss_dev : loss_tmp);
     CH_LAUNCHED("loss_kernel");
     dim3 cgrid((unsigned)((Hd + 4 * kThreads - 1) / (4 * kThreads)), (unsigned)bands);
-    col_pass_kernel<<<cgrid, kThreads, 0, st>>>(H, w2, d2, B, Hd, part);
+    col_pass_kernel<<<cgrid, kThreads, 0, st>>>(H, H, w2, d2, B, Hd, part);
     CH_LAUNCHED("col_pass_kernel");
     sum_slices_sgd_kernel<<<capped_grid(Hd), kThreads, 0, st>>>(part, bands, Hd, dw2, w2, lr);
     CH_LAUNCHED("sum_slices_sgd_kernel(dW2)");
@@ -365,4 +492,47 @@ extern "C" int32_t cleave_hip_mlp_step_f32(const float* x, int64_t xlen, const f
     sum_slices_sgd_kernel<<<capped_grid((int64_t)D * Hd), kThreads, 0, st>>>(slices, splits, (int64_t)D * Hd, dw1, w1, lr);
     CH_LAUNCHED("sum_slices_sgd_kernel(dW1)");
     return CLEAVE_HIP_OK;
+}
+
+extern "C" int32_t cleave_hip_sigmoid_hidden_fwd_f32(const float* x, int64_t xlen, const float* w1, int64_t w1len,
+                                                     const float* w2, int64_t w2len, float* h, int64_t hlen,
+                                                     float* z, int64_t zlen, int32_t B, int32_t D, int32_t Hd) {
+    const char* fn = "cleave_hip_sigmoid_hidden_fwd_f32";
+    CH_REQUIRE(B > 0 && D > 0 && Hd > 0, "%s: dims must be positive (B=%d D=%d Hd=%d)", fn, B, D, Hd);
+    CH_REQUIRE(xlen == (int64_t)B * D && w1len == (int64_t)D * Hd && w2len == Hd && hlen == (int64_t)B * Hd &&
+                   zlen == B,
+               "%s: lengths (%lld, %lld, %lld, %lld, %lld) do not match B=%d D=%d Hd=%d", fn, (long long)xlen,
+               (long long)w1len, (long long)w2len, (long long)hlen, (long long)zlen, B, D, Hd);
+    CH_REQUIRE(x && w1 && w2 && h && z, "%s: null buffer", fn);
+    CH_REQUIRE(aligned16(w2) && aligned16(h), "%s: w2 and h must be 16-byte aligned", fn);
+    CH_INIT_OR_RETURN();
+    CH_DEVICE(fn, x, xlen * 4);
+    CH_DEVICE(fn, w1, w1len * 4);
+    CH_DEVICE(fn, w2, w2len * 4);
+    CH_DEVICE(fn, h, hlen * 4);
+    CH_DEVICE(fn, z, zlen * 4);
+    return hidden_fwd(x, w1, w2, h, z, B, D, Hd, ch::stream());
+}
+
+extern "C" int32_t cleave_hip_sigmoid_hidden_bwd_f32(const float* x, int64_t xlen, const float* h, int64_t hlen,
+                                                     const float* w2, int64_t w2len, const float* g, int64_t glen,
+                                                     float* dw1, int64_t dw1len, float* dw2, int64_t dw2len,
+                                                     int32_t B, int32_t D, int32_t Hd) {
+    const char* fn = "cleave_hip_sigmoid_hidden_bwd_f32";
+    CH_REQUIRE(B > 0 && D > 0 && Hd > 0, "%s: dims must be positive (B=%d D=%d Hd=%d)", fn, B, D, Hd);
+    CH_REQUIRE(xlen == (int64_t)B * D && hlen == (int64_t)B * Hd && w2len == Hd && glen == B,
+               "%s: lengths (%lld, %lld, %lld, %lld) do not match B=%d D=%d Hd=%d", fn, (long long)xlen,
+               (long long)hlen, (long long)w2len, (long long)glen, B, D, Hd);
+    CH_REQUIRE(!dw1 || dw1len == (int64_t)D * Hd, "%s: dw1len %lld != D*Hd", fn, (long long)dw1len);
+    CH_REQUIRE(!dw2 || dw2len == Hd, "%s: dw2len %lld != Hd", fn, (long long)dw2len);
+    CH_REQUIRE(x && h && w2 && g, "%s: null buffer", fn);
+    CH_INIT_OR_RETURN();
+    CH_DEVICE(fn, x, xlen * 4);
+    CH_DEVICE(fn, h, hlen * 4);
+    CH_DEVICE(fn, w2, w2len * 4);
+    CH_DEVICE(fn, g, glen * 4);
+    if (dw1) CH_DEVICE(fn, dw1, dw1len * 4);
+    if (dw2) CH_DEVICE(fn, dw2, dw2len * 4);
+    if (!dw1 && !dw2) return CLEAVE_HIP_OK;
+    return hidden_bwd(x, h, w2, g, dw1, dw2, B, D, Hd, ch::stream());
 }

@@ -297,6 +297,27 @@ CLEAVE_HIP_API int32_t cleave_hip_mlp_step_f32(const float* x, int64_t xlen, con
                                 float* dw1, int64_t dw1len, float* dw2, int64_t dw2len,
                                 float* loss_dev, int32_t B, int32_t D, int32_t Hd, float lr);
 
+/* The hidden layer of that step as its own forward and reverse rule, for a
+ * host that meets the subgraph z = sigmoid(X W1) w2 (w2 a column) in a
+ * program, such as a reverse-mode tape: the step's fused kernels (sigmoid and
+ * the partial products with w2 in the GEMM's epilogue; d1 formed while the
+ * dW1 GEMM reads H) whenever B, D and Hd are multiples of 256, the separate
+ * kernels otherwise.  Reverse rules applied: the MatMul product rule
+ * (stdlib/linalg/matrix.cleave:24) and sigmoid's s(1 - s)
+ * (stdlib/num/num.cleave:132-134, :222).
+ * Forward: H = sigmoid(X W1) [B x Hd], z = H w2 [B]; w2 and h 16-byte aligned.
+ * Backward: given H and g = dL/dz [B], d1 = (g w2^T) * H(1 - H);
+ * dW1 = X^T d1 [D x Hd], dW2 = H^T g [Hd]; either output may be null. */
+CLEAVE_HIP_API int32_t cleave_hip_sigmoid_hidden_fwd_f32(const float* x, int64_t xlen, const float* w1,
+                                                         int64_t w1len, const float* w2, int64_t w2len, float* h,
+                                                         int64_t hlen, float* z, int64_t zlen, int32_t B,
+                                                         int32_t D, int32_t Hd);
+CLEAVE_HIP_API int32_t cleave_hip_sigmoid_hidden_bwd_f32(const float* x, int64_t xlen, const float* h,
+                                                         int64_t hlen, const float* w2, int64_t w2len,
+                                                         const float* g, int64_t glen, float* dw1, int64_t dw1len,
+                                                         float* dw2, int64_t dw2len, int32_t B, int32_t D,
+                                                         int32_t Hd);
+
 /* ---------------------------------------------------------------------- */
 /* Tensor<f64, ...>                                                         */
 /* ---------------------------------------------------------------------- */

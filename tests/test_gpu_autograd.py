@@ -124,3 +124,53 @@ def test_shape_errors_are_raised_before_any_kernel(hip, ad):
         ad.add(a, b)
     with pytest.raises(ValueError, match="one element"):
         ad.backward(a)
+
+
+@pytest.mark.parametrize("B,D,Hd", [(1024, 256, 768), (300, 70, 130)])  # fused kernels, separate kernels
+def test_tape_hidden_layer_takes_the_fused_rule(hip, ad, oracle, B, D, Hd):
+    # sigmoid(X W1) w2 on the tape: X W1 is never written, the sigmoid's value is
+    # the layer's H, and backward leaves the fused subgraph's inner values without
+    # .grad; the gradients still meet the oracle's, entry by entry
+    rng = np.random.default_rng(B + Hd)
+    X = rng.standard_normal((B, D)).astype(np.float32)
+    Y = (rng.random(B) < 0.5).astype(np.float32)
+    W1 = rng.uniform(-0.1, 0.1, (D, Hd)).astype(np.float32)
+    W2 = rng.uniform(-0.1, 0.1, Hd).astype(np.float32)
+    w1, w2 = ad.param(W1), ad.param(W2.reshape(Hd, 1))
+    z1 = ad.const(X) @ w1
+    s = ad.sigmoid(z1)
+    z2 = s @ w2
+    assert z1.pending and not s.pending and not z2.pending
+    e = ad.sigmoid(z2) - ad.const(Y.reshape(B, 1))
+    loss = ad.mean(e * e)
+    ad.backward(loss)
+    assert z1.pending and s.grad is None and z1.grad is None
+    L, dW1_r, dW2_r, _, _ = oracle.mlp_step(X, Y, W1, W2, lr=0.0, threads=16)
+    assert abs(float(loss.numpy()[0]) - L) <= 1e-5 * L
+    assert_mlp_grads_close(w1.grad.numpy(), w2.grad.numpy().ravel(), dW1_r, dW2_r, X, Y, W1, W2, "fused tape")
+
+
+def test_tape_without_the_pattern_uses_the_general_rules(hip, ad):
+    # X takes a gradient here, so the hidden layer is not fused: every rule runs
+    # on its own, and the inner product is computed when the backward reads it
+    rng = np.random.default_rng(77)
+    X = rng.standard_normal((6, 4))
+    W1 = rng.standard_normal((4, 5)) * 0.5
+    W2 = rng.standard_normal((5, 1)) * 0.5
+    x, w1, w2 = ad.param(X.astype(np.float32)), ad.param(W1.astype(np.float32)), ad.param(W2.astype(np.float32))
+    loss = ad.sum(ad.sigmoid(x @ w1) @ w2)
+    ad.backward(loss)
+
+    def f(Xv, W1v, W2v):
+        return float(np.sum((1 / (1 + np.exp(-(Xv @ W1v)))) @ W2v))
+
+    eps = 1e-3
+    for P, v in ((X, x), (W1, w1), (W2, w2)):
+        num = np.zeros_like(P)
+        for i in np.ndindex(P.shape):
+            up, dn = P.copy(), P.copy()
+            up[i] += eps
+            dn[i] -= eps
+            args = [up if Q is P else Q for Q in (X, W1, W2)], [dn if Q is P else Q for Q in (X, W1, W2)]
+            num[i] = (f(*args[0]) - f(*args[1])) / (2 * eps)
+        assert np.allclose(v.grad.numpy().reshape(P.shape), num, rtol=2e-3, atol=2e-4)

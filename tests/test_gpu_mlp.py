@@ -195,3 +195,38 @@ def test_config4_full_size_step(hip, oracle):
     # the SGD update used exactly those gradients: w = w - lr * g, in f32
     assert np.array_equal(w1.numpy(), W1 - np.float32(lr) * got1)
     assert np.array_equal(w2.numpy(), W2 - np.float32(lr) * got2)
+
+
+@pytest.mark.parametrize("B,D,Hd", [(512, 256, 512), (1024, 256, 768),   # fused kernels
+                                    (300, 70, 130), (256, 64, 128)])      # separate kernels
+def test_hidden_layer_forward_and_rule(hip, oracle, B, D, Hd):
+    # z = sigmoid(X W1) w2 and its reverse rule, as the tape calls them
+    rng = np.random.default_rng(B + 3 * D + Hd)
+    X = rng.standard_normal((B, D)).astype(np.float32)
+    W1 = _xavier(rng, D, Hd, (D, Hd))
+    W2 = _xavier(rng, Hd, 1, Hd)
+    x, w1, w2 = hip.from_numpy(X), hip.from_numpy(W1), hip.from_numpy(W2)
+    h, z = hip.sigmoid_hidden_fwd(x, w1, w2)
+    H, Z = h.numpy(), z.numpy().ravel()
+    # H against sigmoid of the oracle's product: the GEMM bound through sigmoid' <= 1/4,
+    # plus the maps' rel 1e-5
+    Zr = oracle.matmul(X, W1, threads=16)
+    Hr = oracle.sigmoid(Zr).astype(np.float64)
+    tolH = 0.25 * 1e-5 * np.sqrt(D) * (np.abs(X).astype(np.float64) @ np.abs(W1)) + 1e-5 * np.abs(Hr)
+    assert np.all(np.abs(H - Hr) <= tolH)
+    # z against the float64 dot of the oracle's H, within the dot's bound plus H's
+    zr = Hr @ W2.astype(np.float64)
+    tolz = 1e-5 * np.sqrt(Hd) * (np.abs(Hr) @ np.abs(W2)) + tolH @ np.abs(W2)
+    assert np.all(np.abs(Z - zr) <= tolz)
+    # the rule, on the device's H and a cotangent g of z: every entry within the GEMM bound
+    g = (rng.standard_normal(B) * 0.01).astype(np.float32)
+    dw1, dw2 = hip.empty((D, Hd)), hip.empty((Hd, 1))
+    hip.sigmoid_hidden_bwd(x, h, w2, hip.from_numpy(g.reshape(B, 1)), dw1, dw2)
+    H64, g64 = H.astype(np.float64), g.astype(np.float64)
+    d1 = g64[:, None] * W2.astype(np.float64)[None, :] * H64 * (1.0 - H64)
+    dW1r, dW2r = X.astype(np.float64).T @ d1, H64.T @ g64
+    a1 = np.abs(X).astype(np.float64).T @ np.abs(d1)
+    a2 = np.abs(H64).T @ np.abs(g64)
+    tol = 1e-5 * np.sqrt(B)
+    assert np.all(np.abs(dw1.numpy() - dW1r) <= tol * a1 + 1e-6 * np.abs(dW1r))
+    assert np.all(np.abs(dw2.numpy().ravel() - dW2r) <= tol * a2)
