@@ -20,7 +20,8 @@ Prints ONE JSON line on stdout:
                baseline from the restated loops on a bounded sample
   vendor_same_device
                (--vendor only) torch.matmul / torch.bmm on the GEMM shapes, timed the
-               same way in a child process on the same device
+               same way in a child process on the same device (with --gemm: on
+               those specs, beside each spec's own figures)
 Progress goes to stderr.
 """
 from __future__ import annotations
@@ -128,6 +129,74 @@ def vendor_yardstick(steps):
     run("gemm_bf16_batched_64x512", lambda: torch.bmm(x, y, out=z), 2.0 * bs * k ** 3, 0.3)
     del x, y, z
     torch.cuda.synchronize()
+    return out
+
+
+def vendor_shapes(specs, steps):
+    """torch.matmul / torch.bmm on the --gemm specs, timed like gemm_shapes
+    (0.3 s warm-up, then HIP events), in the --vendor child process.  bf16
+    products are timed as torch returns them (bf16 C, half the bytes this
+    library writes) and, where this torch build has it, with f32 C
+    (out_dtype=torch.float32: the same bytes as here).  2-D products take the
+    spec's layout as transposed views; batched bf16 products are timed with
+    contiguous operands in every layout (torch.bmm on a transposed bf16 view
+    is avoided on these boxes)."""
+    import torch
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    out = {}
+
+    def clock(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < 0.3:
+            for _ in range(4):
+                fn()
+            torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    for spec in specs:
+        dt, dims, lay = spec.split(":")
+        d = [int(x) for x in dims.split("x")]
+        bs, (m, n, k) = (d[0], d[1:]) if len(d) == 4 else (1, d)
+        batched = len(d) == 4
+        ta, tb = lay[0] == "t", lay[1] == "t"
+        tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f64": torch.float64}[dt]
+        lead = (bs,) if batched else ()
+        if batched:
+            a = torch.randn(lead + (m, k), device=dev, generator=g).to(tdt)
+            b = torch.randn(lead + (k, n), device=dev, generator=g).to(tdt)
+            opa, opb = a, b
+        else:
+            a = torch.randn((k, m) if ta else (m, k), device=dev, generator=g).to(tdt)
+            b = torch.randn((n, k) if tb else (k, n), device=dev, generator=g).to(tdt)
+            opa, opb = (a.t() if ta else a), (b.t() if tb else b)
+        mm = torch.bmm if batched else torch.mm
+        c = torch.empty(lead + (m, n), device=dev, dtype=tdt)
+        ms = clock(lambda: mm(opa, opb, out=c))
+        rec = {"torch_ms": round(ms, 5)}
+        if dt == "bf16":
+            try:
+                mm(opa, opb, out_dtype=torch.float32)
+                rec["torch_f32_out_ms"] = round(clock(lambda: mm(opa, opb, out_dtype=torch.float32)), 5)
+            except (RuntimeError, TypeError) as e:
+                rec["torch_f32_out_ms"] = None
+                rec["torch_f32_out_error"] = str(e).splitlines()[0][:160]
+        out[spec] = rec
+        log(f"vendor {spec}: {ms * 1e3:.1f} us")
+        del a, b, c, opa, opb
+        torch.cuda.synchronize()
     return out
 
 
@@ -521,7 +590,7 @@ def main():
                     help="only time the batched bf16 64 x 512^3 product in the given layouts")
     ap.add_argument("--gemm", metavar="SPECS", default=None,
                     help="only time the comma-separated products dtype:MxNxK:layout or batches dtype:BxMxNxK:layout "
-                         "(e.g. f32:2048x2048x2048:nn)")
+                         "(e.g. f32:2048x2048x2048:nn); with --vendor, torch on the same specs too")
     ap.add_argument("--host-boundary", action="store_true",
                     help="only time the _host entry points (host arrays across the C ABI, PCIe included)")
     ap.add_argument("--mlp", action="store_true", help="only time the MLP step, fused and through the tape")
@@ -533,7 +602,10 @@ def main():
               "out of scope for this build", file=sys.stderr)
         sys.exit(2)
     if args.vendor_only:
-        print(json.dumps(vendor_yardstick(max(20, args.steps // 2))), flush=True)
+        if args.gemm:
+            print(json.dumps(vendor_shapes(args.gemm.split(","), args.steps)), flush=True)
+        else:
+            print(json.dumps(vendor_yardstick(max(20, args.steps // 2))), flush=True)
         return
 
     import numpy as np
@@ -557,8 +629,22 @@ def main():
             ca, args.gemm_bf16_batched.split(","), steps), "library": str(ca._lib.LIB_PATH)}), flush=True)
         return
     if args.gemm:
-        print(json.dumps({"gemm": gemm_shapes(ca, args.gemm.split(","), steps),
-                          "library": str(ca._lib.LIB_PATH)}), flush=True)
+        res = {"gemm": gemm_shapes(ca, args.gemm.split(","), steps), "library": str(ca._lib.LIB_PATH)}
+        if args.vendor:
+            # torch on the same specs in a child process (see vendor_yardstick);
+            # speed ratios are torch's time over this library's
+            proc = subprocess.run([sys.executable, os.path.abspath(__file__), "--vendor-only", "--gemm", args.gemm,
+                                   "--steps", str(steps)], stdout=subprocess.PIPE)
+            if proc.returncode != 0:
+                raise RuntimeError(f"vendor child failed with status {proc.returncode}")
+            ven = json.loads(proc.stdout.decode().strip().splitlines()[-1])
+            for spec, v in ven.items():
+                row = res["gemm"][spec]
+                row.update(v)
+                row["speed_vs_torch"] = round(v["torch_ms"] / row["kernel_ms"], 4)
+                if v.get("torch_f32_out_ms"):
+                    row["speed_vs_torch_f32_out"] = round(v["torch_f32_out_ms"] / row["kernel_ms"], 4)
+        print(json.dumps(res), flush=True)
         return
     if args.host_boundary:
         print(json.dumps({"host_boundary": host_boundary(steps)}), flush=True)
