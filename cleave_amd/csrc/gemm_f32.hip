@@ -254,6 +254,23 @@ bool launch_tiled(const float* a, const float* b, float* c, int M, int N, int K,
     return true;
 }
 
+// The tiled kernel's EDGE form (gemm_f32_tiled.hpp) on any shape whose
+// operands it can mask (fits_edge); false otherwise.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool TA, bool TB>
+bool launch_tiled_edge(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
+                       int64_t ldb, int batch, int64_t sA, int64_t sB, int64_t sC, int32_t* status) {
+    using P = ch::F32Tiled<BM, BN, BK, WM, WN, STAGES, !TA, TB>;
+    if (!P::fits_edge(M, N, K, lda, ldb) || ((uintptr_t)a & 15) || ((uintptr_t)b & 15) || (sA % 4) || (sB % 4))
+        return false;
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
+    dim3 grid((unsigned)(tiles_m * tiles_n * batch));
+    ch::gemm_f32_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB, true><<<grid, P::THREADS, 0, ch::stream()>>>(
+        a, b, c, M, N, K, lda, ldb, sA, sB, sC, tiles_m, tiles_n, batch);
+    *status = ch::check_hip(hipGetLastError(), "gemm_f32_tiled_kernel");
+    return true;
+}
+
 // Small-product kernel (gemm_f32_small.hpp): 32 x 32 tiles, K split over
 // K/64 waves of the workgroup; false when the shape does not fit it.
 template <bool TA, bool TB>
@@ -600,6 +617,7 @@ constexpr double kSkinnyMinFlops = 1u << 20;
 // tiles (4224^3) 0.78, four workgroups per CU.  4097^3 measured 1.23 ms
 // padded to 4224^3, 1.83 ms padded to 4352^2 x 4160 (289 tiles of 256).
 constexpr ch::PadModel kPadModel{0.86, 0.78, false, 1.0};
+constexpr int64_t kEdgeTilesPerCu = 4;
 
 template <bool TA, bool TB>
 int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
@@ -614,6 +632,20 @@ int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, in
     if (packed && (M <= 32 || N <= 32) && 2.0 * M * N * K * batch >= kSkinnyMinFlops)
         return ch::matmul_skinny_f32(a, b, c, M, N, K, batch, TA, TB);
     if (packed && 2.0 * M * N * K * batch >= kPadMinFlops) {
+        // Up to kEdgeTilesPerCu tiles of 64 x 64 per CU: the 64 x 64 kernel
+        // with guarded edges on the operands in place, one launch.  Up to two
+        // tiles per CU its k-tiles are 32 deep (64 KiB of LDS, two workgroups
+        // per CU), beyond that 16 (five): f32 1000^3 22.4 against 23.8 us,
+        // 1000 x 2000 x 1000 37.7 against 38.3, 500^3 12.1 against 13.0;
+        // 1500^3 80.1 against 77.1, 2000^3 136.9 against 132.2.
+        const int64_t tiles64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64) * batch;
+        const int64_t cus = ch::num_cus();
+        if (tiles64 <= 2 * cus &&
+            launch_tiled_edge<64, 64, 32, 2, 2, 4, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
+            return st;
+        if (tiles64 <= kEdgeTilesPerCu * cus &&
+            launch_tiled_edge<64, 64, 16, 2, 2, 4, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
+            return st;
         const ch::PadPlan p = ch::pad_plan(M, N, K, batch, TA, TB, a, b, 4, ch::num_cus(), kPadModel);
         auto gemm = [batch](const float* pa, const float* pb, float* pc, int Mp, int Np, int Kp) {
             const int64_t plda = TA ? Mp : Kp, pldb = TB ? Kp : Np;

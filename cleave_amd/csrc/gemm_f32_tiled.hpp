@@ -9,6 +9,11 @@
 // (A and B agree, so all 8 terms are summed), which lets a k-contiguous
 // operand feed four MFMAs from one ds_read_b128; an m/n-contiguous operand is
 // read with four conflict-free ds_read_b32.
+//
+// EDGE = true takes any M, N and K >= 1 (tiles_m, tiles_n rounded up): the
+// copies become buffer loads that zero-fill what lies outside the operand
+// (EdgeCopy, gemm_tiles.hpp) and the stores are masked, so a ragged product
+// needs no padded copies of its operands and no crop of its result.
 #pragma once
 
 #include "gemm_common.hpp"
@@ -37,9 +42,25 @@ struct F32Tiled {
         const uint64_t a_span = (AKC ? (uint64_t)BM : (uint64_t)BK + 1) * (uint64_t)lda * 4;
         const uint64_t b_span = (BKC ? (uint64_t)BN : (uint64_t)BK + 1) * (uint64_t)ldb * 4;
         return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
-    }};
+    }
+    // Bytes from an operand's base to the end of its last element.
+    static __host__ __device__ int64_t a_bytes(int M, int K, int64_t lda) {
+        return AKC ? ((int64_t)(M - 1) * lda + K) * 4 : ((int64_t)(K - 1) * lda + M) * 4;
+    }
+    static __host__ __device__ int64_t b_bytes(int N, int K, int64_t ldb) {
+        return BKC ? ((int64_t)(N - 1) * ldb + K) * 4 : ((int64_t)(K - 1) * ldb + N) * 4;
+    }
+    // Shapes the EDGE form takes: whole 16-byte chunks along each operand's
+    // contiguous extent and pitch, and operands under 2 GiB.
+    static bool fits_edge(int M, int N, int K, int64_t lda, int64_t ldb) {
+        const bool chunks = (AKC ? K % 4 == 0 : M % 4 == 0) && (BKC ? K % 4 == 0 : N % 4 == 0) && lda % 4 == 0 &&
+                            ldb % 4 == 0;
+        return M >= 1 && N >= 1 && K >= 1 && chunks && a_bytes(M, K, lda) < (1ll << 31) &&
+               b_bytes(N, K, ldb) < (1ll << 31);
+    }
+};
 
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC>
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC, bool EDGE = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N,
     int K, int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC, int tiles_m,
@@ -59,18 +80,39 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
     B += (int64_t)bt * strideB;
     C += (int64_t)bt * strideC;
 
+    const uint32_t lds0 = lds_addr(smem);
+    // aligned shapes: scalar tile bases and 32-bit lane offsets
     TileCopy<AKC, BM, BK, NW, 4> copy_a;
     TileCopy<BKC, BN, BK, NW, 4> copy_b;
-    copy_a.init(lda, m0, wave, lane);
-    copy_b.init(ldb, n0, wave, lane);
-    const int64_t step_a = copy_a.kstep(lda), step_b = copy_b.kstep(ldb);
-    const char* a_src = reinterpret_cast<const char*>(A) + copy_a.base_offset(lda, m0);
-    const char* b_src = reinterpret_cast<const char*>(B) + copy_b.base_offset(ldb, n0);
-    const uint32_t lds0 = lds_addr(smem);
+    const char* a_src = nullptr;
+    const char* b_src = nullptr;
+    int64_t step_a = 0, step_b = 0;
+    // EDGE: buffer resources over the operands, masked lane offsets
+    EdgeCopy<AKC, BM, BK, NW, 4> edge_a;
+    EdgeCopy<BKC, BN, BK, NW, 4> edge_b;
+    v4i rsrc_a{}, rsrc_b{};
+    if constexpr (EDGE) {
+        edge_a.init(lda, m0, M, wave, lane);
+        edge_b.init(ldb, n0, N, wave, lane);
+        rsrc_a = buffer_rsrc(A, (uint32_t)P::a_bytes(M, K, lda));
+        rsrc_b = buffer_rsrc(B, (uint32_t)P::b_bytes(N, K, ldb));
+    } else {
+        copy_a.init(lda, m0, wave, lane);
+        copy_b.init(ldb, n0, wave, lane);
+        step_a = copy_a.kstep(lda);
+        step_b = copy_b.kstep(ldb);
+        a_src = reinterpret_cast<const char*>(A) + copy_a.base_offset(lda, m0);
+        b_src = reinterpret_cast<const char*>(B) + copy_b.base_offset(ldb, n0);
+    }
     auto issue = [&](int kt, int stage) {
         const uint32_t dst = lds0 + (uint32_t)(stage * P::STAGE_BYTES);
-        copy_a.issue(a_src + kt * step_a, dst, wave);
-        copy_b.issue(b_src + kt * step_b, dst + P::A_BYTES, wave);
+        if constexpr (EDGE) {
+            edge_a.issue(rsrc_a, kt, K, (uint32_t)kt * edge_a.kstep(lda), dst, wave);
+            edge_b.issue(rsrc_b, kt, K, (uint32_t)kt * edge_b.kstep(ldb), dst + P::A_BYTES, wave);
+        } else {
+            copy_a.issue(a_src + kt * step_a, dst, wave);
+            copy_b.issue(b_src + kt * step_b, dst + P::A_BYTES, wave);
+        }
     };
 
     v16f acc[FM][FN];
@@ -101,7 +143,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
     static_assert(KB % 2 == 0, "fragment double-buffer parity assumes an even k-block count");
     constexpr int NR = FM * (AKC ? 1 : 4) + FN * (BKC ? 1 : 4);  // ds_reads per k-block
     constexpr int NM = 4 * FM * FN;                              // MFMAs per k-block
-    const int nk = K / BK;
+    const int nk = EDGE ? (K + BK - 1) / BK : K / BK;
 
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s)
@@ -151,7 +193,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_tiled_kernel(
             for (int v = 0; v < 16; ++v) {
                 const int r = m0 + wm * P::TM + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
                 const int c = n0 + wn * P::TN + j * 32 + col;
-                C[(int64_t)r * N + c] = acc[i][j][v];
+                if (!EDGE || (r < M && c < N)) C[(int64_t)r * N + c] = acc[i][j][v];
             }
 }
 

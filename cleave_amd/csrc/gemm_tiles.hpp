@@ -148,6 +148,83 @@ struct TileCopy {
     }
 };
 
+// Copies for tiles that may cross the edge of the operand (M, N or K not a
+// multiple of the tile).  A raw buffer load into LDS (buffer_load_dwordx4
+// ... lds) range-checks voffset + soffset against the resource's byte count
+// and writes zeros to LDS for a lane out of range; each lane whose 16-byte
+// chunk lies outside the matrix is given an offset of kOutOfRange, so the
+// tile arrives zero-padded without a padded copy of the operand.  Requires
+// the operand's contiguous extent (K for a k-contiguous one, M or N
+// otherwise) and its pitch to be multiples of the chunk (16 bytes), so a
+// chunk is wholly inside or wholly outside, and the operand under 2 GiB, so
+// kOutOfRange plus any k-tile step stays out of range.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource over `bytes` bytes from `base` (stride 0; word 3 holds
+// the 32-bit data format these loads need).
+__device__ __forceinline__ v4i buffer_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    v4i r;
+    r[0] = (int)(uint32_t)a;
+    r[1] = (int)((uint32_t)(a >> 32) & 0xFFFFu);
+    r[2] = (int)bytes;
+    r[3] = 0x00020000;
+    return r;
+}
+
+// One buffer -> LDS copy instruction: 16 bytes per lane from the resource at
+// voff + soff into LDS at lds_dst + 16*lane (inline asm for the reason dma16
+// gives).
+__device__ __forceinline__ void dma16_buf(v4i rsrc, uint32_t voff, uint32_t soff, uint32_t lds_dst) {
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" : : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_dst)
+                 : "memory");
+}
+
+// TileCopy's instruction and lane layout, with per-lane masks: a chunk in a
+// row (column) at or past `extent`, or at a k at or past K, loads zeros.
+template <bool KC, int R, int BK, int NW, int ESZ = 2>
+struct EdgeCopy {
+    static constexpr int EPC = 16 / ESZ;
+    static constexpr int NI = R * BK * ESZ / 1024, PER_WAVE = NI / NW;
+    static_assert(NI % NW == 0, "tile copy must split evenly over the waves");
+    uint32_t voff[PER_WAVE];  // byte offset from the operand base at k-tile 0, or kOutOfRange
+    int k0[PER_WAVE];         // k of the lane's chunk (KC) or k-row (MN) at k-tile 0
+
+    // r0: the tile's first row (KC) or column (MN); extent: the operand's rows
+    // (KC) or columns (MN).
+    __device__ __forceinline__ void init(int64_t ld, int r0, int extent, int wave, int lane) {
+#pragma unroll
+        for (int j = 0; j < PER_WAVE; ++j) {
+            const int q = wave + NW * j;
+            if constexpr (KC) {
+                constexpr int CPR = BK / EPC, RPI = 64 / CPR;
+                const int r = q * RPI + lane / CPR;
+                const int c = kc_slot<CPR, ESZ>(r, lane % CPR);
+                voff[j] = r0 + r < extent ? (uint32_t)(((int64_t)(r0 + r) * ld + EPC * c) * ESZ) : kOutOfRange;
+                k0[j] = EPC * c;
+            } else {
+                constexpr int CPR = R / EPC, KPI = 64 / CPR;
+                static_assert(CPR >= 16 && 64 % CPR == 0, "MN row too narrow for its swizzle");
+                const int kr = q * KPI + lane / CPR;
+                const int c = mn_slot<ESZ>(kr, lane % CPR);
+                voff[j] = r0 + EPC * c < extent ? (uint32_t)(((int64_t)kr * ld + r0 + EPC * c) * ESZ) : kOutOfRange;
+                k0[j] = kr;
+            }
+        }
+    }
+    // Byte step of the scalar offset per k-tile.
+    static __device__ __forceinline__ uint32_t kstep(int64_t ld) {
+        return (uint32_t)(KC ? (int64_t)BK * ESZ : (int64_t)BK * ld * ESZ);
+    }
+    __device__ __forceinline__ void issue(v4i rsrc, int kt, int K, uint32_t soff, uint32_t lds_tile, int wave) const {
+#pragma unroll
+        for (int j = 0; j < PER_WAVE; ++j)
+            dma16_buf(rsrc, k0[j] + kt * BK < K ? voff[j] : kOutOfRange, soff,
+                      lds_tile + 1024u * (uint32_t)(wave + NW * j));
+    }
+};
+
 // MFMA operand fragment (32 rows x 16 k) starting at tile row `row0`, k-step kk.
 template <bool KC, int R, int BK>
 __device__ __forceinline__ v8bf read_frag(const char* tile, int row0, int kk, int lane) {

@@ -516,7 +516,9 @@ def _operands(oracle, dtype, M, N, K, ta, tb, seed, batch=None):
 # Ragged shapes large enough for the zero-padded route (the aligned kernels
 # on padded copies of the operands, the valid corner of C copied out): every
 # dimension ragged, K alone ragged (C written in place), M alone ragged (B
-# used in place), N alone ragged (A used in place).
+# used in place), N alone ragged (A used in place).  In f32, the layouts whose
+# contiguous extents are multiples of 4 run the 64 x 64 kernel with guarded
+# edges instead (below); the others, and bf16, the padded route.
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [(1000, 1000, 1000), (640, 2048, 520), (1031, 768, 512), (2048, 1100, 256)])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
@@ -604,6 +606,73 @@ def test_padded_infinities_and_nans(hip, oracle, dtype):
     assert np.isnan(got[9, 7]) and np.isnan(got[5]).all()
     fin = np.isfinite(ref)
     den = np.abs(Au).astype(np.float64) @ np.abs(Bu).astype(np.float64)
+    assert np.all(np.abs(got[fin] - ref[fin]) <= 1e-5 * np.sqrt(K) * den[fin])
+
+
+# f32 ragged shapes with up to 4 tiles of 64 x 64 per CU run the 64 x 64
+# kernel with guarded edges on the operands in place: the copies are buffer
+# loads that read zeros outside the matrix, the stores are masked.  It needs
+# each operand's contiguous extent to be a multiple of 4 (whole 16-byte
+# chunks): K for a k-contiguous operand, M or N for an m/n-contiguous one.
+# Per layout: all three dimensions ragged against the tile (64 x 64 x 16), a
+# tile row or column mostly outside, K below one k-tile, and products of a
+# few tiles.  Every entry against the loop.
+_EDGE_CASES = [
+    (1001, 1000, 996, 0, 0), (100, 104, 52, 0, 0), (200, 300, 12, 0, 0), (1000, 1000, 1000, 0, 0),
+    (999, 1001, 1000, 0, 1), (130, 97, 44, 0, 1), (65, 1000, 4, 0, 1),
+    (1000, 1004, 999, 1, 0), (132, 100, 45, 1, 0), (1000, 1000, 1000, 1, 0),
+    (1000, 999, 1004, 1, 1), (100, 131, 48, 1, 1), (1448, 1448, 1448, 1, 1),
+]
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb", _EDGE_CASES)
+def test_f32_edge_tiles_every_entry(hip, oracle, M, N, K, ta, tb):
+    A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=M + 5 * N + 11 * K + 2 * ta + tb)
+    a, b = hip.from_numpy(A), hip.from_numpy(B)
+    got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    again = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert got.shape == (M, N)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "repeat"
+    ref = oracle.matmul(Au, Bu, trans_a=bool(ta), trans_b=bool(tb), threads=16)
+    den = np.abs(Au.T if ta else Au).astype(np.float64) @ np.abs(Bu.T if tb else Bu).astype(np.float64)
+    assert_gemm_close(got, ref, den, K, f"f32 edge {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+def test_f32_edge_tiles_batched_every_entry(hip, oracle, ta, tb):
+    # 3 x 700 x 900 x 300: 495 tiles of 64 x 64 over three products
+    bsz, M, N, K = 3, 700, 900, 300
+    A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=17 + ta + tb, batch=bsz)
+    got = hip.matmul_batched(hip.from_numpy(A), hip.from_numpy(B), trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    for i in range(bsz):
+        ref = oracle.matmul(Au[i], Bu[i], trans_a=bool(ta), trans_b=bool(tb), threads=16)
+        den = np.abs(Au[i].T if ta else Au[i]).astype(np.float64) @ \
+            np.abs(Bu[i].T if tb else Bu[i]).astype(np.float64)
+        assert_gemm_close(got[i], ref, den, K, f"f32 edge batched entry {i}")
+
+
+def test_f32_edge_tiles_infinities_and_nans(hip, oracle):
+    # The zeros the edge copies read outside the matrix add 0 * 0 = +0 only:
+    # an Inf or NaN in the last row, column or k reaches exactly the entries
+    # it feeds (1000 x 1000 x 70: every dimension ragged against the tile).
+    M, N, K = 1000, 1000, 70
+    rng = np.random.default_rng(31)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    A[999, 69] = np.inf
+    A[5, 3] = np.nan
+    B[69, 999] = -np.inf
+    B[2, 7] = 0.0
+    A[9, 2] = np.inf
+    got = hip.matmul(hip.from_numpy(A), hip.from_numpy(B)).numpy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = A.astype(np.float64) @ B.astype(np.float64)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref))
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))
+    assert np.isnan(got[9, 7]) and np.isnan(got[5]).all()
+    fin = np.isfinite(ref)
+    den = np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64)
     assert np.all(np.abs(got[fin] - ref[fin]) <= 1e-5 * np.sqrt(K) * den[fin])
 
 
