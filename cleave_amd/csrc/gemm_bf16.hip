@@ -246,6 +246,43 @@ bool launch_tiled(const uint16_t* a, const uint16_t* b, float* c, int M, int N, 
     return true;
 }
 
+// The tiled kernel's EDGE form (gemm_bf16_tiled.hpp) on any shape whose
+// operands it can mask (fits_edge); false otherwise.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int MI, bool TA, bool TB>
+bool launch_tiled_edge(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
+                       const Strides& s, int32_t* status) {
+    using P = ch::Bf16Tiled<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI>;
+    if (!P::fits_edge(M, N, K, s.lda, s.ldb) || !bases_aligned(a, b, s)) return false;
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
+    dim3 grid((unsigned)(tiles_m * tiles_n * batch));
+    ch::gemm_bf16_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI, true><<<grid, P::THREADS, 0, ch::stream()>>>(
+        a, b, c, M, N, K, s.lda, s.ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch, 1);
+    *status = ch::check_hip(hipGetLastError(), "gemm_bf16_tiled_kernel");
+    return true;
+}
+
+// Ragged products that the padded route would run on 128 x 128 tiles (fewer
+// 256 x 256 tiles than half a round): the same tiles with guarded edges on
+// the operands in place (three stages up to a round of tiles, as
+// launch_fast, else two), or, for a round at most with a k-contiguous A,
+// 64 x 128 tiles; false when the shape does not fit them.
+template <bool TA, bool TB>
+bool launch_edge(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
+                 const Strides& s, int32_t* st) {
+    const int64_t cus = ch::num_cus();
+    const int64_t big = (int64_t)((M + 255) / 256) * ((N + 255) / 256) * batch;
+    if (big * 2 >= cus) return false;
+    const int64_t tiles128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128) * batch;
+    if (tiles128 <= cus) {
+        if constexpr (!TA) {
+            if (launch_tiled_edge<64, 128, 64, 2, 2, 3, 32, TA, TB>(a, b, c, M, N, K, batch, s, st)) return true;
+        }
+        return launch_tiled_edge<128, 128, 64, 2, 2, 3, 32, TA, TB>(a, b, c, M, N, K, batch, s, st);
+    }
+    return launch_tiled_edge<128, 128, 64, 2, 2, 2, 32, TA, TB>(a, b, c, M, N, K, batch, s, st);
+}
+
 // Ping-pong kernel (gemm_bf16_pingpong.hpp): 256 x 256 x 32 tiles in a ring
 // of five k-tiles (all 160 KiB of LDS).
 template <bool TA, bool TB>
@@ -413,6 +450,7 @@ int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N,
     if ((M <= 32 || N <= 32) && 2.0 * M * N * K * batch >= (1u << 20))
         return ch::matmul_skinny_bf16(a, b, c, M, N, K, batch, TA, TB);
     if (2.0 * M * N * K * batch >= kPadMinFlops) {
+        if (launch_edge<TA, TB>(a, b, c, M, N, K, batch, packed<TA, TB>(M, N, K), &st)) return st;
         const ch::PadPlan p = ch::pad_plan(M, N, K, batch, TA, TB, a, b, 2, ch::num_cus(), kPadModel);
         auto gemm = [batch](const uint16_t* pa, const uint16_t* pb, float* pc, int Mp, int Np, int Kp) {
             int32_t s = CLEAVE_HIP_OK;

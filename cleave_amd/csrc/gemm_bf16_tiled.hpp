@@ -20,6 +20,11 @@
 // barrier is a bare s_barrier, so copies of later tiles stay in flight across
 // it.  Both are inline asm with a memory clobber, which keeps the compiler
 // from moving LDS reads across them.
+//
+// EDGE = true (32 x 32 MFMAs) takes any M, N and K >= 1 (tiles_m, tiles_n
+// rounded up): the copies become buffer loads that zero-fill what lies
+// outside the operand (EdgeCopy, gemm_tiles.hpp) and the stores are masked,
+// so a ragged product needs no padded copies and no crop.
 #pragma once
 
 #include "gemm_common.hpp"
@@ -55,14 +60,30 @@ struct Bf16Tiled {
         const uint64_t a_span = (AKC ? (uint64_t)BM : (uint64_t)BK + 1) * (uint64_t)lda * 2;
         const uint64_t b_span = (BKC ? (uint64_t)BN : (uint64_t)BK + 1) * (uint64_t)ldb * 2;
         return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
-    }};
+    }
+    // Bytes from an operand's base to the end of its last element.
+    static __host__ __device__ int64_t a_bytes(int M, int K, int64_t lda) {
+        return AKC ? ((int64_t)(M - 1) * lda + K) * 2 : ((int64_t)(K - 1) * lda + M) * 2;
+    }
+    static __host__ __device__ int64_t b_bytes(int N, int K, int64_t ldb) {
+        return BKC ? ((int64_t)(N - 1) * ldb + K) * 2 : ((int64_t)(K - 1) * ldb + N) * 2;
+    }
+    // Shapes the EDGE form takes: whole 16-byte chunks (8 elements) along
+    // each operand's contiguous extent and pitch, and operands under 2 GiB.
+    static bool fits_edge(int M, int N, int K, int64_t lda, int64_t ldb) {
+        const bool chunks = (AKC ? K % 8 == 0 : M % 8 == 0) && (BKC ? K % 8 == 0 : N % 8 == 0) && lda % 8 == 0 &&
+                            ldb % 8 == 0;
+        return MI == 32 && M >= 1 && N >= 1 && K >= 1 && chunks && a_bytes(M, K, lda) < (1ll << 31) &&
+               b_bytes(N, K, ldb) < (1ll << 31);
+    }
+};
 
 // `batch` products of M x N x K, product z at A + z strideA, B + z strideB,
 // C + z strideC.  With kslices > 1 (batch a multiple of it) the products are
 // the K slices of batch / kslices products of depth K * kslices: z = s nb + b
 // (nb = batch / kslices) is slice s of product b, at A + b strideA plus s K
 // columns (k-contiguous A) or s K rows of A (likewise B), and C + z strideC.
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC, int MI = 32>
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC, int MI = 32, bool EDGE = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC,
@@ -89,18 +110,40 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
     }
     C += (int64_t)bt * strideC;
 
+    static_assert(!EDGE || (MI == 32), "the EDGE form stores 32 x 32 accumulators");
+    const uint32_t lds0 = lds_addr(smem);
+    // aligned shapes: scalar tile bases and 32-bit lane offsets
     TileCopy<AKC, BM, BK, NW> copy_a;
     TileCopy<BKC, BN, BK, NW> copy_b;
-    copy_a.init(lda, m0, wave, lane);
-    copy_b.init(ldb, n0, wave, lane);
-    const int64_t step_a = copy_a.kstep(lda), step_b = copy_b.kstep(ldb);
-    const char* a_src = reinterpret_cast<const char*>(A) + copy_a.base_offset(lda, m0);
-    const char* b_src = reinterpret_cast<const char*>(B) + copy_b.base_offset(ldb, n0);
-    const uint32_t lds0 = lds_addr(smem);
+    const char* a_src = nullptr;
+    const char* b_src = nullptr;
+    int64_t step_a = 0, step_b = 0;
+    // EDGE: buffer resources over the operands, masked lane offsets
+    EdgeCopy<AKC, BM, BK, NW> edge_a;
+    EdgeCopy<BKC, BN, BK, NW> edge_b;
+    v4i rsrc_a{}, rsrc_b{};
+    if constexpr (EDGE) {
+        edge_a.init(lda, m0, M, wave, lane);
+        edge_b.init(ldb, n0, N, wave, lane);
+        rsrc_a = buffer_rsrc(A, (uint32_t)P::a_bytes(M, K, lda));
+        rsrc_b = buffer_rsrc(B, (uint32_t)P::b_bytes(N, K, ldb));
+    } else {
+        copy_a.init(lda, m0, wave, lane);
+        copy_b.init(ldb, n0, wave, lane);
+        step_a = copy_a.kstep(lda);
+        step_b = copy_b.kstep(ldb);
+        a_src = reinterpret_cast<const char*>(A) + copy_a.base_offset(lda, m0);
+        b_src = reinterpret_cast<const char*>(B) + copy_b.base_offset(ldb, n0);
+    }
     auto issue = [&](int kt, int stage) {
         const uint32_t dst = lds0 + (uint32_t)(stage * P::STAGE_BYTES);
-        copy_a.issue(a_src + kt * step_a, dst, wave);
-        copy_b.issue(b_src + kt * step_b, dst + P::A_BYTES, wave);
+        if constexpr (EDGE) {
+            edge_a.issue(rsrc_a, kt, K, (uint32_t)kt * edge_a.kstep(lda), dst, wave);
+            edge_b.issue(rsrc_b, kt, K, (uint32_t)kt * edge_b.kstep(ldb), dst + P::A_BYTES, wave);
+        } else {
+            copy_a.issue(a_src + kt * step_a, dst, wave);
+            copy_b.issue(b_src + kt * step_b, dst + P::A_BYTES, wave);
+        }
     };
 
     vacc acc[FM][FN];
@@ -129,7 +172,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
 
     constexpr int KS = BK / P::KSTEP;  // k-steps per k-tile
     static_assert(KS % 2 == 0, "fragment double-buffer parity assumes an even k-step count");
-    const int nk = K / BK;
+    const int nk = EDGE ? (K + BK - 1) / BK : K / BK;
     // Prologue: tiles 0 .. STAGES-2 in flight; wait for tile 0; then tile
     // STAGES-1 goes into the last free buffer.
 #pragma unroll
@@ -202,7 +245,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
                 for (int v = 0; v < 16; ++v) {
                     const int r = m0 + wm * P::TM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
                     const int c = n0 + wn * P::TN + j * 32 + (lane & 31);
-                    C[(int64_t)r * N + c] = acc[i][j][v];
+                    if (!EDGE || (r < M && c < N)) C[(int64_t)r * N + c] = acc[i][j][v];
                 }
     }
 }

@@ -518,7 +518,9 @@ def _operands(oracle, dtype, M, N, K, ta, tb, seed, batch=None):
 # dimension ragged, K alone ragged (C written in place), M alone ragged (B
 # used in place), N alone ragged (A used in place).  In f32, the layouts whose
 # contiguous extents are multiples of 4 run the 64 x 64 kernel with guarded
-# edges instead (below); the others, and bf16, the padded route.
+# edges instead, and in bf16 those with extents in multiples of 8 and fewer
+# 256 x 256 tiles than half a round run 128 x 128 (64 x 128) tiles with
+# guarded edges (below); the others the padded route.
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [(1000, 1000, 1000), (640, 2048, 520), (1031, 768, 512), (2048, 1100, 256)])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
@@ -649,6 +651,42 @@ def test_f32_edge_tiles_batched_every_entry(hip, oracle, ta, tb):
         den = np.abs(Au[i].T if ta else Au[i]).astype(np.float64) @ \
             np.abs(Bu[i].T if tb else Bu[i]).astype(np.float64)
         assert_gemm_close(got[i], ref, den, K, f"f32 edge batched entry {i}")
+
+
+# bf16 ragged products that the padded route would run on 128 x 128 tiles
+# (fewer 256 x 256 tiles than half a round) run those tiles with guarded
+# edges (64 x 128 tiles up to a round with a k-contiguous A; three stages up
+# to a round, two beyond), the operands in place.  Contiguous extents are
+# multiples of 8 (whole 16-byte chunks).
+_BF16_EDGE_CASES = [
+    (1001, 1000, 1000, 0, 0), (2000, 2400, 520, 0, 0), (104, 200, 264, 0, 0),
+    (999, 1001, 1000, 0, 1), (2001, 2399, 512, 0, 1),
+    (1000, 1008, 999, 1, 0), (2000, 2400, 333, 1, 0),
+    (1000, 999, 1000, 1, 1), (136, 150, 200, 1, 1),
+]
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb", _BF16_EDGE_CASES)
+def test_bf16_edge_tiles_every_entry(hip, oracle, M, N, K, ta, tb):
+    A, B, Au, Bu = _operands(oracle, "bf16", M, N, K, ta, tb, seed=3 * M + N + 7 * K + 2 * ta + tb)
+    a, b = hip.from_numpy(A, "bf16"), hip.from_numpy(B, "bf16")
+    got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    again = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert got.shape == (M, N)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "repeat"
+    ref = oracle.matmul(Au, Bu, trans_a=bool(ta), trans_b=bool(tb), threads=16)
+    den = np.abs(Au.T if ta else Au).astype(np.float64) @ np.abs(Bu.T if tb else Bu).astype(np.float64)
+    assert_gemm_close(got, ref, den, K, f"bf16 edge {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+def test_bf16_edge_tiles_batched_every_entry(hip, oracle):
+    bsz, M, N, K = 3, 700, 904, 296
+    A, B, Au, Bu = _operands(oracle, "bf16", M, N, K, 0, 0, seed=23, batch=bsz)
+    got = hip.matmul_batched(hip.from_numpy(A, "bf16"), hip.from_numpy(B, "bf16")).numpy()
+    for i in range(bsz):
+        ref = oracle.matmul(Au[i], Bu[i], threads=16)
+        den = np.abs(Au[i]).astype(np.float64) @ np.abs(Bu[i]).astype(np.float64)
+        assert_gemm_close(got[i], ref, den, K, f"bf16 edge batched entry {i}")
 
 
 def test_f32_edge_tiles_infinities_and_nans(hip, oracle):
