@@ -15,7 +15,7 @@ Prints ONE JSON line on stdout:
                f32 A B^T / A^T B, MLP steps/s, escape-count map, u64 count sum), the
                config-2 product on Tensor<f64> (vs 78.6 TFLOP/s FP64 MFMA), the
                MLP step through the reverse-mode tape, a matrix-vector product, and
-               the maps, reductions and row-broadcast bias, each with its own
+               the maps, reductions, row-broadcast bias and general broadcasting, each with its own
                HIP-event roofline figure and (unless --no-cpu) a single-core CPU
                baseline from the restated loops on a bounded sample
   vendor_same_device
@@ -360,6 +360,17 @@ def cpu_secondary(orc, name, budget_s, **kw):
             return _cpu_entry(round(arr_n * 8 / dt / 1e9, 3), "GB/s", f"{m.shape[0]} x {cols} f32 plus a row bias, {dt * 1e3:.0f} ms")
         dt, _ = _timed_cpu(lambda: orc.sum_rows(m))
         return _cpu_entry(round(arr_n * 4 / dt / 1e9, 3), "GB/s", f"{m.shape[0]} x {cols} f32 summed down the columns, {dt * 1e3:.0f} ms")
+    if name in ("mul_bcast_65536x4096_by_65536x1", "sum_to_shape_65536x4096_to_65536x1"):
+        cols = 4096
+        m = v.reshape(-1, cols)
+        if name == "mul_bcast_65536x4096_by_65536x1":
+            sc = rng.standard_normal((m.shape[0], 1)).astype(np.float32)
+            dt, _ = _timed_cpu(lambda: orc.bcast("mul", m, sc))
+            return _cpu_entry(round(arr_n * 8 / dt / 1e9, 3), "GB/s",
+                              f"{m.shape[0]} x {cols} f32 times a {m.shape[0]} x 1 column, broadcast, {dt * 1e3:.0f} ms")
+        dt, _ = _timed_cpu(lambda: orc.sum_to_shape(m, (m.shape[0], 1)))
+        return _cpu_entry(round(arr_n * 4 / dt / 1e9, 3), "GB/s",
+                          f"{m.shape[0]} x {cols} f32 summed along each row, {dt * 1e3:.0f} ms")
     if name == "max_argmax_f32_268M":
         dt, _ = _timed_cpu(lambda: (orc.max_of(v), orc.argmax(v)))
         return _cpu_entry(round(arr_n * 4 / dt / 1e9, 3), "GB/s",
@@ -878,6 +889,26 @@ def main():
         log(f"sum rows: {gbs:.0f} GB/s")
         if want_cpu:
             secondary["sum_rows_65536x4096"]["cpu_baseline"] = cpu_secondary(orc, "sum_rows_65536x4096", cb)
+        # general broadcasting: a per-row scale (65536 x 1 stretched along the
+        # columns) and its reverse rule, the sums along each row
+        hs = ca.fill_normal(ca.empty((65536, 1)), seed=504)
+        wall_s, ev = timed(ca, lambda: ca.mul(hx2, hs, out=hy2), 30, 5, 0.2)
+        gbs = (hn * 8 + 65536 * 4) / (ev * 1e-3) / 1e9
+        secondary["mul_bcast_65536x4096_by_65536x1"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1),
+                                                        "frac_hbm": round(gbs / PEAK_HBM, 4)}
+        log(f"mul broadcast: {gbs:.0f} GB/s")
+        if want_cpu:
+            secondary["mul_bcast_65536x4096_by_65536x1"]["cpu_baseline"] = cpu_secondary(
+                orc, "mul_bcast_65536x4096_by_65536x1", cb)
+        wall_s, ev = timed(ca, lambda: ca.sum_to_shape(hx2, (65536, 1), out=hs), 30, 5, 0.2)
+        gbs = (hn * 4 + 65536 * 4) / (ev * 1e-3) / 1e9
+        secondary["sum_to_shape_65536x4096_to_65536x1"] = {"ms": round(ev, 4), "GB/s": round(gbs, 1),
+                                                           "frac_hbm": round(gbs / PEAK_HBM, 4)}
+        log(f"sum to shape (rows): {gbs:.0f} GB/s")
+        if want_cpu:
+            secondary["sum_to_shape_65536x4096_to_65536x1"]["cpu_baseline"] = cpu_secondary(
+                orc, "sum_to_shape_65536x4096_to_65536x1", cb)
+        del hs
         # f32 Sum and Max/argmax reductions (one read per element)
         sdev = ca.empty(1)
         wall_s, ev = timed(ca, lambda: ca.reduce_sum(hx, sdev), 30, 5, 0.2)

@@ -205,10 +205,58 @@ def _unary(op: str, a: Tensor, out: Tensor | None) -> Tensor:
     return out
 
 
-def add(a, b, out=None): return _binary("add", a, b, out)
-def sub(a, b, out=None): return _binary("sub", a, b, out)
-def mul(a, b, out=None): return _binary("mul", a, b, out)
-def div(a, b, out=None): return _binary("div", a, b, out)
+def broadcast_shape(ashape, bshape) -> tuple:
+    """numpy's broadcast of two shapes: aligned at the last dimension, missing
+    leading dimensions 1, a 1 stretching to the other's; ValueError otherwise."""
+    R = max(len(ashape), len(bshape))
+    da = (1,) * (R - len(ashape)) + tuple(ashape)
+    db = (1,) * (R - len(bshape)) + tuple(bshape)
+    out = []
+    for i, (x, y) in enumerate(zip(da, db)):
+        if x != y and x != 1 and y != 1:
+            raise ValueError(f"shapes {tuple(ashape)} and {tuple(bshape)} do not broadcast (dimension {i})")
+        out.append(y if x == 1 else x)
+    return tuple(out)
+
+
+def _shape_i32(shape):
+    arr = np.ascontiguousarray(np.array(shape, dtype=np.int32).reshape(-1))
+    return arr, (arr.ctypes.data if arr.size else None)
+
+
+def _ring(op: str, a: Tensor, b: Tensor, out: Tensor | None) -> Tensor:
+    """Ring<Tensor> op: equal shapes take the same-shape map; broadcastable
+    shapes the broadcasting map (extension: the reference needs equal shapes)."""
+    if tuple(a.shape) == tuple(b.shape):
+        return _binary(op, a, b, out)
+    sfx = _float_sfx(a, op)
+    if b.dtype != a.dtype:
+        raise TypeError(f"{op}: operands must share a dtype")
+    shape = broadcast_shape(a.shape, b.shape)
+    out = out if out is not None else empty(shape, sfx)
+    sa, pa = _shape_i32(a.shape)
+    sb, pb = _shape_i32(b.shape)
+    call(f"cleave_hip_{op}_bcast_{sfx}", a.ptr, a.size, pa, len(a.shape), b.ptr, b.size, pb, len(b.shape),
+         out.ptr, out.size)
+    return out
+
+
+def add(a, b, out=None): return _ring("add", a, b, out)
+def sub(a, b, out=None): return _ring("sub", a, b, out)
+def mul(a, b, out=None): return _ring("mul", a, b, out)
+def div(a, b, out=None): return _ring("div", a, b, out)
+
+
+def sum_to_shape(g: Tensor, shape, out: Tensor | None = None) -> Tensor:
+    """g summed over the dimensions that broadcasting stretched to reach g's
+    shape from `shape`: the reverse rule of the broadcasting maps."""
+    sfx = _float_sfx(g, "sum_to_shape")
+    shape = tuple(shape)
+    out = out if out is not None else empty(shape, sfx)
+    sg, pg = _shape_i32(g.shape)
+    so, po = _shape_i32(shape)
+    call(f"cleave_hip_sum_to_shape_{sfx}", g.ptr, g.size, pg, len(g.shape), out.ptr, out.size, po, len(shape))
+    return out
 def neg(a, out=None): return _unary("neg", a, out)
 def relu(x, out=None): return _unary("relu", x, out)
 def sigmoid(x, out=None): return _unary("sigmoid", x, out)

@@ -208,6 +208,26 @@ SIGNATURES: dict[str, tuple] = {
     "cleave_hip_relu_bwd_f64_into": (i64, [vp, i64, vp, i64, vp, i64]),
     "cleave_hip_sigmoid_hidden_fwd_f32": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32]),
     "cleave_hip_sigmoid_hidden_bwd_f32": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32]),
+    "cleave_hip_add_bcast_f32": (i32, [vp, i64, vp, i32, vp, i64, vp, i32, vp, i64]),
+    "cleave_hip_sub_bcast_f32": (i32, [vp, i64, vp, i32, vp, i64, vp, i32, vp, i64]),
+    "cleave_hip_mul_bcast_f32": (i32, [vp, i64, vp, i32, vp, i64, vp, i32, vp, i64]),
+    "cleave_hip_div_bcast_f32": (i32, [vp, i64, vp, i32, vp, i64, vp, i32, vp, i64]),
+    "cleave_hip_sum_to_shape_f32": (i32, [vp, i64, vp, i32, vp, i64, vp, i32]),
+    "cleave_hip_add_bcast_f64": (i32, [vp, i64, vp, i32, vp, i64, vp, i32, vp, i64]),
+    "cleave_hip_sub_bcast_f64": (i32, [vp, i64, vp, i32, vp, i64, vp, i32, vp, i64]),
+    "cleave_hip_mul_bcast_f64": (i32, [vp, i64, vp, i32, vp, i64, vp, i32, vp, i64]),
+    "cleave_hip_div_bcast_f64": (i32, [vp, i64, vp, i32, vp, i64, vp, i32, vp, i64]),
+    "cleave_hip_sum_to_shape_f64": (i32, [vp, i64, vp, i32, vp, i64, vp, i32]),
+    "cleave_hip_add_bcast_f32_host": (i32, [vp, i64, vp, i32, vp, i64, vp, i32, vp, i64]),
+    "cleave_hip_sub_bcast_f32_host": (i32, [vp, i64, vp, i32, vp, i64, vp, i32, vp, i64]),
+    "cleave_hip_mul_bcast_f32_host": (i32, [vp, i64, vp, i32, vp, i64, vp, i32, vp, i64]),
+    "cleave_hip_div_bcast_f32_host": (i32, [vp, i64, vp, i32, vp, i64, vp, i32, vp, i64]),
+    "cleave_hip_sum_to_shape_f32_host": (i32, [vp, i64, vp, i32, vp, i64, vp, i32]),
+    "cleave_hip_add_bcast_f64_host": (i32, [vp, i64, vp, i32, vp, i64, vp, i32, vp, i64]),
+    "cleave_hip_sub_bcast_f64_host": (i32, [vp, i64, vp, i32, vp, i64, vp, i32, vp, i64]),
+    "cleave_hip_mul_bcast_f64_host": (i32, [vp, i64, vp, i32, vp, i64, vp, i32, vp, i64]),
+    "cleave_hip_div_bcast_f64_host": (i32, [vp, i64, vp, i32, vp, i64, vp, i32, vp, i64]),
+    "cleave_hip_sum_to_shape_f64_host": (i32, [vp, i64, vp, i32, vp, i64, vp, i32]),
     # memref-descriptor forms: every tensor argument is a pointer to an
     # unranked descriptor {int64 rank; void* ranked descriptor}
     "_mlir_ciface_cleave_hip_matmul_f32": (i32, [vp, vp, vp]),

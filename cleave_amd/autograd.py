@@ -11,6 +11,10 @@ reverse form with the library's backward kernels:
   add / sub / neg   linearity (stdlib/num/num.cleave:123-136)
   mul               product rule d(a*b) = da*b + a*db      -> dA = G*b, dB = a*G
   div               quotient rule (num.cleave:132-134)       -> cleave_hip_div_bwd_f32
+                    add/sub/mul/div also take operands whose shapes broadcast
+                    (an extension: the reference needs equal shapes); an
+                    operand's cotangent is then summed back over the stretched
+                    dimensions (cleave_hip_sum_to_shape_f32)
   sigmoid / tanh    s(1 - s) (= e^-x/(1+e^-x)^2) and 1 - t^2 (num.cleave:222-223)
   relu              x > 0 ? g : 0
   sum               every element receives the cotangent
@@ -151,20 +155,22 @@ def matmul(a: Var, b: Var) -> Var:
                thunk=lambda: ca.matmul(a.tensor, b.tensor), shape=out_shape)
 
 
-def _same_shape(a: Var, b: Var, what: str) -> None:
-    if a.shape != b.shape:
-        raise ValueError(f"{what}: shapes {a.shape} and {b.shape} differ (no broadcasting; see add_row_bias)")
+def _to_shape(g, shape):
+    """The cotangent of a broadcast result, summed back over the dimensions
+    that broadcasting stretched to reach an operand's shape."""
+    return g if tuple(g.shape) == tuple(shape) else ca.sum_to_shape(g, shape)
 
 
 def add(a: Var, b: Var) -> Var:
-    _same_shape(a, b, "add")
-    return Var(ca.add(a.tensor, b.tensor), (a, b), lambda g: (g, g))
+    return Var(ca.add(a.tensor, b.tensor), (a, b),
+               lambda g: (_to_shape(g, a.shape) if a.requires_grad else None,
+                          _to_shape(g, b.shape) if b.requires_grad else None))
 
 
 def sub(a: Var, b: Var) -> Var:
-    _same_shape(a, b, "sub")
     return Var(ca.sub(a.tensor, b.tensor), (a, b),
-               lambda g: (g, ca.neg(g) if b.requires_grad else None))
+               lambda g: (_to_shape(g, a.shape) if a.requires_grad else None,
+                          _to_shape(ca.neg(g), b.shape) if b.requires_grad else None))
 
 
 def neg(a: Var) -> Var:
@@ -172,19 +178,26 @@ def neg(a: Var) -> Var:
 
 
 def mul(a: Var, b: Var) -> Var:
-    _same_shape(a, b, "mul")
-
     def rule(g):
-        ga = ca.mul(g, b.tensor) if a.requires_grad else None
-        gb = ca.mul(a.tensor, g) if b.requires_grad else None
+        ga = _to_shape(ca.mul(g, b.tensor), a.shape) if a.requires_grad else None
+        gb = _to_shape(ca.mul(a.tensor, g), b.shape) if b.requires_grad else None
         return ga, gb
 
     return Var(ca.mul(a.tensor, b.tensor), (a, b), rule)
 
 
 def div(a: Var, b: Var) -> Var:
-    _same_shape(a, b, "div")
-    return Var(ca.div(a.tensor, b.tensor), (a, b), lambda g: ca.div_bwd(a.tensor, b.tensor, g))
+    if a.shape == b.shape:
+        return Var(ca.div(a.tensor, b.tensor), (a, b), lambda g: ca.div_bwd(a.tensor, b.tensor, g))
+
+    def rule(g):  # the quotient rule's two terms, broadcast, then summed back
+        ga = _to_shape(ca.div(g, b.tensor), a.shape) if a.requires_grad else None
+        gb = None
+        if b.requires_grad:
+            gb = _to_shape(ca.neg(ca.div(ca.mul(g, a.tensor), ca.mul(b.tensor, b.tensor))), b.shape)
+        return ga, gb
+
+    return Var(ca.div(a.tensor, b.tensor), (a, b), rule)
 
 
 def sigmoid(a: Var) -> Var:

@@ -489,6 +489,49 @@ int32_t cleave_hip_sum_rows_f32_host(const float* g, int64_t glen, float* out, i
     return s.finish(cleave_hip_sum_rows_f32(s.dev<float>(ig), glen, s.dev<float>(io), outlen, rows, cols));
 }
 
+// Broadcasting maps and their reverse rule: the shapes are host arrays read
+// by the device form; the operands are staged like the other maps'.
+#define CH_BCAST_HOST(op, T, sfx)                                                                               \
+    int32_t cleave_hip_##op##_bcast_##sfx##_host(const T* a, int64_t alen, const int32_t* ashape, int32_t arank, \
+                                                const T* b, int64_t blen, const int32_t* bshape, int32_t brank,  \
+                                                T* out, int64_t outlen) {                                        \
+        Staged s("cleave_hip_" #op "_bcast_" #sfx "_host");                                                     \
+        const int ia = s.in(a, alen, sizeof(T)), ib = s.in(b, blen, sizeof(T)), io = s.out(out, outlen, sizeof(T)); \
+        int32_t st = s.stage();                                                                                  \
+        if (st != CLEAVE_HIP_OK) return st;                                                                      \
+        return s.finish(cleave_hip_##op##_bcast_##sfx(s.dev<T>(ia), alen, ashape, arank, s.dev<T>(ib), blen,      \
+                                                      bshape, brank, s.dev<T>(io), outlen));                     \
+    }
+CH_BCAST_HOST(add, float, f32)
+CH_BCAST_HOST(sub, float, f32)
+CH_BCAST_HOST(mul, float, f32)
+CH_BCAST_HOST(div, float, f32)
+CH_BCAST_HOST(add, double, f64)
+CH_BCAST_HOST(sub, double, f64)
+CH_BCAST_HOST(mul, double, f64)
+CH_BCAST_HOST(div, double, f64)
+#undef CH_BCAST_HOST
+
+int32_t cleave_hip_sum_to_shape_f32_host(const float* g, int64_t glen, const int32_t* gshape, int32_t grank,
+                                         float* out, int64_t outlen, const int32_t* oshape, int32_t orank) {
+    Staged s("cleave_hip_sum_to_shape_f32_host");
+    const int ig = s.in(g, glen, 4), io = s.out(out, outlen, 4);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_sum_to_shape_f32(s.dev<float>(ig), glen, gshape, grank, s.dev<float>(io), outlen,
+                                                oshape, orank));
+}
+
+int32_t cleave_hip_sum_to_shape_f64_host(const double* g, int64_t glen, const int32_t* gshape, int32_t grank,
+                                         double* out, int64_t outlen, const int32_t* oshape, int32_t orank) {
+    Staged s("cleave_hip_sum_to_shape_f64_host");
+    const int ig = s.in(g, glen, 8), io = s.out(out, outlen, 8);
+    int32_t st = s.stage();
+    if (st != CLEAVE_HIP_OK) return st;
+    return s.finish(cleave_hip_sum_to_shape_f64(s.dev<double>(ig), glen, gshape, grank, s.dev<double>(io), outlen,
+                                                oshape, orank));
+}
+
 int32_t cleave_hip_zero_f64_host(double* out, int64_t outlen) {
     Staged s("cleave_hip_zero_f64_host");
     const int io = s.out(out, outlen, 8);

@@ -227,6 +227,37 @@ CLEAVE_HIP_API int32_t cleave_hip_sum_rows_f32(const float* g, int64_t glen, flo
                                                int32_t rows, int32_t cols);
 
 /* ---------------------------------------------------------------------- */
+/* Broadcasting maps (extension: the reference's Ring<Tensor> maps need     */
+/* equal shapes, stdlib/linalg/tensor.cleave:66-71, and Activation<Tensor>  */
+/* is rank 1, stdlib/nn/nn.cleave:82)                                       */
+/* ---------------------------------------------------------------------- */
+
+/* out = a op b with numpy's broadcasting: the shapes (host arrays of rank
+ * 0 .. 8, dimensions >= 0) align at their last dimension, a missing leading
+ * dimension is 1, and a dimension of 1 stretches to the other operand's.
+ * Each output element is one IEEE operation, as in the same-shape maps.
+ * Requires alen and blen to match the shapes and outlen the broadcast shape;
+ * shapes that do not broadcast are CLEAVE_HIP_ERR_ARG. */
+CLEAVE_HIP_API int32_t cleave_hip_add_bcast_f32(const float* a, int64_t alen, const int32_t* ashape, int32_t arank,
+                                                const float* b, int64_t blen, const int32_t* bshape, int32_t brank,
+                                                float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_sub_bcast_f32(const float* a, int64_t alen, const int32_t* ashape, int32_t arank,
+                                                const float* b, int64_t blen, const int32_t* bshape, int32_t brank,
+                                                float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_mul_bcast_f32(const float* a, int64_t alen, const int32_t* ashape, int32_t arank,
+                                                const float* b, int64_t blen, const int32_t* bshape, int32_t brank,
+                                                float* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_div_bcast_f32(const float* a, int64_t alen, const int32_t* ashape, int32_t arank,
+                                                const float* b, int64_t blen, const int32_t* bshape, int32_t brank,
+                                                float* out, int64_t outlen);
+/* Reverse rule of a broadcast: out (shape oshape, which broadcasts to
+ * gshape) = g summed over the dimensions that broadcasting stretched, in an
+ * order fixed by the shapes.  Requires orank <= grank <= 8. */
+CLEAVE_HIP_API int32_t cleave_hip_sum_to_shape_f32(const float* g, int64_t glen, const int32_t* gshape,
+                                                   int32_t grank, float* out, int64_t outlen,
+                                                   const int32_t* oshape, int32_t orank);
+
+/* ---------------------------------------------------------------------- */
 /* Sum / Mean / Max (stdlib/nn/nn.cleave:111-149)                           */
 /* ---------------------------------------------------------------------- */
 
@@ -365,6 +396,21 @@ CLEAVE_HIP_API int32_t cleave_hip_add_row_bias_f64(const double* a, int64_t alen
                                                    double* out, int64_t outlen, int32_t rows, int32_t cols);
 CLEAVE_HIP_API int32_t cleave_hip_sum_rows_f64(const double* g, int64_t glen, double* out, int64_t outlen,
                                                int32_t rows, int32_t cols);
+CLEAVE_HIP_API int32_t cleave_hip_add_bcast_f64(const double* a, int64_t alen, const int32_t* ashape,
+                                                int32_t arank, const double* b, int64_t blen, const int32_t* bshape,
+                                                int32_t brank, double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_sub_bcast_f64(const double* a, int64_t alen, const int32_t* ashape,
+                                                int32_t arank, const double* b, int64_t blen, const int32_t* bshape,
+                                                int32_t brank, double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_mul_bcast_f64(const double* a, int64_t alen, const int32_t* ashape,
+                                                int32_t arank, const double* b, int64_t blen, const int32_t* bshape,
+                                                int32_t brank, double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_div_bcast_f64(const double* a, int64_t alen, const int32_t* ashape,
+                                                int32_t arank, const double* b, int64_t blen, const int32_t* bshape,
+                                                int32_t brank, double* out, int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_sum_to_shape_f64(const double* g, int64_t glen, const int32_t* gshape,
+                                                   int32_t grank, double* out, int64_t outlen,
+                                                   const int32_t* oshape, int32_t orank);
 CLEAVE_HIP_API int32_t cleave_hip_reduce_sum_f64(const double* x, int64_t len, double* out_dev);
 CLEAVE_HIP_API int32_t cleave_hip_reduce_max_f64(const double* x, int64_t len, double* max_dev,
                                                  int64_t* argmax_dev);
@@ -442,6 +488,25 @@ CLEAVE_HIP_API int32_t cleave_hip_add_row_bias_f32_host(const float* a, int64_t 
                                                         int32_t cols);
 CLEAVE_HIP_API int32_t cleave_hip_sum_rows_f32_host(const float* g, int64_t glen, float* out, int64_t outlen,
                                                     int32_t rows, int32_t cols);
+CLEAVE_HIP_API int32_t cleave_hip_add_bcast_f32_host(const float* a, int64_t alen, const int32_t* ashape,
+                                                     int32_t arank, const float* b, int64_t blen,
+                                                     const int32_t* bshape, int32_t brank, float* out,
+                                                     int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_sub_bcast_f32_host(const float* a, int64_t alen, const int32_t* ashape,
+                                                     int32_t arank, const float* b, int64_t blen,
+                                                     const int32_t* bshape, int32_t brank, float* out,
+                                                     int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_mul_bcast_f32_host(const float* a, int64_t alen, const int32_t* ashape,
+                                                     int32_t arank, const float* b, int64_t blen,
+                                                     const int32_t* bshape, int32_t brank, float* out,
+                                                     int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_div_bcast_f32_host(const float* a, int64_t alen, const int32_t* ashape,
+                                                     int32_t arank, const float* b, int64_t blen,
+                                                     const int32_t* bshape, int32_t brank, float* out,
+                                                     int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_sum_to_shape_f32_host(const float* g, int64_t glen, const int32_t* gshape,
+                                                        int32_t grank, float* out, int64_t outlen,
+                                                        const int32_t* oshape, int32_t orank);
 
 /* Sum / Mean / Max (stdlib/nn/nn.cleave:111-149): the value is returned, as
  * by the stdlib functions; NaN (argmax -1, u64 sum 0) after an error. */
@@ -495,6 +560,25 @@ CLEAVE_HIP_API int32_t cleave_hip_add_row_bias_f64_host(const double* a, int64_t
                                                         int32_t cols);
 CLEAVE_HIP_API int32_t cleave_hip_sum_rows_f64_host(const double* g, int64_t glen, double* out, int64_t outlen,
                                                     int32_t rows, int32_t cols);
+CLEAVE_HIP_API int32_t cleave_hip_add_bcast_f64_host(const double* a, int64_t alen, const int32_t* ashape,
+                                                     int32_t arank, const double* b, int64_t blen,
+                                                     const int32_t* bshape, int32_t brank, double* out,
+                                                     int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_sub_bcast_f64_host(const double* a, int64_t alen, const int32_t* ashape,
+                                                     int32_t arank, const double* b, int64_t blen,
+                                                     const int32_t* bshape, int32_t brank, double* out,
+                                                     int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_mul_bcast_f64_host(const double* a, int64_t alen, const int32_t* ashape,
+                                                     int32_t arank, const double* b, int64_t blen,
+                                                     const int32_t* bshape, int32_t brank, double* out,
+                                                     int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_div_bcast_f64_host(const double* a, int64_t alen, const int32_t* ashape,
+                                                     int32_t arank, const double* b, int64_t blen,
+                                                     const int32_t* bshape, int32_t brank, double* out,
+                                                     int64_t outlen);
+CLEAVE_HIP_API int32_t cleave_hip_sum_to_shape_f64_host(const double* g, int64_t glen, const int32_t* gshape,
+                                                        int32_t grank, double* out, int64_t outlen,
+                                                        const int32_t* oshape, int32_t orank);
 CLEAVE_HIP_API double cleave_hip_sum_f64_host(const double* x, int64_t len);
 CLEAVE_HIP_API double cleave_hip_mean_f64_host(const double* x, int64_t len);
 CLEAVE_HIP_API double cleave_hip_max_of_f64_host(const double* x, int64_t len);

@@ -255,6 +255,102 @@ void or_sum_rows_f32(const float* g, float* out, int32_t rows, int32_t cols) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* Broadcasting maps and their reverse rule (extension: the reference's      */
+/* Ring<Tensor> maps need equal shapes, stdlib/linalg/tensor.cleave:66-71,   */
+/* and Activation<Tensor> is rank 1, stdlib/nn/nn.cleave:82).  numpy's rule: */
+/* shapes aligned at their last dimension, a missing leading dimension is 1, */
+/* a dimension of 1 stretches to the other operand's.                        */
+/* ------------------------------------------------------------------------ */
+
+/* Right-aligns a rank-r shape into R dimensions. */
+static void or_align(const int32_t* sh, int32_t r, int R, int64_t* d) {
+    for (int i = 0; i < R; ++i) d[i] = i < R - r ? 1 : sh[i - (R - r)];
+}
+
+/* The output shape of a broadcast: its rank, or -1 when the shapes do not
+ * broadcast (or a rank is outside 0 .. 8). */
+static int or_bcast_shape(const int32_t* ash, int32_t ar, const int32_t* bsh, int32_t br, int64_t* da, int64_t* db,
+                          int64_t* dn) {
+    if (ar < 0 || ar > 8 || br < 0 || br > 8) return -1;
+    const int R = ar > br ? (ar > 0 ? ar : 1) : (br > 0 ? br : 1);
+    or_align(ash, ar, R, da);
+    or_align(bsh, br, R, db);
+    for (int i = 0; i < R; ++i) {
+        if (da[i] != db[i] && da[i] != 1 && db[i] != 1) return -1;
+        dn[i] = da[i] == 1 ? db[i] : da[i];
+    }
+    return R;
+}
+
+/* out = a op b (op 0 add, 1 sub, 2 mul, 3 div), output elements in row-major
+ * order, each one IEEE operation on the elements its index maps to.  Returns
+ * -1 when the shapes do not broadcast. */
+#define OR_BCAST(T, sfx)                                                                                         \
+    int32_t or_bcast_##sfx(int32_t op, const T* a, const int32_t* ash, int32_t ar, const T* b,                   \
+                           const int32_t* bsh, int32_t br, T* out) {                                             \
+        int64_t da[8], db[8], dn[8], idx[8] = {0};                                                               \
+        const int R = or_bcast_shape(ash, ar, bsh, br, da, db, dn);                                              \
+        if (R < 0) return -1;                                                                                    \
+        int64_t total = 1;                                                                                       \
+        for (int i = 0; i < R; ++i) total *= dn[i];                                                              \
+        for (int64_t o = 0; o < total; ++o) {                                                                    \
+            int64_t oa = 0, ob = 0, sa = 1, sb = 1;                                                              \
+            for (int i = R - 1; i >= 0; --i) {                                                                   \
+                oa += (da[i] == 1 ? 0 : idx[i]) * sa;                                                            \
+                ob += (db[i] == 1 ? 0 : idx[i]) * sb;                                                            \
+                sa *= da[i];                                                                                     \
+                sb *= db[i];                                                                                     \
+            }                                                                                                    \
+            const T x = a[oa], y = b[ob];                                                                        \
+            out[o] = op == 0 ? x + y : op == 1 ? x - y : op == 2 ? x * y : x / y;                                \
+            for (int i = R - 1; i >= 0; --i) {                                                                   \
+                if (++idx[i] < dn[i]) break;                                                                     \
+                idx[i] = 0;                                                                                      \
+            }                                                                                                    \
+        }                                                                                                        \
+        return 0;                                                                                                \
+    }
+OR_BCAST(float, f32)
+OR_BCAST(double, f64)
+#undef OR_BCAST
+
+/* out (shape osh, broadcasting to gsh) = g summed over the stretched
+ * dimensions: out starts at zero and every element of g, in row-major order,
+ * is added into the element its index maps to -- for each output element,
+ * its terms in row-major order of the stretched dimensions.  Returns -1 when
+ * osh does not broadcast to gsh. */
+#define OR_SUM_TO_SHAPE(T, sfx)                                                                                  \
+    int32_t or_sum_to_shape_##sfx(const T* g, const int32_t* gsh, int32_t gr, T* out, const int32_t* osh,        \
+                                  int32_t orank) {                                                               \
+        if (gr < 0 || gr > 8 || orank < 0 || orank > gr) return -1;                                              \
+        const int R = gr > 0 ? gr : 1;                                                                           \
+        int64_t dg[8], dout[8], so[8], idx[8] = {0};                                                             \
+        or_align(gsh, gr, R, dg);                                                                                \
+        or_align(osh, orank, R, dout);                                                                           \
+        int64_t gtotal = 1, ototal = 1;                                                                          \
+        for (int i = R - 1; i >= 0; --i) {                                                                       \
+            if (dout[i] != dg[i] && dout[i] != 1) return -1;                                                     \
+            so[i] = ototal;                                                                                      \
+            ototal *= dout[i];                                                                                   \
+            gtotal *= dg[i];                                                                                     \
+        }                                                                                                        \
+        for (int64_t o = 0; o < ototal; ++o) out[o] = 0;                                                         \
+        for (int64_t e = 0; e < gtotal; ++e) {                                                                   \
+            int64_t oo = 0;                                                                                      \
+            for (int i = 0; i < R; ++i) oo += (dout[i] == 1 ? 0 : idx[i]) * so[i];                               \
+            out[oo] = out[oo] + g[e];                                                                            \
+            for (int i = R - 1; i >= 0; --i) {                                                                   \
+                if (++idx[i] < dg[i]) break;                                                                     \
+                idx[i] = 0;                                                                                      \
+            }                                                                                                    \
+        }                                                                                                        \
+        return 0;                                                                                                \
+    }
+OR_SUM_TO_SHAPE(float, f32)
+OR_SUM_TO_SHAPE(double, f64)
+#undef OR_SUM_TO_SHAPE
+
+/* ------------------------------------------------------------------------ */
 /* Index (stdlib/linalg/tensor.cleave:113-133): tensor.extract over the     */
 /* row-major buffer (cleave/src/mlir_lower.rs:1968-2002).                   */
 /* ------------------------------------------------------------------------ */

@@ -100,6 +100,25 @@ void or_add_row_bias_f32(const float* a, const float* bias, float* out, int32_t 
  * sums, a fold-order case that cancels differently, float64 bound. */
 void or_sum_rows_f32(const float* g, float* out, int32_t rows, int32_t cols);
 
+/* ---- broadcasting maps and their reverse rule (extension) ---- */
+
+/* out = a op b (op: 0 add, 1 sub, 2 mul, 3 div) under numpy's broadcasting of
+ * shapes ash (rank ar) and bsh (rank br), ranks 0 .. 8; -1 when they do not
+ * broadcast.  Pinned: numpy's broadcast arithmetic bit for bit (one IEEE
+ * operation per element), and equal shapes reduce to the same-shape maps. */
+int32_t or_bcast_f32(int32_t op, const float* a, const int32_t* ash, int32_t ar, const float* b, const int32_t* bsh,
+                     int32_t br, float* out);
+int32_t or_bcast_f64(int32_t op, const double* a, const int32_t* ash, int32_t ar, const double* b,
+                     const int32_t* bsh, int32_t br, double* out);
+/* out (shape osh) = g (shape gsh) summed over the dimensions osh stretches,
+ * each output's terms in row-major order from zero; -1 when osh does not
+ * broadcast to gsh.  Pinned: numpy sums in float64 under the sum bound, exact
+ * integer-valued cases, and [rows, cols] -> [cols] against or_sum_rows. */
+int32_t or_sum_to_shape_f32(const float* g, const int32_t* gsh, int32_t gr, float* out, const int32_t* osh,
+                            int32_t orank);
+int32_t or_sum_to_shape_f64(const double* g, const int32_t* gsh, int32_t gr, double* out, const int32_t* osh,
+                            int32_t orank);
+
 /* ---- Index (stdlib/linalg/tensor.cleave:113-133) ---- */
 
 /* tensor.extract over the row-major buffer (cleave/src/mlir_lower.rs:1968-2002):

@@ -55,6 +55,10 @@ _SIGS = {
     "or_index_f32": (_i32, [_p, _p, _i32, _p, _p]),
     "or_add_row_bias_f32": (None, [_p, _p, _p, _i32, _i32]),
     "or_sum_rows_f32": (None, [_p, _p, _i32, _i32]),
+    "or_bcast_f32": (_i32, [_i32, _p, _p, _i32, _p, _p, _i32, _p]),
+    "or_bcast_f64": (_i32, [_i32, _p, _p, _i32, _p, _p, _i32, _p]),
+    "or_sum_to_shape_f32": (_i32, [_p, _p, _i32, _p, _p, _i32]),
+    "or_sum_to_shape_f64": (_i32, [_p, _p, _i32, _p, _p, _i32]),
     "or_index_bwd_f32": (_i32, [_f, _p, _p, _i32, _p]),
     "or_sum_u32_u64": (_u64, [_p, _i64]),
     "or_escape_count_f32": (C.c_uint32, [_f, _f, _i32]),
@@ -255,6 +259,61 @@ def sum_rows(g) -> np.ndarray:
     rows, cols = g.shape
     out = np.empty(cols, np.float32)
     lib().or_sum_rows_f32(_ptr(g), _ptr(out), rows, cols)
+    return out
+
+
+# ---- broadcasting maps and their reverse rule (extension) -------------------------------
+
+_BCAST_OPS = {"add": 0, "sub": 1, "mul": 2, "div": 3}
+
+
+def _shape_arg(shape):
+    arr = np.ascontiguousarray(np.array(shape, dtype=np.int32).reshape(-1))
+    return arr, (_ptr(arr) if arr.size else None)
+
+
+def _bcast_out_shape(ashape, bshape):
+    """The broadcast shape, by the rule itself (aligned at the last dimension,
+    missing leading dimensions 1, a 1 stretches); None when it fails."""
+    R = max(len(ashape), len(bshape), 1)
+    da = (1,) * (R - len(ashape)) + tuple(ashape)
+    db = (1,) * (R - len(bshape)) + tuple(bshape)
+    out = []
+    for x, y in zip(da, db):
+        if x != y and x != 1 and y != 1:
+            return None
+        out.append(y if x == 1 else x)
+    return tuple(out) if (len(ashape) or len(bshape)) else ()
+
+
+def bcast(op: str, a, b, f64: bool = False) -> np.ndarray:
+    """a op b under broadcasting (or_bcast_f32 / _f64); ValueError when the
+    shapes do not broadcast."""
+    conv = _f64 if f64 else _f32
+    a, b = conv(a), conv(b)
+    shape = _bcast_out_shape(a.shape, b.shape)
+    if shape is None:
+        raise ValueError(f"shapes {a.shape} and {b.shape} do not broadcast")
+    out = np.empty(shape, np.float64 if f64 else np.float32)
+    sa, pa = _shape_arg(a.shape)
+    sb, pb = _shape_arg(b.shape)
+    fn = lib().or_bcast_f64 if f64 else lib().or_bcast_f32
+    rc = fn(_BCAST_OPS[op], _ptr(a), pa, a.ndim, _ptr(b), pb, b.ndim, _ptr(out))
+    assert rc == 0
+    return out
+
+
+def sum_to_shape(g, shape, f64: bool = False) -> np.ndarray:
+    """g summed down to `shape` over the dimensions it stretches
+    (or_sum_to_shape_f32 / _f64)."""
+    g = (_f64 if f64 else _f32)(g)
+    out = np.empty(tuple(shape), np.float64 if f64 else np.float32)
+    sg, pg = _shape_arg(g.shape)
+    so, po = _shape_arg(tuple(shape))
+    fn = lib().or_sum_to_shape_f64 if f64 else lib().or_sum_to_shape_f32
+    rc = fn(_ptr(g), pg, g.ndim, _ptr(out), po, len(shape))
+    if rc != 0:
+        raise ValueError(f"shape {tuple(shape)} does not broadcast to {g.shape}")
     return out
 
 

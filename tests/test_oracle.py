@@ -460,3 +460,87 @@ def test_xor_tensor_training_matches_reference_record(oracle, golden):
     # The record is the reference's printed f32 output; its gradient expressions
     # come from e-graph extraction and its libm is MSVC's, so bits may differ.
     assert np.allclose(preds, g["predictions"], atol=1e-6, rtol=0)
+
+
+# ---- broadcasting maps and their reverse rule (extension) ---------------------------
+
+_BCAST_PAIRS = [
+    ((3, 4), (4,)), ((3, 4), (3, 1)), ((3, 1), (1, 4)), ((2, 3, 4), (3, 1)), ((2, 1, 4), (1, 3, 1)),
+    ((5,), ()), ((), (2, 3)), ((1,), (7,)), ((2, 3, 4, 5), (1, 3, 1, 5)), ((4, 1, 1), (4, 6, 2)),
+    ((2, 0, 3), (3,)), ((6, 5), (6, 5)),
+]
+
+
+@pytest.mark.parametrize("ashape,bshape", _BCAST_PAIRS)
+@pytest.mark.parametrize("f64", [False, True])
+def test_bcast_is_numpy_broadcast_arithmetic(oracle, ashape, bshape, f64):
+    # numpy applies the same rule and one IEEE operation per element in the
+    # operands' dtype, so the restated loop must agree bit for bit
+    rng = np.random.default_rng(len(ashape) * 31 + len(bshape))
+    dt = np.float64 if f64 else np.float32
+    a = rng.standard_normal(ashape).astype(dt)
+    b = (rng.standard_normal(bshape) + 3.0).astype(dt)
+    for op, f in (("add", np.add), ("sub", np.subtract), ("mul", np.multiply), ("div", np.divide)):
+        got = oracle.bcast(op, a, b, f64=f64)
+        want = f(a, b)
+        assert got.shape == want.shape
+        assert np.array_equal(got.view(np.uint64 if f64 else np.uint32), want.view(np.uint64 if f64 else np.uint32))
+
+
+def test_bcast_equal_shapes_is_the_same_shape_map(oracle):
+    rng = np.random.default_rng(5)
+    a, b = rng.standard_normal((7, 9)).astype(np.float32), rng.standard_normal((7, 9)).astype(np.float32)
+    assert np.array_equal(oracle.bcast("add", a, b).ravel(), oracle.add(a.ravel(), b.ravel()))
+    assert np.array_equal(oracle.bcast("div", a, b).ravel(), oracle.div(a.ravel(), b.ravel()))
+
+
+@pytest.mark.parametrize("ashape,bshape", [((3, 4), (3,)), ((2, 3), (3, 2)), ((4, 1, 5), (2, 5, 1, 1, 3))])
+def test_bcast_rejects_shapes_that_do_not_broadcast(oracle, ashape, bshape):
+    with pytest.raises(ValueError):
+        oracle.bcast("add", np.zeros(ashape), np.zeros(bshape))
+
+
+_SUM_CASES = [((6, 5), (5,)), ((6, 5), (6, 1)), ((6, 5), (1, 1)), ((6, 5), ()), ((2, 3, 4), (3, 1)),
+              ((2, 3, 4), (1, 3, 4)), ((2, 3, 4), (2, 1, 4)), ((3, 1, 4), (1, 1, 4)), ((4, 5), (4, 5))]
+
+
+@pytest.mark.parametrize("gshape,oshape", _SUM_CASES)
+def test_sum_to_shape_against_numpy(oracle, gshape, oshape):
+    rng = np.random.default_rng(len(gshape) + 7 * len(oshape))
+    g = rng.standard_normal(gshape).astype(np.float32)
+    got = oracle.sum_to_shape(g, oshape)
+    R = len(gshape)
+    full = (1,) * (R - len(oshape)) + tuple(oshape)
+    axes = tuple(i for i in range(R) if full[i] == 1 and gshape[i] != 1)
+    want = g.astype(np.float64).sum(axis=axes, keepdims=True).reshape(oshape)
+    den = np.abs(g.astype(np.float64)).sum(axis=axes, keepdims=True).reshape(oshape)
+    n = max(1, int(np.prod([gshape[i] for i in axes])))
+    assert got.shape == tuple(oshape)
+    assert np.all(np.abs(got - want) <= 1e-6 * n * den + 1e-30)
+    # integer values: every partial sum is exact, so any order gives the sum
+    gi = rng.integers(-50, 50, gshape).astype(np.float32)
+    assert np.array_equal(oracle.sum_to_shape(gi, oshape),
+                          gi.astype(np.float64).sum(axis=axes, keepdims=True).reshape(oshape).astype(np.float32))
+    # f64 form
+    got64 = oracle.sum_to_shape(g.astype(np.float64), oshape, f64=True)
+    assert np.all(np.abs(got64 - want) <= 1e-14 * n * den + 1e-300)
+
+
+def test_sum_to_shape_leading_rows_is_the_column_sum(oracle):
+    # [rows, cols] -> [cols] is the row bias's reverse rule: the same left fold
+    # down each column (0 + g[0][j] = g[0][j] for nonzero data)
+    g = np.random.default_rng(3).standard_normal((37, 11)).astype(np.float32)
+    assert np.array_equal(oracle.sum_to_shape(g, (11,)), oracle.sum_rows(g))
+
+
+def test_sum_to_shape_adds_in_row_major_order(oracle):
+    # 1e8 + 1 rounds back to 1e8 in f32, so the row-major order over the
+    # stretched dimension gives 0 where the exact sum is 1; a different order
+    # (1 last, or pairwise) would not
+    g = np.array([[1e8], [1.0], [-1e8]], np.float32)
+    assert oracle.sum_to_shape(g, (1,))[0] == 0.0
+    g2 = np.array([[[1e8, 2.0], [1.0, 0.0]], [[-1e8, 0.0], [0.0, 0.0]]], np.float32)  # (2, 2, 2) -> (1, 2)
+    got = oracle.sum_to_shape(g2, (1, 2))
+    assert got[0, 0] == 0.0 and got[0, 1] == 2.0
+    with pytest.raises(ValueError):
+        oracle.sum_to_shape(np.zeros((3, 4), np.float32), (2, 4))
