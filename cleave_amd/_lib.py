@@ -248,6 +248,16 @@ SIGNATURES: dict[str, tuple] = {
     "_mlir_ciface_cleave_hip_sgd_update_f32": (i32, [vp, vp, f32]),
     "_mlir_ciface_cleave_hip_add_row_bias_f32": (i32, [vp, vp, vp]),
     "_mlir_ciface_cleave_hip_sum_rows_f32": (i32, [vp, vp]),
+    "_mlir_ciface_cleave_hip_add_bcast_f32": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_sub_bcast_f32": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_mul_bcast_f32": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_div_bcast_f32": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_add_bcast_f64": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_sub_bcast_f64": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_mul_bcast_f64": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_div_bcast_f64": (i32, [vp, vp, vp]),
+    "_mlir_ciface_cleave_hip_sum_to_shape_f32": (i32, [vp, vp]),
+    "_mlir_ciface_cleave_hip_sum_to_shape_f64": (i32, [vp, vp]),
     "_mlir_ciface_cleave_hip_sum_f32": (f32, [vp]),
     "_mlir_ciface_cleave_hip_mean_f32": (f32, [vp]),
     "_mlir_ciface_cleave_hip_max_of_f32": (f32, [vp]),

@@ -164,6 +164,52 @@ int32_t map2_mr(int32_t (*f)(const T*, int64_t, const T*, int64_t, T*, int64_t),
              reinterpret_cast<T*>(O.data), O.count);
 }
 
+// Sizes of a view as the int32 shape array the pointer forms take.
+int32_t shape_i32(const View& v, const char* fn, int32_t* out) {
+    for (int64_t d = 0; d < v.rank; ++d) CH_TRY(narrow(v.sizes[d], fn, "extent", &out[d]));
+    return CLEAVE_HIP_OK;
+}
+
+// A broadcasting map: each operand row-major contiguous with its own sizes;
+// out shaped as their broadcast (numpy's rule, checked by the pointer form;
+// out's own sizes checked here).
+template <class T>
+int32_t bcast_mr(int32_t (*f)(const T*, int64_t, const int32_t*, int32_t, const T*, int64_t, const int32_t*, int32_t,
+                              T*, int64_t),
+                 cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out, const char* fn) {
+    View A, B, O;
+    CH_TRY(flat_view(a, sizeof(T), fn, "a", nullptr, &A));
+    CH_TRY(flat_view(b, sizeof(T), fn, "b", nullptr, &B));
+    CH_TRY(flat_view(out, sizeof(T), fn, "out", nullptr, &O));
+    int32_t as[kMaxRank], bs[kMaxRank];
+    CH_TRY(shape_i32(A, fn, as));
+    CH_TRY(shape_i32(B, fn, bs));
+    const int64_t R = A.rank > B.rank ? A.rank : B.rank;
+    bool fits = O.rank == R;
+    for (int64_t i = 0; fits && i < R; ++i) {
+        const int64_t ja = i - (R - A.rank), jb = i - (R - B.rank);
+        const int64_t da = ja < 0 ? 1 : A.sizes[ja], db = jb < 0 ? 1 : B.sizes[jb];
+        if (da != db && da != 1 && db != 1) break;  // the pointer form reports it
+        fits = O.sizes[i] == (da == 1 ? db : da);
+    }
+    CH_REQUIRE(fits, "%s: out's sizes are not the broadcast of a's and b's", fn);
+    return f(reinterpret_cast<const T*>(A.data), A.count, as, (int32_t)A.rank, reinterpret_cast<const T*>(B.data),
+             B.count, bs, (int32_t)B.rank, reinterpret_cast<T*>(O.data), O.count);
+}
+
+template <class T>
+int32_t sum_to_shape_mr(int32_t (*f)(const T*, int64_t, const int32_t*, int32_t, T*, int64_t, const int32_t*, int32_t),
+                        cleave_hip_mr g, cleave_hip_mr out, const char* fn) {
+    View G, O;
+    CH_TRY(flat_view(g, sizeof(T), fn, "g", nullptr, &G));
+    CH_TRY(flat_view(out, sizeof(T), fn, "out", nullptr, &O));
+    int32_t gs[kMaxRank], os[kMaxRank];
+    CH_TRY(shape_i32(G, fn, gs));
+    CH_TRY(shape_i32(O, fn, os));
+    return f(reinterpret_cast<const T*>(G.data), G.count, gs, (int32_t)G.rank, reinterpret_cast<T*>(O.data), O.count,
+             os, (int32_t)O.rank);
+}
+
 // A host-returning reduction over a contiguous operand; `bad` after an error.
 template <class R, class T>
 R reduce_mr(R (*f)(const T*, int64_t), cleave_hip_mr x, const char* fn, R bad) {
@@ -225,6 +271,28 @@ int32_t _mlir_ciface_cleave_hip_matmul_f64(cleave_hip_mr a, cleave_hip_mr b, cle
     CH_MAP2(relu_bwd, T, sfx)
 CH_MAPS(float, f32)
 CH_MAPS(double, f64)
+
+#define CH_BCAST_MR(name, T, sfx)                                                                               \
+    int32_t _mlir_ciface_cleave_hip_##name##_bcast_##sfx(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out) { \
+        return bcast_mr<T>(cleave_hip_##name##_bcast_##sfx, a, b, out,                                           \
+                           "_mlir_ciface_cleave_hip_" #name "_bcast_" #sfx);                                     \
+    }
+CH_BCAST_MR(add, float, f32)
+CH_BCAST_MR(sub, float, f32)
+CH_BCAST_MR(mul, float, f32)
+CH_BCAST_MR(div, float, f32)
+CH_BCAST_MR(add, double, f64)
+CH_BCAST_MR(sub, double, f64)
+CH_BCAST_MR(mul, double, f64)
+CH_BCAST_MR(div, double, f64)
+#undef CH_BCAST_MR
+
+int32_t _mlir_ciface_cleave_hip_sum_to_shape_f32(cleave_hip_mr g, cleave_hip_mr out) {
+    return sum_to_shape_mr<float>(cleave_hip_sum_to_shape_f32, g, out, "_mlir_ciface_cleave_hip_sum_to_shape_f32");
+}
+int32_t _mlir_ciface_cleave_hip_sum_to_shape_f64(cleave_hip_mr g, cleave_hip_mr out) {
+    return sum_to_shape_mr<double>(cleave_hip_sum_to_shape_f64, g, out, "_mlir_ciface_cleave_hip_sum_to_shape_f64");
+}
 
 int32_t _mlir_ciface_cleave_hip_zero_f32(cleave_hip_mr out) {
     const char* fn = "_mlir_ciface_cleave_hip_zero_f32";

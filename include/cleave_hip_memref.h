@@ -26,7 +26,8 @@
  *   - element-wise operands, reduction inputs and every output: row-major
  *     contiguous (stride of dim i = product of the sizes after it; a dim of
  *     size 1 may carry any stride), with identical sizes (no broadcasting,
- *     as in the reference);
+ *     as in the reference), except in the _bcast maps and sum_to_shape,
+ *     whose operands keep their own sizes;
  *   - matmul operands: rank 2 [M x K], [K x N] (rank 3 with a leading batch
  *     for the batched forms), each either row-major or the transpose of a
  *     row-major buffer (strides {1, M} for A).  A transposed operand becomes
@@ -93,6 +94,20 @@ CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_sgd_update_f32(cleave_hip_mr w, c
  * its reverse rule sums g [rows x cols] over the rows into out [cols]. */
 CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_add_row_bias_f32(cleave_hip_mr a, cleave_hip_mr bias, cleave_hip_mr out);
 CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_sum_rows_f32(cleave_hip_mr g, cleave_hip_mr out);
+/* Broadcasting maps (extension): out = a op b under numpy's broadcasting of
+ * a's and b's sizes; out's sizes must be the broadcast shape.  Ranks 0 .. 8. */
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_add_bcast_f32(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_sub_bcast_f32(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_mul_bcast_f32(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_div_bcast_f32(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_add_bcast_f64(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_sub_bcast_f64(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_mul_bcast_f64(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_div_bcast_f64(cleave_hip_mr a, cleave_hip_mr b, cleave_hip_mr out);
+/* Their reverse rule: out (sizes broadcasting to g's) = g summed over the
+ * stretched dimensions. */
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_sum_to_shape_f32(cleave_hip_mr g, cleave_hip_mr out);
+CLEAVE_HIP_API int32_t _mlir_ciface_cleave_hip_sum_to_shape_f64(cleave_hip_mr g, cleave_hip_mr out);
 
 /* Sum / Mean / Max (stdlib/nn/nn.cleave:111-149), host-returning. */
 CLEAVE_HIP_API float _mlir_ciface_cleave_hip_sum_f32(cleave_hip_mr x);

@@ -172,3 +172,29 @@ def test_mlp_step(hip, mr, oracle, B, D, H):
     assert_mlp_grads_close(g1, g2, dW1_r, dW2_r, X, Y, W1, W2, f"memref B={B}")
     assert np.array_equal(w1.numpy(), W1 - np.float32(lr) * g1)
     assert np.array_equal(w2.numpy(), W2 - np.float32(lr) * g2)
+
+
+def test_broadcast_forms(hip, oracle):
+    # the _bcast maps and sum_to_shape on descriptors: each operand keeps its
+    # own sizes, out holds the broadcast shape
+    import cleave_amd.memref as mr
+
+    rng = np.random.default_rng(61)
+    A = rng.standard_normal((6, 1, 40)).astype(np.float32)
+    B = (rng.standard_normal((5, 1)) + 3).astype(np.float32)
+    a, b, out = hip.from_numpy(A), hip.from_numpy(B), hip.empty((6, 5, 40))
+    for op in ("add", "sub", "mul", "div"):
+        mr.call(f"cleave_hip_{op}_bcast_f32", mr.of(a), mr.of(b), mr.of(out))
+        assert np.array_equal(out.numpy(), oracle.bcast(op, A, B)), op
+    with pytest.raises(Exception, match="broadcast"):
+        mr.call("cleave_hip_add_bcast_f32", mr.of(a), mr.of(b), mr.of(hip.empty((6, 40, 5))))
+    s = hip.empty((1, 5, 1))
+    mr.call("cleave_hip_sum_to_shape_f32", mr.of(out), mr.of(s))
+    O = out.numpy()
+    want = O.astype(np.float64).sum(axis=(0, 2), keepdims=True)
+    assert np.all(np.abs(s.numpy() - want) <= 1e-6 * 240 * np.abs(O).astype(np.float64).sum(axis=(0, 2),
+                                                                                              keepdims=True))
+    A64, B64 = A.astype(np.float64), B.astype(np.float64)
+    a64, b64, o64 = hip.from_numpy(A64), hip.from_numpy(B64), hip.empty((6, 5, 40), "f64")
+    mr.call("cleave_hip_mul_bcast_f64", mr.of(a64), mr.of(b64), mr.of(o64))
+    assert np.array_equal(o64.numpy(), oracle.bcast("mul", A64, B64, f64=True))
