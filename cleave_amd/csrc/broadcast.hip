@@ -399,9 +399,16 @@ void bcast_strides(const int64_t* d, int R, int64_t* e) {
     }
 }
 
+// Element count of shape d (rank R): 0 when a dimension is 0, -1 when the
+// count exceeds int64 (no operand length matches it).
 int64_t shape_prod(const int64_t* d, int R) {
+    for (int i = 0; i < R; ++i)
+        if (d[i] == 0) return 0;
     int64_t p = 1;
-    for (int i = 0; i < R; ++i) p *= d[i];
+    for (int i = 0; i < R; ++i) {
+        if (p > INT64_MAX / d[i]) return -1;
+        p *= d[i];
+    }
     return p;
 }
 
@@ -412,6 +419,8 @@ int32_t plan_bcast(const char* fn, const int32_t* ash, int32_t ar, int64_t alen,
     CH_REQUIRE(ar >= 0 && ar <= kMaxRank && br >= 0 && br <= kMaxRank, "%s: ranks %d and %d (each 0 .. %d)", fn,
                ar, br, kMaxRank);
     CH_REQUIRE((ar == 0 || ash) && (br == 0 || bsh), "%s: null shape array", fn);
+    CH_REQUIRE(alen >= 0 && blen >= 0 && outlen >= 0, "%s: negative length (%lld, %lld, %lld)", fn,
+               (long long)alen, (long long)blen, (long long)outlen);
     const int R = ar > br ? (ar > 0 ? ar : 1) : (br > 0 ? br : 1);
     int64_t da[kMaxRank], db[kMaxRank], n[kMaxRank], ea[kMaxRank], eb[kMaxRank];
     CH_REQUIRE(align_shape(ash, ar, R, da) && align_shape(bsh, br, R, db), "%s: negative dimension", fn);
@@ -502,6 +511,14 @@ struct RDims {
     int64_t rtotal;                      // elements summed per output element
 };
 
+// out = 0 (a fill kernel rather than hipMemsetAsync, so that the call can be
+// captured in a graph).
+template <class T>
+__global__ __launch_bounds__(kThreads) void zero_fill_kernel(T* __restrict__ out, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+        out[i] = T(0);
+}
+
 // One thread per output element: its reduced elements in row-major order.
 template <class T>
 __global__ __launch_bounds__(kThreads) void sum_to_shape_kernel(const T* __restrict__ g, T* __restrict__ out, RDims d,
@@ -571,6 +588,8 @@ int32_t run_sum_to_shape(const char* fn, const T* g, int64_t glen, const int32_t
     CH_REQUIRE(gr >= 0 && gr <= kMaxRank && orank >= 0 && orank <= gr, "%s: ranks %d (g) and %d (out): need "
                "0 <= out rank <= g rank <= %d", fn, gr, orank, kMaxRank);
     CH_REQUIRE((gr == 0 || gsh) && (orank == 0 || osh), "%s: null shape array", fn);
+    CH_REQUIRE(glen >= 0 && outlen >= 0, "%s: negative length (%lld, %lld)", fn, (long long)glen,
+               (long long)outlen);
     const int R = gr > 0 ? gr : 1;
     int64_t dg[kMaxRank], dout[kMaxRank], eg[kMaxRank];
     CH_REQUIRE(align_shape(gsh, gr, R, dg) && align_shape(osh, orank, R, dout), "%s: negative dimension", fn);
@@ -581,10 +600,15 @@ int32_t run_sum_to_shape(const char* fn, const T* g, int64_t glen, const int32_t
                "%s: lengths (%lld, %lld) do not match the shapes' (%lld, %lld)", fn, (long long)glen,
                (long long)outlen, (long long)shape_prod(dg, R), (long long)shape_prod(dout, R));
     if (outlen == 0) return CLEAVE_HIP_OK;
-    CH_REQUIRE(g && out, "%s: null buffer", fn);
+    CH_REQUIRE(out && (g || glen == 0), "%s: null buffer", fn);
     CH_INIT_OR_RETURN();
-    CH_DEVICE(fn, g, glen * sizeof(T));
     CH_DEVICE(fn, out, outlen * sizeof(T));
+    if (glen == 0) {  // a reduced dimension of 0: sums over nothing
+        zero_fill_kernel<T><<<blocks_for(outlen), kThreads, 0, ch::stream()>>>(out, outlen);
+        CH_LAUNCHED(fn);
+        return CLEAVE_HIP_OK;
+    }
+    CH_DEVICE(fn, g, glen * sizeof(T));
     // g's row-major strides; runs of kept (dout == dg) and reduced dimensions,
     // dimensions of 1 dropped, alike neighbours merged
     int64_t st = 1;

@@ -37,6 +37,8 @@ int32_t read_view(cleave_hip_mr m, int esz, const char* fn, const char* arg, Vie
     for (int64_t i = 0; i < v->rank; ++i) {
         CH_REQUIRE(v->sizes[i] >= 0, "%s: %s: negative size %lld in dim %lld", fn, arg,
                    (long long)v->sizes[i], (long long)i);
+        CH_REQUIRE(v->sizes[i] == 0 || v->count <= INT64_MAX / v->sizes[i],
+                   "%s: %s: element count past int64 at dim %lld", fn, arg, (long long)i);
         v->count *= v->sizes[i];
     }
     CH_REQUIRE(offset >= 0, "%s: %s: negative offset %lld", fn, arg, (long long)offset);

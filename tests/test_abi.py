@@ -154,6 +154,28 @@ def test_argument_validation_happens_before_any_device_work(fn, args, needle):
     assert fn in msg and needle in msg, msg
 
 
+def test_broadcast_shapes_and_lengths_are_checked_before_any_device_work():
+    import numpy as np
+
+    lib, _lib = _lib_noabort()
+    big = np.array([65536] * 4, np.int32)  # 2^64 elements: past int64, refused rather than wrapped to 0
+    one = np.array([1], np.int32)
+    cases = [
+        (lib.cleave_hip_add_bcast_f32, (None, 0, big.ctypes.data, 4, None, 1, one.ctypes.data, 1, None, 0),
+         "do not match"),
+        (lib.cleave_hip_mul_bcast_f64, (None, -1, one.ctypes.data, 1, None, 1, one.ctypes.data, 1, None, 1),
+         "negative length"),
+        (lib.cleave_hip_sum_to_shape_f32, (None, 0, big.ctypes.data, 4, None, 1, one.ctypes.data, 1),
+         "do not match"),
+        (lib.cleave_hip_sum_to_shape_f64, (None, 1, one.ctypes.data, 1, None, -1, one.ctypes.data, 1),
+         "negative length"),
+    ]
+    for fn, args, needle in cases:
+        assert fn(*args) == _lib.ERR_ARG
+        code, msg = _lib.last_error()
+        assert code == _lib.ERR_ARG and needle in msg, msg
+
+
 def test_zero_length_maps_are_no_ops_without_a_device():
     lib, _lib = _lib_noabort()
     assert lib.cleave_hip_add_f32(None, 0, None, 0, None, 0) == 0

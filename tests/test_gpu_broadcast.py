@@ -139,6 +139,20 @@ def test_sum_to_shape_against_oracle(hip, oracle, gshape, oshape, dt):
                           oracle.sum_to_shape(Gi, oshape, f64=dt == np.float64))
 
 
+@pytest.mark.parametrize("gshape,oshape", [((0, 5), (1, 5)), ((0, 5), (5,)), ((3, 0, 4), (3, 1, 4)), ((0,), ()),
+                                           ((2, 0), (2, 1))])
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_sum_to_shape_over_an_empty_dimension_is_zero(hip, oracle, gshape, oshape, dt):
+    # a reduced dimension of 0 sums over nothing: zeros, as numpy and the
+    # oracle give, over whatever out held before
+    G = np.zeros(gshape, dt)
+    out = hip.from_numpy(np.full(oshape, np.nan, dt))
+    got = hip.sum_to_shape(hip.from_numpy(G), oshape, out=out).numpy()
+    assert got.shape == tuple(oshape)
+    assert np.array_equal(got, oracle.sum_to_shape(G, oshape, f64=dt == np.float64))
+    assert np.array_equal(got, np.zeros(oshape, dt))
+
+
 def test_sum_to_shape_general_path_is_the_oracle_order(hip, oracle):
     # the one-thread-per-output path adds each output's terms in row-major
     # order from zero, as the oracle does: bit for bit
