@@ -46,6 +46,15 @@ void* scratch_try(int slot, size_t bytes);
 // Number of compute units (for grid sizing of persistent/strided kernels).
 int num_cus();
 
+// a * b * c for non-negative factors, or -1 when the product exceeds int64
+// (so that no operand length matches it).
+inline int64_t count3(int64_t a, int64_t b, int64_t c) {
+    if (a == 0 || b == 0 || c == 0) return 0;
+    if (a > INT64_MAX / b) return -1;
+    const int64_t ab = a * b;
+    return ab > INT64_MAX / c ? -1 : ab * c;
+}
+
 // Workspace of the allocation-free entry point (cleave_hip_reduce_sum_f32_noalloc):
 // a static device array of kNoAllocFloats floats, its device address resolved
 // once at init with the library's device current.  nullptr when that failed.

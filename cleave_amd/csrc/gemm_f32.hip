@@ -759,8 +759,8 @@ int32_t cleave_hip_matmul_batched_f32(const float* a, int64_t alen, const float*
                "cleave_hip_matmul_batched_f32: bad dims (batch=%d M=%d N=%d K=%d)", batch, M, N, K);
     CH_REQUIRE((trans_a == 0 || trans_a == 1) && (trans_b == 0 || trans_b == 1),
                "cleave_hip_matmul_batched_f32: trans flags must be 0 or 1");
-    CH_REQUIRE(alen == (int64_t)batch * M * K && blen == (int64_t)batch * K * N &&
-                   clen == (int64_t)batch * M * N,
+    const int64_t na = ch::count3(batch, M, K), nb = ch::count3(batch, K, N), nc = ch::count3(batch, M, N);
+    CH_REQUIRE(na >= 0 && nb >= 0 && nc >= 0 && alen == na && blen == nb && clen == nc,
                "cleave_hip_matmul_batched_f32: lengths do not match batch*M*K, batch*K*N, batch*M*N");
     CH_REQUIRE(a && b && c, "cleave_hip_matmul_batched_f32: null buffer");
     CH_INIT_OR_RETURN();

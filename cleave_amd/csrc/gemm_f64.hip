@@ -213,7 +213,8 @@ int32_t run_matmul_f64(const char* fn, const double* a, int64_t alen, const doub
     CH_REQUIRE((trans_a == 0 || trans_a == 1) && (trans_b == 0 || trans_b == 1), "%s: trans flags must be 0 or 1",
                fn);
     const int64_t sa = (int64_t)M * K, sb = (int64_t)K * N, sc = (int64_t)M * N;
-    CH_REQUIRE(alen == sa * batch && blen == sb * batch && clen == sc * batch,
+    const int64_t na = ch::count3(batch, M, K), nb = ch::count3(batch, K, N), nc = ch::count3(batch, M, N);
+    CH_REQUIRE(na >= 0 && nb >= 0 && nc >= 0 && alen == na && blen == nb && clen == nc,
                "%s: lengths (%lld, %lld, %lld) do not match batch %d of %d x %d x %d", fn, (long long)alen,
                (long long)blen, (long long)clen, batch, M, N, K);
     if (clen == 0) return CLEAVE_HIP_OK;

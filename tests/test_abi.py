@@ -135,6 +135,10 @@ def _lib_noabort():
     ("cleave_hip_matmul_batched_bf16", (None, 8, None, 8, None, 7, 2, 2, 2, 2, 0, 0), "lengths"),
     ("cleave_hip_matmul_batched_bf16", (None, 8, None, 8, None, 8, 2, 2, 2, 2, 0, 3), "trans"),
     ("cleave_hip_matmul_batched_f32", (None, 8, None, 8, None, 8, 0, 2, 2, 2, 0, 0), "batch"),
+    # batch * M * K = 2^64: refused, not wrapped to lengths of 0
+    ("cleave_hip_matmul_batched_f64", (None, 0, None, 0, None, 0, 16, 1 << 30, 1 << 30, 1 << 30, 0, 0), "lengths"),
+    ("cleave_hip_matmul_batched_f32", (None, 0, None, 0, None, 0, 65535, 2147483647, 2147483647, 2147483647, 0, 0),
+     "lengths"),
     ("cleave_hip_add_f32", (None, 3, None, 4, None, 3), "broadcast"),
     ("cleave_hip_sigmoid_f32", (None, 3, None, 2, ), "length"),
     ("cleave_hip_sgd_update_f32", (None, 3, None, 2, 0.1), "glen"),
