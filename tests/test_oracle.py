@@ -526,6 +526,16 @@ def test_sum_to_shape_against_numpy(oracle, gshape, oshape):
     assert np.all(np.abs(got64 - want) <= 1e-14 * n * den + 1e-300)
 
 
+@pytest.mark.parametrize("gshape,oshape,axes", [((0, 5), (1, 5), (0,)), ((3, 0, 4), (3, 1, 4), (1,)), ((0,), (), (0,))])
+def test_sum_to_shape_over_an_empty_dimension_is_zero(oracle, gshape, oshape, axes):
+    # numpy's sum over nothing: zeros of the kept shape
+    g = np.zeros(gshape, np.float32)
+    want = g.sum(axis=axes, keepdims=len(oshape) == len(gshape)).reshape(oshape)
+    assert np.array_equal(want, np.zeros(oshape, np.float32))
+    assert np.array_equal(oracle.sum_to_shape(g, oshape), want)
+    assert np.array_equal(oracle.sum_to_shape(g.astype(np.float64), oshape, f64=True), want)
+
+
 def test_sum_to_shape_leading_rows_is_the_column_sum(oracle):
     # [rows, cols] -> [cols] is the row bias's reverse rule: the same left fold
     # down each column (0 + g[0][j] = g[0][j] for nonzero data)
