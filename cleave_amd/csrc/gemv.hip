@@ -30,30 +30,39 @@ constexpr int kThreads = 256;
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
 
-// 16 bytes of T as floats.
+// 16 bytes of T as floats.  load: a cached load (a vector that every row
+// reads again); load_nt: a non-temporal one, for a matrix streamed once (on
+// data read once, 16-byte loads stream about 7.3 TB/s with the non-temporal
+// hint against 6.2 without it).
 template <typename T>
 struct Vec16;
 template <>
 struct Vec16<float> {
     static constexpr int N = 4;
     typedef float raw __attribute__((ext_vector_type(4)));
-    __device__ static void load(const float* p, float (&o)[4]) {
-        const raw r = *reinterpret_cast<const raw*>(p);
+    __device__ static void unpack(raw r, float (&o)[4]) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = r[i];
+    }
+    __device__ static void load(const float* p, float (&o)[4]) { unpack(*reinterpret_cast<const raw*>(p), o); }
+    __device__ static void load_nt(const float* p, float (&o)[4]) {
+        unpack(__builtin_nontemporal_load(reinterpret_cast<const raw*>(p)), o);
     }
 };
 template <>
 struct Vec16<uint16_t> {
     static constexpr int N = 8;
     typedef uint32_t raw __attribute__((ext_vector_type(4)));
-    __device__ static void load(const uint16_t* p, float (&o)[8]) {
-        const raw r = *reinterpret_cast<const raw*>(p);
+    __device__ static void unpack(raw r, float (&o)[8]) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             o[2 * i] = __uint_as_float(r[i] << 16);
             o[2 * i + 1] = __uint_as_float(r[i] & 0xFFFF0000u);
         }
+    }
+    __device__ static void load(const uint16_t* p, float (&o)[8]) { unpack(*reinterpret_cast<const raw*>(p), o); }
+    __device__ static void load_nt(const uint16_t* p, float (&o)[8]) {
+        unpack(__builtin_nontemporal_load(reinterpret_cast<const raw*>(p)), o);
     }
 };
 
@@ -85,7 +94,7 @@ __global__ __launch_bounds__(kThreads) void row_dots_kernel(const T* __restrict_
                     float a[4][E], b[4][E];
 #pragma unroll
                     for (int u = 0; u < 4; ++u) {
-                        Vec16<T>::load(x + k + u * step, a[u]);
+                        Vec16<T>::load_nt(x + k + u * step, a[u]);
                         Vec16<T>::load(w + k + u * step, b[u]);
                     }
 #pragma unroll
@@ -95,7 +104,7 @@ __global__ __launch_bounds__(kThreads) void row_dots_kernel(const T* __restrict_
                 }
                 for (; k < K; k += step) {
                     float a[E], b[E];
-                    Vec16<T>::load(x + k, a);
+                    Vec16<T>::load_nt(x + k, a);
                     Vec16<T>::load(w + k, b);
 #pragma unroll
                     for (int e = 0; e < E; ++e) acc = acc + a[e] * b[e];
@@ -136,7 +145,7 @@ __global__ __launch_bounds__(kThreads) void row_dots_split_kernel(const T* __res
             float a[4][E], b[4][E];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                Vec16<T>::load(x + k + u * step, a[u]);
+                Vec16<T>::load_nt(x + k + u * step, a[u]);
                 Vec16<T>::load(w + k + u * step, b[u]);
             }
 #pragma unroll
@@ -146,7 +155,7 @@ __global__ __launch_bounds__(kThreads) void row_dots_split_kernel(const T* __res
         }
         for (; k < k1; k += step) {
             float a[E], b[E];
-            Vec16<T>::load(x + k, a);
+            Vec16<T>::load_nt(x + k, a);
             Vec16<T>::load(w + k, b);
 #pragma unroll
             for (int e = 0; e < E; ++e) acc = acc + a[e] * b[e];
@@ -208,7 +217,7 @@ __global__ __launch_bounds__(kThreads) void wsum_stage1(const T* __restrict__ X,
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     w[u] = to_f32(v[r + u]);
-                    Vec16<T>::load(X + (r + u) * cols + c, a[u]);
+                    Vec16<T>::load_nt(X + (r + u) * cols + c, a[u]);
                 }
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
@@ -218,7 +227,7 @@ __global__ __launch_bounds__(kThreads) void wsum_stage1(const T* __restrict__ X,
             for (; r < r1; ++r) {
                 float a[E];
                 const float w = to_f32(v[r]);
-                Vec16<T>::load(X + r * cols + c, a);
+                Vec16<T>::load_nt(X + r * cols + c, a);
 #pragma unroll
                 for (int e = 0; e < E; ++e) acc[e] = acc[e] + w * a[e];
             }
@@ -237,23 +246,46 @@ __global__ __launch_bounds__(kThreads) void wsum_stage1(const T* __restrict__ X,
         if (c + e < cols) p[e] = acc[e];
 }
 
+constexpr int kWsumSplit = 8, kWsumCols = kThreads / kWsumSplit;
 __global__ __launch_bounds__(kThreads) void wsum_stage2(const float* __restrict__ part, float* __restrict__ y,
                                                         int64_t cols, int64_t groups) {
+    // kWsumSplit threads per column, each adding a contiguous eighth of the
+    // groups (eight loads in flight), then the eighths in order.  With one
+    // thread per column, a column's 256 groups took 32 dependent rounds of
+    // loads on 16 workgroups (12.6 us of a 171 us f32 v^T X at 65536 x 4096);
+    // split, the product measured 164 us (bf16 103 -> 89, f32 100000 x 1000
+    // 110 -> 73).
+    __shared__ float red[kWsumSplit][kWsumCols];
     const int64_t b = blockIdx.y;
-    const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (j >= cols) return;
+    const int jj = threadIdx.x % kWsumCols, sp = threadIdx.x / kWsumCols;
+    const int64_t j = (int64_t)blockIdx.x * kWsumCols + jj;
+    const int64_t q0 = groups * sp / kWsumSplit, q1 = groups * (sp + 1) / kWsumSplit;
     const float* p = part + b * groups * cols + j;
-    float acc = p[0];
-    int64_t g = 1;
-    for (; g + 8 <= groups; g += 8) {
-        float t[8];
+    float acc = 0.0f;
+    if (j < cols && q0 < q1) {
+        acc = p[q0 * cols];
+        int64_t g = q0 + 1;
+        for (; g + 8 <= q1; g += 8) {
+            float t[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) t[u] = p[(g + u) * cols];
+            for (int u = 0; u < 8; ++u) t[u] = p[(g + u) * cols];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc = acc + t[u];
+            for (int u = 0; u < 8; ++u) acc = acc + t[u];
+        }
+        for (; g < q1; ++g) acc = acc + p[g * cols];
     }
-    for (; g < groups; ++g) acc = acc + p[g * cols];
-    y[b * cols + j] = acc;
+    red[sp][jj] = acc;
+    __syncthreads();
+    if (sp == 0 && j < cols) {
+        // the non-empty eighths in order (one is empty only when groups < 8;
+        // the last never is)
+        int t = 0;
+        while (groups * (t + 1) / kWsumSplit == groups * t / kWsumSplit) ++t;
+        float r = red[t][jj];
+        for (++t; t < kWsumSplit; ++t)
+            if (groups * (t + 1) / kWsumSplit > groups * t / kWsumSplit) r = r + red[t][jj];
+        y[b * cols + j] = r;
+    }
 }
 
 // ---- outer product ------------------------------------------------------------------
@@ -436,6 +468,8 @@ constexpr int kSkMfmaUnroll = 4;  // blocks of k whose loads are issued together
 //     ds_read_b64_tr_b16 (in a 16-lane group, source lane 4j + q points at
 //     k-row kb + j, values c0 + 4q .. c0 + 4q + 3, and result lane i receives
 //     value c0 + i of k-rows kb .. kb + 3), two per fragment.
+// X is read once (each wave owns its rows over every column), so its loads
+// carry the non-temporal hint wherever a wave reads whole 128-byte lines.
 // Only the wave touches its region, and a wave's LDS instructions execute in
 // order, so no barrier is needed; the asm statements keep the compiler from
 // moving the reads above the writes (or the next writes above the reads).
@@ -509,7 +543,7 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
 #pragma unroll
             for (int l = 0; l < F::LINES; ++l)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) data[l][j] = *reinterpret_cast<const f4v*>(src[j] + kb + 128 * l);
+                for (int j = 0; j < 4; ++j) data[l][j] = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(src[j] + kb + 128 * l));
         };
         auto load_v = [&](int b0, frag(&vv)[UB]) {
 #pragma unroll
@@ -571,7 +605,13 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
         auto load_x = [&](int b0) {
             const int64_t k0 = (int64_t)b0 * F::KBLK;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) data[j] = *reinterpret_cast<const f4v*>(src0 + (k0 + krj[j]) * xs_k);
+            for (int j = 0; j < 4; ++j) {
+                const f4v* q = reinterpret_cast<const f4v*>(src0 + (k0 + krj[j]) * xs_k);
+                // f32: the wave's 32 values are a whole 128-byte line, read once; bf16:
+                // half a line, whose other half the next wave reads (a cached load)
+                if constexpr (ESZ == 4) data[j] = __builtin_nontemporal_load(q);
+                else data[j] = *q;
+            }
         };
         auto load_v = [&](int b0, frag(&vv)[UB]) {
 #pragma unroll
@@ -776,7 +816,7 @@ int32_t weighted_sums(const T* X, const T* v, float* y, int K, int64_t cols, int
         wsum_stage1<T, false><<<g1, kThreads, 0, ch::stream()>>>(X, v, part, K, cols, nseg, groups, rpg);
     int32_t st = ch::check_hip(hipGetLastError(), "wsum_stage1");
     if (st != CLEAVE_HIP_OK) return st;
-    const dim3 g2((unsigned)((cols + kThreads - 1) / kThreads), (unsigned)batch);
+    const dim3 g2((unsigned)((cols + kWsumCols - 1) / kWsumCols), (unsigned)batch);
     wsum_stage2<<<g2, kThreads, 0, ch::stream()>>>(part, y, cols, groups);
     return ch::check_hip(hipGetLastError(), "wsum_stage2");
 }
