@@ -31,9 +31,8 @@ __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
 
 // 16 bytes of T as floats.  load: a cached load (a vector that every row
-// reads again); load_nt: a non-temporal one, for a matrix streamed once (on
-// data read once, 16-byte loads stream about 7.3 TB/s with the non-temporal
-// hint against 6.2 without it).
+// reads again); load_nt: a non-temporal one, for a matrix streamed once and
+// too large for the MALL (below).
 template <typename T>
 struct Vec16;
 template <>
@@ -66,6 +65,21 @@ struct Vec16<uint16_t> {
     }
 };
 
+// A matrix read once streams with non-temporal loads when it is larger than
+// the MI355X's 256 MiB MALL: on data read once, 16-byte loads stream about
+// 7.3 TB/s with the hint against 6.2 without it (f32 65536 x 4096 . v 0.80 ->
+// 0.88 of HBM).  A smaller one stays cached: across calls it is still in the
+// MALL, and the hint then cost 5-38% (bf16 4096^2 . v 4.8 -> 6.6 us, f32
+// 16384 x 4096 . v 37.8 -> 39.8).
+constexpr int64_t kStreamBytes = 256LL << 20;
+inline bool stream_nt(int64_t bytes) { return bytes > kStreamBytes; }
+
+template <typename T, bool NT>
+__device__ __forceinline__ void load_x(const T* p, float (&o)[Vec16<T>::N]) {
+    if constexpr (NT) Vec16<T>::load_nt(p, o);
+    else Vec16<T>::load(p, o);
+}
+
 // ---- row dots ---------------------------------------------------------------------
 //
 // y[r] = sum_k X[r][k] v[(r / rows_per_vec) * K + k] for r < rows.  A row is
@@ -73,7 +87,7 @@ struct Vec16<uint16_t> {
 // does not leave most of a wave idle; lane l of a row takes the 16-byte
 // chunks l, l + lpr, ... (VEC) or the elements l, l + lpr, ... (scalar), four
 // chunks in flight, and the row's lanes are then added by a shuffle tree.
-template <typename T, bool VEC>
+template <typename T, bool VEC, bool NT>
 __global__ __launch_bounds__(kThreads) void row_dots_kernel(const T* __restrict__ X, const T* __restrict__ v,
                                                             float* __restrict__ y, int64_t rows, int K,
                                                             int64_t rows_per_vec, int lpr) {
@@ -94,7 +108,7 @@ __global__ __launch_bounds__(kThreads) void row_dots_kernel(const T* __restrict_
                     float a[4][E], b[4][E];
 #pragma unroll
                     for (int u = 0; u < 4; ++u) {
-                        Vec16<T>::load_nt(x + k + u * step, a[u]);
+                        load_x<T, NT>(x + k + u * step, a[u]);
                         Vec16<T>::load(w + k + u * step, b[u]);
                     }
 #pragma unroll
@@ -104,7 +118,7 @@ __global__ __launch_bounds__(kThreads) void row_dots_kernel(const T* __restrict_
                 }
                 for (; k < K; k += step) {
                     float a[E], b[E];
-                    Vec16<T>::load_nt(x + k, a);
+                    load_x<T, NT>(x + k, a);
                     Vec16<T>::load(w + k, b);
 #pragma unroll
                     for (int e = 0; e < E; ++e) acc = acc + a[e] * b[e];
@@ -125,7 +139,7 @@ __global__ __launch_bounds__(kThreads) void row_dots_kernel(const T* __restrict_
 // chunks as above; its sum is the shuffle tree of each wave, then the four
 // waves in order, into part[row][slice]; row_dots_fold adds a row's slices
 // in order.
-template <typename T, bool VEC>
+template <typename T, bool VEC, bool NT>
 __global__ __launch_bounds__(kThreads) void row_dots_split_kernel(const T* __restrict__ X, const T* __restrict__ v,
                                                                   float* __restrict__ part, int K, int64_t rows_per_vec,
                                                                   int slices, int64_t slice) {
@@ -145,7 +159,7 @@ __global__ __launch_bounds__(kThreads) void row_dots_split_kernel(const T* __res
             float a[4][E], b[4][E];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                Vec16<T>::load_nt(x + k + u * step, a[u]);
+                load_x<T, NT>(x + k + u * step, a[u]);
                 Vec16<T>::load(w + k + u * step, b[u]);
             }
 #pragma unroll
@@ -155,7 +169,7 @@ __global__ __launch_bounds__(kThreads) void row_dots_split_kernel(const T* __res
         }
         for (; k < k1; k += step) {
             float a[E], b[E];
-            Vec16<T>::load_nt(x + k, a);
+            load_x<T, NT>(x + k, a);
             Vec16<T>::load(w + k, b);
 #pragma unroll
             for (int e = 0; e < E; ++e) acc = acc + a[e] * b[e];
@@ -191,7 +205,7 @@ __global__ __launch_bounds__(kThreads) void row_dots_fold(const float* __restric
 // of rows in ascending order, into part[b][group][j]; stage 2 adds the
 // groups in ascending order.  The column sums of broadcast.hip use the same
 // tiling.
-template <typename T, bool VEC>
+template <typename T, bool VEC, bool NT>
 __global__ __launch_bounds__(kThreads) void wsum_stage1(const T* __restrict__ X, const T* __restrict__ v,
                                                         float* __restrict__ part, int K, int64_t cols, int64_t nseg,
                                                         int64_t groups, int64_t rpg) {
@@ -217,7 +231,7 @@ __global__ __launch_bounds__(kThreads) void wsum_stage1(const T* __restrict__ X,
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     w[u] = to_f32(v[r + u]);
-                    Vec16<T>::load_nt(X + (r + u) * cols + c, a[u]);
+                    load_x<T, NT>(X + (r + u) * cols + c, a[u]);
                 }
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
@@ -227,7 +241,7 @@ __global__ __launch_bounds__(kThreads) void wsum_stage1(const T* __restrict__ X,
             for (; r < r1; ++r) {
                 float a[E];
                 const float w = to_f32(v[r]);
-                Vec16<T>::load_nt(X + r * cols + c, a);
+                load_x<T, NT>(X + r * cols + c, a);
 #pragma unroll
                 for (int e = 0; e < E; ++e) acc[e] = acc[e] + w * a[e];
             }
@@ -468,12 +482,14 @@ constexpr int kSkMfmaUnroll = 4;  // blocks of k whose loads are issued together
 //     ds_read_b64_tr_b16 (in a 16-lane group, source lane 4j + q points at
 //     k-row kb + j, values c0 + 4q .. c0 + 4q + 3, and result lane i receives
 //     value c0 + i of k-rows kb .. kb + 3), two per fragment.
-// X is read once (each wave owns its rows over every column), so its loads
-// carry the non-temporal hint wherever a wave reads whole 128-byte lines.
+// X is read once (each wave owns its rows over every column): NT (X larger
+// than the MALL, stream_nt) gives its loads the non-temporal hint wherever a
+// wave reads whole 128-byte lines.  A template flag, since the compiler
+// merges a run-time choice between the two loads into one plain load.
 // Only the wave touches its region, and a wave's LDS instructions execute in
 // order, so no barrier is needed; the asm statements keep the compiler from
 // moving the reads above the writes (or the next writes above the reads).
-template <typename T, int MR, int RB, int XM, bool VV>
+template <typename T, int MR, int RB, int XM, bool VV, bool NT>
 __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
     const T* __restrict__ X, const T* __restrict__ V, float* __restrict__ y, float* __restrict__ part, int64_t R,
     int S, int K, int64_t xs_r, int64_t xs_k, int64_t vs_s, int64_t vs_k, int64_t ys_i, int64_t ys_s,
@@ -543,7 +559,11 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
 #pragma unroll
             for (int l = 0; l < F::LINES; ++l)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) data[l][j] = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(src[j] + kb + 128 * l));
+                for (int j = 0; j < 4; ++j) {
+                    const f4v* q = reinterpret_cast<const f4v*>(src[j] + kb + 128 * l);
+                    if constexpr (NT) data[l][j] = __builtin_nontemporal_load(q);
+                    else data[l][j] = *q;
+                }
         };
         auto load_v = [&](int b0, frag(&vv)[UB]) {
 #pragma unroll
@@ -609,7 +629,7 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
                 const f4v* q = reinterpret_cast<const f4v*>(src0 + (k0 + krj[j]) * xs_k);
                 // f32: the wave's 32 values are a whole 128-byte line, read once; bf16:
                 // half a line, whose other half the next wave reads (a cached load)
-                if constexpr (ESZ == 4) data[j] = __builtin_nontemporal_load(q);
+                if constexpr (NT && ESZ == 4) data[j] = __builtin_nontemporal_load(q);
                 else data[j] = *q;
             }
         };
@@ -762,6 +782,7 @@ template <typename T>
 int32_t row_dots(const T* X, const T* v, float* y, int64_t rows, int K, int64_t rows_per_vec) {
     // vector loads when every row and vector start is 16-byte aligned
     const bool vec = (int64_t)K * (int64_t)sizeof(T) % 16 == 0 && aligned16(X) && aligned16(v);
+    const bool nt = stream_nt(rows * (int64_t)K * (int64_t)sizeof(T));
     const int E = vec ? Vec16<T>::N : 1;
     const int chunks = K / E;
     int lpr = 1;
@@ -779,20 +800,30 @@ int32_t row_dots(const T* X, const T* v, float* y, int64_t rows, int K, int64_t 
         float* part = (float*)ch::scratch(8, sizeof(float) * (size_t)(rows * slices));
         if (!part) return CLEAVE_HIP_ERR_OOM;
         const dim3 g((unsigned)slices, (unsigned)rows);
-        if (vec)
-            row_dots_split_kernel<T, true><<<g, kThreads, 0, ch::stream()>>>(X, v, part, K, rows_per_vec, (int)slices, slice);
+        if (vec && nt)
+            row_dots_split_kernel<T, true, true><<<g, kThreads, 0, ch::stream()>>>(X, v, part, K, rows_per_vec,
+                                                                               (int)slices, slice);
+        else if (vec)
+            row_dots_split_kernel<T, true, false><<<g, kThreads, 0, ch::stream()>>>(X, v, part, K, rows_per_vec,
+                                                                                (int)slices, slice);
         else
-            row_dots_split_kernel<T, false><<<g, kThreads, 0, ch::stream()>>>(X, v, part, K, rows_per_vec, (int)slices, slice);
+            row_dots_split_kernel<T, false, false><<<g, kThreads, 0, ch::stream()>>>(X, v, part, K, rows_per_vec,
+                                                                                 (int)slices, slice);
         int32_t st = ch::check_hip(hipGetLastError(), "row_dots_split_kernel");
         if (st != CLEAVE_HIP_OK) return st;
         row_dots_fold<<<(unsigned)((rows + kThreads - 1) / kThreads), kThreads, 0, ch::stream()>>>(part, y, rows,
                                                                                                    (int)slices);
         return ch::check_hip(hipGetLastError(), "row_dots_fold");
     }
-    if (vec)
-        row_dots_kernel<T, true><<<capped_grid(blocks), kThreads, 0, ch::stream()>>>(X, v, y, rows, K, rows_per_vec, lpr);
+    if (vec && nt)
+        row_dots_kernel<T, true, true><<<capped_grid(blocks), kThreads, 0, ch::stream()>>>(X, v, y, rows, K,
+                                                                                        rows_per_vec, lpr);
+    else if (vec)
+        row_dots_kernel<T, true, false><<<capped_grid(blocks), kThreads, 0, ch::stream()>>>(X, v, y, rows, K,
+                                                                                         rows_per_vec, lpr);
     else
-        row_dots_kernel<T, false><<<capped_grid(blocks), kThreads, 0, ch::stream()>>>(X, v, y, rows, K, rows_per_vec, lpr);
+        row_dots_kernel<T, false, false><<<capped_grid(blocks), kThreads, 0, ch::stream()>>>(X, v, y, rows, K,
+                                                                                          rows_per_vec, lpr);
     return ch::check_hip(hipGetLastError(), "row_dots_kernel");
 }
 
@@ -810,10 +841,12 @@ int32_t weighted_sums(const T* X, const T* v, float* y, int K, int64_t cols, int
     float* part = (float*)ch::scratch(8, sizeof(float) * (size_t)(batch * groups * cols));
     if (!part) return CLEAVE_HIP_ERR_OOM;
     const dim3 g1((unsigned)(nseg * groups), (unsigned)batch);
-    if (vec)
-        wsum_stage1<T, true><<<g1, kThreads, 0, ch::stream()>>>(X, v, part, K, cols, nseg, groups, rpg);
+    if (vec && stream_nt((int64_t)batch * K * cols * (int64_t)sizeof(T)))
+        wsum_stage1<T, true, true><<<g1, kThreads, 0, ch::stream()>>>(X, v, part, K, cols, nseg, groups, rpg);
+    else if (vec)
+        wsum_stage1<T, true, false><<<g1, kThreads, 0, ch::stream()>>>(X, v, part, K, cols, nseg, groups, rpg);
     else
-        wsum_stage1<T, false><<<g1, kThreads, 0, ch::stream()>>>(X, v, part, K, cols, nseg, groups, rpg);
+        wsum_stage1<T, false, false><<<g1, kThreads, 0, ch::stream()>>>(X, v, part, K, cols, nseg, groups, rpg);
     int32_t st = ch::check_hip(hipGetLastError(), "wsum_stage1");
     if (st != CLEAVE_HIP_OK) return st;
     const dim3 g2((unsigned)((cols + kWsumCols - 1) / kWsumCols), (unsigned)batch);
@@ -836,8 +869,14 @@ int32_t skinny_mfma_launch(const T* X, const T* V, float* y, float* part, int64_
                            int64_t v_batch, int64_t y_batch, int batch, int64_t nrb, int groups, int bpg) {
     const int64_t waves = nrb * groups;
     const dim3 g((unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64)), (unsigned)batch);
-    skinny_mfma_kernel<T, MR, RB, XM, VV><<<g, kThreads, 0, ch::stream()>>>(
-        X, V, y, part, R, S, K, xs_r, xs_k, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch, y_batch, nrb, groups, bpg);
+    // the unstaged form (XM 0) and bf16 with r contiguous never take the hint
+    constexpr bool kMayNt = XM == 1 || (XM == 2 && sizeof(T) == 4);
+    if (kMayNt && stream_nt((int64_t)batch * R * K * (int64_t)sizeof(T)))
+        skinny_mfma_kernel<T, MR, RB, XM, VV, kMayNt><<<g, kThreads, 0, ch::stream()>>>(
+            X, V, y, part, R, S, K, xs_r, xs_k, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch, y_batch, nrb, groups, bpg);
+    else
+        skinny_mfma_kernel<T, MR, RB, XM, VV, false><<<g, kThreads, 0, ch::stream()>>>(
+            X, V, y, part, R, S, K, xs_r, xs_k, vs_s, vs_k, ys_i, ys_s, x_batch, v_batch, y_batch, nrb, groups, bpg);
     int32_t st = ch::check_hip(hipGetLastError(), "skinny_mfma_kernel");
     if (st != CLEAVE_HIP_OK || groups == 1) return st;
     const int64_t per = nrb * RB * SkMfma<T, MR>::ACC * 64;
