@@ -283,6 +283,35 @@ bool launch_edge(const uint16_t* a, const uint16_t* b, float* c, int M, int N, i
     return launch_tiled_edge<128, 128, 64, 2, 2, 2, 32, TA, TB>(a, b, c, M, N, K, batch, s, st);
 }
 
+// The paired-copy kernel's EDGE form (gemm_bf16_pingpong.hpp) for ragged
+// shapes in the range where their zero-padded copies would run the
+// paired-copy kernel (launch_fast): at least half a round of 256 x 256
+// tiles, a k-contiguous operand, and K past the short-K kernels' range (over
+// 256, and over 512 for a single round).  The copies and the crop move the
+// operands and C once more; here they are read in place.  False otherwise.
+template <bool TA, bool TB>
+bool launch_pairs_edge(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
+                       const Strides& s, int32_t* status) {
+    if constexpr (TA && !TB) {  // A^T B: no k-contiguous operand to pair
+        return false;
+    } else {
+        using P = ch::Bf16PingPongPairs<!TA, TB, true>;
+        const int64_t cus = ch::num_cus();
+        const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
+        const int64_t big = (int64_t)tiles_m * tiles_n * batch;
+        if (big * 2 < cus || K <= 256 || (big <= cus && K <= 512)) return false;
+        if (!P::fits_edge(M, N, K, s.lda, s.ldb) || !bases_aligned(a, b, s)) return false;
+        if (big > 0x7FFFFFFF) return false;
+        const int total = (int)big;
+        const int resident = cus >= 8 ? (int)(cus / 8 * 8) : (cus > 0 ? (int)cus : 1);
+        dim3 grid((unsigned)(total < resident ? total : resident));
+        ch::gemm_bf16_pingpong_pairs_kernel<!TA, TB, true><<<grid, P::THREADS, 0, ch::stream()>>>(
+            a, b, c, M, N, K, s.lda, s.ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch);
+        *status = ch::check_hip(hipGetLastError(), "gemm_bf16_pingpong_pairs_kernel");
+        return true;
+    }
+}
+
 // Ping-pong kernel (gemm_bf16_pingpong.hpp): 256 x 256 x 32 tiles in a ring
 // of five k-tiles (all 160 KiB of LDS).
 template <bool TA, bool TB>
@@ -451,6 +480,7 @@ int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N,
         return ch::matmul_skinny_bf16(a, b, c, M, N, K, batch, TA, TB);
     if (2.0 * M * N * K * batch >= kPadMinFlops) {
         if (launch_edge<TA, TB>(a, b, c, M, N, K, batch, packed<TA, TB>(M, N, K), &st)) return st;
+        if (launch_pairs_edge<TA, TB>(a, b, c, M, N, K, batch, packed<TA, TB>(M, N, K), &st)) return st;
         const ch::PadPlan p = ch::pad_plan(M, N, K, batch, TA, TB, a, b, 2, ch::num_cus(), kPadModel);
         auto gemm = [batch](const uint16_t* pa, const uint16_t* pb, float* pc, int Mp, int Np, int Kp) {
             int32_t s = CLEAVE_HIP_OK;

@@ -183,7 +183,7 @@ namespace ch {
 // single operand, copied as 64-byte row segments into k-contiguous single
 // stages: two pair rings would not fit 160 KiB with copies issued far
 // enough ahead.
-template <bool AKC, bool BKC>
+template <bool AKC, bool BKC, bool EDGE = false>
 struct Bf16PingPongPairs {
     static_assert(AKC || BKC, "at least one k-contiguous operand");
     static constexpr bool SKC = AKC && BKC;  // the single operand is k-contiguous too
@@ -204,15 +204,36 @@ struct Bf16PingPongPairs {
         const uint64_t b_span = (uint64_t)(BKC ? BN : K + 1) * (uint64_t)ldb * 2;
         return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
     }
+    // Bytes from an operand's base to the end of its last element.
+    static __host__ __device__ int64_t a_bytes(int M, int K, int64_t lda) {
+        return AKC ? ((int64_t)(M - 1) * lda + K) * 2 : ((int64_t)(K - 1) * lda + M) * 2;
+    }
+    static __host__ __device__ int64_t b_bytes(int N, int K, int64_t ldb) {
+        return BKC ? ((int64_t)(N - 1) * ldb + K) * 2 : ((int64_t)(K - 1) * ldb + N) * 2;
+    }
+    // Shapes the EDGE form takes (any M, N, K >= 1): whole 16-byte chunks (8
+    // elements) along each operand's contiguous extent and pitch, and
+    // operands under 2 GiB, so that a masked offset stays out of range.
+    static bool fits_edge(int M, int N, int K, int64_t lda, int64_t ldb) {
+        const bool chunks = (AKC ? K % 8 == 0 : M % 8 == 0) && (BKC ? K % 8 == 0 : N % 8 == 0) && lda % 8 == 0 &&
+                            ldb % 8 == 0;
+        return M >= 1 && N >= 1 && K >= 1 && chunks && a_bytes(M, K, lda) < (1ll << 31) &&
+               b_bytes(N, K, ldb) < (1ll << 31);
+    }
 };
 
-template <bool AKC, bool BKC>
+// EDGE (any M, N and K, fits_edge): tiles_m and tiles_n rounded up; the
+// copies become buffer loads into LDS whose lanes past the operand's rows
+// (columns) or past K read zeros (a masked offset past the resource's range,
+// as EdgeCopy), K is walked in whole pairs of k-tiles, and the stores skip
+// what lies past M or N.
+template <bool AKC, bool BKC, bool EDGE = false>
 __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC,
     int tiles_m, int tiles_n, int batch) {
     using namespace ch::tiles;
-    using P = Bf16PingPongPairs<AKC, BKC>;
+    using P = Bf16PingPongPairs<AKC, BKC, EDGE>;
     constexpr int FM = P::FM, FN = P::FN, NW = P::NW, BK = P::BK;
     constexpr int PAIRS = P::PAIRS, SINGLES = P::SINGLES;
     __shared__ __attribute__((aligned(1024))) char smem[P::LDS_BYTES];
@@ -221,7 +242,7 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int grp = wave / P::WN, wn = wave % P::WN;
     const uint32_t lds0 = lds_addr(smem);
-    const int nk = K / BK, np = nk / 2;
+    const int nk = EDGE ? (K + 2 * BK - 1) / (2 * BK) * 2 : K / BK, np = nk / 2;
 
     // The paired (k-contiguous) operand and the single one.  Each copy's
     // 64-bit scalar base holds the tile's first row (paired operand; single
@@ -234,6 +255,14 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
     const char* sbase;
     float* Ct;
     int m0, n0;
+    // EDGE: resources over this product's operands; per-lane pair-copy
+    // offsets from the paired operand's base (kOutOfRange past its rows) and
+    // the k of each lane's chunk in pair 0; the single operand's EdgeCopy.
+    const int pext = AKC ? M : N, sext = AKC ? N : M;  // rows of the paired / single operand
+    v4i rsrc_p{}, rsrc_s{};
+    uint32_t pvoff_e[4];
+    int pk0[4];
+    EdgeCopy<SKC, 256, BK, NW> ecopy;
     auto set_tile = [&](int t) {
         int bt, tm, tn;
         ch::block_coords(t, tiles_m, tiles_n, batch, bt, tm, tn);
@@ -242,8 +271,22 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
         const int pr0 = AKC ? m0 : n0, sr0 = AKC ? n0 : m0;
         const uint16_t* Ab = A + (int64_t)bt * strideA;
         const uint16_t* Bb = B + (int64_t)bt * strideB;
-        pbase = reinterpret_cast<const char*>(AKC ? Ab : Bb) + (int64_t)pr0 * pld * 2;
-        sbase = reinterpret_cast<const char*>(AKC ? Bb : Ab) + (SKC ? (int64_t)sr0 * sld * 2 : (int64_t)sr0 * 2);
+        if constexpr (EDGE) {
+            rsrc_p = buffer_rsrc(AKC ? Ab : Bb, (uint32_t)(AKC ? P::a_bytes(M, K, lda) : P::b_bytes(N, K, ldb)));
+            rsrc_s = buffer_rsrc(AKC ? Bb : Ab, (uint32_t)(AKC ? P::b_bytes(N, K, ldb) : P::a_bytes(M, K, lda)));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int q = wave + NW * j;
+                const int r = 8 * q + (lane >> 3);
+                const int c = (lane & 7) ^ ((r >> 1) & 7);
+                pvoff_e[j] = pr0 + r < pext ? (uint32_t)(((int64_t)(pr0 + r) * pld + 8 * c) * 2) : kOutOfRange;
+                pk0[j] = 8 * c;
+            }
+            ecopy.init(sld, sr0, sext, wave, lane);
+        } else {
+            pbase = reinterpret_cast<const char*>(AKC ? Ab : Bb) + (int64_t)pr0 * pld * 2;
+            sbase = reinterpret_cast<const char*>(AKC ? Bb : Ab) + (SKC ? (int64_t)sr0 * sld * 2 : (int64_t)sr0 * 2);
+        }
         Ct = C + (int64_t)bt * strideC;
     };
 
@@ -263,10 +306,19 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
     // half h of pair p: instructions j = 2h, 2h + 1 (rows 8q .. 8q+7, q = wave + 8j)
     auto issue_pair_half = [&](auto stage, auto half, int p) {
         constexpr int PS = decltype(stage)::value, HF = decltype(half)::value;
-        const char* src = pbase + (uint32_t)min(p, np - 1) * (uint32_t)(2 * BK * 2);
+        const int pc = min(p, np - 1);
+        if constexpr (EDGE) {
+            const uint32_t soff = (uint32_t)pc * (uint32_t)(2 * BK * 2);
 #pragma unroll
-        for (int j = 2 * HF; j < 2 * HF + 2; ++j)
-            dma16(src, pvoff[j], lds0 + (uint32_t)(PS * P::PAIR_BYTES + 1024 * (wave + NW * j)));
+            for (int j = 2 * HF; j < 2 * HF + 2; ++j)
+                dma16_buf(rsrc_p, pk0[j] + pc * 2 * BK < K ? pvoff_e[j] : kOutOfRange, soff,
+                          lds0 + (uint32_t)(PS * P::PAIR_BYTES + 1024 * (wave + NW * j)));
+        } else {
+            const char* src = pbase + (uint32_t)pc * (uint32_t)(2 * BK * 2);
+#pragma unroll
+            for (int j = 2 * HF; j < 2 * HF + 2; ++j)
+                dma16(src, pvoff[j], lds0 + (uint32_t)(PS * P::PAIR_BYTES + 1024 * (wave + NW * j)));
+        }
     };
     auto issue_pair = [&](auto stage, int p) {
         issue_pair_half(stage, std::integral_constant<int, 0>{}, p);
@@ -274,8 +326,10 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
     };
     auto issue_single = [&](auto stage, int kt) {
         constexpr int SS = decltype(stage)::value;
-        scopy.issue(sbase + (uint32_t)min(kt, nk - 1) * sstep,
-                    lds0 + (uint32_t)(P::SINGLE_REGION + SS * P::SINGLE_BYTES), wave);
+        const int kc = min(kt, nk - 1);
+        const uint32_t dst = lds0 + (uint32_t)(P::SINGLE_REGION + SS * P::SINGLE_BYTES);
+        if constexpr (EDGE) ecopy.issue(rsrc_s, kc, K, (uint32_t)kc * ecopy.kstep(sld), dst, wave);
+        else scopy.issue(sbase + (uint32_t)kc * sstep, dst, wave);
     };
 
     // Fragment addresses.  Paired operand: per 64 KiB window (pair-stages 0-1,
@@ -367,12 +421,16 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
     zero_acc();
     prologue();
     asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    auto store_c = [&](float* Cdone, int r0, int c0) {
+        if constexpr (EDGE) store_acc16_lines_masked(Cdone, N, r0, c0, acc, lane, M, N);
+        else store_acc16_lines(Cdone, N, r0, c0, acc, lane);
+    };
     auto next_tile = [&]() {
         float* const Cdone = Ct;
         const int r0 = m0 + grp * P::TM, c0 = n0 + wn * P::TN;
         tile += (int)gridDim.x;
         if (tile >= total) {
-            store_acc16_lines(Cdone, N, r0, c0, acc, lane);
+            store_c(Cdone, r0, c0);
             return false;
         }
         // every wave's copies have landed (each waited for its own) before
@@ -380,7 +438,7 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
         asm volatile("s_barrier" ::: "memory");
         set_tile(tile);
         prologue();
-        store_acc16_lines(Cdone, N, r0, c0, acc, lane);
+        store_c(Cdone, r0, c0);
         zero_acc();
         // everything but the last 8 stores has landed: the whole prologue,
         // so k-tile 0 of the next tile (the next M phase waits for the rest)

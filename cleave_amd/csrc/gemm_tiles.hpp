@@ -379,6 +379,42 @@ __device__ __forceinline__ void store_acc16_lines(float* __restrict__ C, int64_t
                 p[4 * ldc] = __uint_as_float(s[1]);
             }
 }
+// The same stores, skipping elements at or past row M or column N (the
+// guarded-edge kernels' last tiles), without branches: buffer stores over C
+// from this wave's first row r0, sized to end at C's last element.  A row at
+// or past M then lies past the resource's range (its offset is at least
+// (M - r0) * ldc + c elements, and the range ends at (M - 1 - r0) * ldc + N,
+// ldc >= N), so the hardware drops it; a column at or past N, which would
+// land in the next row, gets an offset past the range (kOutOfRange).  The
+// column test takes one value per pair of blocks and lane; testing every
+// element's row and column instead kept 128 conditions live and spilled.
+// Needs the block's rows of C (16 * FM of ldc floats) under 2 GiB.
+template <int FM, int FN>
+__device__ __forceinline__ void store_acc16_lines_masked(float* __restrict__ C, int64_t ldc, int r0, int c0,
+                                                         const v4f (&acc)[FM][FN], int lane, int M, int N) {
+    static_assert(FN % 2 == 0, "blocks are paired along n");
+    if (r0 >= M) return;  // wave-uniform: the whole block lies past the last row
+    const int64_t left = ((int64_t)(M - 1 - r0) * ldc + N) * 4;  // bytes from row r0 to C's last element
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        C + (int64_t)r0 * ldc, (short)0, (int)(left < 0x7FFFFFF0 ? left : 0x7FFFFFF0), 0x00020000);
+    const int rl = 8 * (lane >> 5), cl = lane & 31;
+    const uint32_t ld4 = (uint32_t)ldc * 4u;
+#pragma unroll
+    for (int j = 0; j < FN; j += 2) {
+        const int c = c0 + j * 16 + cl;
+        const bool col_ok = c < N;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[i][j][v]),
+                                                                __float_as_uint(acc[i][j + 1][v]), false, false);
+                const uint32_t o0 = (uint32_t)(i * 16 + rl + v) * ld4 + (uint32_t)c * 4u;
+                __builtin_amdgcn_raw_buffer_store_b32(s[0], rsrc, (int)(col_ok ? o0 : kOutOfRange), 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b32(s[1], rsrc, (int)(col_ok ? o0 + 4u * ld4 : kOutOfRange), 0, 0);
+            }
+    }
+}
 
 }  // namespace tiles
 }  // namespace ch

@@ -689,6 +689,64 @@ def test_bf16_edge_tiles_batched_every_entry(hip, oracle):
         assert_gemm_close(got[i], ref, den, K, f"bf16 edge batched entry {i}")
 
 
+# At least half a round of 256 x 256 tiles with K past the short-K kernels:
+# the paired-copy kernel's guarded-edge form (A.B, A.B^T, A^T.B^T) reads the
+# ragged operands in place; A^T.B (no k-contiguous operand) stays on padded
+# copies.  Ragged M, N and K (K % 64 != 0: a pair of k-tiles half past K).
+_BF16_PAIRS_EDGE_CASES = [
+    (3000, 3000, 1000, 0, 0), (2600, 4100, 520, 0, 1), (3000, 2900, 1000, 1, 1), (300, 30000, 700, 0, 0),
+    (4000, 3000, 2056, 0, 0), (3000, 3000, 1000, 1, 0),
+]
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb", _BF16_PAIRS_EDGE_CASES)
+def test_bf16_pairs_edge_every_entry(hip, oracle, M, N, K, ta, tb):
+    A, B, Au, Bu = _operands(oracle, "bf16", M, N, K, ta, tb, seed=5 * M + N + 3 * K + 2 * ta + tb)
+    a, b = hip.from_numpy(A, "bf16"), hip.from_numpy(B, "bf16")
+    out = hip.from_numpy(np.full((M, N), np.nan, np.float32))  # every entry must be written
+    got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb), out=out).numpy()
+    again = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert got.shape == (M, N)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "repeat"
+    ref = oracle.matmul(Au, Bu, trans_a=bool(ta), trans_b=bool(tb), threads=16)
+    den = np.abs(Au.T if ta else Au).astype(np.float64) @ np.abs(Bu.T if tb else Bu).astype(np.float64)
+    assert_gemm_close(got, ref, den, K, f"bf16 pairs edge {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+def test_bf16_pairs_edge_batched_every_entry(hip, oracle):
+    bsz, M, N, K = 3, 1800, 2000, 600
+    A, B, Au, Bu = _operands(oracle, "bf16", M, N, K, 0, 1, seed=29, batch=bsz)
+    got = hip.matmul_batched(hip.from_numpy(A, "bf16"), hip.from_numpy(B, "bf16"), trans_b=True).numpy()
+    for i in range(bsz):
+        ref = oracle.matmul(Au[i], Bu[i], trans_b=True, threads=16)
+        den = np.abs(Au[i]).astype(np.float64) @ np.abs(Bu[i]).astype(np.float64).T
+        assert_gemm_close(got[i], ref, den, K, f"bf16 pairs edge batched entry {i}")
+
+
+def test_bf16_pairs_edge_infinities_and_nans(hip):
+    # the zeros read past the operands add 0 * 0 only: an Inf or NaN in the
+    # last row, column or k reaches exactly the entries it feeds
+    M, N, K = 3000, 3000, 1000
+    rng = np.random.default_rng(37)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    A[M - 1, K - 1] = np.inf
+    A[7, 3] = np.nan
+    B[K - 1, N - 1] = -np.inf
+    B[K - 2, 11] = np.inf
+    a = hip.to_bf16(hip.from_numpy(A))
+    b = hip.to_bf16(hip.from_numpy(B))
+    got = hip.matmul(a, b).numpy()
+    Ab = a.numpy().astype(np.uint32) << 16
+    Bb = b.numpy().astype(np.uint32) << 16
+    Af, Bf = Ab.view(np.float32).astype(np.float64), Bb.view(np.float32).astype(np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = Af @ Bf
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref))
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))
+
+
 def test_f32_edge_tiles_infinities_and_nans(hip, oracle):
     # The zeros the edge copies read outside the matrix add 0 * 0 = +0 only:
     # an Inf or NaN in the last row, column or k reaches exactly the entries
