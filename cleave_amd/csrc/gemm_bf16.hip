@@ -272,7 +272,18 @@ bool launch_edge(const uint16_t* a, const uint16_t* b, float* c, int M, int N, i
                  const Strides& s, int32_t* st) {
     const int64_t cus = ch::num_cus();
     const int64_t big = (int64_t)((M + 255) / 256) * ((N + 255) / 256) * batch;
-    if (big * 2 >= cus) return false;
+    if (big * 2 >= cus) {
+        // At least half a round of 256 x 256 tiles.  A short K runs on 128 x
+        // 128 tiles, two workgroups per CU, as the aligned short-K products;
+        // padding such a product's C and cropping it doubled its C traffic
+        // (10000^2 x 256: 283 against 139 us, 16000^2 x 248: 760 against 330).
+        // A longer K: the paired-copy kernel's EDGE form (launch_pairs_edge),
+        // or for A^T.B the padded copies (on these tiles 8000^3 A^T.B took
+        // 1190 against 883 us).
+        const bool short_k = K <= 256 || (big <= cus && K <= 512);
+        if (!short_k) return false;
+        return launch_tiled_edge<128, 128, 64, 2, 2, 2, 32, TA, TB>(a, b, c, M, N, K, batch, s, st);
+    }
     const int64_t tiles128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128) * batch;
     if (tiles128 <= cus) {
         if constexpr (!TA) {
