@@ -637,13 +637,17 @@ int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, in
         // tiles per CU its k-tiles are 32 deep (64 KiB of LDS, two workgroups
         // per CU), beyond that 16 (five): f32 1000^3 22.4 against 23.8 us,
         // 1000 x 2000 x 1000 37.7 against 38.3, 500^3 12.1 against 13.0;
-        // 1500^3 80.1 against 77.1, 2000^3 136.9 against 132.2.
+        // 1500^3 80.1 against 77.1, 2000^3 136.9 against 132.2.  With K up to
+        // 512 also beyond that: padding such a product's C and cropping it
+        // moved more than the math took (10000^2 x 256 604 against 470 us on
+        // padded copies, 3000^2 x 500 103 against 82, 5000 x 8000 x 300 A.B^T
+        // 269 against 229; 16000^2 x 128 A^T.B level).
         const int64_t tiles64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64) * batch;
         const int64_t cus = ch::num_cus();
         if (tiles64 <= 2 * cus &&
             launch_tiled_edge<64, 64, 32, 2, 2, 4, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
             return st;
-        if (tiles64 <= kEdgeTilesPerCu * cus &&
+        if ((tiles64 <= kEdgeTilesPerCu * cus || K <= 512) &&
             launch_tiled_edge<64, 64, 16, 2, 2, 4, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
             return st;
         const ch::PadPlan p = ch::pad_plan(M, N, K, batch, TA, TB, a, b, 4, ch::num_cus(), kPadModel);

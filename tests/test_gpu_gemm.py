@@ -624,6 +624,8 @@ _EDGE_CASES = [
     (999, 1001, 1000, 0, 1), (130, 97, 44, 0, 1), (65, 1000, 4, 0, 1),
     (1000, 1004, 999, 1, 0), (132, 100, 45, 1, 0), (1000, 1000, 1000, 1, 0),
     (1000, 999, 1004, 1, 1), (100, 131, 48, 1, 1), (1448, 1448, 1448, 1, 1),
+    # a short K over many tiles (past four per CU)
+    (5000, 5000, 252, 0, 0), (3000, 3000, 500, 1, 1), (6000, 4000, 128, 1, 0), (4100, 4000, 300, 0, 1),
 ]
 
 
