@@ -298,13 +298,26 @@ bool launch_edge(const uint16_t* a, const uint16_t* b, float* c, int M, int N, i
 // shapes in the range where their zero-padded copies would run the
 // paired-copy kernel (launch_fast): at least half a round of 256 x 256
 // tiles, a k-contiguous operand, and K past the short-K kernels' range (over
-// 256, and over 512 for a single round).  The copies and the crop move the
-// operands and C once more; here they are read in place.  False otherwise.
+// 256, and over 512 for a single round); A^T.B, which has no k-contiguous
+// operand, runs the single-ring ping-pong kernel's EDGE form there.  The
+// copies and the crop move the operands and C once more; here they are read
+// in place.  False otherwise.
 template <bool TA, bool TB>
 bool launch_pairs_edge(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
                        const Strides& s, int32_t* status) {
-    if constexpr (TA && !TB) {  // A^T B: no k-contiguous operand to pair
-        return false;
+    if constexpr (TA && !TB) {  // A^T B: no k-contiguous operand to pair; the single-ring kernel
+        using P = ch::Bf16PingPong<false, false>;
+        const int64_t cus = ch::num_cus();
+        const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
+        const int64_t big = (int64_t)tiles_m * tiles_n * batch;
+        if (big * 2 < cus || K <= 256 || (big <= cus && K <= 512)) return false;
+        if (!P::fits_edge(M, N, K, s.lda, s.ldb) || !bases_aligned(a, b, s)) return false;
+        if (big > 0x7FFFFFFF) return false;
+        ch::gemm_bf16_pingpong_kernel<false, false, false, 5, true><<<dim3((unsigned)big), P::THREADS, 0,
+                                                                      ch::stream()>>>(
+            a, b, c, M, N, K, s.lda, s.ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch);
+        *status = ch::check_hip(hipGetLastError(), "gemm_bf16_pingpong_kernel");
+        return true;
     } else {
         using P = ch::Bf16PingPongPairs<!TA, TB, true>;
         const int64_t cus = ch::num_cus();

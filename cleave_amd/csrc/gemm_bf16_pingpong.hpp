@@ -39,12 +39,29 @@ struct Bf16PingPong {
         const uint64_t b_span = (BKC ? (uint64_t)BN : (uint64_t)BK + 1) * (uint64_t)ldb * 2;
         return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
     }
+    // Bytes from an operand's base to the end of its last element, and the
+    // shapes the EDGE form takes (as Bf16PingPongPairs::fits_edge).
+    static __host__ __device__ int64_t a_bytes(int M, int K, int64_t lda) {
+        return AKC ? ((int64_t)(M - 1) * lda + K) * 2 : ((int64_t)(K - 1) * lda + M) * 2;
+    }
+    static __host__ __device__ int64_t b_bytes(int N, int K, int64_t ldb) {
+        return BKC ? ((int64_t)(N - 1) * ldb + K) * 2 : ((int64_t)(K - 1) * ldb + N) * 2;
+    }
+    static bool fits_edge(int M, int N, int K, int64_t lda, int64_t ldb) {
+        const bool chunks = (AKC ? K % 8 == 0 : M % 8 == 0) && (BKC ? K % 8 == 0 : N % 8 == 0) && lda % 8 == 0 &&
+                            ldb % 8 == 0;
+        return M >= 1 && N >= 1 && K >= 1 && chunks && a_bytes(M, K, lda) < (1ll << 31) &&
+               b_bytes(N, K, ldb) < (1ll << 31);
+    }
 };
 
 // OFF32: every k-tile's offset from an operand's base fits 32 bits (K times
 // the operand's k-step under 4 GiB), so the M phase forms the copy sources
 // with one 32-bit scalar multiply instead of a 64-bit one (0.5-1% at 8192^3).
-template <bool AKC, bool BKC, bool OFF32 = false, int STAGES_ = 5>
+// EDGE (any M, N and K, fits_edge): tiles_m and tiles_n rounded up; both
+// copies become EdgeCopy buffer loads that read zeros past the operands' rows
+// (columns) and past K, and the stores skip what lies past M or N.
+template <bool AKC, bool BKC, bool OFF32 = false, int STAGES_ = 5, bool EDGE = false>
 __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC,
@@ -70,14 +87,26 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
     copy_b.init(ldb, n0, wave, lane);
     const int64_t step_a = copy_a.kstep(lda), step_b = copy_b.kstep(ldb);
     const uint32_t lds0 = lds_addr(smem);
-    const int nk = K / BK;
+    const int nk = EDGE ? (K + BK - 1) / BK : K / BK;
     const uint32_t step_a32 = (uint32_t)step_a, step_b32 = (uint32_t)step_b;
     const char* a_src = reinterpret_cast<const char*>(A) + copy_a.base_offset(lda, m0);
     const char* b_src = reinterpret_cast<const char*>(B) + copy_b.base_offset(ldb, n0);
+    EdgeCopy<AKC, P::BM, BK, NW> edge_a;
+    EdgeCopy<BKC, P::BN, BK, NW> edge_b;
+    v4i rsrc_a{}, rsrc_b{};
+    if constexpr (EDGE) {
+        edge_a.init(lda, m0, M, wave, lane);
+        edge_b.init(ldb, n0, N, wave, lane);
+        rsrc_a = buffer_rsrc(A, (uint32_t)P::a_bytes(M, K, lda));
+        rsrc_b = buffer_rsrc(B, (uint32_t)P::b_bytes(N, K, ldb));
+    }
     auto issue = [&](int kt) {  // k-tile min(kt, nk-1) into stage kt % S
         const int src = min(kt, nk - 1);
         const uint32_t dst = lds0 + (uint32_t)((kt % S) * P::STAGE_BYTES);
-        if constexpr (OFF32) {
+        if constexpr (EDGE) {
+            edge_a.issue(rsrc_a, src, K, (uint32_t)src * edge_a.kstep(lda), dst, wave);
+            edge_b.issue(rsrc_b, src, K, (uint32_t)src * edge_b.kstep(ldb), dst + P::A_BYTES, wave);
+        } else if constexpr (OFF32) {
             copy_a.issue(a_src + (uint32_t)src * step_a32, dst, wave);
             copy_b.issue(b_src + (uint32_t)src * step_b32, dst + P::A_BYTES, wave);
         } else {
@@ -149,7 +178,8 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
     };
     pingpong_schedule<LPW, S>(nk, grp, issue, m_phase, c_phase);
 
-    store_acc16_lines(C, N, m0 + grp * P::TM, n0 + wn * P::TN, acc, lane);
+    if constexpr (EDGE) store_acc16_lines_masked(C, N, m0 + grp * P::TM, n0 + wn * P::TN, acc, lane, M, N);
+    else store_acc16_lines(C, N, m0 + grp * P::TM, n0 + wn * P::TN, acc, lane);
 }
 
 }  // namespace ch

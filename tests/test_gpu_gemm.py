@@ -693,11 +693,12 @@ def test_bf16_edge_tiles_batched_every_entry(hip, oracle):
 
 # At least half a round of 256 x 256 tiles with K past the short-K kernels:
 # the paired-copy kernel's guarded-edge form (A.B, A.B^T, A^T.B^T) reads the
-# ragged operands in place; A^T.B (no k-contiguous operand) stays on padded
-# copies.  Ragged M, N and K (K % 64 != 0: a pair of k-tiles half past K).
+# ragged operands in place, and for A^T.B (no k-contiguous operand) the
+# single-ring ping-pong kernel's.  Ragged M, N and K (K % 64 != 0: a pair of
+# k-tiles half past K).
 _BF16_PAIRS_EDGE_CASES = [
     (3000, 3000, 1000, 0, 0), (2600, 4100, 520, 0, 1), (3000, 2900, 1000, 1, 1), (300, 30000, 700, 0, 0),
-    (4000, 3000, 2056, 0, 0), (3000, 3000, 1000, 1, 0),
+    (4000, 3000, 2056, 0, 0), (3000, 3000, 1000, 1, 0), (3000, 5000, 2000, 1, 0), (2900, 4100, 1000, 1, 0),
     # a short K over as many tiles: 128 x 128 tiles with guarded edges
     (5000, 5000, 248, 0, 0), (3000, 3000, 504, 0, 1), (6000, 5000, 128, 1, 0), (4100, 4000, 200, 1, 1),
 ]
