@@ -699,6 +699,7 @@ def test_bf16_edge_tiles_batched_every_entry(hip, oracle):
 _BF16_PAIRS_EDGE_CASES = [
     (3000, 3000, 1000, 0, 0), (2600, 4100, 520, 0, 1), (3000, 2900, 1000, 1, 1), (300, 30000, 700, 0, 0),
     (4000, 3000, 2056, 0, 0), (3000, 3000, 1000, 1, 0), (3000, 5000, 2000, 1, 0), (2900, 4100, 1000, 1, 0),
+    (40000, 200, 1000, 0, 0), (40000, 200, 1000, 1, 0),  # one partial column of tiles
     # a short K over as many tiles: 128 x 128 tiles with guarded edges
     (5000, 5000, 248, 0, 0), (3000, 3000, 504, 0, 1), (6000, 5000, 128, 1, 0), (4100, 4000, 200, 1, 1),
 ]
