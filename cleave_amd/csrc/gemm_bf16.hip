@@ -5,8 +5,11 @@
 // gemm_bf16_pingpong.hpp; 128 x 128 x 64 tiles run the large-tile kernel of
 // gemm_bf16_tiled.hpp (LDS filled by global_load_lds,
 // transposing LDS reads for m/n-contiguous operands).  Large products of
-// other shapes run those kernels on zero-padded copies (gemm_pad.hpp); the
-// rest run the general kernel below, which guards every access.
+// other shapes run those kernels' guarded-edge forms on the operands in
+// place, or on aligned copies of operands whose rows are not whole 16-byte
+// chunks (gemm_pad.hpp); zero-padded copies of the whole product remain for
+// operands past the edge forms' 2 GiB; the rest run the general kernel
+// below, which guards every access.
 //
 // Same operator as gemm_f32.hip (linalg.matmul of stdlib/linalg/matrix.cleave:
 // 27-61) with bf16 operands; the reference is f32/f64 only, so this is an
@@ -201,6 +204,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const uint16_t* __restric
 // the K slices of one product (gemm_bf16's split below).
 struct Strides {
     int64_t lda, ldb, sA, sB, sC;
+    bool padded = false;  // aligned copies: every row holds its last chunk whole (ch::edge_chunks)
 };
 template <bool TA, bool TB>
 Strides packed(int M, int N, int K) {
@@ -252,7 +256,7 @@ template <int BM, int BN, int BK, int WM, int WN, int STAGES, int MI, bool TA, b
 bool launch_tiled_edge(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch,
                        const Strides& s, int32_t* status) {
     using P = ch::Bf16Tiled<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI>;
-    if (!P::fits_edge(M, N, K, s.lda, s.ldb) || !bases_aligned(a, b, s)) return false;
+    if (!P::fits_edge(M, N, K, s.lda, s.ldb, s.padded) || !bases_aligned(a, b, s)) return false;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
     dim3 grid((unsigned)(tiles_m * tiles_n * batch));
@@ -311,7 +315,7 @@ bool launch_pairs_edge(const uint16_t* a, const uint16_t* b, float* c, int M, in
         const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
         const int64_t big = (int64_t)tiles_m * tiles_n * batch;
         if (big * 2 < cus || K <= 256 || (big <= cus && K <= 512)) return false;
-        if (!P::fits_edge(M, N, K, s.lda, s.ldb) || !bases_aligned(a, b, s)) return false;
+        if (!P::fits_edge(M, N, K, s.lda, s.ldb, s.padded) || !bases_aligned(a, b, s)) return false;
         if (big > 0x7FFFFFFF) return false;
         ch::gemm_bf16_pingpong_kernel<false, false, false, 5, true><<<dim3((unsigned)big), P::THREADS, 0,
                                                                       ch::stream()>>>(
@@ -324,7 +328,7 @@ bool launch_pairs_edge(const uint16_t* a, const uint16_t* b, float* c, int M, in
         const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
         const int64_t big = (int64_t)tiles_m * tiles_n * batch;
         if (big * 2 < cus || K <= 256 || (big <= cus && K <= 512)) return false;
-        if (!P::fits_edge(M, N, K, s.lda, s.ldb) || !bases_aligned(a, b, s)) return false;
+        if (!P::fits_edge(M, N, K, s.lda, s.ldb, s.padded) || !bases_aligned(a, b, s)) return false;
         if (big > 0x7FFFFFFF) return false;
         const int total = (int)big;
         const int resident = cus >= 8 ? (int)(cus / 8 * 8) : (cus > 0 ? (int)cus : 1);
@@ -505,6 +509,22 @@ int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N,
     if (2.0 * M * N * K * batch >= kPadMinFlops) {
         if (launch_edge<TA, TB>(a, b, c, M, N, K, batch, packed<TA, TB>(M, N, K), &st)) return st;
         if (launch_pairs_edge<TA, TB>(a, b, c, M, N, K, batch, packed<TA, TB>(M, N, K), &st)) return st;
+        // Rows that are not whole 16-byte chunks (an extent that is not a
+        // multiple of 8, a misaligned view): the same guarded-edge kernels on
+        // aligned copies of those operands, C in place (ch::run_aligned).
+        // Against the padded route below, which also pads C and crops it
+        // (same box, two runs): 12300^2 x 200 239 against 472 us, 5000 x
+        // 5004 x 200 37 against 64, 64 x 700 x 900 x 300 94 against 161,
+        // 2048 x 1100 x 256 10.2 against 16.4, 3001 x 3000 x 1000 A^T.B 37
+        // against 42; 1500^3 level (28.5 against 28.9).
+        const ch::AlignPlan ap = ch::align_plan(M, N, K, batch, TA, TB, a, b, 2);
+        auto edge = [&](const uint16_t* pa, const uint16_t* pb, int64_t lda, int64_t ldb, int64_t sA, int64_t sB,
+                        int Kq, int32_t* s) {
+            const Strides str{lda, ldb, sA, sB, (int64_t)M * N, true};
+            return launch_edge<TA, TB>(pa, pb, c, M, N, Kq, batch, str, s) ||
+                   launch_pairs_edge<TA, TB>(pa, pb, c, M, N, Kq, batch, str, s);
+        };
+        if (ch::run_aligned(ap, a, b, M, N, K, batch, TA, TB, edge, &st)) return st;
         const ch::PadPlan p = ch::pad_plan(M, N, K, batch, TA, TB, a, b, 2, ch::num_cus(), kPadModel);
         auto gemm = [batch](const uint16_t* pa, const uint16_t* pb, float* pc, int Mp, int Np, int Kp) {
             int32_t s = CLEAVE_HIP_OK;

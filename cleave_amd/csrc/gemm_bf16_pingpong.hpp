@@ -39,17 +39,17 @@ struct Bf16PingPong {
         const uint64_t b_span = (BKC ? (uint64_t)BN : (uint64_t)BK + 1) * (uint64_t)ldb * 2;
         return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
     }
-    // Bytes from an operand's base to the end of its last element, and the
-    // shapes the EDGE form takes (as Bf16PingPongPairs::fits_edge).
+    // Bytes from an operand's base to the end of its last chunk
+    // (ch::edge_bytes), and the shapes the EDGE form takes (as
+    // Bf16PingPongPairs::fits_edge).
     static __host__ __device__ int64_t a_bytes(int M, int K, int64_t lda) {
-        return AKC ? ((int64_t)(M - 1) * lda + K) * 2 : ((int64_t)(K - 1) * lda + M) * 2;
+        return edge_bytes<8, 2>(AKC, M, K, lda);
     }
     static __host__ __device__ int64_t b_bytes(int N, int K, int64_t ldb) {
-        return BKC ? ((int64_t)(N - 1) * ldb + K) * 2 : ((int64_t)(K - 1) * ldb + N) * 2;
+        return edge_bytes<8, 2>(BKC, N, K, ldb);
     }
-    static bool fits_edge(int M, int N, int K, int64_t lda, int64_t ldb) {
-        const bool chunks = (AKC ? K % 8 == 0 : M % 8 == 0) && (BKC ? K % 8 == 0 : N % 8 == 0) && lda % 8 == 0 &&
-                            ldb % 8 == 0;
+    static bool fits_edge(int M, int N, int K, int64_t lda, int64_t ldb, bool padded = false) {
+        const bool chunks = edge_chunks<8>(AKC, M, K, lda, padded) && edge_chunks<8>(BKC, N, K, ldb, padded);
         return M >= 1 && N >= 1 && K >= 1 && chunks && a_bytes(M, K, lda) < (1ll << 31) &&
                b_bytes(N, K, ldb) < (1ll << 31);
     }
@@ -234,19 +234,19 @@ struct Bf16PingPongPairs {
         const uint64_t b_span = (uint64_t)(BKC ? BN : K + 1) * (uint64_t)ldb * 2;
         return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
     }
-    // Bytes from an operand's base to the end of its last element.
+    // Bytes from an operand's base to the end of its last chunk (ch::edge_bytes).
     static __host__ __device__ int64_t a_bytes(int M, int K, int64_t lda) {
-        return AKC ? ((int64_t)(M - 1) * lda + K) * 2 : ((int64_t)(K - 1) * lda + M) * 2;
+        return edge_bytes<8, 2>(AKC, M, K, lda);
     }
     static __host__ __device__ int64_t b_bytes(int N, int K, int64_t ldb) {
-        return BKC ? ((int64_t)(N - 1) * ldb + K) * 2 : ((int64_t)(K - 1) * ldb + N) * 2;
+        return edge_bytes<8, 2>(BKC, N, K, ldb);
     }
     // Shapes the EDGE form takes (any M, N, K >= 1): whole 16-byte chunks (8
-    // elements) along each operand's contiguous extent and pitch, and
-    // operands under 2 GiB, so that a masked offset stays out of range.
-    static bool fits_edge(int M, int N, int K, int64_t lda, int64_t ldb) {
-        const bool chunks = (AKC ? K % 8 == 0 : M % 8 == 0) && (BKC ? K % 8 == 0 : N % 8 == 0) && lda % 8 == 0 &&
-                            ldb % 8 == 0;
+    // elements) along each operand's pitch and along K, an m/n extent in
+    // whole chunks unless `padded` (ch::edge_chunks), and operands under
+    // 2 GiB, so that a masked offset stays out of range.
+    static bool fits_edge(int M, int N, int K, int64_t lda, int64_t ldb, bool padded = false) {
+        const bool chunks = edge_chunks<8>(AKC, M, K, lda, padded) && edge_chunks<8>(BKC, N, K, ldb, padded);
         return M >= 1 && N >= 1 && K >= 1 && chunks && a_bytes(M, K, lda) < (1ll << 31) &&
                b_bytes(N, K, ldb) < (1ll << 31);
     }

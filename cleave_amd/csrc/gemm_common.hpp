@@ -60,6 +60,33 @@ __device__ __forceinline__ void block_coords(int bid, int tiles_m, int tiles_n, 
     tn = in_group / gsize;
 }
 
+// The guarded-edge kernels copy 16-byte chunks (Q elements) along each
+// operand's contiguous extent, masking a chunk that starts past it.  A chunk
+// that starts inside an m/n-contiguous row and runs past its extent reads
+// columns that feed only entries of C outside the product, so that extent
+// may be ragged when the memory the chunk reads exists: `padded` says every
+// row holds its last chunk whole (an aligned copy, pitch at least the extent
+// rounded up to Q).  A k-contiguous operand's extent is K and stays whole
+// chunks: a chunk past K would multiply the other operand's zero k-rows by
+// whatever it read, Inf and NaN included.
+template <int Q>
+__host__ __device__ constexpr int64_t chunk_up(int64_t x) {
+    return (x + Q - 1) / Q * Q;
+}
+template <int Q>
+inline bool edge_chunks(bool kc, int extent, int K, int64_t ld, bool padded) {
+    if (ld % Q) return false;
+    if (kc) return K % Q == 0;
+    return extent % Q == 0 || (padded && ld >= chunk_up<Q>(extent));
+}
+// Bytes from an operand's base to the end of its last chunk: k-contiguous,
+// `extent` rows of K; m/n-contiguous, K rows of `extent` (rounded up to a
+// chunk).  The range of the operand's buffer resource.
+template <int Q, int ESZ>
+__host__ __device__ inline int64_t edge_bytes(bool kc, int extent, int K, int64_t ld) {
+    return kc ? ((int64_t)(extent - 1) * ld + K) * ESZ : ((int64_t)(K - 1) * ld + chunk_up<Q>(extent)) * ESZ;
+}
+
 // Operands of the fused epilogues and operand transforms of the two GEMMs
 // of the MLP step (mlp.hip); a plain GEMM passes {}.  The f32 kernels
 // document what each MODE does with them.

@@ -43,18 +43,18 @@ struct F32Tiled {
         const uint64_t b_span = (BKC ? (uint64_t)BN : (uint64_t)BK + 1) * (uint64_t)ldb * 4;
         return dims && a_span < (1ull << 32) && b_span < (1ull << 32);
     }
-    // Bytes from an operand's base to the end of its last element.
+    // Bytes from an operand's base to the end of its last chunk (ch::edge_bytes).
     static __host__ __device__ int64_t a_bytes(int M, int K, int64_t lda) {
-        return AKC ? ((int64_t)(M - 1) * lda + K) * 4 : ((int64_t)(K - 1) * lda + M) * 4;
+        return edge_bytes<4, 4>(AKC, M, K, lda);
     }
     static __host__ __device__ int64_t b_bytes(int N, int K, int64_t ldb) {
-        return BKC ? ((int64_t)(N - 1) * ldb + K) * 4 : ((int64_t)(K - 1) * ldb + N) * 4;
+        return edge_bytes<4, 4>(BKC, N, K, ldb);
     }
-    // Shapes the EDGE form takes: whole 16-byte chunks along each operand's
-    // contiguous extent and pitch, and operands under 2 GiB.
-    static bool fits_edge(int M, int N, int K, int64_t lda, int64_t ldb) {
-        const bool chunks = (AKC ? K % 4 == 0 : M % 4 == 0) && (BKC ? K % 4 == 0 : N % 4 == 0) && lda % 4 == 0 &&
-                            ldb % 4 == 0;
+    // Shapes the EDGE form takes: whole 16-byte chunks (4 elements) along
+    // each operand's pitch and along K, an m/n extent in whole chunks unless
+    // `padded` (ch::edge_chunks), and operands under 2 GiB.
+    static bool fits_edge(int M, int N, int K, int64_t lda, int64_t ldb, bool padded = false) {
+        const bool chunks = edge_chunks<4>(AKC, M, K, lda, padded) && edge_chunks<4>(BKC, N, K, ldb, padded);
         return M >= 1 && N >= 1 && K >= 1 && chunks && a_bytes(M, K, lda) < (1ll << 31) &&
                b_bytes(N, K, ldb) < (1ll << 31);
     }

@@ -214,4 +214,89 @@ bool run_padded(const PadPlan& p, const T* a, const T* b, float* c, int batch, b
     return true;
 }
 
+// Ragged products whose only obstacle to the guarded-edge kernels is
+// alignment: an operand row that is not a whole number of 16-byte chunks (a
+// contiguous extent not a multiple of Q = 16 / element size) or a base that
+// is not 16-byte aligned.  Each such operand is copied, in the caller's
+// layout, with its contiguous extent rounded up to a multiple of 8 (zeros
+// past it); when K is not a multiple of Q, K is rounded up to Kq in both
+// operands (zero k-columns or k-rows), so that no 16-byte chunk of a
+// k-contiguous operand straddles the kernels' K.  The guarded-edge kernels
+// then run on the copies with C written in place: C is neither padded nor
+// cropped, and only the operands move once more.  The zeros change no entry,
+// as for the padded copies above.
+struct AlignPlan {
+    bool ok;            // an operand needs its copy, and the copies fit the edge kernels
+    int Kq;             // K rounded up to Q
+    bool copy_a, copy_b;
+    int64_t lda, ldb;   // pitches of the operands the kernels read, in elements
+    int64_t sA, sB;     // their per-product strides
+    int64_t rows_a, rows_b;  // rows of each copy (its stored layout)
+    size_t bytes_a, bytes_b;  // scratch bytes of each copy (0: used in place)
+};
+
+inline AlignPlan align_plan(int M, int N, int K, int batch, bool ta, bool tb, const void* a, const void* b,
+                            int esz) {
+    AlignPlan p{};
+    const int q = 16 / esz;
+    const int64_t kq = pad_up(K, q);
+    const int64_t pa = ta ? M : K, pb = tb ? K : N;  // stored pitches
+    const bool a_al = ((uintptr_t)a & 15) == 0 && pa % q == 0;
+    const bool b_al = ((uintptr_t)b & 15) == 0 && pb % q == 0;
+    p.copy_a = !a_al || kq != K;
+    p.copy_b = !b_al || kq != K;
+    if ((!p.copy_a && !p.copy_b) || kq > INT32_MAX) return p;
+    p.Kq = (int)kq;
+    p.rows_a = ta ? kq : M;
+    p.rows_b = tb ? N : kq;
+    p.lda = p.copy_a ? pad_up((int)(ta ? M : kq), 8) : pa;
+    p.ldb = p.copy_b ? pad_up((int)(tb ? kq : N), 8) : pb;
+    p.sA = p.rows_a * p.lda;
+    p.sB = p.rows_b * p.ldb;
+    // the edge kernels address each product's operand with 32-bit byte offsets
+    p.ok = p.sA * esz < (1ll << 31) && p.sB * esz < (1ll << 31);
+    auto r256 = [](size_t x) { return (x + 255) / 256 * 256; };
+    p.bytes_a = p.copy_a ? r256((size_t)batch * p.sA * esz) : 0;
+    p.bytes_b = p.copy_b ? r256((size_t)batch * p.sB * esz) : 0;
+    return p;
+}
+
+// Copies the operands `p` names and runs `gemm(pa, pb, lda, ldb, sA, sB, Kq,
+// status)`, which launches a guarded-edge kernel on M x N x Kq with C in
+// place and returns whether it did.  Returns false when nothing was launched
+// for the product (plan not ok, no scratch, or `gemm` declined after the
+// copies: the caller then takes another route on the original operands).
+template <typename T, typename Gemm>
+bool run_aligned(const AlignPlan& p, const T* a, const T* b, int M, int N, int K, int batch, bool ta, bool tb,
+                 Gemm gemm, int32_t* status) {
+    constexpr int kSlot = 7;
+    if (!p.ok) return false;
+    char* base = (char*)scratch_try(kSlot, p.bytes_a + p.bytes_b);
+    if (!base) return false;
+    const T* pa = a;
+    const T* pb = b;
+    PadCopy<T> ja{}, jb{};
+    if (p.copy_a) {
+        T* d = (T*)base;
+        const int rows = ta ? K : M, cols = ta ? M : K;
+        const bool vec = ((uintptr_t)a & 15) == 0 && ((int64_t)cols * sizeof(T)) % 16 == 0;
+        ja = PadCopy<T>{a, d, rows, cols, (int)p.rows_a, (int)p.lda, (int64_t)batch * p.rows_a, vec};
+        pa = d;
+    }
+    if (p.copy_b) {
+        T* d = (T*)(base + p.bytes_a);
+        const int rows = tb ? N : K, cols = tb ? K : N;
+        const bool vec = ((uintptr_t)b & 15) == 0 && ((int64_t)cols * sizeof(T)) % 16 == 0;
+        jb = PadCopy<T>{b, d, rows, cols, (int)p.rows_b, (int)p.ldb, (int64_t)batch * p.rows_b, vec};
+        pb = d;
+    }
+    pad_copy_kernel<T><<<pad_grid(ja.total_rows + jb.total_rows, num_cus()), 256, 0, stream()>>>(ja, jb);
+    int32_t st = check_hip(hipGetLastError(), "pad_copy_kernel");
+    if (st != CLEAVE_HIP_OK) {
+        *status = st;
+        return true;
+    }
+    return gemm(pa, pb, p.lda, p.ldb, p.sA, p.sB, p.Kq, status);
+}
+
 }  // namespace ch

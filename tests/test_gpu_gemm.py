@@ -513,14 +513,13 @@ def _operands(oracle, dtype, M, N, K, ta, tb, seed, batch=None):
     return A32, B32, A32, B32
 
 
-# Ragged shapes large enough for the zero-padded route (the aligned kernels
-# on padded copies of the operands, the valid corner of C copied out): every
-# dimension ragged, K alone ragged (C written in place), M alone ragged (B
-# used in place), N alone ragged (A used in place).  In f32, the layouts whose
-# contiguous extents are multiples of 4 run the 64 x 64 kernel with guarded
-# edges instead, and in bf16 those with extents in multiples of 8 and fewer
-# 256 x 256 tiles than half a round run 128 x 128 (64 x 128) tiles with
-# guarded edges (below); the others the padded route.
+# Ragged shapes past the general kernel: every dimension ragged, K alone
+# ragged, M alone ragged, N alone ragged.  They run the guarded-edge kernels
+# (below) on the operands in place when each operand's rows are whole 16-byte
+# chunks, else on aligned copies of the operands that are not (C in place
+# either way); the zero-padded route (padded copies of the operands, the
+# valid corner of C copied out) takes f32 with K past 512 over more than
+# four 64 x 64 tiles per CU.
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [(1000, 1000, 1000), (640, 2048, 520), (1031, 768, 512), (2048, 1100, 256)])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
@@ -727,6 +726,47 @@ def test_bf16_pairs_edge_batched_every_entry(hip, oracle):
         ref = oracle.matmul(Au[i], Bu[i], trans_b=True, threads=16)
         den = np.abs(Au[i]).astype(np.float64) @ np.abs(Bu[i]).astype(np.float64).T
         assert_gemm_close(got[i], ref, den, K, f"bf16 pairs edge batched entry {i}")
+
+
+# Rows that are not whole 16-byte chunks (an extent not a multiple of 8 in
+# bf16 or 4 in f32): the operands that need it are copied with their
+# contiguous extent rounded up (and K rounded up in both when K itself is
+# ragged), and the guarded-edge kernels run on the copies with C written in
+# place.  One case per route: fewer 256 x 256 tiles than half a round, a
+# short K over many tiles, the paired-copy kernel (K ragged to 8 too), A^T.B's
+# single-ring kernel; f32's 64 x 64 kernels.  C pre-filled with NaN.
+_ALIGN_CASES = [
+    ("bf16", 1500, 1500, 1500, 0, 0), ("bf16", 1500, 1500, 1500, 0, 1), ("bf16", 1500, 1500, 1500, 1, 0),
+    ("bf16", 1500, 1500, 1500, 1, 1), ("bf16", 2048, 1100, 256, 0, 0), ("bf16", 5000, 5004, 200, 0, 0),
+    ("bf16", 5004, 5000, 202, 1, 1), ("bf16", 3000, 3004, 1000, 0, 0), ("bf16", 3000, 3000, 1002, 0, 1),
+    ("bf16", 3001, 3000, 1000, 1, 0), ("bf16", 3000, 2999, 998, 1, 1),
+    ("f32", 1001, 1001, 1001, 0, 0), ("f32", 1001, 1001, 1001, 0, 1), ("f32", 1001, 1001, 1001, 1, 0),
+    ("f32", 1001, 1001, 1001, 1, 1), ("f32", 3000, 3001, 501, 0, 0), ("f32", 2999, 3000, 250, 1, 1),
+]
+
+
+@pytest.mark.parametrize("dtype,M,N,K,ta,tb", _ALIGN_CASES)
+def test_aligned_copies_every_entry(hip, oracle, dtype, M, N, K, ta, tb):
+    A, B, Au, Bu = _operands(oracle, dtype, M, N, K, ta, tb, seed=7 * M + 3 * N + K + 2 * ta + tb)
+    a, b = hip.from_numpy(A, dtype), hip.from_numpy(B, dtype)
+    out = hip.from_numpy(np.full((M, N), np.nan, np.float32))  # every entry must be written
+    got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb), out=out).numpy()
+    again = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "repeat"
+    ref = oracle.matmul(Au, Bu, trans_a=bool(ta), trans_b=bool(tb), threads=16)
+    den = np.abs(Au.T if ta else Au).astype(np.float64) @ np.abs(Bu.T if tb else Bu).astype(np.float64)
+    assert_gemm_close(got, ref, den, K, f"aligned copies {dtype} {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_aligned_copies_batched_every_entry(hip, oracle, dtype):
+    bsz, M, N, K = 3, 701, 899, 301
+    A, B, Au, Bu = _operands(oracle, dtype, M, N, K, 1, 0, seed=43, batch=bsz)
+    got = hip.matmul_batched(hip.from_numpy(A, dtype), hip.from_numpy(B, dtype), trans_a=True).numpy()
+    for i in range(bsz):
+        ref = oracle.matmul(Au[i], Bu[i], trans_a=True, threads=16)
+        den = np.abs(Au[i].T).astype(np.float64) @ np.abs(Bu[i]).astype(np.float64)
+        assert_gemm_close(got[i], ref, den, K, f"aligned copies batched {dtype} entry {i}")
 
 
 def test_bf16_pairs_edge_infinities_and_nans(hip):

@@ -94,13 +94,16 @@ def test_index_past_2pow31(hip, oracle):
     assert hip.index(dt, (shape[0] - 1, 7)) == 2.5
 
 
-@pytest.mark.parametrize("dtype,M,K,tb", [("f32", 1 << 20, 1024, 0), ("f32", 1 << 20, 1024, 1),
-                                         ("bf16", 1 << 21, 1024, 0), ("bf16", 1 << 21, 1024, 1)])
-def test_gemm_operand_past_4gib(hip, oracle, dtype, M, K, tb):
+@pytest.mark.parametrize("dtype,M,K,tb,N", [("f32", 1 << 20, 1024, 0, 256), ("f32", 1 << 20, 1024, 1, 256),
+                                           ("bf16", 1 << 21, 1024, 0, 256), ("bf16", 1 << 21, 1024, 1, 256),
+                                           ("bf16", (1 << 21) + 5, 1024, 0, 260)])
+def test_gemm_operand_past_4gib(hip, oracle, dtype, M, K, tb, N):
     # A (M x K) spans exactly 4 GiB, one byte past what a 32-bit offset from
     # the operand's base reaches; with tb, B (N x K) is k-contiguous too.
     # The product must still be the reference loop's, within the GEMM bound.
-    N = 256
+    # The ragged case is past the guarded-edge kernels' 2 GiB per operand and
+    # B's rows are not whole 16-byte chunks: zero-padded copies of both
+    # operands, the valid corner of C copied out.
     print(f"{dtype} gemm {M}x{N}x{K} tb={tb}: A spans {M * K * (4 if dtype == 'f32' else 2) / 2**30:.1f} GiB",
           flush=True)
     a32 = hip.fill_normal(hip.empty((M, K)), seed=31)
