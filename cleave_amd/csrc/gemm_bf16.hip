@@ -32,7 +32,7 @@ int32_t matmul_vector_bf16(const uint16_t* a, const uint16_t* b, float* c, int M
                            int tb);
 int32_t matmul_skinny_bf16(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int batch, int ta,
                            int tb);
-int32_t sum_slices_f32(const float* part, float* c, int64_t n, int S);
+int32_t sum_slices_f32(const float* part, float* c, int64_t n, int S, int64_t stride);
 }
 
 namespace {
@@ -469,22 +469,42 @@ int split_count(int M, int N, int K) {
     return S;
 }
 
+// Whether K slices of depth kk with these strides go to an aligned kernel
+// (128 x 128 tiles and whole k-tiles) or a guarded-edge one, not to the
+// general kernel: on that kernel 1000^2 x 65536 ran as two slices in
+// 2.36 ms, against 0.20 ms for 1024^2 x 65536 on the tiled kernel.
+template <bool TA, bool TB>
+bool slices_fit(const uint16_t* a, const uint16_t* b, int M, int N, int kk, const Strides& s) {
+    if (!bases_aligned(a, b, s)) return false;
+    if (M % 128 == 0 && N % 128 == 0 && kk % 64 == 0 && s.lda % 8 == 0 && s.ldb % 8 == 0) return true;
+    return ch::edge_chunks<8>(!TA, M, kk, s.lda, s.padded) && ch::edge_chunks<8>(TB, N, kk, s.ldb, s.padded) &&
+           ch::edge_bytes<8, 2>(!TA, M, kk, s.lda) < (1ll << 31) && ch::edge_bytes<8, 2>(TB, N, kk, s.ldb) < (1ll << 31);
+}
+
 // One product (C of pitch N; A and B of pitches lda and ldb, so that a band
 // of a larger product's rows keeps its operand pitches) as split_count's K
 // slices into a scratch buffer, added in order (ch::sum_slices_f32,
-// deterministic); false when not split.
+// deterministic): the aligned kernels, or on a ragged M or N the
+// guarded-edge ones (`padded`: the operands are aligned copies,
+// ch::edge_chunks).  Each slice's C starts on a 16-byte boundary of the
+// buffer.  False when not split.
 template <bool TA, bool TB>
 bool try_k_split(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb,
-                 int32_t* st) {
-    const int64_t n = (int64_t)M * N;
-    if (((uintptr_t)c & 15) != 0 || n % 4 != 0) return false;
+                 bool padded, int32_t* st) {
+    if (((uintptr_t)c & 15) != 0) return false;
     const int S = split_count(M, N, K);
-    float* part = S > 1 ? (float*)ch::scratch_try(10, sizeof(float) * (size_t)(S * n)) : nullptr;
-    if (!part) return false;
+    if (S <= 1) return false;
     const int kk = K / S;
-    const Strides sl{lda, ldb, TA ? (int64_t)kk * lda : kk, TB ? kk : (int64_t)kk * ldb, n};
-    if (!launch_fast<TA, TB>(a, b, part, M, N, kk, S, sl, st)) *st = launch<TA, TB>(a, b, part, M, N, kk, S, sl);
-    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, n, S);
+    const int64_t n = (int64_t)M * N, n4 = (n + 3) / 4 * 4;
+    const Strides sl{lda, ldb, TA ? (int64_t)kk * lda : kk, TB ? kk : (int64_t)kk * ldb, n4, padded};
+    if (!slices_fit<TA, TB>(a, b, M, N, kk, sl)) return false;
+    float* part = (float*)ch::scratch_try(10, sizeof(float) * (size_t)(S * n4));
+    if (!part) return false;
+    if (!launch_fast<TA, TB>(a, b, part, M, N, kk, S, sl, st) &&
+        !launch_edge<TA, TB>(a, b, part, M, N, kk, S, sl, st) &&
+        !launch_pairs_edge<TA, TB>(a, b, part, M, N, kk, S, sl, st))
+        *st = launch<TA, TB>(a, b, part, M, N, kk, S, sl);
+    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, n, S, n4);
     return true;
 }
 
@@ -507,6 +527,26 @@ int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N,
     if ((M <= 32 || N <= 32) && 2.0 * M * N * K * batch >= (1u << 20))
         return ch::matmul_skinny_bf16(a, b, c, M, N, K, batch, TA, TB);
     if (2.0 * M * N * K * batch >= kPadMinFlops) {
+        // The guarded-edge kernels on aligned copies (ch::run_aligned): K
+        // slices for one product with few tiles and a long K, else one launch.
+        auto edge = [&](const uint16_t* pa, const uint16_t* pb, int64_t lda, int64_t ldb, int64_t sA, int64_t sB,
+                        int Kq, int32_t* s) {
+            if (batch == 1 && M > 32 && N > 32 && try_k_split<TA, TB>(pa, pb, c, M, N, Kq, lda, ldb, true, s))
+                return true;
+            const Strides str{lda, ldb, sA, sB, (int64_t)M * N, true};
+            return launch_edge<TA, TB>(pa, pb, c, M, N, Kq, batch, str, s) ||
+                   launch_pairs_edge<TA, TB>(pa, pb, c, M, N, Kq, batch, str, s);
+        };
+        // Few tiles and a long K that the slices do not divide (split_count
+        // wants K % (128 S) == 0): K rounded up to a multiple of 2048 in
+        // aligned copies of both operands, then the slices.  In one launch,
+        // 704 x 896 x 30000 took 216 us; as padded copies and four slices
+        // (the padded route below, which pads C too), 101.
+        if (batch == 1 && M > 32 && N > 32 && K >= 16384 && K % 2048 != 0 &&
+            split_count(M, N, (int)ch::pad_up(K, 2048)) > 1) {
+            const ch::AlignPlan kp = ch::align_plan(M, N, K, batch, TA, TB, a, b, 2, 2048);
+            if (ch::run_aligned(kp, a, b, M, N, K, batch, TA, TB, edge, &st)) return st;
+        }
         if (launch_edge<TA, TB>(a, b, c, M, N, K, batch, packed<TA, TB>(M, N, K), &st)) return st;
         if (launch_pairs_edge<TA, TB>(a, b, c, M, N, K, batch, packed<TA, TB>(M, N, K), &st)) return st;
         // Rows that are not whole 16-byte chunks (an extent that is not a
@@ -518,17 +558,12 @@ int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N,
         // 2048 x 1100 x 256 10.2 against 16.4, 3001 x 3000 x 1000 A^T.B 37
         // against 42; 1500^3 level (28.5 against 28.9).
         const ch::AlignPlan ap = ch::align_plan(M, N, K, batch, TA, TB, a, b, 2);
-        auto edge = [&](const uint16_t* pa, const uint16_t* pb, int64_t lda, int64_t ldb, int64_t sA, int64_t sB,
-                        int Kq, int32_t* s) {
-            const Strides str{lda, ldb, sA, sB, (int64_t)M * N, true};
-            return launch_edge<TA, TB>(pa, pb, c, M, N, Kq, batch, str, s) ||
-                   launch_pairs_edge<TA, TB>(pa, pb, c, M, N, Kq, batch, str, s);
-        };
         if (ch::run_aligned(ap, a, b, M, N, K, batch, TA, TB, edge, &st)) return st;
         const ch::PadPlan p = ch::pad_plan(M, N, K, batch, TA, TB, a, b, 2, ch::num_cus(), kPadModel);
         auto gemm = [batch](const uint16_t* pa, const uint16_t* pb, float* pc, int Mp, int Np, int Kp) {
             int32_t s = CLEAVE_HIP_OK;
-            if (batch == 1 && try_k_split<TA, TB>(pa, pb, pc, Mp, Np, Kp, TA ? Mp : Kp, TB ? Kp : Np, &s)) return s;
+            if (batch == 1 && try_k_split<TA, TB>(pa, pb, pc, Mp, Np, Kp, TA ? Mp : Kp, TB ? Kp : Np, false, &s))
+                return s;
             if (launch_fast<TA, TB>(pa, pb, pc, Mp, Np, Kp, batch, packed<TA, TB>(Mp, Np, Kp), &s)) return s;
             return launch<TA, TB>(pa, pb, pc, Mp, Np, Kp, batch, packed<TA, TB>(Mp, Np, Kp));
         };
@@ -585,7 +620,7 @@ template <bool TA, bool TB>
 int32_t product(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb,
                 int depth) {
     int32_t st = CLEAVE_HIP_OK;
-    if (M > 32 && N > 32 && try_k_split<TA, TB>(a, b, c, M, N, K, lda, ldb, &st)) return st;
+    if (M > 32 && N > 32 && try_k_split<TA, TB>(a, b, c, M, N, K, lda, ldb, false, &st)) return st;
     if (try_round_split<TA, TB>(a, b, c, M, N, K, lda, ldb, depth, &st)) return st;
     if (lda == (TA ? M : K) && ldb == (TB ? K : N)) return launch_any<TA, TB>(a, b, c, M, N, K, 1);
     // a band of rows of a larger product (aligned: 256-row bands)
@@ -619,7 +654,7 @@ bool try_batched_k_slices(const uint16_t* a, const uint16_t* b, float* c, int M,
     if (!launch_tiled<128, 128, 64, 2, 2, 3, 32, TA, TB>(a, b, part, M, N, K / S, batch * S, packed<TA, TB>(M, N, K),
                                                          st, S))
         return false;
-    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, n, S);
+    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, n, S, n);
     return true;
 }
 

@@ -313,19 +313,27 @@ bool launch_pingpong(const float* a, const float* b, float* c, int M, int N, int
 // c[i] = part[0][i] + part[1][i] + ... + part[S-1][i], in slice order; n is
 // a multiple of 4 and every slice 16-byte aligned.
 __global__ __launch_bounds__(256) void sum_slices_kernel(const float* __restrict__ part, float* __restrict__ c,
-                                                         int64_t n, int S) {
-    for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < n; i += (int64_t)gridDim.x * 256 * 4) {
+                                                         int64_t n, int S, int64_t stride) {
+    const int64_t n4 = n / 4 * 4;
+    for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < n4; i += (int64_t)gridDim.x * 256 * 4) {
         f4 acc = *reinterpret_cast<const f4*>(part + i);
         int s = 1;
         for (; s + 8 <= S; s += 8) {  // eight loads in flight, added in order
             f4 v[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const f4*>(part + (int64_t)(s + u) * n + i);
+            for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const f4*>(part + (int64_t)(s + u) * stride + i);
 #pragma unroll
             for (int u = 0; u < 8; ++u) acc = acc + v[u];
         }
-        for (; s < S; ++s) acc = acc + *reinterpret_cast<const f4*>(part + (int64_t)s * n + i);
+        for (; s < S; ++s) acc = acc + *reinterpret_cast<const f4*>(part + (int64_t)s * stride + i);
         *reinterpret_cast<f4*>(c + i) = acc;
+    }
+    // the last n % 4 entries, in the same order
+    if (blockIdx.x == 0 && threadIdx.x < n - n4) {
+        const int64_t i = n4 + threadIdx.x;
+        float acc = part[i];
+        for (int s = 1; s < S; ++s) acc = acc + part[(int64_t)s * stride + i];
+        c[i] = acc;
     }
 }
 
@@ -378,11 +386,13 @@ int32_t dispatch(const float* a, const float* b, float* c, int M, int N, int K, 
 }  // namespace
 
 namespace ch {
-// c = the S slices of part added in order; n % 4 == 0, c and part 16-byte
-// aligned.  Also the bf16 products' K slices (gemm_bf16.hip).
-int32_t sum_slices_f32(const float* part, float* c, int64_t n, int S) {
+// c (n entries) = the S slices of part, `stride` floats apart, added in
+// order; stride % 4 == 0, c and part 16-byte aligned.  Also the bf16
+// products' K slices (gemm_bf16.hip).
+int32_t sum_slices_f32(const float* part, float* c, int64_t n, int S, int64_t stride) {
     const int64_t blocks = (n / 4 + 255) / 256, cap = (int64_t)ch::num_cus() * 8;
-    sum_slices_kernel<<<(unsigned)(blocks < cap ? blocks : cap), 256, 0, ch::stream()>>>(part, c, n, S);
+    const int64_t grid = blocks < 1 ? 1 : (blocks < cap ? blocks : cap);
+    sum_slices_kernel<<<(unsigned)grid, 256, 0, ch::stream()>>>(part, c, n, S, stride);
     return ch::check_hip(hipGetLastError(), "sum_slices_kernel");
 }
 }  // namespace ch
@@ -415,7 +425,7 @@ bool run_k_slices(const float* a, const float* b, float* c, int M, int N, int K,
     const int kk = K / S;
     const int64_t sA = ta ? (int64_t)kk * lda : kk, sB = tb ? kk : (int64_t)kk * ldb;
     *st = launch_layout(ta, tb, a, b, part, M, N, kk, lda, ldb, N, S, sA, sB, (int64_t)M * N);
-    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, (int64_t)M * N, S);
+    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, (int64_t)M * N, S, (int64_t)M * N);
     return true;
 }
 
@@ -708,7 +718,7 @@ bool try_batched_k_slices(const float* a, const float* b, float* c, int M, int N
     if (!launch_pingpong<TA, TB, 128>(a, b, part, M, N, K / S, lda, ldb, batch * S, (int64_t)M * K,
                                       (int64_t)K * N, (int64_t)M * N, st, S))
         return false;
-    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, n, S);
+    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, n, S, n);
     return true;
 }
 

@@ -221,7 +221,7 @@ bool run_padded(const PadPlan& p, const T* a, const T* b, float* c, int batch, b
 // layout, with its contiguous extent rounded up to a multiple of 8 (zeros
 // past it); when K is not a multiple of Q, K is rounded up to Kq in both
 // operands (zero k-columns or k-rows), so that no 16-byte chunk of a
-// k-contiguous operand straddles the kernels' K.  The guarded-edge kernels
+// k-contiguous operand straddles the kernels' K (or further, kround below).  The guarded-edge kernels
 // then run on the copies with C written in place: C is neither padded nor
 // cropped, and only the operands move once more.  The zeros change no entry,
 // as for the padded copies above.
@@ -235,11 +235,13 @@ struct AlignPlan {
     size_t bytes_a, bytes_b;  // scratch bytes of each copy (0: used in place)
 };
 
+// kround: K is rounded up to a multiple of it (at least Q), e.g. so that K
+// slices divide it.
 inline AlignPlan align_plan(int M, int N, int K, int batch, bool ta, bool tb, const void* a, const void* b,
-                            int esz) {
+                            int esz, int kround = 1) {
     AlignPlan p{};
     const int q = 16 / esz;
-    const int64_t kq = pad_up(K, q);
+    const int64_t kq = pad_up(K, kround > q ? kround : q);
     const int64_t pa = ta ? M : K, pb = tb ? K : N;  // stored pitches
     const bool a_al = ((uintptr_t)a & 15) == 0 && pa % q == 0;
     const bool b_al = ((uintptr_t)b & 15) == 0 && pb % q == 0;

@@ -1009,17 +1009,22 @@ def test_f32_ragged_long_k_every_entry(hip, oracle, M, N, K, ta, tb):
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [(64, 64, 65536), (128, 128, 65536), (512, 1024, 16384), (100, 100, 100000),
-                                   (256, 8448, 4096)])
+                                   (256, 8448, 4096), (1000, 1000, 32768), (1001, 1001, 32768),
+                                   (704, 896, 30000)])
 def test_bf16_k_split_every_entry(hip, oracle, M, N, K, ta, tb):
-    # bf16 products with few 128 x 128 tiles and a long K run as K slices
-    # (on the tiled kernels, on the general kernel for 64 x 64, and on the
-    # padded copies for 100 x 100), and with fewer 256 x 256 tiles than half a
-    # round as slices of those (256 x 8448: 33 tiles, 4 slices); added in
-    # order; every entry against the f32 loop on the upcast values, and a
-    # second call gives the same bits.
+    # bf16 products with few 128 x 128 tiles and a long K run as K slices:
+    # on the tiled kernels, on their guarded-edge forms for a ragged M or N
+    # (64 x 64, 1000^2 in place; 1001^2 on aligned copies, M x N odd so the
+    # slice sum has a tail), on aligned copies with K rounded up to 2048 where
+    # the slices do not divide K (100 x 100 x 100000, 704 x 896 x 30000);
+    # with fewer 256 x 256 tiles than half a round as slices of those (256 x
+    # 8448: 33 tiles, 4 slices).  Added in order; C pre-filled with NaN;
+    # every entry against the f32 loop on the upcast values, and a second
+    # call gives the same bits.
     A, B, Au, Bu = _operands(oracle, "bf16", M, N, K, ta, tb, seed=M + N + K + 2 * ta + tb)
     a, b = hip.from_numpy(A, "bf16"), hip.from_numpy(B, "bf16")
-    got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    out = hip.from_numpy(np.full((M, N), np.nan, np.float32))
+    got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb), out=out).numpy()
     again = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
     Ak = np.ascontiguousarray(Au.T if ta else Au)
