@@ -539,9 +539,8 @@ int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N,
         };
         // Few tiles and a long K that the slices do not divide (split_count
         // wants K % (128 S) == 0): K rounded up to a multiple of 2048 in
-        // aligned copies of both operands, then the slices.  In one launch,
-        // 704 x 896 x 30000 took 216 us; as padded copies and four slices
-        // (the padded route below, which pads C too), 101.
+        // aligned copies of both operands, then the slices.  704 x 896 x
+        // 30000: 134 us, against 216 in one launch on the operands in place.
         if (batch == 1 && M > 32 && N > 32 && K >= 16384 && K % 2048 != 0 &&
             split_count(M, N, (int)ch::pad_up(K, 2048)) > 1) {
             const ch::AlignPlan kp = ch::align_plan(M, N, K, batch, TA, TB, a, b, 2, 2048);

@@ -630,6 +630,39 @@ constexpr double kSkinnyMinFlops = 1u << 20;
 constexpr ch::PadModel kPadModel{0.86, 0.78, false, 1.0};
 constexpr int64_t kEdgeTilesPerCu = 4;
 
+// One ragged product (an M or N off the 64 grid) with at most a round of
+// 64 x 64 tiles and a long K, as S K slices (a power of two, each at least
+// 1024 deep, up to kEdgeTilesPerCu tiles per CU over all slices) on the
+// 64 x 64 kernel's guarded-edge form, its batch running over the slices,
+// added in order (deterministic).  `padded`: the operands are aligned copies
+// (ch::edge_chunks).  False when not split.
+template <bool TA, bool TB>
+bool try_edge_slices(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb,
+                     bool padded, int32_t* st) {
+    if (((uintptr_t)c & 15) || (M % 64 == 0 && N % 64 == 0)) return false;
+    const int64_t cus = ch::num_cus() > 0 ? ch::num_cus() : 1;
+    const int64_t tiles = (int64_t)((M + 63) / 64) * ((N + 63) / 64);
+    if (tiles > cus) return false;
+    int S = 1;
+    while (tiles * S * 2 <= kEdgeTilesPerCu * cus && K % (64 * S * 2) == 0 && K / (S * 2) >= 1024) S *= 2;
+    if (S == 1) return false;
+    const int kk = K / S;
+    const int64_t sA = TA ? (int64_t)kk * lda : kk, sB = TB ? kk : (int64_t)kk * ldb;
+    using P = ch::F32Tiled<64, 64, 16, 2, 2, 4, !TA, TB>;
+    if (!P::fits_edge(M, N, kk, lda, ldb, padded) || ((uintptr_t)a & 15) || ((uintptr_t)b & 15) || sA % 4 ||
+        sB % 4)
+        return false;
+    const int64_t n = (int64_t)M * N, n4 = (n + 3) / 4 * 4;
+    float* part = (float*)ch::scratch_try(9, sizeof(float) * (size_t)S * n4);
+    if (!part) return false;
+    if (!(tiles * S <= 2 * cus && launch_tiled_edge<64, 64, 32, 2, 2, 4, TA, TB>(a, b, part, M, N, kk, lda, ldb, S,
+                                                                                 sA, sB, n4, st, padded)) &&
+        !launch_tiled_edge<64, 64, 16, 2, 2, 4, TA, TB>(a, b, part, M, N, kk, lda, ldb, S, sA, sB, n4, st, padded))
+        *st = launch_general<TA, TB>(a, b, part, M, N, kk, lda, ldb, N, S, sA, sB, n4);
+    if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, n, S, n4);
+    return true;
+}
+
 template <bool TA, bool TB>
 int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda,
                int64_t ldb, int64_t ldc, int batch, int64_t sA, int64_t sB, int64_t sC) {
@@ -655,28 +688,39 @@ int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, in
         // 269 against 229; 16000^2 x 128 A^T.B level).
         const int64_t tiles64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64) * batch;
         const int64_t cus = ch::num_cus();
+        const bool edge16 = tiles64 <= kEdgeTilesPerCu * cus || K <= 512;
+        // The same kernels on aligned copies (ch::run_aligned): K slices for
+        // one product with few tiles and a long K, else one launch.
+        auto edge = [&](const float* pa, const float* pb, int64_t plda, int64_t pldb, int64_t psA, int64_t psB,
+                        int Kq, int32_t* s) {
+            if (batch == 1 && try_edge_slices<TA, TB>(pa, pb, c, M, N, Kq, plda, pldb, true, s)) return true;
+            if (tiles64 <= 2 * cus && launch_tiled_edge<64, 64, 32, 2, 2, 4, TA, TB>(
+                                          pa, pb, c, M, N, Kq, plda, pldb, batch, psA, psB, sC, s, true))
+                return true;
+            return launch_tiled_edge<64, 64, 16, 2, 2, 4, TA, TB>(pa, pb, c, M, N, Kq, plda, pldb, batch, psA, psB,
+                                                                  sC, s, true);
+        };
+        // Few tiles and a long K that the slices do not divide: K rounded up
+        // to a multiple of 2048 in aligned copies of both operands, then the
+        // slices.
+        if (batch == 1 && K >= 16384 && K % 2048 != 0 && (M % 64 || N % 64) && tiles64 <= cus) {
+            const ch::AlignPlan kp = ch::align_plan(M, N, K, batch, TA, TB, a, b, 4, 2048);
+            if (ch::run_aligned(kp, a, b, M, N, K, batch, TA, TB, edge, &st)) return st;
+        }
+        if (batch == 1 && try_edge_slices<TA, TB>(a, b, c, M, N, K, lda, ldb, false, &st)) return st;
         if (tiles64 <= 2 * cus &&
             launch_tiled_edge<64, 64, 32, 2, 2, 4, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
             return st;
-        const bool edge16 = tiles64 <= kEdgeTilesPerCu * cus || K <= 512;
         if (edge16 &&
             launch_tiled_edge<64, 64, 16, 2, 2, 4, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
             return st;
         // Rows that are not whole 16-byte chunks (an extent that is not a
         // multiple of 4, a misaligned view): the same kernels on aligned
-        // copies of those operands, C in place (ch::run_aligned).  Against
-        // the padded route below (same box, two runs): 1001^3 30.5 against
-        // 33.8 us, 3000 x 3001 x 501 89 against 105.
+        // copies of those operands, C in place.  Against the padded route
+        // below (same box, two runs): 1001^3 30.5 against 33.8 us, 3000 x
+        // 3001 x 501 89 against 105.
         if (edge16) {
             const ch::AlignPlan ap = ch::align_plan(M, N, K, batch, TA, TB, a, b, 4);
-            auto edge = [&](const float* pa, const float* pb, int64_t plda, int64_t pldb, int64_t psA, int64_t psB,
-                            int Kq, int32_t* s) {
-                if (tiles64 <= 2 * cus && launch_tiled_edge<64, 64, 32, 2, 2, 4, TA, TB>(
-                                              pa, pb, c, M, N, Kq, plda, pldb, batch, psA, psB, sC, s, true))
-                    return true;
-                return launch_tiled_edge<64, 64, 16, 2, 2, 4, TA, TB>(pa, pb, c, M, N, Kq, plda, pldb, batch, psA,
-                                                                      psB, sC, s, true);
-            };
             if (ch::run_aligned(ap, a, b, M, N, K, batch, TA, TB, edge, &st)) return st;
         }
         const ch::PadPlan p = ch::pad_plan(M, N, K, batch, TA, TB, a, b, 4, ch::num_cus(), kPadModel);
