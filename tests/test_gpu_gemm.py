@@ -994,14 +994,15 @@ def test_bf16_ragged_round_split_every_entry(hip, oracle, ta, tb):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
-@pytest.mark.parametrize("M,N,K", [(100, 100, 100000), (70, 300, 30000), (1000, 1000, 32768), (1001, 1003, 20000)])
+@pytest.mark.parametrize("M,N,K", [(100, 100, 100000), (70, 300, 30000), (1000, 1000, 32768), (1001, 1003, 20000),
+                                   (1001, 1003, 32768)])
 def test_f32_ragged_long_k_every_entry(hip, oracle, M, N, K, ta, tb):
     # Ragged M or N, few tiles and a long K: K slices on the 64 x 64 kernel's
-    # guarded-edge form, on the operands in place (1000^2 x 32768) or on
-    # aligned copies with K rounded up to 2048 where the slices do not divide
-    # K (the others; 1001 x 1003 also has rows that are not whole chunks and
-    # an odd M x N for the slice sum's tail).  C pre-filled with NaN; every
-    # entry against the loop.
+    # guarded-edge form, on the operands in place (1000^2 x 32768), on aligned
+    # copies of the operands whose rows are not whole chunks (1001 x 1003 x
+    # 32768), or on aligned copies of both with K rounded up to 2048 where the
+    # slices do not divide K (the others).  1001 x 1003 is odd for the slice
+    # sum's tail.  C pre-filled with NaN; every entry against the loop.
     A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=M + N + K + ta)
     out = hip.from_numpy(np.full((M, N), np.nan, np.float32))
     got = hip.matmul(hip.from_numpy(A), hip.from_numpy(B), trans_a=bool(ta), trans_b=bool(tb), out=out).numpy()
