@@ -469,6 +469,22 @@ int split_count(int M, int N, int K) {
     return S;
 }
 
+// Slices for a product the guarded-edge kernels take (M or N off the
+// 128 x 128 tile, or K off the 64-deep k-tile; split_count's rules are for
+// the aligned kernels): with fewer 128 x 128 tiles than half a round, the
+// most slices, at least 512 deep, that one round of those tiles holds, whose
+// depth is whole 16-byte chunks (K % 8S == 0).  128 x 300 x 5000 A^T.B^T
+// (three tiles) 47.7 -> 15.9 us, 300^2 x 3000 31 -> 17.  1 = no split.
+int edge_split_count(int M, int N, int K) {
+    if (M % 128 == 0 && N % 128 == 0 && K % 64 == 0) return 1;
+    const int64_t cus = ch::num_cus() > 0 ? ch::num_cus() : 1;
+    const int64_t tiles = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+    if (tiles * 2 > cus) return 1;
+    for (int S = (int)std::min<int64_t>(cus / tiles, K / 512); S >= 2; --S)
+        if (K % (8 * S) == 0) return S;
+    return 1;
+}
+
 // Whether K slices of depth kk with these strides go to an aligned kernel
 // (128 x 128 tiles and whole k-tiles) or a guarded-edge one, not to the
 // general kernel: on that kernel 1000^2 x 65536 ran as two slices in
@@ -492,7 +508,8 @@ template <bool TA, bool TB>
 bool try_k_split(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb,
                  bool padded, int32_t* st) {
     if (((uintptr_t)c & 15) != 0) return false;
-    const int S = split_count(M, N, K);
+    int S = edge_split_count(M, N, K);
+    if (S <= 1) S = split_count(M, N, K);
     if (S <= 1) return false;
     const int kk = K / S;
     const int64_t n = (int64_t)M * N, n4 = (n + 3) / 4 * 4;
@@ -537,12 +554,11 @@ int32_t launch_any(const uint16_t* a, const uint16_t* b, float* c, int M, int N,
             return launch_edge<TA, TB>(pa, pb, c, M, N, Kq, batch, str, s) ||
                    launch_pairs_edge<TA, TB>(pa, pb, c, M, N, Kq, batch, str, s);
         };
-        // Few tiles and a long K that the slices do not divide (split_count
-        // wants K % (128 S) == 0): K rounded up to a multiple of 2048 in
-        // aligned copies of both operands, then the slices.  704 x 896 x
-        // 30000: 134 us, against 216 in one launch on the operands in place.
-        if (batch == 1 && M > 32 && N > 32 && K >= 16384 && K % 2048 != 0 &&
-            split_count(M, N, (int)ch::pad_up(K, 2048)) > 1) {
+        // Few tiles and a long K that no slice count divides in whole
+        // chunks: K rounded up to a multiple of 2048 in aligned copies of
+        // both operands, then the slices.
+        if (batch == 1 && M > 32 && N > 32 && K >= 16384 && K % 2048 != 0 && edge_split_count(M, N, K) <= 1 &&
+            edge_split_count(M, N, (int)ch::pad_up(K, 2048)) > 1) {
             const ch::AlignPlan kp = ch::align_plan(M, N, K, batch, TA, TB, a, b, 2, 2048);
             if (ch::run_aligned(kp, a, b, M, N, K, batch, TA, TB, edge, &st)) return st;
         }

@@ -995,14 +995,15 @@ def test_bf16_ragged_round_split_every_entry(hip, oracle, ta, tb):
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [(100, 100, 100000), (70, 300, 30000), (1000, 1000, 32768), (1001, 1003, 20000),
-                                   (1001, 1003, 32768)])
+                                   (1001, 1003, 32768), (2048, 200, 2000)])
 def test_f32_ragged_long_k_every_entry(hip, oracle, M, N, K, ta, tb):
     # Ragged M or N, few tiles and a long K: K slices on the 64 x 64 kernel's
-    # guarded-edge form, on the operands in place (1000^2 x 32768), on aligned
+    # guarded-edge form, on the operands in place (1000^2 x 32768, 100^2 x
+    # 100000 as 125 slices, 70 x 300 x 30000, 2048 x 200 x 2000), on aligned
     # copies of the operands whose rows are not whole chunks (1001 x 1003 x
-    # 32768), or on aligned copies of both with K rounded up to 2048 where the
-    # slices do not divide K (the others).  1001 x 1003 is odd for the slice
-    # sum's tail.  C pre-filled with NaN; every entry against the loop.
+    # 32768), or on aligned copies of both with K rounded up to 2048 (1001 x
+    # 1003 x 20000).  1001 x 1003 is odd for the slice sum's tail.  C
+    # pre-filled with NaN; every entry against the loop.
     A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=M + N + K + ta)
     out = hip.from_numpy(np.full((M, N), np.nan, np.float32))
     got = hip.matmul(hip.from_numpy(A), hip.from_numpy(B), trans_a=bool(ta), trans_b=bool(tb), out=out).numpy()
@@ -1016,17 +1017,18 @@ def test_f32_ragged_long_k_every_entry(hip, oracle, M, N, K, ta, tb):
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [(64, 64, 65536), (128, 128, 65536), (512, 1024, 16384), (100, 100, 100000),
                                    (256, 8448, 4096), (1000, 1000, 32768), (1001, 1001, 32768),
-                                   (704, 896, 30000)])
+                                   (704, 896, 30000), (128, 300, 5000), (300, 400, 20024)])
 def test_bf16_k_split_every_entry(hip, oracle, M, N, K, ta, tb):
     # bf16 products with few 128 x 128 tiles and a long K run as K slices:
-    # on the tiled kernels, on their guarded-edge forms for a ragged M or N
-    # (64 x 64, 1000^2 in place; 1001^2 on aligned copies, M x N odd so the
-    # slice sum has a tail), on aligned copies with K rounded up to 2048 where
-    # the slices do not divide K (100 x 100 x 100000, 704 x 896 x 30000);
-    # with fewer 256 x 256 tiles than half a round as slices of those (256 x
-    # 8448: 33 tiles, 4 slices).  Added in order; C pre-filled with NaN;
-    # every entry against the f32 loop on the upcast values, and a second
-    # call gives the same bits.
+    # on the tiled kernels; on their guarded-edge forms for a ragged M, N or
+    # K, as many slices as whole 16-byte chunks allow (64 x 64, 1000^2, 704 x
+    # 896 x 30000, 128 x 300 x 5000 in place; 1001^2 and 100^2 on aligned
+    # copies, 1001^2 odd so the slice sum has a tail); on aligned copies with
+    # K rounded up to 2048 where no slice count divides K in whole chunks
+    # (300 x 400 x 20024, 20024 = 8 x 2503); with fewer 256 x 256 tiles than
+    # half a round as slices of those (256 x 8448: 33 tiles, 4 slices).
+    # Added in order; C pre-filled with NaN; every entry against the f32 loop
+    # on the upcast values, and a second call gives the same bits.
     A, B, Au, Bu = _operands(oracle, "bf16", M, N, K, ta, tb, seed=M + N + K + 2 * ta + tb)
     a, b = hip.from_numpy(A, "bf16"), hip.from_numpy(B, "bf16")
     out = hip.from_numpy(np.full((M, N), np.nan, np.float32))
