@@ -641,6 +641,56 @@ def test_f32_edge_tiles_every_entry(hip, oracle, M, N, K, ta, tb):
     assert_gemm_close(got, ref, den, K, f"f32 edge {M}x{N}x{K} ta={ta} tb={tb}")
 
 
+# f32 ragged products of one or two rounds of 128 x 128 tiles (M, N and K
+# ragged against 128 x 128 x 16, all four layouts, batched): the 64 x 64
+# guarded-edge tiles or the padded route.  C pre-filled with NaN.
+_F32_RAGGED_ROUND_CASES = [
+    (2000, 2000, 1000, 0, 0), (2000, 2000, 1004, 0, 1), (1900, 2100, 996, 1, 0), (2000, 2000, 2004, 1, 1),
+    (2500, 2500, 600, 0, 0), (2540, 2532, 100, 1, 1),
+]
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb", _F32_RAGGED_ROUND_CASES)
+def test_f32_ragged_rounds_every_entry(hip, oracle, M, N, K, ta, tb):
+    A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=M + 3 * N + 5 * K + 2 * ta + tb)
+    a, b = hip.from_numpy(A), hip.from_numpy(B)
+    out = hip.from_numpy(np.full((M, N), np.nan, np.float32))
+    got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb), out=out).numpy()
+    again = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "repeat"
+    ref = oracle.matmul(Au, Bu, trans_a=bool(ta), trans_b=bool(tb), threads=16)
+    den = np.abs(Au.T if ta else Au).astype(np.float64) @ np.abs(Bu.T if tb else Bu).astype(np.float64)
+    assert_gemm_close(got, ref, den, K, f"f32 ragged rounds {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+def test_f32_ragged_rounds_batched_every_entry(hip, oracle):
+    bsz, M, N, K = 4, 1000, 1000, 500  # 256 tiles of 128 x 128 over four products
+    A, B, Au, Bu = _operands(oracle, "f32", M, N, K, 0, 1, seed=61, batch=bsz)
+    got = hip.matmul_batched(hip.from_numpy(A), hip.from_numpy(B), trans_b=True).numpy()
+    for i in range(bsz):
+        ref = oracle.matmul(Au[i], Bu[i], trans_b=True, threads=16)
+        den = np.abs(Au[i]).astype(np.float64) @ np.abs(Bu[i]).astype(np.float64).T
+        assert_gemm_close(got[i], ref, den, K, f"f32 ragged rounds batched entry {i}")
+
+
+def test_f32_ragged_rounds_infinities_and_nans(hip):
+    # the zeros read past the operands add 0 * 0 only (2000 x 2000 x 1000)
+    M, N, K = 2000, 2000, 1000
+    rng = np.random.default_rng(67)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    A[M - 1, K - 1] = np.inf
+    A[7, 3] = np.nan
+    B[K - 1, N - 1] = -np.inf
+    B[K - 2, 11] = np.inf
+    got = hip.matmul(hip.from_numpy(A), hip.from_numpy(B)).numpy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = A.astype(np.float64) @ B.astype(np.float64)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref))
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))
+
+
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
 def test_f32_edge_tiles_batched_every_entry(hip, oracle, ta, tb):
     # 3 x 700 x 900 x 300: 495 tiles of 64 x 64 over three products
