@@ -233,6 +233,13 @@ int32_t launch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int
     return CLEAVE_HIP_OK;
 }
 
+// Whether the 32 x 32 store loop of the tiled kernel writes C non-temporally
+// (its NTC form): C rows of whole 128-byte lines, every product's C 128-byte
+// aligned.
+bool nt_c(const float* c, int N, const Strides& s) {
+    return N % 32 == 0 && ((uintptr_t)c & 127) == 0 && s.sC % 32 == 0;
+}
+
 // Large-tile kernel (gemm_bf16_tiled.hpp) for shapes that divide its tile.
 // Returns false when the shape or alignment does not fit.
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int MI, bool TA, bool TB>
@@ -244,8 +251,17 @@ bool launch_tiled(const uint16_t* a, const uint16_t* b, float* c, int M, int N, 
     const int tiles_m = M / BM, tiles_n = N / BN;
     if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
     dim3 grid((unsigned)(tiles_m * tiles_n * batch));
-    ch::gemm_bf16_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI><<<grid, P::THREADS, 0, ch::stream()>>>(
-        a, b, c, M, N, K, lda, ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch, kslices);
+    bool nt = false;
+    if constexpr (MI == 32) nt = nt_c(c, N, s);
+    if constexpr (MI == 32) {
+        if (nt)
+            ch::gemm_bf16_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI, false, true>
+                <<<grid, P::THREADS, 0, ch::stream()>>>(a, b, c, M, N, K, lda, ldb, s.sA, s.sB, s.sC, tiles_m,
+                                                        tiles_n, batch, kslices);
+    }
+    if (!nt)
+        ch::gemm_bf16_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI><<<grid, P::THREADS, 0, ch::stream()>>>(
+            a, b, c, M, N, K, lda, ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch, kslices);
     *status = ch::check_hip(hipGetLastError(), "gemm_bf16_tiled_kernel");
     return true;
 }
@@ -260,8 +276,14 @@ bool launch_tiled_edge(const uint16_t* a, const uint16_t* b, float* c, int M, in
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
     dim3 grid((unsigned)(tiles_m * tiles_n * batch));
-    ch::gemm_bf16_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI, true><<<grid, P::THREADS, 0, ch::stream()>>>(
-        a, b, c, M, N, K, s.lda, s.ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch, 1);
+    if (nt_c(c, N, s))
+        ch::gemm_bf16_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI, true, true>
+            <<<grid, P::THREADS, 0, ch::stream()>>>(a, b, c, M, N, K, s.lda, s.ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n,
+                                                    batch, 1);
+    else
+        ch::gemm_bf16_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI, true>
+            <<<grid, P::THREADS, 0, ch::stream()>>>(a, b, c, M, N, K, s.lda, s.ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n,
+                                                    batch, 1);
     *status = ch::check_hip(hipGetLastError(), "gemm_bf16_tiled_kernel");
     return true;
 }

@@ -83,7 +83,13 @@ struct Bf16Tiled {
 // the K slices of batch / kslices products of depth K * kslices: z = s nb + b
 // (nb = batch / kslices) is slice s of product b, at A + b strideA plus s K
 // columns (k-contiguous A) or s K rows of A (likewise B), and C + z strideC.
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC, int MI = 32, bool EDGE = false>
+// NTC (32 x 32 accumulators): C stored non-temporally, for C rows of whole
+// 128-byte lines (N % 32 == 0, C 128-byte aligned).  Measured (same box,
+// two runs): 16384^2 x 256 313 -> 245 us, 24576^2 x 256 727 -> 526,
+// 65536 x 1024 x 256 77 -> 61, 2048^2 x 1024 14.4 -> 12.9; on rows that are
+// not whole lines (12300^2 x 200) 239 -> 363, so those keep cached stores.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC, int MI = 32, bool EDGE = false,
+          bool NTC = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC,
@@ -111,6 +117,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
     C += (int64_t)bt * strideC;
 
     static_assert(!EDGE || (MI == 32), "the EDGE form stores 32 x 32 accumulators");
+    static_assert(!NTC || (MI == 32), "non-temporal C stores are the 32 x 32 store loop's");
     const uint32_t lds0 = lds_addr(smem);
     // aligned shapes: scalar tile bases and 32-bit lane offsets
     TileCopy<AKC, BM, BK, NW> copy_a;
@@ -245,7 +252,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
                 for (int v = 0; v < 16; ++v) {
                     const int r = m0 + wm * P::TM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
                     const int c = n0 + wn * P::TN + j * 32 + (lane & 31);
-                    if (!EDGE || (r < M && c < N)) C[(int64_t)r * N + c] = acc[i][j][v];
+                    if (!EDGE || (r < M && c < N)) {
+                        if constexpr (NTC) __builtin_nontemporal_store(acc[i][j][v], C + (int64_t)r * N + c);
+                        else C[(int64_t)r * N + c] = acc[i][j][v];
+                    }
                 }
     }
 }
