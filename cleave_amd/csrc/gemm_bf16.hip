@@ -21,6 +21,8 @@
 // k-contiguous in global memory is copied in 16-byte chunks; one that is
 // contiguous along m/n is read as 8(k) x 2(m/n) blocks of 4-byte words and
 // transposed in registers before a pair of 16-byte LDS stores.
+#include <type_traits>
+
 #include "common.hpp"
 #include "gemm_bf16_pingpong.hpp"
 #include "gemm_bf16_tiled.hpp"
@@ -239,6 +241,19 @@ int32_t launch(const uint16_t* a, const uint16_t* b, float* c, int M, int N, int
 bool nt_c(const float* c, int N, const Strides& s) {
     return N % 32 == 0 && ((uintptr_t)c & 127) == 0 && s.sC % 32 == 0;
 }
+// The 16 x 16 accumulator store paths (ping-pong, paired-copy and 256 x 256
+// tiled kernels, tiles::store_acc16_lines) store C non-temporally when one
+// launch writes at least this many bytes of it, in whole 128-byte lines.
+// Same box, two runs: a C of 256 MiB or more gains (8192^3 A.B 712-718 ->
+// 699-706 us, A.B^T 742 -> 714-723, 65536 x 1024 x 1024 149 -> 122, 16384^2
+// x 512 437 -> 296, 16384^2 x 1024 A^T.B 622 -> 500, 32768 x 8192 x 1024 568
+// -> 473); one that the 256 MiB MALL holds loses (4096^3, 64 MiB, 95.5 ->
+// 98.5; batched 64 x 512^3 24.2 -> 25.1; 4096 x 8192 x 2048, 128 MiB, 106
+// -> 111) or is level (6144^2 x 4096, 144 MiB, 239 -> 237).
+constexpr int64_t kNtStoreBytes = 192ll << 20;
+bool nt_c16(const float* c, int M, int N, int batch, const Strides& s) {
+    return nt_c(c, N, s) && (int64_t)batch * M * N * 4 >= kNtStoreBytes;
+}
 
 // Large-tile kernel (gemm_bf16_tiled.hpp) for shapes that divide its tile.
 // Returns false when the shape or alignment does not fit.
@@ -251,15 +266,12 @@ bool launch_tiled(const uint16_t* a, const uint16_t* b, float* c, int M, int N, 
     const int tiles_m = M / BM, tiles_n = N / BN;
     if ((int64_t)tiles_m * tiles_n * batch > 0x7FFFFFFF) return false;
     dim3 grid((unsigned)(tiles_m * tiles_n * batch));
-    bool nt = false;
-    if constexpr (MI == 32) nt = nt_c(c, N, s);
-    if constexpr (MI == 32) {
-        if (nt)
-            ch::gemm_bf16_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI, false, true>
-                <<<grid, P::THREADS, 0, ch::stream()>>>(a, b, c, M, N, K, lda, ldb, s.sA, s.sB, s.sC, tiles_m,
-                                                        tiles_n, batch, kslices);
-    }
-    if (!nt)
+    // 32 x 32 stores: non-temporal in whole lines at any size; 16 x 16: past kNtStoreBytes
+    if (MI == 32 ? nt_c(c, N, s) : nt_c16(c, M, N, batch, s))
+        ch::gemm_bf16_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI, false, true>
+            <<<grid, P::THREADS, 0, ch::stream()>>>(a, b, c, M, N, K, lda, ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n,
+                                                    batch, kslices);
+    else
         ch::gemm_bf16_tiled_kernel<BM, BN, BK, WM, WN, STAGES, !TA, TB, MI><<<grid, P::THREADS, 0, ch::stream()>>>(
             a, b, c, M, N, K, lda, ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch, kslices);
     *status = ch::check_hip(hipGetLastError(), "gemm_bf16_tiled_kernel");
@@ -339,9 +351,14 @@ bool launch_pairs_edge(const uint16_t* a, const uint16_t* b, float* c, int M, in
         if (big * 2 < cus || K <= 256 || (big <= cus && K <= 512)) return false;
         if (!P::fits_edge(M, N, K, s.lda, s.ldb, s.padded) || !bases_aligned(a, b, s)) return false;
         if (big > 0x7FFFFFFF) return false;
-        ch::gemm_bf16_pingpong_kernel<false, false, false, 5, true><<<dim3((unsigned)big), P::THREADS, 0,
-                                                                      ch::stream()>>>(
-            a, b, c, M, N, K, s.lda, s.ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch);
+        if (nt_c16(c, M, N, batch, s))
+            ch::gemm_bf16_pingpong_kernel<false, false, false, 5, true, true>
+                <<<dim3((unsigned)big), P::THREADS, 0, ch::stream()>>>(a, b, c, M, N, K, s.lda, s.ldb, s.sA, s.sB,
+                                                                       s.sC, tiles_m, tiles_n, batch);
+        else
+            ch::gemm_bf16_pingpong_kernel<false, false, false, 5, true>
+                <<<dim3((unsigned)big), P::THREADS, 0, ch::stream()>>>(a, b, c, M, N, K, s.lda, s.ldb, s.sA, s.sB,
+                                                                       s.sC, tiles_m, tiles_n, batch);
         *status = ch::check_hip(hipGetLastError(), "gemm_bf16_pingpong_kernel");
         return true;
     } else {
@@ -355,8 +372,12 @@ bool launch_pairs_edge(const uint16_t* a, const uint16_t* b, float* c, int M, in
         const int total = (int)big;
         const int resident = cus >= 8 ? (int)(cus / 8 * 8) : (cus > 0 ? (int)cus : 1);
         dim3 grid((unsigned)(total < resident ? total : resident));
-        ch::gemm_bf16_pingpong_pairs_kernel<!TA, TB, true><<<grid, P::THREADS, 0, ch::stream()>>>(
-            a, b, c, M, N, K, s.lda, s.ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch);
+        if (nt_c16(c, M, N, batch, s))
+            ch::gemm_bf16_pingpong_pairs_kernel<!TA, TB, true, true><<<grid, P::THREADS, 0, ch::stream()>>>(
+                a, b, c, M, N, K, s.lda, s.ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch);
+        else
+            ch::gemm_bf16_pingpong_pairs_kernel<!TA, TB, true><<<grid, P::THREADS, 0, ch::stream()>>>(
+                a, b, c, M, N, K, s.lda, s.ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch);
         *status = ch::check_hip(hipGetLastError(), "gemm_bf16_pingpong_pairs_kernel");
         return true;
     }
@@ -378,12 +399,15 @@ bool launch_pingpong(const uint16_t* a, const uint16_t* b, float* c, int M, int 
     const uint64_t last_a = (uint64_t)K * (TA ? (uint64_t)lda * 2 : 2);
     const uint64_t last_b = (uint64_t)K * (TB ? 2 : (uint64_t)ldb * 2);
     const int64_t sa = s.sA, sb = s.sB, sc = s.sC;
-    if (last_a < (1ull << 32) && last_b < (1ull << 32))
-        ch::gemm_bf16_pingpong_kernel<!TA, TB, true><<<grid, P::THREADS, 0, ch::stream()>>>(
-            a, b, c, M, N, K, lda, ldb, sa, sb, sc, tiles_m, tiles_n, batch);
-    else
-        ch::gemm_bf16_pingpong_kernel<!TA, TB, false><<<grid, P::THREADS, 0, ch::stream()>>>(
-            a, b, c, M, N, K, lda, ldb, sa, sb, sc, tiles_m, tiles_n, batch);
+    const bool off32 = last_a < (1ull << 32) && last_b < (1ull << 32), nt = nt_c16(c, M, N, batch, s);
+    auto go = [&](auto off32_t, auto nt_t) {
+        ch::gemm_bf16_pingpong_kernel<!TA, TB, decltype(off32_t)::value, 5, false, decltype(nt_t)::value>
+            <<<grid, P::THREADS, 0, ch::stream()>>>(a, b, c, M, N, K, lda, ldb, sa, sb, sc, tiles_m, tiles_n, batch);
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    if (off32) nt ? go(T{}, T{}) : go(T{}, F{});
+    else nt ? go(F{}, T{}) : go(F{}, F{});
     *status = ch::check_hip(hipGetLastError(), "gemm_bf16_pingpong_kernel");
     return true;
 }
@@ -408,8 +432,12 @@ bool launch_pairs(const uint16_t* a, const uint16_t* b, float* c, int M, int N, 
         const int cus = ch::num_cus();
         const int resident = cus >= 8 ? cus / 8 * 8 : (cus > 0 ? cus : 1);
         dim3 grid((unsigned)(total < resident ? total : resident));
-        ch::gemm_bf16_pingpong_pairs_kernel<!TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
-            a, b, c, M, N, K, lda, ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch);
+        if (nt_c16(c, M, N, batch, s))
+            ch::gemm_bf16_pingpong_pairs_kernel<!TA, TB, false, true><<<grid, P::THREADS, 0, ch::stream()>>>(
+                a, b, c, M, N, K, lda, ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch);
+        else
+            ch::gemm_bf16_pingpong_pairs_kernel<!TA, TB><<<grid, P::THREADS, 0, ch::stream()>>>(
+                a, b, c, M, N, K, lda, ldb, s.sA, s.sB, s.sC, tiles_m, tiles_n, batch);
         *status = ch::check_hip(hipGetLastError(), "gemm_bf16_pingpong_pairs_kernel");
         return true;
     }

@@ -61,7 +61,8 @@ struct Bf16PingPong {
 // EDGE (any M, N and K, fits_edge): tiles_m and tiles_n rounded up; both
 // copies become EdgeCopy buffer loads that read zeros past the operands' rows
 // (columns) and past K, and the stores skip what lies past M or N.
-template <bool AKC, bool BKC, bool OFF32 = false, int STAGES_ = 5, bool EDGE = false>
+// NTC: C stored non-temporally (tiles::store_acc16_lines).
+template <bool AKC, bool BKC, bool OFF32 = false, int STAGES_ = 5, bool EDGE = false, bool NTC = false>
 __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC,
@@ -178,8 +179,9 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(
     };
     pingpong_schedule<LPW, S>(nk, grp, issue, m_phase, c_phase);
 
-    if constexpr (EDGE) store_acc16_lines_masked(C, N, m0 + grp * P::TM, n0 + wn * P::TN, acc, lane, M, N);
-    else store_acc16_lines(C, N, m0 + grp * P::TM, n0 + wn * P::TN, acc, lane);
+    const int r0 = m0 + grp * P::TM, c0 = n0 + wn * P::TN;
+    if constexpr (EDGE) store_acc16_lines_masked<FM, FN, NTC>(C, N, r0, c0, acc, lane, M, N);
+    else store_acc16_lines<FM, FN, NTC>(C, N, r0, c0, acc, lane);
 }
 
 }  // namespace ch
@@ -257,7 +259,8 @@ struct Bf16PingPongPairs {
 // (columns) or past K read zeros (a masked offset past the resource's range,
 // as EdgeCopy), K is walked in whole pairs of k-tiles, and the stores skip
 // what lies past M or N.
-template <bool AKC, bool BKC, bool EDGE = false>
+// NTC: C stored non-temporally (tiles::store_acc16_lines).
+template <bool AKC, bool BKC, bool EDGE = false, bool NTC = false>
 __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, int64_t lda, int64_t ldb, int64_t strideA, int64_t strideB, int64_t strideC,
@@ -452,8 +455,8 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_pairs_kernel(
     prologue();
     asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
     auto store_c = [&](float* Cdone, int r0, int c0) {
-        if constexpr (EDGE) store_acc16_lines_masked(Cdone, N, r0, c0, acc, lane, M, N);
-        else store_acc16_lines(Cdone, N, r0, c0, acc, lane);
+        if constexpr (EDGE) store_acc16_lines_masked<FM, FN, NTC>(Cdone, N, r0, c0, acc, lane, M, N);
+        else store_acc16_lines<FM, FN, NTC>(Cdone, N, r0, c0, acc, lane);
     };
     auto next_tile = [&]() {
         float* const Cdone = Ct;

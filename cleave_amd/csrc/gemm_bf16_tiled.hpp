@@ -83,11 +83,8 @@ struct Bf16Tiled {
 // the K slices of batch / kslices products of depth K * kslices: z = s nb + b
 // (nb = batch / kslices) is slice s of product b, at A + b strideA plus s K
 // columns (k-contiguous A) or s K rows of A (likewise B), and C + z strideC.
-// NTC (32 x 32 accumulators): C stored non-temporally, for C rows of whole
-// 128-byte lines (N % 32 == 0, C 128-byte aligned).  Measured (same box,
-// two runs): 16384^2 x 256 313 -> 245 us, 24576^2 x 256 727 -> 526,
-// 65536 x 1024 x 256 77 -> 61, 2048^2 x 1024 14.4 -> 12.9; on rows that are
-// not whole lines (12300^2 x 200) 239 -> 363, so those keep cached stores.
+// NTC: C stored non-temporally, for C rows of whole 128-byte lines (the
+// launchers' nt_c).
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, bool AKC, bool BKC, int MI = 32, bool EDGE = false,
           bool NTC = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
@@ -117,7 +114,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
     C += (int64_t)bt * strideC;
 
     static_assert(!EDGE || (MI == 32), "the EDGE form stores 32 x 32 accumulators");
-    static_assert(!NTC || (MI == 32), "non-temporal C stores are the 32 x 32 store loop's");
     const uint32_t lds0 = lds_addr(smem);
     // aligned shapes: scalar tile bases and 32-bit lane offsets
     TileCopy<AKC, BM, BK, NW> copy_a;
@@ -242,7 +238,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tiled_kernel(
     // 32 x 32 accumulator layout: lane holds column l%32, rows
     // 8*(v/4) + 4*(l/32) + v%4, so a store already covers whole 128-byte rows.
     if constexpr (MI == 16) {
-        store_acc16_lines(C, N, m0 + wm * P::TM, n0 + wn * P::TN, acc, lane);
+        store_acc16_lines<FM, FN, NTC>(C, N, m0 + wm * P::TM, n0 + wn * P::TN, acc, lane);
     } else {
 #pragma unroll
         for (int i = 0; i < FM; ++i)

@@ -361,7 +361,10 @@ __device__ __forceinline__ v4f read_frag_f32(const char* tile, int row0, int kb,
 // Values go in and out through __float_as_uint / __uint_as_float:
 // __builtin_bit_cast of a vector subscript (acc[i][j][v], or the swap's
 // result pair) reads element 0 whatever the index, in ROCm 7.2's clang.
-template <int FM, int FN>
+//
+// NT: non-temporal stores (`nt`), for a C larger than the MALL whose rows are
+// whole 128-byte lines; the caller decides.
+template <int FM, int FN, bool NT = false>
 __device__ __forceinline__ void store_acc16_lines(float* __restrict__ C, int64_t ldc, int r0, int c0,
                                                   const v4f (&acc)[FM][FN], int lane) {
     static_assert(FN % 2 == 0, "blocks are paired along n");
@@ -375,8 +378,13 @@ __device__ __forceinline__ void store_acc16_lines(float* __restrict__ C, int64_t
                 const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[i][j][v]),
                                                                 __float_as_uint(acc[i][j + 1][v]), false, false);
                 float* p = C + (int64_t)(r0 + i * 16 + rl + v) * ldc + (c0 + j * 16 + cl);
-                p[0] = __uint_as_float(s[0]);
-                p[4 * ldc] = __uint_as_float(s[1]);
+                if constexpr (NT) {
+                    __builtin_nontemporal_store(__uint_as_float(s[0]), p);
+                    __builtin_nontemporal_store(__uint_as_float(s[1]), p + 4 * ldc);
+                } else {
+                    p[0] = __uint_as_float(s[0]);
+                    p[4 * ldc] = __uint_as_float(s[1]);
+                }
             }
 }
 // The same stores, skipping elements at or past row M or column N (the
@@ -389,9 +397,10 @@ __device__ __forceinline__ void store_acc16_lines(float* __restrict__ C, int64_t
 // column test takes one value per pair of blocks and lane; testing every
 // element's row and column instead kept 128 conditions live and spilled.
 // Needs the block's rows of C (16 * FM of ldc floats) under 2 GiB.
-template <int FM, int FN>
+template <int FM, int FN, bool NT = false>
 __device__ __forceinline__ void store_acc16_lines_masked(float* __restrict__ C, int64_t ldc, int r0, int c0,
                                                          const v4f (&acc)[FM][FN], int lane, int M, int N) {
+    constexpr int kAux = NT ? 2 : 0;  // cache policy: 2 = nt
     static_assert(FN % 2 == 0, "blocks are paired along n");
     if (r0 >= M) return;  // wave-uniform: the whole block lies past the last row
     const int64_t left = ((int64_t)(M - 1 - r0) * ldc + N) * 4;  // bytes from row r0 to C's last element
@@ -410,8 +419,9 @@ __device__ __forceinline__ void store_acc16_lines_masked(float* __restrict__ C, 
                 const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[i][j][v]),
                                                                 __float_as_uint(acc[i][j + 1][v]), false, false);
                 const uint32_t o0 = (uint32_t)(i * 16 + rl + v) * ld4 + (uint32_t)c * 4u;
-                __builtin_amdgcn_raw_buffer_store_b32(s[0], rsrc, (int)(col_ok ? o0 : kOutOfRange), 0, 0);
-                __builtin_amdgcn_raw_buffer_store_b32(s[1], rsrc, (int)(col_ok ? o0 + 4u * ld4 : kOutOfRange), 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b32(s[0], rsrc, (int)(col_ok ? o0 : kOutOfRange), 0, kAux);
+                __builtin_amdgcn_raw_buffer_store_b32(s[1], rsrc, (int)(col_ok ? o0 + 4u * ld4 : kOutOfRange), 0,
+                                                      kAux);
             }
     }
 }
