@@ -68,6 +68,43 @@ def test_shape_every_entry(hip, oracle, dtype, M, N, K, ta, tb):
         assert_gemm_close(got, ref, den, K, f"{dtype} {M}x{N}x{K} ta={ta} tb={tb}")
 
 
+# Ragged shapes for the routes past the aligned kernels: extents that are not
+# whole 16-byte chunks (aligned copies of those operands), few tiles with a
+# long K (K slices on the guarded-edge kernels, K rounded up where no slice
+# count divides it), and rows of C that are whole 128-byte lines or not (the
+# non-temporal C stores).  C pre-filled with NaN.
+_RDIMS = [33, 100, 300, 700, 900, 1000, 1001, 1500, 2047, 2500, 3001]
+_RKS = [100, 300, 1000, 1002, 3000, 5000, 8192, 20000, 20024, 30000]
+
+
+def _ragged_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        M, N = int(rng.choice(_RDIMS)), int(rng.choice(_RDIMS))
+        K = int(rng.choice(_RKS))
+        if M * N * K > _MAX_MAC:
+            continue
+        dtype = "bf16" if rng.random() < 0.5 else "f32"
+        out.append((dtype, M, N, K, int(rng.integers(2)), int(rng.integers(2))))
+    return out
+
+
+@pytest.mark.parametrize("dtype,M,N,K,ta,tb", _ragged_cases(60, seed=31))
+def test_ragged_shape_every_entry(hip, oracle, dtype, M, N, K, ta, tb):
+    A, B, Au, Bu = _operands(oracle, dtype, M, N, K, ta, tb, seed=M * 5 + N * 11 + K + 2 * ta + tb)
+    a, b = hip.from_numpy(A, dtype), hip.from_numpy(B, dtype)
+    out = hip.from_numpy(np.full((M, N), np.nan, np.float32))
+    got = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb), out=out).numpy()
+    again = hip.matmul(a, b, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "repeat"
+    Ak = np.ascontiguousarray(Au.T if ta else Au)
+    Bk = np.ascontiguousarray(Bu if tb else Bu.T)
+    ref = oracle.matmul(Ak, Bk, trans_b=True, threads=16)
+    den = np.abs(Ak).astype(np.float64) @ np.abs(Bk).astype(np.float64).T
+    assert_gemm_close(got, ref, den, K, f"{dtype} {M}x{N}x{K} ta={ta} tb={tb}")
+
+
 def _batched_cases(n, seed):
     rng = np.random.default_rng(seed)
     out = []
