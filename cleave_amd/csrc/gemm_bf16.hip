@@ -544,13 +544,14 @@ bool slices_fit(const uint16_t* a, const uint16_t* b, int M, int N, int kk, cons
     if (!bases_aligned(a, b, s)) return false;
     if (M % 128 == 0 && N % 128 == 0 && kk % 64 == 0 && s.lda % 8 == 0 && s.ldb % 8 == 0) return true;
     return ch::edge_chunks<8>(!TA, M, kk, s.lda, s.padded) && ch::edge_chunks<8>(TB, N, kk, s.ldb, s.padded) &&
-           ch::edge_bytes<8, 2>(!TA, M, kk, s.lda) < (1ll << 31) && ch::edge_bytes<8, 2>(TB, N, kk, s.ldb) < (1ll << 31);
+           ch::edge_bytes<8, 2>(!TA, M, kk, s.lda) < (1ll << 31) &&
+           ch::edge_bytes<8, 2>(TB, N, kk, s.ldb) < (1ll << 31);
 }
 
 // One product (C of pitch N; A and B of pitches lda and ldb, so that a band
 // of a larger product's rows keeps its operand pitches) as split_count's K
 // slices into a scratch buffer, added in order (ch::sum_slices_f32,
-// deterministic): the aligned kernels, or on a ragged M or N the
+// deterministic): the aligned kernels, or on a ragged M, N or K the
 // guarded-edge ones (`padded`: the operands are aligned copies,
 // ch::edge_chunks).  Each slice's C starts on a 16-byte boundary of the
 // buffer.  False when not split.
