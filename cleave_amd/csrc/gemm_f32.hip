@@ -630,12 +630,23 @@ constexpr double kSkinnyMinFlops = 1u << 20;
 constexpr ch::PadModel kPadModel{0.86, 0.78, false, 1.0};
 constexpr int64_t kEdgeTilesPerCu = 4;
 
-// One ragged product (an M or N off the 64 grid) with at most a round of
-// 64 x 64 tiles and a long K, as S K slices (the most, each at least 512
-// deep and whole 16-byte chunks, K % 4S == 0, up to kEdgeTilesPerCu tiles
-// per CU over all slices) on the 64 x 64 kernel's guarded-edge form, its
-// batch running over the slices, added in order (deterministic).  2048 x
-// 200 x 2000: 40.2 us in one launch of 128 tiles.  `padded`: the operands
+// Time of one 64 x 64 guarded-edge tile per k on a CU, in microseconds,
+// whatever the number of tiles sharing it (one to five): 2000^3 (four tiles
+// a CU) 132 us, 2500 x 640 x 16384 (two on most CUs) 535.
+constexpr double kEdgeTileKUs = 0.0163;
+
+// One ragged product (an M or N off the 64 grid) with a long K as S K
+// slices on the 64 x 64 kernel's guarded-edge form, its batch running over
+// the slices, added in order (deterministic); each slice at least 512 deep
+// and whole 16-byte chunks (K % 4S == 0).  At most a round of tiles: the
+// most slices, up to kEdgeTilesPerCu tiles per CU over all of them (2048 x
+// 200 x 2000: 40.2 us in one launch of 128 tiles).  Up to kEdgeTilesPerCu
+// tiles per CU and K from 4096: the count (up to 16) that evens out the
+// tiles per CU, priced as the busiest CU's tiles times the slice depth
+// (kEdgeTileKUs) plus the slices written and read back at 5 TB/s, when that
+// saves 5%: 2500 x 640 x 16384 (400 tiles, 2 on most CUs) 8 slices, 535 ->
+// 437-446 us; 1500^2 x 16384 A^T.B 4, 792 -> 603; 1200 x 1100 x 12000 A.B^T
+// 5, 377 -> 278; 1536 x 1100 x 8192 4, 269 -> 239.  `padded`: the operands
 // are aligned copies (ch::edge_chunks).  False when not split.
 template <bool TA, bool TB>
 bool try_edge_slices(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb,
@@ -643,9 +654,20 @@ bool try_edge_slices(const float* a, const float* b, float* c, int M, int N, int
     if (((uintptr_t)c & 15) || (M % 64 == 0 && N % 64 == 0)) return false;
     const int64_t cus = ch::num_cus() > 0 ? ch::num_cus() : 1;
     const int64_t tiles = (int64_t)((M + 63) / 64) * ((N + 63) / 64);
-    if (tiles > cus) return false;
-    int S = (int)std::min<int64_t>(kEdgeTilesPerCu * cus / tiles, K / 512);
-    while (S >= 2 && K % (4 * S) != 0) --S;
+    int S = 1;
+    if (tiles <= cus) {
+        S = (int)std::min<int64_t>(kEdgeTilesPerCu * cus / tiles, K / 512);
+        while (S >= 2 && K % (4 * S) != 0) --S;
+    } else {
+        if (tiles > kEdgeTilesPerCu * cus || K < 4096) return false;
+        auto cost = [&](int s) {
+            const double busiest = (double)((tiles * s + cus - 1) / cus);
+            return busiest * ((double)K / s) * kEdgeTileKUs + (s > 1 ? 8.0 * s * (double)M * N / 5.0e6 : 0.0);
+        };
+        double best = 0.95 * cost(1);
+        for (int s = 2; s <= 16 && K / s >= 512; ++s)
+            if (K % (4 * s) == 0 && cost(s) < best) best = cost(s), S = s;
+    }
     if (S < 2) return false;
     const int kk = K / S;
     const int64_t sA = TA ? (int64_t)kk * lda : kk, sB = TB ? kk : (int64_t)kk * ldb;
@@ -691,7 +713,8 @@ int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, in
         const int64_t cus = ch::num_cus();
         const bool edge16 = tiles64 <= kEdgeTilesPerCu * cus || K <= 512;
         // The same kernels on aligned copies (ch::run_aligned): K slices for
-        // one product with few tiles and a long K, else one launch.
+        // one product with a long K over few or unevenly spread tiles
+        // (try_edge_slices), else one launch.
         auto edge = [&](const float* pa, const float* pb, int64_t plda, int64_t pldb, int64_t psA, int64_t psB,
                         int Kq, int32_t* s) {
             if (batch == 1 && try_edge_slices<TA, TB>(pa, pb, c, M, N, Kq, plda, pldb, true, s)) return true;

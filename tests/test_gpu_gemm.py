@@ -1064,6 +1064,28 @@ def test_f32_ragged_long_k_every_entry(hip, oracle, M, N, K, ta, tb):
     assert_gemm_close(got, ref, den, K, f"ragged long-K {M}x{N}x{K} ta={ta} tb={tb}")
 
 
+@pytest.mark.parametrize("M,N,K,ta,tb", [(2500, 640, 16384, 1, 1), (1536, 1100, 8192, 0, 0), (1200, 1100, 12000, 0, 1),
+                                         (1500, 1500, 8192, 1, 0), (1201, 1103, 8192, 0, 0)])
+def test_f32_balanced_slices_every_entry(hip, oracle, M, N, K, ta, tb):
+    # Ragged products with more 64 x 64 tiles than CUs and a long K: K
+    # slices that even out the tiles per CU (2500 x 640 x 16384, 400 tiles,
+    # in 8 slices; 1536 x 1100 x 8192 and 1500^2 x 8192 in 4; 1200 x 1100 x
+    # 12000 in 5, slices of 2400; 1201 x 1103 x 8192 on aligned copies, odd
+    # M*N for the slice sum's tail).  C pre-filled with NaN; every entry
+    # against the loop, and a second call bit for bit.
+    A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=M + N + K + 2 * ta + tb)
+    ha, hb = hip.from_numpy(A), hip.from_numpy(B)
+    out = hip.from_numpy(np.full((M, N), np.nan, np.float32))
+    got = hip.matmul(ha, hb, trans_a=bool(ta), trans_b=bool(tb), out=out).numpy()
+    again = hip.matmul(ha, hb, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    Ak = np.ascontiguousarray(Au.T if ta else Au)
+    Bk = np.ascontiguousarray(Bu if tb else Bu.T)
+    ref = oracle.matmul(Ak, Bk, trans_b=True, threads=16)
+    den = np.abs(Ak).astype(np.float64) @ np.abs(Bk).astype(np.float64).T
+    assert_gemm_close(got, ref, den, K, f"balanced slices {M}x{N}x{K} ta={ta} tb={tb}")
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+
+
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [(64, 64, 65536), (128, 128, 65536), (512, 1024, 16384), (100, 100, 100000),
                                    (256, 8448, 4096), (1000, 1000, 32768), (1001, 1001, 32768),
