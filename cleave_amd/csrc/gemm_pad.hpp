@@ -94,6 +94,7 @@ struct PadCopy {
     int rows, cols, rows_p, cols_p;
     int64_t total_rows;
     bool vec_src;
+    __host__ __device__ int64_t chunks() const { return total_rows * (cols_p / 8); }
 };
 
 // Destination row rr of one padded copy, each thread 8 consecutive elements.
@@ -133,6 +134,77 @@ __global__ __launch_bounds__(256) void pad_copy_kernel(PadCopy<T> a, PadCopy<T> 
     }
 }
 
+// 8 consecutive elements from s, in the widest loads its alignment allows
+// (a source row that is not whole 16-byte chunks starts 8, 4 or 2 bytes
+// off in every other row).
+template <typename T>
+__device__ __forceinline__ void load8(const T* s, T (&v)[8]) {
+    constexpr int ES = (int)sizeof(T);
+    const uintptr_t al = (uintptr_t)s & 15;
+    if (al == 0) {
+        typedef uint32_t w4 __attribute__((ext_vector_type(4)));
+        w4 w[ES / 2];
+#pragma unroll
+        for (int i = 0; i < ES / 2; ++i) w[i] = reinterpret_cast<const w4*>(s)[i];
+        __builtin_memcpy(v, w, sizeof(v));
+    } else if ((al & 7) == 0) {
+        uint64_t w[ES];
+#pragma unroll
+        for (int i = 0; i < ES; ++i) w[i] = reinterpret_cast<const uint64_t*>(s)[i];
+        __builtin_memcpy(v, w, sizeof(v));
+    } else if ((al & 3) == 0) {
+        uint32_t w[2 * ES];
+#pragma unroll
+        for (int i = 0; i < 2 * ES; ++i) w[i] = reinterpret_cast<const uint32_t*>(s)[i];
+        __builtin_memcpy(v, w, sizeof(v));
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[t] = s[t];
+    }
+}
+
+// Destination chunk q (8 elements; row q / (cols_p / 8)) of one padded copy.
+template <typename T>
+__device__ __forceinline__ void pad_copy_chunk(const PadCopy<T>& j, int64_t q) {
+    const int cpr = j.cols_p / 8;
+    int64_t rr, bt;
+    if (q < (1ll << 32)) {  // 32-bit divisions (a 64-bit one costs ~10x the instructions)
+        const uint32_t r32 = (uint32_t)q / (uint32_t)cpr;
+        rr = r32;
+        bt = r32 / (uint32_t)j.rows_p;
+    } else {
+        rr = q / cpr;
+        bt = rr / j.rows_p;
+    }
+    const int c0 = (int)(q - rr * cpr) * 8;
+    const int r = (int)(rr - bt * j.rows_p);
+    const T* s = j.src + (bt * j.rows + r) * (int64_t)j.cols + c0;
+    T v[8];
+    if (r < j.rows && c0 + 8 <= j.cols) {
+        load8(s, v);
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[t] = (r < j.rows && c0 + t < j.cols) ? s[t] : (T)0;
+    }
+    typedef uint32_t w4 __attribute__((ext_vector_type(4)));
+    w4 w[sizeof(T) / 2];
+    __builtin_memcpy(w, v, sizeof(v));
+    w4* d = reinterpret_cast<w4*>(j.dst + rr * (int64_t)j.cols_p + c0);
+#pragma unroll
+    for (int i = 0; i < (int)sizeof(T) / 2; ++i) d[i] = w[i];
+}
+
+// The same copies, one thread per 8-element destination chunk (grid-
+// strided): chunks 0 .. a.chunks() - 1 are a's, the next b.chunks() are b's.
+template <typename T>
+__global__ __launch_bounds__(256) void pad_copy_chunks_kernel(PadCopy<T> a, PadCopy<T> b) {
+    const int64_t na = a.chunks(), total = na + b.chunks();
+    for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < total; q += (int64_t)gridDim.x * 256) {
+        if (q < na) pad_copy_chunk(a, q);
+        else pad_copy_chunk(b, q - na);
+    }
+}
+
 // dst (batch x M x N, pitch N) = the top-left M x N of each src matrix
 // (batch x Mp x Np, pitch Np); Np % 4 == 0 and src 16-byte aligned (for
 // T = float).
@@ -163,6 +235,34 @@ __global__ __launch_bounds__(256) void crop_kernel(const T* __restrict__ src, T*
 inline unsigned pad_grid(int64_t total_rows, int cus) {
     const int64_t cap = (int64_t)(cus > 0 ? cus : 1) * 64;
     return (unsigned)(total_rows < cap ? total_rows : cap);
+}
+
+// Launches the padded copies a and b (either may be empty).  A workgroup per
+// destination row (pad_copy_kernel) unless a copied operand has rows under
+// 512 elements or fewer rows than CUs: then a thread per chunk
+// (pad_copy_chunks_kernel, at most 8 workgroups per CU, full occupancy),
+// which keeps every thread busy (a row of 300 bf16 leaves 218 of 256
+// threads idle) and every CU fed.  Same box, copy kernel alone: 64 x 700 x
+// 900 x 300 (rows of 300 and 900 bf16) 37.5 -> 30.3 us (the product 94.7 ->
+// 87.8), 200 rows of 12300 10.2 -> 8.4.  As chunks, more rows of 1000 or
+// more elements copied slower than a row per workgroup: f32 6000^3 118
+// against 104 us, bf16 1001 x 32768 (K rounded to 2048) 24.2 against 21.8,
+// 1500^3 10.4 against 9.7.  (One kernel taking either mapping per operand
+// made the row path slower still, 27.9 against 21.8 at 1001 x 32768.)
+template <typename T>
+int32_t launch_pad_copies(const PadCopy<T>& a, const PadCopy<T>& b, int cus) {
+    const int64_t rows = a.total_rows + b.total_rows;
+    if (rows == 0) return CLEAVE_HIP_OK;
+    auto short_rows = [cus](const PadCopy<T>& j) {
+        return j.total_rows > 0 && (j.cols_p < 512 || j.total_rows < cus);
+    };
+    if (short_rows(a) || short_rows(b)) {
+        const int64_t cap = (int64_t)(cus > 0 ? cus : 1) * 8, need = (a.chunks() + b.chunks() + 255) / 256;
+        pad_copy_chunks_kernel<T><<<(unsigned)(need < cap ? need : cap), 256, 0, stream()>>>(a, b);
+        return check_hip(hipGetLastError(), "pad_copy_chunks_kernel");
+    }
+    pad_copy_kernel<T><<<pad_grid(rows, cus), 256, 0, stream()>>>(a, b);
+    return check_hip(hipGetLastError(), "pad_copy_kernel");
 }
 
 // Runs `gemm(a, b, c, Mp, Np, Kp)` (which must take the padded shape with
@@ -197,11 +297,7 @@ bool run_padded(const PadPlan& p, const T* a, const T* b, float* c, int batch, b
         jb = PadCopy<T>{b, d, rows, cols, rows_p, cols_p, (int64_t)batch * rows_p, vec};
         pb = d;
     }
-    int32_t st = CLEAVE_HIP_OK;
-    if (ja.total_rows + jb.total_rows > 0) {
-        pad_copy_kernel<T><<<pad_grid(ja.total_rows + jb.total_rows, cus), 256, 0, stream()>>>(ja, jb);
-        st = check_hip(hipGetLastError(), "pad_copy_kernel");
-    }
+    int32_t st = launch_pad_copies(ja, jb, cus);
     if (p.crop_c) pc = (float*)(base + p.bytes_a + p.bytes_b);
     if (st == CLEAVE_HIP_OK) st = gemm(pa, pb, pc, p.Mp, p.Np, p.Kp);
     if (st == CLEAVE_HIP_OK && p.crop_c) {
@@ -292,8 +388,7 @@ bool run_aligned(const AlignPlan& p, const T* a, const T* b, int M, int N, int K
         jb = PadCopy<T>{b, d, rows, cols, (int)p.rows_b, (int)p.ldb, (int64_t)batch * p.rows_b, vec};
         pb = d;
     }
-    pad_copy_kernel<T><<<pad_grid(ja.total_rows + jb.total_rows, num_cus()), 256, 0, stream()>>>(ja, jb);
-    int32_t st = check_hip(hipGetLastError(), "pad_copy_kernel");
+    int32_t st = launch_pad_copies(ja, jb, num_cus());
     if (st != CLEAVE_HIP_OK) {
         *status = st;
         return true;
