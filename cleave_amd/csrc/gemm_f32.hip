@@ -747,6 +747,18 @@ int32_t launch(const float* a, const float* b, float* c, int M, int N, int K, in
             const ch::AlignPlan ap = ch::align_plan(M, N, K, batch, TA, TB, a, b, 4);
             if (ch::run_aligned(ap, a, b, M, N, K, batch, TA, TB, edge, &st)) return st;
         }
+        // Past four 64 x 64 tiles per CU with K over 512, at least three
+        // 128 x 128 tiles per CU: that kernel with guarded edges, in place,
+        // instead of padded copies and a crop (same box, two runs: 3000 x
+        // 5000 x 2000 506 -> 479 us, 4000^2 x 1000 A^T.B^T 268 -> 250, 4000 x
+        // 3000 x 3000 A^T.B 553 -> 543, 6000^3 level).  With fewer tiles it
+        // ran slower than the routes above: 1500^3 101 against 78 us (144
+        // tiles), 3000 x 1000 x 6000 A.B^T 384 against 295 (192), 2500^2 x
+        // 4096 497 against 457 on the padded route (400).
+        const int64_t tiles128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128) * batch;
+        if (!edge16 && tiles128 >= 3 * cus &&
+            launch_tiled_edge<128, 128, 16, 2, 2, 2, TA, TB>(a, b, c, M, N, K, lda, ldb, batch, sA, sB, sC, &st))
+            return st;
         const ch::PadPlan p = ch::pad_plan(M, N, K, batch, TA, TB, a, b, 4, ch::num_cus(), kPadModel);
         auto gemm = [batch](const float* pa, const float* pb, float* pc, int Mp, int Np, int Kp) {
             const int64_t plda = TA ? Mp : Kp, pldb = TB ? Kp : Np;

@@ -535,9 +535,10 @@ def test_padded_ragged_every_entry(hip, oracle, dtype, M, N, K, ta, tb):
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_padded_large_ragged_every_entry(hip, oracle, dtype):
-    # 3000 x 5000 x 2000: M, N and K all ragged, padded to the 256 x 256
-    # kernels' tiles; every entry against the loop (its A·Bᵀ form on a
-    # transposed copy of B, bit for bit its A·B loop)
+    # 3000 x 5000 x 2000: M, N and K all ragged (bf16 on the 256 x 256
+    # kernels with guarded edges, f32 on the 128 x 128 tiled kernel's); every
+    # entry against the loop (its A·Bᵀ form on a transposed copy of B, bit
+    # for bit its A·B loop)
     M, N, K = 3000, 5000, 2000
     A, B, Au, Bu = _operands(oracle, dtype, M, N, K, 0, 0, seed=41)
     got = hip.matmul(hip.from_numpy(A, dtype), hip.from_numpy(B, dtype)).numpy()
@@ -545,6 +546,38 @@ def test_padded_large_ragged_every_entry(hip, oracle, dtype):
     ref = oracle.matmul(Au, Bt, trans_b=True, threads=16)
     den = np.abs(Au) @ np.abs(Bt).T
     assert_gemm_close(got, ref, den, K, f"padded {dtype} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb", [(3000, 5000, 600, 0, 0), (3001, 4200, 520, 0, 1), (4100, 3000, 700, 1, 0),
+                                         (3000, 4100, 600, 1, 1)])
+def test_f32_edge128_every_entry(hip, oracle, M, N, K, ta, tb):
+    # f32 ragged products past four 64 x 64 tiles per CU with K over 512 and
+    # at least three 128 x 128 tiles per CU: the 128 x 128 tiled kernel with
+    # guarded edges on the operands in place (K ragged to the 16-deep
+    # k-tile).  C pre-filled with NaN; every entry against the loop.
+    A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=7 * M + N + K + 2 * ta + tb)
+    out = hip.from_numpy(np.full((M, N), np.nan, np.float32))
+    got = hip.matmul(hip.from_numpy(A), hip.from_numpy(B), trans_a=bool(ta), trans_b=bool(tb), out=out).numpy()
+    Ak = np.ascontiguousarray(Au.T if ta else Au)
+    Bk = np.ascontiguousarray(Bu if tb else Bu.T)
+    ref = oracle.matmul(Ak, Bk, trans_b=True, threads=16)
+    den = np.abs(Ak).astype(np.float64) @ np.abs(Bk).astype(np.float64).T
+    assert_gemm_close(got, ref, den, K, f"f32 edge128 {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+def test_f32_edge128_batched_every_entry(hip, oracle):
+    # four 1500 x 2100 x 520 products: 816 tiles of 128 x 128 over the batch
+    bs, M, N, K = 4, 1500, 2100, 520
+    rng = np.random.default_rng(88)
+    A = rng.uniform(-1, 1, (bs, M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (bs, K, N)).astype(np.float32)
+    out = hip.from_numpy(np.full((bs, M, N), np.nan, np.float32))
+    got = hip.matmul_batched(hip.from_numpy(A), hip.from_numpy(B), out=out).numpy()
+    for i in range(bs):
+        Bt = np.ascontiguousarray(B[i].T)
+        ref = oracle.matmul(A[i], Bt, trans_b=True, threads=16)
+        den = np.abs(A[i]).astype(np.float64) @ np.abs(Bt).astype(np.float64).T
+        assert_gemm_close(got[i], ref, den, K, f"f32 edge128 batched {i}")
 
 
 @pytest.mark.parametrize("dtype,off", [("f32", 1), ("bf16", 1), ("bf16", 4)])
