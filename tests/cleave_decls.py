@@ -1,5 +1,5 @@
-"""Reads the cleave-side drop-in declarations of INTEGRATION.md (its ```cleave
-blocks) and lowers each `extern(symbol) fn` the way the reference compiler
+"""Reads the cleave-side drop-in declarations of the repository's integration
+guide (its ```cleave blocks) and lowers each `extern(symbol) fn` the way the reference compiler
 would, for tests/test_integration_decls.py (CPU) and tests/test_gpu_extern.py.
 
 What is restated from the reference (read as text, not run):

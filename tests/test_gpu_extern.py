@@ -1,4 +1,4 @@
-"""Every `extern(symbol) fn` that INTEGRATION.md declares on the cleave side,
+"""Every `extern(symbol) fn` that the integration guide declares on the cleave side,
 called on the GPU exactly as the reference's lowering would call it
 (tests/cleave_decls.py: each array argument as (pointer, i64 length), an array
 result as the first array argument handed back, the C result an i64), and its

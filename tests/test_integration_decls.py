@@ -1,4 +1,4 @@
-"""The cleave-side drop-in text of INTEGRATION.md, checked on the CPU against
+"""The cleave-side drop-in text of the integration guide, checked on the CPU against
 what the reference's compiler accepts and emits (tests/cleave_decls.py holds
 the restated rules):
 
