@@ -634,6 +634,9 @@ constexpr int64_t kEdgeTilesPerCu = 4;
 // whatever the number of tiles sharing it (one to five): 2000^3 (four tiles
 // a CU) 132 us, 2500 x 640 x 16384 (two on most CUs) 535.
 constexpr double kEdgeTileKUs = 0.0163;
+// The same for a 128 x 128 tile (3000 x 5000 x 2000, four tiles on most
+// CUs, 479 us): 8% less per flop than 64 x 64 when the tiles are many.
+constexpr double kEdge128TileKUs = 0.0599;
 
 // One ragged product (an M or N off the 64 grid) with a long K as S K
 // slices on the 64 x 64 kernel's guarded-edge form, its batch running over
@@ -646,27 +649,44 @@ constexpr double kEdgeTileKUs = 0.0163;
 // (kEdgeTileKUs) plus the slices written and read back at 5 TB/s, when that
 // saves 5%: 2500 x 640 x 16384 (400 tiles, 2 on most CUs) 8 slices, 535 ->
 // 437-446 us; 1500^2 x 16384 A^T.B 4, 792 -> 603; 1200 x 1100 x 12000 A.B^T
-// 5, 377 -> 278; 1536 x 1100 x 8192 4, 269 -> 239.  `padded`: the operands
-// are aligned copies (ch::edge_chunks).  False when not split.
+// 5, 377 -> 278; 1536 x 1100 x 8192 4, 269 -> 239.  From K = 4096 the
+// slices run on 128 x 128 tiles instead (up to 4 per CU) where the same
+// pricing (kEdge128TileKUs) puts them 3% under the 64 x 64 choice: 1000^2 x
+// 65536 16 slices, 1070 -> 985 us; 1000^2 x 32768 A.B^T 529 -> 501; 1001 x
+// 1003 x 32768 (aligned copies) 582 -> 553.  It priced 700 x 900 x 30000
+// and 512 x 2000 x 20000 within 3% of their times on 128 x 128 tiles (373
+// and 372 us, against 335 and 330 on 64 x 64), which it therefore keeps.
+// `padded`: the operands are aligned copies (ch::edge_chunks).  False when
+// not split.
 template <bool TA, bool TB>
 bool try_edge_slices(const float* a, const float* b, float* c, int M, int N, int K, int64_t lda, int64_t ldb,
                      bool padded, int32_t* st) {
     if (((uintptr_t)c & 15) || (M % 64 == 0 && N % 64 == 0)) return false;
     const int64_t cus = ch::num_cus() > 0 ? ch::num_cus() : 1;
     const int64_t tiles = (int64_t)((M + 63) / 64) * ((N + 63) / 64);
+    // predicted time: the busiest CU's tiles times the slice depth, plus
+    // the slices written and read back at 5 TB/s
+    auto cost = [&](int64_t t, double tile_k_us, int s) {
+        const double busiest = (double)((t * s + cus - 1) / cus);
+        return busiest * ((double)K / s) * tile_k_us + (s > 1 ? 8.0 * s * (double)M * N / 5.0e6 : 0.0);
+    };
     int S = 1;
     if (tiles <= cus) {
         S = (int)std::min<int64_t>(kEdgeTilesPerCu * cus / tiles, K / 512);
         while (S >= 2 && K % (4 * S) != 0) --S;
     } else {
         if (tiles > kEdgeTilesPerCu * cus || K < 4096) return false;
-        auto cost = [&](int s) {
-            const double busiest = (double)((tiles * s + cus - 1) / cus);
-            return busiest * ((double)K / s) * kEdgeTileKUs + (s > 1 ? 8.0 * s * (double)M * N / 5.0e6 : 0.0);
-        };
-        double best = 0.95 * cost(1);
+        double best = 0.95 * cost(tiles, kEdgeTileKUs, 1);
         for (int s = 2; s <= 16 && K / s >= 512; ++s)
-            if (K % (4 * s) == 0 && cost(s) < best) best = cost(s), S = s;
+            if (K % (4 * s) == 0 && cost(tiles, kEdgeTileKUs, s) < best) best = cost(tiles, kEdgeTileKUs, s), S = s;
+    }
+    bool big = false;  // 128 x 128 tiles, at least three per CU (the rate kEdge128TileKUs holds for)
+    if (K >= 4096) {
+        const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+        double best = 0.97 * cost(tiles, kEdgeTileKUs, S);
+        for (int s = 2; s <= 64 && K / s >= 512 && t128 * s <= kEdgeTilesPerCu * cus; ++s)
+            if (K % (4 * s) == 0 && t128 * s >= 3 * cus && cost(t128, kEdge128TileKUs, s) < best)
+                best = cost(t128, kEdge128TileKUs, s), S = s, big = true;
     }
     if (S < 2) return false;
     const int kk = K / S;
@@ -678,10 +698,16 @@ bool try_edge_slices(const float* a, const float* b, float* c, int M, int N, int
     const int64_t n = (int64_t)M * N, n4 = (n + 3) / 4 * 4;
     float* part = (float*)ch::scratch_try(9, sizeof(float) * (size_t)S * n4);
     if (!part) return false;
-    if (!(tiles * S <= 2 * cus && launch_tiled_edge<64, 64, 32, 2, 2, 4, TA, TB>(a, b, part, M, N, kk, lda, ldb, S,
-                                                                                 sA, sB, n4, st, padded)) &&
-        !launch_tiled_edge<64, 64, 16, 2, 2, 4, TA, TB>(a, b, part, M, N, kk, lda, ldb, S, sA, sB, n4, st, padded))
-        *st = launch_general<TA, TB>(a, b, part, M, N, kk, lda, ldb, N, S, sA, sB, n4);
+    bool launched;
+    if (big)
+        launched =
+            launch_tiled_edge<128, 128, 16, 2, 2, 2, TA, TB>(a, b, part, M, N, kk, lda, ldb, S, sA, sB, n4, st, padded);
+    else
+        launched =
+            (tiles * S <= 2 * cus &&
+             launch_tiled_edge<64, 64, 32, 2, 2, 4, TA, TB>(a, b, part, M, N, kk, lda, ldb, S, sA, sB, n4, st, padded)) ||
+            launch_tiled_edge<64, 64, 16, 2, 2, 4, TA, TB>(a, b, part, M, N, kk, lda, ldb, S, sA, sB, n4, st, padded);
+    if (!launched) *st = launch_general<TA, TB>(a, b, part, M, N, kk, lda, ldb, N, S, sA, sB, n4);
     if (*st == CLEAVE_HIP_OK) *st = ch::sum_slices_f32(part, c, n, S, n4);
     return true;
 }

@@ -1081,7 +1081,8 @@ def test_bf16_ragged_round_split_every_entry(hip, oracle, ta, tb):
                                    (1001, 1003, 32768), (2048, 200, 2000)])
 def test_f32_ragged_long_k_every_entry(hip, oracle, M, N, K, ta, tb):
     # Ragged M or N, few tiles and a long K: K slices on the 64 x 64 kernel's
-    # guarded-edge form, on the operands in place (1000^2 x 32768, 100^2 x
+    # guarded-edge form (1000^2 x 32768 and 1001 x 1003 x 32768 on the 128 x
+    # 128 kernel's, 16 slices), on the operands in place (1000^2 x 32768, 100^2 x
     # 100000 as 125 slices, 70 x 300 x 30000, 2048 x 200 x 2000), on aligned
     # copies of the operands whose rows are not whole chunks (1001 x 1003 x
     # 32768), or on aligned copies of both with K rounded up to 2048 (1001 x
@@ -1098,14 +1099,15 @@ def test_f32_ragged_long_k_every_entry(hip, oracle, M, N, K, ta, tb):
 
 
 @pytest.mark.parametrize("M,N,K,ta,tb", [(2500, 640, 16384, 1, 1), (1536, 1100, 8192, 0, 0), (1200, 1100, 12000, 0, 1),
-                                         (1500, 1500, 8192, 1, 0), (1201, 1103, 8192, 0, 0)])
+                                         (1500, 1500, 8192, 1, 0), (1201, 1103, 8192, 0, 0), (2000, 2000, 8192, 1, 0)])
 def test_f32_balanced_slices_every_entry(hip, oracle, M, N, K, ta, tb):
     # Ragged products with more 64 x 64 tiles than CUs and a long K: K
     # slices that even out the tiles per CU (2500 x 640 x 16384, 400 tiles,
     # in 8 slices; 1536 x 1100 x 8192 and 1500^2 x 8192 in 4; 1200 x 1100 x
     # 12000 in 5, slices of 2400; 1201 x 1103 x 8192 on aligned copies, odd
-    # M*N for the slice sum's tail).  C pre-filled with NaN; every entry
-    # against the loop, and a second call bit for bit.
+    # M*N for the slice sum's tail; 2000^2 x 8192 in 4 slices of 128 x 128
+    # tiles).  C pre-filled with NaN; every entry against the loop, and a
+    # second call bit for bit.
     A, B, Au, Bu = _operands(oracle, "f32", M, N, K, ta, tb, seed=M + N + K + 2 * ta + tb)
     ha, hb = hip.from_numpy(A), hip.from_numpy(B)
     out = hip.from_numpy(np.full((M, N), np.nan, np.float32))
