@@ -651,9 +651,10 @@ constexpr double kEdge128TileKUs = 0.0599;
 // 437-446 us; 1500^2 x 16384 A^T.B 4, 792 -> 603; 1200 x 1100 x 12000 A.B^T
 // 5, 377 -> 278; 1536 x 1100 x 8192 4, 269 -> 239.  From K = 4096 the
 // slices run on 128 x 128 tiles instead (up to 4 per CU) where the same
-// pricing (kEdge128TileKUs) puts them 3% under the 64 x 64 choice: 1000^2 x
-// 65536 16 slices, 1070 -> 985 us; 1000^2 x 32768 A.B^T 529 -> 501; 1001 x
-// 1003 x 32768 (aligned copies) 582 -> 553.  It priced 700 x 900 x 30000
+// pricing (kEdge128TileKUs) puts them 3% under the 64 x 64 choice, at
+// least three per CU: 1000^2 x 65536 16 slices, 1082 -> 988 us; 1000^2 x
+// 32768 A.B^T 532 -> 503; 1001 x 1003 x 32768 (aligned copies) 586 -> 554;
+// 2000^2 x 8192 4 slices (unsplit before) 530 -> 506.  It priced 700 x 900 x 30000
 // and 512 x 2000 x 20000 within 3% of their times on 128 x 128 tiles (373
 // and 372 us, against 335 and 330 on 64 x 64), which it therefore keeps.
 // `padded`: the operands are aligned copies (ch::edge_chunks).  False when
