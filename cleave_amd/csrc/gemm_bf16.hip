@@ -521,18 +521,42 @@ int split_count(int M, int N, int K) {
 
 // Slices for a product the guarded-edge kernels take (M or N off the
 // 128 x 128 tile, or K off the 64-deep k-tile; split_count's rules are for
-// the aligned kernels): with fewer 128 x 128 tiles than half a round, the
-// most slices, at least 512 deep, that one round of those tiles holds, whose
-// depth is whole 16-byte chunks (K % 8S == 0).  128 x 300 x 5000 A^T.B^T
-// (three tiles) 47.7 -> 15.9 us, 300^2 x 3000 31 -> 17.  1 = no split.
+// the aligned kernels), with at most a round of 128 x 128 tiles; each
+// slice's depth whole 16-byte chunks (K % 8S == 0).  The more of: the most
+// slices, at least 512 deep, that one round of tiles holds (128 x 300 x 5000
+// A^T.B^T, three tiles, 47.7 -> 15.9 us; 300^2 x 3000 31 -> 17); and a
+// count past one round, up to 4 tiles per CU over all slices, each slice at
+// least 2000 deep: of those, the largest whose busiest CU's tiles times the
+// slice depth is within 10% of the least.  A tile alone on a CU runs at
+// about a third of the CU's bf16 rate, so more tiles per CU pay for the
+// slices' partial sums, but not a third tile on some CUs where two would
+// do: 1200 x 1100 x 12000 A.B^T 53 us in 5 slices (2 tiles on the busiest
+// CUs), 68 in 6 (3).  Same box, two runs, against one round at most (and no
+// split past half a round): 1500^2 x 16384 165 -> 102 us, 1000^2 x 65536
+// 212 -> 121, 704 x 896 x 30000 92 -> 64, 5000 x 512 x 8192 A.B^T 62 -> 50,
+// 3000 x 700 x 8192 87 -> 61, 2500 x 640 x 16384 A^T.B^T 107 -> 86, 1100 x
+// 1000 x 10000 A^T.B^T 64 -> 50, 1001^2 x 32768 117 -> 97; one loss, 2000 x
+// 1000 x 8000 A^T.B 49 -> 52 (4 slices against 2).  1 = no split.
 int edge_split_count(int M, int N, int K) {
     if (M % 128 == 0 && N % 128 == 0 && K % 64 == 0) return 1;
     const int64_t cus = ch::num_cus() > 0 ? ch::num_cus() : 1;
     const int64_t tiles = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
-    if (tiles * 2 > cus) return 1;
+    if (tiles > cus) return 1;
+    int one = 1;  // within one round
     for (int S = (int)std::min<int64_t>(cus / tiles, K / 512); S >= 2; --S)
-        if (K % (8 * S) == 0) return S;
-    return 1;
+        if (K % (8 * S) == 0) {
+            one = S;
+            break;
+        }
+    // past one round: the busiest CU's tiles times the slice depth
+    auto work = [&](int S) { return (double)((tiles * S + cus - 1) / cus) * ((double)K / S); };
+    double least = 0;
+    for (int S = 2; S <= K / 2000 && tiles * S <= 4 * cus; ++S)
+        if (tiles * S > cus && K % (8 * S) == 0 && (least == 0 || work(S) < least)) least = work(S);
+    int past = 1;
+    for (int S = 2; S <= K / 2000 && tiles * S <= 4 * cus; ++S)
+        if (tiles * S > cus && K % (8 * S) == 0 && work(S) <= 1.1 * least) past = S;
+    return std::max(one, past);
 }
 
 // Whether K slices of depth kk with these strides go to an aligned kernel
