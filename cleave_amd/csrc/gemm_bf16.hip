@@ -500,7 +500,13 @@ bool launch_fast(const uint16_t* a, const uint16_t* b, float* c, int M, int N, i
 
 // K slices of one product with few 128 x 128 tiles and a long K: up to one
 // workgroup per CU, each slice at least 1024 deep (the slices' partial sums
-// are then small next to the product).  1 = no split.
+// are then small next to the product); or, where more, a count past one
+// round chosen as edge_split_count chooses it (up to 4 tiles per CU, slices
+// at least 2000 deep and whole 64-deep k-tiles).  Same box, two runs, against
+// one round at most: 1024^2 x 65536 192 -> 116-124 us, A^T.B 173 -> 117-124;
+// 1152^2 x 16384 94 -> 62; 1280^2 x 32768 A^T.B^T 150 -> 90; 1024 x 2048 x
+// 16384 A.B^T 82 -> 68; 512 x 1024 x 16384 and 2048^2 x 8192 level.  1 = no
+// split.
 int split_count(int M, int N, int K) {
     const int cus = ch::num_cus();
     const int64_t tiles = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
@@ -516,7 +522,15 @@ int split_count(int M, int N, int K) {
     }
     int S = 1;
     while (tiles * S * 2 <= cus && K % (64 * S * 2) == 0 && K / (S * 2) >= 1024) S *= 2;
-    return S;
+    // past one round: the busiest CU's tiles times the slice depth
+    auto work = [&](int s) { return (double)((tiles * s + cus - 1) / cus) * ((double)K / s); };
+    double least = 0;
+    for (int s = 2; s <= K / 2000 && tiles * s <= 4 * cus; ++s)
+        if (tiles * s > cus && K % (64 * s) == 0 && (least == 0 || work(s) < least)) least = work(s);
+    int past = 1;
+    for (int s = 2; s <= K / 2000 && tiles * s <= 4 * cus; ++s)
+        if (tiles * s > cus && K % (64 * s) == 0 && work(s) <= 1.1 * least) past = s;
+    return std::max(S, past);
 }
 
 // Slices for a product the guarded-edge kernels take (M or N off the

@@ -1121,13 +1121,16 @@ def test_f32_balanced_slices_every_entry(hip, oracle, M, N, K, ta, tb):
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
 
 
-@pytest.mark.parametrize("M,N,K,ta,tb", [(1500, 1500, 8192, 1, 1), (1200, 1100, 12000, 0, 1), (900, 900, 20000, 1, 0)])
+@pytest.mark.parametrize("M,N,K,ta,tb", [(1500, 1500, 8192, 1, 1), (1200, 1100, 12000, 0, 1), (900, 900, 20000, 1, 0),
+                                         (1152, 1152, 8192, 0, 0), (1024, 1024, 16384, 1, 0)])
 def test_bf16_slices_past_one_round_every_entry(hip, oracle, M, N, K, ta, tb):
-    # Ragged bf16 products with a partial round of 128 x 128 tiles and a long
-    # K: K slices past one round of tiles, up to 4 per CU (1500^2 x 8192, 144
-    # tiles, in 4 slices; 1200 x 1100 x 12000 in 5, slices of 2400, ragged to
-    # the 64-deep k-tile; 900^2 x 20000 in 10).  C pre-filled with NaN; every
-    # entry against the loop, and a second call bit for bit.
+    # bf16 products with a partial round of 128 x 128 tiles and a long K: K
+    # slices past one round of tiles, up to 4 per CU.  Ragged, on the
+    # guarded-edge kernels: 1500^2 x 8192 (144 tiles) in 4 slices; 1200 x
+    # 1100 x 12000 in 5, slices of 2400, ragged to the 64-deep k-tile; 900^2 x
+    # 20000 in 10.  Aligned, on the tiled kernels: 1152^2 x 8192 in 4, 1024^2
+    # x 16384 A^T.B in 8.  C pre-filled with NaN; every entry against the
+    # loop, and a second call bit for bit.
     A, B, Au, Bu = _operands(oracle, "bf16", M, N, K, ta, tb, seed=3 * M + N + K + 2 * ta + tb)
     a, b = hip.from_numpy(A, "bf16"), hip.from_numpy(B, "bf16")
     out = hip.from_numpy(np.full((M, N), np.nan, np.float32))
